@@ -1,0 +1,272 @@
+#!/usr/bin/env python3
+"""Benchmark: Q8_0 GEMM + fused attention TFLOP/s at SDXL-1024 shapes on one MI355X.
+
+A "step" is one pass over the SDXL 1024^2 kernel set with every input already
+resident in HBM:
+  * the Q8_0 GEMM sweep of BASELINE config 1 (8 shapes: level-1 and level-2
+    projections, cross-attention K/V), fp32 activations N(0,1), Q8_0 weights
+    from N(0, 0.02^2), fp32 out;
+  * fused self-attention (config 2: batch 2 x 10 heads x 4096, batch 2 x 20 x 1024,
+    d = 64, fp16 in/out, no mask) and cross-attention (config 3: 77 context
+    tokens, key-padding lengths U{1..77}).
+value = algorithmic FLOP of one step x steps / elapsed (HIP events on the
+launch stream), in TFLOP/s. The JSON line also carries a per-shape breakdown
+(hot-cache, each shape timed alone), the roofline of the dominant kernel and a
+CPU baseline (the oracle's OpenMP fp32 restatement, bounded sample).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA (published)
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E (published)
+
+GEMM_SHAPES = [  # (tag, M, N, K)
+    ("L1 q/k/v/out 640->640", 8192, 640, 640),
+    ("L1 geglu-up 640->5120", 8192, 5120, 640),
+    ("L1 ff-down 2560->640", 8192, 640, 2560),
+    ("L2 q/k/v/out 1280->1280", 2048, 1280, 1280),
+    ("L2 geglu-up 1280->10240", 2048, 10240, 1280),
+    ("L2 ff-down 5120->1280", 2048, 1280, 5120),
+    ("cross k/v 2048->640", 154, 640, 2048),
+    ("cross k/v 2048->1280", 154, 1280, 2048),
+]
+ATTN_SHAPES = [  # (tag, batch, heads, Tq, Tk, kv_len?)
+    ("self L1 2x10x4096^2", 2, 10, 4096, 4096, False),
+    ("self L2 2x20x1024^2", 2, 20, 1024, 1024, False),
+    ("cross L1 2x10x4096x77", 2, 10, 4096, 77, True),
+    ("cross L2 2x20x1024x77", 2, 20, 1024, 77, True),
+]
+
+
+def quantize_q8_0(w: np.ndarray) -> np.ndarray:
+    """GGUF Q8_0 blocks of a float32 [N, K] weight (d = fp16(amax/127), q = round-half-away)."""
+    b = w.reshape(-1, 32).astype(np.float32)
+    amax = np.abs(b).max(1, keepdims=True)
+    inv = np.where(amax > 0, np.float32(127.0) / np.where(amax > 0, amax, 1), 0).astype(np.float32)
+    x = b * inv
+    q = np.clip(np.trunc(x + np.where(x >= 0, 0.5, -0.5)), -127, 127).astype(np.int8)
+    d = (amax / np.float32(127.0)).astype(np.float16)
+    out = np.empty((b.shape[0], 34), dtype=np.uint8)
+    out[:, :2] = d.view(np.uint8).reshape(-1, 2)
+    out[:, 2:] = q.view(np.uint8)
+    return out.reshape(-1)
+
+
+class GemmCase:
+    kernel = "gemm_q8"
+
+    def __init__(self, tag, M, N, K, rng, hip, ops):
+        self.tag, self.M, self.N, self.K = tag, M, N, K
+        self.ops = ops
+        self.A = hip.DeviceBuffer.from_array(rng.standard_normal(M * K, dtype=np.float32))
+        self.W = hip.DeviceBuffer.from_array(quantize_q8_0(rng.standard_normal(N * K, dtype=np.float32) * 0.02))
+        self.C = hip.DeviceBuffer(M * N * 4)
+        self.flops = 2.0 * M * N * K
+        self.bytes = 4.0 * M * K + 34.0 / 32.0 * N * K + 4.0 * M * N
+
+    def run(self, stream):
+        self.ops.gemm_nt_q8_0(self.A, self.W, self.C, self.M, self.N, self.K, stream=stream)
+
+
+class AttnCase:
+    kernel = "attention"
+
+    def __init__(self, tag, B, H, Tq, Tk, masked, rng, hip, ops):
+        self.tag, self.B, self.H, self.Tq, self.Tk = tag, B, H, Tq, Tk
+        self.C = H * 64
+        self.ops = ops
+        self.q = hip.DeviceBuffer.from_array(rng.standard_normal(B * Tq * self.C, dtype=np.float32).astype(np.float16))
+        self.k = hip.DeviceBuffer.from_array(rng.standard_normal(B * Tk * self.C, dtype=np.float32).astype(np.float16))
+        self.v = hip.DeviceBuffer.from_array(rng.standard_normal(B * Tk * self.C, dtype=np.float32).astype(np.float16))
+        self.o = hip.DeviceBuffer(B * Tq * self.C * 2)
+        self.kv_len = None
+        if masked:
+            self.kv_len = hip.DeviceBuffer.from_array(rng.integers(1, 78, B).astype(np.int32))
+        # dense Tk (mask not subtracted), softmax/exp not counted
+        self.flops = 4.0 * B * H * Tq * Tk * 64
+        self.bytes = 2.0 * B * (2 * Tq * self.C + 2 * Tk * self.C) + (4 * B if masked else 0)
+
+    def run(self, stream):
+        self.ops.fused_attention_ex(self.q, self.k, self.v, self.o, batch=self.B, Tq=self.Tq, Tk=self.Tk,
+                                    C=self.C, heads=self.H, in_dtype=1, out_dtype=1, kv_len=self.kv_len,
+                                    stream=stream)
+
+
+def roofline_pct(c, seconds):
+    ai = c.flops / c.bytes
+    roof = min(PEAK_FP16_TFLOPS, ai * PEAK_HBM_GBS / 1e3)
+    tf = c.flops / seconds / 1e12
+    return tf, roof, tf / roof
+
+
+def cpu_baseline(threads: int) -> dict:
+    """The oracle's fp32 OpenMP restatement on a bounded sample of the same
+    shapes: 1/32 of each GEMM's rows and 1/64 of each attention's queries."""
+    from oracle import binding as ob
+
+    rng = np.random.default_rng(7)
+    flops = 0.0
+    t_total = 0.0
+    for tag, M, N, K in GEMM_SHAPES:
+        m = max(16, M // 32)
+        A = rng.standard_normal(m * K, dtype=np.float32)
+        blocks = quantize_q8_0(rng.standard_normal(N * K, dtype=np.float32) * 0.02)
+        t0 = time.perf_counter()
+        ob.gemm_nt_q8_0(A, blocks, m, N, K, acc64=False, threads=threads)
+        t_total += time.perf_counter() - t0
+        flops += 2.0 * m * N * K
+    for tag, B, H, Tq, Tk, masked in ATTN_SHAPES:
+        C = H * 64
+        nq = max(16, Tq // 64)
+        q = rng.standard_normal(B * Tq * C, dtype=np.float32)
+        k = rng.standard_normal(B * Tk * C, dtype=np.float32)
+        v = rng.standard_normal(B * Tk * C, dtype=np.float32)
+        kv = rng.integers(1, 78, B).astype(np.int32) if masked else None
+        t0 = time.perf_counter()
+        ob.fused_attention_f32(q, k, v, batch=B, Tq=Tq, Tk=Tk, C=C, heads=H, kv_len=kv, q_rows=nq,
+                               threads=threads)
+        t_total += time.perf_counter() - t0
+        flops += 4.0 * B * H * nq * Tk * 64
+    return {"value": round(flops / t_total / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "seconds": round(t_total, 2),
+            "sample": "oracle fp32 OpenMP restatement (not the reference GLSL shaders: no Vulkan/lavapipe here): "
+                      "every config-1 GEMM shape on M/32 rows, every config-2/3 attention shape on Tq/64 queries"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--reps", type=int, default=20, help="launches per shape for the breakdown")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", choices=["gemm", "attention"], default=None,
+                    help="profile one kernel family (breakdown only)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (multi-GPU sharding is "
+                                   "design-only, see DESIGN.md)"}))
+        return 2
+
+    from sdvk_amd import _lib, hip, ops
+
+    _lib.load()
+    if hip.device_count() < 1:
+        raise SystemExit("no HIP device")
+    rng = np.random.default_rng(1)
+    stream = hip.Stream()
+    cases = []
+    if args.only in (None, "gemm"):
+        cases += [GemmCase(t, M, N, K, rng, hip, ops) for t, M, N, K in GEMM_SHAPES]
+    if args.only in (None, "attention"):
+        cases += [AttnCase(t, B, H, Tq, Tk, m, rng, hip, ops) for t, B, H, Tq, Tk, m in ATTN_SHAPES]
+    hip.synchronize()
+    print(f"[bench] {hip.device_name(0)}: {len(cases)} shapes resident", file=sys.stderr, flush=True)
+
+    for _ in range(args.warmup):
+        for c in cases:
+            c.run(stream)
+    stream.synchronize()
+
+    e0, e1 = hip.Event(), hip.Event()
+    hip.synchronize()
+    e0.record(stream)
+    for _ in range(args.steps):
+        for c in cases:
+            c.run(stream)
+    e1.record(stream)
+    e1.synchronize()
+    hip.synchronize()
+    ms_total = e0.elapsed_ms(e1)
+    step_flops = sum(c.flops for c in cases)
+    value = step_flops * args.steps / (ms_total / 1e3) / 1e12
+    print(f"[bench] timed {args.steps} steps: {ms_total:.3f} ms", file=sys.stderr, flush=True)
+
+    # per-shape breakdown (each shape alone, back-to-back launches, hot cache)
+    breakdown = []
+    fam_time, fam_flops, fam_bytes, fam_launch = {}, {}, {}, {}
+    for c in cases:
+        a, b = hip.Event(), hip.Event()
+        a.record(stream)
+        for _ in range(args.reps):
+            c.run(stream)
+        b.record(stream)
+        b.synchronize()
+        sec = a.elapsed_ms(b) / 1e3 / args.reps
+        tf, roof, frac = roofline_pct(c, sec)
+        breakdown.append({"shape": c.tag, "kernel": c.kernel, "us": round(sec * 1e6, 2), "tflops": round(tf, 2),
+                          "pct_mfma_peak": round(100 * tf / PEAK_FP16_TFLOPS, 2),
+                          "roofline_tflops": round(roof, 1), "pct_of_roofline": round(100 * frac, 2),
+                          "gbs": round(c.bytes / sec / 1e9, 1)})
+        fam_time[c.kernel] = fam_time.get(c.kernel, 0.0) + sec
+        fam_flops[c.kernel] = fam_flops.get(c.kernel, 0.0) + c.flops
+        fam_bytes[c.kernel] = fam_bytes.get(c.kernel, 0.0) + c.bytes
+        fam_launch[c.kernel] = fam_launch.get(c.kernel, 0) + 1
+        print(f"[bench] {c.tag:<28} {sec * 1e6:9.2f} us {tf:8.1f} TFLOP/s {100 * frac:6.1f}% of roofline",
+              file=sys.stderr, flush=True)
+
+    dom = max(fam_time, key=fam_time.get)
+    avg_launch = fam_time[dom] / fam_launch[dom]
+    achieved = fam_flops[dom] / fam_launch[dom] / avg_launch / 1e12
+    traffic = None
+    tfile = ROOT / "profiles" / f"traffic_{dom}.json"
+    if tfile.exists():
+        try:
+            traffic = json.loads(tfile.read_text()).get("bytes_per_launch")
+        except Exception:
+            traffic = None
+    roofline = {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4), "traffic": traffic,
+                "avg_launch_us": round(avg_launch * 1e6, 2),
+                "algorithmic_flop_per_launch": fam_flops[dom] / fam_launch[dom],
+                "algorithmic_bytes_per_launch": fam_bytes[dom] / fam_launch[dom]}
+
+    cpu = None
+    if not args.no_cpu_baseline and args.only is None:
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+        print(f"[bench] cpu baseline on {threads} threads", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(threads)
+
+    out = {
+        "metric": "Q8_0 GEMM & fused-attn TFLOP/s at SDXL-1024 shapes; % of MFMA peak",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_total / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "pct_mfma_peak": round(100 * value / PEAK_FP16_TFLOPS, 2),
+        "config": {"workload": "sdxl1024: Q8_0 GEMM sweep (BASELINE config 1) + fused self/cross attention "
+                               "(configs 2-3), fp32 GEMM I/O, fp16 attention I/O, one pass = 1 step",
+                   "gemm_shapes_MNK": [[M, N, K] for _, M, N, K in GEMM_SHAPES] if args.only != "attention" else [],
+                   "attn_shapes_B_H_Tq_Tk": [[B, H, Tq, Tk] for _, B, H, Tq, Tk, _ in ATTN_SHAPES]
+                   if args.only != "gemm" else [],
+                   "step_gflop": round(step_flops / 1e9, 3)},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "breakdown": breakdown,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,167 @@
+/*
+ * mi_sdvk.h -- C-ABI of the MI355X (gfx950) Q8_0 GEMM and fused-attention
+ * kernels. Drop-in for the two hot operators of sdvk's SDXL UNet.
+ *
+ * Contract shared by every entry point:
+ *   - Pointers are device pointers (hipMalloc'd or offsets into one); the
+ *     caller owns every buffer, the library allocates nothing.
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = the legacy default
+ *     stream) and is asynchronous: results are valid after the stream syncs.
+ *   - The return value is an mi_status (0 = MI_OK). Nothing is printed, no
+ *     entry point exits the process and no C++ exception crosses the ABI
+ *     (the reference's exit(1) paths -- fused_attn.cpp:41-44,
+ *     vk_engine.cpp:1147-1150 -- become MI_ERR_UNSUPPORTED / _INVALID_ARG).
+ *   - mi_last_error() gives a human-readable reason for the calling thread's
+ *     last non-OK status.
+ *   - Entry points are reentrant; calls on one stream execute in order, so
+ *     the reference's single in-order command buffer needs no barriers here.
+ *   - Strides and leading dimensions are in ELEMENTS of the tensor's type.
+ *
+ * Reference interfaces replaced (paths relative to the sdvk source root):
+ *   Engine::dispatch("gemm_nt_q8_v*"/"gemm_nt_q8", {A,Bq,C,S[,bias]}, Pg, ...)
+ *       src/Modules/GPU/vk_engine.cpp:1143-1180, KERNELS[] :55-63,
+ *       push layout Pg src/Modules/Diffusion/sdvkgen.cpp:901-903
+ *   gemmNtQ8 / gemmNtQ8Bias      src/Modules/Diffusion/sdvkgen.cpp:917-936
+ *   fusedAttnSupported / fusedAttention / FusedAttnArgs
+ *       src/Modules/GPU/fused_attn.hpp:13-28, fused_attn.cpp:34-61
+ *   Q8_0 decode (readFloat / readQ8Into) src/Modules/Model/Gguf.cpp:514-583
+ */
+#ifndef MI_SDVK_H
+#define MI_SDVK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum mi_status {
+    MI_OK = 0,
+    MI_ERR_INVALID_ARG = 1,  /* null pointer, bad mode / dtype, size overflow */
+    MI_ERR_UNSUPPORTED = 2,  /* shape the kernels do not serve (head dim > 64, K % 32 != 0, ...) */
+    MI_ERR_ALIGNMENT = 3,    /* pointer or leading-dimension alignment not met */
+    MI_ERR_ALIASING = 4,     /* output overlaps an input */
+    MI_ERR_HIP = 5,          /* HIP runtime error (launch failure, no device) */
+} mi_status;
+
+typedef enum mi_dtype {
+    MI_F32 = 0,
+    MI_F16 = 1,
+} mi_dtype;
+
+/* ---------------------------------------------------------------- misc -- */
+
+/* Text for a status code (static storage). */
+const char* mi_status_string(int status);
+/* Detail for the calling thread's last non-OK status ("" if none). */
+const char* mi_last_error(void);
+/* Library version: major * 10000 + minor * 100 + patch. */
+int mi_version(void);
+
+/* ------------------------------------------------------------ Q8_0 format --
+ * GGUF Q8_0 block: 34 bytes {fp16 d (little-endian), int8 q[32]}; element i of
+ * a tensor lives in block i/32 (flat GGUF order, Gguf.cpp:83, :514-523).
+ *
+ * mi_q8_0_dequant: out[i] = fp32(d) * q (bit-exact with Gguf.cpp:514-523) when
+ *   out_dtype == MI_F32; fp16 round-to-nearest-even of that product when
+ *   MI_F16. n % 32 == 0. blocks: 2-byte aligned; out: 16-byte aligned.
+ * Replaces GgufFile::readFloat's Q8_0 branch (Gguf.cpp:514-523).          */
+int mi_q8_0_dequant(const void* blocks, void* out, int out_dtype, uint64_t n, void* stream);
+
+/* The reference's split device layout (Gguf.cpp:559-583, sdvkgen.cpp:560-586):
+ * payload = int8 values packed 4 per uint32 little-endian in flat order,
+ * scales = fp32, one per 32 flat elements. out[i] = q[i] * scales[i >> 5]
+ * (gemm_nt_q8_v.comp:37-43 deqB). n % 4 == 0; payload and scales 4-byte
+ * aligned, out 16-byte aligned.                                            */
+int mi_q8_split_dequant(const uint32_t* payload, const float* scales, void* out, int out_dtype,
+                        uint64_t n, void* stream);
+
+/* Device-side repack of 34-byte blocks into the split layout (readQ8Into,
+ * Gguf.cpp:559-583: scales[b] = fp32(d_b), payload = q in flat order).
+ * n % 32 == 0; payload 4-byte aligned, scales 4-byte aligned.             */
+int mi_q8_0_to_split(const void* blocks, uint32_t* payload, float* scales, uint64_t n,
+                     void* stream);
+
+/* ---------------------------------------------------------------- GEMM -- *
+ * C[M,N] (=|+=) A[M,K] . deq(W[N,K])^T (+ bias[N])
+ *   A      fp32 row-major, row stride lda (0 -> K), batch stride sA
+ *   C      fp32 row-major, row stride ldc (0 -> N), batch stride sC
+ *   mode 0 stores acc (+ bias[n] when bias != NULL); mode 1 adds acc to C and
+ *          ignores bias (gemm_nt_q8_v.comp:115-127)
+ *   batch  grid z: item z reads A + z*sA and writes C + z*sC; W (and bias)
+ *          are shared by every item (the reference never offsets B)
+ * Arithmetic: A is rounded to fp16, the weight d*q is rounded to fp16, the
+ * products are summed in fp32 by the gfx950 MFMA units; accuracy vs the
+ * reference's fp32 shader is max|err| <= 2e-3 x RMS(C) at the SDXL shapes.
+ * Activations must lie within the fp16 range (|a| < 65504).
+ * Alignment: A 16-byte aligned with lda % 4 == 0 and sA % 4 == 0; C 4-byte
+ * aligned. C must not overlap A, W or bias.
+ * Returns MI_OK for M == 0 || N == 0 (nothing to do); K == 0 stores bias/0.
+ */
+
+/* North-star entry: W is the raw GGUF stream of 34-byte Q8_0 blocks, row n's
+ * K/32 blocks starting at byte n*(K/32)*34. K % 32 == 0 (else
+ * MI_ERR_UNSUPPORTED). W must be 16-byte aligned; it is read in aligned
+ * 16-byte pieces, none of which extends past the 16-byte-aligned end of W.
+ * No reference counterpart consumes blocks directly; it replaces the
+ * load-time split (Gguf.cpp:559-583) + gemm_nt_q8_v dispatch pair.        */
+int mi_gemm_nt_q8_0(const float* A, const void* W, const float* bias, float* C, uint32_t M,
+                    uint32_t N, uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldc,
+                    uint32_t batch, uint64_t sA, uint64_t sC, void* stream);
+
+/* Reference device layout: payload (int8 x4 per uint32, flat [N,K] order) +
+ * fp32 scale per 32 flat elements (any fp32 value: LoRA requantisation writes
+ * non-fp16 scales, sdvkgen.cpp:536-538). K % 4 == 0 (the reference's 4-wide
+ * staging zero-fills otherwise, gemm_nt_q8_v.comp:69,86; rejected here).
+ * Replaces Engine::dispatch("gemm_nt_q8_v[_bm128][_b]", {A, Bq, C, S[, bias]},
+ * Pg{M,N,K,mode,sA,0,sC,batch,lda,0,ldc,0}) (vk_engine.cpp:55-63,
+ * sdvkgen.cpp:917-936).                                                     */
+int mi_gemm_nt_q8_split(const float* A, const uint32_t* payload, const float* scales,
+                        const float* bias, float* C, uint32_t M, uint32_t N, uint32_t K,
+                        uint32_t mode, uint32_t lda, uint32_t ldc, uint32_t batch, uint64_t sA,
+                        uint64_t sC, void* stream);
+
+/* ----------------------------------------------------------- attention -- *
+ * O = softmax(Q K^T / sqrt(hd) + mask) V per head, hd = C / heads <= 64,
+ * never materialising Tq x Tk. Head h occupies columns [h*hd, h*hd + hd) of
+ * every token row. Masked keys: key > query when causal (fused_attn.comp:103);
+ * key >= kv_len[b] (key padding). A query whose keys are all masked gets
+ * O = 0 (fused_attn_tiled.comp:189). Online softmax in fp32; QK^T and PV on
+ * fp16 MFMA with fp32 accumulation.                                         */
+
+/* Same predicate as fusedAttnSupported (fused_attn.cpp:34-38): 1 if heads
+ * divides C and 1 <= C/heads <= 64, else 0.                                */
+int mi_fused_attn_supported(uint32_t C, uint32_t heads);
+
+/* fusedAttention(Engine&, const FusedAttnArgs&) (fused_attn.cpp:40-61):
+ * fp32 q/k/v/out [T, C] contiguous, scale 1/sqrt(C/heads).
+ * q, k, v, out 16-byte aligned; out must not overlap q, k or v.            */
+int mi_fused_attention(const float* q, const float* k, const float* v, float* out, uint32_t Tq,
+                       uint32_t Tk, uint32_t C, uint32_t heads, int causal, void* stream);
+
+/* Extended form: batch, strides, fp16/fp32 I/O and key-padding lengths.
+ * FusedAttnArgs (fused_attn.hpp:13-23) plus the batch / dtype / kv_len
+ * extensions the SDXL configs need.                                         */
+typedef struct mi_attn_args {
+    const void* q;        /* [batch][Tq][ldq] */
+    const void* k;        /* [batch][Tk][ldk] */
+    const void* v;        /* [batch][Tk][ldv] */
+    void* out;            /* [batch][Tq][ldo] */
+    uint32_t batch;       /* >= 1 */
+    uint32_t Tq, Tk, C, heads;
+    int32_t causal;
+    int32_t in_dtype;     /* mi_dtype of q, k, v */
+    int32_t out_dtype;    /* mi_dtype of out */
+    uint64_t ldq, ldk, ldv, ldo;   /* token stride, 0 -> C */
+    uint64_t sq, sk, sv, so;       /* batch stride, 0 -> T * ld */
+    const int32_t* kv_len;         /* device int32[batch] or NULL (all Tk keys) */
+    float scale;                   /* 0 -> 1/sqrt(C/heads) (fused_attn.cpp:55) */
+} mi_attn_args;
+
+int mi_fused_attention_ex(const mi_attn_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MI_SDVK_H */

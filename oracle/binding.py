@@ -1,0 +1,236 @@
+"""numpy front end of the CPU oracle (oracle/liboracle.so) and of the reference
+GGUF reader compiled into oracle/_ref/libgguf_ref.so.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, never by the product package.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+import tempfile
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "liboracle.so"
+REF_LIB = HERE / "_ref" / "libgguf_ref.so"
+OR_F32, OR_F16 = 0, 1
+
+_lib = None
+_ref = None
+
+_vp, _u32, _u64, _i32 = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int32
+
+
+def build() -> None:
+    """Builds liboracle.so (and _ref when /root/reference is present)."""
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        L = ctypes.CDLL(str(LIB))
+        L.or_fp16_to_fp32.restype = ctypes.c_float
+        L.or_fp16_to_fp32.argtypes = [ctypes.c_uint16]
+        L.or_fp32_to_fp16.restype = ctypes.c_uint16
+        L.or_fp32_to_fp16.argtypes = [ctypes.c_float]
+        L.or_gelu_erf.restype = ctypes.c_float
+        L.or_gelu_erf.argtypes = [ctypes.c_float]
+        L.or_fill_normal.argtypes = [_u64, ctypes.c_float, ctypes.c_float, _vp, _u64]
+        L.or_fill_uniform_int.argtypes = [_u64, _i32, _i32, _vp, _u64]
+        L.or_q8_0_quantize.argtypes = [_vp, _u64, _vp]
+        L.or_q8_0_dequant.argtypes = [_vp, _u64, _vp]
+        L.or_q8_0_to_split.argtypes = [_vp, _u64, _vp, _vp]
+        L.or_q8_split_dequant.argtypes = [_vp, _vp, _u64, _vp]
+        L.or_gemm_nt_q8_split.argtypes = [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32,
+                                          _u32, _u64, _u64, ctypes.c_int, ctypes.c_int]
+        L.or_gemm_nt_q8_0.argtypes = [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32,
+                                      _u64, _u64, ctypes.c_int, ctypes.c_int]
+        L.or_gemm_nt_q8_0_rows.argtypes = [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp, _u32,
+                                           ctypes.c_int]
+        L.or_fused_attention.argtypes = [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, ctypes.c_int]
+        L.or_fused_attention_ex.argtypes = [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, ctypes.c_int,
+                                            _u64, _u64, _u64, _u64, _u64, _u64, _u64, _u64, ctypes.c_int,
+                                            ctypes.c_int, _vp, _vp, _u32, ctypes.c_int]
+        L.or_fused_attention_f32.argtypes = [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp, _u32,
+                                             ctypes.c_int]
+        L.or_layernorm.argtypes = [_vp, _vp, _vp, _vp, _u32, _u32, ctypes.c_float]
+        L.or_geglu.argtypes = [_vp, _vp, _u32, _u32]
+        L.or_add.argtypes = [_vp, _vp, _vp, _u64]
+        L.or_max_threads.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def ref_lib() -> ctypes.CDLL | None:
+    """The reference's own Gguf.cpp (None when it was not built here)."""
+    global _ref
+    if _ref is None:
+        if not REF_LIB.exists():
+            return None
+        R = ctypes.CDLL(str(REF_LIB))
+        R.ref_fp16_to_fp32.restype = ctypes.c_float
+        R.ref_fp16_to_fp32.argtypes = [ctypes.c_uint16]
+        R.ref_q8_0_decode.restype = ctypes.c_int
+        R.ref_q8_0_decode.argtypes = [ctypes.c_char_p, _vp, _u64, _u64, _vp, _vp, _vp, _vp, _vp]
+        _ref = R
+    return _ref
+
+
+def _p(a) -> int | None:
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def max_threads() -> int:
+    return int(lib().or_max_threads())
+
+
+# ---------------------------------------------------------------- generators --
+
+def normal(seed: int, n: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    lib().or_fill_normal(seed, mean, std, _p(out), n)
+    return out
+
+
+def uniform_int(seed: int, lo: int, hi: int, n: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.int32)
+    lib().or_fill_uniform_int(seed, lo, hi, _p(out), n)
+    return out
+
+
+# ---------------------------------------------------------------------- Q8_0 --
+
+def q8_0_quantize(w: np.ndarray) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.float32).reshape(-1)
+    assert w.size % 32 == 0
+    blocks = np.empty(w.size // 32 * 34, dtype=np.uint8)
+    lib().or_q8_0_quantize(_p(w), w.size, _p(blocks))
+    return blocks
+
+
+def q8_0_dequant(blocks: np.ndarray, n: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    lib().or_q8_0_dequant(_p(np.ascontiguousarray(blocks)), n, _p(out))
+    return out
+
+
+def q8_0_to_split(blocks: np.ndarray, n: int) -> tuple[np.ndarray, np.ndarray]:
+    payload = np.empty(n, dtype=np.int8)
+    scales = np.empty(n // 32, dtype=np.float32)
+    lib().or_q8_0_to_split(_p(np.ascontiguousarray(blocks)), n, _p(payload), _p(scales))
+    return payload, scales
+
+
+def q8_split_dequant(payload: np.ndarray, scales: np.ndarray, n: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    lib().or_q8_split_dequant(_p(np.ascontiguousarray(payload)), _p(np.ascontiguousarray(scales)), n, _p(out))
+    return out
+
+
+def ref_q8_0_decode(blocks: np.ndarray, rows: int, cols: int):
+    """Runs the reference GgufFile readers on a one-tensor GGUF file."""
+    R = ref_lib()
+    if R is None:
+        return None
+    n = rows * cols
+    out = np.empty(n, dtype=np.float32)
+    q = np.empty(n, dtype=np.int8)
+    s = np.empty(n // 32, dtype=np.float32)
+    q2 = np.empty(n, dtype=np.int8)
+    s2 = np.empty(n // 32, dtype=np.float32)
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "t.gguf").encode()
+        st = R.ref_q8_0_decode(path, _p(np.ascontiguousarray(blocks)), rows, cols, _p(out), _p(q), _p(s),
+                               _p(q2), _p(s2))
+    if st != 0:
+        raise RuntimeError(f"reference GGUF decode failed: {st}")
+    return out, q, s, q2, s2
+
+
+# ---------------------------------------------------------------------- GEMM --
+
+def gemm_nt_q8_0(A: np.ndarray, blocks: np.ndarray, M: int, N: int, K: int, *, bias=None, C=None,
+                 mode: int = 0, lda: int = 0, ldc: int = 0, batch: int = 1, sA: int = 0, sC: int = 0,
+                 acc64: bool = True, threads: int = 1) -> np.ndarray:
+    ldc_e = ldc or N
+    if C is None:
+        C = np.zeros(((batch - 1) * sC + (M - 1) * ldc_e + N) if batch > 1 else M * ldc_e, dtype=np.float32)
+    lib().or_gemm_nt_q8_0(_p(A), _p(blocks), _p(bias), _p(C), M, N, K, mode, lda, ldc, batch, sA, sC,
+                          1 if acc64 else 0, threads)
+    return C
+
+
+def gemm_nt_q8_split(A, payload, scales, M, N, K, *, bias=None, C=None, mode=0, lda=0, ldc=0, batch=1,
+                     sA=0, sC=0, acc64=True, threads=1) -> np.ndarray:
+    ldc_e = ldc or N
+    if C is None:
+        C = np.zeros(((batch - 1) * sC + (M - 1) * ldc_e + N) if batch > 1 else M * ldc_e, dtype=np.float32)
+    lib().or_gemm_nt_q8_split(_p(A), _p(payload), _p(scales), _p(bias), _p(C), M, N, K, mode, lda, ldc,
+                              batch, sA, sC, 1 if acc64 else 0, threads)
+    return C
+
+
+def gemm_rows(A, blocks, M, N, K, rows, *, bias=None, lda=0, threads=1) -> np.ndarray:
+    rows = np.ascontiguousarray(rows, dtype=np.uint32)
+    C = np.zeros(len(rows) * N, dtype=np.float32)
+    lib().or_gemm_nt_q8_0_rows(_p(A), _p(blocks), _p(bias), _p(C), M, N, K, lda, 0, _p(rows), len(rows),
+                               threads)
+    return C.reshape(len(rows), N)
+
+
+# ----------------------------------------------------------------- attention --
+
+def fused_attention(q, k, v, Tq, Tk, C, heads, causal=False) -> np.ndarray:
+    out = np.zeros(Tq * C, dtype=np.float32)
+    lib().or_fused_attention(_p(q), _p(k), _p(v), _p(out), Tq, Tk, C, heads, 1 if causal else 0)
+    return out
+
+
+def fused_attention_ex(q, k, v, *, batch, Tq, Tk, C, heads, causal=False, in_dtype=OR_F32,
+                       out_dtype=OR_F32, kv_len=None, rows=None, threads=1) -> np.ndarray:
+    """Contiguous [batch, T, C] inputs; returns [batch, nrows, C] (all rows when rows is None)."""
+    nr = Tq if rows is None else len(rows)
+    odt = np.float32 if out_dtype == OR_F32 else np.float16
+    out = np.zeros(batch * nr * C, dtype=odt)
+    kl = None if kv_len is None else np.ascontiguousarray(kv_len, dtype=np.int32)
+    rw = None if rows is None else np.ascontiguousarray(rows, dtype=np.uint32)
+    lib().or_fused_attention_ex(_p(q), _p(k), _p(v), _p(out), batch, Tq, Tk, C, heads, 1 if causal else 0,
+                                C, C, C, C, Tq * C, Tk * C, Tk * C, nr * C, in_dtype, out_dtype, _p(kl), _p(rw),
+                                nr, threads)
+    return out.reshape(batch, nr, C)
+
+
+def fused_attention_f32(q, k, v, *, batch, Tq, Tk, C, heads, kv_len=None, q_rows=None, threads=1):
+    out = np.zeros(batch * Tq * C, dtype=np.float32)
+    kl = None if kv_len is None else np.ascontiguousarray(kv_len, dtype=np.int32)
+    lib().or_fused_attention_f32(_p(q), _p(k), _p(v), _p(out), batch, Tq, Tk, C, heads, _p(kl),
+                                 Tq if q_rows is None else q_rows, threads)
+    return out
+
+
+# ---------------------------------------------------------------------- glue --
+
+def layernorm(x, gamma, beta, rows, d, eps=1e-5):
+    y = np.empty(rows * d, dtype=np.float32)
+    lib().or_layernorm(_p(x), _p(gamma), _p(beta), _p(y), rows, d, eps)
+    return y
+
+
+def gelu_erf(x: float) -> float:
+    return float(lib().or_gelu_erf(x))
+
+
+def geglu(h, rows, F):
+    y = np.empty(rows * F, dtype=np.float32)
+    lib().or_geglu(_p(h), _p(y), rows, F)
+    return y

@@ -1,0 +1,94 @@
+"""ctypes binding of libmi_sdvk.so (declarations in include/mi_sdvk.h).
+
+Loading fails loudly when the library has not been built: there is no CPU
+fallback for any operator.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+from . import hip
+
+LIB_PATH = Path(__file__).resolve().parent / "libmi_sdvk.so"
+
+MI_OK, MI_ERR_INVALID_ARG, MI_ERR_UNSUPPORTED, MI_ERR_ALIGNMENT, MI_ERR_ALIASING, MI_ERR_HIP = range(6)
+MI_F32, MI_F16 = 0, 1
+
+# Every function declared in include/mi_sdvk.h, with its ctypes signature.
+_u32, _u64, _i32, _vp = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int32, ctypes.c_void_p
+
+
+class MiAttnArgs(ctypes.Structure):
+    """Mirror of mi_attn_args (include/mi_sdvk.h)."""
+    _fields_ = [
+        ("q", _vp), ("k", _vp), ("v", _vp), ("out", _vp),
+        ("batch", _u32), ("Tq", _u32), ("Tk", _u32), ("C", _u32), ("heads", _u32),
+        ("causal", _i32), ("in_dtype", _i32), ("out_dtype", _i32),
+        ("ldq", _u64), ("ldk", _u64), ("ldv", _u64), ("ldo", _u64),
+        ("sq", _u64), ("sk", _u64), ("sv", _u64), ("so", _u64),
+        ("kv_len", _vp),
+        ("scale", ctypes.c_float),
+    ]
+
+
+SIGNATURES = {
+    "mi_status_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "mi_last_error": (ctypes.c_char_p, []),
+    "mi_version": (ctypes.c_int, []),
+    "mi_q8_0_dequant": (ctypes.c_int, [_vp, _vp, ctypes.c_int, _u64, _vp]),
+    "mi_q8_split_dequant": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_int, _u64, _vp]),
+    "mi_q8_0_to_split": (ctypes.c_int, [_vp, _vp, _vp, _u64, _vp]),
+    "mi_gemm_nt_q8_0": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32,
+                                       _u64, _u64, _vp]),
+    "mi_gemm_nt_q8_split": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32,
+                                           _u32, _u64, _u64, _vp]),
+    "mi_fused_attn_supported": (ctypes.c_int, [_u32, _u32]),
+    "mi_fused_attention": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, ctypes.c_int, _vp]),
+    "mi_fused_attention_ex": (ctypes.c_int, [ctypes.POINTER(MiAttnArgs), _vp]),
+}
+
+_lib = None
+
+
+class MiError(RuntimeError):
+    def __init__(self, status: int, fn: str, detail: str):
+        self.status = status
+        super().__init__(f"{fn}: {status_string(status)} ({detail})")
+
+
+def load() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise ImportError(f"{LIB_PATH} is not built: run `python -m sdvk_amd.build` "
+                              "(or __graft_entry__.build()); there is no fallback path")
+        hip.lib()  # bind ROCm's HIP runtime first so the library reuses it
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def status_string(status: int) -> str:
+    return load().mi_status_string(status).decode()
+
+
+def call(name: str, *args) -> None:
+    """Calls `name`; raises MiError with mi_last_error() on a non-OK status."""
+    lib = load()
+    st = getattr(lib, name)(*args)
+    if st != MI_OK:
+        raise MiError(st, name, lib.mi_last_error().decode())
+
+
+def ptr(x) -> int | None:
+    """Device address of a DeviceBuffer / int / None."""
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    return x.value

@@ -1,0 +1,322 @@
+// attention.hip -- fused attention for gfx950: O = softmax(Q K^T * scale + mask) V
+//
+// Reference behaviour: src/Modules/GPU/fused_attn.cpp:34-61 (support predicate,
+// scale 1/sqrt(hd)), shaders/fused_attn_tiled.comp and fused_attn.comp (causal
+// and Tk bounds masks, O = 0 when the running sum is 0). The reference's two
+// kernels (tiled for Tk >= 256, per-key butterfly otherwise) become one kernel
+// here; the algorithm is our own:
+//
+//   * a workgroup owns 128 queries of one (batch, head): 4 waves x 32 queries;
+//   * K and V tiles of 64 keys are staged in LDS as fp16 (double-buffered, the
+//     next tile's global loads in flight during the current tile's math);
+//   * each wave computes S^T = K Q^T with v_mfma_f32_32x32x16_f16 so that a lane
+//     owns one query and 32 of the tile's keys: the row max and row sum are
+//     in-register reductions plus one exchange with the partner lane (lane ^ 32);
+//   * online softmax in fp32 in the exp2 domain (scale * log2 e folded into one
+//     FMA per score), masked scores are -inf, all-masked rows give O = 0;
+//   * O^T = V^T P^T on the same MFMA: P stays in registers (the S^T output
+//     layout is, key for key, the B-operand layout the PV product needs); V is
+//     stored in LDS as [key/4][d][key%4] so each A fragment is two 8-byte reads.
+#include "common.hpp"
+
+namespace mi {
+namespace {
+
+constexpr int kBQ = 128;   // queries per workgroup
+constexpr int kBKV = 64;   // keys per tile
+constexpr int kKld = 72;   // K tile LDS row stride (halves): 64 d + 8 pad
+constexpr int kThreads = 256;
+
+struct AttnArgs {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+    uint32_t Tq, Tk, heads, hd;
+    int causal;
+    uint64_t ldq, ldk, ldv, ldo, sq, sk, sv, so;
+    const int32_t* kv_len;
+    float c;  // scale * log2(e)
+};
+
+template <typename T>
+__device__ __forceinline__ half8 load8(const T* p, bool vec, int valid) {
+    half8 h;
+    if (vec) {
+        if constexpr (sizeof(T) == 2) {
+            h = *reinterpret_cast<const half8*>(p);
+        } else {
+            floatx4 a = reinterpret_cast<const floatx4*>(p)[0];
+            floatx4 b = reinterpret_cast<const floatx4*>(p)[1];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                h[i] = static_cast<_Float16>(a[i]);
+                h[4 + i] = static_cast<_Float16>(b[i]);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) h[i] = i < valid ? static_cast<_Float16>(p[i]) : static_cast<_Float16>(0.0f);
+    }
+    return h;
+}
+
+template <typename TI, typename TO, bool VEC>
+__global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
+    __shared__ _Float16 Ks[2][kBKV * kKld];
+    __shared__ _Float16 Vs[2][kBKV * 64];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, g = lane >> 5;
+    const uint32_t b = blockIdx.z, h = blockIdx.y;
+    const uint32_t qcta = blockIdx.x * kBQ;
+    const uint32_t qi = qcta + wave * 32 + l32;  // this lane's query
+    const int hd = static_cast<int>(a.hd);
+
+    uint32_t L = a.Tk;
+    if (a.kv_len) {
+        int32_t l = a.kv_len[b];
+        L = l < 0 ? 0u : (static_cast<uint32_t>(l) < a.Tk ? static_cast<uint32_t>(l) : a.Tk);
+    }
+    uint32_t kend = L;
+    if (a.causal) kend = min(kend, qcta + kBQ);  // keys past the CTA's last query are all masked
+
+    const TI* Qp = static_cast<const TI*>(a.q) + b * a.sq + static_cast<uint64_t>(h) * a.hd;
+    const TI* Kp = static_cast<const TI*>(a.k) + b * a.sk + static_cast<uint64_t>(h) * a.hd;
+    const TI* Vp = static_cast<const TI*>(a.v) + b * a.sv + static_cast<uint64_t>(h) * a.hd;
+
+    // Q^T fragments (B operand): d = 16 s + 8 g .. +8 of query qi
+    half8 qf[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const int d0 = 16 * s + 8 * g;
+        const int valid = hd - d0;
+        if (qi < a.Tq && valid > 0)
+            qf[s] = load8(Qp + static_cast<uint64_t>(qi) * a.ldq + d0, VEC, valid);
+        else
+            qf[s] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+
+    // Staging: a tile is 64 keys x 8 chunks of 8 d for K and for V; thread
+    // handles chunks tid and tid + 256 (key = c / 8, d0 = 8 (c % 8)).
+    half8 kreg[2], vreg[2];
+    auto load_tile = [&](uint32_t kv0) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int c = tid + i * kThreads;
+            const uint32_t key = kv0 + (c >> 3);
+            const int d0 = (c & 7) * 8;
+            const int valid = hd - d0;
+            if (key < L && valid > 0) {
+                kreg[i] = load8(Kp + static_cast<uint64_t>(key) * a.ldk + d0, VEC, valid);
+                vreg[i] = load8(Vp + static_cast<uint64_t>(key) * a.ldv + d0, VEC, valid);
+            } else {
+                kreg[i] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+                vreg[i] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+            }
+        }
+    };
+    auto store_tile = [&](int st) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int c = tid + i * kThreads;
+            const int key = c >> 3, d0 = (c & 7) * 8;
+            *reinterpret_cast<half8*>(&Ks[st][key * kKld + d0]) = kreg[i];
+            _Float16* vb = &Vs[st][((key >> 2) * 64 + d0) * 4 + (key & 3)];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) vb[e * 4] = vreg[i][e];
+        }
+    };
+
+    floatx16 o[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[u][r] = 0.0f;
+    float m = -INFINITY, l = 0.0f;
+
+    if (kend > 0) {
+        load_tile(0);
+        store_tile(0);
+    }
+    __syncthreads();
+
+    int it = 0;
+    for (uint32_t kv0 = 0; kv0 < kend; kv0 += kBKV, ++it) {
+        const int st = it & 1;
+        const bool more = kv0 + kBKV < kend;
+        if (more) load_tile(kv0 + kBKV);
+
+        // S^T tile: rows = keys kv0 + 32 t + 8(r/4) + 4 g + r%4, column = query qi
+        floatx16 sc[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sc[t][r] = 0.0f;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                half8 kf = *reinterpret_cast<const half8*>(&Ks[st][(32 * t + l32) * kKld + 16 * s + 8 * g]);
+                sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], sc[t], 0, 0, 0);
+            }
+        }
+
+        const bool need_mask = (kv0 + kBKV > L) || (a.causal && kv0 + kBKV - 1 > qcta + wave * 32);
+        if (need_mask) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t key = kv0 + 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
+                    if (key >= L || (a.causal && key > qi)) sc[t][r] = -INFINITY;
+                }
+        }
+
+        float mx = sc[0][0];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[t][r]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m, mx * a.c);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m - m_use);
+        m = m_new;
+        l *= alpha;
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[u][r] *= alpha;
+
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int sp = 0; sp < 2; ++sp) {
+                half8 pf;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[t][8 * sp + i], a.c, -m_use));
+                    l += p;
+                    pf[i] = static_cast<_Float16>(p);
+                }
+                const int kg = 8 * t + 4 * sp + g;  // key group of slots 0-3; slots 4-7 are kg + 2
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const int d = 32 * u + l32;
+                    half4 v0 = *reinterpret_cast<const half4*>(&Vs[st][(kg * 64 + d) * 4]);
+                    half4 v1 = *reinterpret_cast<const half4*>(&Vs[st][((kg + 2) * 64 + d) * 4]);
+                    half8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                    o[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, o[u], 0, 0, 0);
+                }
+            }
+        }
+
+        if (more) store_tile(st ^ 1);
+        __syncthreads();
+    }
+
+    const float lt = l + __shfl_xor(l, 32);
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    if (qi >= a.Tq) return;
+    TO* Op = static_cast<TO*>(a.o) + b * a.so + static_cast<uint64_t>(qi) * a.ldo + static_cast<uint64_t>(h) * a.hd;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int run = 0; run < 4; ++run) {
+            const int d0 = 32 * u + 8 * run + 4 * g;
+            if (VEC && d0 + 4 <= hd) {
+                if constexpr (sizeof(TO) == 4) {
+                    *reinterpret_cast<floatx4*>(Op + d0) =
+                        floatx4{o[u][4 * run] * inv, o[u][4 * run + 1] * inv, o[u][4 * run + 2] * inv, o[u][4 * run + 3] * inv};
+                } else {
+                    *reinterpret_cast<half4*>(Op + d0) =
+                        half4{static_cast<_Float16>(o[u][4 * run] * inv), static_cast<_Float16>(o[u][4 * run + 1] * inv),
+                              static_cast<_Float16>(o[u][4 * run + 2] * inv), static_cast<_Float16>(o[u][4 * run + 3] * inv)};
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (d0 + e < hd) Op[d0 + e] = static_cast<TO>(o[u][4 * run + e] * inv);
+            }
+        }
+}
+
+template <typename TI, typename TO>
+void launch_typed(const AttnArgs& a, uint32_t batch, bool vec, hipStream_t s) {
+    dim3 grid(ceil_div(a.Tq, kBQ), a.heads, batch);
+    if (vec) attn_kernel<TI, TO, true><<<grid, kThreads, 0, s>>>(a);
+    else attn_kernel<TI, TO, false><<<grid, kThreads, 0, s>>>(a);
+}
+
+int run(const mi_attn_args& x, hipStream_t s, const char* fn) {
+    if (!x.q || !x.k || !x.v || !x.out) return fail(MI_ERR_INVALID_ARG, "%s: null pointer", fn);
+    if (x.in_dtype != MI_F32 && x.in_dtype != MI_F16) return fail(MI_ERR_INVALID_ARG, "%s: in_dtype %d", fn, x.in_dtype);
+    if (x.out_dtype != MI_F32 && x.out_dtype != MI_F16) return fail(MI_ERR_INVALID_ARG, "%s: out_dtype %d", fn, x.out_dtype);
+    if (x.batch == 0) return fail(MI_ERR_INVALID_ARG, "%s: batch 0", fn);
+    if (!mi_fused_attn_supported(x.C, x.heads))
+        return fail(MI_ERR_UNSUPPORTED, "%s: unsupported C=%u heads=%u (need heads | C and C/heads <= 64)", fn, x.C, x.heads);
+    if (x.batch > 65535 || x.heads > 65535) return fail(MI_ERR_UNSUPPORTED, "%s: batch/heads > 65535", fn);
+    if (x.Tq == 0) return MI_OK;
+    const uint64_t ldq = x.ldq ? x.ldq : x.C, ldk = x.ldk ? x.ldk : x.C, ldv = x.ldv ? x.ldv : x.C,
+                   ldo = x.ldo ? x.ldo : x.C;
+    if (ldq < x.C || ldk < x.C || ldv < x.C || ldo < x.C) return fail(MI_ERR_INVALID_ARG, "%s: token stride < C", fn);
+    const uint64_t sq = x.sq ? x.sq : x.Tq * ldq, sk = x.sk ? x.sk : x.Tk * ldk, sv = x.sv ? x.sv : x.Tk * ldv,
+                   so = x.so ? x.so : x.Tq * ldo;
+    const uint64_t ei = x.in_dtype == MI_F32 ? 4 : 2, eo = x.out_dtype == MI_F32 ? 4 : 2;
+    const uint64_t obytes = ((x.batch - 1) * so + (x.Tq - 1) * ldo + x.C) * eo;
+    const uint64_t qbytes = ((x.batch - 1) * sq + (x.Tq - 1) * ldq + x.C) * ei;
+    const uint64_t kbytes = x.Tk ? ((x.batch - 1) * sk + (x.Tk - 1) * ldk + x.C) * ei : 0;
+    const uint64_t vbytes = x.Tk ? ((x.batch - 1) * sv + (x.Tk - 1) * ldv + x.C) * ei : 0;
+    if (overlaps(x.out, obytes, x.q, qbytes) || overlaps(x.out, obytes, x.k, kbytes) ||
+        overlaps(x.out, obytes, x.v, vbytes))
+        return fail(MI_ERR_ALIASING, "%s: out overlaps q, k or v", fn);
+    if (!aligned(x.q, ei) || !aligned(x.k, ei) || !aligned(x.v, ei) || !aligned(x.out, eo))
+        return fail(MI_ERR_ALIGNMENT, "%s: tensors must be aligned to their element size", fn);
+
+    AttnArgs a;
+    a.q = x.q; a.k = x.k; a.v = x.v; a.o = x.out;
+    a.Tq = x.Tq; a.Tk = x.Tk; a.heads = x.heads; a.hd = x.C / x.heads;
+    a.causal = x.causal ? 1 : 0;
+    a.ldq = ldq; a.ldk = ldk; a.ldv = ldv; a.ldo = ldo;
+    a.sq = sq; a.sk = sk; a.sv = sv; a.so = so;
+    a.kv_len = x.kv_len;
+    const float scale = x.scale != 0.0f ? x.scale : 1.0f / sqrtf(static_cast<float>(a.hd));
+    a.c = scale * 1.4426950408889634f;
+
+    // 16-byte vector path: every 8-element chunk of every row is 16-byte aligned.
+    const uintptr_t vin = 8 * ei, vout = 4 * eo;
+    const bool vec = a.hd % 8 == 0 && aligned(x.q, 16) && aligned(x.k, 16) && aligned(x.v, 16) &&
+                     aligned(x.out, vout) && (ldq * ei) % 16 == 0 && (ldk * ei) % 16 == 0 && (ldv * ei) % 16 == 0 &&
+                     (sq * ei) % 16 == 0 && (sk * ei) % 16 == 0 && (sv * ei) % 16 == 0 && (ldo * eo) % vout == 0 &&
+                     (so * eo) % vout == 0 && (a.hd * ei) % vin == 0;
+    if (x.in_dtype == MI_F16 && x.out_dtype == MI_F16) launch_typed<_Float16, _Float16>(a, x.batch, vec, s);
+    else if (x.in_dtype == MI_F16) launch_typed<_Float16, float>(a, x.batch, vec, s);
+    else if (x.out_dtype == MI_F16) launch_typed<float, _Float16>(a, x.batch, vec, s);
+    else launch_typed<float, float>(a, x.batch, vec, s);
+    return check_launch(fn);
+}
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" int mi_fused_attn_supported(uint32_t C, uint32_t heads) {
+    if (!C || !heads || C % heads) return 0;
+    uint32_t hd = C / heads;
+    return hd > 0 && hd <= 64 ? 1 : 0;
+}
+
+extern "C" int mi_fused_attention(const float* q, const float* k, const float* v, float* out, uint32_t Tq,
+                                  uint32_t Tk, uint32_t C, uint32_t heads, int causal, void* stream) {
+    mi_attn_args x{};
+    x.q = q; x.k = k; x.v = v; x.out = out;
+    x.batch = 1; x.Tq = Tq; x.Tk = Tk; x.C = C; x.heads = heads; x.causal = causal;
+    x.in_dtype = MI_F32; x.out_dtype = MI_F32;
+    return run(x, static_cast<hipStream_t>(stream), "mi_fused_attention");
+}
+
+extern "C" int mi_fused_attention_ex(const mi_attn_args* args, void* stream) {
+    if (!args) return fail(MI_ERR_INVALID_ARG, "mi_fused_attention_ex: null args");
+    return run(*args, static_cast<hipStream_t>(stream), "mi_fused_attention_ex");
+}

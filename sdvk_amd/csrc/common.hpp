@@ -1,0 +1,65 @@
+// common.hpp -- shared types, status plumbing and small device helpers for the
+// gfx950 kernels behind include/mi_sdvk.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+
+#include "mi_sdvk.h"
+
+namespace mi {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2 __attribute__((ext_vector_type(2)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+// ------------------------------------------------------------- host status --
+
+// Records a thread-local reason and returns `code` (used as `return fail(...)`).
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// Maps the launch's hipGetLastError() to MI_ERR_HIP (with its text) or MI_OK.
+int check_launch(const char* what);
+
+inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+// [a, a+na) and [b, b+nb) overlap (byte ranges); empty ranges never overlap.
+inline bool overlaps(const void* a, uint64_t na, const void* b, uint64_t nb) {
+    if (!a || !b || na == 0 || nb == 0) return false;
+    uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+    return x < y + nb && y < x + na;
+}
+
+inline unsigned ceil_div(uint64_t a, uint64_t b) { return static_cast<unsigned>((a + b - 1) / b); }
+
+// ----------------------------------------------------------- device helpers --
+
+// fp16 bit pattern -> fp32, exact for every pattern (subnormals scaled by
+// 2^-24 explicitly so the result does not depend on the denormal mode).
+__device__ __forceinline__ float fp16_bits_to_f32(uint32_t h) {
+    uint32_t sign = (h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1fu;
+    uint32_t m = h & 0x3ffu;
+    if (e == 0) {
+        float v = static_cast<float>(m) * 5.9604644775390625e-8f;  // m * 2^-24
+        return __uint_as_float(__float_as_uint(v) | sign);
+    }
+    uint32_t bits = (e == 0x1fu) ? (sign | 0x7f800000u | (m << 13)) : (sign | ((e + 112u) << 23) | (m << 13));
+    return __uint_as_float(bits);
+}
+
+// Remaps a linear workgroup id so that consecutive logical tiles land on the
+// same XCD. The dispatcher hands workgroup b to XCD b % 8; tiles that share an
+// operand should share that XCD's L2.
+__device__ __forceinline__ unsigned xcd_swizzle(unsigned b, unsigned nb) {
+    constexpr unsigned kXcd = 8;
+    unsigned xcd = b % kXcd, local = b / kXcd;
+    unsigned per = nb / kXcd, rem = nb % kXcd;
+    return xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+}
+
+}  // namespace mi

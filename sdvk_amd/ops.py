@@ -1,0 +1,163 @@
+"""Host-side mirror of sdvk's operator surface for the Q8 GEMM / fused attention.
+
+Names, argument meaning and error behaviour follow the reference
+(paths relative to the sdvk source root):
+
+  FusedAttnArgs, fused_attn_supported, fused_attention
+      src/Modules/GPU/fused_attn.hpp:13-28, fused_attn.cpp:34-61
+  gemm_nt_q8 / gemm_nt_q8_bias (split int8 + fp32-scale layout)
+      src/Modules/Diffusion/sdvkgen.cpp:917-936
+  Pg push layout + dispatch(kernel_name, bufs, push)
+      sdvkgen.cpp:901-903, vk_engine.cpp:1143-1180, KERNELS[] :55-63,123-124
+
+Where the reference calls exit(1) (unsupported attention shape, binding-count
+mismatch) these raise MiError / ValueError instead. Every call goes to
+libmi_sdvk.so; nothing here computes on the CPU.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+from . import _lib
+from ._lib import MI_F16, MI_F32, MiAttnArgs, MiError, call, ptr
+
+__all__ = [
+    "MiError", "MI_F32", "MI_F16", "FusedAttnArgs", "fused_attn_supported", "fused_attention",
+    "fused_attention_ex", "gemm_nt_q8", "gemm_nt_q8_bias", "gemm_nt_q8_0", "q8_0_dequant",
+    "q8_split_dequant", "q8_0_to_split", "Pg", "dispatch", "KERNELS",
+]
+
+
+def _s(stream) -> Optional[int]:
+    if stream is None:
+        return None
+    return stream.handle.value if hasattr(stream, "handle") else int(stream)
+
+
+# ------------------------------------------------------------------ attention --
+
+@dataclass
+class FusedAttnArgs:
+    """fused_attn.hpp:13-23: fp32 [T, C] buffers, heads interleaved inside C."""
+    q: object = None
+    k: object = None
+    v: object = None
+    out: object = None
+    Tq: int = 0
+    Tk: int = 0
+    C: int = 0
+    heads: int = 1
+    causal: bool = False
+
+
+def fused_attn_supported(C: int, heads: int) -> bool:
+    """fused_attn.cpp:34-38: heads divides C and 1 <= C/heads <= 64."""
+    return bool(_lib.load().mi_fused_attn_supported(C, heads))
+
+
+def fused_attention(a: FusedAttnArgs, stream=None) -> None:
+    """fused_attn.cpp:40-61. Raises MiError(MI_ERR_UNSUPPORTED) where the
+    reference prints and exits."""
+    call("mi_fused_attention", ptr(a.q), ptr(a.k), ptr(a.v), ptr(a.out), a.Tq, a.Tk, a.C, a.heads,
+         1 if a.causal else 0, _s(stream))
+
+
+def fused_attention_ex(q, k, v, out, *, batch: int, Tq: int, Tk: int, C: int, heads: int,
+                       causal: bool = False, in_dtype: int = MI_F32, out_dtype: int = MI_F32,
+                       ldq: int = 0, ldk: int = 0, ldv: int = 0, ldo: int = 0, sq: int = 0,
+                       sk: int = 0, sv: int = 0, so: int = 0, kv_len=None, scale: float = 0.0,
+                       stream=None) -> None:
+    """Batched / strided / fp16 / key-padded form (mi_fused_attention_ex)."""
+    x = MiAttnArgs(q=ptr(q), k=ptr(k), v=ptr(v), out=ptr(out), batch=batch, Tq=Tq, Tk=Tk, C=C,
+                   heads=heads, causal=1 if causal else 0, in_dtype=in_dtype, out_dtype=out_dtype,
+                   ldq=ldq, ldk=ldk, ldv=ldv, ldo=ldo, sq=sq, sk=sk, sv=sv, so=so,
+                   kv_len=ptr(kv_len), scale=scale)
+    call("mi_fused_attention_ex", ctypes.byref(x), _s(stream))
+
+
+# ------------------------------------------------------------------------ GEMM --
+
+def gemm_nt_q8(A, Bq, C, Bs, M: int, N: int, K: int, *, mode: int = 0, lda: int = 0, ldc: int = 0,
+               batch: int = 1, sA: int = 0, sC: int = 0, stream=None) -> None:
+    """sdvkgen.cpp:917-926 gemmNtQ8: C = A . deq(Bq, Bs)^T on the split layout."""
+    call("mi_gemm_nt_q8_split", ptr(A), ptr(Bq), ptr(Bs), None, ptr(C), M, N, K, mode, lda, ldc,
+         batch, sA, sC, _s(stream))
+
+
+def gemm_nt_q8_bias(A, Bq, C, Bs, bias, M: int, N: int, K: int, *, mode: int = 0, lda: int = 0,
+                    ldc: int = 0, batch: int = 1, sA: int = 0, sC: int = 0, stream=None) -> None:
+    """sdvkgen.cpp:928-936 gemmNtQ8Bias: as gemm_nt_q8, + bias[n] in mode 0."""
+    call("mi_gemm_nt_q8_split", ptr(A), ptr(Bq), ptr(Bs), ptr(bias), ptr(C), M, N, K, mode, lda,
+         ldc, batch, sA, sC, _s(stream))
+
+
+def gemm_nt_q8_0(A, W, C, M: int, N: int, K: int, *, bias=None, mode: int = 0, lda: int = 0,
+                 ldc: int = 0, batch: int = 1, sA: int = 0, sC: int = 0, stream=None) -> None:
+    """North-star entry: W is the raw stream of 34-byte GGUF Q8_0 blocks."""
+    call("mi_gemm_nt_q8_0", ptr(A), ptr(W), ptr(bias), ptr(C), M, N, K, mode, lda, ldc, batch, sA,
+         sC, _s(stream))
+
+
+# ------------------------------------------------------------------ Q8_0 utils --
+
+def q8_0_dequant(blocks, out, n: int, out_dtype: int = MI_F32, stream=None) -> None:
+    """Gguf.cpp:514-523 on the device (fp32 bit-exact)."""
+    call("mi_q8_0_dequant", ptr(blocks), ptr(out), out_dtype, n, _s(stream))
+
+
+def q8_split_dequant(payload, scales, out, n: int, out_dtype: int = MI_F32, stream=None) -> None:
+    call("mi_q8_split_dequant", ptr(payload), ptr(scales), ptr(out), out_dtype, n, _s(stream))
+
+
+def q8_0_to_split(blocks, payload, scales, n: int, stream=None) -> None:
+    """Gguf.cpp:559-583 (readQ8Into) on the device."""
+    call("mi_q8_0_to_split", ptr(blocks), ptr(payload), ptr(scales), n, _s(stream))
+
+
+# --------------------------------------------- reference kernel-name dispatch --
+
+@dataclass
+class Pg:
+    """sdvkgen.cpp:901-903 / gemm_q8_bench.cpp:19-21 push layout (48 bytes)."""
+    M: int
+    N: int
+    K: int
+    mode: int = 0
+    sA: int = 0
+    sB: int = 0
+    sC: int = 0
+    batch: int = 1
+    lda: int = 0
+    ldb: int = 0
+    ldc: int = 0
+    pad: int = 0
+
+
+# name -> number of bindings (vk_engine.cpp:55-63,123-124)
+KERNELS = {
+    "gemm_nt_q8": 4, "gemm_nt_q8_v": 4, "gemm_nt_q8_v_bm128": 4, "gemm_nt_q8_v_bk32": 4,
+    "gemm_nt_q8_v_bm128_bk32": 4, "gemm_nt_q8_v_b": 5, "gemm_nt_q8_v_bm128_b": 5,
+    "fused_attn": 4, "fused_attn_tiled": 4,
+}
+
+
+def dispatch(kernel: str, bufs: Sequence, push, stream=None) -> None:
+    """Engine::dispatch(kernelName, {BufRef...}, push) for the kernels this
+    library replaces. Tile-size variants (_bm128, _bk32) all map to the same
+    MFMA kernel; the grid is chosen here, so no gx/gy/gz arguments."""
+    if kernel not in KERNELS:
+        raise ValueError(f"unknown kernel {kernel}")
+    if len(bufs) != KERNELS[kernel]:
+        raise ValueError(f"kernel {kernel} expects {KERNELS[kernel]} bindings, got {len(bufs)}")
+    if kernel.startswith("gemm_nt_q8"):
+        A, Bq, C, S = bufs[:4]
+        bias = bufs[4] if len(bufs) == 5 else None
+        pc: Pg = push
+        call("mi_gemm_nt_q8_split", ptr(A), ptr(Bq), ptr(S), ptr(bias), ptr(C), pc.M, pc.N, pc.K,
+             pc.mode, pc.lda, pc.ldc, max(pc.batch, 1), pc.sA, pc.sC, _s(stream))
+    else:
+        q, k, v, o = bufs
+        a: FusedAttnArgs = push
+        fused_attention(FusedAttnArgs(q, k, v, o, a.Tq, a.Tk, a.C, a.heads, a.causal), stream)

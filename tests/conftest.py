@@ -1,0 +1,34 @@
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU and the built libmi_sdvk.so")
+
+
+@pytest.fixture(scope="session")
+def gpu():
+    """The HIP device. On a GPU run a missing device or library is a failure,
+    never a skip: the product path has no fallback."""
+    from sdvk_amd import _lib, hip
+
+    n = hip.device_count()
+    assert n >= 1, "no HIP device visible"
+    lib = _lib.load()
+    name = hip.device_name(0)
+    print(f"[gpu] device 0: {name}; libmi_sdvk version {lib.mi_version()}", flush=True)
+    return lib
+
+
+@pytest.fixture(scope="session")
+def oracle():
+    from oracle import binding
+
+    binding.lib()
+    return binding

@@ -1,0 +1,97 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol
+include/mi_sdvk.h declares, and rejects bad arguments before touching HIP."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from sdvk_amd import _lib, ops
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "mi_sdvk.h"
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(mi_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    names = declared_functions()
+    for n in ["mi_gemm_nt_q8_0", "mi_gemm_nt_q8_split", "mi_fused_attention", "mi_fused_attention_ex",
+              "mi_fused_attn_supported", "mi_q8_0_dequant", "mi_q8_split_dequant", "mi_q8_0_to_split",
+              "mi_status_string", "mi_last_error", "mi_version"]:
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), f"libmi_sdvk.so does not export {name}"
+        assert name in _lib.SIGNATURES, f"no ctypes signature for {name}"
+
+
+def test_attn_args_struct_layout():
+    # mi_attn_args: 4 pointers, 5 u32, 3 i32, 8 u64, 1 pointer, 1 float (+ tail padding)
+    assert ctypes.sizeof(_lib.MiAttnArgs) == 4 * 8 + 5 * 4 + 3 * 4 + 8 * 8 + 8 + 4 + 4
+
+
+def test_status_strings():
+    lib = _lib.load()
+    assert lib.mi_status_string(0) == b"ok"
+    assert lib.mi_status_string(2) == b"unsupported shape"
+    assert lib.mi_status_string(99) == b"unknown status"
+    assert lib.mi_version() >= 100
+
+
+@pytest.mark.parametrize("C,heads,ok", [(640, 10, True), (1280, 20, True), (320, 8, True), (320, 5, True),
+                                        (64, 1, True), (65, 1, False), (100, 3, False), (0, 1, False),
+                                        (128, 0, False), (130, 2, False)])
+def test_fused_attn_supported_predicate(C, heads, ok):
+    """fused_attn.cpp:34-38: heads | C and 1 <= C/heads <= 64."""
+    assert ops.fused_attn_supported(C, heads) is ok
+
+
+def test_errors_are_returned_not_raised_through_the_abi():
+    lib = _lib.load()
+    # null pointers -> MI_ERR_INVALID_ARG, detail in mi_last_error
+    st = lib.mi_gemm_nt_q8_0(None, None, None, None, 8, 8, 32, 0, 0, 0, 1, 0, 0, None)
+    assert st == _lib.MI_ERR_INVALID_ARG
+    assert b"null" in lib.mi_last_error()
+    # empty problem is a no-op
+    assert lib.mi_gemm_nt_q8_0(None, None, None, None, 0, 8, 32, 0, 0, 0, 1, 0, 0, None) == _lib.MI_OK
+    # K % 32 != 0 on the block entry: unsupported (checked before any device work)
+    fake = 1 << 20
+    st = lib.mi_gemm_nt_q8_0(fake, fake * 2, None, fake * 3, 8, 8, 48, 0, 0, 0, 1, 0, 0, None)
+    assert st == _lib.MI_ERR_UNSUPPORTED
+    # misaligned A
+    st = lib.mi_gemm_nt_q8_0(fake + 4, fake * 2, None, fake * 3, 8, 8, 32, 0, 0, 0, 1, 0, 0, None)
+    assert st == _lib.MI_ERR_ALIGNMENT
+    # C overlapping A
+    st = lib.mi_gemm_nt_q8_0(fake, fake * 2, None, fake + 64, 8, 8, 32, 0, 0, 0, 1, 0, 0, None)
+    assert st == _lib.MI_ERR_ALIASING
+    # bad mode
+    st = lib.mi_gemm_nt_q8_split(fake, fake * 2, fake * 4, None, fake * 3, 8, 8, 32, 2, 0, 0, 1, 0, 0, None)
+    assert st == _lib.MI_ERR_INVALID_ARG
+    # split entry rejects K % 4 != 0 (the reference's 4-wide staging zero-fills there)
+    st = lib.mi_gemm_nt_q8_split(fake, fake * 2, fake * 4, None, fake * 3, 8, 8, 30, 0, 0, 0, 1, 0, 0, None)
+    assert st == _lib.MI_ERR_UNSUPPORTED
+    # unsupported attention head dim: the reference exit(1)s; here an error code
+    st = lib.mi_fused_attention(fake, fake * 2, fake * 3, fake * 4, 8, 8, 130, 1, 0, None)
+    assert st == _lib.MI_ERR_UNSUPPORTED
+    # attention output aliasing q
+    st = lib.mi_fused_attention(fake, fake * 2, fake * 3, fake, 8, 8, 128, 2, 0, None)
+    assert st == _lib.MI_ERR_ALIASING
+    # dequant: n not a multiple of 32
+    assert lib.mi_q8_0_dequant(fake, fake * 2, 0, 33, None) == _lib.MI_ERR_UNSUPPORTED
+    assert lib.mi_q8_0_dequant(fake, fake * 2, 7, 32, None) == _lib.MI_ERR_INVALID_ARG
+
+
+def test_python_mirror_raises_mi_error():
+    with pytest.raises(ops.MiError) as e:
+        ops.fused_attention(ops.FusedAttnArgs(1 << 20, 2 << 20, 3 << 20, 4 << 20, 8, 8, 130, 1))
+    assert e.value.status == _lib.MI_ERR_UNSUPPORTED
+    with pytest.raises(ValueError):
+        ops.dispatch("gemm_nt_q8_v_b", [1, 2, 3, 4], ops.Pg(8, 8, 32))  # 5 bindings expected
+    with pytest.raises(ValueError):
+        ops.dispatch("no_such_kernel", [], None)

@@ -1,0 +1,164 @@
+"""GPU parity for the fused attention against the CPU oracle (fp64 online softmax,
+tests/fused_attn_test.cpp:25-61 semantics).
+
+Bar: max |O_gpu - O_ref| <= 2e-3 x RMS(O_ref) for fp32 outputs. fp16 outputs
+add their own storage rounding (half an fp16 ulp of |O|), stated per element.
+"""
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from helpers import REL_RMS_TOL, assert_parity, fp16_half_ulp, rms
+from sdvk_amd import MI_F16, MI_F32, ops
+from sdvk_amd.hip import DeviceBuffer, synchronize
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).parent / "golden"
+
+
+def run_ref_api(q, k, v, Tq, Tk, C, heads, causal):
+    """The reference call shape: fusedAttention on fp32 [T, C] buffers."""
+    dq, dk, dv = (DeviceBuffer.from_array(x.astype(np.float32)) for x in (q, k, v))
+    do = DeviceBuffer(max(Tq * C * 4, 4))
+    ops.fused_attention(ops.FusedAttnArgs(dq, dk, dv, do, Tq, Tk, C, heads, causal))
+    synchronize()
+    return do.download(np.float32, Tq * C).reshape(Tq, C)
+
+
+def run_ex(q, k, v, *, batch, Tq, Tk, C, heads, in_dtype, out_dtype, kv_len=None, causal=False, **kw):
+    dq, dk, dv = (DeviceBuffer.from_array(x) for x in (q, k, v))
+    osz = 4 if out_dtype == MI_F32 else 2
+    do = DeviceBuffer(batch * Tq * C * osz)
+    dl = DeviceBuffer.from_array(np.asarray(kv_len, dtype=np.int32)) if kv_len is not None else None
+    ops.fused_attention_ex(dq, dk, dv, do, batch=batch, Tq=Tq, Tk=Tk, C=C, heads=heads, causal=causal,
+                           in_dtype=in_dtype, out_dtype=out_dtype, kv_len=dl, **kw)
+    synchronize()
+    return do.download(np.float32 if out_dtype == MI_F32 else np.float16, batch * Tq * C).reshape(batch, Tq, C)
+
+
+def test_reference_test_shapes(gpu):
+    """tests/fused_attn_test.cpp:74-79 (incl. hd = 40 and causal), fp32 API."""
+    f = np.load(GOLDEN / "attn_ref_shapes.npz")
+    for i in range(4):
+        Tq, Tk, C, heads, causal = (int(x) for x in f[f"s{i}_shape"])
+        print(f"[case] ref shape Tq={Tq} Tk={Tk} C={C} heads={heads} causal={causal}", flush=True)
+        got = run_ref_api(f[f"s{i}_q"], f[f"s{i}_k"], f[f"s{i}_v"], Tq, Tk, C, heads, bool(causal))
+        want = f[f"s{i}_o"].reshape(Tq, C)
+        e = assert_parity(got, want, what=f"shape {i}")
+        print(f"  err/rms = {e:.3e}", flush=True)
+
+
+@pytest.mark.parametrize("Tq,Tk,C,heads,causal", [
+    (100, 300, 128, 2, False), (100, 300, 128, 2, True), (257, 513, 640, 10, True), (1, 1, 64, 1, False),
+    (300, 256, 320, 5, False), (129, 64, 1280, 20, True), (50, 1000, 40, 1, False)])
+def test_fp32_api_tiled_sizes(gpu, oracle, Tq, Tk, C, heads, causal):
+    """Tk >= 256 (the reference's tiled kernel, never numerically checked there)."""
+    print(f"[case] fp32 Tq={Tq} Tk={Tk} C={C} heads={heads} causal={causal}", flush=True)
+    q, k, v = oracle.normal(1, Tq * C), oracle.normal(2, Tk * C), oracle.normal(3, Tk * C)
+    want = oracle.fused_attention(q, k, v, Tq, Tk, C, heads, causal).reshape(Tq, C)
+    got = run_ref_api(q, k, v, Tq, Tk, C, heads, causal)
+    assert_parity(got, want, what="fp32 api")
+
+
+@pytest.mark.parametrize("Tq,Tk,C,heads", [(70, 90, 74, 2), (33, 40, 21, 3), (64, 100, 320, 8)])
+def test_general_head_dims(gpu, oracle, Tq, Tk, C, heads):
+    """hd not a multiple of 8 (scalar staging path) and hd = 40."""
+    q, k, v = oracle.normal(4, Tq * C), oracle.normal(5, Tk * C), oracle.normal(6, Tk * C)
+    want = oracle.fused_attention(q, k, v, Tq, Tk, C, heads, False).reshape(Tq, C)
+    assert_parity(run_ref_api(q, k, v, Tq, Tk, C, heads, False), want, what=f"hd={C // heads}")
+
+
+def test_special_cases(gpu, oracle):
+    C, heads = 128, 2
+    # Tk = 1: O = the V row
+    q, k, v = oracle.normal(1, 5 * C), oracle.normal(2, C), oracle.normal(3, C)
+    got = run_ref_api(q, k, v, 5, 1, C, heads, False)
+    assert np.allclose(got, np.tile(v.astype(np.float16).astype(np.float32), (5, 1)), atol=1e-6)
+    # Tk = 0: no keys, O = 0 (the reference's l == 0 guard)
+    got = run_ref_api(q, np.zeros(C, np.float32), np.zeros(C, np.float32), 5, 0, C, heads, False)
+    assert np.all(got == 0)
+    # kv_len = 0 for one batch item, full for the other
+    batch, Tq, Tk = 2, 40, 77
+    q = oracle.normal(4, batch * Tq * C).astype(np.float16)
+    k = oracle.normal(5, batch * Tk * C).astype(np.float16)
+    v = oracle.normal(6, batch * Tk * C).astype(np.float16)
+    got = run_ex(q, k, v, batch=batch, Tq=Tq, Tk=Tk, C=C, heads=heads, in_dtype=MI_F16, out_dtype=MI_F32,
+                 kv_len=[0, 77])
+    assert np.all(got[0] == 0)
+    want = oracle.fused_attention_ex(q, k, v, batch=batch, Tq=Tq, Tk=Tk, C=C, heads=heads, in_dtype=1,
+                                     kv_len=np.array([0, 77], np.int32))
+    assert_parity(got[1], want[1], what="kv_len full")
+
+
+def _sample_rows(Tq, n, seed):
+    rng = np.random.default_rng(seed)
+    return np.unique(np.concatenate([[0, Tq - 1, 127, 128], rng.integers(0, Tq, n)])).astype(np.uint32)
+
+
+@pytest.mark.parametrize("heads,T", [(10, 4096), (20, 1024)])
+def test_config2_self_attention(gpu, oracle, heads, T):
+    """batch 2, no mask, fp16 [B, T, H*64], scale 1/8."""
+    print(f"[case] self-attn B=2 H={heads} T={T}", flush=True)
+    B, C = 2, heads * 64
+    q = oracle.normal(3, B * T * C).astype(np.float16)
+    k = oracle.normal(4, B * T * C).astype(np.float16)
+    v = oracle.normal(5, B * T * C).astype(np.float16)
+    rows = _sample_rows(T, 40, heads)
+    want = oracle.fused_attention_ex(q, k, v, batch=B, Tq=T, Tk=T, C=C, heads=heads, in_dtype=1, rows=rows,
+                                     threads=oracle.max_threads())
+    got32 = run_ex(q, k, v, batch=B, Tq=T, Tk=T, C=C, heads=heads, in_dtype=MI_F16, out_dtype=MI_F32)
+    e = assert_parity(got32[:, rows], want, what="fp16 in / fp32 out")
+    got16 = run_ex(q, k, v, batch=B, Tq=T, Tk=T, C=C, heads=heads, in_dtype=MI_F16, out_dtype=MI_F16)
+    g16 = got16[:, rows].astype(np.float64)
+    bound = REL_RMS_TOL * rms(want) + fp16_half_ulp(want)
+    assert np.all(np.abs(g16 - want) <= bound), "fp16 output beyond parity + storage rounding"
+    print(f"  err/rms = {e:.3e} (fp32 out); fp16-out max err/rms = {np.abs(g16 - want).max() / rms(want):.3e}",
+          flush=True)
+
+
+@pytest.mark.parametrize("heads,T", [(10, 4096), (20, 1024)])
+def test_config3_cross_attention(gpu, oracle, heads, T):
+    """77 context tokens, key-padding lengths U{1..77} (seed 7)."""
+    print(f"[case] cross-attn B=2 H={heads} T={T}", flush=True)
+    B, C, Tk = 2, heads * 64, 77
+    q = oracle.normal(3, B * T * C).astype(np.float16)
+    k = oracle.normal(4, B * Tk * C).astype(np.float16)
+    v = oracle.normal(5, B * Tk * C).astype(np.float16)
+    kv_len = oracle.uniform_int(7, 1, 77, B)
+    rows = _sample_rows(T, 60, heads + 1)
+    want = oracle.fused_attention_ex(q, k, v, batch=B, Tq=T, Tk=Tk, C=C, heads=heads, in_dtype=1,
+                                     kv_len=kv_len, rows=rows, threads=oracle.max_threads())
+    got = run_ex(q, k, v, batch=B, Tq=T, Tk=Tk, C=C, heads=heads, in_dtype=MI_F16, out_dtype=MI_F32,
+                 kv_len=kv_len)
+    e = assert_parity(got[:, rows], want, what="cross")
+    print(f"  kv_len={kv_len.tolist()} err/rms = {e:.3e}", flush=True)
+
+
+def test_strided_layouts_and_scale(gpu, oracle):
+    """Token strides > C (e.g. fused QKV buffers), batch strides with gaps, custom scale."""
+    B, Tq, Tk, C, heads = 2, 150, 200, 128, 2
+    ldq, ldk, ldv = 3 * C, 3 * C, 3 * C
+    sq, sk = Tq * ldq + 64, Tk * ldk + 64
+    base = oracle.normal(9, B * max(sq, sk) + 3 * C).astype(np.float16)
+    qv = base[: B * sq]
+    kv = base[C: C + B * sk]
+    vv = base[2 * C: 2 * C + B * sk]
+    dq, dk, dv = DeviceBuffer.from_array(qv), DeviceBuffer.from_array(kv), DeviceBuffer.from_array(vv)
+    do = DeviceBuffer(B * Tq * C * 4)
+    scale = 0.07
+    ops.fused_attention_ex(dq, dk, dv, do, batch=B, Tq=Tq, Tk=Tk, C=C, heads=heads, in_dtype=MI_F16,
+                           out_dtype=MI_F32, ldq=ldq, ldk=ldk, ldv=ldv, sq=sq, sk=sk, sv=sk, scale=scale)
+    synchronize()
+    got = do.download(np.float32, B * Tq * C).reshape(B, Tq, C)
+    hd = C // heads
+    for b in range(B):
+        Q = qv[b * sq: b * sq + Tq * ldq].reshape(Tq, ldq)[:, :C].astype(np.float64)
+        K = kv[b * sk: b * sk + Tk * ldk].reshape(Tk, ldk)[:, :C].astype(np.float64)
+        V = vv[b * sk: b * sk + Tk * ldv].reshape(Tk, ldv)[:, :C].astype(np.float64)
+        want = np.zeros((Tq, C))
+        for h in range(heads):
+            s = Q[:, h * hd:(h + 1) * hd] @ K[:, h * hd:(h + 1) * hd].T * np.float64(np.float32(scale))
+            p = np.exp(s - s.max(1, keepdims=True))
+            want[:, h * hd:(h + 1) * hd] = (p @ V[:, h * hd:(h + 1) * hd]) / p.sum(1, keepdims=True)
+        assert_parity(got[b], want, what=f"strided b={b}")
