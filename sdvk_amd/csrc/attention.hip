@@ -16,7 +16,11 @@
 //     FMA per score), masked scores are -inf, all-masked rows give O = 0;
 //   * O^T = V^T P^T on the same MFMA: P stays in registers (the S^T output
 //     layout is, key for key, the B-operand layout the PV product needs); V is
-//     stored in LDS as [key/4][d][key%4] so each A fragment is two 8-byte reads.
+//     stored in LDS as [key/4][d][key%4] so each A fragment is two 8-byte reads;
+//   * fp32 inputs (the reference layout) are carried as fp16 hi + lo pairs
+//     (x = hi + lo to 2^-22): S = K_hi Q_hi + K_lo Q_hi + K_hi Q_lo and
+//     O = V_hi P + V_lo P, so only P is rounded to fp16. fp16 inputs take one
+//     MFMA per product.
 #include "common.hpp"
 
 namespace mi {
@@ -39,32 +43,47 @@ struct AttnArgs {
     float c;  // scale * log2(e)
 };
 
+// 8 consecutive elements as fp16 (hi); for fp32 sources also the residual
+// lo = fp16(x - hi), so that hi + lo carries x to 2^-22 relative.
 template <typename T>
-__device__ __forceinline__ half8 load8(const T* p, bool vec, int valid) {
-    half8 h;
-    if (vec) {
-        if constexpr (sizeof(T) == 2) {
-            h = *reinterpret_cast<const half8*>(p);
+__device__ __forceinline__ void load8(const T* p, bool vec, int valid, half8& hi, half8& lo) {
+    if constexpr (sizeof(T) == 2) {
+        if (vec) {
+            hi = *reinterpret_cast<const half8*>(p);
         } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) hi[i] = i < valid ? p[i] : static_cast<_Float16>(0.0f);
+        }
+    } else {
+        float x[8];
+        if (vec) {
             floatx4 a = reinterpret_cast<const floatx4*>(p)[0];
             floatx4 b = reinterpret_cast<const floatx4*>(p)[1];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                h[i] = static_cast<_Float16>(a[i]);
-                h[4 + i] = static_cast<_Float16>(b[i]);
+                x[i] = a[i];
+                x[4 + i] = b[i];
             }
-        }
-    } else {
+        } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) h[i] = i < valid ? static_cast<_Float16>(p[i]) : static_cast<_Float16>(0.0f);
+            for (int i = 0; i < 8; ++i) x[i] = i < valid ? p[i] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            hi[i] = static_cast<_Float16>(x[i]);
+            lo[i] = static_cast<_Float16>(x[i] - static_cast<float>(hi[i]));
+        }
     }
-    return h;
 }
+
+__device__ __forceinline__ half8 zero8() { return half8{0, 0, 0, 0, 0, 0, 0, 0}; }
 
 template <typename TI, typename TO, bool VEC>
 __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
-    __shared__ _Float16 Ks[2][kBKV * kKld];
-    __shared__ _Float16 Vs[2][kBKV * 64];
+    constexpr bool kSplit = sizeof(TI) == 4;  // fp32 inputs: hi + lo planes
+    constexpr int NP = kSplit ? 2 : 1;
+    __shared__ _Float16 Ks[2][NP][kBKV * kKld];
+    __shared__ _Float16 Vs[2][NP][kBKV * 64];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -87,20 +106,19 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
     const TI* Vp = static_cast<const TI*>(a.v) + b * a.sv + static_cast<uint64_t>(h) * a.hd;
 
     // Q^T fragments (B operand): d = 16 s + 8 g .. +8 of query qi
-    half8 qf[4];
+    half8 qf[4], qlo[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
         const int d0 = 16 * s + 8 * g;
         const int valid = hd - d0;
-        if (qi < a.Tq && valid > 0)
-            qf[s] = load8(Qp + static_cast<uint64_t>(qi) * a.ldq + d0, VEC, valid);
-        else
-            qf[s] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+        qf[s] = zero8();
+        qlo[s] = zero8();
+        if (qi < a.Tq && valid > 0) load8(Qp + static_cast<uint64_t>(qi) * a.ldq + d0, VEC, valid, qf[s], qlo[s]);
     }
 
     // Staging: a tile is 64 keys x 8 chunks of 8 d for K and for V; thread
     // handles chunks tid and tid + 256 (key = c / 8, d0 = 8 (c % 8)).
-    half8 kreg[2], vreg[2];
+    half8 kreg[2][NP], vreg[2][NP];
     auto load_tile = [&](uint32_t kv0) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -108,12 +126,16 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
             const uint32_t key = kv0 + (c >> 3);
             const int d0 = (c & 7) * 8;
             const int valid = hd - d0;
+            half8 klo = zero8(), vlo = zero8();
+            kreg[i][0] = zero8();
+            vreg[i][0] = zero8();
             if (key < L && valid > 0) {
-                kreg[i] = load8(Kp + static_cast<uint64_t>(key) * a.ldk + d0, VEC, valid);
-                vreg[i] = load8(Vp + static_cast<uint64_t>(key) * a.ldv + d0, VEC, valid);
-            } else {
-                kreg[i] = half8{0, 0, 0, 0, 0, 0, 0, 0};
-                vreg[i] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+                load8(Kp + static_cast<uint64_t>(key) * a.ldk + d0, VEC, valid, kreg[i][0], klo);
+                load8(Vp + static_cast<uint64_t>(key) * a.ldv + d0, VEC, valid, vreg[i][0], vlo);
+            }
+            if constexpr (kSplit) {
+                kreg[i][NP - 1] = klo;
+                vreg[i][NP - 1] = vlo;
             }
         }
     };
@@ -122,10 +144,13 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
         for (int i = 0; i < 2; ++i) {
             const int c = tid + i * kThreads;
             const int key = c >> 3, d0 = (c & 7) * 8;
-            *reinterpret_cast<half8*>(&Ks[st][key * kKld + d0]) = kreg[i];
-            _Float16* vb = &Vs[st][((key >> 2) * 64 + d0) * 4 + (key & 3)];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) vb[e * 4] = vreg[i][e];
+            for (int pl = 0; pl < NP; ++pl) {
+                *reinterpret_cast<half8*>(&Ks[st][pl][key * kKld + d0]) = kreg[i][pl];
+                _Float16* vb = &Vs[st][pl][((key >> 2) * 64 + d0) * 4 + (key & 3)];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) vb[e * 4] = vreg[i][pl][e];
+            }
         }
     };
 
@@ -156,8 +181,14 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
             for (int r = 0; r < 16; ++r) sc[t][r] = 0.0f;
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                half8 kf = *reinterpret_cast<const half8*>(&Ks[st][(32 * t + l32) * kKld + 16 * s + 8 * g]);
+                const int off = (32 * t + l32) * kKld + 16 * s + 8 * g;
+                half8 kf = *reinterpret_cast<const half8*>(&Ks[st][0][off]);
                 sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], sc[t], 0, 0, 0);
+                if constexpr (kSplit) {
+                    half8 kl = *reinterpret_cast<const half8*>(&Ks[st][NP - 1][off]);
+                    sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kl, qf[s], sc[t], 0, 0, 0);
+                    sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qlo[s], sc[t], 0, 0, 0);
+                }
             }
         }
 
@@ -203,10 +234,13 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
 #pragma unroll
                 for (int u = 0; u < 2; ++u) {
                     const int d = 32 * u + l32;
-                    half4 v0 = *reinterpret_cast<const half4*>(&Vs[st][(kg * 64 + d) * 4]);
-                    half4 v1 = *reinterpret_cast<const half4*>(&Vs[st][((kg + 2) * 64 + d) * 4]);
-                    half8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-                    o[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, o[u], 0, 0, 0);
+#pragma unroll
+                    for (int pl = 0; pl < NP; ++pl) {
+                        half4 v0 = *reinterpret_cast<const half4*>(&Vs[st][pl][(kg * 64 + d) * 4]);
+                        half4 v1 = *reinterpret_cast<const half4*>(&Vs[st][pl][((kg + 2) * 64 + d) * 4]);
+                        half8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                        o[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, o[u], 0, 0, 0);
+                    }
                 }
             }
         }

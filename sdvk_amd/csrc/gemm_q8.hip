@@ -4,25 +4,30 @@
 // lda / ldc / batch semantics :37-54,115-127) and gemm_nt_q8.comp; host routing
 // sdvkgen.cpp:917-936. The algorithm here is our own:
 //
-//   * one workgroup computes a BM x BN tile of C; the K loop advances one Q8_0
-//     block column (32 k) per step, so every step sees exactly one scale per
-//     weight row;
+//   * a workgroup computes a BM x BN tile of C; each K step covers KB Q8_0
+//     block columns (32 k each), so every weight row sees whole blocks;
 //   * A (fp32) is streamed with coalesced 16-byte loads, rounded to fp16 and
-//     written to LDS; the weight block is streamed (34-byte GGUF blocks or the
-//     reference's split int8 + fp32-scale planes), dequantised to fp16
-//     (w = d * q, rounded once) and written to LDS;
+//     written to LDS; the weight blocks are streamed (34-byte GGUF blocks or
+//     the reference's split int8 + fp32-scale planes), dequantised once per
+//     workgroup to fp16 (w = d * q, rounded once) and written to LDS;
 //   * waves multiply LDS fragments with v_mfma_f32_32x32x16_f16 (fp32
-//     accumulation); the next step's global loads are in flight while the
+//     accumulation). The next step's global loads are in flight while the
 //     current step's MFMAs run (register prefetch + two LDS stages, one
 //     barrier per step);
-//   * workgroup ids are remapped so the tiles of one A row-panel run on one
-//     XCD and share its L2.
+//   * workgroup ids are remapped so the tiles of one A row panel run on one
+//     XCD and share its L2;
+//   * grids too small to fill 256 CUs split K: each split adds its partial tile
+//     into C with fp32 atomics after a fill kernel has written bias / 0.
+//     Summation order then varies run to run (last-bit differences only).
+#include <algorithm>
+#include <type_traits>
+#include <cstdlib>
+#include <cstring>
+
 #include "common.hpp"
 
 namespace mi {
 namespace {
-
-constexpr int kLdk = 40;  // LDS row stride in halves: 32 k + 8 pad (80 B, conflict-free 16-B reads)
 
 struct GemmArgs {
     const float* A;
@@ -33,83 +38,60 @@ struct GemmArgs {
     uint32_t M, N, K, mode, lda, ldc;
     uint64_t sA, sC;
     uint32_t tiles_n;       // ceil(N / BN)
-    uint32_t ksteps;        // ceil(K / 32)
+    uint32_t ksteps;        // ceil(K / BK)
+    uint32_t steps_per_split;
+    uint32_t rowbytes;      // 34-byte layout: bytes per weight row
 };
-
-// ---- weight loaders: 8 consecutive k of one weight row per thread ---------------
 
 enum WKind { kBlocks34 = 0, kSplit = 1 };
 
-struct WRaw {
-    uint32_t lo, hi;  // 8 int8 weights, little-endian
-    float s0, s1;     // scale of weights 0-3 and 4-7
-};
-
-// 34-byte blocks: row n, block kb starts at byte (n*K/32 + kb)*34; the 8 q bytes
-// for group j sit at +2+8j, which is 2-byte aligned: read the covering aligned
-// dwords and funnel-shift.
-__device__ __forceinline__ WRaw load_w_blocks(const GemmArgs& a, uint32_t n, uint32_t kb, uint32_t j) {
-    WRaw r;
-    uint64_t blk = (static_cast<uint64_t>(n) * (a.K >> 5) + kb) * 34u;
-    float d = fp16_bits_to_f32(*reinterpret_cast<const uint16_t*>(a.W + blk));
-    uint64_t addr = blk + 2u + 8u * j;
-    const uint32_t* p = reinterpret_cast<const uint32_t*>(a.W + (addr & ~uint64_t(3)));
-    uint32_t w0 = p[0], w1 = p[1];
-    if (addr & 2u) {
-        uint32_t w2 = p[2];
-        r.lo = __builtin_amdgcn_alignbit(w1, w0, 16);
-        r.hi = __builtin_amdgcn_alignbit(w2, w1, 16);
-    } else {
-        r.lo = w0;
-        r.hi = w1;
-    }
-    r.s0 = d;
-    r.s1 = d;
-    return r;
+// fp16 bits of (1024 + u) for each byte u of x ^ 0x80808080: subtracting 1152
+// leaves the signed byte value exactly (|q| <= 128 < 2^11).
+__device__ __forceinline__ half8 dequant8_f16(uint32_t lo, uint32_t hi, _Float16 d) {
+    const uint32_t xl = lo ^ 0x80808080u, xh = hi ^ 0x80808080u;
+    const half2 bias = {static_cast<_Float16>(1152.0f), static_cast<_Float16>(1152.0f)};
+    const half2 dd = {d, d};
+    half2 h0 = __builtin_bit_cast(half2, __builtin_amdgcn_perm(0x64646464u, xl, 0x04010400u));
+    half2 h1 = __builtin_bit_cast(half2, __builtin_amdgcn_perm(0x64646464u, xl, 0x04030402u));
+    half2 h2 = __builtin_bit_cast(half2, __builtin_amdgcn_perm(0x64646464u, xh, 0x04010400u));
+    half2 h3 = __builtin_bit_cast(half2, __builtin_amdgcn_perm(0x64646464u, xh, 0x04030402u));
+    h0 = (h0 - bias) * dd;  // one rounding of the exact product q * d
+    h1 = (h1 - bias) * dd;
+    h2 = (h2 - bias) * dd;
+    h3 = (h3 - bias) * dd;
+    return half8{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
 }
 
-// Split layout: flat element f = n*K + k, int8 at byte f, scale at f >> 5.
-// K % 4 == 0, so each 4-group shares a scale; weights at k >= K are zero.
-__device__ __forceinline__ WRaw load_w_split(const GemmArgs& a, uint32_t n, uint32_t kb, uint32_t j) {
-    WRaw r{0u, 0u, 0.0f, 0.0f};
-    uint32_t k = kb * 32u + 8u * j;
-    if (k >= a.K) return r;
-    uint64_t f = static_cast<uint64_t>(n) * a.K + k;
-    const uint32_t* p = reinterpret_cast<const uint32_t*>(a.W);
-    r.lo = p[f >> 2];
-    r.s0 = a.scales[f >> 5];
-    if (k + 4u < a.K) {
-        r.hi = p[(f >> 2) + 1u];
-        r.s1 = a.scales[(f + 4u) >> 5];
-    }
-    return r;
-}
-
-__device__ __forceinline__ half8 dequant8(const WRaw& r) {
+// fp32 scales (split layout, arbitrary fp32): w = fp16(fp32(q) * s).
+__device__ __forceinline__ half8 dequant8_f32(uint32_t lo, uint32_t hi, float s0, float s1) {
     half8 h;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        h[i] = static_cast<_Float16>(static_cast<float>(static_cast<int8_t>((r.lo >> (8 * i)) & 0xffu)) * r.s0);
-        h[4 + i] = static_cast<_Float16>(static_cast<float>(static_cast<int8_t>((r.hi >> (8 * i)) & 0xffu)) * r.s1);
+        h[i] = static_cast<_Float16>(static_cast<float>(static_cast<int8_t>((lo >> (8 * i)) & 0xffu)) * s0);
+        h[4 + i] = static_cast<_Float16>(static_cast<float>(static_cast<int8_t>((hi >> (8 * i)) & 0xffu)) * s1);
     }
     return h;
 }
 
-// ---- the kernel ---------------------------------------------------------------------
-
-template <int BM, int BN, int WM, int WN, int WK>
+template <int BM, int BN, int WM, int WN, int KB, int WK, bool SPLITK, bool KTAIL, int PF>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     constexpr int NT = WM * WN * 64;
+    constexpr int BK = 32 * KB;
+    constexpr int LDK = BK + 8;                   // LDS row stride in halves (16-B pad)
     constexpr int TM = BM / WM, TN = BN / WN;     // wave tile
     constexpr int FM = TM / 32, FN = TN / 32;     // 32x32 MFMA tiles per wave
-    constexpr int A_IT = BM * 8 / NT;             // float4 loads per thread per step
-    constexpr int W_UNITS = BN * 4;               // (row, 8-k group) units per step
-    constexpr int W_IT = (W_UNITS + NT - 1) / NT;
-    static_assert(BM * 8 % NT == 0, "A staging must divide evenly");
+    constexpr int A_UNITS = BM * BK / 4;          // float4 per step
+    constexpr int A_IT = A_UNITS / NT;
+    constexpr int W_UNITS = BN * BK / 8;          // (row, 8-k group) per step
+    constexpr int W_IT = W_UNITS / NT;
+    // Buffer-load fast path: two blocks per step keep each lane's byte
+    // alignment fixed (68 = 0 mod 4), so the step advance is a scalar offset.
+    constexpr bool FAST = KB == 2 && !KTAIL;
+    static_assert(A_UNITS % NT == 0 && W_UNITS % NT == 0, "staging must divide evenly");
     static_assert(FM >= 1 && FN >= 1, "wave tile below 32x32");
 
-    __shared__ _Float16 As[2][BM * kLdk];
-    __shared__ _Float16 Ws[2][BN * kLdk];
+    __shared__ _Float16 As[2][BM * LDK];
+    __shared__ _Float16 Ws[2][BN * LDK];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -119,49 +101,134 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     const unsigned tile = xcd_swizzle(blockIdx.x, gridDim.x);
     const uint32_t m0 = (tile / a.tiles_n) * BM;
     const uint32_t n0 = (tile % a.tiles_n) * BN;
-    const float* A = a.A + static_cast<uint64_t>(blockIdx.z) * a.sA;
-    float* C = a.C + static_cast<uint64_t>(blockIdx.z) * a.sC;
+    const uint32_t s_begin = SPLITK ? blockIdx.y * a.steps_per_split : 0;
+    const uint32_t s_end = SPLITK ? min(a.ksteps, s_begin + a.steps_per_split) : a.ksteps;
 
-    floatx4 areg[A_IT];
-    WRaw wreg[W_IT];
+    // Per-thread byte offsets, fixed for the whole K loop. Rows past M / N read
+    // the last valid row: they only feed outputs that are never stored.
+    const float* Apanel = a.A + static_cast<uint64_t>(blockIdx.z) * a.sA + static_cast<uint64_t>(m0) * a.lda;
+    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Apanel), 0, -1, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.W), 0, -1, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rS =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(WK == kSplit ? a.scales : a.A), 0, -1, 0x00020000);
+    uint32_t a_off[A_IT];
+#pragma unroll
+    for (int i = 0; i < A_IT; ++i) {
+        const int f = tid + i * NT;
+        const uint32_t row = min(m0 + f / (BK / 4), a.M - 1) - m0;
+        a_off[i] = (row * a.lda + (f % (BK / 4)) * 4) * 4;
+    }
+    uint32_t w_off[W_IT];   // blocks: byte of the unit's first q; split: flat element
+    uint32_t w_aux[W_IT];   // blocks: byte of the block's scale; split: byte of the scale
+    uint32_t w_k[W_IT];     // k of the unit's first weight within the step
+#pragma unroll
+    for (int i = 0; i < W_IT; ++i) {
+        const int u = tid + i * NT;
+        const uint32_t n = min(n0 + u / (BK / 8), a.N - 1);
+        w_k[i] = (u % (BK / 8)) * 8;
+        if constexpr (WK == kBlocks34) {
+            w_aux[i] = n * a.rowbytes + (w_k[i] / 32) * 34;
+            w_off[i] = w_aux[i] + 2 + (w_k[i] % 32);
+        } else {
+            w_off[i] = n * a.K + w_k[i];
+            w_aux[i] = (w_off[i] >> 5) * 4;
+        }
+    }
 
-    auto load_step = [&](uint32_t kb) {
+    // PF register sets of prefetched raw data. PF = 2: the loads for step k+2
+    // are issued before step k's MFMAs (sets indexed by step parity, like the
+    // LDS stages), so every global load has two steps of MFMA work to arrive
+    // in; PF = 1 (large tiles, whose steps are long): the loads for step k+1.
+    // The load phase is branch-free (raw words only; alignment shifts and
+    // conversions happen at store time) so the waitcnt before each store
+    // waits for its own set alone.
+    floatx4 areg_[PF][A_IT];
+    uint32_t w0_[PF][W_IT], w1_[PF][W_IT], w2_[PF][W_IT], wd_[PF][W_IT];
+    float ws0_[PF][W_IT], ws1_[PF][W_IT];
+    // 34-byte layout: lanes whose 8 q bytes start 2 mod 4 read one more dword
+    // and funnel-shift by 16 bits; in the fast path the shift is fixed per lane.
+    uint32_t w_sh[PF][W_IT];
+#pragma unroll
+    for (int i = 0; i < W_IT; ++i)
+#pragma unroll
+        for (int r = 0; r < PF; ++r) w_sh[r][i] = (w_off[i] & 2u) * 8u;
+
+    auto load_step = [&](uint32_t ks, auto RS) {
+        constexpr int rs = decltype(RS)::value;
 #pragma unroll
         for (int i = 0; i < A_IT; ++i) {
-            int f = tid + i * NT;
-            uint32_t row = m0 + (f >> 3);
-            uint32_t k = kb * 32u + (f & 7) * 4u;
-            floatx4 v = {0.f, 0.f, 0.f, 0.f};
-            if (row < a.M && k < a.K) v = *reinterpret_cast<const floatx4*>(A + static_cast<uint64_t>(row) * a.lda + k);
-            areg[i] = v;
+            if constexpr (KTAIL) {
+                const uint32_t k = ks * BK + ((tid + i * NT) % (BK / 4)) * 4;
+                areg_[rs][i] = floatx4{0.f, 0.f, 0.f, 0.f};
+                if (k < a.K) areg_[rs][i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rA, a_off[i], ks * BK * 4, 0));
+            } else {
+                areg_[rs][i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rA, a_off[i], ks * BK * 4, 0));
+            }
         }
 #pragma unroll
         for (int i = 0; i < W_IT; ++i) {
-            int u = tid + i * NT;
-            uint32_t n = n0 + (u >> 2);
-            WRaw r{0u, 0u, 0.0f, 0.0f};
-            if (u < W_UNITS && n < a.N) {
-                if constexpr (WK == kBlocks34) r = load_w_blocks(a, n, kb, u & 3);
-                else r = load_w_split(a, n, kb, u & 3);
+            if constexpr (WK == kBlocks34) {
+                const uint32_t soff = ks * (KB * 34);
+                const uint32_t addr = FAST ? w_off[i] : w_off[i] + soff;
+                const uint32_t base = addr & ~3u;
+                const uint32_t so = FAST ? soff : 0u;
+                const auto w01 = __builtin_amdgcn_raw_buffer_load_b64(rW, base, so, 0);
+                w0_[rs][i] = w01[0];
+                w1_[rs][i] = w01[1];
+                // third dword only matters when shifted; otherwise re-read the second
+                w2_[rs][i] = __builtin_amdgcn_raw_buffer_load_b32(rW, base + ((addr & 2u) ? 8u : 4u), so, 0);
+                wd_[rs][i] = __builtin_amdgcn_raw_buffer_load_b16(rW, FAST ? w_aux[i] : w_aux[i] + soff, so, 0);
+                if constexpr (!FAST) w_sh[rs][i] = (addr & 2u) * 8u;  // shift of this set's step
+            } else if constexpr (FAST) {
+                const auto w01 = __builtin_amdgcn_raw_buffer_load_b64(rW, w_off[i], ks * BK, 0);
+                w0_[rs][i] = w01[0];
+                w1_[rs][i] = w01[1];
+                ws0_[rs][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rS, w_aux[i], ks * KB * 4, 0));
+                ws1_[rs][i] = ws0_[rs][i];
+            } else {
+                const uint32_t k = ks * BK + w_k[i];
+                const uint64_t f = static_cast<uint64_t>(w_off[i]) + static_cast<uint64_t>(ks) * BK;
+                const uint32_t* p = reinterpret_cast<const uint32_t*>(a.W);
+                w0_[rs][i] = 0u;
+                w1_[rs][i] = 0u;
+                ws0_[rs][i] = 0.0f;
+                ws1_[rs][i] = 0.0f;
+                if (!KTAIL || k < a.K) {
+                    w0_[rs][i] = p[f >> 2];
+                    ws0_[rs][i] = a.scales[f >> 5];
+                    if (!KTAIL || k + 4u < a.K) {
+                        w1_[rs][i] = p[(f >> 2) + 1u];
+                        ws1_[rs][i] = a.scales[(f + 4u) >> 5];
+                    }
+                }
             }
-            wreg[i] = r;
         }
     };
-    auto store_step = [&](int st) {
+    auto store_step = [&](auto RS, auto ST) {
+        constexpr int rs = decltype(RS)::value;  // register set
+        constexpr int st = decltype(ST)::value;  // LDS stage
 #pragma unroll
         for (int i = 0; i < A_IT; ++i) {
-            int f = tid + i * NT;
+            const int f = tid + i * NT;
             half4 h;
-            h[0] = static_cast<_Float16>(areg[i][0]);
-            h[1] = static_cast<_Float16>(areg[i][1]);
-            h[2] = static_cast<_Float16>(areg[i][2]);
-            h[3] = static_cast<_Float16>(areg[i][3]);
-            *reinterpret_cast<half4*>(&As[st][(f >> 3) * kLdk + (f & 7) * 4]) = h;
+            h[0] = static_cast<_Float16>(areg_[rs][i][0]);
+            h[1] = static_cast<_Float16>(areg_[rs][i][1]);
+            h[2] = static_cast<_Float16>(areg_[rs][i][2]);
+            h[3] = static_cast<_Float16>(areg_[rs][i][3]);
+            *reinterpret_cast<half4*>(&As[st][(f / (BK / 4)) * LDK + (f % (BK / 4)) * 4]) = h;
         }
 #pragma unroll
         for (int i = 0; i < W_IT; ++i) {
-            int u = tid + i * NT;
-            if (u < W_UNITS) *reinterpret_cast<half8*>(&Ws[st][(u >> 2) * kLdk + (u & 3) * 8]) = dequant8(wreg[i]);
+            const int u = tid + i * NT;
+            half8 h;
+            if constexpr (WK == kBlocks34) {
+                const uint32_t lo = __builtin_amdgcn_alignbit(w1_[rs][i], w0_[rs][i], w_sh[rs][i]);
+                const uint32_t hi = __builtin_amdgcn_alignbit(w2_[rs][i], w1_[rs][i], w_sh[rs][i]);
+                h = dequant8_f16(lo, hi, __builtin_bit_cast(_Float16, static_cast<uint16_t>(wd_[rs][i])));
+            } else {
+                h = dequant8_f32(w0_[rs][i], w1_[rs][i], ws0_[rs][i], ws1_[rs][i]);
+            }
+            *reinterpret_cast<half8*>(&Ws[st][(u / (BK / 8)) * LDK + w_k[i]]) = h;
         }
     };
 
@@ -173,41 +240,75 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    if (a.ksteps > 0) {
-        load_step(0);
-        store_step(0);
-    }
-    __syncthreads();
-
-    for (uint32_t kb = 0; kb < a.ksteps; ++kb) {
-        const int st = kb & 1;
-        const bool more = kb + 1 < a.ksteps;
-        if (more) load_step(kb + 1);
+    auto compute = [&](auto ST) {
+        constexpr int st = decltype(ST)::value;
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
+        for (int s = 0; s < BK / 16; ++s) {
             half8 af[FM], bf[FN];
 #pragma unroll
             for (int i = 0; i < FM; ++i)
-                af[i] = *reinterpret_cast<const half8*>(&As[st][(wm * TM + 32 * i + l32) * kLdk + 16 * s + 8 * g]);
+                af[i] = *reinterpret_cast<const half8*>(&As[st][(wm * TM + 32 * i + l32) * LDK + 16 * s + 8 * g]);
 #pragma unroll
             for (int j = 0; j < FN; ++j)
-                bf[j] = *reinterpret_cast<const half8*>(&Ws[st][(wn * TN + 32 * j + l32) * kLdk + 16 * s + 8 * g]);
+                bf[j] = *reinterpret_cast<const half8*>(&Ws[st][(wn * TN + 32 * j + l32) * LDK + 16 * s + 8 * g]);
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll
                 for (int j = 0; j < FN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
-        if (more) store_step(st ^ 1);
-        __syncthreads();
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+
+    // Step k computes from LDS stage k&1. PF = 2: the loads of step k+2 (into
+    // register set k&1) are in flight meanwhile, then set (k+1)&1, loaded one
+    // step earlier, is stored. PF = 1: the loads of step k+1 are in flight and
+    // stored after the MFMAs. Prefetches past the last step re-read it
+    // (clamped, unused), so the load phase has no branches. Two steps per trip
+    // keep every stage / set index a compile-time constant.
+    const uint32_t last = s_end - 1;
+    if (s_begin < s_end) {
+        load_step(s_begin, S0{});
+        store_step(S0{}, S0{});
+        if constexpr (PF == 2) load_step(min(s_begin + 1, last), S1{});
     }
+    __syncthreads();
+    uint32_t ks = s_begin;
+    for (; ks + 2 <= s_end; ks += 2) {
+        if constexpr (PF == 2) {
+            load_step(min(ks + 2, last), S0{});
+            __builtin_amdgcn_sched_barrier(0);  // issue the prefetch before the MFMAs
+            compute(S0{});
+            store_step(S1{}, S1{});
+            __syncthreads();
+            load_step(min(ks + 3, last), S1{});
+            __builtin_amdgcn_sched_barrier(0);
+            compute(S1{});
+            store_step(S0{}, S0{});
+            __syncthreads();
+        } else {
+            load_step(ks + 1, S0{});
+            __builtin_amdgcn_sched_barrier(0);
+            compute(S0{});
+            store_step(S0{}, S1{});
+            __syncthreads();
+            load_step(min(ks + 2, last), S0{});
+            __builtin_amdgcn_sched_barrier(0);
+            compute(S1{});
+            store_step(S0{}, S0{});
+            __syncthreads();
+        }
+    }
+    if (ks < s_end) compute(S0{});
 
     // Epilogue. Lane holds column l32 of each 32x32 tile and rows 8(r/4) + 4g + r%4.
+    float* C = a.C + static_cast<uint64_t>(blockIdx.z) * a.sC;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
         const uint32_t n = n0 + wn * TN + 32 * j + l32;
         if (n >= a.N) continue;
-        const float bv = (a.mode == 0 && a.bias) ? a.bias[n] : 0.0f;
+        const float bv = (!SPLITK && a.mode == 0 && a.bias) ? a.bias[n] : 0.0f;
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -215,27 +316,122 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
                 const uint32_t m = m0 + wm * TM + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
                 if (m >= a.M) continue;
                 float* c = C + static_cast<uint64_t>(m) * a.ldc + n;
-                if (a.mode == 0) *c = acc[i][j][r] + bv;
-                else *c += acc[i][j][r];
+                if constexpr (SPLITK) {
+                    unsafeAtomicAdd(c, acc[i][j][r]);  // native global_atomic_add_f32
+                } else {
+                    if (a.mode == 0) *c = acc[i][j][r] + bv;
+                    else *c += acc[i][j][r];
+                }
             }
         }
     }
 }
 
-template <int BM, int BN, int WM, int WN, int WK>
-void launch(const GemmArgs& a0, uint32_t batch, hipStream_t s) {
-    GemmArgs a = a0;
-    a.tiles_n = ceil_div(a.N, BN);
-    unsigned tiles = ceil_div(a.M, BM) * a.tiles_n;
-    gemm_q8_kernel<BM, BN, WM, WN, WK><<<dim3(tiles, 1, batch), WM * WN * 64, 0, s>>>(a);
+// C[m, n] = bias[n] (or 0) for the split-K accumulation (mode 0 only).
+__global__ __launch_bounds__(256) void gemm_init_kernel(float* C, const float* bias, uint32_t M, uint32_t N,
+                                                        uint32_t ldc, uint64_t sC) {
+    const uint32_t n = blockIdx.x * 256 + threadIdx.x;
+    if (n >= N) return;
+    const float v = bias ? bias[n] : 0.0f;
+    float* c = C + static_cast<uint64_t>(blockIdx.z) * sC + n;
+    for (uint32_t m = blockIdx.y; m < M; m += gridDim.y) c[static_cast<uint64_t>(m) * ldc] = v;
 }
 
-// Tile configuration by problem size. Large M: 256x128 tiles (8 waves, 64x64
-// each); small M (cross-attention K/V projections, M = 2 x 77): 64x64 tiles.
+void launch_init(float* C, const float* bias, uint32_t M, uint32_t N, uint32_t ldc, uint64_t sC, uint32_t batch,
+                 hipStream_t s) {
+    gemm_init_kernel<<<dim3(ceil_div(N, 256), std::min<uint32_t>(M, 4096), batch), 256, 0, s>>>(C, bias, M, N, ldc, sC);
+}
+
+// ---- configurations -------------------------------------------------------------
+
+struct Cfg {
+    int bm, bn, kb;
+    int ctas_per_cu;  // resident workgroups per CU (LDS / VGPR bound)
+};
+
+enum CfgId { kC256x128 = 0, kC128x128, kC128x64, kC64x64, kC256x256w4, kC256x128w4, kNumCfg };
+constexpr Cfg kCfgs[kNumCfg] = {{256, 128, 2, 1}, {128, 128, 2, 2}, {128, 64, 2, 2}, {64, 64, 2, 4},
+                                {256, 256, 2, 1}, {256, 128, 2, 1}};
+
+template <int BM, int BN, int WM, int WN, int KB, int WK, bool KTAIL, int PF = 2>
+void launch_cfg(const GemmArgs& a0, uint32_t batch, uint32_t splits, hipStream_t s) {
+    GemmArgs a = a0;
+    a.tiles_n = ceil_div(a.N, BN);
+    a.ksteps = ceil_div(a.K, 32 * KB);
+    const unsigned tiles = ceil_div(a.M, BM) * a.tiles_n;
+    if (splits > 1) {
+        a.steps_per_split = ceil_div(a.ksteps, splits);
+        splits = ceil_div(a.ksteps, a.steps_per_split);
+    }
+    if (splits > 1) {
+        if (a.mode == 0) launch_init(a.C, a.bias, a.M, a.N, a.ldc, a.sC, batch, s);
+        gemm_q8_kernel<BM, BN, WM, WN, KB, WK, true, KTAIL, PF><<<dim3(tiles, splits, batch), WM * WN * 64, 0, s>>>(a);
+    } else {
+        a.steps_per_split = a.ksteps;
+        gemm_q8_kernel<BM, BN, WM, WN, KB, WK, false, KTAIL, PF><<<dim3(tiles, 1, batch), WM * WN * 64, 0, s>>>(a);
+    }
+}
+
+template <int WK>
+void launch(int cfg, const GemmArgs& a, uint32_t batch, uint32_t splits, hipStream_t s) {
+    switch (cfg) {
+        case kC256x128: launch_cfg<256, 128, 4, 2, 2, WK, false>(a, batch, splits, s); break;
+        case kC128x128: launch_cfg<128, 128, 2, 2, 2, WK, false>(a, batch, splits, s); break;
+        case kC128x64: launch_cfg<128, 64, 2, 2, 2, WK, false>(a, batch, splits, s); break;
+        case kC256x256w4: launch_cfg<256, 256, 2, 2, 2, WK, false, 1>(a, batch, splits, s); break;
+        case kC256x128w4: launch_cfg<256, 128, 2, 2, 2, WK, false, 2>(a, batch, splits, s); break;
+        default: launch_cfg<64, 64, 2, 2, 2, WK, false>(a, batch, splits, s); break;
+    }
+}
+
+// General K (K % 64 != 0): one block column per step, 64x64 tiles; the split
+// layout with K % 32 != 0 also zero-fills the partial last step.
+template <int WK>
+void launch_general(const GemmArgs& a, uint32_t batch, uint32_t splits, hipStream_t s) {
+    if (a.K % 32 == 0) launch_cfg<64, 64, 2, 2, 1, WK, false>(a, batch, splits, s);
+    else launch_cfg<64, 64, 2, 2, 1, WK, true>(a, batch, splits, s);
+}
+
+constexpr int kCUs = 256;
+
+// Picks the tile and K split for a shape (measured on MI355X over the SDXL
+// projection shapes): 256x128 tiles once they give at least half a wave of
+// workgroups per CU; long-K shapes with fewer tiles split K in two; small
+// grids use 64x64 tiles and split K until ~256 workgroups are resident.
+void choose(uint32_t M, uint32_t N, uint32_t K, uint32_t batch, int& cfg, uint32_t& splits) {
+    const char* env = std::getenv("MI_GEMM_CFG");  // "<cfg>[:<splits>]" overrides (tuning sweeps)
+    if (env && *env) {
+        cfg = std::atoi(env);
+        const char* c = std::strchr(env, ':');
+        splits = c ? static_cast<uint32_t>(std::atoi(c + 1)) : 1u;
+        if (cfg < 0 || cfg >= kNumCfg) cfg = kC64x64;
+        if (splits < 1) splits = 1;
+        return;
+    }
+    const uint64_t t256 = static_cast<uint64_t>(ceil_div(M, 256)) * ceil_div(N, 128) * batch;
+    const uint64_t t64 = static_cast<uint64_t>(ceil_div(M, 64)) * ceil_div(N, 64) * batch;
+    splits = 1;
+    if (t256 >= kCUs / 2) {
+        cfg = kC256x128;
+    } else if (K >= 4096 && t256 * 2 >= kCUs / 2) {
+        cfg = kC256x128;
+        splits = 2;
+    } else {
+        cfg = kC64x64;
+        const uint64_t want = (kCUs + t64 - 1) / t64;
+        uint32_t s = 1;
+        while (s * 2 <= want && s * 2 * 128 <= K) s *= 2;
+        splits = s;
+    }
+}
+
 template <int WK>
 void dispatch(const GemmArgs& a, uint32_t batch, hipStream_t s) {
-    if (a.M >= 1024) launch<256, 128, 4, 2, WK>(a, batch, s);
-    else launch<64, 64, 2, 2, WK>(a, batch, s);
+    int cfg;
+    uint32_t splits;
+    choose(a.M, a.N, a.K, batch, cfg, splits);
+    if (a.K % 64 != 0) launch_general<WK>(a, batch, splits, s);
+    else launch<WK>(cfg, a, batch, splits, s);
 }
 
 int validate(const char* fn, const float* A, const void* W, const float* C, uint32_t M, uint32_t N, uint32_t K,
@@ -249,7 +445,9 @@ int validate(const char* fn, const float* A, const void* W, const float* C, uint
     if (lda < K || ldc < N) return fail(MI_ERR_INVALID_ARG, "%s: lda %u < K %u or ldc %u < N %u", fn, lda, K, ldc, N);
     if (!aligned(A, 16) || lda % 4 || sA % 4) return fail(MI_ERR_ALIGNMENT, "%s: A must be 16-byte aligned, lda and sA multiples of 4", fn);
     if (!aligned(C, 4)) return fail(MI_ERR_ALIGNMENT, "%s: C must be 4-byte aligned", fn);
-    if (static_cast<uint64_t>(M) * N > (uint64_t(1) << 40)) return fail(MI_ERR_UNSUPPORTED, "%s: M*N too large", fn);
+    // per-workgroup A offsets are 32-bit: a 256-row panel must stay below 4 GiB
+    if (static_cast<uint64_t>(lda) * 4 * 256 >= (uint64_t(1) << 32))
+        return fail(MI_ERR_UNSUPPORTED, "%s: lda=%u too large", fn, lda);
     return MI_OK;
 }
 
@@ -267,12 +465,18 @@ extern "C" int mi_gemm_nt_q8_0(const float* A, const void* W, const float* bias,
     int st = validate(fn, A, W, C, M, N, K, mode, lda, ldc, batch, sA, sC);
     if (st) return st;
     if (!aligned(W, 16)) return fail(MI_ERR_ALIGNMENT, "%s: W must be 16-byte aligned", fn);
-    uint64_t cbytes = (static_cast<uint64_t>(batch - 1) * sC + static_cast<uint64_t>(M - 1) * ldc + N) * 4;
-    uint64_t abytes = (static_cast<uint64_t>(batch - 1) * sA + static_cast<uint64_t>(M - 1) * lda + K) * 4;
-    uint64_t wbytes = static_cast<uint64_t>(N) * (K / 32) * 34;
+    const uint64_t wbytes = static_cast<uint64_t>(N) * (K / 32) * 34;
+    if (wbytes + 16 >= (uint64_t(1) << 32)) return fail(MI_ERR_UNSUPPORTED, "%s: weight >= 4 GiB", fn);
+    const uint64_t cbytes = (static_cast<uint64_t>(batch - 1) * sC + static_cast<uint64_t>(M - 1) * ldc + N) * 4;
+    const uint64_t abytes = (static_cast<uint64_t>(batch - 1) * sA + static_cast<uint64_t>(M - 1) * lda + K) * 4;
     if (overlaps(C, cbytes, A, abytes) || overlaps(C, cbytes, W, wbytes) || overlaps(C, cbytes, bias, uint64_t(N) * 4))
         return fail(MI_ERR_ALIASING, "%s: C overlaps an input", fn);
-    GemmArgs a{A, static_cast<const uint8_t*>(W), nullptr, bias, C, M, N, K, mode, lda, ldc, sA, sC, 0, K / 32};
+    if (K == 0) {
+        if (mode == 0) launch_init(C, bias, M, N, ldc, sC, batch, static_cast<hipStream_t>(stream));
+        return check_launch(fn);
+    }
+    GemmArgs a{A, static_cast<const uint8_t*>(W), nullptr, bias, C, M, N, K, mode, lda, ldc, sA, sC, 0, 0, 0,
+               (K / 32) * 34};
     dispatch<kBlocks34>(a, batch, static_cast<hipStream_t>(stream));
     return check_launch(fn);
 }
@@ -287,14 +491,18 @@ extern "C" int mi_gemm_nt_q8_split(const float* A, const uint32_t* payload, cons
     if (st) return st;
     if (!scales) return fail(MI_ERR_INVALID_ARG, "%s: null scales", fn);
     if (!aligned(payload, 4) || !aligned(scales, 4)) return fail(MI_ERR_ALIGNMENT, "%s: payload/scales alignment", fn);
-    uint64_t cbytes = (static_cast<uint64_t>(batch - 1) * sC + static_cast<uint64_t>(M - 1) * ldc + N) * 4;
-    uint64_t abytes = (static_cast<uint64_t>(batch - 1) * sA + static_cast<uint64_t>(M - 1) * lda + K) * 4;
-    uint64_t nk = static_cast<uint64_t>(N) * K;
+    const uint64_t nk = static_cast<uint64_t>(N) * K;
+    if (nk + 16 >= (uint64_t(1) << 32)) return fail(MI_ERR_UNSUPPORTED, "%s: weight >= 4 GiB", fn);
+    const uint64_t cbytes = (static_cast<uint64_t>(batch - 1) * sC + static_cast<uint64_t>(M - 1) * ldc + N) * 4;
+    const uint64_t abytes = (static_cast<uint64_t>(batch - 1) * sA + static_cast<uint64_t>(M - 1) * lda + K) * 4;
     if (overlaps(C, cbytes, A, abytes) || overlaps(C, cbytes, payload, nk) ||
         overlaps(C, cbytes, scales, (nk + 31) / 32 * 4) || overlaps(C, cbytes, bias, uint64_t(N) * 4))
         return fail(MI_ERR_ALIASING, "%s: C overlaps an input", fn);
-    GemmArgs a{A, reinterpret_cast<const uint8_t*>(payload), scales, bias, C, M, N, K, mode, lda, ldc, sA, sC, 0,
-               (K + 31) / 32};
+    if (K == 0) {
+        if (mode == 0) launch_init(C, bias, M, N, ldc, sC, batch, static_cast<hipStream_t>(stream));
+        return check_launch(fn);
+    }
+    GemmArgs a{A, reinterpret_cast<const uint8_t*>(payload), scales, bias, C, M, N, K, mode, lda, ldc, sA, sC, 0, 0, 0, 0};
     dispatch<kSplit>(a, batch, static_cast<hipStream_t>(stream));
     return check_launch(fn);
 }

@@ -25,7 +25,7 @@ def run_q8_0(A, blocks, M, N, K, bias=None, C0=None, mode=0, lda=0, ldc=0, batch
     dC = DeviceBuffer.from_array(C0) if C0 is not None else DeviceBuffer(csize * 4)
     ops.gemm_nt_q8_0(dA, dW, dC, M, N, K, bias=dB, mode=mode, lda=lda, ldc=ldc, batch=batch, sA=sA, sC=sC)
     synchronize()
-    return dC.download(np.float32, csize)
+    return dC.download(np.float32, C0.size if C0 is not None else csize)
 
 
 def test_reference_bench_case_every_variant(gpu):
@@ -64,8 +64,10 @@ def test_q8_0_shapes_bias_and_accumulate(gpu, oracle, M, N, K):
     print(f"  err/rms = {e:.3e}", flush=True)
 
 
-def test_q8_0_and_split_entries_agree_bitwise(gpu, oracle):
-    """Both entries dequantise w = fp16(fp32(d) * q): identical results."""
+def test_q8_0_and_split_entries_agree_bitwise(gpu, oracle, monkeypatch):
+    """Both entries dequantise w = fp16(fp32(d) * q): identical results (on a
+    configuration without K splitting, whose fp32 atomics reorder the sum)."""
+    monkeypatch.setenv("MI_GEMM_CFG", "1")
     M, N, K = 1100, 320, 640
     A = oracle.normal(1, M * K)
     blocks = q8_weights(oracle, 2, N, K)
@@ -132,3 +134,26 @@ def test_baseline_shapes_sampled_rows(gpu, oracle, M, N, K):
     e = err_vs_rms(got[rows], want)
     print(f"  err/rms = {e:.3e} over {len(rows)} rows", flush=True)
     assert e <= REL_RMS_TOL
+
+
+@pytest.mark.parametrize("cfg", ["0", "1", "2", "3", "0:3", "1:2", "2:5", "3:16"])
+@pytest.mark.parametrize("M,N,K", [(300, 200, 640), (1030, 130, 256)])
+def test_every_tile_config_and_split_k(gpu, oracle, monkeypatch, cfg, M, N, K):
+    """Forces each tile configuration / K split (MI_GEMM_CFG="<cfg>[:<splits>]")."""
+    print(f"[case] cfg={cfg} M={M} N={N} K={K}", flush=True)
+    monkeypatch.setenv("MI_GEMM_CFG", cfg)
+    A = oracle.normal(11, M * K)
+    blocks = q8_weights(oracle, 12, N, K)
+    bias = oracle.normal(13, N, 0.0, 0.02)
+    want = oracle.gemm_nt_q8_0(A, blocks, M, N, K, bias=bias, threads=oracle.max_threads()).reshape(M, N)
+    got = run_q8_0(A, blocks, M, N, K, bias=bias).reshape(M, N)
+    assert_parity(got, want, what=f"cfg {cfg} mode0")
+    C0 = oracle.normal(14, M * N)
+    got1 = run_q8_0(A, blocks, M, N, K, C0=C0, mode=1).reshape(M, N)
+    assert_parity(got1 - C0.reshape(M, N), want - bias, what=f"cfg {cfg} mode1")
+    payload, scales = oracle.q8_0_to_split(blocks, N * K)
+    dC = DeviceBuffer(M * N * 4)
+    ops.gemm_nt_q8_bias(DeviceBuffer.from_array(A), DeviceBuffer.from_array(payload), dC,
+                        DeviceBuffer.from_array(scales), DeviceBuffer.from_array(bias), M, N, K)
+    synchronize()
+    assert_parity(dC.download(np.float32, M * N).reshape(M, N), want, what=f"cfg {cfg} split layout")
