@@ -10,9 +10,11 @@ resident in HBM:
     d = 64, fp16 in/out, no mask) and cross-attention (config 3: 77 context
     tokens, key-padding lengths U{1..77}).
 value = algorithmic FLOP of one step x steps / elapsed (HIP events on the
-launch stream), in TFLOP/s. The JSON line also carries a per-shape breakdown
-(hot-cache, each shape timed alone), the roofline of the dominant kernel and a
-CPU baseline (the oracle's OpenMP fp32 restatement, bounded sample).
+launch stream), in TFLOP/s. The roofline of the dominant kernel family uses its
+launch durations inside the timed steps (events at the family boundaries). The
+JSON line also carries a per-shape breakdown (each shape launched back to back
+after the timed region) and a CPU baseline (the oracle's OpenMP fp32
+restatement, bounded sample).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 """
@@ -112,39 +114,44 @@ def roofline_pct(c, seconds):
     return tf, roof, tf / roof
 
 
-def cpu_baseline(threads: int) -> dict:
-    """The oracle's fp32 OpenMP restatement timed on one full step of the same
-    workload (every GEMM and attention shape at full size)."""
+def cpu_baseline(threads: int, min_seconds: float = 10.0, max_passes: int = 8) -> dict:
+    """The oracle's fp32 OpenMP restatement timed on the same workload: full
+    passes over every GEMM and attention shape of one step, repeated until at
+    least `min_seconds` of CPU work have been timed (bounded by `max_passes`)."""
     from oracle import binding as ob
 
     rng = np.random.default_rng(7)
-    flops = 0.0
-    t_total = 0.0
+    gemm_in, attn_in = [], []
     for tag, M, N, K in GEMM_SHAPES:
-        m = M
-        A = rng.standard_normal(m * K, dtype=np.float32)
-        blocks = quantize_q8_0(rng.standard_normal(N * K, dtype=np.float32) * 0.02)
-        t0 = time.perf_counter()
-        ob.gemm_nt_q8_0(A, blocks, m, N, K, acc64=False, threads=threads)
-        t_total += time.perf_counter() - t0
-        flops += 2.0 * m * N * K
+        gemm_in.append((rng.standard_normal(M * K, dtype=np.float32),
+                        quantize_q8_0(rng.standard_normal(N * K, dtype=np.float32) * 0.02), M, N, K))
     for tag, B, H, Tq, Tk, masked in ATTN_SHAPES:
         C = H * 64
-        nq = Tq
-        q = rng.standard_normal(B * Tq * C, dtype=np.float32)
-        k = rng.standard_normal(B * Tk * C, dtype=np.float32)
-        v = rng.standard_normal(B * Tk * C, dtype=np.float32)
-        kv = rng.integers(1, 78, B).astype(np.int32) if masked else None
-        t0 = time.perf_counter()
-        ob.fused_attention_f32(q, k, v, batch=B, Tq=Tq, Tk=Tk, C=C, heads=H, kv_len=kv, q_rows=nq,
-                               threads=threads)
-        t_total += time.perf_counter() - t0
-        flops += 4.0 * B * H * nq * Tk * 64
+        attn_in.append((rng.standard_normal(B * Tq * C, dtype=np.float32),
+                        rng.standard_normal(B * Tk * C, dtype=np.float32),
+                        rng.standard_normal(B * Tk * C, dtype=np.float32),
+                        rng.integers(1, 78, B).astype(np.int32) if masked else None, B, H, Tq, Tk, C))
+    flops = 0.0
+    t_total = 0.0
+    passes = 0
+    while passes < max_passes and (passes == 0 or t_total < min_seconds):
+        for A, blocks, M, N, K in gemm_in:
+            t0 = time.perf_counter()
+            ob.gemm_nt_q8_0(A, blocks, M, N, K, acc64=False, threads=threads)
+            t_total += time.perf_counter() - t0
+            flops += 2.0 * M * N * K
+        for q, k, v, kv, B, H, Tq, Tk, C in attn_in:
+            t0 = time.perf_counter()
+            ob.fused_attention_f32(q, k, v, batch=B, Tq=Tq, Tk=Tk, C=C, heads=H, kv_len=kv, q_rows=Tq,
+                                   threads=threads)
+            t_total += time.perf_counter() - t0
+            flops += 4.0 * B * H * Tq * Tk * 64
+        passes += 1
     return {"value": round(flops / t_total / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "seconds": round(t_total, 2),
-            "sample": "oracle fp32 OpenMP restatement (not the reference GLSL shaders: no Vulkan/lavapipe here) "
-                      "on one full step of the same workload: the 8 config-1 GEMM shapes and the 4 config-2/3 "
-                      "attention shapes at full size"}
+            "seconds": round(t_total, 2), "passes": passes,
+            "sample": f"oracle fp32 OpenMP restatement (the reference GLSL shaders need Vulkan/lavapipe, absent "
+                      f"here) over {passes} full pass(es) of one step of the same workload: the 8 config-1 GEMM "
+                      f"shapes and the 4 config-2/3 attention shapes at full size"}
 
 
 def main() -> int:
@@ -152,7 +159,9 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--reps", type=int, default=20, help="launches per shape for the breakdown")
+    ap.add_argument("--reps", type=int, default=10, help="back-to-back launches per shape for the breakdown")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="run one device-to-device copy of this many MiB first (profiler byte calibration)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["gemm", "attention"], default=None,
                     help="profile one kernel family (breakdown only)")
@@ -182,23 +191,52 @@ def main() -> int:
             c.run(stream)
     stream.synchronize()
 
-    e0, e1 = hip.Event(), hip.Event()
+    if args.copy_probe_mib:
+        # one plain device-to-device copy of known size: calibrates the HBM byte
+        # counters (FETCH_SIZE / WRITE_SIZE) of a profiling run of this command
+        nb = args.copy_probe_mib << 20
+        src, dst = hip.DeviceBuffer(nb), hip.DeviceBuffer(nb)
+        src.fill_zero(stream)
+        dst.copy_from(src, nb, stream)
+        stream.synchronize()
+        del src, dst
+
+    # Timed region: K steps. Events sit only where the kernel family changes
+    # (cases are grouped by family), on the launch stream, so each family's
+    # launch durations are measured inside the timed steps at the cost of two
+    # event packets per step.
+    groups = []  # (family, [cases]) in launch order
+    for c in cases:
+        if groups and groups[-1][0] == c.kernel:
+            groups[-1][1].append(c)
+        else:
+            groups.append((c.kernel, [c]))
+    marks = [[hip.Event() for _ in range(len(groups) + 1)] for _ in range(args.steps)]
     hip.synchronize()
-    e0.record(stream)
-    for _ in range(args.steps):
-        for c in cases:
-            c.run(stream)
-    e1.record(stream)
-    e1.synchronize()
+    for st in range(args.steps):
+        marks[st][0].record(stream)
+        for g, (_, members) in enumerate(groups):
+            for c in members:
+                c.run(stream)
+            marks[st][g + 1].record(stream)
+    marks[-1][-1].synchronize()
     hip.synchronize()
-    ms_total = e0.elapsed_ms(e1)
+    ms_total = marks[0][0].elapsed_ms(marks[-1][-1])
     step_flops = sum(c.flops for c in cases)
     value = step_flops * args.steps / (ms_total / 1e3) / 1e12
     print(f"[bench] timed {args.steps} steps: {ms_total:.3f} ms", file=sys.stderr, flush=True)
 
-    # per-shape breakdown (each shape alone, back-to-back launches, hot cache)
-    breakdown = []
     fam_time, fam_flops, fam_bytes, fam_launch = {}, {}, {}, {}
+    for g, (fam, members) in enumerate(groups):
+        sec = sum(marks[st][g].elapsed_ms(marks[st][g + 1]) for st in range(args.steps)) / 1e3 / args.steps
+        fam_time[fam] = fam_time.get(fam, 0.0) + sec
+        fam_flops[fam] = fam_flops.get(fam, 0.0) + sum(c.flops for c in members)
+        fam_bytes[fam] = fam_bytes.get(fam, 0.0) + sum(c.bytes for c in members)
+        fam_launch[fam] = fam_launch.get(fam, 0) + len(members)
+
+    # Per-shape breakdown (after the timed region): each shape launched `reps`
+    # times back to back between two events.
+    breakdown = []
     for c in cases:
         a, b = hip.Event(), hip.Event()
         a.record(stream)
@@ -212,10 +250,6 @@ def main() -> int:
                           "pct_mfma_peak": round(100 * tf / PEAK_FP16_TFLOPS, 2),
                           "roofline_tflops": round(roof, 1), "pct_of_roofline": round(100 * frac, 2),
                           "gbs": round(c.bytes / sec / 1e9, 1)})
-        fam_time[c.kernel] = fam_time.get(c.kernel, 0.0) + sec
-        fam_flops[c.kernel] = fam_flops.get(c.kernel, 0.0) + c.flops
-        fam_bytes[c.kernel] = fam_bytes.get(c.kernel, 0.0) + c.bytes
-        fam_launch[c.kernel] = fam_launch.get(c.kernel, 0) + 1
         print(f"[bench] {c.tag:<28} {sec * 1e6:9.2f} us {tf:8.1f} TFLOP/s {100 * frac:6.1f}% of roofline",
               file=sys.stderr, flush=True)
 
@@ -223,7 +257,7 @@ def main() -> int:
     avg_launch = fam_time[dom] / fam_launch[dom]
     achieved = fam_flops[dom] / fam_launch[dom] / avg_launch / 1e12
     traffic = None
-    tfile = ROOT / "profiles" / f"traffic_{dom}.json"
+    tfile = ROOT / "profiles" / f"traffic_{dom}_sdxl1024.json"
     if tfile.exists():
         try:
             traffic = json.loads(tfile.read_text()).get("bytes_per_launch")

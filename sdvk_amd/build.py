@@ -17,6 +17,11 @@ ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 
 SOURCES = ["status.hip", "q8_0.hip", "gemm_q8.hip", "attention.hip"]
 
+# Per-source extra flags. The attention kernel rescales its MFMA accumulators
+# with VALU ops; keeping MFMA operands in VGPRs (rather than AGPRs) removes the
+# per-tile AGPR<->VGPR copies around every rescale.
+EXTRA_FLAGS = {"attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
     "-O3",
@@ -35,24 +40,40 @@ def hipcc() -> str:
     return str(p) if p.exists() else "hipcc"
 
 
-def build(save_temps: str | None = None, verbose: bool = False) -> Path:
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{ROOT / 'include'}", f"-I{CSRC}"]
-    if save_temps:
-        Path(save_temps).mkdir(parents=True, exist_ok=True)
-        cmd.append(f"--save-temps={'obj'}")
-    cmd += [str(CSRC / s) for s in SOURCES]
-    cmd += ["-o", str(LIB) + ".tmp", f"-Wl,-rpath,{ROCM / 'lib'}"]
-    env = dict(os.environ)
-    cwd = save_temps if save_temps else None
+def _run(cmd: list[str], cwd: str | None, verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
-    r = subprocess.run(cmd, cwd=cwd, env=env, capture_output=True, text=True)
-    out = "\n".join(l for l in (r.stdout + r.stderr).splitlines()
-                    if "packed-fp32-ops" not in l)
+    r = subprocess.run(cmd, cwd=cwd, capture_output=True, text=True)
+    out = "\n".join(l for l in (r.stdout + r.stderr).splitlines() if "packed-fp32-ops" not in l)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed ({r.returncode}):\n{out}")
     if verbose and out.strip():
         print(out)
+
+
+def build(save_temps: str | None = None, verbose: bool = False) -> Path:
+    """Compiles every source to an object (in parallel) and links libmi_sdvk.so."""
+    import concurrent.futures
+    import tempfile
+
+    with tempfile.TemporaryDirectory(prefix="mi_sdvk_build_") as tmp:
+        cwd = save_temps if save_temps else None
+        if save_temps:
+            Path(save_temps).mkdir(parents=True, exist_ok=True)
+        jobs = []
+        for src in SOURCES:
+            obj = str(Path(tmp) / (src + ".o"))
+            cmd = [hipcc(), *HIPCC_FLAGS, "-c", *EXTRA_FLAGS.get(src, []), f"-I{ROOT / 'include'}", f"-I{CSRC}",
+                   str(CSRC / src), "-o", obj]
+            cmd.remove("-shared")
+            if save_temps:
+                cmd.append("--save-temps=obj")
+            jobs.append((cmd, obj))
+        with concurrent.futures.ThreadPoolExecutor(max_workers=len(jobs)) as ex:
+            list(ex.map(lambda j: _run(j[0], cwd, verbose), jobs))
+        link = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *[o for _, o in jobs],
+                "-o", str(LIB) + ".tmp", f"-Wl,-rpath,{ROCM / 'lib'}"]
+        _run(link, cwd, verbose)
     os.replace(str(LIB) + ".tmp", LIB)
     return LIB
 

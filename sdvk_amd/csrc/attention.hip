@@ -13,10 +13,15 @@
 //     owns one query and 32 of the tile's keys: the row max and row sum are
 //     in-register reductions plus one exchange with the partner lane (lane ^ 32);
 //   * online softmax in fp32 in the exp2 domain (scale * log2 e folded into one
-//     FMA per score), masked scores are -inf, all-masked rows give O = 0;
+//     FMA per score), masked scores are -inf, all-masked rows give O = 0. The
+//     running max is raised lazily (only when a tile exceeds it by 2^8), so
+//     the O / l rescale is skipped on most tiles; masks are applied only on
+//     boundary tiles (a wave-uniform branch);
 //   * O^T = V^T P^T on the same MFMA: P stays in registers (the S^T output
 //     layout is, key for key, the B-operand layout the PV product needs); V is
-//     stored in LDS as [key/4][d][key%4] so each A fragment is two 8-byte reads;
+//     stored in LDS grouped by the PV step that consumes each key, so each A
+//     fragment is one 16-byte read; the row sums of P come from the same MFMA
+//     (an all-ones A operand);
 //   * fp32 inputs (the reference layout) are carried as fp16 hi + lo pairs
 //     (x = hi + lo to 2^-22): S = K_hi Q_hi + K_lo Q_hi + K_hi Q_lo and
 //     O = V_hi P + V_lo P, so only P is rounded to fp16. fp16 inputs take one
@@ -78,6 +83,37 @@ __device__ __forceinline__ void load8(const T* p, bool vec, int valid, half8& hi
 
 __device__ __forceinline__ half8 zero8() { return half8{0, 0, 0, 0, 0, 0, 0, 0}; }
 
+// 4 consecutive elements as fp16 (hi) and, for fp32 sources, the residual lo.
+template <typename T>
+__device__ __forceinline__ void load4(const T* p, bool vec, int valid, half4& hi, half4& lo) {
+    if constexpr (sizeof(T) == 2) {
+        if (vec) {
+            hi = *reinterpret_cast<const half4*>(p);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) hi[i] = i < valid ? p[i] : static_cast<_Float16>(0.0f);
+        }
+    } else {
+        floatx4 x;
+        if (vec) {
+            x = *reinterpret_cast<const floatx4*>(p);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[i] = i < valid ? p[i] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            hi[i] = static_cast<_Float16>(x[i]);
+            lo[i] = static_cast<_Float16>(x[i] - static_cast<float>(hi[i]));
+        }
+    }
+}
+
+// Lazy rescaling threshold (exp2 domain): the running max is only raised when
+// a tile's max exceeds it by more than this, so P = exp2(s - m) <= 2^8 stays
+// far inside fp16 range while the O / l rescale runs on few tiles.
+constexpr float kLazy = 8.0f;
+
 template <typename TI, typename TO, bool VEC>
 __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
     constexpr bool kSplit = sizeof(TI) == 4;  // fp32 inputs: hi + lo planes
@@ -90,7 +126,8 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
     const int l32 = lane & 31, g = lane >> 5;
     const uint32_t b = blockIdx.z, h = blockIdx.y;
     const uint32_t qcta = blockIdx.x * kBQ;
-    const uint32_t qi = qcta + wave * 32 + l32;  // this lane's query
+    const uint32_t qwave = qcta + wave * 32;     // first query of this wave
+    const uint32_t qi = qwave + l32;             // this lane's query
     const int hd = static_cast<int>(a.hd);
 
     uint32_t L = a.Tk;
@@ -100,6 +137,9 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
     }
     uint32_t kend = L;
     if (a.causal) kend = min(kend, qcta + kBQ);  // keys past the CTA's last query are all masked
+    // Tiles [0, kfull) need no mask for any query of this wave.
+    uint32_t kfull = L / kBKV * kBKV;
+    if (a.causal) kfull = min(kfull, (qwave + 1) / kBKV * kBKV);
 
     const TI* Qp = static_cast<const TI*>(a.q) + b * a.sq + static_cast<uint64_t>(h) * a.hd;
     const TI* Kp = static_cast<const TI*>(a.k) + b * a.sk + static_cast<uint64_t>(h) * a.hd;
@@ -116,26 +156,81 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
         if (qi < a.Tq && valid > 0) load8(Qp + static_cast<uint64_t>(qi) * a.ldq + d0, VEC, valid, qf[s], qlo[s]);
     }
 
-    // Staging: a tile is 64 keys x 8 chunks of 8 d for K and for V; thread
-    // handles chunks tid and tid + 256 (key = c / 8, d0 = 8 (c % 8)).
-    half8 kreg[2][NP], vreg[2][NP];
+    // Staging. K: chunks of 8 d (thread handles chunks tid and tid + 256: key =
+    // c / 8, d0 = 8 (c % 8)), stored row-major. V: a 4-key x 4-d block per
+    // thread (key group kg = tid / 16, d0 = 4 (tid % 16)), transposed in
+    // registers and stored as [G][d][8] halves, G = (t, sp, g) the PV MFMA step
+    // and lane half that consumes the key: key 32t + 16sp + 8j + 4g + i sits in
+    // slot 4j + i, so a PV fragment is one 16-byte read and the stores are four
+    // 8-byte writes.
+    half8 kreg[2][NP];
+    half4 vreg[4][NP];
+    const int vkg = tid >> 4, vd0 = (tid & 15) * 4;
+    // Vector path: K/V rows through buffer resources whose base advances with
+    // the tile (scalar work only) and whose size ends at key L-1, so rows past
+    // the valid keys read as zeros (hardware range check) with no lane guards.
+    const uint32_t k_off0 = ((tid >> 3) * static_cast<uint32_t>(a.ldk) + (tid & 7) * 8) * sizeof(TI);
+    const uint32_t k_off1 = k_off0 + 32u * static_cast<uint32_t>(a.ldk) * sizeof(TI);
+    const uint32_t v_off = (vkg * 4 * static_cast<uint32_t>(a.ldv) + vd0) * sizeof(TI);
+    const uint32_t v_row = static_cast<uint32_t>(a.ldv) * sizeof(TI);
     auto load_tile = [&](uint32_t kv0) {
+        if constexpr (VEC) {
+            const uint32_t kbytes = kv0 < L ? ((L - kv0 - 1) * static_cast<uint32_t>(a.ldk) + a.hd) * sizeof(TI) : 0u;
+            const uint32_t vbytes = kv0 < L ? ((L - kv0 - 1) * static_cast<uint32_t>(a.ldv) + a.hd) * sizeof(TI) : 0u;
+            const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<TI*>(Kp + static_cast<uint64_t>(kv0) * a.ldk), 0, static_cast<int>(kbytes), 0x00020000);
+            const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<TI*>(Vp + static_cast<uint64_t>(kv0) * a.ldv), 0, static_cast<int>(vbytes), 0x00020000);
+            if constexpr (sizeof(TI) == 2) {
+                kreg[0][0] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rk, k_off0, 0, 0));
+                kreg[1][0] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rk, k_off1, 0, 0));
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int c = tid + i * kThreads;
-            const uint32_t key = kv0 + (c >> 3);
-            const int d0 = (c & 7) * 8;
-            const int valid = hd - d0;
-            half8 klo = zero8(), vlo = zero8();
-            kreg[i][0] = zero8();
-            vreg[i][0] = zero8();
-            if (key < L && valid > 0) {
-                load8(Kp + static_cast<uint64_t>(key) * a.ldk + d0, VEC, valid, kreg[i][0], klo);
-                load8(Vp + static_cast<uint64_t>(key) * a.ldv + d0, VEC, valid, vreg[i][0], vlo);
+                for (int i = 0; i < 4; ++i)
+                    vreg[i][0] = __builtin_bit_cast(half4, __builtin_amdgcn_raw_buffer_load_b64(rv, v_off + i * v_row, 0, 0));
+            } else {
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const uint32_t off = i ? k_off1 : k_off0;
+                    const floatx4 x0 = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+                    const floatx4 x1 = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rk, off + 16, 0, 0));
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        kreg[i][0][e] = static_cast<_Float16>(x0[e]);
+                        kreg[i][0][4 + e] = static_cast<_Float16>(x1[e]);
+                        kreg[i][NP - 1][e] = static_cast<_Float16>(x0[e] - static_cast<float>(kreg[i][0][e]));
+                        kreg[i][NP - 1][4 + e] = static_cast<_Float16>(x1[e] - static_cast<float>(kreg[i][0][4 + e]));
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const floatx4 x = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rv, v_off + i * v_row, 0, 0));
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        vreg[i][0][e] = static_cast<_Float16>(x[e]);
+                        vreg[i][NP - 1][e] = static_cast<_Float16>(x[e] - static_cast<float>(vreg[i][0][e]));
+                    }
+                }
             }
-            if constexpr (kSplit) {
-                kreg[i][NP - 1] = klo;
-                vreg[i][NP - 1] = vlo;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int c = tid + i * kThreads;
+                const uint32_t key = kv0 + (c >> 3);
+                const int d0 = (c & 7) * 8;
+                const int valid = hd - d0;
+                half8 klo = zero8();
+                kreg[i][0] = zero8();
+                if (key < L && valid > 0) load8(Kp + static_cast<uint64_t>(key) * a.ldk + d0, VEC, valid, kreg[i][0], klo);
+                if constexpr (kSplit) kreg[i][NP - 1] = klo;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t key = kv0 + vkg * 4 + i;
+                const int valid = hd - vd0;
+                half4 vlo = half4{0, 0, 0, 0};
+                vreg[i][0] = half4{0, 0, 0, 0};
+                if (key < L && valid > 0) load4(Vp + static_cast<uint64_t>(key) * a.ldv + vd0, VEC, valid, vreg[i][0], vlo);
+                if constexpr (kSplit) vreg[i][NP - 1] = vlo;
             }
         }
     };
@@ -145,33 +240,43 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
             const int c = tid + i * kThreads;
             const int key = c >> 3, d0 = (c & 7) * 8;
 #pragma unroll
-            for (int pl = 0; pl < NP; ++pl) {
-                *reinterpret_cast<half8*>(&Ks[st][pl][key * kKld + d0]) = kreg[i][pl];
-                _Float16* vb = &Vs[st][pl][((key >> 2) * 64 + d0) * 4 + (key & 3)];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) vb[e * 4] = vreg[i][pl][e];
-            }
+            for (int pl = 0; pl < NP; ++pl) *reinterpret_cast<half8*>(&Ks[st][pl][key * kKld + d0]) = kreg[i][pl];
         }
+        // keys 4 vkg .. +3: t = vkg / 8, sp = (vkg / 4) % 2, j = (vkg / 2) % 2, g = vkg % 2
+        const int vG = (vkg >> 3) * 4 + ((vkg >> 2) & 1) * 2 + (vkg & 1);
+        const int vslot = ((vkg >> 1) & 1) * 4;
+#pragma unroll
+        for (int pl = 0; pl < NP; ++pl)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                *reinterpret_cast<half4*>(&Vs[st][pl][(vG * 64 + vd0 + e) * 8 + vslot]) =
+                    half4{vreg[0][pl][e], vreg[1][pl][e], vreg[2][pl][e], vreg[3][pl][e]};
     };
 
-    floatx16 o[2];
+    // o[0..1]: O^T for d in [0, 32) and [32, 64); o[2]: the row sums of P,
+    // computed by the same MFMA with an all-ones A operand (every row of that
+    // 32x32 tile holds sum_k P[q, k] for the lane's query q).
+    floatx16 o[3];
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int u = 0; u < 3; ++u)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[u][r] = 0.0f;
-    float m = -INFINITY, l = 0.0f;
+    float m = -INFINITY;
+    const half8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
 
-    if (kend > 0) {
+    const uint32_t ntiles = (kend + kBKV - 1) / kBKV;
+    if (ntiles > 0) {
         load_tile(0);
         store_tile(0);
     }
     __syncthreads();
 
-    int it = 0;
-    for (uint32_t kv0 = 0; kv0 < kend; kv0 += kBKV, ++it) {
+    for (uint32_t it = 0; it < ntiles; ++it) {
         const int st = it & 1;
-        const bool more = kv0 + kBKV < kend;
-        if (more) load_tile(kv0 + kBKV);
+        const uint32_t kv0 = it * kBKV;
+        // next tile's loads first (clamped: the last trip re-reads its own tile)
+        load_tile(min(it + 1, ntiles - 1) * kBKV);
+        __builtin_amdgcn_sched_barrier(0);
 
         // S^T tile: rows = keys kv0 + 32 t + 8(r/4) + 4 g + r%4, column = query qi
         floatx16 sc[2];
@@ -192,8 +297,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
             }
         }
 
-        const bool need_mask = (kv0 + kBKV > L) || (a.causal && kv0 + kBKV - 1 > qcta + wave * 32);
-        if (need_mask) {
+        if (kv0 >= kfull) {  // wave-uniform: a boundary tile (key padding / Tk end / causal)
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -209,15 +313,17 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[t][r]);
         mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m, mx * a.c);
-        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m - m_use);
-        m = m_new;
-        l *= alpha;
+        const float mt = mx * a.c;  // tile max, exp2 domain (same in both lanes of a query)
+        if (__any(mt > m + kLazy)) {
+            const float m_new = fmaxf(m, mt);
+            const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - m_new);
+            m = m_new;
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+            for (int u = 0; u < 3; ++u)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) o[u][r] *= alpha;
+                for (int r = 0; r < 16; ++r) o[u][r] *= alpha;
+        }
+        const float m_use = m == -INFINITY ? 0.0f : m;
 
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
@@ -225,31 +331,27 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
             for (int sp = 0; sp < 2; ++sp) {
                 half8 pf;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[t][8 * sp + i], a.c, -m_use));
-                    l += p;
-                    pf[i] = static_cast<_Float16>(p);
-                }
-                const int kg = 8 * t + 4 * sp + g;  // key group of slots 0-3; slots 4-7 are kg + 2
+                for (int i = 0; i < 8; ++i)
+                    pf[i] = static_cast<_Float16>(__builtin_amdgcn_exp2f(__builtin_fmaf(sc[t][8 * sp + i], a.c, -m_use)));
+                o[2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones, pf, o[2], 0, 0, 0);
+                const int G = t * 4 + sp * 2 + g;
 #pragma unroll
                 for (int u = 0; u < 2; ++u) {
                     const int d = 32 * u + l32;
 #pragma unroll
                     for (int pl = 0; pl < NP; ++pl) {
-                        half4 v0 = *reinterpret_cast<const half4*>(&Vs[st][pl][(kg * 64 + d) * 4]);
-                        half4 v1 = *reinterpret_cast<const half4*>(&Vs[st][pl][((kg + 2) * 64 + d) * 4]);
-                        half8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                        const half8 vf = *reinterpret_cast<const half8*>(&Vs[st][pl][(G * 64 + d) * 8]);
                         o[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, o[u], 0, 0, 0);
                     }
                 }
             }
         }
 
-        if (more) store_tile(st ^ 1);
+        store_tile(st ^ 1);
         __syncthreads();
     }
 
-    const float lt = l + __shfl_xor(l, 32);
+    const float lt = o[2][0];
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
     if (qi >= a.Tq) return;
     TO* Op = static_cast<TO*>(a.o) + b * a.so + static_cast<uint64_t>(qi) * a.ldo + static_cast<uint64_t>(h) * a.hd;

@@ -73,6 +73,24 @@ __device__ __forceinline__ half8 dequant8_f32(uint32_t lo, uint32_t hi, float s0
     return h;
 }
 
+// Scheduling groups for one K step (instruction-class masks of
+// __builtin_amdgcn_sched_group_barrier: 0x008 MFMA, 0x002 VALU, 0x100 LDS read,
+// 0x200 LDS write). The step's first fragment reads go first; then every MFMA
+// is followed by a share of the next fragment reads and of the store phase
+// (conversions, dequantisation, LDS writes of the other stage), so that work
+// issues in the MFMA shadow instead of between MFMA bursts.
+template <int NMFMA, int NREAD0, int NREAD, int NVALU, int NWRITE>
+__device__ __forceinline__ void interleave_step() {
+    __builtin_amdgcn_sched_group_barrier(0x100, NREAD0, 0);
+#pragma unroll
+    for (int i = 0; i < NMFMA; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, (NREAD + NMFMA - 1) / NMFMA, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, (NVALU + NMFMA - 1) / NMFMA, 0);
+        __builtin_amdgcn_sched_group_barrier(0x200, (NWRITE + NMFMA - 1) / NMFMA, 0);
+    }
+}
+
 template <int BM, int BN, int WM, int WN, int KB, int WK, bool SPLITK, bool KTAIL, int PF>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     constexpr int NT = WM * WN * 64;
@@ -261,46 +279,66 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
 
-    // Step k computes from LDS stage k&1. PF = 2: the loads of step k+2 (into
-    // register set k&1) are in flight meanwhile, then set (k+1)&1, loaded one
-    // step earlier, is stored. PF = 1: the loads of step k+1 are in flight and
+    // Step j computes from LDS stage j&1. PF = 2: the loads of step j+2 (into
+    // register set j&1) are in flight meanwhile, then set (j+1)&1, loaded one
+    // step earlier, is stored. PF = 1: the loads of step j+1 are in flight and
     // stored after the MFMAs. Prefetches past the last step re-read it
     // (clamped, unused), so the load phase has no branches. Two steps per trip
     // keep every stage / set index a compile-time constant.
-    const uint32_t last = s_end - 1;
-    if (s_begin < s_end) {
-        load_step(s_begin, S0{});
+    constexpr int kMfma = FM * FN * (BK / 16);       // MFMAs per step
+    constexpr int kRead0 = FM + FN;                  // fragment reads of the first k16 slice
+    constexpr int kReads = (FM + FN) * (BK / 16);    // all fragment reads of a step
+    constexpr int kWrites = A_IT + W_IT;             // LDS writes of the store phase
+    constexpr int kValu = A_IT * 2 + W_IT * 16;      // conversions + dequantisation (approx.)
+    // Workgroups start their K loop at different steps (rotation by tile id):
+    // all workgroups sweep K in lockstep otherwise, so at any moment every CU
+    // would read the same column window of its A panel and the same few L2
+    // channels (rows are lda*4 bytes apart, a multiple of the channel stride
+    // for the SDXL shapes). Step j of this workgroup is physical step
+    // s_begin + (j + rot) mod n.
+    const uint32_t n_steps = s_end - s_begin;
+    const uint32_t rot = n_steps ? tile % n_steps : 0;
+    auto phys = [&](uint32_t j) {
+        uint32_t t = j + rot;
+        if (t >= n_steps) t -= n_steps;
+        return s_begin + t;
+    };
+    const uint32_t last = n_steps - 1;
+    if (n_steps > 0) {
+        load_step(phys(0), S0{});
         store_step(S0{}, S0{});
-        if constexpr (PF == 2) load_step(min(s_begin + 1, last), S1{});
+        if constexpr (PF == 2) load_step(phys(min(1u, last)), S1{});
     }
     __syncthreads();
-    uint32_t ks = s_begin;
-    for (; ks + 2 <= s_end; ks += 2) {
+    uint32_t j = 0;
+    for (; j + 2 <= n_steps; j += 2) {
         if constexpr (PF == 2) {
-            load_step(min(ks + 2, last), S0{});
+            load_step(phys(min(j + 2, last)), S0{});
             __builtin_amdgcn_sched_barrier(0);  // issue the prefetch before the MFMAs
             compute(S0{});
             store_step(S1{}, S1{});
+            interleave_step<kMfma, kRead0, kReads - kRead0, kValu, kWrites>();
             __syncthreads();
-            load_step(min(ks + 3, last), S1{});
+            load_step(phys(min(j + 3, last)), S1{});
             __builtin_amdgcn_sched_barrier(0);
             compute(S1{});
             store_step(S0{}, S0{});
+            interleave_step<kMfma, kRead0, kReads - kRead0, kValu, kWrites>();
             __syncthreads();
         } else {
-            load_step(ks + 1, S0{});
+            load_step(phys(j + 1), S0{});
             __builtin_amdgcn_sched_barrier(0);
             compute(S0{});
             store_step(S0{}, S1{});
             __syncthreads();
-            load_step(min(ks + 2, last), S0{});
+            load_step(phys(min(j + 2, last)), S0{});
             __builtin_amdgcn_sched_barrier(0);
             compute(S1{});
             store_step(S0{}, S0{});
             __syncthreads();
         }
     }
-    if (ks < s_end) compute(S0{});
+    if (j < n_steps) compute(S0{});
 
     // Epilogue. Lane holds column l32 of each 32x32 tile and rows 8(r/4) + 4g + r%4.
     float* C = a.C + static_cast<uint64_t>(blockIdx.z) * a.sC;
@@ -319,7 +357,9 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
                 if constexpr (SPLITK) {
                     unsafeAtomicAdd(c, acc[i][j][r]);  // native global_atomic_add_f32
                 } else {
-                    if (a.mode == 0) *c = acc[i][j][r] + bv;
+                    // C is written once and not re-read here: streaming stores keep
+                    // it from displacing the A / W working set in L2.
+                    if (a.mode == 0) __builtin_nontemporal_store(acc[i][j][r] + bv, c);
                     else *c += acc[i][j][r];
                 }
             }
@@ -344,14 +384,9 @@ void launch_init(float* C, const float* bias, uint32_t M, uint32_t N, uint32_t l
 
 // ---- configurations -------------------------------------------------------------
 
-struct Cfg {
-    int bm, bn, kb;
-    int ctas_per_cu;  // resident workgroups per CU (LDS / VGPR bound)
-};
-
-enum CfgId { kC256x128 = 0, kC128x128, kC128x64, kC64x64, kC256x256w4, kC256x128w4, kNumCfg };
-constexpr Cfg kCfgs[kNumCfg] = {{256, 128, 2, 1}, {128, 128, 2, 2}, {128, 64, 2, 2}, {64, 64, 2, 4},
-                                {256, 256, 2, 1}, {256, 128, 2, 1}};
+// Tile shapes (BM x BN, waves WM x WN, two 32-wide K blocks per step). The
+// 256x256 tile keeps one register set in flight (PF = 1) to stay within 256 VGPRs.
+enum CfgId { kC256x128 = 0, kC128x128, kC128x64, kC64x64, kC256x256, kNumCfg };
 
 template <int BM, int BN, int WM, int WN, int KB, int WK, bool KTAIL, int PF = 2>
 void launch_cfg(const GemmArgs& a0, uint32_t batch, uint32_t splits, hipStream_t s) {
@@ -378,8 +413,7 @@ void launch(int cfg, const GemmArgs& a, uint32_t batch, uint32_t splits, hipStre
         case kC256x128: launch_cfg<256, 128, 4, 2, 2, WK, false>(a, batch, splits, s); break;
         case kC128x128: launch_cfg<128, 128, 2, 2, 2, WK, false>(a, batch, splits, s); break;
         case kC128x64: launch_cfg<128, 64, 2, 2, 2, WK, false>(a, batch, splits, s); break;
-        case kC256x256w4: launch_cfg<256, 256, 2, 2, 2, WK, false, 1>(a, batch, splits, s); break;
-        case kC256x128w4: launch_cfg<256, 128, 2, 2, 2, WK, false, 2>(a, batch, splits, s); break;
+        case kC256x256: launch_cfg<256, 256, 4, 2, 2, WK, false, 1>(a, batch, splits, s); break;
         default: launch_cfg<64, 64, 2, 2, 2, WK, false>(a, batch, splits, s); break;
     }
 }
@@ -395,7 +429,8 @@ void launch_general(const GemmArgs& a, uint32_t batch, uint32_t splits, hipStrea
 constexpr int kCUs = 256;
 
 // Picks the tile and K split for a shape (measured on MI355X over the SDXL
-// projection shapes): 256x128 tiles once they give at least half a wave of
+// projection shapes): 256x256 tiles when they nearly fill the 256 CUs and K is
+// moderate, else 256x128 tiles once they give at least half a wave of
 // workgroups per CU; long-K shapes with fewer tiles split K in two; small
 // grids use 64x64 tiles and split K until ~256 workgroups are resident.
 void choose(uint32_t M, uint32_t N, uint32_t K, uint32_t batch, int& cfg, uint32_t& splits) {
@@ -410,8 +445,11 @@ void choose(uint32_t M, uint32_t N, uint32_t K, uint32_t batch, int& cfg, uint32
     }
     const uint64_t t256 = static_cast<uint64_t>(ceil_div(M, 256)) * ceil_div(N, 128) * batch;
     const uint64_t t64 = static_cast<uint64_t>(ceil_div(M, 64)) * ceil_div(N, 64) * batch;
+    const uint64_t tsq = static_cast<uint64_t>(ceil_div(M, 256)) * ceil_div(N, 256) * batch;
     splits = 1;
-    if (t256 >= kCUs / 2) {
+    if (tsq >= 160 && K <= 2048) {
+        cfg = kC256x256;
+    } else if (t256 >= kCUs / 2) {
         cfg = kC256x128;
     } else if (K >= 4096 && t256 * 2 >= kCUs / 2) {
         cfg = kC256x128;

@@ -111,6 +111,13 @@ class DeviceBuffer:
                               out.nbytes, D2H), "hipMemcpy D2H")
         return out
 
+    def copy_from(self, src: "DeviceBuffer", nbytes: int, stream: "Stream | None" = None) -> None:
+        """Device-to-device copy of the first `nbytes` of `src` (asynchronous on `stream`)."""
+        assert nbytes <= self.nbytes and nbytes <= src.nbytes, "copy past the end of a buffer"
+        s = stream.handle if stream else None
+        check(lib().hipMemcpyAsync(ctypes.c_void_p(self.value), ctypes.c_void_p(src.value), nbytes, D2D, s),
+              "hipMemcpyAsync D2D")
+
     def fill_zero(self, stream: "Stream | None" = None) -> None:
         s = stream.handle if stream else None
         check(lib().hipMemsetAsync(ctypes.c_void_p(self.value), 0, self.nbytes, s), "hipMemsetAsync")

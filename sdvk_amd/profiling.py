@@ -1,0 +1,151 @@
+"""Summaries of rocprofv3 output for this library's kernels.
+
+Two reports, both plain text so they can be kept next to the source:
+
+* ``stats``: a ``*_kernel_stats.csv`` (``rocprofv3 --kernel-trace --stats``)
+  turned into a markdown table per kernel plus per-family aggregates
+  (``gemm_q8`` = the GEMM kernels with their split-K init fills, one entry per
+  API call; ``attention`` = the fused attention kernel).
+* ``traffic``: two ``*_counter_collection.csv`` files (``--pmc FETCH_SIZE``,
+  then ``--pmc WRITE_SIZE``) turned into HBM bytes per launch of a family.
+  Each counter (KiB per dispatch) is scaled by what it reads for the runtime's
+  device-to-device copy of a known size in the same run (``bench.py
+  --copy-probe-mib``): the copy reads and writes exactly that many bytes, so
+  ``factor = bytes / (counter x 1024)``.
+
+Usage:
+  python -m sdvk_amd.profiling stats  <kernel_stats.csv> <out.md> --command "<cmd>"
+  python -m sdvk_amd.profiling traffic <fetch.csv> <write.csv> <copy_mib> <family> <out.json> --command "<cmd>"
+"""
+from __future__ import annotations
+
+import argparse
+import collections
+import csv
+import json
+import re
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+FAMILIES = {
+    "gemm_q8": ("gemm_q8_kernel", "gemm_init_kernel"),
+    "attention": ("attn_kernel",),
+}
+COPY_KERNEL = re.compile(r"copyBuffer", re.I)
+
+
+def short_name(name: str) -> str:
+    """`void mi::(anonymous namespace)::gemm_q8_kernel<256, 128, ...>(mi::...)` -> `gemm_q8_kernel<256, 128, ...>`."""
+    if name.startswith("_Z"):
+        tool = shutil.which("c++filt") or shutil.which("llvm-cxxfilt")
+        if tool:
+            name = subprocess.run([tool, name], capture_output=True, text=True).stdout.strip() or name
+        m = re.search(r"\d([a-z][a-z_0-9]*?_kernel)I((?:DF16_|f|Lb[01]E)+)E", name) if name.startswith("_Z") else None
+        if m:  # template arguments this library uses that binutils' demangler may not know (_Float16)
+            toks = re.findall(r"DF16_|f|Lb[01]E", m.group(2))
+            conv = {"DF16_": "_Float16", "f": "float", "Lb0E": "false", "Lb1E": "true"}
+            name = f"{m.group(1)}<{', '.join(conv[t] for t in toks)}>"
+    n = re.sub(r"^void\s+", "", name)
+    n = n.replace("mi::(anonymous namespace)::", "")
+    n = re.sub(r"\(.*\)$", "", n)
+    return n
+
+
+def family_of(name: str) -> str | None:
+    for fam, keys in FAMILIES.items():
+        if any(k in name for k in keys):
+            return fam
+    return None
+
+
+def stats_report(csv_path: str, command: str) -> str:
+    rows = list(csv.DictReader(open(csv_path)))
+    lines = [f"# rocprofv3 kernel statistics", "", f"Command: `{command}`", "",
+             "| kernel | calls | avg us | min us | max us | total % |", "|---|---:|---:|---:|---:|---:|"]
+    fam = collections.defaultdict(lambda: [0, 0.0])  # calls of the main kernel, total ns (incl. helpers)
+    for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"])):
+        name = r["Name"]
+        calls, tot = int(r["Calls"]), float(r["TotalDurationNs"])
+        lines.append(f"| `{short_name(name)}` | {calls} | {float(r['AverageNs']) / 1e3:.2f} | "
+                     f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.2f} |")
+        f = family_of(name)
+        if f:
+            if FAMILIES[f][0] in name:
+                fam[f][0] += calls
+            fam[f][1] += tot
+    lines += ["", "Family aggregates (total time of the family's kernels / calls of its main kernel, i.e. per API "
+                  "call; the GEMM family includes the split-K init fills):", "",
+              "| family | calls | avg us per call |", "|---|---:|---:|"]
+    for f, (calls, tot) in fam.items():
+        if calls:
+            lines.append(f"| {f} | {calls} | {tot / calls / 1e3:.2f} |")
+    return "\n".join(lines) + "\n"
+
+
+def _per_dispatch(csv_path: str, counter: str):
+    out = []
+    for r in csv.DictReader(open(csv_path)):
+        if r["Counter_Name"] == counter:
+            out.append((r["Kernel_Name"], int(r["Grid_Size"]), float(r["Counter_Value"])))
+    return out
+
+
+def traffic_report(fetch_csv: str, write_csv: str, copy_mib: int, family: str, command: str) -> dict:
+    nbytes = copy_mib << 20
+    result = {"family": family, "copy_probe_bytes": nbytes, "command": command}
+    per_shape = collections.OrderedDict()
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        rows = _per_dispatch(path, counter)
+        copies = [v for n, _, v in rows if COPY_KERNEL.search(n)]
+        if not copies:
+            raise SystemExit(f"{path}: no copy-probe dispatch found")
+        factor = nbytes / (max(copies) * 1024.0)
+        result[f"{counter.lower()}_factor"] = round(factor, 5)
+        result[f"{counter.lower()}_copy_kib"] = max(copies)
+        main_key = FAMILIES[family][0]
+        for n, grid, v in rows:
+            if main_key in n:
+                d = per_shape.setdefault((short_name(n), grid), {"fetch": [], "write": []})
+                d["fetch" if counter == "FETCH_SIZE" else "write"].append(v * 1024.0 * factor)
+    shapes = []
+    tot, cnt = 0.0, 0
+    for (name, grid), d in per_shape.items():
+        f = sum(d["fetch"]) / max(len(d["fetch"]), 1)
+        w = sum(d["write"]) / max(len(d["write"]), 1)
+        shapes.append({"kernel": name, "grid": grid, "fetch_bytes": round(f), "write_bytes": round(w),
+                       "dispatches": len(d["fetch"])})
+        tot += (f + w) * len(d["fetch"])
+        cnt += len(d["fetch"])
+    result["per_kernel_grid"] = shapes
+    result["bytes_per_launch"] = round(tot / cnt) if cnt else None
+    return result
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    s = sub.add_parser("stats")
+    s.add_argument("csv")
+    s.add_argument("out")
+    s.add_argument("--command", required=True)
+    t = sub.add_parser("traffic")
+    t.add_argument("fetch_csv")
+    t.add_argument("write_csv")
+    t.add_argument("copy_mib", type=int)
+    t.add_argument("family", choices=sorted(FAMILIES))
+    t.add_argument("out")
+    t.add_argument("--command", required=True)
+    a = ap.parse_args(argv)
+    if a.cmd == "stats":
+        Path(a.out).write_text(stats_report(a.csv, a.command))
+    else:
+        Path(a.out).write_text(json.dumps(traffic_report(a.fetch_csv, a.write_csv, a.copy_mib, a.family,
+                                                         a.command), indent=1) + "\n")
+    print(Path(a.out).read_text())
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -136,7 +136,7 @@ def test_baseline_shapes_sampled_rows(gpu, oracle, M, N, K):
     assert e <= REL_RMS_TOL
 
 
-@pytest.mark.parametrize("cfg", ["0", "1", "2", "3", "0:3", "1:2", "2:5", "3:16"])
+@pytest.mark.parametrize("cfg", ["0", "1", "2", "3", "4", "0:3", "1:2", "2:5", "3:16", "4:2"])
 @pytest.mark.parametrize("M,N,K", [(300, 200, 640), (1030, 130, 256)])
 def test_every_tile_config_and_split_k(gpu, oracle, monkeypatch, cfg, M, N, K):
     """Forces each tile configuration / K split (MI_GEMM_CFG="<cfg>[:<splits>]")."""
