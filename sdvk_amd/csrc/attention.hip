@@ -28,12 +28,18 @@
 //     MFMA per product.
 #include "common.hpp"
 
+#include <type_traits>
+
 namespace mi {
 namespace {
 
 constexpr int kBQ = 128;   // queries per workgroup
 constexpr int kBKV = 64;   // keys per tile
 constexpr int kKld = 72;   // K tile LDS row stride (halves): 64 d + 8 pad
+// V tile LDS layout [G][d][8 keys] with the G stride padded from 64 to 66
+// 16-byte units: the staging stores (16 lanes = 16 key groups of one d block)
+// then spread over the banks instead of hitting one bank in four.
+constexpr int kVG = 66;
 constexpr int kThreads = 256;
 
 struct AttnArgs {
@@ -109,6 +115,19 @@ __device__ __forceinline__ void load4(const T* p, bool vec, int valid, half4& hi
     }
 }
 
+// A buffer offset past every record: the load returns zeros. Valid offsets
+// stay below it (run() bounds a 64-row tile's extent to 2^30 bytes).
+constexpr uint32_t kOob = 0x80000000u;
+
+// Bytes of rows kv0 .. min(kv0 + 64, L) - 1 of a [*, ld] tensor (the last row
+// counted up to hd): the record size of one tile's buffer resource, so rows
+// at or past L read as zeros.
+__device__ __forceinline__ uint32_t tile_bytes(uint32_t kv0, uint32_t L, uint64_t ld, uint32_t hd, uint32_t esz) {
+    if (kv0 >= L) return 0u;
+    const uint32_t rows = min(L - kv0, 64u);
+    return static_cast<uint32_t>(((rows - 1) * ld + hd) * esz);
+}
+
 // Lazy rescaling threshold (exp2 domain): the running max is only raised when
 // a tile's max exceeds it by more than this, so P = exp2(s - m) <= 2^8 stays
 // far inside fp16 range while the O / l rescale runs on few tiles.
@@ -119,7 +138,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
     constexpr bool kSplit = sizeof(TI) == 4;  // fp32 inputs: hi + lo planes
     constexpr int NP = kSplit ? 2 : 1;
     __shared__ _Float16 Ks[2][NP][kBKV * kKld];
-    __shared__ _Float16 Vs[2][NP][kBKV * 64];
+    __shared__ _Float16 Vs[2][NP][8 * kVG * 8];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -158,25 +177,28 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
 
     // Staging. K: chunks of 8 d (thread handles chunks tid and tid + 256: key =
     // c / 8, d0 = 8 (c % 8)), stored row-major. V: a 4-key x 4-d block per
-    // thread (key group kg = tid / 16, d0 = 4 (tid % 16)), transposed in
+    // thread (key group kg = tid % 16, d0 = 4 (tid / 16)), transposed in
     // registers and stored as [G][d][8] halves, G = (t, sp, g) the PV MFMA step
     // and lane half that consumes the key: key 32t + 16sp + 8j + 4g + i sits in
     // slot 4j + i, so a PV fragment is one 16-byte read and the stores are four
     // 8-byte writes.
     half8 kreg[2][NP];
     half4 vreg[4][NP];
-    const int vkg = tid >> 4, vd0 = (tid & 15) * 4;
+    const int vkg = tid & 15, vd0 = (tid >> 4) * 4;
     // Vector path: K/V rows through buffer resources whose base advances with
     // the tile (scalar work only) and whose size ends at key L-1, so rows past
     // the valid keys read as zeros (hardware range check) with no lane guards.
-    const uint32_t k_off0 = ((tid >> 3) * static_cast<uint32_t>(a.ldk) + (tid & 7) * 8) * sizeof(TI);
-    const uint32_t k_off1 = k_off0 + 32u * static_cast<uint32_t>(a.ldk) * sizeof(TI);
-    const uint32_t v_off = (vkg * 4 * static_cast<uint32_t>(a.ldv) + vd0) * sizeof(TI);
+    // Chunks at d >= hd take an offset past every record (the load returns
+    // zeros) instead of reading the neighbouring head's columns.
+    const bool kin = (tid & 7) * 8 < hd;
+    const uint32_t k_off0 = kin ? ((tid >> 3) * static_cast<uint32_t>(a.ldk) + (tid & 7) * 8) * sizeof(TI) : kOob;
+    const uint32_t k_off1 = kin ? k_off0 + 32u * static_cast<uint32_t>(a.ldk) * sizeof(TI) : kOob;
+    const uint32_t v_off = vd0 < hd ? (vkg * 4 * static_cast<uint32_t>(a.ldv) + vd0) * sizeof(TI) : kOob;
     const uint32_t v_row = static_cast<uint32_t>(a.ldv) * sizeof(TI);
     auto load_tile = [&](uint32_t kv0) {
         if constexpr (VEC) {
-            const uint32_t kbytes = kv0 < L ? ((L - kv0 - 1) * static_cast<uint32_t>(a.ldk) + a.hd) * sizeof(TI) : 0u;
-            const uint32_t vbytes = kv0 < L ? ((L - kv0 - 1) * static_cast<uint32_t>(a.ldv) + a.hd) * sizeof(TI) : 0u;
+            const uint32_t kbytes = tile_bytes(kv0, L, a.ldk, a.hd, sizeof(TI));
+            const uint32_t vbytes = tile_bytes(kv0, L, a.ldv, a.hd, sizeof(TI));
             const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
                 const_cast<TI*>(Kp + static_cast<uint64_t>(kv0) * a.ldk), 0, static_cast<int>(kbytes), 0x00020000);
             const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
@@ -249,7 +271,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
         for (int pl = 0; pl < NP; ++pl)
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                *reinterpret_cast<half4*>(&Vs[st][pl][(vG * 64 + vd0 + e) * 8 + vslot]) =
+                *reinterpret_cast<half4*>(&Vs[st][pl][(vG * kVG + vd0 + e) * 8 + vslot]) =
                     half4{vreg[0][pl][e], vreg[1][pl][e], vreg[2][pl][e], vreg[3][pl][e]};
     };
 
@@ -340,7 +362,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
                     const int d = 32 * u + l32;
 #pragma unroll
                     for (int pl = 0; pl < NP; ++pl) {
-                        const half8 vf = *reinterpret_cast<const half8*>(&Vs[st][pl][(G * 64 + d) * 8]);
+                        const half8 vf = *reinterpret_cast<const half8*>(&Vs[st][pl][(G * kVG + d) * 8]);
                         o[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, o[u], 0, 0, 0);
                     }
                 }
@@ -377,6 +399,315 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
         }
 }
 
+
+// ---- fp16 inputs: software-pipelined kernel --------------------------------
+//
+// Same math as attn_kernel, arranged so that matrix and vector work overlap
+// inside each wave (a wave issues in order, so an MFMA only hides VALU work
+// placed between MFMAs): iteration j issues the S MFMAs of tile j+1 between
+// the exp2 / fp16 packing of tile j, then the PV MFMAs of tile j between the
+// scale / max of tile j+1. Every LDS fragment of an iteration is read up
+// front. K runs one tile ahead of V in LDS (K tiles j+1, j+2; V tiles j,
+// j+1), so one barrier per tile keeps both double buffers race-free. The
+// workgroup has NW waves of 32 queries; blocks are mapped so that the
+// workgroups of one (batch, head) share an XCD (and its L2).
+template <typename TO, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t qtiles) {
+    constexpr int NT = 64 * NW, BQ = 32 * NW;
+    constexpr int KCH = 512 / NT;  // 16-byte K chunks per thread per tile
+    constexpr int VBL = 256 / NT;  // 4-key x 4-d V blocks per thread per tile
+    __shared__ _Float16 Ks[2][kBKV * kKld];
+    __shared__ _Float16 Vs[2][8 * kVG * 8];
+
+    const unsigned blk = xcd_swizzle(blockIdx.x, gridDim.x);
+    const uint32_t qt = blk % qtiles, bh = blk / qtiles;
+    const uint32_t h = bh % a.heads, b = bh / a.heads;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, g = lane >> 5;
+    const uint32_t qcta = qt * BQ, qwave = qcta + wave * 32, qi = qwave + l32;
+    const int hd = static_cast<int>(a.hd);
+
+    uint32_t L = a.Tk;
+    if (a.kv_len) {
+        int32_t l = a.kv_len[b];
+        L = l < 0 ? 0u : (static_cast<uint32_t>(l) < a.Tk ? static_cast<uint32_t>(l) : a.Tk);
+    }
+    uint32_t kend = L;
+    if (a.causal) kend = min(kend, qcta + BQ);
+    uint32_t kfull = L / kBKV * kBKV;
+    if (a.causal) kfull = min(kfull, (qwave + 1) / kBKV * kBKV);
+    const uint32_t ntiles = (kend + kBKV - 1) / kBKV;
+
+    const _Float16* Qp = static_cast<const _Float16*>(a.q) + b * a.sq + static_cast<uint64_t>(h) * a.hd;
+    const _Float16* Kp = static_cast<const _Float16*>(a.k) + b * a.sk + static_cast<uint64_t>(h) * a.hd;
+    const _Float16* Vp = static_cast<const _Float16*>(a.v) + b * a.sv + static_cast<uint64_t>(h) * a.hd;
+
+    half8 qf[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const int d0 = 16 * s + 8 * g;
+        qf[s] = qi < a.Tq && d0 < hd ? *reinterpret_cast<const half8*>(Qp + static_cast<uint64_t>(qi) * a.ldq + d0)
+                                     : zero8();
+    }
+
+    // Staging offsets (bytes from the tile's first row). K: chunk c = tid + i NT
+    // is key c / 8, d 8 (c % 8). V: block c = tid + i NT is keys 4 (c % 16) .. +3,
+    // d 4 (c / 16) .. +3. Chunks at d >= hd read zeros.
+    uint32_t k_off[KCH], v_off[VBL];
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+        const int c = tid + i * NT;
+        k_off[i] = (c & 7) * 8 < hd ? ((c >> 3) * static_cast<uint32_t>(a.ldk) + (c & 7) * 8) * 2u : kOob;
+    }
+#pragma unroll
+    for (int i = 0; i < VBL; ++i) {
+        const int c = tid + i * NT;
+        v_off[i] = (c >> 4) * 4 < hd ? ((c & 15) * 4 * static_cast<uint32_t>(a.ldv) + (c >> 4) * 4) * 2u : kOob;
+    }
+    const uint32_t v_row = static_cast<uint32_t>(a.ldv) * 2u;
+    half8 kreg[KCH];
+    half4 vreg[VBL][4];
+    auto load_k = [&](uint32_t kv0) {
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<_Float16*>(Kp + static_cast<uint64_t>(kv0) * a.ldk), 0,
+            static_cast<int>(tile_bytes(kv0, L, a.ldk, a.hd, 2)), 0x00020000);
+#pragma unroll
+        for (int i = 0; i < KCH; ++i)
+            kreg[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(r, k_off[i], 0, 0));
+    };
+    auto load_v = [&](uint32_t kv0) {
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<_Float16*>(Vp + static_cast<uint64_t>(kv0) * a.ldv), 0,
+            static_cast<int>(tile_bytes(kv0, L, a.ldv, a.hd, 2)), 0x00020000);
+#pragma unroll
+        for (int i = 0; i < VBL; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                vreg[i][e] = __builtin_bit_cast(half4, __builtin_amdgcn_raw_buffer_load_b64(r, v_off[i] + e * v_row, 0, 0));
+    };
+    auto store_k = [&](int st) {
+#pragma unroll
+        for (int i = 0; i < KCH; ++i) {
+            const int c = tid + i * NT;
+            *reinterpret_cast<half8*>(&Ks[st][(c >> 3) * kKld + (c & 7) * 8]) = kreg[i];
+        }
+    };
+    // V as [G][d][8]: key 32t + 16sp + 8j + 4g' + i sits in group G = 4t + 2sp + g',
+    // slot 4j + i (the PV step (t, sp) and lane half g' that consume it).
+    auto store_v = [&](int st) {
+#pragma unroll
+        for (int i = 0; i < VBL; ++i) {
+            const int c = tid + i * NT;
+            const int vkg = c & 15, vd0 = (c >> 4) * 4;
+            const int vG = (vkg >> 3) * 4 + ((vkg >> 2) & 1) * 2 + (vkg & 1);
+            const int vslot = ((vkg >> 1) & 1) * 4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                *reinterpret_cast<half4*>(&Vs[st][(vG * kVG + vd0 + e) * 8 + vslot]) =
+                    half4{vreg[i][0][e], vreg[i][1][e], vreg[i][2][e], vreg[i][3][e]};
+        }
+    };
+
+    half8 kf[2][4], vf[2][2][2];
+    auto read_k = [&](int st) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                kf[t][s] = *reinterpret_cast<const half8*>(&Ks[st][(32 * t + l32) * kKld + 16 * s + 8 * g]);
+    };
+    auto read_v = [&](int st) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int sp = 0; sp < 2; ++sp)
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+                    vf[t][sp][u] = *reinterpret_cast<const half8*>(&Vs[st][((t * 4 + sp * 2 + g) * kVG + 32 * u + l32) * 8]);
+    };
+    // S^T = K Q^T: rows (keys) kv0 + 32t + 8(r/4) + 4g + r%4, column = query qi
+    auto qk = [&](floatx16 (&sc)[2]) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sc[t][r] = 0.0f;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[t][s], qf[s], sc[t], 0, 0, 0);
+        }
+    };
+    auto mask = [&](floatx16 (&sc)[2], uint32_t kv0) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t key = kv0 + 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
+                if (key >= L || (a.causal && key > qi)) sc[t][r] = -INFINITY;
+            }
+    };
+    auto lane_max = [&](const floatx16 (&sc)[2]) {
+        float m0 = fmaxf(sc[0][0], sc[0][1]), m1 = fmaxf(sc[1][0], sc[1][1]);
+#pragma unroll
+        for (int r = 2; r < 16; r += 2) {
+            m0 = fmaxf(m0, fmaxf(sc[0][r], sc[0][r + 1]));
+            m1 = fmaxf(m1, fmaxf(sc[1][r], sc[1][r + 1]));
+        }
+        const float mx = fmaxf(m0, m1);
+        // the partner lane (lane ^ 32) holds the query's other 32 keys
+        const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, mx),
+                                                          __builtin_bit_cast(unsigned, mx), false, false);
+        return fmaxf(__builtin_bit_cast(float, sw[0]), __builtin_bit_cast(float, sw[1]));
+    };
+    auto exp_pack = [&](const floatx16 (&sc)[2], half8 (&pf)[2][2]) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int sp = 0; sp < 2; ++sp)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) pf[t][sp][i] = static_cast<_Float16>(__builtin_amdgcn_exp2f(sc[t][8 * sp + i]));
+    };
+
+    floatx16 o[3];  // O^T for d in [0, 32), [32, 64); row sums of P (all-ones A operand)
+#pragma unroll
+    for (int u = 0; u < 3; ++u)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[u][r] = 0.0f;
+    const half8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+    auto pv = [&](const half8 (&pf)[2][2]) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int sp = 0; sp < 2; ++sp) {
+                o[2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones, pf[t][sp], o[2], 0, 0, 0);
+#pragma unroll
+                for (int u = 0; u < 2; ++u) o[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[t][sp][u], pf[t][sp], o[u], 0, 0, 0);
+            }
+    };
+
+    if (ntiles > 0) {
+        // prologue: K tiles 0, 1 and V tile 0 in LDS; S of tile 0; the running
+        // max starts at tile 0's max (every query has a valid key in tile 0:
+        // key 0 < L, and key 0 <= qi under the causal mask)
+        load_k(0);
+        load_v(0);
+        store_k(0);
+        store_v(0);
+        if (ntiles > 1) {
+            load_k(kBKV);
+            store_k(1);
+        }
+        __syncthreads();
+        read_k(0);
+        floatx16 s0[2];
+        qk(s0);
+        if (0 >= kfull) mask(s0, 0);
+        const float mx0 = lane_max(s0);
+        float m = mx0 == -INFINITY ? 0.0f : mx0 * a.c;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s0[t][r] = __builtin_fmaf(s0[t][r], a.c, -m);
+        __syncthreads();  // every wave has read K tile 0 before it is overwritten
+
+        // One pipelined iteration; boundary tiles (key padding, Tk end, causal
+        // diagonal) take the masked instantiation so that neither body branches
+        // between its two phases.
+        auto step = [&](uint32_t j, auto masked) {
+            constexpr bool kMasked = decltype(masked)::value;
+            const uint32_t kv1 = (j + 1) * kBKV;
+            const bool more = j + 2 < ntiles;
+            if (more) load_k(kv1 + kBKV);
+            load_v(kv1);
+            read_k((j + 1) & 1);
+            read_v(j & 1);
+            __builtin_amdgcn_sched_barrier(0);
+
+            // phase A: S of tile j+1 (8 MFMA) || exp2 + fp16 pack of tile j
+            floatx16 s1[2];
+            half8 pf[2][2];
+            qk(s1);
+            exp_pack(s0, pf);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+
+            // phase B: PV of tile j (12 MFMA) || mask + scale + max of tile j+1
+            pv(pf);
+            if constexpr (kMasked) mask(s1, kv1);
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) s1[t][r] = __builtin_fmaf(s1[t][r], a.c, -m);
+            const float mx = lane_max(s1);
+#pragma unroll
+            for (int i = 0; i < 12; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, kMasked ? 10 : 4, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (__any(mx > kLazy)) {  // raise the running max (rare)
+                const float d = fmaxf(mx, 0.0f);
+                const float alpha = __builtin_amdgcn_exp2f(-d);
+                m += d;
+#pragma unroll
+                for (int u = 0; u < 3; ++u)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) o[u][r] *= alpha;
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) s1[t][r] -= d;
+            }
+#pragma unroll
+            for (int t = 0; t < 2; ++t) s0[t] = s1[t];
+            if (more) store_k(j & 1);
+            store_v((j + 1) & 1);
+            __syncthreads();
+        };
+        for (uint32_t j = 0; j + 1 < ntiles; ++j) {
+            if ((j + 1) * kBKV >= kfull) step(j, std::true_type{});
+            else step(j, std::false_type{});
+        }
+        // last tile
+        read_v((ntiles - 1) & 1);
+        half8 pf[2][2];
+        exp_pack(s0, pf);
+        pv(pf);
+    }
+
+    const float lt = o[2][0];
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    if (qi >= a.Tq) return;
+    TO* Op = static_cast<TO*>(a.o) + b * a.so + static_cast<uint64_t>(qi) * a.ldo + static_cast<uint64_t>(h) * a.hd;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int run = 0; run < 4; ++run) {
+            const int d0 = 32 * u + 8 * run + 4 * g;
+            if (d0 >= hd) continue;
+            if constexpr (sizeof(TO) == 4) {
+                *reinterpret_cast<floatx4*>(Op + d0) =
+                    floatx4{o[u][4 * run] * inv, o[u][4 * run + 1] * inv, o[u][4 * run + 2] * inv, o[u][4 * run + 3] * inv};
+            } else {
+                *reinterpret_cast<half4*>(Op + d0) =
+                    half4{static_cast<_Float16>(o[u][4 * run] * inv), static_cast<_Float16>(o[u][4 * run + 1] * inv),
+                          static_cast<_Float16>(o[u][4 * run + 2] * inv), static_cast<_Float16>(o[u][4 * run + 3] * inv)};
+            }
+        }
+}
+
+template <typename TO>
+void launch_f16(const AttnArgs& a, uint32_t batch, hipStream_t s) {
+    // 4-wave workgroups when they give at least two per CU, else 2-wave ones
+    const uint32_t q4 = ceil_div(a.Tq, 128u), q2 = ceil_div(a.Tq, 64u);
+    const uint64_t groups = static_cast<uint64_t>(a.heads) * batch;
+    if (q4 * groups >= 512) attn_f16_kernel<TO, 4><<<static_cast<unsigned>(q4 * groups), 256, 0, s>>>(a, q4);
+    else attn_f16_kernel<TO, 2><<<static_cast<unsigned>(q2 * groups), 128, 0, s>>>(a, q2);
+}
+
 template <typename TI, typename TO>
 void launch_typed(const AttnArgs& a, uint32_t batch, bool vec, hipStream_t s) {
     dim3 grid(ceil_div(a.Tq, kBQ), a.heads, batch);
@@ -396,6 +727,9 @@ int run(const mi_attn_args& x, hipStream_t s, const char* fn) {
     const uint64_t ldq = x.ldq ? x.ldq : x.C, ldk = x.ldk ? x.ldk : x.C, ldv = x.ldv ? x.ldv : x.C,
                    ldo = x.ldo ? x.ldo : x.C;
     if (ldq < x.C || ldk < x.C || ldv < x.C || ldo < x.C) return fail(MI_ERR_INVALID_ARG, "%s: token stride < C", fn);
+    // a 64-row K/V tile must span under 2^30 bytes (32-bit buffer offsets)
+    if (ldk * 64 * 4 >= (1ull << 30) || ldv * 64 * 4 >= (1ull << 30))
+        return fail(MI_ERR_UNSUPPORTED, "%s: K/V token stride too large", fn);
     const uint64_t sq = x.sq ? x.sq : x.Tq * ldq, sk = x.sk ? x.sk : x.Tk * ldk, sv = x.sv ? x.sv : x.Tk * ldv,
                    so = x.so ? x.so : x.Tq * ldo;
     const uint64_t ei = x.in_dtype == MI_F32 ? 4 : 2, eo = x.out_dtype == MI_F32 ? 4 : 2;
@@ -425,7 +759,13 @@ int run(const mi_attn_args& x, hipStream_t s, const char* fn) {
                      aligned(x.out, vout) && (ldq * ei) % 16 == 0 && (ldk * ei) % 16 == 0 && (ldv * ei) % 16 == 0 &&
                      (sq * ei) % 16 == 0 && (sk * ei) % 16 == 0 && (sv * ei) % 16 == 0 && (ldo * eo) % vout == 0 &&
                      (so * eo) % vout == 0 && (a.hd * ei) % vin == 0;
-    if (x.in_dtype == MI_F16 && x.out_dtype == MI_F16) launch_typed<_Float16, _Float16>(a, x.batch, vec, s);
+    // fp16 inputs on the vector path: the pipelined kernel (one workgroup per
+    // 64 or 128 queries of one (batch, head), 1-D grid)
+    const bool fast = vec && x.in_dtype == MI_F16 &&
+                      static_cast<uint64_t>(ceil_div(x.Tq, 64u)) * x.heads * x.batch < (1ull << 31);
+    if (fast && x.out_dtype == MI_F16) launch_f16<_Float16>(a, x.batch, s);
+    else if (fast) launch_f16<float>(a, x.batch, s);
+    else if (x.in_dtype == MI_F16 && x.out_dtype == MI_F16) launch_typed<_Float16, _Float16>(a, x.batch, vec, s);
     else if (x.in_dtype == MI_F16) launch_typed<_Float16, float>(a, x.batch, vec, s);
     else if (x.out_dtype == MI_F16) launch_typed<float, _Float16>(a, x.batch, vec, s);
     else launch_typed<float, float>(a, x.batch, vec, s);
