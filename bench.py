@@ -107,6 +107,73 @@ class AttnCase:
                                     stream=stream)
 
 
+class BlockStack:
+    """ten SDXL BasicTransformerBlocks at level 2 (1280
+    channels, 2 x 1024 tokens, 20 heads, context 2 x 77 x 2048, FF 1280 ->
+    10240 -> 5120 -> 1280), Q8_0 linear weights from N(0, 0.02^2), biases
+    N(0, 0.02^2), LayerNorm gamma = 1, beta = 0. Each block has its own
+    weights: windows of one device pool of N(0, 0.02^2) values at distinct
+    offsets, quantized on the device."""
+
+    DIMS = (2, 1024, 1280, 20, 77, 2048, 5120)  # batch, tokens, channels, heads, ctx_tokens, ctx_channels, ff_inner
+
+    def __init__(self, rng, hip, ops, nblocks=10):
+        B, T, C, H, Tc, Cc, F = self.DIMS
+        self.ops, self.hip, self.nblocks = ops, hip, nblocks
+        self.dims = ops.BlockDims(*self.DIMS)
+        shapes = {"attn1_q": (C, C), "attn1_k": (C, C), "attn1_v": (C, C), "attn1_out": (C, C),
+                  "attn2_q": (C, C), "attn2_k": (C, Cc), "attn2_v": (C, Cc), "attn2_out": (C, C),
+                  "ff_up": (2 * F, C), "ff_down": (C, F)}
+        pool_n = 16 << 20
+        pool = hip.DeviceBuffer.from_array(rng.standard_normal(pool_n, dtype=np.float32) * np.float32(0.02))
+        ones, zeros = np.ones(C, np.float32), np.zeros(C, np.float32)
+        self.keep = [pool]
+        self.weights = []
+        for i in range(nblocks):
+            d = {}
+            for j, (nm, (n, k)) in enumerate(shapes.items()):
+                cnt = n * k
+                off = ((i * len(shapes) + j) * 1000003 * 32) % (pool_n - cnt) // 32 * 32
+                d[nm] = hip.DeviceBuffer(cnt // 32 * 34)
+                ops.q8_0_quantize(pool.value + 4 * off, d[nm], cnt)
+            for nm, n in {"attn1_out_b": C, "attn2_out_b": C, "ff_up_b": 2 * F, "ff_down_b": C}.items():
+                d[nm] = hip.DeviceBuffer.from_array(rng.standard_normal(n, dtype=np.float32) * np.float32(0.02))
+            for nm in ("norm1", "norm2", "norm3"):
+                d[nm + "_w"] = hip.DeviceBuffer.from_array(ones)
+                d[nm + "_b"] = hip.DeviceBuffer.from_array(zeros)
+            self.keep.append(d)
+            self.weights.append(ops.BlockWeights(**d))
+        self.x = hip.DeviceBuffer.from_array(rng.standard_normal(B * T * C, dtype=np.float32))
+        self.ctx = hip.DeviceBuffer.from_array(
+            rng.standard_normal(B * Tc * Cc, dtype=np.float32).astype(np.float16).astype(np.float32))
+        self.ws = hip.DeviceBuffer(ops.block_workspace_bytes(self.dims))
+        rows, crow = B * T, B * Tc
+        self.flops_per_block = (2.0 * rows * C * C * 4 + 4.0 * B * H * T * T * (C // H)          # self-attention
+                                + 2.0 * rows * C * C * 2 + 2.0 * crow * C * Cc * 2 + 4.0 * B * H * T * Tc * (C // H)
+                                + 2.0 * rows * 2 * F * C + 2.0 * rows * C * F)                   # GEGLU FF
+
+    def run(self, stream):
+        for w in self.weights:
+            self.ops.sdxl_block_forward(w, self.dims, self.x, self.ctx, self.ws, stream=stream)
+
+    def measure(self, stream, reps):
+        self.run(stream)
+        stream.synchronize()
+        a, b = self.hip.Event(), self.hip.Event()
+        a.record(stream)
+        for _ in range(reps):
+            self.run(stream)
+        b.record(stream)
+        b.synchronize()
+        ms = a.elapsed_ms(b) / reps
+        flops = self.flops_per_block * self.nblocks
+        return {"config": "BASELINE config 4: %d SDXL BasicTransformerBlocks, level 2 (C=1280, 2x1024 tokens, "
+                          "20 heads, ctx 2x77x2048, FF 1280->10240->5120->1280), Q8_0 weights, fp32 activations"
+                          % self.nblocks,
+                "blocks": self.nblocks, "latency_ms": round(ms, 4), "ms_per_block": round(ms / self.nblocks, 4),
+                "gflop": round(flops / 1e9, 1), "tflops": round(flops / (ms / 1e3) / 1e12, 2), "reps": reps}
+
+
 def roofline_pct(c, seconds):
     ai = c.flops / c.bytes
     roof = min(PEAK_FP16_TFLOPS, ai * PEAK_HBM_GBS / 1e3)
@@ -163,8 +230,8 @@ def main() -> int:
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run one device-to-device copy of this many MiB first (profiler byte calibration)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["gemm", "attention"], default=None,
-                    help="profile one kernel family (breakdown only)")
+    ap.add_argument("--only", choices=["gemm", "attention", "block"], default=None,
+                    help="run one part only (profiling): a kernel family, or the config-4 block stack")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (multi-GPU sharding is "
@@ -178,6 +245,11 @@ def main() -> int:
         raise SystemExit("no HIP device")
     rng = np.random.default_rng(1)
     stream = hip.Stream()
+    if args.only == "block":
+        stack = BlockStack(rng, hip, ops)
+        res = stack.measure(stream, max(args.steps // 4, 1))
+        print(json.dumps({"block_stack": res}), flush=True)
+        return 0
     cases = []
     if args.only in (None, "gemm"):
         cases += [GemmCase(t, M, N, K, rng, hip, ops) for t, M, N, K in GEMM_SHAPES]
@@ -269,6 +341,13 @@ def main() -> int:
                 "algorithmic_flop_per_launch": fam_flops[dom] / fam_launch[dom],
                 "algorithmic_bytes_per_launch": fam_bytes[dom] / fam_launch[dom]}
 
+    block = None
+    if args.only is None:
+        print("[bench] config-4 block stack", file=sys.stderr, flush=True)
+        block = BlockStack(rng, hip, ops).measure(stream, 5)
+        print(f"[bench] block stack: {block['latency_ms']:.3f} ms for {block['blocks']} blocks "
+              f"({block['tflops']:.1f} TFLOP/s)", file=sys.stderr, flush=True)
+
     cpu = None
     if not args.no_cpu_baseline and args.only is None:
         threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
@@ -297,6 +376,7 @@ def main() -> int:
                    "step_gflop": round(step_flops / 1e9, 3)},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "block_stack": block,
         "breakdown": breakdown,
     }
     print(json.dumps(out), flush=True)

@@ -83,6 +83,12 @@ int mi_q8_split_dequant(const uint32_t* payload, const float* scales, void* out,
 int mi_q8_0_to_split(const void* blocks, uint32_t* payload, float* scales, uint64_t n,
                      void* stream);
 
+/* Quantizer with the reference's requantization rule (sdvkgen.cpp:533-544):
+ * per block of 32, d = fp16(amax / 127), q = clamp(trunc(w * 127 / amax
+ * +- 0.5), -127, 127), all-zero blocks -> d = 0, q = 0. w: fp32, 4-byte
+ * aligned, n % 32 == 0; blocks: 34-byte entries, 2-byte aligned.           */
+int mi_q8_0_quantize(const float* w, void* blocks, uint64_t n, void* stream);
+
 /* ---------------------------------------------------------------- GEMM -- *
  * C[M,N] (=|+=) A[M,K] . deq(W[N,K])^T (+ bias[N])
  *   A      fp32 row-major, row stride lda (0 -> K), batch stride sA
@@ -160,6 +166,57 @@ typedef struct mi_attn_args {
 } mi_attn_args;
 
 int mi_fused_attention_ex(const mi_attn_args* args, void* stream);
+
+/* --------------------------------------------------------- block glue -- *
+ * The SDXL transformer block's row / elementwise operators, fp32.          */
+
+/* layernorm (sdvkgen.cpp:1094-1103, layernorm_fwd.comp:15-38): per row of d,
+ * y = (x - mean) / sqrt(var + eps) [* gamma + beta], mean and var in two
+ * passes. gamma and beta both NULL (no affine) or both set. y may equal x. */
+int mi_layernorm(const float* x, const float* gamma, const float* beta, float* y, uint32_t rows,
+                 uint32_t d, float eps, void* stream);
+
+/* geglu (sdvkgen.cpp:1709-1720, unary_fwd.comp:28-36): h = [rows, 2F],
+ * y[r, j] = h[r, j] * gelu_erf(h[r, F + j]), erf by Abramowitz-Stegun 7.1.26. */
+int mi_geglu(const float* h, float* y, uint32_t rows, uint32_t F, void* stream);
+
+/* add2 in place (sdvkgen.cpp:1746,1751,1762): x[i] += a[i], i < n.         */
+int mi_add_inplace(float* x, const float* a, uint64_t n, void* stream);
+
+/* One SDXL BasicTransformerBlock (diffusers parameter names), in the order of
+ * spatialTransformer's inner loop (sdvkgen.cpp:1739-1763) with crossAttention
+ * (:1283-1290) and geglu (:1709-1720): LayerNorm -> self-attention -> add ->
+ * LayerNorm -> cross-attention on ctx -> add -> LayerNorm -> GEGLU FF -> add.
+ * Linear weights are Q8_0 blocks [out, in] (K = in, a multiple of 32);
+ * LayerNorm eps = 1e-5 with affine. Rows are batch-stacked: x is
+ * [batch * tokens, channels] (updated in place), ctx is
+ * [batch * ctx_tokens, ctx_channels]; attention runs per batch item.
+ * ctx_len: device int32[batch] key-padding lengths for the cross-attention,
+ * or NULL. workspace: device memory of mi_block_workspace_bytes() bytes,
+ * 256-byte aligned; nothing is allocated. Calls sharing a workspace must be
+ * ordered (same stream).                                                   */
+typedef struct mi_block_weights {
+    const float *norm1_w, *norm1_b, *norm2_w, *norm2_b, *norm3_w, *norm3_b; /* [channels] */
+    const void *attn1_q, *attn1_k, *attn1_v, *attn1_out;    /* [channels, channels] */
+    const float* attn1_out_b;                                /* [channels] or NULL */
+    const void* attn2_q;                                     /* [channels, channels] */
+    const void *attn2_k, *attn2_v;                           /* [channels, ctx_channels] */
+    const void* attn2_out;                                   /* [channels, channels] */
+    const float* attn2_out_b;                                /* [channels] or NULL */
+    const void* ff_up;                                       /* [2 ff_inner, channels] */
+    const float* ff_up_b;                                    /* [2 ff_inner] or NULL */
+    const void* ff_down;                                     /* [channels, ff_inner] */
+    const float* ff_down_b;                                  /* [channels] or NULL */
+} mi_block_weights;
+
+typedef struct mi_block_dims {
+    uint32_t batch, tokens, channels, heads, ctx_tokens, ctx_channels, ff_inner;
+} mi_block_dims;
+
+uint64_t mi_block_workspace_bytes(const mi_block_dims* dims);
+int mi_sdxl_block_forward(const mi_block_weights* w, const mi_block_dims* dims, float* x,
+                          const float* ctx, const int32_t* ctx_len, void* workspace,
+                          uint64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -234,3 +234,50 @@ def geglu(h, rows, F):
     y = np.empty(rows * F, dtype=np.float32)
     lib().or_geglu(_p(h), _p(y), rows, F)
     return y
+
+
+def add(a, b):
+    c = np.empty_like(a, dtype=np.float32)
+    lib().or_add(_p(np.ascontiguousarray(a, np.float32)), _p(np.ascontiguousarray(b, np.float32)), _p(c), a.size)
+    return c
+
+
+# ----------------------------------------------------------- transformer block --
+
+BLOCK_FIELDS = ("norm1_w", "norm1_b", "norm2_w", "norm2_b", "norm3_w", "norm3_b",
+                "attn1_q", "attn1_k", "attn1_v", "attn1_out", "attn1_out_b",
+                "attn2_q", "attn2_k", "attn2_v", "attn2_out", "attn2_out_b",
+                "ff_up", "ff_up_b", "ff_down", "ff_down_b")
+
+
+def sdxl_block(w: dict, x, ctx, *, batch, tokens, channels, heads, ctx_tokens, ctx_channels, ff_inner,
+               ctx_len=None, threads=1):
+    """One SDXL BasicTransformerBlock on the oracle's primitives, in the order of
+    sdvkgen.cpp:1739-1763 (crossAttention :1283-1290, geglu :1709-1720):
+    LN1 -> self-attention -> add -> LN2 -> cross-attention on ctx -> add -> LN3
+    -> GEGLU FF -> add. Linear weights are Q8_0 blocks [out, in]; x is
+    [batch * tokens, channels], ctx [batch * ctx_tokens, ctx_channels].
+    GEMMs accumulate in fp64, attention is the fp64 online softmax."""
+    rows, crow, C = batch * tokens, batch * ctx_tokens, channels
+    x = np.array(x, dtype=np.float32, copy=True)
+
+    def lin(a, wq, bias, m, n, k):
+        return gemm_nt_q8_0(np.ascontiguousarray(a, np.float32), wq, m, n, k, bias=bias, threads=threads)
+
+    def attn(a_q, a_kv, prefix, m_kv, tk, k_in, kl):
+        q = lin(a_q, w[prefix + "_q"], None, rows, C, C)
+        k = lin(a_kv, w[prefix + "_k"], None, m_kv, C, k_in)
+        v = lin(a_kv, w[prefix + "_v"], None, m_kv, C, k_in)
+        o = fused_attention_ex(q, k, v, batch=batch, Tq=tokens, Tk=tk, C=C, heads=heads, kv_len=kl,
+                               threads=threads).reshape(-1)
+        return lin(o, w[prefix + "_out"], w[prefix + "_out_b"], rows, C, C)
+
+    n = layernorm(x, w["norm1_w"], w["norm1_b"], rows, C)
+    x = add(x, attn(n, n, "attn1", rows, tokens, C, None))
+    n = layernorm(x, w["norm2_w"], w["norm2_b"], rows, C)
+    x = add(x, attn(n, np.ascontiguousarray(ctx, np.float32), "attn2", crow, ctx_tokens, ctx_channels, ctx_len))
+    n = layernorm(x, w["norm3_w"], w["norm3_b"], rows, C)
+    h = lin(n, w["ff_up"], w["ff_up_b"], rows, 2 * ff_inner, C)
+    g = geglu(h, rows, ff_inner)
+    x = add(x, lin(g, w["ff_down"], w["ff_down_b"], rows, C, ff_inner))
+    return x

@@ -32,6 +32,21 @@ class MiAttnArgs(ctypes.Structure):
     ]
 
 
+class MiBlockWeights(ctypes.Structure):
+    """Mirror of mi_block_weights (include/mi_sdvk.h)."""
+    _fields_ = [(n, _vp) for n in (
+        "norm1_w", "norm1_b", "norm2_w", "norm2_b", "norm3_w", "norm3_b",
+        "attn1_q", "attn1_k", "attn1_v", "attn1_out", "attn1_out_b",
+        "attn2_q", "attn2_k", "attn2_v", "attn2_out", "attn2_out_b",
+        "ff_up", "ff_up_b", "ff_down", "ff_down_b")]
+
+
+class MiBlockDims(ctypes.Structure):
+    """Mirror of mi_block_dims (include/mi_sdvk.h)."""
+    _fields_ = [(n, _u32) for n in ("batch", "tokens", "channels", "heads", "ctx_tokens", "ctx_channels",
+                                    "ff_inner")]
+
+
 SIGNATURES = {
     "mi_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "mi_last_error": (ctypes.c_char_p, []),
@@ -39,6 +54,7 @@ SIGNATURES = {
     "mi_q8_0_dequant": (ctypes.c_int, [_vp, _vp, ctypes.c_int, _u64, _vp]),
     "mi_q8_split_dequant": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_int, _u64, _vp]),
     "mi_q8_0_to_split": (ctypes.c_int, [_vp, _vp, _vp, _u64, _vp]),
+    "mi_q8_0_quantize": (ctypes.c_int, [_vp, _vp, _u64, _vp]),
     "mi_gemm_nt_q8_0": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32,
                                        _u64, _u64, _vp]),
     "mi_gemm_nt_q8_split": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32,
@@ -46,6 +62,12 @@ SIGNATURES = {
     "mi_fused_attn_supported": (ctypes.c_int, [_u32, _u32]),
     "mi_fused_attention": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, ctypes.c_int, _vp]),
     "mi_fused_attention_ex": (ctypes.c_int, [ctypes.POINTER(MiAttnArgs), _vp]),
+    "mi_layernorm": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, ctypes.c_float, _vp]),
+    "mi_geglu": (ctypes.c_int, [_vp, _vp, _u32, _u32, _vp]),
+    "mi_add_inplace": (ctypes.c_int, [_vp, _vp, _u64, _vp]),
+    "mi_block_workspace_bytes": (_u64, [ctypes.POINTER(MiBlockDims)]),
+    "mi_sdxl_block_forward": (ctypes.c_int, [ctypes.POINTER(MiBlockWeights), ctypes.POINTER(MiBlockDims), _vp, _vp,
+                                             _vp, _vp, _u64, _vp]),
 }
 
 _lib = None

@@ -1,0 +1,134 @@
+// block.hip -- one SDXL BasicTransformerBlock (diffusers layout) on the
+// library's kernels, in the reference's order (src/Modules/Diffusion/
+// sdvkgen.cpp:1739-1763, crossAttention :1283-1290, geglu :1709-1720):
+//
+//   n = LN1(x); x += attn1(n, n)        attn(a, b) = out(attention(q(a), k(b), v(b))) + out_bias
+//   n = LN2(x); x += attn2(n, ctx)
+//   n = LN3(x); x += ff_down(geglu(ff_up(n) + up_bias)) + down_bias
+//
+// Rows are batch-stacked ([batch * tokens, C]); self- and cross-attention run
+// per batch item through the batched attention entry. All intermediates live
+// in a caller-provided workspace (nothing is allocated), every launch is
+// ordered on the caller's stream.
+#include "common.hpp"
+
+namespace mi {
+namespace {
+
+struct Workspace {
+    float *n, *q, *k, *v, *o, *a, *h, *g;
+};
+
+uint64_t round256(uint64_t b) { return (b + 255) / 256 * 256; }
+
+// Byte layout of the workspace; returns the total.
+uint64_t layout(const mi_block_dims& d, char* base, Workspace* w) {
+    const uint64_t rows = static_cast<uint64_t>(d.batch) * d.tokens;
+    const uint64_t crow = static_cast<uint64_t>(d.batch) * d.ctx_tokens;
+    const uint64_t kvrows = rows > crow ? rows : crow;
+    const uint64_t sizes[8] = {rows * d.channels, rows * d.channels, kvrows * d.channels, kvrows * d.channels,
+                               rows * d.channels, rows * d.channels, rows * 2ull * d.ff_inner, rows * d.ff_inner};
+    float** slots[8] = {&w->n, &w->q, &w->k, &w->v, &w->o, &w->a, &w->h, &w->g};
+    uint64_t off = 0;
+    for (int i = 0; i < 8; ++i) {
+        if (base) *slots[i] = reinterpret_cast<float*>(base + off);
+        off += round256(sizes[i] * 4);
+    }
+    return off;
+}
+
+int check_dims(const mi_block_dims& d, const char* fn) {
+    if (!d.batch || !d.tokens || !d.channels || !d.heads || !d.ctx_tokens || !d.ctx_channels || !d.ff_inner)
+        return fail(MI_ERR_INVALID_ARG, "%s: zero dimension", fn);
+    if (!mi_fused_attn_supported(d.channels, d.heads))
+        return fail(MI_ERR_UNSUPPORTED, "%s: channels %u / heads %u not served by the fused attention", fn, d.channels,
+                    d.heads);
+    if (d.channels % 32 || d.ctx_channels % 32 || d.ff_inner % 32)
+        return fail(MI_ERR_UNSUPPORTED, "%s: channels, ctx_channels and ff_inner must be multiples of 32 (Q8_0 K)", fn);
+    return MI_OK;
+}
+
+#define MI_TRY(expr)              \
+    do {                          \
+        const int st_ = (expr);   \
+        if (st_ != MI_OK) return st_; \
+    } while (0)
+
+int attention(const mi_block_dims& d, const float* q, const float* k, const float* v, float* o, uint32_t tk,
+              const int32_t* kv_len, hipStream_t s) {
+    mi_attn_args x{};
+    x.q = q;
+    x.k = k;
+    x.v = v;
+    x.out = o;
+    x.batch = d.batch;
+    x.Tq = d.tokens;
+    x.Tk = tk;
+    x.C = d.channels;
+    x.heads = d.heads;
+    x.in_dtype = MI_F32;
+    x.out_dtype = MI_F32;
+    x.kv_len = kv_len;
+    return mi_fused_attention_ex(&x, s);
+}
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" uint64_t mi_block_workspace_bytes(const mi_block_dims* dims) {
+    if (!dims) return 0;
+    Workspace w;
+    return layout(*dims, nullptr, &w);
+}
+
+extern "C" int mi_sdxl_block_forward(const mi_block_weights* wt, const mi_block_dims* dims, float* x, const float* ctx,
+                                     const int32_t* ctx_len, void* workspace, uint64_t workspace_bytes, void* stream) {
+    const char* fn = "mi_sdxl_block_forward";
+    if (!wt || !dims || !x || !ctx || !workspace) return fail(MI_ERR_INVALID_ARG, "%s: null pointer", fn);
+    const mi_block_dims d = *dims;
+    MI_TRY(check_dims(d, fn));
+    const mi_block_weights w = *wt;
+    const void* mats[10] = {w.attn1_q, w.attn1_k, w.attn1_v, w.attn1_out, w.attn2_q,
+                            w.attn2_k, w.attn2_v, w.attn2_out, w.ff_up, w.ff_down};
+    for (const void* m : mats)
+        if (!m) return fail(MI_ERR_INVALID_ARG, "%s: null weight", fn);
+    Workspace ws;
+    const uint64_t need = layout(d, static_cast<char*>(workspace), &ws);
+    if (workspace_bytes < need)
+        return fail(MI_ERR_INVALID_ARG, "%s: workspace %llu bytes < %llu needed", fn,
+                    static_cast<unsigned long long>(workspace_bytes), static_cast<unsigned long long>(need));
+    if (!aligned(workspace, 256)) return fail(MI_ERR_ALIGNMENT, "%s: workspace must be 256-byte aligned", fn);
+
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint32_t rows = d.batch * d.tokens, crow = d.batch * d.ctx_tokens, C = d.channels;
+    const uint64_t nx = static_cast<uint64_t>(rows) * C;
+    auto gemm = [&](const float* A, const void* W, const float* bias, float* out, uint32_t M, uint32_t N, uint32_t K) {
+        return mi_gemm_nt_q8_0(A, W, bias, out, M, N, K, 0, 0, 0, 1, 0, 0, s);
+    };
+
+    // self-attention
+    MI_TRY(mi_layernorm(x, w.norm1_w, w.norm1_b, ws.n, rows, C, 1e-5f, s));
+    MI_TRY(gemm(ws.n, w.attn1_q, nullptr, ws.q, rows, C, C));
+    MI_TRY(gemm(ws.n, w.attn1_k, nullptr, ws.k, rows, C, C));
+    MI_TRY(gemm(ws.n, w.attn1_v, nullptr, ws.v, rows, C, C));
+    MI_TRY(attention(d, ws.q, ws.k, ws.v, ws.o, d.tokens, nullptr, s));
+    MI_TRY(gemm(ws.o, w.attn1_out, w.attn1_out_b, ws.a, rows, C, C));
+    MI_TRY(mi_add_inplace(x, ws.a, nx, s));
+    // cross-attention over the context
+    MI_TRY(mi_layernorm(x, w.norm2_w, w.norm2_b, ws.n, rows, C, 1e-5f, s));
+    MI_TRY(gemm(ws.n, w.attn2_q, nullptr, ws.q, rows, C, C));
+    MI_TRY(gemm(ctx, w.attn2_k, nullptr, ws.k, crow, C, d.ctx_channels));
+    MI_TRY(gemm(ctx, w.attn2_v, nullptr, ws.v, crow, C, d.ctx_channels));
+    MI_TRY(attention(d, ws.q, ws.k, ws.v, ws.o, d.ctx_tokens, ctx_len, s));
+    MI_TRY(gemm(ws.o, w.attn2_out, w.attn2_out_b, ws.a, rows, C, C));
+    MI_TRY(mi_add_inplace(x, ws.a, nx, s));
+    // GEGLU feed-forward
+    MI_TRY(mi_layernorm(x, w.norm3_w, w.norm3_b, ws.n, rows, C, 1e-5f, s));
+    MI_TRY(gemm(ws.n, w.ff_up, w.ff_up_b, ws.h, rows, 2 * d.ff_inner, C));
+    MI_TRY(mi_geglu(ws.h, ws.g, rows, d.ff_inner, s));
+    MI_TRY(gemm(ws.g, w.ff_down, w.ff_down_b, ws.a, rows, C, d.ff_inner));
+    MI_TRY(mi_add_inplace(x, ws.a, nx, s));
+    return MI_OK;
+}

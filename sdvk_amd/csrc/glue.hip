@@ -1,0 +1,215 @@
+// glue.hip -- the SDXL transformer block's elementwise / row kernels for gfx950:
+// LayerNorm, GEGLU and the in-place residual add.
+//
+// Reference behaviour:
+//   * LayerNorm: src/Modules/Diffusion/sdvkgen.cpp:1094-1103 and
+//     shaders/layernorm_fwd.comp:15-38 -- per row of d, mean first, then the
+//     mean of squared deviations (two passes, no E[x^2] - mean^2), eps inside
+//     the square root, optional affine gamma / beta;
+//   * GEGLU: sdvkgen.cpp:1709-1720 -- h = [rows, 2F] (one linear), y = h[:, :F]
+//     * gelu(h[:, F:]) with the erf GELU of unary_fwd.comp:28-36
+//     (Abramowitz & Stegun 7.1.26, |error| <= 1.5e-7);
+//   * residual add: add2 {t, t, a} in place (sdvkgen.cpp:1746,1751,1762).
+//
+// All three are HBM-bound: each element is read and written once. LayerNorm
+// keeps a wave's row in registers (one wave per row, float4 lanes) so the
+// two passes cost no extra traffic; GEGLU and add stream float4 with a
+// grid-stride loop.
+#include "common.hpp"
+
+namespace mi {
+namespace {
+
+constexpr int kLnCache = 16;  // float4 per lane cached in registers: rows up to 64 * 4 * 16 = 4096
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// One wave per row; 4 rows per 256-thread workgroup. d % 4 == 0, 16-byte aligned rows.
+__global__ __launch_bounds__(256) void layernorm_vec_kernel(const float* __restrict__ x, const float* __restrict__ gamma,
+                                                            const float* __restrict__ beta, float* __restrict__ y,
+                                                            uint32_t rows, uint32_t d, float eps) {
+    const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const uint32_t n4 = d / 4;
+    const floatx4* xr = reinterpret_cast<const floatx4*>(x + static_cast<uint64_t>(row) * d);
+    floatx4* yr = reinterpret_cast<floatx4*>(y + static_cast<uint64_t>(row) * d);
+    floatx4 c[kLnCache];
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kLnCache; ++i) {
+        const uint32_t j = lane + 64 * i;
+        c[i] = j < n4 ? xr[j] : floatx4{0, 0, 0, 0};
+        s += (c[i][0] + c[i][1]) + (c[i][2] + c[i][3]);
+    }
+    const float mean = wave_sum(s) / static_cast<float>(d);
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kLnCache; ++i) {
+        const uint32_t j = lane + 64 * i;
+        if (j < n4) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float dv = c[i][e] - mean;
+                ss += dv * dv;
+            }
+        }
+    }
+    const float var = wave_sum(ss) / static_cast<float>(d);
+    const float inv = 1.0f / sqrtf(var + eps);
+#pragma unroll
+    for (int i = 0; i < kLnCache; ++i) {
+        const uint32_t j = lane + 64 * i;
+        if (j < n4) {
+            floatx4 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = (c[i][e] - mean) * inv;
+            if (gamma) {
+                const floatx4 g = reinterpret_cast<const floatx4*>(gamma)[j];
+                const floatx4 b = reinterpret_cast<const floatx4*>(beta)[j];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = v[e] * g[e] + b[e];
+            }
+            yr[j] = v;
+        }
+    }
+}
+
+// General rows (any d, any alignment): one wave per row, three passes over memory.
+__global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict__ x, const float* __restrict__ gamma,
+                                                        const float* __restrict__ beta, float* __restrict__ y,
+                                                        uint32_t rows, uint32_t d, float eps) {
+    const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float* xr = x + static_cast<uint64_t>(row) * d;
+    float* yr = y + static_cast<uint64_t>(row) * d;
+    float s = 0.0f;
+    for (uint32_t j = lane; j < d; j += 64) s += xr[j];
+    const float mean = wave_sum(s) / static_cast<float>(d);
+    float ss = 0.0f;
+    for (uint32_t j = lane; j < d; j += 64) {
+        const float dv = xr[j] - mean;
+        ss += dv * dv;
+    }
+    const float inv = 1.0f / sqrtf(wave_sum(ss) / static_cast<float>(d) + eps);
+    for (uint32_t j = lane; j < d; j += 64) {
+        float v = (xr[j] - mean) * inv;
+        if (gamma) v = v * gamma[j] + beta[j];
+        yr[j] = v;
+    }
+}
+
+// erf GELU, Abramowitz & Stegun 7.1.26 (the published rational approximation
+// the reference shader uses): erf(z) ~ 1 - (a1 t + ... + a5 t^5) exp(-z^2),
+// t = 1 / (1 + p z), z >= 0, odd extension.
+__device__ __forceinline__ float gelu_erf(float v) {
+    const float xs = v * 0.70710678118654752440f;
+    const float ax = fabsf(xs);
+    const float t = 1.0f / (1.0f + 0.3275911f * ax);
+    const float poly = ((((1.061405429f * t - 1.453152027f) * t + 1.421413741f) * t - 0.284496736f) * t + 0.254829592f) * t;
+    const float e = 1.0f - poly * expf(-ax * ax);
+    const float erf = xs >= 0.0f ? e : -e;
+    return 0.5f * v * (1.0f + erf);
+}
+
+// y[r, j] = h[r, j] * gelu(h[r, F + j]); F % 4 == 0 and 16-byte aligned rows.
+__global__ __launch_bounds__(256) void geglu_vec_kernel(const float* __restrict__ h, float* __restrict__ y, uint32_t rows,
+                                                        uint32_t F) {
+    const uint32_t f4 = F / 4;
+    const uint64_t total = static_cast<uint64_t>(rows) * f4;
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < total; i += static_cast<uint64_t>(gridDim.x) * 256) {
+        const uint64_t r = i / f4, j = i % f4;
+        const floatx4* hr = reinterpret_cast<const floatx4*>(h + r * 2 * F);
+        const floatx4 a = hr[j], b = hr[f4 + j];
+        floatx4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = a[e] * gelu_erf(b[e]);
+        reinterpret_cast<floatx4*>(y + r * F)[j] = o;
+    }
+}
+
+__global__ __launch_bounds__(256) void geglu_kernel(const float* __restrict__ h, float* __restrict__ y, uint32_t rows,
+                                                    uint32_t F) {
+    const uint64_t total = static_cast<uint64_t>(rows) * F;
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < total; i += static_cast<uint64_t>(gridDim.x) * 256) {
+        const uint64_t r = i / F, j = i % F;
+        y[i] = h[r * 2 * F + j] * gelu_erf(h[r * 2 * F + F + j]);
+    }
+}
+
+__global__ __launch_bounds__(256) void add_vec_kernel(floatx4* __restrict__ x, const floatx4* __restrict__ a, uint64_t n4) {
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n4; i += static_cast<uint64_t>(gridDim.x) * 256) {
+        floatx4 v = x[i];
+        const floatx4 w = a[i];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += w[e];
+        x[i] = v;
+    }
+}
+
+__global__ __launch_bounds__(256) void add_kernel(float* __restrict__ x, const float* __restrict__ a, uint64_t n) {
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += static_cast<uint64_t>(gridDim.x) * 256) x[i] += a[i];
+}
+
+// Grid for a grid-stride elementwise kernel: enough workgroups to cover the
+// work, capped at 8 per CU.
+unsigned stride_grid(uint64_t items) {
+    const uint64_t g = (items + 255) / 256;
+    return static_cast<unsigned>(g < 2048 ? (g ? g : 1) : 2048);
+}
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" int mi_layernorm(const float* x, const float* gamma, const float* beta, float* y, uint32_t rows, uint32_t d,
+                            float eps, void* stream) {
+    const char* fn = "mi_layernorm";
+    if (!x || !y) return fail(MI_ERR_INVALID_ARG, "%s: null pointer", fn);
+    if ((gamma == nullptr) != (beta == nullptr)) return fail(MI_ERR_INVALID_ARG, "%s: gamma and beta go together", fn);
+    if (rows == 0) return MI_OK;
+    if (d == 0) return fail(MI_ERR_INVALID_ARG, "%s: d == 0", fn);
+    const uint64_t bytes = static_cast<uint64_t>(rows) * d * 4;
+    if (x != y && overlaps(x, bytes, y, bytes)) return fail(MI_ERR_ALIASING, "%s: y partially overlaps x", fn);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool vec = d % 4 == 0 && d <= 64u * 4 * kLnCache && aligned(x, 16) && aligned(y, 16) &&
+                     (!gamma || (aligned(gamma, 16) && aligned(beta, 16)));
+    const unsigned grid = ceil_div(rows, 4);
+    if (vec) layernorm_vec_kernel<<<grid, 256, 0, s>>>(x, gamma, beta, y, rows, d, eps);
+    else layernorm_kernel<<<grid, 256, 0, s>>>(x, gamma, beta, y, rows, d, eps);
+    return check_launch(fn);
+}
+
+extern "C" int mi_geglu(const float* h, float* y, uint32_t rows, uint32_t F, void* stream) {
+    const char* fn = "mi_geglu";
+    if (!h || !y) return fail(MI_ERR_INVALID_ARG, "%s: null pointer", fn);
+    if (rows == 0 || F == 0) return MI_OK;
+    if (overlaps(h, static_cast<uint64_t>(rows) * 2 * F * 4, y, static_cast<uint64_t>(rows) * F * 4))
+        return fail(MI_ERR_ALIASING, "%s: y overlaps h", fn);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (F % 4 == 0 && aligned(h, 16) && aligned(y, 16))
+        geglu_vec_kernel<<<stride_grid(static_cast<uint64_t>(rows) * F / 4), 256, 0, s>>>(h, y, rows, F);
+    else
+        geglu_kernel<<<stride_grid(static_cast<uint64_t>(rows) * F), 256, 0, s>>>(h, y, rows, F);
+    return check_launch(fn);
+}
+
+extern "C" int mi_add_inplace(float* x, const float* a, uint64_t n, void* stream) {
+    const char* fn = "mi_add_inplace";
+    if (!x || !a) return fail(MI_ERR_INVALID_ARG, "%s: null pointer", fn);
+    if (n == 0) return MI_OK;
+    if (x != a && overlaps(x, n * 4, a, n * 4)) return fail(MI_ERR_ALIASING, "%s: a partially overlaps x", fn);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (n % 4 == 0 && aligned(x, 16) && aligned(a, 16))
+        add_vec_kernel<<<stride_grid(n / 4), 256, 0, s>>>(reinterpret_cast<floatx4*>(x),
+                                                           reinterpret_cast<const floatx4*>(a), n / 4);
+    else
+        add_kernel<<<stride_grid(n), 256, 0, s>>>(x, a, n);
+    return check_launch(fn);
+}

@@ -90,6 +90,41 @@ __global__ __launch_bounds__(256) void q8_0_to_split_kernel(const uint8_t* __res
 
 constexpr uint64_t kMaxElems = uint64_t(1) << 40;
 
+// Quantizer (sdvkgen.cpp:533-544, the reference's requantization rule): per
+// block of 32, amax = max |w|, d = fp16(amax / 127), q = clamp(trunc(w * 127 /
+// amax +- 0.5), -127, 127); an all-zero block gives d = 0, q = 0. One thread
+// per block. Contraction stays off so that w * inv + 0.5 rounds twice, as in
+// the reference's scalar code.
+__global__ __launch_bounds__(256) void q8_0_quantize_kernel(const float* __restrict__ w, uint8_t* __restrict__ blocks,
+                                                            uint64_t nblocks) {
+#pragma clang fp contract(off)
+    const uint64_t b = blockIdx.x * 256ull + threadIdx.x;
+    if (b >= nblocks) return;
+    const float* x = w + b * 32;
+    float v[32];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        v[i] = x[i];
+        amax = fmaxf(amax, fabsf(v[i]));
+    }
+    const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+    const _Float16 d = static_cast<_Float16>(amax > 0.0f ? amax / 127.0f : 0.0f);
+    uint16_t* out = reinterpret_cast<uint16_t*>(blocks + b * 34);
+    out[0] = __builtin_bit_cast(uint16_t, d);
+#pragma unroll
+    for (int i = 0; i < 32; i += 2) {
+        int q[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const float t = v[i + e] * inv;
+            int r = static_cast<int>(t + (t >= 0.0f ? 0.5f : -0.5f));
+            q[e] = r < -127 ? -127 : (r > 127 ? 127 : r);
+        }
+        out[1 + i / 2] = static_cast<uint16_t>((q[0] & 0xff) | ((q[1] & 0xff) << 8));
+    }
+}
+
 }  // namespace
 }  // namespace mi
 
@@ -152,4 +187,17 @@ extern "C" int mi_q8_0_to_split(const void* blocks, uint32_t* payload, float* sc
     q8_0_to_split_kernel<<<dim3(ceil_div(groups, 256)), 256, 0, static_cast<hipStream_t>(stream)>>>(
         static_cast<const uint8_t*>(blocks), payload, scales, groups);
     return check_launch("mi_q8_0_to_split");
+}
+
+extern "C" int mi_q8_0_quantize(const float* w, void* blocks, uint64_t n, void* stream) {
+    if (n == 0) return MI_OK;
+    if (!w || !blocks) return fail(MI_ERR_INVALID_ARG, "mi_q8_0_quantize: null pointer");
+    if (n % 32 || n > kMaxElems)
+        return fail(MI_ERR_UNSUPPORTED, "mi_q8_0_quantize: n=%llu is not a multiple of 32", (unsigned long long)n);
+    if (!aligned(w, 4) || !aligned(blocks, 2)) return fail(MI_ERR_ALIGNMENT, "mi_q8_0_quantize: alignment");
+    if (overlaps(w, n * 4, blocks, n / 32 * 34)) return fail(MI_ERR_ALIASING, "mi_q8_0_quantize: blocks overlap w");
+    const uint64_t nb = n / 32;
+    q8_0_quantize_kernel<<<dim3(ceil_div(nb, 256)), 256, 0, static_cast<hipStream_t>(stream)>>>(
+        w, static_cast<uint8_t*>(blocks), nb);
+    return check_launch("mi_q8_0_quantize");
 }

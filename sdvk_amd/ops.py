@@ -9,6 +9,10 @@ Names, argument meaning and error behaviour follow the reference
       src/Modules/Diffusion/sdvkgen.cpp:917-936
   Pg push layout + dispatch(kernel_name, bufs, push)
       sdvkgen.cpp:901-903, vk_engine.cpp:1143-1180, KERNELS[] :55-63,123-124
+  layernorm / geglu / add2 (block glue)
+      sdvkgen.cpp:1094-1103, :1709-1720, :1746,1751,1762
+  BlockWeights / BlockDims / sdxl_block_forward (one transformer block)
+      sdvkgen.cpp:1739-1763 with crossAttention :1283-1290
 
 Where the reference calls exit(1) (unsupported attention shape, binding-count
 mismatch) these raise MiError / ValueError instead. Every call goes to
@@ -21,12 +25,13 @@ from dataclasses import dataclass
 from typing import Optional, Sequence
 
 from . import _lib
-from ._lib import MI_F16, MI_F32, MiAttnArgs, MiError, call, ptr
+from ._lib import MI_F16, MI_F32, MiAttnArgs, MiBlockDims, MiBlockWeights, MiError, call, ptr
 
 __all__ = [
     "MiError", "MI_F32", "MI_F16", "FusedAttnArgs", "fused_attn_supported", "fused_attention",
     "fused_attention_ex", "gemm_nt_q8", "gemm_nt_q8_bias", "gemm_nt_q8_0", "q8_0_dequant",
-    "q8_split_dequant", "q8_0_to_split", "Pg", "dispatch", "KERNELS",
+    "q8_split_dequant", "q8_0_to_split", "q8_0_quantize", "Pg", "dispatch", "KERNELS", "layernorm", "geglu", "add2",
+    "BlockWeights", "BlockDims", "block_workspace_bytes", "sdxl_block_forward",
 ]
 
 
@@ -111,9 +116,87 @@ def q8_split_dequant(payload, scales, out, n: int, out_dtype: int = MI_F32, stre
     call("mi_q8_split_dequant", ptr(payload), ptr(scales), ptr(out), out_dtype, n, _s(stream))
 
 
+def q8_0_quantize(w, blocks, n: int, stream=None) -> None:
+    """sdvkgen.cpp:533-544 quantization rule on the device (fp32 -> 34-byte Q8_0 blocks)."""
+    call("mi_q8_0_quantize", ptr(w), ptr(blocks), n, _s(stream))
+
+
 def q8_0_to_split(blocks, payload, scales, n: int, stream=None) -> None:
     """Gguf.cpp:559-583 (readQ8Into) on the device."""
     call("mi_q8_0_to_split", ptr(blocks), ptr(payload), ptr(scales), n, _s(stream))
+
+
+# ------------------------------------------------------------------ block glue --
+
+def layernorm(x, gamma, beta, y, rows: int, d: int, eps: float = 1e-5, stream=None) -> None:
+    """layernorm_fwd (two-pass mean / variance, affine when gamma/beta are given)."""
+    call("mi_layernorm", ptr(x), ptr(gamma), ptr(beta), ptr(y), rows, d, eps, _s(stream))
+
+
+def geglu(h, y, rows: int, F: int, stream=None) -> None:
+    """y = h[:, :F] * gelu_erf(h[:, F:]) for h = [rows, 2F]."""
+    call("mi_geglu", ptr(h), ptr(y), rows, F, _s(stream))
+
+
+def add2(x, a, n: int, stream=None) -> None:
+    """x += a (n floats, in place)."""
+    call("mi_add_inplace", ptr(x), ptr(a), n, _s(stream))
+
+
+@dataclass
+class BlockDims:
+    batch: int
+    tokens: int
+    channels: int
+    heads: int
+    ctx_tokens: int
+    ctx_channels: int
+    ff_inner: int
+
+    def c(self) -> MiBlockDims:
+        return MiBlockDims(self.batch, self.tokens, self.channels, self.heads, self.ctx_tokens,
+                           self.ctx_channels, self.ff_inner)
+
+
+@dataclass
+class BlockWeights:
+    """Device buffers of one block (diffusers names); linear weights are Q8_0 blocks [out, in]."""
+    norm1_w: object
+    norm1_b: object
+    norm2_w: object
+    norm2_b: object
+    norm3_w: object
+    norm3_b: object
+    attn1_q: object
+    attn1_k: object
+    attn1_v: object
+    attn1_out: object
+    attn1_out_b: object
+    attn2_q: object
+    attn2_k: object
+    attn2_v: object
+    attn2_out: object
+    attn2_out_b: object
+    ff_up: object
+    ff_up_b: object
+    ff_down: object
+    ff_down_b: object
+
+    def c(self) -> MiBlockWeights:
+        return MiBlockWeights(*[ptr(getattr(self, f[0])) for f in MiBlockWeights._fields_])
+
+
+def block_workspace_bytes(dims: BlockDims) -> int:
+    return int(_lib.load().mi_block_workspace_bytes(ctypes.byref(dims.c())))
+
+
+def sdxl_block_forward(w: BlockWeights, dims: BlockDims, x, ctx, workspace, *, ctx_len=None,
+                       workspace_bytes: Optional[int] = None, stream=None) -> None:
+    """One SDXL BasicTransformerBlock, x [batch*tokens, channels] updated in place."""
+    nbytes = workspace_bytes if workspace_bytes is not None else getattr(workspace, "nbytes", 0)
+    wc, dc = w.c(), dims.c()
+    call("mi_sdxl_block_forward", ctypes.byref(wc), ctypes.byref(dc), ptr(x), ptr(ctx), ptr(ctx_len),
+         ptr(workspace), nbytes, _s(stream))
 
 
 # --------------------------------------------- reference kernel-name dispatch --

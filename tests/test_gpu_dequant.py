@@ -68,3 +68,22 @@ def test_split_dequant_arbitrary_fp32_scales(gpu, oracle):
     ops.q8_split_dequant(DeviceBuffer.from_array(payload), DeviceBuffer.from_array(scales), out, n)
     synchronize()
     _bits_equal(out.download(np.float32, n), want)
+
+
+def test_quantize_bit_exact(gpu, oracle):
+    """mi_q8_0_quantize vs the oracle's restatement of sdvkgen.cpp:533-544:
+    N(0, 0.02^2) weights plus edge blocks (all zero, exact halves, one
+    non-zero, huge / tiny magnitudes)."""
+    w = oracle.normal(41, 32 * 4096, 0.0, 0.02)
+    edge = np.zeros(32 * 6, np.float32)
+    edge[32:64] = np.arange(32, dtype=np.float32) - 15.5          # .5 steps relative to amax
+    edge[64] = 1e-3                                                # one non-zero
+    edge[96:128] = np.linspace(-6e4, 6e4, 32, dtype=np.float32)    # near the fp16 top
+    edge[128:160] = np.linspace(-1e-6, 1e-6, 32, dtype=np.float32) # fp16 subnormal scale
+    edge[160:192] = 127.0 * np.sign(np.arange(32) - 15.5).astype(np.float32)
+    for x in (w, edge):
+        n = x.size
+        dw, db = DeviceBuffer.from_array(x), DeviceBuffer(n // 32 * 34)
+        ops.q8_0_quantize(dw, db, n)
+        synchronize()
+        assert np.array_equal(db.download(np.uint8, n // 32 * 34), oracle.q8_0_quantize(x))

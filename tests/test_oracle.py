@@ -353,3 +353,68 @@ def test_layernorm_gelu_geglu(oracle):
     hh = h.reshape(rows, 2 * F).astype(np.float64)
     ge = 0.5 * hh[:, F:] * (1 + np.vectorize(math.erf)(hh[:, F:] / math.sqrt(2)))
     assert np.allclose(gg, hh[:, :F] * ge, atol=1e-5)
+
+
+def _block_weights(oracle, C, Cc, F, seed=100):
+    w, s = {}, seed
+    for nm in ("norm1", "norm2", "norm3"):
+        w[nm + "_w"] = oracle.normal(s, C, 1.0, 0.1); w[nm + "_b"] = oracle.normal(s + 1, C, 0.0, 0.1); s += 2
+    for nm, (n, k) in {"attn1_q": (C, C), "attn1_k": (C, C), "attn1_v": (C, C), "attn1_out": (C, C),
+                       "attn2_q": (C, C), "attn2_k": (C, Cc), "attn2_v": (C, Cc), "attn2_out": (C, C),
+                       "ff_up": (2 * F, C), "ff_down": (C, F)}.items():
+        w[nm] = oracle.q8_0_quantize(oracle.normal(s, n * k, 0.0, 0.08)); s += 1
+    for nm, n in {"attn1_out_b": C, "attn2_out_b": C, "ff_up_b": 2 * F, "ff_down_b": C}.items():
+        w[nm] = oracle.normal(s, n, 0.0, 0.02); s += 1
+    return w
+
+
+def test_block_composition(oracle):
+    """oracle.sdxl_block vs an independent numpy fp64 block (dequantised weights,
+    softmax attention, erf GELU via math.erf): pins the order of the block
+    (sdvkgen.cpp:1739-1763), the GEGLU halves and the key-padding mask."""
+    B, T, C, H, Tc, Cc, F = 2, 24, 64, 2, 7, 96, 96
+    w = _block_weights(oracle, C, Cc, F)
+    x = oracle.normal(1, B * T * C)
+    ctx = oracle.normal(2, B * Tc * Cc)
+    kl = np.array([7, 3], np.int32)
+    got = oracle.sdxl_block(w, x, ctx, batch=B, tokens=T, channels=C, heads=H, ctx_tokens=Tc, ctx_channels=Cc,
+                            ff_inner=F, ctx_len=kl).reshape(B * T, C)
+
+    def deq(nm, n, k):
+        return oracle.q8_0_dequant(w[nm], n * k).astype(np.float64).reshape(n, k)
+
+    def ln(a, g, b):
+        return (a - a.mean(1, keepdims=True)) / np.sqrt(a.var(1, keepdims=True) + 1e-5) * g + b
+
+    def attn(q, k, v, tk, lens):
+        o = np.zeros((B * T, C))
+        hd = C // H
+        for b in range(B):
+            L = tk if lens is None else int(lens[b])
+            for h in range(H):
+                cs = slice(h * hd, (h + 1) * hd)
+                qq = q[b * T:(b + 1) * T, cs]
+                kk, vv = k[b * tk:b * tk + L, cs], v[b * tk:b * tk + L, cs]
+                s = qq @ kk.T / math.sqrt(hd)
+                p = np.exp(s - s.max(1, keepdims=True))
+                o[b * T:(b + 1) * T, cs] = (p @ vv) / p.sum(1, keepdims=True)
+        return o
+
+    X = x.astype(np.float64).reshape(B * T, C)
+    Cx = ctx.astype(np.float64).reshape(B * Tc, Cc)
+    n = ln(X, w["norm1_w"], w["norm1_b"])
+    a = attn(n @ deq("attn1_q", C, C).T, n @ deq("attn1_k", C, C).T, n @ deq("attn1_v", C, C).T, T, None)
+    X = X + a @ deq("attn1_out", C, C).T + w["attn1_out_b"]
+    n = ln(X, w["norm2_w"], w["norm2_b"])
+    a = attn(n @ deq("attn2_q", C, C).T, Cx @ deq("attn2_k", C, Cc).T, Cx @ deq("attn2_v", C, Cc).T, Tc, kl)
+    X = X + a @ deq("attn2_out", C, C).T + w["attn2_out_b"]
+    n = ln(X, w["norm3_w"], w["norm3_b"])
+    hh = n @ deq("ff_up", 2 * F, C).T + w["ff_up_b"]
+    g = hh[:, :F] * (0.5 * hh[:, F:] * (1 + np.vectorize(math.erf)(hh[:, F:] / math.sqrt(2))))
+    X = X + g @ deq("ff_down", C, F).T + w["ff_down_b"]
+    delta_ref = X - x.reshape(B * T, C)
+    delta = got - x.reshape(B * T, C)
+    # fp32 restatement vs fp64 (relative to the RMS of the block's update)
+    e = np.max(np.abs(delta - delta_ref)) / np.sqrt(np.mean(delta_ref ** 2))
+    print(f"block oracle vs fp64: {e:.2e}")
+    assert e <= 2e-5
