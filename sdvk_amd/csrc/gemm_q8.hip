@@ -14,8 +14,9 @@
 //     accumulation). The next step's global loads are in flight while the
 //     current step's MFMAs run (register prefetch + two LDS stages, one
 //     barrier per step);
-//   * workgroup ids are remapped so the tiles of one A row panel run on one
-//     XCD and share its L2;
+//   * workgroup ids are remapped so that each XCD runs a compact block of
+//     tiles (a grouped tile order cut into one contiguous chunk per XCD) and
+//     its workgroups share A and W panels in that XCD's L2;
 //   * grids too small to fill 256 CUs split K: each split adds its partial tile
 //     into C with fp32 atomics after a fill kernel has written bias / 0.
 //     Summation order then varies run to run (last-bit differences only).
@@ -41,7 +42,30 @@ struct GemmArgs {
     uint32_t ksteps;        // ceil(K / BK)
     uint32_t steps_per_split;
     uint32_t rowbytes;      // 34-byte layout: bytes per weight row
+    uint32_t tiles_m;       // ceil(M / BM)
+    uint32_t group_m;       // tile order: groups of group_m row panels, column-major inside a group
 };
+
+GemmArgs make_args(const float* A, const uint8_t* W, const float* scales, const float* bias, float* C, uint32_t M,
+                   uint32_t N, uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldc, uint64_t sA, uint64_t sC,
+                   uint32_t rowbytes) {
+    GemmArgs a{};
+    a.A = A;
+    a.W = W;
+    a.scales = scales;
+    a.bias = bias;
+    a.C = C;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.mode = mode;
+    a.lda = lda;
+    a.ldc = ldc;
+    a.sA = sA;
+    a.sC = sC;
+    a.rowbytes = rowbytes;
+    return a;
+}
 
 enum WKind { kBlocks34 = 0, kSplit = 1 };
 
@@ -116,9 +140,15 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     const int l32 = lane & 31, g = lane >> 5;
     const int wm = wave % WM, wn = wave / WM;
 
-    const unsigned tile = xcd_swizzle(blockIdx.x, gridDim.x);
-    const uint32_t m0 = (tile / a.tiles_n) * BM;
-    const uint32_t n0 = (tile % a.tiles_n) * BN;
+    // Tile order: each XCD takes a contiguous chunk of a grouped order (groups
+    // of group_m row panels, column-major inside a group), so the chunk is a
+    // compact block of tiles and its workgroups share A and W panels in L2.
+    const unsigned lin = xcd_swizzle(blockIdx.x, gridDim.x);
+    const uint32_t gsz = a.group_m * a.tiles_n;
+    const uint32_t grp = lin / gsz, rem = lin % gsz;
+    const uint32_t rows_in = min(a.group_m, a.tiles_m - grp * a.group_m);
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((grp * a.group_m + rem % rows_in) * BM);
+    const uint32_t n0 = __builtin_amdgcn_readfirstlane((rem / rows_in) * BN);
     const uint32_t s_begin = SPLITK ? blockIdx.y * a.steps_per_split : 0;
     const uint32_t s_end = SPLITK ? min(a.ksteps, s_begin + a.steps_per_split) : a.ksteps;
 
@@ -171,8 +201,11 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
 #pragma unroll
         for (int r = 0; r < PF; ++r) w_sh[r][i] = (w_off[i] & 2u) * 8u;
 
-    auto load_step = [&](uint32_t ks, auto RS) {
+    auto load_step = [&](uint32_t ks_in, auto RS) {
         constexpr int rs = decltype(RS)::value;
+        // the step is wave-uniform; say so, or the buffer loads' scalar offsets
+        // are built with a per-lane loop
+        const uint32_t ks = __builtin_amdgcn_readfirstlane(ks_in);
 #pragma unroll
         for (int i = 0; i < A_IT; ++i) {
             if constexpr (KTAIL) {
@@ -290,19 +323,10 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     constexpr int kReads = (FM + FN) * (BK / 16);    // all fragment reads of a step
     constexpr int kWrites = A_IT + W_IT;             // LDS writes of the store phase
     constexpr int kValu = A_IT * 2 + W_IT * 16;      // conversions + dequantisation (approx.)
-    // Workgroups start their K loop at different steps (rotation by tile id):
-    // all workgroups sweep K in lockstep otherwise, so at any moment every CU
-    // would read the same column window of its A panel and the same few L2
-    // channels (rows are lda*4 bytes apart, a multiple of the channel stride
-    // for the SDXL shapes). Step j of this workgroup is physical step
-    // s_begin + (j + rot) mod n.
+    // Every workgroup sweeps K in the same order, so the workgroups that share
+    // a panel read the same K slice at about the same time (L2 reuse).
     const uint32_t n_steps = s_end - s_begin;
-    const uint32_t rot = n_steps ? tile % n_steps : 0;
-    auto phys = [&](uint32_t j) {
-        uint32_t t = j + rot;
-        if (t >= n_steps) t -= n_steps;
-        return s_begin + t;
-    };
+    auto phys = [&](uint32_t j) { return s_begin + j; };
     const uint32_t last = n_steps - 1;
     if (n_steps > 0) {
         load_step(phys(0), S0{});
@@ -330,11 +354,17 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
             __builtin_amdgcn_sched_barrier(0);
             compute(S0{});
             store_step(S0{}, S1{});
+#ifdef MI_GEMM_PF1_INTERLEAVE
+            interleave_step<kMfma, kRead0, kReads - kRead0, kValu, kWrites>();
+#endif
             __syncthreads();
             load_step(phys(min(j + 2, last)), S0{});
             __builtin_amdgcn_sched_barrier(0);
             compute(S1{});
             store_step(S0{}, S0{});
+#ifdef MI_GEMM_PF1_INTERLEAVE
+            interleave_step<kMfma, kRead0, kReads - kRead0, kValu, kWrites>();
+#endif
             __syncthreads();
         }
     }
@@ -388,10 +418,62 @@ void launch_init(float* C, const float* bias, uint32_t M, uint32_t N, uint32_t l
 // 256x256 tile keeps one register set in flight (PF = 1) to stay within 256 VGPRs.
 enum CfgId { kC256x128 = 0, kC128x128, kC128x64, kC64x64, kC256x256, kNumCfg };
 
+// Group height for the tile order: the XCD chunks (blocks b with b % 8 == x,
+// contiguous in the grouped order) each read the A panels of the rows and the
+// W panels of the columns they cover; pick the height that minimises the sum
+// over chunks (A panel = BM*K*4 bytes, W panel = BN*K*34/32 bytes).
+uint32_t pick_group(uint32_t tm, uint32_t tn, uint32_t BM, uint32_t BN, uint32_t K) {
+    const uint64_t tiles = static_cast<uint64_t>(tm) * tn;
+    if (tiles <= 8 || tiles > 65536) return tm;
+    const double pa = static_cast<double>(BM) * K * 4, pw = static_cast<double>(BN) * K * 34.0 / 32.0;
+    uint32_t best = tm;
+    double best_cost = 1e300;
+    for (uint32_t gm = 1;; gm *= 2) {
+        const uint32_t g = std::min(gm, tm);
+        const uint64_t per = tiles / 8, extra = tiles % 8;
+        double cost = 0;
+        uint64_t start = 0;
+        for (uint32_t x = 0; x < 8; ++x) {
+            const uint64_t len = per + (x < extra ? 1 : 0);
+            // rows / columns touched by grouped-order positions [start, start + len)
+            uint32_t rmin = tm, rmax = 0, cmin = tn, cmax = 0;
+            uint64_t pos = start;
+            while (pos < start + len) {
+                const uint64_t gsz = static_cast<uint64_t>(g) * tn;
+                const uint64_t grp = pos / gsz, off = pos % gsz;
+                const uint32_t rows_in = std::min<uint32_t>(g, tm - static_cast<uint32_t>(grp) * g);
+                const uint64_t take = std::min<uint64_t>(start + len - pos, static_cast<uint64_t>(rows_in) * tn - off);
+                const uint32_t c0 = static_cast<uint32_t>(off / rows_in), c1 = static_cast<uint32_t>((off + take - 1) / rows_in);
+                const uint32_t r0 = static_cast<uint32_t>(grp) * g;
+                const uint32_t rlast = take >= rows_in ? r0 + rows_in - 1 : std::max(r0 + static_cast<uint32_t>(off % rows_in), r0 + static_cast<uint32_t>((off + take - 1) % rows_in));
+                const uint32_t rfirst = take >= rows_in ? r0 : std::min(r0 + static_cast<uint32_t>(off % rows_in), r0 + static_cast<uint32_t>((off + take - 1) % rows_in));
+                rmin = std::min(rmin, rfirst);
+                rmax = std::max(rmax, rlast);
+                cmin = std::min(cmin, c0);
+                cmax = std::max(cmax, c1);
+                pos += take;
+            }
+            if (len) cost += (rmax - rmin + 1) * pa + (cmax - cmin + 1) * pw;
+            start += len;
+        }
+        // near-equal cross-XCD costs: prefer a group height near 4 (32 resident
+        // workgroups per XCD then form a 4 x 8 block: reuse inside the XCD)
+        const auto dist = [](uint32_t v) { return v > 4 ? v / 4 : 4 / v; };
+        if (cost < best_cost * 0.999 || (cost <= best_cost * 1.001 && dist(g) < dist(best))) {
+            best_cost = std::min(cost, best_cost);
+            best = g;
+        }
+        if (g >= tm) break;
+    }
+    return best;
+}
+
 template <int BM, int BN, int WM, int WN, int KB, int WK, bool KTAIL, int PF = 2>
 void launch_cfg(const GemmArgs& a0, uint32_t batch, uint32_t splits, hipStream_t s) {
     GemmArgs a = a0;
     a.tiles_n = ceil_div(a.N, BN);
+    a.tiles_m = ceil_div(a.M, BM);
+    a.group_m = pick_group(a.tiles_m, a.tiles_n, BM, BN, a.K);
     a.ksteps = ceil_div(a.K, 32 * KB);
     const unsigned tiles = ceil_div(a.M, BM) * a.tiles_n;
     if (splits > 1) {
@@ -513,8 +595,8 @@ extern "C" int mi_gemm_nt_q8_0(const float* A, const void* W, const float* bias,
         if (mode == 0) launch_init(C, bias, M, N, ldc, sC, batch, static_cast<hipStream_t>(stream));
         return check_launch(fn);
     }
-    GemmArgs a{A, static_cast<const uint8_t*>(W), nullptr, bias, C, M, N, K, mode, lda, ldc, sA, sC, 0, 0, 0,
-               (K / 32) * 34};
+    GemmArgs a = make_args(A, static_cast<const uint8_t*>(W), nullptr, bias, C, M, N, K, mode, lda, ldc, sA, sC,
+                           (K / 32) * 34);
     dispatch<kBlocks34>(a, batch, static_cast<hipStream_t>(stream));
     return check_launch(fn);
 }
@@ -540,7 +622,8 @@ extern "C" int mi_gemm_nt_q8_split(const float* A, const uint32_t* payload, cons
         if (mode == 0) launch_init(C, bias, M, N, ldc, sC, batch, static_cast<hipStream_t>(stream));
         return check_launch(fn);
     }
-    GemmArgs a{A, reinterpret_cast<const uint8_t*>(payload), scales, bias, C, M, N, K, mode, lda, ldc, sA, sC, 0, 0, 0, 0};
+    GemmArgs a = make_args(A, reinterpret_cast<const uint8_t*>(payload), scales, bias, C, M, N, K, mode, lda, ldc, sA,
+                           sC, 0);
     dispatch<kSplit>(a, batch, static_cast<hipStream_t>(stream));
     return check_launch(fn);
 }
