@@ -44,6 +44,8 @@ struct GemmArgs {
     uint32_t rowbytes;      // 34-byte layout: bytes per weight row
     uint32_t tiles_m;       // ceil(M / BM)
     uint32_t group_m;       // tile order: groups of group_m row panels, column-major inside a group
+    uint32_t cvec;          // C rows 16-byte aligned (C % 16 == 0, ldc % 4 == 0, sC % 4 == 0)
+    uint32_t bvec;          // bias 16-byte aligned
 };
 
 GemmArgs make_args(const float* A, const uint8_t* W, const float* scales, const float* bias, float* C, uint32_t M,
@@ -64,6 +66,9 @@ GemmArgs make_args(const float* A, const uint8_t* W, const float* scales, const 
     a.sA = sA;
     a.sC = sC;
     a.rowbytes = rowbytes;
+    const uint32_t ldc_e = ldc ? ldc : N;
+    a.cvec = (reinterpret_cast<uintptr_t>(C) % 16 == 0 && ldc_e % 4 == 0 && sC % 4 == 0) ? 1u : 0u;
+    a.bvec = reinterpret_cast<uintptr_t>(bias) % 16 == 0 ? 1u : 0u;
     return a;
 }
 
@@ -126,6 +131,12 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     constexpr int A_IT = A_UNITS / NT;
     constexpr int W_UNITS = BN * BK / 8;          // (row, 8-k group) per step
     constexpr int W_IT = W_UNITS / NT;
+    // 34-byte blocks with two blocks per step: one whole block per lane (three
+    // loads for 32 weights). Block wb of a step is weight row wb % BN, block
+    // column wb / BN, so a wave's blocks share one byte alignment.
+    constexpr bool WBLK = WK == kBlocks34 && KB == 2 && !KTAIL;
+    constexpr int W_BLOCKS = BN * KB;
+    constexpr int WB_IT = (W_BLOCKS + NT - 1) / NT;
     // Buffer-load fast path: two blocks per step keep each lane's byte
     // alignment fixed (68 = 0 mod 4), so the step advance is a scalar offset.
     constexpr bool FAST = KB == 2 && !KTAIL;
@@ -156,7 +167,11 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     // the last valid row: they only feed outputs that are never stored.
     const float* Apanel = a.A + static_cast<uint64_t>(blockIdx.z) * a.sA + static_cast<uint64_t>(m0) * a.lda;
     const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Apanel), 0, -1, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.W), 0, -1, 0x00020000);
+    // 34-byte layout: records up to W's 16-byte-aligned end (the documented
+    // read extent); the range check zeroes whole dwords only past that.
+    const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(a.W), 0, WK == kBlocks34 ? static_cast<int>((a.N * a.rowbytes + 15u) & ~15u) : -1,
+        0x00020000);
     const __amdgpu_buffer_rsrc_t rS =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(WK == kSplit ? a.scales : a.A), 0, -1, 0x00020000);
     uint32_t a_off[A_IT];
@@ -200,6 +215,21 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     for (int i = 0; i < W_IT; ++i)
 #pragma unroll
         for (int r = 0; r < PF; ++r) w_sh[r][i] = (w_off[i] & 2u) * 8u;
+    // Whole-block staging: the 36-byte window at the block's 4-byte-aligned
+    // start; the row stride is 0 mod 4 (K % 64 == 0) and a step advances 68
+    // bytes, so a block's position inside its window (0 or 2 bytes) is fixed
+    // for the lane. v_perm selectors pick d and the eight q dwords for either.
+    uint32_t wb_off[WB_IT], wb_qsel[WB_IT], wb_dsel[WB_IT];
+    uint32_t wbx_[PF][WB_IT][9];
+#pragma unroll
+    for (int i = 0; i < WB_IT; ++i) {
+        const int wb = tid + i * NT;
+        const uint32_t n = min(n0 + wb % BN, a.N - 1);
+        const uint32_t byte = n * a.rowbytes + (wb / BN) * 34;
+        wb_off[i] = byte & ~3u;
+        wb_qsel[i] = (byte & 2u) ? 0x07060504u : 0x05040302u;  // bytes 4..7 or 2..5 of (x[j+1]:x[j])
+        wb_dsel[i] = (byte & 2u) ? 0x0c0c0302u : 0x0c0c0100u;  // bytes 2,3 or 0,1 of x[0]; 0x0c = zero
+    }
 
     auto load_step = [&](uint32_t ks_in, auto RS) {
         constexpr int rs = decltype(RS)::value;
@@ -216,8 +246,24 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
                 areg_[rs][i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rA, a_off[i], ks * BK * 4, 0));
             }
         }
+        if constexpr (WBLK) {
+            const uint32_t soff = ks * (KB * 34);
 #pragma unroll
-        for (int i = 0; i < W_IT; ++i) {
+            for (int i = 0; i < WB_IT; ++i) {
+                if (W_BLOCKS % NT == 0 || tid + i * NT < W_BLOCKS) {
+                    const auto x0 = __builtin_amdgcn_raw_buffer_load_b128(rW, wb_off[i], soff, 0);
+                    const auto x1 = __builtin_amdgcn_raw_buffer_load_b128(rW, wb_off[i] + 16, soff, 0);
+                    wbx_[rs][i][8] = __builtin_amdgcn_raw_buffer_load_b32(rW, wb_off[i] + 32, soff, 0);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        wbx_[rs][i][e] = x0[e];
+                        wbx_[rs][i][4 + e] = x1[e];
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < (WBLK ? 0 : W_IT); ++i) {
             if constexpr (WK == kBlocks34) {
                 const uint32_t soff = ks * (KB * 34);
                 const uint32_t addr = FAST ? w_off[i] : w_off[i] + soff;
@@ -268,8 +314,26 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
             h[3] = static_cast<_Float16>(areg_[rs][i][3]);
             *reinterpret_cast<half4*>(&As[st][(f / (BK / 4)) * LDK + (f % (BK / 4)) * 4]) = h;
         }
+        if constexpr (WBLK) {
 #pragma unroll
-        for (int i = 0; i < W_IT; ++i) {
+            for (int i = 0; i < WB_IT; ++i) {
+                const int wb = tid + i * NT;
+                if (W_BLOCKS % NT == 0 || wb < W_BLOCKS) {
+                    const uint32_t* x = wbx_[rs][i];
+                    const _Float16 d = __builtin_bit_cast(
+                        _Float16, static_cast<uint16_t>(__builtin_amdgcn_perm(x[0], x[0], wb_dsel[i])));
+                    uint32_t q[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) q[j] = __builtin_amdgcn_perm(x[j + 1], x[j], wb_qsel[i]);
+                    _Float16* dst = &Ws[st][(wb % BN) * LDK + (wb / BN) * 32];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        *reinterpret_cast<half8*>(dst + 8 * j) = dequant8_f16(q[2 * j], q[2 * j + 1], d);
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < (WBLK ? 0 : W_IT); ++i) {
             const int u = tid + i * NT;
             half8 h;
             if constexpr (WK == kBlocks34) {
@@ -306,7 +370,14 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
             for (int i = 0; i < FM; ++i)
 #pragma unroll
                 for (int j = 0; j < FN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+                    // Stores: the transposed product (C^T), so a lane holds row
+                    // m = l32 and four runs of four consecutive columns (16-byte
+                    // stores). Split K: C, so a lane holds column l32 and the
+                    // atomics of one instruction hit 32 consecutive floats.
+                    if constexpr (SPLITK)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+                    else
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[j], af[i], acc[i][j], 0, 0, 0);
         }
     };
     using S0 = std::integral_constant<int, 0>;
@@ -321,8 +392,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     constexpr int kMfma = FM * FN * (BK / 16);       // MFMAs per step
     constexpr int kRead0 = FM + FN;                  // fragment reads of the first k16 slice
     constexpr int kReads = (FM + FN) * (BK / 16);    // all fragment reads of a step
-    constexpr int kWrites = A_IT + W_IT;             // LDS writes of the store phase
-    constexpr int kValu = A_IT * 2 + W_IT * 16;      // conversions + dequantisation (approx.)
+    constexpr int kWrites = A_IT + (WBLK ? 4 * WB_IT : W_IT);            // LDS writes of the store phase
+    constexpr int kValu = A_IT * 2 + (WBLK ? 60 * WB_IT : W_IT * 16);     // conversions + dequantisation (approx.)
     // Every workgroup sweeps K in the same order, so the workgroups that share
     // a panel read the same K slice at about the same time (L2 reuse).
     const uint32_t n_steps = s_end - s_begin;
@@ -370,27 +441,67 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     }
     if (j < n_steps) compute(S0{});
 
-    // Epilogue. Lane holds column l32 of each 32x32 tile and rows 8(r/4) + 4g + r%4.
+    // Epilogue. Stores: lane holds row m = l32 of each 32x32 tile and columns
+    // 8 q + 4 g + e (run q = 0..3, e = 0..3): one 16-byte store per run when C
+    // rows are 16-byte aligned.
     float* C = a.C + static_cast<uint64_t>(blockIdx.z) * a.sC;
+    if constexpr (SPLITK) {
+        // lane holds column l32 and rows 8(r/4) + 4g + r%4 of each 32x32 tile
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const uint32_t n = n0 + wn * TN + 32 * j + l32;
+            if (n >= a.N) continue;
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t m = m0 + wm * TM + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+                    if (m < a.M) unsafeAtomicAdd(C + static_cast<uint64_t>(m) * a.ldc + n, acc[i][j][r]);  // native global_atomic_add_f32
+                }
+        }
+        return;
+    }
+    const bool cvec = a.cvec != 0;
+    const bool use_bias = a.mode == 0 && a.bias;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-        const uint32_t n = n0 + wn * TN + 32 * j + l32;
-        if (n >= a.N) continue;
-        const float bv = (!SPLITK && a.mode == 0 && a.bias) ? a.bias[n] : 0.0f;
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t n = n0 + wn * TN + 32 * j + 8 * q + 4 * g;
+            float b[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (use_bias) {
+                if (a.bvec && n + 3 < a.N) {
+                    const floatx4 b4 = *reinterpret_cast<const floatx4*>(a.bias + n);
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const uint32_t m = m0 + wm * TM + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
-                if (m >= a.M) continue;
-                float* c = C + static_cast<uint64_t>(m) * a.ldc + n;
-                if constexpr (SPLITK) {
-                    unsafeAtomicAdd(c, acc[i][j][r]);  // native global_atomic_add_f32
+                    for (int e = 0; e < 4; ++e) b[e] = b4[e];
                 } else {
-                    // C is written once and not re-read here: streaming stores keep
-                    // it from displacing the A / W working set in L2.
-                    if (a.mode == 0) __builtin_nontemporal_store(acc[i][j][r] + bv, c);
-                    else *c += acc[i][j][r];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) b[e] = n + e < a.N ? a.bias[n + e] : 0.0f;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                const uint32_t m = m0 + wm * TM + 32 * i + l32;
+                if (m >= a.M) continue;
+                float* crow = C + static_cast<uint64_t>(m) * a.ldc;
+                float v[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                if (cvec && n + 3 < a.N) {
+                    floatx4* c4 = reinterpret_cast<floatx4*>(crow + n);
+                    if (a.mode == 0) {
+                        // C is written once and not re-read here: streaming stores keep
+                        // it from displacing the A / W working set in L2.
+                        __builtin_nontemporal_store(floatx4{v[0] + b[0], v[1] + b[1], v[2] + b[2], v[3] + b[3]}, c4);
+                    } else {
+                        const floatx4 o = *c4;
+                        *c4 = floatx4{o[0] + v[0], o[1] + v[1], o[2] + v[2], o[3] + v[3]};
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        if (n + e >= a.N) continue;
+                        if (a.mode == 0) crow[n + e] = v[e] + b[e];
+                        else crow[n + e] += v[e];
+                    }
                 }
             }
         }
@@ -510,11 +621,12 @@ void launch_general(const GemmArgs& a, uint32_t batch, uint32_t splits, hipStrea
 
 constexpr int kCUs = 256;
 
-// Picks the tile and K split for a shape (measured on MI355X over the SDXL
-// projection shapes): 256x256 tiles when they nearly fill the 256 CUs and K is
-// moderate, else 256x128 tiles once they give at least half a wave of
-// workgroups per CU; long-K shapes with fewer tiles split K in two; small
-// grids use 64x64 tiles and split K until ~256 workgroups are resident.
+// Picks the tile and K split for a shape (rules from sweeps of every tile on
+// MI355X over the SDXL shapes): 256x256 tiles for tall grids that nearly fill
+// the CUs; 128x128 (two workgroups per CU) for wide grids with few row
+// panels; 256x128 once that gives half a wave of workgroups; long-K shapes
+// with fewer tiles split K in two; 64x64 when that alone fills the CUs twice;
+// smaller grids split K on 64x64 tiles until ~256 workgroups are resident.
 void choose(uint32_t M, uint32_t N, uint32_t K, uint32_t batch, int& cfg, uint32_t& splits) {
     const char* env = std::getenv("MI_GEMM_CFG");  // "<cfg>[:<splits>]" overrides (tuning sweeps)
     if (env && *env) {
@@ -525,17 +637,22 @@ void choose(uint32_t M, uint32_t N, uint32_t K, uint32_t batch, int& cfg, uint32
         if (splits < 1) splits = 1;
         return;
     }
-    const uint64_t t256 = static_cast<uint64_t>(ceil_div(M, 256)) * ceil_div(N, 128) * batch;
-    const uint64_t t64 = static_cast<uint64_t>(ceil_div(M, 64)) * ceil_div(N, 64) * batch;
-    const uint64_t tsq = static_cast<uint64_t>(ceil_div(M, 256)) * ceil_div(N, 256) * batch;
+    auto tiles = [&](uint32_t bm, uint32_t bn) {
+        return static_cast<uint64_t>(ceil_div(M, bm)) * ceil_div(N, bn) * batch;
+    };
+    const uint64_t tsq = tiles(256, 256), t128 = tiles(128, 128), t256 = tiles(256, 128), t64 = tiles(64, 64);
     splits = 1;
-    if (tsq >= 160 && K <= 2048) {
+    if (tsq >= 160 && M >= 4096 && K <= 2048) {
         cfg = kC256x256;
+    } else if (t128 >= 4 * kCUs && K <= 2048) {
+        cfg = kC128x128;
     } else if (t256 >= kCUs / 2) {
         cfg = kC256x128;
     } else if (K >= 4096 && t256 * 2 >= kCUs / 2) {
         cfg = kC256x128;
         splits = 2;
+    } else if (t64 >= 2 * kCUs) {
+        cfg = kC64x64;
     } else {
         cfg = kC64x64;
         const uint64_t want = (kCUs + t64 - 1) / t64;

@@ -96,11 +96,13 @@ def test_split_general_k(gpu, oracle, K):
     assert_parity(dC.download(np.float32, M * N).reshape(M, N), want, what=f"split K={K}")
 
 
-def test_batch_and_strides(gpu, oracle):
-    """Grid z offsets A and C, never W (gemm_nt_q8_v.comp:51-52,87); lda/ldc padding untouched."""
-    M, N, K, batch = 300, 200, 96, 3
-    lda, ldc = K + 4, N + 8
-    sA, sC = M * lda + 16, M * ldc + 8
+@pytest.mark.parametrize("ldc_pad,sc_pad,K", [(8, 8, 96), (3, 5, 96), (8, 8, 128), (1, 0, 256)])
+def test_batch_and_strides(gpu, oracle, ldc_pad, sc_pad, K):
+    """Grid z offsets A and C, never W (gemm_nt_q8_v.comp:51-52,87); lda/ldc padding untouched.
+    Odd ldc / sC take the scalar epilogue, multiples of 4 the 16-byte one."""
+    M, N, batch = 300, 200, 3
+    lda, ldc = K + 4, N + ldc_pad
+    sA, sC = M * lda + 16, M * ldc + sc_pad
     A = oracle.normal(1, (batch - 1) * sA + M * lda)
     blocks = q8_weights(oracle, 2, N, K)
     C0 = oracle.normal(3, (batch - 1) * sC + M * ldc)
