@@ -128,6 +128,21 @@ __device__ __forceinline__ uint32_t tile_bytes(uint32_t kv0, uint32_t L, uint64_
     return static_cast<uint32_t>(((rows - 1) * ld + hd) * esz);
 }
 
+// 16 bytes per lane from a buffer into LDS (lane l's bytes land at lds + 16 l).
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, 0, 0, 0);
+}
+
+// Transposing LDS read: within each 16-lane group, lane i returns element i % 4
+// of the 8-byte pieces addressed by lanes i/4, i/4 + 4, i/4 + 8, i/4 + 12.
+__device__ __forceinline__ half4 lds_read_tr16(const _Float16* p) {
+    typedef __fp16 fp16x4 __attribute__((ext_vector_type(4)));
+    return __builtin_bit_cast(
+        half4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) fp16x4*)(const_cast<_Float16*>(p))));
+}
+
+__device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // Lazy rescaling threshold (exp2 domain): the running max is only raised when
 // a tile's max exceeds it by more than this, so P = exp2(s - m) <= 2^8 stays
 // far inside fp16 range while the O / l rescale runs on few tiles.
@@ -404,20 +419,28 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
 //
 // Same math as attn_kernel, arranged so that matrix and vector work overlap
 // inside each wave (a wave issues in order, so an MFMA only hides VALU work
-// placed between MFMAs): iteration j issues the S MFMAs of tile j+1 between
-// the exp2 / fp16 packing of tile j, then the PV MFMAs of tile j between the
-// scale / max of tile j+1. Every LDS fragment of an iteration is read up
-// front. K runs one tile ahead of V in LDS (K tiles j+1, j+2; V tiles j,
+// placed between MFMAs; waves sharing a SIMD do not overlap them): iteration
+// j issues the S MFMAs of tile j+1 between the exp2 / fp16 packing of tile j,
+// then the PV MFMAs of tile j between the scale / max of tile j+1. Every LDS
+// fragment of an iteration is read up front.
+//
+// K and V tiles travel from memory straight into LDS (buffer loads with the
+// LDS-DMA bit: no registers, no conversion, no LDS store instructions), as
+// row-major [64 keys][64 d] fp16 with the eight 16-byte chunks of key row k
+// stored at slot chunk ^ f(k) (a bank-conflict-free XOR swizzle for the
+// fragment reads below). K fragments are plain 16-byte reads; V fragments come
+// from ds_read_b64_tr_b16, whose 16-lane transpose turns four 8-byte row
+// pieces into four consecutive keys at one d per lane -- exactly the key order
+// of P in registers. K runs one tile ahead of V (K tiles j+1, j+2; V tiles j,
 // j+1), so one barrier per tile keeps both double buffers race-free. The
 // workgroup has NW waves of 32 queries; blocks are mapped so that the
 // workgroups of one (batch, head) share an XCD (and its L2).
 template <typename TO, int NW>
 __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t qtiles) {
-    constexpr int NT = 64 * NW, BQ = 32 * NW;
-    constexpr int KCH = 512 / NT;  // 16-byte K chunks per thread per tile
-    constexpr int VBL = 256 / NT;  // 4-key x 4-d V blocks per thread per tile
-    __shared__ _Float16 Ks[2][kBKV * kKld];
-    __shared__ _Float16 Vs[2][8 * kVG * 8];
+    constexpr int BQ = 32 * NW;
+    constexpr int DMA_IT = 8 / NW;  // 1 KB (8-row) DMA pieces per wave per tile, for K and for V
+    __shared__ __attribute__((aligned(16))) _Float16 Ks[2][kBKV * 64];
+    __shared__ __attribute__((aligned(16))) _Float16 Vs[2][kBKV * 64];
 
     const unsigned blk = xcd_swizzle(blockIdx.x, gridDim.x);
     const uint32_t qt = blk % qtiles, bh = blk / qtiles;
@@ -451,80 +474,71 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
                                      : zero8();
     }
 
-    // Staging offsets (bytes from the tile's first row). K: chunk c = tid + i NT
-    // is key c / 8, d 8 (c % 8). V: block c = tid + i NT is keys 4 (c % 16) .. +3,
-    // d 4 (c / 16) .. +3. Chunks at d >= hd read zeros.
-    uint32_t k_off[KCH], v_off[VBL];
+    // Chunk slots: K row k keeps chunk c at slot c ^ ((k / 2) % 8), V row k at
+    // c ^ 4 ((k / 2) % 2) (conflict-free for the K reads and the transposing V
+    // reads). DMA piece p of a tile is key rows 8p .. 8p+7; lane l of the wave
+    // writes slot l % 8 of row 8p + l / 8, so it fetches that slot's chunk.
+    // Chunks at d >= hd and rows at or past L read as zeros.
+    uint32_t k_dma[DMA_IT], v_dma[DMA_IT];
 #pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-        const int c = tid + i * NT;
-        k_off[i] = (c & 7) * 8 < hd ? ((c >> 3) * static_cast<uint32_t>(a.ldk) + (c & 7) * 8) * 2u : kOob;
+    for (int ii = 0; ii < DMA_IT; ++ii) {
+        const uint32_t row = 8 * (wave * DMA_IT + ii) + (lane >> 3), slot = lane & 7;
+        const uint32_t ck = slot ^ ((row >> 1) & 7), cv = slot ^ (((row >> 1) & 1) << 2);
+        k_dma[ii] = static_cast<int>(ck * 8) < hd ? (row * static_cast<uint32_t>(a.ldk) + ck * 8) * 2u : kOob;
+        v_dma[ii] = static_cast<int>(cv * 8) < hd ? (row * static_cast<uint32_t>(a.ldv) + cv * 8) * 2u : kOob;
     }
-#pragma unroll
-    for (int i = 0; i < VBL; ++i) {
-        const int c = tid + i * NT;
-        v_off[i] = (c >> 4) * 4 < hd ? ((c & 15) * 4 * static_cast<uint32_t>(a.ldv) + (c >> 4) * 4) * 2u : kOob;
-    }
-    const uint32_t v_row = static_cast<uint32_t>(a.ldv) * 2u;
-    half8 kreg[KCH];
-    half4 vreg[VBL][4];
-    auto load_k = [&](uint32_t kv0) {
+    auto dma_k = [&](uint32_t kv0, int st) {
         const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<_Float16*>(Kp + static_cast<uint64_t>(kv0) * a.ldk), 0,
             static_cast<int>(tile_bytes(kv0, L, a.ldk, a.hd, 2)), 0x00020000);
 #pragma unroll
-        for (int i = 0; i < KCH; ++i)
-            kreg[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(r, k_off[i], 0, 0));
+        for (int ii = 0; ii < DMA_IT; ++ii)
+            lds_dma16(r, &Ks[st][(wave * DMA_IT + ii) * 512], k_dma[ii]);
     };
-    auto load_v = [&](uint32_t kv0) {
+    auto dma_v = [&](uint32_t kv0, int st) {
         const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<_Float16*>(Vp + static_cast<uint64_t>(kv0) * a.ldv), 0,
             static_cast<int>(tile_bytes(kv0, L, a.ldv, a.hd, 2)), 0x00020000);
 #pragma unroll
-        for (int i = 0; i < VBL; ++i)
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                vreg[i][e] = __builtin_bit_cast(half4, __builtin_amdgcn_raw_buffer_load_b64(r, v_off[i] + e * v_row, 0, 0));
+        for (int ii = 0; ii < DMA_IT; ++ii)
+            lds_dma16(r, &Vs[st][(wave * DMA_IT + ii) * 512], v_dma[ii]);
     };
-    auto store_k = [&](int st) {
-#pragma unroll
-        for (int i = 0; i < KCH; ++i) {
-            const int c = tid + i * NT;
-            *reinterpret_cast<half8*>(&Ks[st][(c >> 3) * kKld + (c & 7) * 8]) = kreg[i];
-        }
-    };
-    // V as [G][d][8]: key 32t + 16sp + 8j + 4g' + i sits in group G = 4t + 2sp + g',
-    // slot 4j + i (the PV step (t, sp) and lane half g' that consume it).
-    auto store_v = [&](int st) {
-#pragma unroll
-        for (int i = 0; i < VBL; ++i) {
-            const int c = tid + i * NT;
-            const int vkg = c & 15, vd0 = (c >> 4) * 4;
-            const int vG = (vkg >> 3) * 4 + ((vkg >> 2) & 1) * 2 + (vkg & 1);
-            const int vslot = ((vkg >> 1) & 1) * 4;
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                *reinterpret_cast<half4*>(&Vs[st][(vG * kVG + vd0 + e) * 8 + vslot]) =
-                    half4{vreg[i][0][e], vreg[i][1][e], vreg[i][2][e], vreg[i][3][e]};
-        }
-    };
+    // The DMA writes land asynchronously: wait for this wave's before the
+    // barrier that hands the tile to the other waves.
+    auto dma_wait = [] { wait_vmcnt0(); };
 
     half8 kf[2][4], vf[2][2][2];
     auto read_k = [&](int st) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < 2; ++t) {
+            const int row = 32 * t + l32;
 #pragma unroll
             for (int s = 0; s < 4; ++s)
-                kf[t][s] = *reinterpret_cast<const half8*>(&Ks[st][(32 * t + l32) * kKld + 16 * s + 8 * g]);
+                kf[t][s] = *reinterpret_cast<const half8*>(&Ks[st][row * 64 + (((2 * s + g) ^ ((row >> 1) & 7)) * 8)]);
+        }
     };
+    // V^T fragment (PV step t, sp; d block u): lane l = 16G + i needs d = 32u +
+    // l%32 and keys 32t + 16sp + 8rd + 4(l/32) + 0..3 for rd = 0, 1. Lane i of
+    // the 16-lane group supplies the 8-byte piece of key (base + i/4) at d =
+    // 32u + 16(G%2) + 4(i%4); the transpose hands it keys base..base+3 at d.
+    const int v_key = lane >> 2 & 3, v_d = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
     auto read_v = [&](int st) {
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int sp = 0; sp < 2; ++sp)
 #pragma unroll
-                for (int u = 0; u < 2; ++u)
-                    vf[t][sp][u] = *reinterpret_cast<const half8*>(&Vs[st][((t * 4 + sp * 2 + g) * kVG + 32 * u + l32) * 8]);
+                for (int u = 0; u < 2; ++u) {
+                    half4 hv[2];
+#pragma unroll
+                    for (int rd = 0; rd < 2; ++rd) {
+                        const int key = 32 * t + 16 * sp + 8 * rd + 4 * g + v_key;
+                        const int d = 32 * u + v_d;
+                        const int off = key * 64 + (((d >> 3) ^ (((key >> 1) & 1) << 2)) * 8) + (d & 7);
+                        hv[rd] = lds_read_tr16(&Vs[st][off]);
+                    }
+                    vf[t][sp][u] = half8{hv[0][0], hv[0][1], hv[0][2], hv[0][3], hv[1][0], hv[1][1], hv[1][2], hv[1][3]};
+                }
     };
     // S^T = K Q^T: rows (keys) kv0 + 32t + 8(r/4) + 4g + r%4, column = query qi
     auto qk = [&](floatx16 (&sc)[2]) {
@@ -588,14 +602,10 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
         // prologue: K tiles 0, 1 and V tile 0 in LDS; S of tile 0; the running
         // max starts at tile 0's max (every query has a valid key in tile 0:
         // key 0 < L, and key 0 <= qi under the causal mask)
-        load_k(0);
-        load_v(0);
-        store_k(0);
-        store_v(0);
-        if (ntiles > 1) {
-            load_k(kBKV);
-            store_k(1);
-        }
+        dma_k(0, 0);
+        dma_v(0, 0);
+        if (ntiles > 1) dma_k(kBKV, 1);
+        dma_wait();
         __syncthreads();
         read_k(0);
         floatx16 s0[2];
@@ -616,10 +626,12 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
             constexpr bool kMasked = decltype(masked)::value;
             const uint32_t kv1 = (j + 1) * kBKV;
             const bool more = j + 2 < ntiles;
-            if (more) load_k(kv1 + kBKV);
-            load_v(kv1);
             read_k((j + 1) & 1);
             read_v(j & 1);
+            __builtin_amdgcn_sched_barrier(0);
+            // into the stages read in the previous iteration (free after its barrier)
+            if (more) dma_k(kv1 + kBKV, j & 1);
+            dma_v(kv1, (j + 1) & 1);
             __builtin_amdgcn_sched_barrier(0);
 
             // phase A: S of tile j+1 (8 MFMA) || exp2 + fp16 pack of tile j
@@ -663,8 +675,7 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
             }
 #pragma unroll
             for (int t = 0; t < 2; ++t) s0[t] = s1[t];
-            if (more) store_k(j & 1);
-            store_v((j + 1) & 1);
+            dma_wait();
             __syncthreads();
         };
         for (uint32_t j = 0; j + 1 < ntiles; ++j) {
