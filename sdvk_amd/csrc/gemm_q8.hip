@@ -120,6 +120,89 @@ __device__ __forceinline__ void interleave_step() {
     }
 }
 
+// ---- epilogue ---------------------------------------------------------------------
+//
+// Non-split: a wave's FM x FN accumulator tiles (32 x 32 each, transposed
+// product: a lane holds row l32 and columns 8 q + 4 g + e) go to C one tile at
+// a time through a wave-private 32 x kStageLd float region of LDS, read back
+// as (row, 4 columns) units, so eight lanes write one 128-byte row segment per
+// instruction. One runtime loop serves every tile, which keeps the epilogue a
+// few hundred instructions (an unrolled per-tile epilogue with bias / mode /
+// edge branches is tens of KB of code that every workgroup runs once, cold in
+// the instruction cache).
+// Split K: the plain product (a lane holds column l32 and rows
+// 8 (r / 4) + 4 g + r % 4) is added with fp32 atomics straight from the
+// registers, 32 consecutive floats per instruction; bias came from the fill
+// kernel.
+constexpr int kStageLd = 36;                       // floats per staged row (16-byte pad)
+constexpr int kStageFloats = 32 * kStageLd;        // per wave
+
+template <int FM, int FN, bool SPLITK>
+__device__ __forceinline__ void store_tiles(const GemmArgs& a, float* C, float* stage, uint32_t mw, uint32_t nw,
+                                            const floatx16 (&acc)[FM][FN], int lane) {
+    const int l32 = lane & 31, g = lane >> 5;
+    const bool vec = a.cvec != 0;
+    const bool use_bias = !SPLITK && a.mode == 0 && a.bias != nullptr;
+    const bool vec_bias = !use_bias || a.bvec != 0;
+    if constexpr (SPLITK) {
+        // no staging: one atomic instruction covers 32 consecutive floats of a row
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+            const uint32_t n = nw + 32 * fn + l32;
+            if (n >= a.N) continue;
+#pragma unroll
+            for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t m = mw + 32 * fm + 8 * (r >> 2) + 4 * g + (r & 3);
+                    if (m < a.M) unsafeAtomicAdd(C + static_cast<uint64_t>(m) * a.ldc + n, acc[fm][fn][r]);  // native global_atomic_add_f32
+                }
+        }
+        return;
+    }
+    for (int b = 0; b < FM * FN; ++b) {
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+            for (int fn = 0; fn < FN; ++fn)
+                if (b == fm * FN + fn) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        *reinterpret_cast<floatx4*>(&stage[l32 * kStageLd + 8 * q + 4 * g]) =
+                            floatx4{acc[fm][fn][4 * q], acc[fm][fn][4 * q + 1], acc[fm][fn][4 * q + 2],
+                                    acc[fm][fn][4 * q + 3]};
+                }
+        const uint32_t mb = mw + 32 * (b / FN), nb = nw + 32 * (b % FN);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int u = lane + 64 * i;
+            const int row = u >> 3, col = (u & 7) * 4;
+            const floatx4 v = *reinterpret_cast<const floatx4*>(&stage[row * kStageLd + col]);
+            const uint32_t m = mb + row, n = nb + col;
+            if (m >= a.M) continue;
+            float* c = C + static_cast<uint64_t>(m) * a.ldc + n;
+            if (vec && vec_bias && n + 3 < a.N) {
+                if (a.mode == 0) {
+                    floatx4 o = v;
+                    if (use_bias) o += *reinterpret_cast<const floatx4*>(a.bias + n);
+                    // C is written once and not re-read here: streaming stores keep
+                    // it from displacing the operand working set in L2
+                    __builtin_nontemporal_store(o, reinterpret_cast<floatx4*>(c));
+                } else {
+                    *reinterpret_cast<floatx4*>(c) = *reinterpret_cast<const floatx4*>(c) + v;
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (n + e >= a.N) continue;
+                    if (a.mode == 0) c[e] = v[e] + (use_bias ? a.bias[n + e] : 0.0f);
+                    else c[e] += v[e];
+                }
+            }
+        }
+    }
+}
+
 template <int BM, int BN, int WM, int WN, int KB, int WK, bool SPLITK, bool KTAIL, int PF>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     constexpr int NT = WM * WN * 64;
@@ -143,8 +226,11 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     static_assert(A_UNITS % NT == 0 && W_UNITS % NT == 0, "staging must divide evenly");
     static_assert(FM >= 1 && FN >= 1, "wave tile below 32x32");
 
-    __shared__ _Float16 As[2][BM * LDK];
-    __shared__ _Float16 Ws[2][BN * LDK];
+    constexpr int kOperandHalves = 2 * (BM + BN) * LDK;
+    constexpr int kStageHalves = 2 * NT / 64 * kStageFloats;
+    __shared__ __attribute__((aligned(16))) _Float16 smem[kOperandHalves > kStageHalves ? kOperandHalves : kStageHalves];
+    auto As = reinterpret_cast<_Float16 (*)[BM * LDK]>(smem);
+    auto Ws = reinterpret_cast<_Float16 (*)[BN * LDK]>(smem + 2 * BM * LDK);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -166,7 +252,10 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     // Per-thread byte offsets, fixed for the whole K loop. Rows past M / N read
     // the last valid row: they only feed outputs that are never stored.
     const float* Apanel = a.A + static_cast<uint64_t>(blockIdx.z) * a.sA + static_cast<uint64_t>(m0) * a.lda;
-    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Apanel), 0, -1, 0x00020000);
+    // the range covers exactly the panel's rows: a read past them returns zeros, never faults
+    const uint32_t a_bytes = ((min(a.M - m0, static_cast<uint32_t>(BM)) - 1) * a.lda + a.K) * 4;
+    const __amdgpu_buffer_rsrc_t rA =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Apanel), 0, static_cast<int>(a_bytes), 0x00020000);
     // 34-byte layout: records up to W's 16-byte-aligned end (the documented
     // read extent); the range check zeroes whole dwords only past that.
     const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc(
@@ -441,71 +530,280 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     }
     if (j < n_steps) compute(S0{});
 
-    // Epilogue. Stores: lane holds row m = l32 of each 32x32 tile and columns
-    // 8 q + 4 g + e (run q = 0..3, e = 0..3): one 16-byte store per run when C
-    // rows are 16-byte aligned.
     float* C = a.C + static_cast<uint64_t>(blockIdx.z) * a.sC;
-    if constexpr (SPLITK) {
-        // lane holds column l32 and rows 8(r/4) + 4g + r%4 of each 32x32 tile
+    __syncthreads();  // every wave is done with the operand tiles before LDS is reused
+    store_tiles<FM, FN, SPLITK>(a, C, reinterpret_cast<float*>(smem) + wave * kStageFloats, m0 + wm * TM,
+                                n0 + wn * TN, acc, lane);
+}
+
+// ---- row-stationary kernel --------------------------------------------------------
+//
+// One workgroup = 4 waves, one per SIMD, stacked in M: wave w owns rows
+// [64w, 64w + 64) of a 256 x BN tile (BN = 32 * FN) and keeps its 2 x FN
+// 32x32 fp32 accumulators (256 registers at FN = 8) for the whole K sweep.
+//
+//   * A never touches LDS. A lane loads the fp32 values of its own MFMA
+//     operand straight into registers and rounds them to fp16 there. K is
+//     permuted inside each 32-wide step (operand slot (slice s, half g) holds
+//     k = 16 g + 8 s .. + 8, applied to both operands), so a lane's 16 values
+//     of a step are contiguous: four 16-byte loads per 32 rows, and the two
+//     halves of a wave cover one 128-byte line per row.
+//   * W is read once per workgroup: thread t < BN dequantises column t's
+//     Q8_0 block of the step (a 36-byte window, three loads) into LDS, where
+//     the four waves read their operand fragments.
+//   * Steps alternate between two register sets and two LDS stages by the
+//     parity of the step, so the raw loads of step j + 2 are in flight while
+//     step j's MFMAs run and step j + 1 is dequantised / converted; one
+//     barrier per step.
+template <int FN, int WK, bool SPLITK>
+__global__ __launch_bounds__(256) void gemm_q8_rows_kernel(GemmArgs a) {
+    constexpr int BM = 256, BN = 32 * FN, FM = 2, LDW = 40;  // LDW: 32 halves + 16-byte pad per column
+    constexpr int kOperandHalves = 2 * BN * LDW;
+    constexpr int kStageHalves = 2 * 4 * kStageFloats;
+    __shared__ __attribute__((aligned(16))) _Float16 smem[kOperandHalves > kStageHalves ? kOperandHalves : kStageHalves];
+    auto Ws = reinterpret_cast<_Float16 (*)[BN * LDW]>(smem);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, g = lane >> 5;
+
+    const unsigned lin = xcd_swizzle(blockIdx.x, gridDim.x);
+    const uint32_t gsz = a.group_m * a.tiles_n;
+    const uint32_t grp = lin / gsz, rem = lin % gsz;
+    const uint32_t rows_in = min(a.group_m, a.tiles_m - grp * a.group_m);
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((grp * a.group_m + rem % rows_in) * BM);
+    const uint32_t n0 = __builtin_amdgcn_readfirstlane((rem / rows_in) * BN);
+    // split K: steps_per_split is even, so a split starts on an even step and
+    // step parity = register set = LDS stage
+    const uint32_t s_begin = SPLITK ? blockIdx.y * a.steps_per_split : 0;
+    const uint32_t s_end = SPLITK ? min(a.ksteps, s_begin + a.steps_per_split) : a.ksteps;
+
+    const float* Apanel = a.A + static_cast<uint64_t>(blockIdx.z) * a.sA + static_cast<uint64_t>(m0) * a.lda;
+    // the range covers exactly the panel's rows: a read past them returns zeros, never faults
+    const uint32_t a_bytes = ((min(a.M - m0, static_cast<uint32_t>(BM)) - 1) * a.lda + a.K) * 4;
+    const __amdgpu_buffer_rsrc_t rA =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Apanel), 0, static_cast<int>(a_bytes), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(a.W), 0, WK == kBlocks34 ? static_cast<int>((a.N * a.rowbytes + 15u) & ~15u) : -1,
+        0x00020000);
+    const __amdgpu_buffer_rsrc_t rS =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(WK == kSplit ? a.scales : a.A), 0, -1, 0x00020000);
+
+    // A: rows past M read row M - 1 (their outputs are never stored)
+    uint32_t a_off[FM];
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            const uint32_t n = n0 + wn * TN + 32 * j + l32;
-            if (n >= a.N) continue;
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const uint32_t m = m0 + wm * TM + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
-                    if (m < a.M) unsafeAtomicAdd(C + static_cast<uint64_t>(m) * a.ldc + n, acc[i][j][r]);  // native global_atomic_add_f32
-                }
-        }
-        return;
+    for (int fm = 0; fm < FM; ++fm) {
+        const uint32_t row = min(m0 + 64 * wave + 32 * fm + l32, a.M - 1) - m0;
+        a_off[fm] = (row * a.lda + 16 * g) * 4;
     }
-    const bool cvec = a.cvec != 0;
-    const bool use_bias = a.mode == 0 && a.bias;
+    // W: column t = tid (tid < BN). 34-byte layout: the block of step ks
+    // starts at byte wb + 34 ks; even steps read the window at
+    // (wb & ~3) + 68 (ks / 2), odd steps at ((wb + 34) & ~3) + 68 (ks / 2), and
+    // the block sits 0 or 2 bytes into its window (v_perm selectors per parity).
+    const bool wlane = BN == 256 || tid < BN;
+    const uint32_t wn = min(n0 + static_cast<uint32_t>(tid % BN), a.N - 1);
+    uint32_t w_vo[2], w_qsel[2], w_dsel[2];
+    if constexpr (WK == kBlocks34) {
+        const uint32_t wb = wn * a.rowbytes;
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
+        for (int p = 0; p < 2; ++p) {
+            const uint32_t byte = wb + 34u * p;
+            w_vo[p] = byte & ~3u;
+            w_qsel[p] = (byte & 2u) ? 0x07060504u : 0x05040302u;
+            w_dsel[p] = (byte & 2u) ? 0x0c0c0302u : 0x0c0c0100u;
+        }
+    } else {
+        // split layout: payload byte wn*K + 32 ks, scale float (wn*K)/32 + ks
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint32_t n = n0 + wn * TN + 32 * j + 8 * q + 4 * g;
-            float b[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (use_bias) {
-                if (a.bvec && n + 3 < a.N) {
-                    const floatx4 b4 = *reinterpret_cast<const floatx4*>(a.bias + n);
+        for (int p = 0; p < 2; ++p) {
+            w_vo[p] = wn * a.K + 32u * p;
+            w_qsel[p] = (wn * a.K / 32u + p) * 4u;
+            w_dsel[p] = 0;
+        }
+    }
+
+    floatx4 ar[2][FM][4];   // raw A of a step, per parity
+    uint32_t wx[2][9];      // raw W of a step, per parity
+
+    auto load = [&](uint32_t ks_in, auto P) {
+        constexpr int p = decltype(P)::value;
+        const uint32_t ks = __builtin_amdgcn_readfirstlane(ks_in);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) b[e] = b4[e];
-                } else {
+        for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) b[e] = n + e < a.N ? a.bias[n + e] : 0.0f;
+            for (int q = 0; q < 4; ++q)
+                ar[p][fm][q] = __builtin_bit_cast(
+                    floatx4, __builtin_amdgcn_raw_buffer_load_b128(rA, a_off[fm] + 16 * q, ks * 128, 0));
+        if (wlane) {
+            if constexpr (WK == kBlocks34) {
+                const uint32_t so = 68u * (ks >> 1);
+                const auto x0 = __builtin_amdgcn_raw_buffer_load_b128(rW, w_vo[p], so, 0);
+                const auto x1 = __builtin_amdgcn_raw_buffer_load_b128(rW, w_vo[p] + 16, so, 0);
+                wx[p][8] = __builtin_amdgcn_raw_buffer_load_b32(rW, w_vo[p] + 32, so, 0);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    wx[p][e] = x0[e];
+                    wx[p][4 + e] = x1[e];
+                }
+            } else {
+                const uint32_t so = 64u * (ks >> 1);
+                const auto x0 = __builtin_amdgcn_raw_buffer_load_b128(rW, w_vo[p], so, 0);
+                const auto x1 = __builtin_amdgcn_raw_buffer_load_b128(rW, w_vo[p] + 16, so, 0);
+                wx[p][8] = __builtin_amdgcn_raw_buffer_load_b32(rS, w_qsel[p], 8u * (ks >> 1), 0);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    wx[p][e] = x0[e];
+                    wx[p][4 + e] = x1[e];
                 }
             }
-#pragma unroll
-            for (int i = 0; i < FM; ++i) {
-                const uint32_t m = m0 + wm * TM + 32 * i + l32;
-                if (m >= a.M) continue;
-                float* crow = C + static_cast<uint64_t>(m) * a.ldc;
-                float v[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-                if (cvec && n + 3 < a.N) {
-                    floatx4* c4 = reinterpret_cast<floatx4*>(crow + n);
-                    if (a.mode == 0) {
-                        // C is written once and not re-read here: streaming stores keep
-                        // it from displacing the A / W working set in L2.
-                        __builtin_nontemporal_store(floatx4{v[0] + b[0], v[1] + b[1], v[2] + b[2], v[3] + b[3]}, c4);
-                    } else {
-                        const floatx4 o = *c4;
-                        *c4 = floatx4{o[0] + v[0], o[1] + v[1], o[2] + v[2], o[3] + v[3]};
-                    }
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        if (n + e >= a.N) continue;
-                        if (a.mode == 0) crow[n + e] = v[e] + b[e];
-                        else crow[n + e] += v[e];
-                    }
-                }
-            }
         }
+    };
+    // dequantise the W block of set p into LDS stage p
+    auto store_w = [&](auto P) {
+        constexpr int p = decltype(P)::value;
+        if (!wlane) return;
+        _Float16* dst = &Ws[p][(tid % BN) * LDW];
+        if constexpr (WK == kBlocks34) {
+            const uint32_t* x = wx[p];
+            const _Float16 d = __builtin_bit_cast(
+                _Float16, static_cast<uint16_t>(__builtin_amdgcn_perm(x[0], x[0], w_dsel[p])));
+            uint32_t q[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) q[j] = __builtin_amdgcn_perm(x[j + 1], x[j], w_qsel[p]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) *reinterpret_cast<half8*>(dst + 8 * j) = dequant8_f16(q[2 * j], q[2 * j + 1], d);
+        } else {
+            const float s = __builtin_bit_cast(float, wx[p][8]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                *reinterpret_cast<half8*>(dst + 8 * j) = dequant8_f32(wx[p][2 * j], wx[p][2 * j + 1], s, s);
+        }
+    };
+    half8 af[2][FM][2];     // fp16 A operands of a step, per parity: [fm][slice]
+    auto cvt_a = [&](auto P) {
+        constexpr int p = decltype(P)::value;
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                const floatx4 lo = ar[p][fm][2 * s], hi = ar[p][fm][2 * s + 1];
+                af[p][fm][s] = half8{static_cast<_Float16>(lo[0]), static_cast<_Float16>(lo[1]),
+                                     static_cast<_Float16>(lo[2]), static_cast<_Float16>(lo[3]),
+                                     static_cast<_Float16>(hi[0]), static_cast<_Float16>(hi[1]),
+                                     static_cast<_Float16>(hi[2]), static_cast<_Float16>(hi[3])};
+                // materialise the operand here: the raw registers must be free
+                // before the loads that refill them are issued
+                asm volatile("" : "+v"(af[p][fm][s]));
+            }
+    };
+
+    floatx16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+
+    auto mfma1 = [&](auto P, int s, int fn, const half8& w) {
+        constexpr int p = decltype(P)::value;
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+            if constexpr (SPLITK)
+                acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[p][fm][s], w, acc[fm][fn], 0, 0, 0);
+            else
+                acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w, af[p][fm][s], acc[fm][fn], 0, 0, 0);
+    };
+    auto read1 = [&](auto P, int s, int fn) {
+        constexpr int p = decltype(P)::value;
+        return *reinterpret_cast<const half8*>(&Ws[p][(32 * fn + l32) * LDW + 16 * g + 8 * s]);
+    };
+
+    // W fragments in flight: one slice (FN x 16 bytes per lane). A step with
+    // operand set P (LDS stage P, A operands af[P]) enters with slice 0 of
+    // stage P in wf and runs three scheduling regions:
+    //   A: slice 0's MFMAs; each column fragment is re-read for slice 1 once
+    //      its MFMAs are issued; meanwhile the other set Q (step + 1) is
+    //      dequantised into stage Q and its A values converted;
+    //   B: set Q's loads for step + 3 (behind a fence: never hoisted above the
+    //      last use of the registers they refill) and slice 1's MFMAs but the
+    //      last two columns;
+    //   barrier (stage Q complete, stage P no longer read), then C: the last
+    //      two columns' MFMAs overlap the reads of slice 0 of stage Q.
+    constexpr int kTail = FN >= 4 ? 2 : 1;
+    constexpr int kValu = 8 * FM + (WK == kBlocks34 ? 60 : 40);
+    constexpr int kVmem = 4 * FM + 3;
+    half8 wf[FN];
+    auto step = [&](auto P, auto Q, uint32_t ks_next3) {
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+            mfma1(P, 0, fn, wf[fn]);
+            wf[fn] = read1(P, 1, fn);
+        }
+        store_w(Q);
+        cvt_a(Q);
+#pragma unroll
+        for (int i = 0; i < FN; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, FM, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, (kValu + FN - 1) / FN, 0);
+            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        load(ks_next3, Q);
+#pragma unroll
+        for (int fn = 0; fn < FN - kTail; ++fn) mfma1(P, 1, fn, wf[fn]);
+#pragma unroll
+        for (int i = 0; i < FN - kTail; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, FM, 0);
+            __builtin_amdgcn_sched_group_barrier(0x020, (kVmem + FN - kTail - 1) / (FN - kTail), 0);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int fn = 0; fn < FN - kTail; ++fn) wf[fn] = read1(Q, 0, fn);
+#pragma unroll
+        for (int fn = FN - kTail; fn < FN; ++fn) {
+            mfma1(P, 1, fn, wf[fn]);
+            wf[fn] = read1(Q, 0, fn);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    const uint32_t n_steps = s_end - s_begin;
+    const uint32_t last = s_end - 1;
+    if (n_steps > 0) {
+        load(s_begin, P0{});
+        load(min(s_begin + 1, last), P1{});
+        store_w(P0{});
+        cvt_a(P0{});
+        load(min(s_begin + 2, last), P0{});
     }
+    __syncthreads();
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) wf[fn] = read1(P0{}, 0, fn);
+    uint32_t j = 0;
+    for (; j + 2 <= n_steps; j += 2) {
+        const uint32_t ks = s_begin + j;
+        step(P0{}, P1{}, min(ks + 3, last));
+        step(P1{}, P0{}, min(ks + 4, last));
+    }
+    if (j < n_steps) {
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+            mfma1(P0{}, 0, fn, wf[fn]);
+            wf[fn] = read1(P0{}, 1, fn);
+        }
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) mfma1(P0{}, 1, fn, wf[fn]);
+    }
+
+    float* C = a.C + static_cast<uint64_t>(blockIdx.z) * a.sC;
+    __syncthreads();  // every wave is done with the W tiles before LDS is reused
+    store_tiles<FM, FN, SPLITK>(a, C, reinterpret_cast<float*>(smem) + wave * kStageFloats, m0 + 64 * wave, n0, acc,
+                                lane);
 }
 
 // C[m, n] = bias[n] (or 0) for the split-K accumulation (mode 0 only).
@@ -527,7 +825,7 @@ void launch_init(float* C, const float* bias, uint32_t M, uint32_t N, uint32_t l
 
 // Tile shapes (BM x BN, waves WM x WN, two 32-wide K blocks per step). The
 // 256x256 tile keeps one register set in flight (PF = 1) to stay within 256 VGPRs.
-enum CfgId { kC256x128 = 0, kC128x128, kC128x64, kC64x64, kC256x256, kNumCfg };
+enum CfgId { kC256x128 = 0, kC128x128, kC128x64, kC64x64, kC256x256, kR256x256, kR256x128, kNumCfg };
 
 // Group height for the tile order: the XCD chunks (blocks b with b % 8 == x,
 // contiguous in the grouped order) each read the A panels of the rows and the
@@ -600,9 +898,35 @@ void launch_cfg(const GemmArgs& a0, uint32_t batch, uint32_t splits, hipStream_t
     }
 }
 
+// Row-stationary kernel: 256 x (32 FN) tiles, K % 32 == 0. A K split covers an
+// even number of 32-wide steps.
+template <int FN, int WK>
+void launch_rows(const GemmArgs& a0, uint32_t batch, uint32_t splits, hipStream_t s) {
+    GemmArgs a = a0;
+    constexpr uint32_t BM = 256, BN = 32 * FN;
+    a.tiles_n = ceil_div(a.N, BN);
+    a.tiles_m = ceil_div(a.M, BM);
+    a.group_m = pick_group(a.tiles_m, a.tiles_n, BM, BN, a.K);
+    a.ksteps = a.K / 32;
+    const unsigned tiles = a.tiles_m * a.tiles_n;
+    if (splits > 1) {
+        a.steps_per_split = (ceil_div(a.ksteps, splits) + 1u) & ~1u;
+        splits = ceil_div(a.ksteps, a.steps_per_split);
+    }
+    if (splits > 1) {
+        if (a.mode == 0) launch_init(a.C, a.bias, a.M, a.N, a.ldc, a.sC, batch, s);
+        gemm_q8_rows_kernel<FN, WK, true><<<dim3(tiles, splits, batch), 256, 0, s>>>(a);
+    } else {
+        a.steps_per_split = a.ksteps;
+        gemm_q8_rows_kernel<FN, WK, false><<<dim3(tiles, 1, batch), 256, 0, s>>>(a);
+    }
+}
+
 template <int WK>
 void launch(int cfg, const GemmArgs& a, uint32_t batch, uint32_t splits, hipStream_t s) {
     switch (cfg) {
+        case kR256x256: launch_rows<8, WK>(a, batch, splits, s); break;
+        case kR256x128: launch_rows<4, WK>(a, batch, splits, s); break;
         case kC256x128: launch_cfg<256, 128, 4, 2, 2, WK, false>(a, batch, splits, s); break;
         case kC128x128: launch_cfg<128, 128, 2, 2, 2, WK, false>(a, batch, splits, s); break;
         case kC128x64: launch_cfg<128, 64, 2, 2, 2, WK, false>(a, batch, splits, s); break;

@@ -96,10 +96,13 @@ def test_split_general_k(gpu, oracle, K):
     assert_parity(dC.download(np.float32, M * N).reshape(M, N), want, what=f"split K={K}")
 
 
-@pytest.mark.parametrize("ldc_pad,sc_pad,K", [(8, 8, 96), (3, 5, 96), (8, 8, 128), (1, 0, 256)])
-def test_batch_and_strides(gpu, oracle, ldc_pad, sc_pad, K):
+@pytest.mark.parametrize("ldc_pad,sc_pad,K,cfg", [(8, 8, 96, ""), (3, 5, 96, ""), (8, 8, 128, ""), (1, 0, 256, ""),
+                                                  (8, 8, 128, "5"), (3, 5, 256, "6:2")])
+def test_batch_and_strides(gpu, oracle, monkeypatch, ldc_pad, sc_pad, K, cfg):
     """Grid z offsets A and C, never W (gemm_nt_q8_v.comp:51-52,87); lda/ldc padding untouched.
     Odd ldc / sC take the scalar epilogue, multiples of 4 the 16-byte one."""
+    if cfg:
+        monkeypatch.setenv("MI_GEMM_CFG", cfg)
     M, N, batch = 300, 200, 3
     lda, ldc = K + 4, N + ldc_pad
     sA, sC = M * lda + 16, M * ldc + sc_pad
@@ -138,7 +141,8 @@ def test_baseline_shapes_sampled_rows(gpu, oracle, M, N, K):
     assert e <= REL_RMS_TOL
 
 
-@pytest.mark.parametrize("cfg", ["0", "1", "2", "3", "4", "0:3", "1:2", "2:5", "3:16", "4:2"])
+@pytest.mark.parametrize("cfg", ["0", "1", "2", "3", "4", "5", "6", "0:3", "1:2", "2:5", "3:16", "4:2", "5:2",
+                                 "6:3"])
 @pytest.mark.parametrize("M,N,K", [(300, 200, 640), (1030, 130, 256)])
 def test_every_tile_config_and_split_k(gpu, oracle, monkeypatch, cfg, M, N, K):
     """Forces each tile configuration / K split (MI_GEMM_CFG="<cfg>[:<splits>]")."""
