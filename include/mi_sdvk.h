@@ -25,6 +25,9 @@
  *   fusedAttnSupported / fusedAttention / FusedAttnArgs
  *       src/Modules/GPU/fused_attn.hpp:13-28, fused_attn.cpp:34-61
  *   Q8_0 decode (readFloat / readQ8Into) src/Modules/Model/Gguf.cpp:514-583
+ *   GgufFile (open / tensors / find / meta / readRaw / readFloat / readQ8Into)
+ *       src/Modules/Model/Gguf.hpp:90-140, Gguf.cpp:290-583; weight upload
+ *       loadGgufUnet and ggdims src/Modules/Diffusion/sdvkgen.cpp:151-176,549-611
  */
 #ifndef MI_SDVK_H
 #define MI_SDVK_H
@@ -43,6 +46,8 @@ typedef enum mi_status {
     MI_ERR_ALIGNMENT = 3,    /* pointer or leading-dimension alignment not met */
     MI_ERR_ALIASING = 4,     /* output overlaps an input */
     MI_ERR_HIP = 5,          /* HIP runtime error (launch failure, no device) */
+    MI_ERR_IO = 6,           /* file cannot be opened / mapped, or is not a valid GGUF container */
+    MI_ERR_NOT_FOUND = 7,    /* no tensor / metadata key of that name, tensor index out of range */
 } mi_status;
 
 typedef enum mi_dtype {
@@ -217,6 +222,75 @@ uint64_t mi_block_workspace_bytes(const mi_block_dims* dims);
 int mi_sdxl_block_forward(const mi_block_weights* w, const mi_block_dims* dims, float* x,
                           const float* ctx, const int32_t* ctx_len, void* workspace,
                           uint64_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------- GGUF -- *
+ * Checkpoint access: the container reader and the upload of its tensors into
+ * caller-owned device buffers in the layouts the GEMM entries read.
+ * Replaces ofc::GgufFile (Gguf.hpp:90-140) and the Q8_0 branch of loadGgufUnet
+ * (sdvkgen.cpp:549-611). Differences from the common contract above:
+ *   - mi_gguf_read_* write HOST memory; mi_gguf_upload_* write device memory
+ *     and are stream-ordered like the kernels (the host bytes are consumed
+ *     before the call returns, so the file may be closed afterwards);
+ *   - a handle owns two 8 MiB pinned HOST staging buffers, allocated on its
+ *     first upload and freed by mi_gguf_close (no device memory is allocated);
+ *   - one handle must not be used by two threads at once; separate handles
+ *     are independent.
+ * Parse rules, limits and the readFloat decode follow Gguf.cpp:290-416,489-527
+ * (v2/v3, prefix filter + strip, general.alignment, 1..4 dims, F32 / F16 /
+ * BF16 / Q4_0 / Q8_0 decode, a partial trailing block decodes to zeros).   */
+typedef struct mi_gguf mi_gguf;
+
+typedef struct mi_gguf_tensor_info {
+    const char* name;     /* NUL-terminated, owned by the handle (prefix stripped) */
+    uint32_t type;        /* ggml type id: 0 F32, 1 F16, 2 Q4_0, 8 Q8_0, 30 BF16, ... */
+    uint32_t n_dims;      /* 1..4 */
+    uint64_t dims[4];     /* dims[0] fastest-varying (ggml ne[0]); unused dims = 1 */
+    uint64_t offset;      /* byte offset in the data section */
+    uint64_t nbytes;      /* stored bytes (whole blocks) */
+    uint64_t n_elems;
+    /* logical (rows, cols) of the weight (ggdims, sdvkgen.cpp:151-176):
+     * comfy.gguf.orig_shape.<name> if present, else 1-D (n, 1), 2-D
+     * (dims[1], dims[0]), N-D (dims[N-1], product of the rest) */
+    uint64_t rows, cols;
+} mi_gguf_tensor_info;
+
+typedef struct mi_gguf_meta_info {
+    uint32_t type;        /* GGUF value type: 0 u8 .. 7 bool, 8 string, 9 array, 10 u64, 11 i64, 12 f64 */
+    uint32_t arr_type;    /* element type of an array */
+    uint64_t u;           /* integer scalars (signed ones sign-extended) */
+    double f;             /* f32 / f64 scalars */
+    int32_t b;            /* bool */
+    const char* str;      /* string value (owned by the handle, NUL-terminated) */
+    uint64_t str_len;
+    uint64_t arr_len;     /* array item count */
+} mi_gguf_meta_info;
+
+/* Maps and parses `path`; prefix (or NULL) keeps only tensors named
+ * prefix* and strips it (GgufFile::open, Gguf.cpp:290-416). */
+int mi_gguf_open(const char* path, const char* prefix, mi_gguf** out);
+void mi_gguf_close(mi_gguf* g);
+int mi_gguf_info(const mi_gguf* g, uint32_t* version, uint64_t* n_tensors, uint64_t* data_offset,
+                 uint64_t* file_size);
+int mi_gguf_tensor(const mi_gguf* g, uint64_t index, mi_gguf_tensor_info* info);
+int mi_gguf_find(const mi_gguf* g, const char* name, uint64_t* index);
+int mi_gguf_meta(const mi_gguf* g, const char* key, mi_gguf_meta_info* info);
+/* Items [first, first + count) of an array: integer / bool arrays into u64s,
+ * float arrays into f64s, string arrays into strs (pointers owned by the
+ * handle); the other outputs may be NULL. */
+int mi_gguf_meta_array(const mi_gguf* g, const char* key, uint64_t first, uint64_t count, uint64_t* u64s,
+                       double* f64s, const char** strs);
+/* Host reads: stored bytes (GgufFile::readRaw), fp32 decode (readFloat), and
+ * the split Q8_0 layout int8 payload + fp32 scale per block (readQ8Into). */
+int mi_gguf_read_raw(const mi_gguf* g, uint64_t index, void* dst, uint64_t dst_bytes);
+int mi_gguf_read_f32(const mi_gguf* g, uint64_t index, float* dst, uint64_t n);
+int mi_gguf_read_q8_split(const mi_gguf* g, uint64_t index, int8_t* payload, float* scales);
+/* Device uploads. upload_raw copies the stored bytes (a Q8_0 weight lands as
+ * the 34-byte blocks mi_gemm_nt_q8_0 reads); upload_f32 the readFloat decode;
+ * upload_q8_split the reference's device layout for mi_gemm_nt_q8_split
+ * (sdvkgen.cpp:560-582: payload n bytes, scales n / 32 floats). */
+int mi_gguf_upload_raw(mi_gguf* g, uint64_t index, void* dst, uint64_t dst_bytes, void* stream);
+int mi_gguf_upload_f32(mi_gguf* g, uint64_t index, float* dst, uint64_t n, void* stream);
+int mi_gguf_upload_q8_split(mi_gguf* g, uint64_t index, int8_t* payload, float* scales, void* stream);
 
 #ifdef __cplusplus
 }

@@ -79,6 +79,33 @@ def ref_lib() -> ctypes.CDLL | None:
         R.ref_fp16_to_fp32.argtypes = [ctypes.c_uint16]
         R.ref_q8_0_decode.restype = ctypes.c_int
         R.ref_q8_0_decode.argtypes = [ctypes.c_char_p, _vp, _u64, _u64, _vp, _vp, _vp, _vp, _vp]
+        cp, i32 = ctypes.c_char_p, ctypes.c_int
+        R.ref_gguf_open.restype = _vp
+        R.ref_gguf_open.argtypes = [cp, cp, cp, i32]
+        R.ref_gguf_close.argtypes = [_vp]
+        R.ref_gguf_version.restype = ctypes.c_uint32
+        R.ref_gguf_version.argtypes = [_vp]
+        R.ref_gguf_count.restype = _u64
+        R.ref_gguf_count.argtypes = [_vp]
+        R.ref_gguf_data_offset.restype = _u64
+        R.ref_gguf_data_offset.argtypes = [_vp]
+        R.ref_gguf_tensor.argtypes = [_vp, _u64, cp, i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
+        R.ref_gguf_read_float.restype = ctypes.c_int64
+        R.ref_gguf_read_float.argtypes = [_vp, cp, _vp, _u64, cp, i32]
+        R.ref_gguf_read_q8.argtypes = [_vp, cp, _vp, _vp, i32, cp, i32]
+        R.ref_gguf_read_raw.argtypes = [_vp, _u64, _vp, _u64]
+        R.ref_gguf_meta.argtypes = [_vp, cp, _vp, _vp, _vp, _vp, cp, i32, _vp, _vp]
+        R.ref_gguf_meta_array.argtypes = [_vp, cp, _vp, _vp, _u64]
+        R.ref_gguf_meta_str_item.argtypes = [_vp, cp, _u64, cp, i32]
+        R.ref_gguf_get_u64.restype = _u64
+        R.ref_gguf_get_u64.argtypes = [_vp, cp, _u64]
+        R.ref_gguf_get_i64.restype = ctypes.c_int64
+        R.ref_gguf_get_i64.argtypes = [_vp, cp, ctypes.c_int64]
+        R.ref_gguf_get_f64.restype = ctypes.c_double
+        R.ref_gguf_get_f64.argtypes = [_vp, cp, ctypes.c_double]
+        R.ref_gguf_get_f32.restype = ctypes.c_float
+        R.ref_gguf_get_f32.argtypes = [_vp, cp, ctypes.c_float]
+        R.ref_gguf_get_str.argtypes = [_vp, cp, cp, cp, i32]
         _ref = R
     return _ref
 
@@ -155,6 +182,115 @@ def ref_q8_0_decode(blocks: np.ndarray, rows: int, cols: int):
     if st != 0:
         raise RuntimeError(f"reference GGUF decode failed: {st}")
     return out, q, s, q2, s2
+
+
+class RefGguf:
+    """The reference's ofc::GgufFile (Gguf.hpp:90-140) opened on a file, with its
+    table, metadata and decoders returned as numpy / Python values. Test
+    infrastructure: the checker for libmi_sdvk.so's mi_gguf_* entries."""
+
+    def __init__(self, path, prefix: str = ""):
+        R = ref_lib()
+        if R is None:
+            raise RuntimeError("oracle/_ref/libgguf_ref.so is not built")
+        self.R = R
+        err = ctypes.create_string_buffer(512)
+        self.h = R.ref_gguf_open(str(path).encode(), prefix.encode() if prefix else None, err, 512)
+        self.error = None if self.h else err.value.decode()
+
+    def close(self):
+        if self.h:
+            self.R.ref_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    @property
+    def ok(self) -> bool:
+        return bool(self.h)
+
+    def version(self) -> int:
+        return int(self.R.ref_gguf_version(self.h))
+
+    def data_offset(self) -> int:
+        return int(self.R.ref_gguf_data_offset(self.h))
+
+    def tensors(self) -> list:
+        """[(name, type, dims, offset, nbytes, shape)] in table order."""
+        out = []
+        for i in range(int(self.R.ref_gguf_count(self.h))):
+            name = ctypes.create_string_buffer(4096)
+            t, nd = ctypes.c_uint32(), ctypes.c_uint32()
+            dims = (ctypes.c_uint64 * 4)()
+            off, nb, r, c = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
+            assert self.R.ref_gguf_tensor(self.h, i, name, 4096, ctypes.byref(t), ctypes.byref(nd), dims,
+                                          ctypes.byref(off), ctypes.byref(nb), ctypes.byref(r), ctypes.byref(c)) == 0
+            out.append((name.value.decode(), t.value, tuple(dims[: nd.value]), off.value, nb.value, (r.value, c.value)))
+        return out
+
+    def read_raw(self, index: int, nbytes: int):
+        out = np.empty(nbytes, dtype=np.uint8)
+        st = self.R.ref_gguf_read_raw(self.h, index, _p(out), nbytes)
+        return out if st == 0 else None
+
+    def read_float(self, name: str, n: int):
+        """(values or None, error text)."""
+        out = np.empty(max(n, 1), dtype=np.float32)
+        err = ctypes.create_string_buffer(512)
+        k = self.R.ref_gguf_read_float(self.h, name.encode(), _p(out), out.size, err, 512)
+        return (out[:k], "") if k >= 0 else (None, err.value.decode())
+
+    def read_q8(self, name: str, n: int, into: bool):
+        q = np.empty(max(n, 1), dtype=np.int8)
+        s = np.empty(max(n // 32, 1), dtype=np.float32)
+        err = ctypes.create_string_buffer(512)
+        st = self.R.ref_gguf_read_q8(self.h, name.encode(), _p(q), _p(s), 1 if into else 0, err, 512)
+        return (q[:n], s[: n // 32], "") if st == 0 else (None, None, err.value.decode())
+
+    def meta(self, key: str):
+        """None, or dict(type, u, f, b, s, arr_type, items)."""
+        t, ar, n = ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_uint64()
+        u, f, b = ctypes.c_uint64(), ctypes.c_double(), ctypes.c_int()
+        s = ctypes.create_string_buffer(1 << 16)
+        if self.R.ref_gguf_meta(self.h, key.encode(), ctypes.byref(t), ctypes.byref(u), ctypes.byref(f),
+                                ctypes.byref(b), s, 1 << 16, ctypes.byref(ar), ctypes.byref(n)) != 0:
+            return None
+        items: tuple = ()
+        if t.value == 9 and n.value:
+            if ar.value == 8:
+                lst = []
+                for i in range(n.value):
+                    sb = ctypes.create_string_buffer(1 << 16)
+                    self.R.ref_gguf_meta_str_item(self.h, key.encode(), i, sb, 1 << 16)
+                    lst.append(sb.value.decode("utf-8", "replace"))
+                items = tuple(lst)
+            else:
+                uu = np.zeros(n.value, dtype=np.uint64)
+                ff = np.zeros(n.value, dtype=np.float64)
+                self.R.ref_gguf_meta_array(self.h, key.encode(), _p(uu), _p(ff), n.value)
+                if ar.value in (6, 12):
+                    items = tuple(float(x) for x in ff)
+                elif ar.value == 7:
+                    items = tuple(bool(x) for x in uu)
+                else:
+                    items = tuple(int(x) for x in uu)
+        return dict(type=t.value, u=u.value, f=f.value, b=bool(b.value), s=s.value.decode("utf-8", "replace"),
+                    arr_type=ar.value, items=items)
+
+    def get(self, kind: str, key: str, default):
+        k = key.encode()
+        if kind == "u64":
+            return int(self.R.ref_gguf_get_u64(self.h, k, default))
+        if kind == "i64":
+            return int(self.R.ref_gguf_get_i64(self.h, k, default))
+        if kind == "f64":
+            return float(self.R.ref_gguf_get_f64(self.h, k, default))
+        if kind == "f32":
+            return float(self.R.ref_gguf_get_f32(self.h, k, default))
+        out = ctypes.create_string_buffer(1 << 16)
+        self.R.ref_gguf_get_str(self.h, k, default.encode(), out, 1 << 16)
+        return out.value.decode("utf-8", "replace")
 
 
 # ---------------------------------------------------------------------- GEMM --

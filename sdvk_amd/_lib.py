@@ -12,7 +12,8 @@ from . import hip
 
 LIB_PATH = Path(__file__).resolve().parent / "libmi_sdvk.so"
 
-MI_OK, MI_ERR_INVALID_ARG, MI_ERR_UNSUPPORTED, MI_ERR_ALIGNMENT, MI_ERR_ALIASING, MI_ERR_HIP = range(6)
+(MI_OK, MI_ERR_INVALID_ARG, MI_ERR_UNSUPPORTED, MI_ERR_ALIGNMENT, MI_ERR_ALIASING, MI_ERR_HIP, MI_ERR_IO,
+ MI_ERR_NOT_FOUND) = range(8)
 MI_F32, MI_F16 = 0, 1
 
 # Every function declared in include/mi_sdvk.h, with its ctypes signature.
@@ -47,6 +48,18 @@ class MiBlockDims(ctypes.Structure):
                                     "ff_inner")]
 
 
+class MiGgufTensorInfo(ctypes.Structure):
+    """Mirror of mi_gguf_tensor_info (include/mi_sdvk.h)."""
+    _fields_ = [("name", ctypes.c_char_p), ("type", _u32), ("n_dims", _u32), ("dims", _u64 * 4),
+                ("offset", _u64), ("nbytes", _u64), ("n_elems", _u64), ("rows", _u64), ("cols", _u64)]
+
+
+class MiGgufMetaInfo(ctypes.Structure):
+    """Mirror of mi_gguf_meta_info (include/mi_sdvk.h)."""
+    _fields_ = [("type", _u32), ("arr_type", _u32), ("u", _u64), ("f", ctypes.c_double), ("b", _i32),
+                ("str", ctypes.POINTER(ctypes.c_char)), ("str_len", _u64), ("arr_len", _u64)]
+
+
 SIGNATURES = {
     "mi_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "mi_last_error": (ctypes.c_char_p, []),
@@ -68,6 +81,20 @@ SIGNATURES = {
     "mi_block_workspace_bytes": (_u64, [ctypes.POINTER(MiBlockDims)]),
     "mi_sdxl_block_forward": (ctypes.c_int, [ctypes.POINTER(MiBlockWeights), ctypes.POINTER(MiBlockDims), _vp, _vp,
                                              _vp, _vp, _u64, _vp]),
+    "mi_gguf_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "mi_gguf_close": (None, [_vp]),
+    "mi_gguf_info": (ctypes.c_int, [_vp, ctypes.POINTER(_u32), ctypes.POINTER(_u64), ctypes.POINTER(_u64),
+                                    ctypes.POINTER(_u64)]),
+    "mi_gguf_tensor": (ctypes.c_int, [_vp, _u64, ctypes.POINTER(MiGgufTensorInfo)]),
+    "mi_gguf_find": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.POINTER(_u64)]),
+    "mi_gguf_meta": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.POINTER(MiGgufMetaInfo)]),
+    "mi_gguf_meta_array": (ctypes.c_int, [_vp, ctypes.c_char_p, _u64, _u64, _vp, _vp, _vp]),
+    "mi_gguf_read_raw": (ctypes.c_int, [_vp, _u64, _vp, _u64]),
+    "mi_gguf_read_f32": (ctypes.c_int, [_vp, _u64, _vp, _u64]),
+    "mi_gguf_read_q8_split": (ctypes.c_int, [_vp, _u64, _vp, _vp]),
+    "mi_gguf_upload_raw": (ctypes.c_int, [_vp, _u64, _vp, _u64, _vp]),
+    "mi_gguf_upload_f32": (ctypes.c_int, [_vp, _u64, _vp, _u64, _vp]),
+    "mi_gguf_upload_q8_split": (ctypes.c_int, [_vp, _u64, _vp, _vp, _vp]),
 }
 
 _lib = None

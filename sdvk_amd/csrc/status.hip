@@ -36,6 +36,8 @@ extern "C" const char* mi_status_string(int status) {
         case MI_ERR_ALIGNMENT: return "alignment requirement not met";
         case MI_ERR_ALIASING: return "output overlaps an input";
         case MI_ERR_HIP: return "HIP runtime error";
+        case MI_ERR_IO: return "file or format error";
+        case MI_ERR_NOT_FOUND: return "not found";
         default: return "unknown status";
     }
 }

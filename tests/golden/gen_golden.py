@@ -13,6 +13,12 @@ attn_ref_shapes.npz -- the reference attention test's four shapes
     (tests/fused_attn_test.cpp:74-79) with inputs on an fp16-exact grid
     (k/2048, |k| <= 2048) and the fp64 online-softmax outputs.
 
+gguf_sample_ref.npz -- the sample checkpoint of tests/gguf_writer.py
+    (sample_spec: every metadata type, F32 / F16 / BF16 / Q4_0 / Q8_0 / Q4_K
+    tensors) and what the REFERENCE'S OWN GgufFile returns for it opened with
+    the UNet prefix: tensor table, data offset, readFloat and readQ8Into per
+    tensor (Gguf.cpp:290-583). Requires oracle/_ref.
+
 Run from the repo root: python tests/golden/gen_golden.py
 """
 from __future__ import annotations
@@ -26,6 +32,9 @@ ROOT = Path(__file__).resolve().parents[2]
 sys.path.insert(0, str(ROOT))
 
 from oracle import binding as ob  # noqa: E402
+
+sys.path.insert(0, str(ROOT / "tests"))
+import gguf_writer as gw  # noqa: E402
 
 OUT = Path(__file__).resolve().parent
 
@@ -80,9 +89,39 @@ def gen_attn() -> None:
     np.savez_compressed(OUT / "attn_ref_shapes.npz", **data)
 
 
+def gen_gguf() -> None:
+    import tempfile
+
+    with tempfile.TemporaryDirectory() as d:
+        path = Path(d) / "sample.gguf"
+        data = gw.write(path, gw.sample_spec())
+        r = ob.RefGguf(path, gw.PREFIX)
+        if not r.ok:
+            raise SystemExit(f"reference reader rejects the sample: {r.error}")
+        out = {"file_bytes": np.frombuffer(data, dtype=np.uint8), "data_offset": r.data_offset()}
+        table = r.tensors()
+        out["names"] = np.array([t[0] for t in table])
+        for i, (name, ty, dims, off, nb, _) in enumerate(table):
+            out[f"t{i}_tob"] = np.array([ty, off, nb], dtype=np.uint64)
+            out[f"t{i}_dims"] = np.array(dims, dtype=np.uint64)
+            n = int(np.prod(dims))
+            f, _ = r.read_float(name, n)
+            if f is not None:
+                out[f"t{i}_float"] = f
+            q, sc, _ = r.read_q8(name, n, True)
+            if q is not None:
+                out[f"t{i}_q"], out[f"t{i}_s"] = q, sc
+        r.close()
+    np.savez_compressed(OUT / "gguf_sample_ref.npz", **out)
+
+
 if __name__ == "__main__":
+    if ob.ref_lib() is None:
+        raise SystemExit("oracle/_ref/libgguf_ref.so missing: build it with `make -C oracle` "
+                         "where /root/reference is present")
     gen_q8()
     gen_gemm()
     gen_attn()
+    gen_gguf()
     for p in sorted(OUT.glob("*.npz")):
         print(p.name, p.stat().st_size)
