@@ -223,6 +223,23 @@ int mi_sdxl_block_forward(const mi_block_weights* w, const mi_block_dims* dims, 
                           const float* ctx, const int32_t* ctx_len, void* workspace,
                           uint64_t workspace_bytes, void* stream);
 
+/* Cross-attention K / V caching. The context is fixed for a sampling job, yet
+ * crossAttention projects it with to_k / to_v for every block, guidance pass
+ * and step (sdvkgen.cpp:1283-1290; ctx uploaded once at :3659-3667).
+ * mi_block_ctx_kv computes K = ctx . attn2_k^T and V = ctx . attn2_v^T once
+ * into `kv` (K, then V at byte offset mi_block_ctx_kv_bytes / 2; each
+ * [batch * ctx_tokens, channels] fp32; 256-byte aligned, caller-owned);
+ * mi_sdxl_block_forward_kv then runs the block exactly like
+ * mi_sdxl_block_forward but reads K / V from `kv` instead of projecting ctx.
+ * The K / V GEMMs split K with fp32 atomics, so a fresh projection and a
+ * cached one may differ in the last bits.                                   */
+uint64_t mi_block_ctx_kv_bytes(const mi_block_dims* dims);
+int mi_block_ctx_kv(const mi_block_weights* w, const mi_block_dims* dims, const float* ctx, float* kv,
+                    uint64_t kv_bytes, void* stream);
+int mi_sdxl_block_forward_kv(const mi_block_weights* w, const mi_block_dims* dims, float* x,
+                             const float* kv, uint64_t kv_bytes, const int32_t* ctx_len, void* workspace,
+                             uint64_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------- GGUF -- *
  * Checkpoint access: the container reader and the upload of its tensors into
  * caller-owned device buffers in the layouts the GEMM entries read.

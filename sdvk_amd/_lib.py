@@ -81,6 +81,11 @@ SIGNATURES = {
     "mi_block_workspace_bytes": (_u64, [ctypes.POINTER(MiBlockDims)]),
     "mi_sdxl_block_forward": (ctypes.c_int, [ctypes.POINTER(MiBlockWeights), ctypes.POINTER(MiBlockDims), _vp, _vp,
                                              _vp, _vp, _u64, _vp]),
+    "mi_block_ctx_kv_bytes": (_u64, [ctypes.POINTER(MiBlockDims)]),
+    "mi_block_ctx_kv": (ctypes.c_int, [ctypes.POINTER(MiBlockWeights), ctypes.POINTER(MiBlockDims), _vp, _vp, _u64,
+                                       _vp]),
+    "mi_sdxl_block_forward_kv": (ctypes.c_int, [ctypes.POINTER(MiBlockWeights), ctypes.POINTER(MiBlockDims), _vp,
+                                                _vp, _u64, _vp, _vp, _u64, _vp]),
     "mi_gguf_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "mi_gguf_close": (None, [_vp]),
     "mi_gguf_info": (ctypes.c_int, [_vp, ctypes.POINTER(_u32), ctypes.POINTER(_u64), ctypes.POINTER(_u64),

@@ -72,28 +72,31 @@ int attention(const mi_block_dims& d, const float* q, const float* k, const floa
     return mi_fused_attention_ex(&x, s);
 }
 
-}  // namespace
-}  // namespace mi
-
-using namespace mi;
-
-extern "C" uint64_t mi_block_workspace_bytes(const mi_block_dims* dims) {
-    if (!dims) return 0;
-    Workspace w;
-    return layout(*dims, nullptr, &w);
-}
-
-extern "C" int mi_sdxl_block_forward(const mi_block_weights* wt, const mi_block_dims* dims, float* x, const float* ctx,
-                                     const int32_t* ctx_len, void* workspace, uint64_t workspace_bytes, void* stream) {
-    const char* fn = "mi_sdxl_block_forward";
-    if (!wt || !dims || !x || !ctx || !workspace) return fail(MI_ERR_INVALID_ARG, "%s: null pointer", fn);
-    const mi_block_dims d = *dims;
-    MI_TRY(check_dims(d, fn));
-    const mi_block_weights w = *wt;
+int check_weights(const mi_block_weights& w, const char* fn) {
     const void* mats[10] = {w.attn1_q, w.attn1_k, w.attn1_v, w.attn1_out, w.attn2_q,
                             w.attn2_k, w.attn2_v, w.attn2_out, w.ff_up, w.ff_down};
     for (const void* m : mats)
         if (!m) return fail(MI_ERR_INVALID_ARG, "%s: null weight", fn);
+    return MI_OK;
+}
+
+// Bytes of the cached cross-attention K and V: two [batch * ctx_tokens, channels] fp32 tensors.
+uint64_t ctx_kv_bytes(const mi_block_dims& d) {
+    return 2 * round256(static_cast<uint64_t>(d.batch) * d.ctx_tokens * d.channels * 4);
+}
+
+int ctx_kv(const mi_block_weights& w, const mi_block_dims& d, const float* ctx, float* k, float* v, hipStream_t s) {
+    const uint32_t crow = d.batch * d.ctx_tokens;
+    MI_TRY(mi_gemm_nt_q8_0(ctx, w.attn2_k, nullptr, k, crow, d.channels, d.ctx_channels, 0, 0, 0, 1, 0, 0, s));
+    return mi_gemm_nt_q8_0(ctx, w.attn2_v, nullptr, v, crow, d.channels, d.ctx_channels, 0, 0, 0, 1, 0, 0, s);
+}
+
+// One block. Cross-attention K / V come from `kv` (K then V, ctx_kv_bytes
+// layout) when given, else are projected from `ctx` into the workspace.
+int forward(const mi_block_weights& w, const mi_block_dims& d, float* x, const float* ctx, const float* kv,
+            const int32_t* ctx_len, void* workspace, uint64_t workspace_bytes, hipStream_t s, const char* fn) {
+    MI_TRY(check_dims(d, fn));
+    MI_TRY(check_weights(w, fn));
     Workspace ws;
     const uint64_t need = layout(d, static_cast<char*>(workspace), &ws);
     if (workspace_bytes < need)
@@ -101,8 +104,7 @@ extern "C" int mi_sdxl_block_forward(const mi_block_weights* wt, const mi_block_
                     static_cast<unsigned long long>(workspace_bytes), static_cast<unsigned long long>(need));
     if (!aligned(workspace, 256)) return fail(MI_ERR_ALIGNMENT, "%s: workspace must be 256-byte aligned", fn);
 
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    const uint32_t rows = d.batch * d.tokens, crow = d.batch * d.ctx_tokens, C = d.channels;
+    const uint32_t rows = d.batch * d.tokens, C = d.channels;
     const uint64_t nx = static_cast<uint64_t>(rows) * C;
     auto gemm = [&](const float* A, const void* W, const float* bias, float* out, uint32_t M, uint32_t N, uint32_t K) {
         return mi_gemm_nt_q8_0(A, W, bias, out, M, N, K, 0, 0, 0, 1, 0, 0, s);
@@ -119,9 +121,14 @@ extern "C" int mi_sdxl_block_forward(const mi_block_weights* wt, const mi_block_
     // cross-attention over the context
     MI_TRY(mi_layernorm(x, w.norm2_w, w.norm2_b, ws.n, rows, C, 1e-5f, s));
     MI_TRY(gemm(ws.n, w.attn2_q, nullptr, ws.q, rows, C, C));
-    MI_TRY(gemm(ctx, w.attn2_k, nullptr, ws.k, crow, C, d.ctx_channels));
-    MI_TRY(gemm(ctx, w.attn2_v, nullptr, ws.v, crow, C, d.ctx_channels));
-    MI_TRY(attention(d, ws.q, ws.k, ws.v, ws.o, d.ctx_tokens, ctx_len, s));
+    const float *ck = ws.k, *cv = ws.v;
+    if (kv) {
+        ck = kv;
+        cv = kv + ctx_kv_bytes(d) / 2 / 4;
+    } else {
+        MI_TRY(ctx_kv(w, d, ctx, ws.k, ws.v, s));
+    }
+    MI_TRY(attention(d, ws.q, ck, cv, ws.o, d.ctx_tokens, ctx_len, s));
     MI_TRY(gemm(ws.o, w.attn2_out, w.attn2_out_b, ws.a, rows, C, C));
     MI_TRY(mi_add_inplace(x, ws.a, nx, s));
     // GEGLU feed-forward
@@ -131,4 +138,51 @@ extern "C" int mi_sdxl_block_forward(const mi_block_weights* wt, const mi_block_
     MI_TRY(gemm(ws.g, w.ff_down, w.ff_down_b, ws.a, rows, C, d.ff_inner));
     MI_TRY(mi_add_inplace(x, ws.a, nx, s));
     return MI_OK;
+}
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" uint64_t mi_block_workspace_bytes(const mi_block_dims* dims) {
+    if (!dims) return 0;
+    Workspace w;
+    return layout(*dims, nullptr, &w);
+}
+
+extern "C" int mi_sdxl_block_forward(const mi_block_weights* wt, const mi_block_dims* dims, float* x, const float* ctx,
+                                     const int32_t* ctx_len, void* workspace, uint64_t workspace_bytes, void* stream) {
+    const char* fn = "mi_sdxl_block_forward";
+    if (!wt || !dims || !x || !ctx || !workspace) return fail(MI_ERR_INVALID_ARG, "%s: null pointer", fn);
+    return forward(*wt, *dims, x, ctx, nullptr, ctx_len, workspace, workspace_bytes, static_cast<hipStream_t>(stream),
+                   fn);
+}
+
+extern "C" uint64_t mi_block_ctx_kv_bytes(const mi_block_dims* dims) { return dims ? ctx_kv_bytes(*dims) : 0; }
+
+extern "C" int mi_block_ctx_kv(const mi_block_weights* wt, const mi_block_dims* dims, const float* ctx, float* kv,
+                               uint64_t kv_bytes, void* stream) {
+    const char* fn = "mi_block_ctx_kv";
+    if (!wt || !dims || !ctx || !kv) return fail(MI_ERR_INVALID_ARG, "%s: null pointer", fn);
+    MI_TRY(check_dims(*dims, fn));
+    MI_TRY(check_weights(*wt, fn));
+    if (kv_bytes < ctx_kv_bytes(*dims))
+        return fail(MI_ERR_INVALID_ARG, "%s: kv buffer %llu bytes < %llu needed", fn,
+                    static_cast<unsigned long long>(kv_bytes), static_cast<unsigned long long>(ctx_kv_bytes(*dims)));
+    if (!aligned(kv, 256)) return fail(MI_ERR_ALIGNMENT, "%s: kv buffer must be 256-byte aligned", fn);
+    return ctx_kv(*wt, *dims, ctx, kv, kv + ctx_kv_bytes(*dims) / 2 / 4, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mi_sdxl_block_forward_kv(const mi_block_weights* wt, const mi_block_dims* dims, float* x,
+                                        const float* kv, uint64_t kv_bytes, const int32_t* ctx_len, void* workspace,
+                                        uint64_t workspace_bytes, void* stream) {
+    const char* fn = "mi_sdxl_block_forward_kv";
+    if (!wt || !dims || !x || !kv || !workspace) return fail(MI_ERR_INVALID_ARG, "%s: null pointer", fn);
+    if (kv_bytes < ctx_kv_bytes(*dims))
+        return fail(MI_ERR_INVALID_ARG, "%s: kv buffer %llu bytes < %llu needed", fn,
+                    static_cast<unsigned long long>(kv_bytes), static_cast<unsigned long long>(ctx_kv_bytes(*dims)));
+    if (!aligned(kv, 256)) return fail(MI_ERR_ALIGNMENT, "%s: kv buffer must be 256-byte aligned", fn);
+    return forward(*wt, *dims, x, nullptr, kv, ctx_len, workspace, workspace_bytes, static_cast<hipStream_t>(stream),
+                   fn);
 }

@@ -13,6 +13,7 @@ Names, argument meaning and error behaviour follow the reference
       sdvkgen.cpp:1094-1103, :1709-1720, :1746,1751,1762
   BlockWeights / BlockDims / sdxl_block_forward (one transformer block)
       sdvkgen.cpp:1739-1763 with crossAttention :1283-1290
+  block_ctx_kv / sdxl_block_forward_kv (the block with cached context K / V)
 
 Where the reference calls exit(1) (unsupported attention shape, binding-count
 mismatch) these raise MiError / ValueError instead. Every call goes to
@@ -31,7 +32,8 @@ __all__ = [
     "MiError", "MI_F32", "MI_F16", "FusedAttnArgs", "fused_attn_supported", "fused_attention",
     "fused_attention_ex", "gemm_nt_q8", "gemm_nt_q8_bias", "gemm_nt_q8_0", "q8_0_dequant",
     "q8_split_dequant", "q8_0_to_split", "q8_0_quantize", "Pg", "dispatch", "KERNELS", "layernorm", "geglu", "add2",
-    "BlockWeights", "BlockDims", "block_workspace_bytes", "sdxl_block_forward",
+    "BlockWeights", "BlockDims", "block_workspace_bytes", "sdxl_block_forward", "block_ctx_kv_bytes", "block_ctx_kv",
+    "sdxl_block_forward_kv",
 ]
 
 
@@ -197,6 +199,28 @@ def sdxl_block_forward(w: BlockWeights, dims: BlockDims, x, ctx, workspace, *, c
     wc, dc = w.c(), dims.c()
     call("mi_sdxl_block_forward", ctypes.byref(wc), ctypes.byref(dc), ptr(x), ptr(ctx), ptr(ctx_len),
          ptr(workspace), nbytes, _s(stream))
+
+
+def block_ctx_kv_bytes(dims: BlockDims) -> int:
+    """Bytes of one block's cached cross-attention K and V."""
+    return int(_lib.load().mi_block_ctx_kv_bytes(ctypes.byref(dims.c())))
+
+
+def block_ctx_kv(w: BlockWeights, dims: BlockDims, ctx, kv, *, stream=None) -> None:
+    """K = ctx . attn2_k^T, V = ctx . attn2_v^T into kv, once per sampling job
+    (crossAttention recomputes them every call, sdvkgen.cpp:1283-1290)."""
+    wc, dc = w.c(), dims.c()
+    call("mi_block_ctx_kv", ctypes.byref(wc), ctypes.byref(dc), ptr(ctx), ptr(kv), getattr(kv, "nbytes", 0),
+         _s(stream))
+
+
+def sdxl_block_forward_kv(w: BlockWeights, dims: BlockDims, x, kv, workspace, *, ctx_len=None,
+                          workspace_bytes: Optional[int] = None, stream=None) -> None:
+    """sdxl_block_forward with the cross-attention K / V of block_ctx_kv."""
+    nbytes = workspace_bytes if workspace_bytes is not None else getattr(workspace, "nbytes", 0)
+    wc, dc = w.c(), dims.c()
+    call("mi_sdxl_block_forward_kv", ctypes.byref(wc), ctypes.byref(dc), ptr(x), ptr(kv), getattr(kv, "nbytes", 0),
+         ptr(ctx_len), ptr(workspace), nbytes, _s(stream))
 
 
 # --------------------------------------------- reference kernel-name dispatch --
