@@ -133,6 +133,21 @@ int mi_gemm_nt_q8_split(const float* A, const uint32_t* payload, const float* sc
                         uint32_t mode, uint32_t lda, uint32_t ldc, uint32_t batch, uint64_t sA,
                         uint64_t sC, void* stream);
 
+/* Q8 NN GEMM (the conv / 1x1 paths' weights-left product):
+ *   C[M,N] (=|+=) deq(A[M,K]) . B[K,N]
+ * A in the split layout, read at FLAT index fl = z*sA + m*lda + k: value
+ * int8(payload byte fl) * scales[fl >> 5] (gemm_nn_q8_v.comp:23-28,54-64);
+ * B fp32 row-major (ldb); mode 0 stores, 1 accumulates, no bias; batch z
+ * offsets A by z*sA, B by z*sB, C by z*sC; lda/ldb/ldc == 0 -> K, N, N.
+ * K and N must be multiples of 4 (the shader's 4-wide staging zero-fills a
+ * partial group, :58,79: rejected, not emulated). payload 4-byte aligned with
+ * lda, sA % 4 == 0; B 16-byte aligned with ldb, sB % 4 == 0; each operand
+ * below 2 GiB. Replaces Engine::dispatch("gemm_nn_q8_v" / "gemm_nn_q8",
+ * {Aq, B, C, S}, Pg) (vk_engine.cpp:57,63) behind gemmNnQ8 (sdvkgen.cpp:944-948). */
+int mi_gemm_nn_q8_split(const uint32_t* payload, const float* scales, const float* B, float* C,
+                        uint32_t M, uint32_t N, uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldb,
+                        uint32_t ldc, uint32_t batch, uint64_t sA, uint64_t sB, uint64_t sC, void* stream);
+
 /* ----------------------------------------------------------- attention -- *
  * O = softmax(Q K^T / sqrt(hd) + mask) V per head, hd = C / heads <= 64,
  * never materialising Tq x Tk. Head h occupies columns [h*hd, h*hd + hd) of

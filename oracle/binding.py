@@ -48,6 +48,8 @@ def lib() -> ctypes.CDLL:
         L.or_q8_0_dequant.argtypes = [_vp, _u64, _vp]
         L.or_q8_0_to_split.argtypes = [_vp, _u64, _vp, _vp]
         L.or_q8_split_dequant.argtypes = [_vp, _vp, _u64, _vp]
+        L.or_gemm_nn_q8_split.argtypes = [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32,
+                                          _u64, _u64, _u64, ctypes.c_int, ctypes.c_int]
         L.or_gemm_nt_q8_split.argtypes = [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32,
                                           _u32, _u64, _u64, ctypes.c_int, ctypes.c_int]
         L.or_gemm_nt_q8_0.argtypes = [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32,
@@ -313,6 +315,18 @@ def gemm_nt_q8_split(A, payload, scales, M, N, K, *, bias=None, C=None, mode=0, 
         C = np.zeros(((batch - 1) * sC + (M - 1) * ldc_e + N) if batch > 1 else M * ldc_e, dtype=np.float32)
     lib().or_gemm_nt_q8_split(_p(A), _p(payload), _p(scales), _p(bias), _p(C), M, N, K, mode, lda, ldc,
                               batch, sA, sC, 1 if acc64 else 0, threads)
+    return C
+
+
+def gemm_nn_q8_split(payload, scales, B, M, N, K, *, C=None, mode=0, lda=0, ldb=0, ldc=0, batch=1, sA=0, sB=0,
+                     sC=0, acc64=True, threads=1) -> np.ndarray:
+    """C[M,N] (=|+=) deq(A)[M,K] . B[K,N] (gemm_nn_q8_v.comp), C flat with ldc / sC."""
+    ldc_e = ldc or N
+    if C is None:
+        C = np.zeros(((batch - 1) * sC + (M - 1) * ldc_e + N) if batch > 1 else M * ldc_e, dtype=np.float32)
+    lib().or_gemm_nn_q8_split(_p(np.ascontiguousarray(payload)), _p(np.ascontiguousarray(scales)),
+                              _p(np.ascontiguousarray(B)), _p(C), M, N, K, mode, lda, ldb, ldc, batch, sA, sB, sC,
+                              1 if acc64 else 0, threads)
     return C
 
 

@@ -11,6 +11,7 @@
  *   src/Modules/Model/Gguf.cpp:514-523    Q8_0 dequant to fp32
  *   src/Modules/Model/Gguf.cpp:559-583    Q8_0 -> split int8 payload + fp32 scale
  *   src/Modules/GPU/shaders/gemm_nt_q8_v.comp:37-43,53-54,115-127   deqB, lda/ldc, epilogue
+ *   src/Modules/GPU/shaders/gemm_nn_q8_v.comp:23-28,38-40,54-64,107-108   deqA, ld*, modes
  *   src/Modules/GPU/shaders/fused_attn_tiled.comp, fused_attn.comp   masks, l == 0 guard
  *   tests/fused_attn_test.cpp:25-61       fp64 online-softmax reference
  *   src/Modules/GPU/shaders/layernorm_fwd.comp:15-38, unary_fwd.comp:28-36 (mode 4)
@@ -26,6 +27,10 @@
  *   or_gemm_nt_q8_*      numpy float64 matmul of the dequantized weight (an independent
  *                        library routine), linearity, mode 1 == C0 + mode 0 without bias,
  *                        bias broadcast, batch with shared W, lda/ldc padding
+ *   or_gemm_nn_q8_split  numpy float64 matmul with the flat-index scales, NN(W, B) ==
+ *                        NT(B^T, W)^T through the pinned or_gemm_nt_q8_split, mode 1,
+ *                        batch offsets of all three operands, lda/ldb/ldc padding, a
+ *                        scale block that straddles rows (lda % 32 != 0)
  *   or_fused_attention*  torch/numpy float64 softmax(QK^T s) V (independent library route),
  *                        Tk = 1 -> O = V row, constant scores -> mean of V, causal row 0 = V[0],
  *                        kv_len slicing == unmasked call on the prefix, kv_len = 0 -> O = 0
@@ -272,6 +277,58 @@ void or_gemm_nt_q8_0_rows(const float* A, const uint8_t* blocks, const float* bi
         }
     }
     free(Wf);
+}
+
+/* gemm_nn_q8_v.comp:30-111 (the weights-left GEMM of the conv / 1x1 paths,
+ * sdvkgen.cpp:944-948,1133-1180): C[M,N] (=|+=) A[M,K] . B[K,N] with A the
+ * split Q8 layout read at flat index fl = z*sA + m*lda + k, value
+ * int8(payload byte fl) * scales[fl >> 5] (:23-28,54-64), B fp32 at
+ * z*sB + k*ldb + n, C at z*sC + m*ldc + n; lda = 0 -> K, ldb = 0 -> N,
+ * ldc = 0 -> N (:38-40); mode 1 accumulates (:107-108); no bias. The shader's
+ * 4-wide staging zero-fills a last partial group when K % 4 or N % 4 != 0
+ * (:58,79); this restates the plain product, which the shader equals for
+ * K % 4 == 0 and N % 4 == 0 (the only shapes the HIP entry accepts). */
+void or_gemm_nn_q8_split(const uint32_t* payload, const float* scales, const float* B, float* C, uint32_t M,
+                         uint32_t N, uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldb, uint32_t ldc,
+                         uint32_t batch, uint64_t sA, uint64_t sB, uint64_t sC, int acc64, int threads) {
+    if (lda == 0) lda = K;
+    if (ldb == 0) ldb = N;
+    if (ldc == 0) ldc = N;
+    const int8_t* q = (const int8_t*)payload;
+    for (uint32_t z = 0; z < batch; ++z) {
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : 1)
+#endif
+        for (long long mm = 0; mm < (long long)M; ++mm) {
+            const uint32_t m = (uint32_t)mm;
+            const uint64_t arow = z * sA + (uint64_t)m * lda;
+            float* c = C + z * sC + (uint64_t)m * ldc;
+            double* acc = (double*)calloc(N, sizeof(double));
+            float* accf = (float*)calloc(N, sizeof(float));
+            if (!acc || !accf) {
+                free(acc);
+                free(accf);
+                continue;
+            }
+            for (uint32_t k = 0; k < K; ++k) {
+                const uint64_t fl = arow + k;
+                const float a = (float)q[fl] * scales[fl >> 5];
+                const float* b = B + z * sB + (uint64_t)k * ldb;
+                if (acc64) {
+                    for (uint32_t n = 0; n < N; ++n) acc[n] += (double)a * (double)b[n];
+                } else {
+                    for (uint32_t n = 0; n < N; ++n) accf[n] += a * b[n];
+                }
+            }
+            for (uint32_t n = 0; n < N; ++n) {
+                const float v = acc64 ? (float)acc[n] : accf[n];
+                if (mode == 0) c[n] = v;
+                else c[n] += v;
+            }
+            free(acc);
+            free(accf);
+        }
+    }
 }
 
 /* ------------------------------------------------------------ attention ---- */

@@ -52,6 +52,12 @@ void or_gemm_nt_q8_0(const float* A, const uint8_t* blocks, const float* bias, f
                      uint32_t M, uint32_t N, uint32_t K, uint32_t mode, uint32_t lda,
                      uint32_t ldc, uint32_t batch, uint64_t sA, uint64_t sC, int acc64,
                      int threads);
+/* ---- Q8 NN GEMM:  C[M,N] (=|+=) deq(A[M,K]) . B[K,N] (gemm_nn_q8_v.comp) ---
+ * A in the split layout read at flat index z*sA + m*lda + k (scale index =
+ * flat >> 5), B fp32 row-major with ldb, no bias. 0 leading dims -> K, N, N. */
+void or_gemm_nn_q8_split(const uint32_t* payload, const float* scales, const float* B, float* C, uint32_t M,
+                         uint32_t N, uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldb, uint32_t ldc,
+                         uint32_t batch, uint64_t sA, uint64_t sB, uint64_t sC, int acc64, int threads);
 /* Output rows rows[0..nrows) of batch item `z` only (parity on sampled rows). */
 void or_gemm_nt_q8_0_rows(const float* A, const uint8_t* blocks, const float* bias, float* C,
                           uint32_t M, uint32_t N, uint32_t K, uint32_t lda, uint32_t ldc,

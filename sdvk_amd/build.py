@@ -15,7 +15,8 @@ CSRC = PKG / "csrc"
 LIB = PKG / "libmi_sdvk.so"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 
-SOURCES = ["status.hip", "q8_0.hip", "gemm_q8.hip", "attention.hip", "glue.hip", "block.hip", "gguf.cpp"]
+SOURCES = ["status.hip", "q8_0.hip", "gemm_q8.hip", "gemm_nn_q8.hip", "attention.hip", "glue.hip", "block.hip",
+           "gguf.cpp"]
 
 # Per-source extra flags. The attention kernel rescales its MFMA accumulators
 # with VALU ops; keeping MFMA operands in VGPRs (rather than AGPRs) removes the

@@ -7,6 +7,8 @@ Names, argument meaning and error behaviour follow the reference
       src/Modules/GPU/fused_attn.hpp:13-28, fused_attn.cpp:34-61
   gemm_nt_q8 / gemm_nt_q8_bias (split int8 + fp32-scale layout)
       src/Modules/Diffusion/sdvkgen.cpp:917-936
+  gemm_nn_q8 (weights-left GEMM of the conv paths, gemm_nn_q8_v.comp)
+      sdvkgen.cpp:944-948
   Pg push layout + dispatch(kernel_name, bufs, push)
       sdvkgen.cpp:901-903, vk_engine.cpp:1143-1180, KERNELS[] :55-63,123-124
   layernorm / geglu / add2 (block glue)
@@ -30,7 +32,7 @@ from ._lib import MI_F16, MI_F32, MiAttnArgs, MiBlockDims, MiBlockWeights, MiErr
 
 __all__ = [
     "MiError", "MI_F32", "MI_F16", "FusedAttnArgs", "fused_attn_supported", "fused_attention",
-    "fused_attention_ex", "gemm_nt_q8", "gemm_nt_q8_bias", "gemm_nt_q8_0", "q8_0_dequant",
+    "fused_attention_ex", "gemm_nt_q8", "gemm_nt_q8_bias", "gemm_nt_q8_0", "gemm_nn_q8", "q8_0_dequant",
     "q8_split_dequant", "q8_0_to_split", "q8_0_quantize", "Pg", "dispatch", "KERNELS", "layernorm", "geglu", "add2",
     "BlockWeights", "BlockDims", "block_workspace_bytes", "sdxl_block_forward", "block_ctx_kv_bytes", "block_ctx_kv",
     "sdxl_block_forward_kv",
@@ -91,6 +93,13 @@ def gemm_nt_q8(A, Bq, C, Bs, M: int, N: int, K: int, *, mode: int = 0, lda: int 
     """sdvkgen.cpp:917-926 gemmNtQ8: C = A . deq(Bq, Bs)^T on the split layout."""
     call("mi_gemm_nt_q8_split", ptr(A), ptr(Bq), ptr(Bs), None, ptr(C), M, N, K, mode, lda, ldc,
          batch, sA, sC, _s(stream))
+
+
+def gemm_nn_q8(Aq, As, B, C, M: int, N: int, K: int, *, mode: int = 0, lda: int = 0, ldb: int = 0, ldc: int = 0,
+               batch: int = 1, sA: int = 0, sB: int = 0, sC: int = 0, stream=None) -> None:
+    """sdvkgen.cpp:944-948 gemmNnQ8: C[M,N] = deq(Aq, As)[M,K] . B[K,N] (the conv paths' weights-left GEMM)."""
+    call("mi_gemm_nn_q8_split", ptr(Aq), ptr(As), ptr(B), ptr(C), M, N, K, mode, lda, ldb, ldc, batch, sA, sB, sC,
+         _s(stream))
 
 
 def gemm_nt_q8_bias(A, Bq, C, Bs, bias, M: int, N: int, K: int, *, mode: int = 0, lda: int = 0,
@@ -246,6 +255,7 @@ class Pg:
 KERNELS = {
     "gemm_nt_q8": 4, "gemm_nt_q8_v": 4, "gemm_nt_q8_v_bm128": 4, "gemm_nt_q8_v_bk32": 4,
     "gemm_nt_q8_v_bm128_bk32": 4, "gemm_nt_q8_v_b": 5, "gemm_nt_q8_v_bm128_b": 5,
+    "gemm_nn_q8_v": 4, "gemm_nn_q8": 4,
     "fused_attn": 4, "fused_attn_tiled": 4,
 }
 
@@ -258,7 +268,12 @@ def dispatch(kernel: str, bufs: Sequence, push, stream=None) -> None:
         raise ValueError(f"unknown kernel {kernel}")
     if len(bufs) != KERNELS[kernel]:
         raise ValueError(f"kernel {kernel} expects {KERNELS[kernel]} bindings, got {len(bufs)}")
-    if kernel.startswith("gemm_nt_q8"):
+    if kernel.startswith("gemm_nn_q8"):
+        Aq, B, C, S = bufs  # binding order {Aq, B, C, S} (vk_engine.cpp:57,63)
+        pc: Pg = push
+        call("mi_gemm_nn_q8_split", ptr(Aq), ptr(S), ptr(B), ptr(C), pc.M, pc.N, pc.K, pc.mode, pc.lda, pc.ldb,
+             pc.ldc, max(pc.batch, 1), pc.sA, pc.sB, pc.sC, _s(stream))
+    elif kernel.startswith("gemm_nt_q8"):
         A, Bq, C, S = bufs[:4]
         bias = bufs[4] if len(bufs) == 5 else None
         pc: Pg = push

@@ -418,3 +418,79 @@ def test_block_composition(oracle):
     e = np.max(np.abs(delta - delta_ref)) / np.sqrt(np.mean(delta_ref ** 2))
     print(f"block oracle vs fp64: {e:.2e}")
     assert e <= 2e-5
+
+
+# ------------------------------------------------------------------ NN GEMM --
+
+def nn_numpy(payload, scales, B, M, N, K, lda=0, ldb=0, z=0, sA=0, sB=0):
+    """float64 numpy: deq(A)[m, k] = int8(payload[fl]) * scales[fl >> 5], fl = z*sA + m*lda + k."""
+    lda, ldb = lda or K, ldb or N
+    fl = z * sA + np.arange(M)[:, None] * lda + np.arange(K)[None, :]
+    A = payload.view(np.int8)[fl].astype(np.float64) * scales[fl >> 5].astype(np.float64)
+    Bm = B[z * sB + np.arange(K)[:, None] * ldb + np.arange(N)[None, :]].astype(np.float64)
+    return A @ Bm
+
+
+def nn_inputs(oracle, M, N, K, seed, lda=0, ldb=0, batch=1, sA=0, sB=0):
+    lda_e, ldb_e = lda or K, ldb or N
+    na = (batch - 1) * sA + (M - 1) * lda_e + K
+    nb = (batch - 1) * sB + (K - 1) * ldb_e + N
+    payload = oracle.uniform_int(seed, -127, 127, na).astype(np.int8)
+    scales = oracle.normal(seed + 1, (na + 31) // 32, 0.01, 0.004)
+    B = oracle.normal(seed + 2, nb)
+    return payload, scales, B
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 4, 4), (7, 12, 36), (64, 64, 64), (100, 68, 288), (33, 200, 96)])
+def test_gemm_nn_oracle_vs_numpy(oracle, M, N, K):
+    payload, scales, B = nn_inputs(oracle, M, N, K, 40)
+    got = oracle.gemm_nn_q8_split(payload, scales, B, M, N, K).reshape(M, N)
+    want = nn_numpy(payload, scales, B, M, N, K)
+    assert np.max(np.abs(got - want)) <= 1e-6 * max(1.0, np.max(np.abs(want)))
+    f32 = oracle.gemm_nn_q8_split(payload, scales, B, M, N, K, acc64=False).reshape(M, N)
+    assert np.max(np.abs(f32 - want)) <= 1e-4 * max(1.0, np.max(np.abs(want)))
+
+
+def test_gemm_nn_is_transposed_nt(oracle):
+    """NN(W, B) = NT(B^T, W)^T: the same weight (split layout, rows of K with
+    K % 32 == 0 so flat scale blocks are per row) through the pinned NT oracle."""
+    M, N, K = 48, 40, 96
+    payload, scales, B = nn_inputs(oracle, M, N, K, 50)
+    nn = oracle.gemm_nn_q8_split(payload, scales, B, M, N, K).reshape(M, N)
+    Bt = np.ascontiguousarray(B.reshape(K, N).T).reshape(-1)
+    nt = oracle.gemm_nt_q8_split(Bt, payload, scales, N, M, K).reshape(N, M)
+    assert np.max(np.abs(nn - nt.T)) <= 1e-5 * np.max(np.abs(nn))
+
+
+def test_gemm_nn_modes_batch_strides(oracle):
+    """Batch z offsets A, B and C; lda / ldb / ldc padding (lda % 32 != 0, so a
+    scale block straddles two rows); padding columns of C untouched; mode 1
+    adds onto C."""
+    M, N, K, batch = 20, 24, 40, 3
+    lda, ldb, ldc = 44, 28, 30
+    sA, sB, sC = M * lda + 12, K * ldb + 8, M * ldc + 5
+    payload, scales, B = nn_inputs(oracle, M, N, K, 60, lda=lda, ldb=ldb, batch=batch, sA=sA, sB=sB)
+    C0 = oracle.normal(63, (batch - 1) * sC + M * ldc)
+    got = oracle.gemm_nn_q8_split(payload, scales, B, M, N, K, C=C0.copy(), lda=lda, ldb=ldb, ldc=ldc, batch=batch,
+                                  sA=sA, sB=sB, sC=sC)
+    acc = oracle.gemm_nn_q8_split(payload, scales, B, M, N, K, C=C0.copy(), mode=1, lda=lda, ldb=ldb, ldc=ldc,
+                                  batch=batch, sA=sA, sB=sB, sC=sC)
+    for z in range(batch):
+        g = got[z * sC: z * sC + M * ldc].reshape(M, ldc)
+        a = acc[z * sC: z * sC + M * ldc].reshape(M, ldc)
+        c0 = C0[z * sC: z * sC + M * ldc].reshape(M, ldc)
+        want = nn_numpy(payload, scales, B, M, N, K, lda=lda, ldb=ldb, z=z, sA=sA, sB=sB)
+        assert np.max(np.abs(g[:, :N] - want)) <= 1e-5 * np.max(np.abs(want))
+        assert np.array_equal(g[:, N:], c0[:, N:])
+        assert np.max(np.abs(a[:, :N] - c0[:, :N] - want)) <= 1e-5 * np.max(np.abs(want)) + 1e-6
+    assert np.array_equal(got[M * ldc: sC], C0[M * ldc: sC])
+
+
+def test_gemm_nn_linearity(oracle):
+    M, N, K = 16, 36, 64
+    payload, scales, B1 = nn_inputs(oracle, M, N, K, 70)
+    B2 = oracle.normal(74, K * N)
+    c1 = oracle.gemm_nn_q8_split(payload, scales, B1, M, N, K)
+    c2 = oracle.gemm_nn_q8_split(payload, scales, B2, M, N, K)
+    c12 = oracle.gemm_nn_q8_split(payload, scales, (2.0 * B1 - 3.0 * B2).astype(np.float32), M, N, K)
+    assert np.max(np.abs(c12 - (2.0 * c1 - 3.0 * c2))) <= 1e-5 * np.max(np.abs(c12))
