@@ -107,6 +107,36 @@ class AttnCase:
                                     stream=stream)
 
 
+# SDXL 1024^2 convolutions as the NN GEMM sees them after im2col (M = output
+# channels, N = pixels of a row chunk, K = cin * 9, or cin for a 1x1 shortcut)
+NN_SHAPES = [  # (tag, M, N, K)
+    ("L0 conv3x3 320 (4096 px chunk)", 320, 4096, 320 * 9),
+    ("L1 conv3x3 640 (64x64)", 640, 4096, 640 * 9),
+    ("L2 conv3x3 1280 (32x32)", 1280, 1024, 1280 * 9),
+    ("L2 conv1x1 640->1280 (32x32)", 1280, 1024, 640),
+]
+CONFIG0 = ("cfg0 gemm_q8_bench 9216x1280x1280", 9216, 1280, 1280)
+
+
+class NnCase:
+    """C[M,N] = deq(W)[M,K] . B[K,N]: Q8_0 weights N(0, 0.02^2) in the split layout, B N(0, 1)."""
+    kernel = "gemm_nn_q8"
+
+    def __init__(self, tag, M, N, K, rng, hip, ops):
+        self.tag, self.M, self.N, self.K = tag, M, N, K
+        self.ops = ops
+        blk = quantize_q8_0(rng.standard_normal(M * K, dtype=np.float32) * np.float32(0.02)).reshape(-1, 34)
+        self.Aq = hip.DeviceBuffer.from_array(np.ascontiguousarray(blk[:, 2:]).reshape(-1))
+        self.As = hip.DeviceBuffer.from_array(blk[:, :2].copy().view(np.float16).astype(np.float32).reshape(-1))
+        self.B = hip.DeviceBuffer.from_array(rng.standard_normal(K * N, dtype=np.float32))
+        self.C = hip.DeviceBuffer(M * N * 4)
+        self.flops = 2.0 * M * N * K
+        self.bytes = M * K * (1.0 + 4.0 / 32.0) + 4.0 * K * N + 4.0 * M * N
+
+    def run(self, stream):
+        self.ops.gemm_nn_q8(self.Aq, self.As, self.B, self.C, self.M, self.N, self.K, stream=stream)
+
+
 class BlockStack:
     """ten SDXL BasicTransformerBlocks at level 2 (1280
     channels, 2 x 1024 tokens, 20 heads, context 2 x 77 x 2048, FF 1280 ->
@@ -156,22 +186,86 @@ class BlockStack:
         for w in self.weights:
             self.ops.sdxl_block_forward(w, self.dims, self.x, self.ctx, self.ws, stream=stream)
 
-    def measure(self, stream, reps):
-        self.run(stream)
+    def run_cached(self, stream):
+        for w, kv in zip(self.weights, self.kv):
+            self.ops.sdxl_block_forward_kv(w, self.dims, self.x, kv, self.ws, stream=stream)
+
+    def measure(self, stream, reps, cached_kv=False):
+        """Latency of one pass over the stack; cached_kv: the context's K / V
+        projected once per block before timing (a sampling job does this once,
+        mi_block_ctx_kv) and every timed pass runs mi_sdxl_block_forward_kv."""
+        run = self.run
+        if cached_kv:
+            self.kv = []
+            for w in self.weights:
+                kv = self.hip.DeviceBuffer(self.ops.block_ctx_kv_bytes(self.dims))
+                self.ops.block_ctx_kv(w, self.dims, self.ctx, kv, stream=stream)
+                self.kv.append(kv)
+            run = self.run_cached
+        run(stream)
         stream.synchronize()
         a, b = self.hip.Event(), self.hip.Event()
         a.record(stream)
         for _ in range(reps):
-            self.run(stream)
+            run(stream)
         b.record(stream)
         b.synchronize()
         ms = a.elapsed_ms(b) / reps
         flops = self.flops_per_block * self.nblocks
+        if cached_kv:
+            B, T, C, H, Tc, Cc, F = self.DIMS
+            flops -= 2.0 * B * Tc * C * Cc * 2 * self.nblocks  # the K / V projections are not in the timed pass
         return {"config": "BASELINE config 4: %d SDXL BasicTransformerBlocks, level 2 (C=1280, 2x1024 tokens, "
                           "20 heads, ctx 2x77x2048, FF 1280->10240->5120->1280), Q8_0 weights, fp32 activations"
                           % self.nblocks,
                 "blocks": self.nblocks, "latency_ms": round(ms, 4), "ms_per_block": round(ms / self.nblocks, 4),
                 "gflop": round(flops / 1e9, 1), "tflops": round(flops / (ms / 1e3) / 1e12, 2), "reps": reps}
+
+
+def time_case(c, stream, hip, reps):
+    """Average launch time of `reps` back-to-back launches of case c (seconds) and its breakdown entry."""
+    c.run(stream)
+    a, b = hip.Event(), hip.Event()
+    a.record(stream)
+    for _ in range(reps):
+        c.run(stream)
+    b.record(stream)
+    b.synchronize()
+    sec = a.elapsed_ms(b) / 1e3 / reps
+    tf, roof, frac = roofline_pct(c, sec)
+    return sec, {"shape": c.tag, "kernel": c.kernel, "M_N_K": [c.M, c.N, c.K], "us": round(sec * 1e6, 2),
+                 "tflops": round(tf, 2), "pct_mfma_peak": round(100 * tf / PEAK_FP16_TFLOPS, 2),
+                 "roofline_tflops": round(roof, 1), "pct_of_roofline": round(100 * frac, 2),
+                 "gbs": round(c.bytes / sec / 1e9, 1)}
+
+
+def extras(rng, hip, ops, stream, reps, stack):
+    """Measurements outside the step metric (after the timed region): BASELINE
+    config 0 (the reference harness's GEMM shape), the NN GEMM at the SDXL conv
+    shapes, and the config-4 stack with the context's K / V cached. Each part
+    reports its error instead of stopping the bench."""
+    out = {}
+    try:
+        c = GemmCase(*CONFIG0, rng, hip, ops)
+        out["config0_gemm"] = time_case(c, stream, hip, reps)[1]
+        del c
+    except Exception as e:  # noqa: BLE001 -- reported, not fatal
+        out["config0_gemm"] = {"error": str(e)}
+    try:
+        nn = []
+        for t, M, N, K in NN_SHAPES:
+            c = NnCase(t, M, N, K, rng, hip, ops)
+            nn.append(time_case(c, stream, hip, reps)[1])
+            del c
+        out["nn_gemm"] = nn
+    except Exception as e:  # noqa: BLE001
+        out["nn_gemm"] = {"error": str(e)}
+    if stack is not None:
+        try:
+            out["block_stack_cached_kv"] = stack.measure(stream, 5, cached_kv=True)
+        except Exception as e:  # noqa: BLE001
+            out["block_stack_cached_kv"] = {"error": str(e)}
+    return out
 
 
 def roofline_pct(c, seconds):
@@ -341,12 +435,19 @@ def main() -> int:
                 "algorithmic_flop_per_launch": fam_flops[dom] / fam_launch[dom],
                 "algorithmic_bytes_per_launch": fam_bytes[dom] / fam_launch[dom]}
 
-    block = None
+    block, stack = None, None
     if args.only is None:
         print("[bench] config-4 block stack", file=sys.stderr, flush=True)
-        block = BlockStack(rng, hip, ops).measure(stream, 5)
+        stack = BlockStack(rng, hip, ops)
+        block = stack.measure(stream, 5)
         print(f"[bench] block stack: {block['latency_ms']:.3f} ms for {block['blocks']} blocks "
               f"({block['tflops']:.1f} TFLOP/s)", file=sys.stderr, flush=True)
+
+    more = None
+    if args.only is None:
+        print("[bench] extras: config 0, NN GEMM conv shapes, cached-K/V block stack", file=sys.stderr, flush=True)
+        more = extras(rng, hip, ops, stream, args.reps, stack)
+        del stack
 
     cpu = None
     if not args.no_cpu_baseline and args.only is None:
@@ -378,6 +479,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "block_stack": block,
         "breakdown": breakdown,
+        "extras": more,
     }
     print(json.dumps(out), flush=True)
     return 0
