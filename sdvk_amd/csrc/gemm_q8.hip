@@ -555,7 +555,37 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
 //     parity of the step, so the raw loads of step j + 2 are in flight while
 //     step j's MFMAs run and step j + 1 is dequantised / converted; one
 //     barrier per step.
-template <int FN, int WK, bool SPLITK>
+// 4 x 4 transpose of dwords across the four lanes of each quad: lane j's
+// register k becomes lane k's register j (two DPP quad-permute rounds: swap
+// across lane bit 1 / register bit 1, then across lane bit 0 / register bit 0).
+__device__ __forceinline__ void quad_transpose4(uint32_t (&e)[4], int lane) {
+    const bool b1 = (lane & 2) != 0, b0 = (lane & 1) != 0;
+    uint32_t r[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        // quad_perm [2,3,0,1]: lane j reads lane j ^ 2's register k ^ 2
+        const uint32_t x = static_cast<uint32_t>(
+            __builtin_amdgcn_mov_dpp(static_cast<int>(e[k ^ 2]), 0x4E, 0xF, 0xF, false));
+        r[k] = (b1 == ((k & 2) != 0)) ? e[k] : x;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        // quad_perm [1,0,3,2]: lane j reads lane j ^ 1's register k ^ 1
+        const uint32_t x = static_cast<uint32_t>(
+            __builtin_amdgcn_mov_dpp(static_cast<int>(r[k ^ 1]), 0xB1, 0xF, 0xF, false));
+        e[k] = (b0 == ((k & 1) != 0)) ? r[k] : x;
+    }
+}
+
+// AQ = false: a lane loads its own MFMA operand row (16-byte loads touching 64
+//   rows per instruction).
+// AQ = true: row-coalesced A. Load k (0..3) of a 32-row half gives lane 4Q + j
+//   row 4 (Q % 8) + k, 16-byte chunk 4 (Q / 8) + j of the step, so each
+//   instruction reads 8 whole 128-byte rows; a 4 x 4 quad transpose (after the
+//   fp16 conversion) then leaves lane l holding chunks 4 g .. 4 g + 3 of row
+//   l % 32 -- the same operand layout as AQ = false, so W, the MFMAs and the
+//   epilogue are shared.
+template <int FN, int WK, bool SPLITK, bool AQ = false>
 __global__ __launch_bounds__(256) void gemm_q8_rows_kernel(GemmArgs a) {
     constexpr int BM = 256, BN = 32 * FN, FM = 2, LDW = 40;  // LDW: 32 halves + 16-byte pad per column
     constexpr int kOperandHalves = 2 * BN * LDW;
@@ -590,11 +620,19 @@ __global__ __launch_bounds__(256) void gemm_q8_rows_kernel(GemmArgs a) {
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(WK == kSplit ? a.scales : a.A), 0, -1, 0x00020000);
 
     // A: rows past M read row M - 1 (their outputs are never stored)
-    uint32_t a_off[FM];
+    uint32_t a_off[FM][AQ ? 4 : 1];
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
-        const uint32_t row = min(m0 + 64 * wave + 32 * fm + l32, a.M - 1) - m0;
-        a_off[fm] = (row * a.lda + 16 * g) * 4;
+        if constexpr (AQ) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t row = min(m0 + 64 * wave + 32 * fm + 4 * ((lane >> 2) & 7) + k, a.M - 1) - m0;
+                a_off[fm][k] = (row * a.lda + 16 * g + 4 * (lane & 3)) * 4;
+            }
+        } else {
+            const uint32_t row = min(m0 + 64 * wave + 32 * fm + l32, a.M - 1) - m0;
+            a_off[fm][0] = (row * a.lda + 16 * g) * 4;
+        }
     }
     // W: column t = tid (tid < BN). 34-byte layout: the block of step ks
     // starts at byte wb + 34 ks; even steps read the window at
@@ -633,7 +671,8 @@ __global__ __launch_bounds__(256) void gemm_q8_rows_kernel(GemmArgs a) {
 #pragma unroll
             for (int q = 0; q < 4; ++q)
                 ar[p][fm][q] = __builtin_bit_cast(
-                    floatx4, __builtin_amdgcn_raw_buffer_load_b128(rA, a_off[fm] + 16 * q, ks * 128, 0));
+                    floatx4, __builtin_amdgcn_raw_buffer_load_b128(rA, AQ ? a_off[fm][q] : a_off[fm][0] + 16 * q,
+                                                                    ks * 128, 0));
         if (wlane) {
             if constexpr (WK == kBlocks34) {
                 const uint32_t so = 68u * (ks >> 1);
@@ -683,7 +722,26 @@ __global__ __launch_bounds__(256) void gemm_q8_rows_kernel(GemmArgs a) {
     auto cvt_a = [&](auto P) {
         constexpr int p = decltype(P)::value;
 #pragma unroll
-        for (int fm = 0; fm < FM; ++fm)
+        for (int fm = 0; fm < FM; ++fm) {
+            if constexpr (AQ) {
+                // fp16 pairs of the four loads, then the quad transpose of each dword
+                uint32_t d0[4], d1[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const floatx4 v = ar[p][fm][k];
+                    d0[k] = __builtin_bit_cast(uint32_t, half2{static_cast<_Float16>(v[0]), static_cast<_Float16>(v[1])});
+                    d1[k] = __builtin_bit_cast(uint32_t, half2{static_cast<_Float16>(v[2]), static_cast<_Float16>(v[3])});
+                }
+                quad_transpose4(d0, lane);
+                quad_transpose4(d1, lane);
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+                    af[p][fm][s] = __builtin_bit_cast(half8, u32x4{d0[2 * s], d1[2 * s], d0[2 * s + 1], d1[2 * s + 1]});
+                    asm volatile("" : "+v"(af[p][fm][s]));
+                }
+                continue;
+            }
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
                 const floatx4 lo = ar[p][fm][2 * s], hi = ar[p][fm][2 * s + 1];
@@ -695,6 +753,7 @@ __global__ __launch_bounds__(256) void gemm_q8_rows_kernel(GemmArgs a) {
                 // before the loads that refill them are issued
                 asm volatile("" : "+v"(af[p][fm][s]));
             }
+        }
     };
 
     floatx16 acc[FM][FN];
@@ -825,7 +884,7 @@ void launch_init(float* C, const float* bias, uint32_t M, uint32_t N, uint32_t l
 
 // Tile shapes (BM x BN, waves WM x WN, two 32-wide K blocks per step). The
 // 256x256 tile keeps one register set in flight (PF = 1) to stay within 256 VGPRs.
-enum CfgId { kC256x128 = 0, kC128x128, kC128x64, kC64x64, kC256x256, kR256x256, kR256x128, kNumCfg };
+enum CfgId { kC256x128 = 0, kC128x128, kC128x64, kC64x64, kC256x256, kR256x256, kR256x128, kR256x256Q, kNumCfg };
 
 // Group height for the tile order: the XCD chunks (blocks b with b % 8 == x,
 // contiguous in the grouped order) each read the A panels of the rows and the
@@ -900,7 +959,7 @@ void launch_cfg(const GemmArgs& a0, uint32_t batch, uint32_t splits, hipStream_t
 
 // Row-stationary kernel: 256 x (32 FN) tiles, K % 32 == 0. A K split covers an
 // even number of 32-wide steps.
-template <int FN, int WK>
+template <int FN, int WK, bool AQ = false>
 void launch_rows(const GemmArgs& a0, uint32_t batch, uint32_t splits, hipStream_t s) {
     GemmArgs a = a0;
     constexpr uint32_t BM = 256, BN = 32 * FN;
@@ -915,10 +974,10 @@ void launch_rows(const GemmArgs& a0, uint32_t batch, uint32_t splits, hipStream_
     }
     if (splits > 1) {
         if (a.mode == 0) launch_init(a.C, a.bias, a.M, a.N, a.ldc, a.sC, batch, s);
-        gemm_q8_rows_kernel<FN, WK, true><<<dim3(tiles, splits, batch), 256, 0, s>>>(a);
+        gemm_q8_rows_kernel<FN, WK, true, AQ><<<dim3(tiles, splits, batch), 256, 0, s>>>(a);
     } else {
         a.steps_per_split = a.ksteps;
-        gemm_q8_rows_kernel<FN, WK, false><<<dim3(tiles, 1, batch), 256, 0, s>>>(a);
+        gemm_q8_rows_kernel<FN, WK, false, AQ><<<dim3(tiles, 1, batch), 256, 0, s>>>(a);
     }
 }
 
@@ -926,6 +985,7 @@ template <int WK>
 void launch(int cfg, const GemmArgs& a, uint32_t batch, uint32_t splits, hipStream_t s) {
     switch (cfg) {
         case kR256x256: launch_rows<8, WK>(a, batch, splits, s); break;
+        case kR256x256Q: launch_rows<8, WK, true>(a, batch, splits, s); break;
         case kR256x128: launch_rows<4, WK>(a, batch, splits, s); break;
         case kC256x128: launch_cfg<256, 128, 4, 2, 2, WK, false>(a, batch, splits, s); break;
         case kC128x128: launch_cfg<128, 128, 2, 2, 2, WK, false>(a, batch, splits, s); break;
