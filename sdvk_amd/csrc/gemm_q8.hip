@@ -548,9 +548,10 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
 //     k = 16 g + 8 s .. + 8, applied to both operands), so a lane's 16 values
 //     of a step are contiguous: four 16-byte loads per 32 rows, and the two
 //     halves of a wave cover one 128-byte line per row.
-//   * W is read once per workgroup: thread t < BN dequantises column t's
-//     Q8_0 block of the step (a 36-byte window, three loads) into LDS, where
-//     the four waves read their operand fragments.
+//   * W is read once per workgroup: thread t dequantises column n0 + t's
+//     Q8_0 block of the step (a 36-byte window, three loads) into LDS row t,
+//     where the four waves read their operand fragments (rows >= BN are
+//     staged but never read, so the loop has no thread-dependent branch).
 //   * Steps alternate between two register sets and two LDS stages by the
 //     parity of the step, so the raw loads of step j + 2 are in flight while
 //     step j's MFMAs run and step j + 1 is dequantised / converted; one
@@ -588,10 +589,12 @@ __device__ __forceinline__ void quad_transpose4(uint32_t (&e)[4], int lane) {
 template <int FN, int WK, bool SPLITK, bool AQ = false>
 __global__ __launch_bounds__(256) void gemm_q8_rows_kernel(GemmArgs a) {
     constexpr int BM = 256, BN = 32 * FN, FM = 2, LDW = 40;  // LDW: 32 halves + 16-byte pad per column
-    constexpr int kOperandHalves = 2 * BN * LDW;
+    // every thread stages one W column (threads t >= BN a clamped column into
+    // LDS rows no wave reads), so the K loop has no thread-dependent branch
+    constexpr int kOperandHalves = 2 * 256 * LDW;
     constexpr int kStageHalves = 2 * 4 * kStageFloats;
     __shared__ __attribute__((aligned(16))) _Float16 smem[kOperandHalves > kStageHalves ? kOperandHalves : kStageHalves];
-    auto Ws = reinterpret_cast<_Float16 (*)[BN * LDW]>(smem);
+    auto Ws = reinterpret_cast<_Float16 (*)[256 * LDW]>(smem);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -634,12 +637,11 @@ __global__ __launch_bounds__(256) void gemm_q8_rows_kernel(GemmArgs a) {
             a_off[fm][0] = (row * a.lda + 16 * g) * 4;
         }
     }
-    // W: column t = tid (tid < BN). 34-byte layout: the block of step ks
+    // W: column n0 + tid (clamped to N - 1). 34-byte layout: the block of step ks
     // starts at byte wb + 34 ks; even steps read the window at
     // (wb & ~3) + 68 (ks / 2), odd steps at ((wb + 34) & ~3) + 68 (ks / 2), and
     // the block sits 0 or 2 bytes into its window (v_perm selectors per parity).
-    const bool wlane = BN == 256 || tid < BN;
-    const uint32_t wn = min(n0 + static_cast<uint32_t>(tid % BN), a.N - 1);
+    const uint32_t wn = min(n0 + static_cast<uint32_t>(tid), a.N - 1);
     uint32_t w_vo[2], w_qsel[2], w_dsel[2];
     if constexpr (WK == kBlocks34) {
         const uint32_t wb = wn * a.rowbytes;
@@ -673,7 +675,7 @@ __global__ __launch_bounds__(256) void gemm_q8_rows_kernel(GemmArgs a) {
                 ar[p][fm][q] = __builtin_bit_cast(
                     floatx4, __builtin_amdgcn_raw_buffer_load_b128(rA, AQ ? a_off[fm][q] : a_off[fm][0] + 16 * q,
                                                                     ks * 128, 0));
-        if (wlane) {
+        {
             if constexpr (WK == kBlocks34) {
                 const uint32_t so = 68u * (ks >> 1);
                 const auto x0 = __builtin_amdgcn_raw_buffer_load_b128(rW, w_vo[p], so, 0);
@@ -700,8 +702,7 @@ __global__ __launch_bounds__(256) void gemm_q8_rows_kernel(GemmArgs a) {
     // dequantise the W block of set p into LDS stage p
     auto store_w = [&](auto P) {
         constexpr int p = decltype(P)::value;
-        if (!wlane) return;
-        _Float16* dst = &Ws[p][(tid % BN) * LDW];
+        _Float16* dst = &Ws[p][tid * LDW];
         if constexpr (WK == kBlocks34) {
             const uint32_t* x = wx[p];
             const _Float16 d = __builtin_bit_cast(
@@ -884,7 +885,12 @@ void launch_init(float* C, const float* bias, uint32_t M, uint32_t N, uint32_t l
 
 // Tile shapes (BM x BN, waves WM x WN, two 32-wide K blocks per step). The
 // 256x256 tile keeps one register set in flight (PF = 1) to stay within 256 VGPRs.
-enum CfgId { kC256x128 = 0, kC128x128, kC128x64, kC64x64, kC256x256, kR256x256, kR256x128, kR256x256Q, kNumCfg };
+enum CfgId {
+    kC256x128 = 0, kC128x128, kC128x64, kC64x64, kC256x256,  // LDS kernel (gemm_q8_kernel)
+    kR256x256, kR256x128,                                     // row kernel, per-lane-row A loads
+    kR256x256Q, kR256x192Q, kR256x160Q, kR256x128Q,           // row kernel, row-coalesced A
+    kNumCfg
+};
 
 // Group height for the tile order: the XCD chunks (blocks b with b % 8 == x,
 // contiguous in the grouped order) each read the A panels of the rows and the
@@ -986,6 +992,9 @@ void launch(int cfg, const GemmArgs& a, uint32_t batch, uint32_t splits, hipStre
     switch (cfg) {
         case kR256x256: launch_rows<8, WK>(a, batch, splits, s); break;
         case kR256x256Q: launch_rows<8, WK, true>(a, batch, splits, s); break;
+        case kR256x192Q: launch_rows<6, WK, true>(a, batch, splits, s); break;
+        case kR256x160Q: launch_rows<5, WK, true>(a, batch, splits, s); break;
+        case kR256x128Q: launch_rows<4, WK, true>(a, batch, splits, s); break;
         case kR256x128: launch_rows<4, WK>(a, batch, splits, s); break;
         case kC256x128: launch_cfg<256, 128, 4, 2, 2, WK, false>(a, batch, splits, s); break;
         case kC128x128: launch_cfg<128, 128, 2, 2, 2, WK, false>(a, batch, splits, s); break;

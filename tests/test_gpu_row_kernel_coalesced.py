@@ -1,6 +1,6 @@
 """GPU parity of the row-stationary Q8_0 GEMM with row-coalesced A loads and
-the quad transpose (MI_GEMM_CFG=7; not chosen by the tile rules until it is
-measured faster), against the CPU oracle: the same bar and cases as the other
+the quad transpose (MI_GEMM_CFG=7..10: 256 x 256 / 192 / 160 / 128 tiles; not
+chosen by the tile rules until measured faster), against the CPU oracle: the same bar and cases as the other
 tile configurations (tests/test_gpu_gemm.py)."""
 import numpy as np
 import pytest
@@ -13,7 +13,7 @@ from test_gpu_gemm import run_q8_0
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("cfg", ["7", "7:2"])
+@pytest.mark.parametrize("cfg", ["7", "7:2", "8", "9:3", "10"])  # 256x256, 256x192, 256x160, 256x128
 @pytest.mark.parametrize("M,N,K", [(300, 200, 640), (1030, 130, 256), (257, 512, 128)])
 def test_coalesced_rows_config(gpu, oracle, monkeypatch, cfg, M, N, K):
     print(f"[case] cfg={cfg} M={M} N={N} K={K}", flush=True)
