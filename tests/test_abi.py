@@ -4,6 +4,7 @@ import ctypes
 import re
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 from sdvk_amd import _lib, ops
@@ -95,3 +96,45 @@ def test_python_mirror_raises_mi_error():
         ops.dispatch("gemm_nt_q8_v_b", [1, 2, 3, 4], ops.Pg(8, 8, 32))  # 5 bindings expected
     with pytest.raises(ValueError):
         ops.dispatch("no_such_kernel", [], None)
+
+
+def test_c_and_cpp_callers_link_and_run(tmp_path):
+    """include/mi_sdvk.h compiles as C99 and C++17, and a C++ program linked
+    against libmi_sdvk.so makes the host-side calls (no GPU work): status text,
+    argument rejection through the return value, the GGUF reader."""
+    import shutil
+    import subprocess
+    import sys
+
+    sys.path.insert(0, str(Path(__file__).resolve().parent))
+    import gguf_writer as gw
+    from sdvk_amd.gguf import GgufFile
+
+    if not shutil.which("gcc") or not shutil.which("g++"):
+        pytest.skip("no host C/C++ compiler")
+    here = Path(__file__).resolve().parent / "cabi"
+    inc = HEADER.parent
+    lib = Path(_lib.LIB_PATH)
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-c", str(here / "abi_c.c"), f"-I{inc}", "-o",
+                    str(tmp_path / "abi_c.o")], check=True)
+    exe = tmp_path / "abi_host"
+    subprocess.run(["g++", "-std=c++17", "-Wall", "-Werror", str(here / "abi_host.cpp"), f"-I{inc}", str(lib),
+                    f"-Wl,-rpath,{lib.parent}", "-o", str(exe)], check=True)
+    sample = tmp_path / "sample.gguf"
+    gw.write(sample, gw.sample_spec())
+    out = subprocess.run([str(exe), str(sample), gw.PREFIX], check=True, capture_output=True, text=True).stdout
+    lines = dict(l.split(" ", 1) for l in out.strip().splitlines() if not l.startswith("tensor "))
+    assert lines["status2"] == "unsupported shape"
+    assert lines["null_gemm"] == f"{_lib.MI_ERR_INVALID_ARG} reason"
+    assert lines["attn_supported"] == "1 0"
+    assert lines["open"] == "0" and lines["arch"] == "sdxl"
+    assert lines["find_missing"] == str(_lib.MI_ERR_NOT_FOUND)
+    g = GgufFile()
+    assert g.open(str(sample), [], gw.PREFIX)
+    tens = [l.split() for l in out.splitlines() if l.startswith("tensor ")]
+    assert [t[1] for t in tens] == [t.name for t in g.tensors()]
+    for row, t in zip(tens, g.tensors()):
+        assert (int(row[2]), int(row[3]), int(row[4]), int(row[5])) == (t.type, t.nbytes, t.rows, t.cols)
+        f = g.readFloat(t.name, [])
+        want = float(np.sum(f[np.isfinite(f)], dtype=np.float64)) if f.size else 0.0
+        assert abs(float(row[6]) - want) <= 1e-6 * max(1.0, abs(want))
