@@ -172,6 +172,9 @@ __device__ __forceinline__ void store_tiles(const GemmArgs& a, float* C, float* 
                             floatx4{acc[fm][fn][4 * q], acc[fm][fn][4 * q + 1], acc[fm][fn][4 * q + 2],
                                     acc[fm][fn][4 * q + 3]};
                 }
+        // the staged tile is read back by other lanes of the wave: keep every
+        // write of the wave ahead of every read (no instruction is emitted)
+        __builtin_amdgcn_wave_barrier();
         const uint32_t mb = mw + 32 * (b / FN), nb = nw + 32 * (b % FN);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -200,6 +203,8 @@ __device__ __forceinline__ void store_tiles(const GemmArgs& a, float* C, float* 
                 }
             }
         }
+        // every read of this tile precedes the next tile's writes
+        __builtin_amdgcn_wave_barrier();
     }
 }
 
