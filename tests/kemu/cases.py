@@ -1,0 +1,260 @@
+"""Cases run on the kernel emulator, one child process per case (a fault in
+an emulated kernel ends that process with the emulator's report, not the
+test session).
+
+    python tests/kemu/cases.py '<json: {"case": name, ...params}>'
+
+Each case calls the emulation build of the C-ABI on guarded buffers and
+compares with the CPU oracle to the same bar as the GPU parity tests; it
+also checks that nothing outside the logical output changed (padding
+columns, batch gaps). Test infrastructure only.
+"""
+from __future__ import annotations
+
+import json
+import os
+import sys
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+sys.path.insert(0, str(HERE.parent))     # tests/ (helpers)
+sys.path.insert(0, str(HERE))
+
+import ctypes  # noqa: E402
+
+import emu as kemu  # noqa: E402
+from helpers import assert_parity, fp16_half_ulp, q8_weights, rms  # noqa: E402
+from oracle import binding as ob  # noqa: E402
+from sdvk_amd._lib import MI_F16, MI_F32, MiAttnArgs, MiBlockDims, MiBlockWeights  # noqa: E402
+from test_gpu_block import BLOCK_TOL, make_weights  # noqa: E402
+import gguf_writer as gw  # noqa: E402
+from sdvk_amd._lib import MiGgufTensorInfo  # noqa: E402
+
+SENTINEL = np.float32(12345.0)
+
+
+def _set_cfg(cfg):
+    if cfg is None:
+        os.environ.pop("MI_GEMM_CFG", None)
+    else:
+        os.environ["MI_GEMM_CFG"] = str(cfg)
+
+
+def _logical_mask(M, N, ldc, batch, sC, size):
+    mask = np.zeros(size, dtype=bool)
+    for z in range(batch):
+        for m in range(M):
+            s = z * sC + m * ldc
+            mask[s:s + N] = True
+    return mask
+
+
+def gemm_nt(E, *, M, N, K, layout="q8_0", cfg=None, mode=0, bias=True, batch=1, lda=0, ldc=0, sA=0, sC=0,
+            seed=1, front=False, order=0, tol=2e-3):
+    """mi_gemm_nt_q8_0 / mi_gemm_nt_q8_split against the oracle."""
+    _set_cfg(cfg)
+    E.order(order)
+    lda_e, ldc_e = lda or K, ldc or N
+    a_el = (batch - 1) * sA + (M - 1) * lda_e + K
+    c_el = (batch - 1) * sC + (M - 1) * ldc_e + N
+    A = ob.normal(seed, a_el)
+    blocks = q8_weights(ob, seed + 1, N, K)
+    b = ob.normal(seed + 2, N, 0.0, 0.02) if bias else None
+    C0 = ob.normal(seed + 3, c_el) if mode == 1 else np.full(c_el, SENTINEL, dtype=np.float32)
+    dA, dC = E.buf(A, front=front), E.buf(C0, front=front)
+    dB = E.buf(b, front=front) if bias else None
+    if layout == "q8_0":
+        dW = E.buf(blocks, front=front)
+        E.call("mi_gemm_nt_q8_0", dA.ptr, dW.ptr, dB.ptr if dB else None, dC.ptr, M, N, K, mode, lda, ldc, batch,
+               sA, sC, None)
+        want = ob.gemm_nt_q8_0(A, blocks, M, N, K, bias=b, C=C0.copy(), mode=mode, lda=lda, ldc=ldc, batch=batch,
+                               sA=sA, sC=sC, threads=ob.max_threads())
+    else:
+        payload, scales = ob.q8_0_to_split(blocks, N * K)
+        dP, dS = E.buf(payload, front=front), E.buf(scales, front=front)
+        E.call("mi_gemm_nt_q8_split", dA.ptr, dP.ptr, dS.ptr, dB.ptr if dB else None, dC.ptr, M, N, K, mode, lda,
+               ldc, batch, sA, sC, None)
+        want = ob.gemm_nt_q8_split(A, payload, scales, M, N, K, bias=b, C=C0.copy(), mode=mode, lda=lda, ldc=ldc,
+                                   batch=batch, sA=sA, sC=sC, threads=ob.max_threads())
+    got = dC.get(np.float32, c_el)
+    mask = _logical_mask(M, N, ldc_e, batch, sC, c_el)
+    assert np.array_equal(got[~mask], C0[~mask]), "elements outside the logical output changed"
+    if mode == 1:
+        return assert_parity(got[mask] - C0[mask], want[mask] - C0[mask], tol=tol, what="gemm_nt mode 1")
+    return assert_parity(got[mask], want[mask], tol=tol, what="gemm_nt")
+
+
+def gemm_nn(E, *, M, N, K, mode=0, batch=1, lda=0, ldb=0, ldc=0, sA=0, sB=0, sC=0, seed=1, front=False,
+            order=0, tol=2e-3):
+    """mi_gemm_nn_q8_split against the oracle (flat-index scales)."""
+    E.order(order)
+    lda_e, ldb_e, ldc_e = lda or K, ldb or N, ldc or N
+    a_el = (batch - 1) * sA + (M - 1) * lda_e + K
+    b_el = (batch - 1) * sB + (K - 1) * ldb_e + N if K else N
+    c_el = (batch - 1) * sC + (M - 1) * ldc_e + N
+    n_a = (a_el + 31) // 32 * 32
+    w = ob.normal(seed, n_a, 0.0, 0.02)
+    payload, scales = ob.q8_0_to_split(ob.q8_0_quantize(w), n_a)
+    payload = payload.view(np.uint8)[:a_el]
+    payload = np.concatenate([payload, np.zeros((-a_el) % 4, np.uint8)]).view(np.uint32)
+    scales = scales[: (a_el + 31) // 32]
+    B = ob.normal(seed + 1, b_el)
+    C0 = ob.normal(seed + 3, c_el) if mode == 1 else np.full(c_el, SENTINEL, dtype=np.float32)
+    dP, dS, dB, dC = (E.buf(payload, front=front), E.buf(scales, front=front), E.buf(B, front=front),
+                      E.buf(C0, front=front))
+    E.call("mi_gemm_nn_q8_split", dP.ptr, dS.ptr, dB.ptr, dC.ptr, M, N, K, mode, lda, ldb, ldc, batch, sA, sB, sC,
+           None)
+    want = ob.gemm_nn_q8_split(payload, scales, B, M, N, K, C=C0.copy(), mode=mode, lda=lda, ldb=ldb, ldc=ldc,
+                               batch=batch, sA=sA, sB=sB, sC=sC, threads=ob.max_threads())
+    got = dC.get(np.float32, c_el)
+    mask = _logical_mask(M, N, ldc_e, batch, sC, c_el)
+    assert np.array_equal(got[~mask], C0[~mask]), "elements outside the logical output changed"
+    if mode == 1:
+        return assert_parity(got[mask] - C0[mask], want[mask] - C0[mask], tol=tol, what="gemm_nn mode 1")
+    return assert_parity(got[mask], want[mask], tol=tol, what="gemm_nn")
+
+
+def attention(E, *, batch=1, Tq, Tk, C, heads, causal=False, f16_in=False, f16_out=False, kv_len=None, seed=1,
+              front=False, order=0, tol=2e-3):
+    """mi_fused_attention_ex (contiguous [batch, T, C]) against the oracle."""
+    E.order(order)
+    idt = np.float16 if f16_in else np.float32
+    q = ob.normal(seed, batch * Tq * C).astype(idt)
+    k = ob.normal(seed + 1, batch * Tk * C).astype(idt)
+    v = ob.normal(seed + 2, batch * Tk * C).astype(idt)
+    odt = np.float16 if f16_out else np.float32
+    n_out = batch * Tq * C
+    dq, dk, dv = E.buf(q, front=front), E.buf(k, front=front), E.buf(v, front=front)
+    do = E.buf(np.full(n_out, 7.0, dtype=odt), front=front)
+    dl = E.buf(np.asarray(kv_len, dtype=np.int32), front=front) if kv_len is not None else None
+    x = MiAttnArgs(q=dq.ptr, k=dk.ptr, v=dv.ptr, out=do.ptr, batch=batch, Tq=Tq, Tk=Tk, C=C, heads=heads,
+                   causal=1 if causal else 0, in_dtype=MI_F16 if f16_in else MI_F32,
+                   out_dtype=MI_F16 if f16_out else MI_F32, kv_len=dl.ptr if dl else None)
+    E.call("mi_fused_attention_ex", ctypes.byref(x), None)
+    got = do.get(odt, n_out).astype(np.float64)
+    want = ob.fused_attention_ex(q, k, v, batch=batch, Tq=Tq, Tk=Tk, C=C, heads=heads, causal=causal,
+                                 in_dtype=ob.OR_F16 if f16_in else ob.OR_F32, out_dtype=ob.OR_F32, kv_len=kv_len,
+                                 threads=ob.max_threads()).reshape(-1).astype(np.float64)
+    assert np.all(np.isfinite(got)), "attention: non-finite output"
+    if f16_out:
+        bound = tol * rms(want) + fp16_half_ulp(want)
+        assert np.all(np.abs(got - want) <= bound), "attention: fp16 output beyond tol x RMS + half an ulp"
+        return float(np.max(np.abs(got - want)) / rms(want))
+    return assert_parity(got, want, tol=tol, what="attention")
+
+
+def block(E, *, B, T, C, H, Tc, Cc, F, masked=False, blocks=2, order=0, front=False):
+    """Two applications of one SDXL transformer block: uncached
+    (mi_sdxl_block_forward) vs context K / V projected once (mi_block_ctx_kv,
+    mi_sdxl_block_forward_kv), both against the oracle's block."""
+    E.order(order)
+    w = make_weights(ob, C, Cc, F, seed=500)
+    dw = {k: E.buf(v, front=front) for k, v in w.items()}
+    bw = MiBlockWeights(*[dw[f[0]].ptr for f in MiBlockWeights._fields_])
+    dims = MiBlockDims(B, T, C, H, Tc, Cc, F)
+    x = ob.normal(3, B * T * C)
+    ctx = ob.normal(4, B * Tc * Cc).astype(np.float16).astype(np.float32)
+    kl = ob.uniform_int(8, 1, Tc, B) if masked else None
+    dc = E.buf(ctx, front=front)
+    dl = E.buf(np.asarray(kl, np.int32), front=front) if kl is not None else None
+    ws_bytes = E.lib.mi_block_workspace_bytes(ctypes.byref(dims))
+    kv_bytes = E.lib.mi_block_ctx_kv_bytes(ctypes.byref(dims))
+    ws, kv = E.buf(nbytes=ws_bytes, front=front).fill(0xFF), E.buf(nbytes=kv_bytes, front=front).fill(0xFF)
+    dx_fresh, dx_cached = E.buf(x, front=front), E.buf(x, front=front)
+    for _ in range(blocks):
+        E.call("mi_sdxl_block_forward", ctypes.byref(bw), ctypes.byref(dims), dx_fresh.ptr, dc.ptr,
+               dl.ptr if dl else None, ws.ptr, ws_bytes, None)
+    E.call("mi_block_ctx_kv", ctypes.byref(bw), ctypes.byref(dims), dc.ptr, kv.ptr, kv_bytes, None)
+    for _ in range(blocks):
+        E.call("mi_sdxl_block_forward_kv", ctypes.byref(bw), ctypes.byref(dims), dx_cached.ptr, kv.ptr, kv_bytes,
+               dl.ptr if dl else None, ws.ptr, ws_bytes, None)
+    fresh, cached = dx_fresh.get(np.float32), dx_cached.get(np.float32)
+    want = x
+    for _ in range(blocks):
+        want = ob.sdxl_block(w, want, ctx, batch=B, tokens=T, channels=C, heads=H, ctx_tokens=Tc, ctx_channels=Cc,
+                             ff_inner=F, ctx_len=kl, threads=ob.max_threads())
+    assert np.all(np.isfinite(cached)) and np.all(np.isfinite(fresh)), "block: non-finite output"
+    e_kv = float(np.max(np.abs(cached - fresh)) / rms(fresh - x))
+    assert e_kv <= 1e-5, f"cached vs fresh K / V: {e_kv:.3e} x RMS(update)"
+    e = float(np.max(np.abs(fresh - want)) / rms(want - x))
+    assert e <= blocks * BLOCK_TOL, f"block vs oracle: {e:.3e} x RMS(update)"
+    return e
+
+
+def gguf_upload(E, *, big_rows=10240, big_cols=1280, order=0, front=False):
+    """mi_gguf_upload_raw / _f32 / _q8_split of every tensor of the sample
+    checkpoint plus a Q8_0 weight that crosses the 8 MiB staging buffers
+    several times, each into a guarded buffer of exactly the tensor's size,
+    against the host readers (mi_gguf_read_*, whose parity with the
+    reference's Gguf.cpp is tests/test_gguf.py). Copies run deferred, so a
+    staging buffer refilled before its copy was waited for is caught."""
+    import tempfile
+    E.order(order)
+    blocks = ob.q8_0_quantize(ob.normal(5, big_rows * big_cols, 0.0, 0.02))
+    spec = gw.sample_spec()
+    spec.tensors.append(gw.Tensor(gw.PREFIX + "big.weight", (big_cols, big_rows), gw.T_Q8_0, blocks.tobytes()))
+    with tempfile.TemporaryDirectory() as d:
+        path = Path(d) / "sample.gguf"
+        gw.write(path, spec)
+        h = ctypes.c_void_p()
+        E.call("mi_gguf_open", str(path).encode(), gw.PREFIX.encode(), ctypes.byref(h))
+        ver, n, off, size = ctypes.c_uint32(), ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
+        E.call("mi_gguf_info", h, ctypes.byref(ver), ctypes.byref(n), ctypes.byref(off), ctypes.byref(size))
+        checked, big_seen = 0, False
+        for i in range(n.value):
+            t = MiGgufTensorInfo()
+            E.call("mi_gguf_tensor", h, i, ctypes.byref(t))
+            raw = np.zeros(max(t.nbytes, 1), np.uint8)
+            E.call("mi_gguf_read_raw", h, i, raw.ctypes.data, t.nbytes)
+            d_raw = E.buf(nbytes=t.nbytes, front=front).fill(0xA5)
+            E.call("mi_gguf_upload_raw", h, i, d_raw.ptr, t.nbytes, None)
+            if E.status("mi_gguf_read_f32", h, i, None, 0) != 2:  # decodable type
+                host = np.zeros(max(t.n_elems, 1), np.float32)
+                E.call("mi_gguf_read_f32", h, i, host.ctypes.data, t.n_elems)
+                d_f = E.buf(nbytes=t.n_elems * 4, front=front).fill(0xA5)
+                E.call("mi_gguf_upload_f32", h, i, d_f.ptr, t.n_elems, None)
+            else:
+                d_f = None
+            q8 = t.type == gw.T_Q8_0
+            if q8:
+                nb = t.n_elems // 32
+                hq, hs = np.zeros(nb * 32, np.int8), np.zeros(nb, np.float32)
+                E.call("mi_gguf_read_q8_split", h, i, hq.ctypes.data, hs.ctypes.data)
+                d_q = E.buf(nbytes=nb * 32, front=front).fill(0xA5)
+                d_s = E.buf(nbytes=nb * 4, front=front).fill(0xA5)
+                E.call("mi_gguf_upload_q8_split", h, i, d_q.ptr, d_s.ptr, None)
+            E.lib.kemu_sync()
+            name = t.name.decode()
+            assert np.array_equal(d_raw.get(np.uint8, t.nbytes), raw[: t.nbytes]), f"upload_raw {name}"
+            if d_f is not None:
+                assert np.array_equal(d_f.get(np.uint32, t.n_elems), host[: t.n_elems].view(np.uint32)), \
+                    f"upload_f32 {name}"
+            if q8:
+                assert np.array_equal(d_q.get(np.int8, nb * 32), hq), f"upload_q8_split payload {name}"
+                assert np.array_equal(d_s.get(np.uint32, nb), hs.view(np.uint32)), f"upload_q8_split scales {name}"
+            checked += 1
+            big_seen |= name == "big.weight" and t.nbytes == blocks.nbytes
+        E.lib.mi_gguf_close(h)
+    assert checked == n.value and checked >= 3 and big_seen
+    return 0.0
+
+
+CASES = {"gemm_nt": gemm_nt, "gemm_nn": gemm_nn, "attention": attention, "block": block, "gguf_upload": gguf_upload}
+
+
+def main(argv):
+    spec = json.loads(argv[1])
+    name = spec.pop("case")
+    schedules = spec.pop("schedules", [spec.pop("order", 0)])
+    E = kemu.Emu()
+    ob.build()
+    for order in schedules:
+        e = CASES[name](E, order=order, **spec)
+        print(f"OK {name} order={order} err/rms={e:.3e} launches={E.lib.kemu_launches()}", flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main(sys.argv))

@@ -1,0 +1,169 @@
+"""CPU checks of the HIP kernels on the kernel emulator (tests/kemu).
+
+The product's .hip sources are compiled for the host against an emulation of
+the gfx950 builtins they use (wave-wide MFMA / DPP / transposing LDS reads as
+64-lane rendezvous, range-checked buffer resources, LDS filled with NaN
+before every workgroup, deferred asynchronous copies) and called through the
+same C-ABI. Every case compares with the CPU oracle to the GPU tests' bar,
+checks that nothing outside the logical output changed, runs on buffers that
+end at a PROT_NONE page (an out-of-bounds access faults and names the
+kernel, workgroup and work-item), and runs under two schedules: one
+wave operation per wave per pass, and wave-major with lanes and waves
+reversed, so a missing barrier changes the result under one of them.
+
+This is where paths are checked before they reach a GPU (the coalesced-A row
+kernel configurations, the NN GEMM, the cached-K/V block, the GGUF uploads);
+it does not measure anything and nothing in the product loads the emulation
+build. test_emulator_catches_planted_faults pins the checker itself: copies
+of the sources with one planted mistake each (compiled for the host only)
+must fail.
+"""
+from __future__ import annotations
+
+import json
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+import pytest
+
+HERE = Path(__file__).resolve().parent
+KEMU = HERE / "kemu"
+ROOT = HERE.parent
+CSRC = ROOT / "sdvk_amd" / "csrc"
+BOTH = [0, 7]  # interleaved; wave-major with lanes and waves reversed
+
+FAMILIES = {
+    # LDS-tiled kernel through the shape rules (choose), every tile config,
+    # K splits, the general-K path, both weight layouts, batch / strides
+    "gemm_lds": [
+        dict(M=1, N=1, K=32), dict(M=77, N=96, K=64), dict(M=100, N=100, K=96),
+        dict(M=130, N=257, K=320), dict(M=130, N=257, K=320, mode=1), dict(M=154, N=96, K=2048),
+        dict(M=60, N=40, K=100, layout="split"), dict(M=77, N=96, K=64, layout="split", mode=1),
+        dict(M=300, N=300, K=256, cfg="0"), dict(M=300, N=200, K=256, cfg="1", layout="split"),
+        dict(M=130, N=100, K=128, cfg="2"), dict(M=70, N=70, K=128, cfg="3", front=True),
+        dict(M=300, N=300, K=256, cfg="4"), dict(M=200, N=300, K=512, cfg="0:3"),
+        dict(M=70, N=36, K=64, batch=3, lda=72, ldc=40, sA=5200, sC=3000),
+        dict(M=70, N=36, K=128, batch=2, lda=132, ldc=40, sA=9300, sC=3000, cfg="4:2", mode=1),
+    ],
+    # row-stationary kernel: per-lane-row A (5, 6) and row-coalesced A (7-10)
+    "gemm_rows": [
+        dict(M=300, N=200, K=256, cfg="5"), dict(M=77, N=96, K=64, cfg="6"),
+        dict(M=300, N=200, K=256, cfg="7"), dict(M=154, N=300, K=256, cfg="7:2"),
+        dict(M=300, N=200, K=128, cfg="8"), dict(M=154, N=300, K=256, cfg="9:3", layout="split"),
+        dict(M=300, N=200, K=128, cfg="10", mode=1), dict(M=260, N=130, K=192, cfg="7", front=True),
+        dict(M=70, N=36, K=128, batch=2, lda=132, ldc=40, sA=9300, sC=3000, cfg="8"),
+        dict(M=70, N=36, K=256, batch=2, lda=260, ldc=40, sA=18300, sC=3000, cfg="10:2", layout="split"),
+    ],
+    "gemm_nn": [
+        dict(M=64, N=64, K=32), dict(M=100, N=72, K=96), dict(M=130, N=260, K=100, mode=1),
+        dict(M=60, N=36, K=44, batch=3, lda=48, ldb=40, ldc=44, sA=3000, sB=1800, sC=2800),
+        dict(M=5, N=4, K=4), dict(M=64, N=64, K=0), dict(M=64, N=64, K=0, mode=1),
+        dict(M=33, N=68, K=36, front=True),
+    ],
+    "attention": [
+        dict(Tq=100, Tk=300, C=128, heads=2), dict(Tq=100, Tk=300, C=128, heads=2, causal=True),
+        dict(Tq=1, Tk=1, C=64, heads=1), dict(Tq=50, Tk=100, C=40, heads=1),
+        dict(batch=2, Tq=70, Tk=77, C=640, heads=10, f16_in=True, f16_out=True, kv_len=[77, 40]),
+        dict(batch=2, Tq=130, Tk=200, C=128, heads=2, f16_in=True, f16_out=True, causal=True),
+        dict(batch=2, Tq=33, Tk=70, C=320, heads=5, f16_in=True, f16_out=False, kv_len=[1, 70]),
+    ],
+    "block": [
+        dict(B=1, T=33, C=64, H=1, Tc=5, Cc=96, F=160),
+        dict(B=2, T=64, C=128, H=2, Tc=77, Cc=256, F=256, masked=True),
+    ],
+    "gguf_upload": [dict()],
+}
+CASE_OF = {"gemm_lds": "gemm_nt", "gemm_rows": "gemm_nt"}
+
+
+def _workers() -> int:
+    return max(1, min(8, os.cpu_count() or 1))
+
+
+def _run(spec: dict, env: dict | None = None, timeout: int = 600) -> subprocess.CompletedProcess:
+    return subprocess.run([sys.executable, str(KEMU / "cases.py"), json.dumps(spec)], capture_output=True, text=True,
+                          timeout=timeout, env=env, cwd=str(ROOT))
+
+
+@pytest.fixture(scope="module")
+def emulator():
+    if not Path(os.environ.get("KEMU_CXX", "/opt/rocm/llvm/bin/clang++")).exists():
+        pytest.skip("no host clang++ for the emulation build")
+    sys.path.insert(0, str(KEMU))
+    import kemu_build
+    from oracle import binding as ob
+    ob.build()
+    return kemu_build.build()
+
+
+@pytest.mark.parametrize("family", list(FAMILIES))
+def test_kernels_on_emulator(emulator, family):
+    specs = [dict(case=CASE_OF.get(family, family), schedules=BOTH, **s) for s in FAMILIES[family]]
+    with ThreadPoolExecutor(_workers()) as ex:
+        results = list(ex.map(_run, specs))
+    failed = []
+    for spec, r in zip(specs, results):
+        ok = r.returncode == 0 and r.stdout.count("OK ") == len(BOTH)
+        print(f"{json.dumps(spec)}: {r.stdout.strip() if ok else 'FAILED'}")
+        if not ok:
+            failed.append(f"{json.dumps(spec)}\n{(r.stdout + r.stderr).strip()[-1500:]}")
+    assert not failed, "\n\n".join(failed)
+
+
+# One planted mistake per copy of the sources: (file, text, replacement, case).
+PLANTED = {
+    # DPP quad permute of the wrong pattern in the row-coalesced A transpose
+    "dpp_pattern": ("gemm_q8.hip", "static_cast<int>(e[k ^ 2]), 0x4E", "static_cast<int>(e[k ^ 2]), 0xB1",
+                    dict(case="gemm_nt", M=300, N=200, K=128, cfg="7")),
+    # the row kernel's per-step barrier removed (stage Q read before other waves wrote it)
+    "missing_barrier": ("gemm_q8.hip",
+                        "        __syncthreads();\n#pragma unroll\n        for (int fn = 0; fn < FN - kTail; ++fn) wf[fn]",
+                        "#pragma unroll\n        for (int fn = 0; fn < FN - kTail; ++fn) wf[fn]",
+                        dict(case="gemm_nt", M=300, N=200, K=256, cfg="5")),
+    # staged epilogue without the wave barrier between its LDS writes and reads
+    "missing_wave_barrier": ("gemm_q8.hip", "__builtin_amdgcn_wave_barrier();", "",
+                             dict(case="gemm_nt", M=77, N=96, K=64)),
+    # NN GEMM weight rows past M read through a plain pointer (out of bounds)
+    "oob_read": ("gemm_nn_q8.hip", "if (wm_row < a.M && k < a.K) {", "if (k < a.K) {",
+                 dict(case="gemm_nn", M=60, N=64, K=32)),
+    # GGUF upload refills a staging buffer without waiting for its last copy
+    "staging_reuse": ("gguf.cpp",
+                      "    if (g->stage_used[i] && hipEventSynchronize(g->done[i]) != hipSuccess)\n"
+                      "        return fail(MI_ERR_HIP, \"%s: staging wait failed\", fn);\n", "",
+                      dict(case="gguf_upload", big_rows=2048, big_cols=1280)),
+}
+
+
+def test_emulator_catches_planted_faults(emulator, tmp_path):
+    """Each planted mistake makes its case fail (wrong result, a fault or a
+    deadlock report); the unmodified sources pass the same cases."""
+    def build_and_run(name):
+        fname, old, new, spec = PLANTED[name]
+        src = tmp_path / name / "src"
+        shutil.copytree(CSRC, src)
+        text = (src / fname).read_text()
+        assert old in text, f"{name}: planting site not found in {fname}"
+        text = text.replace(old, new, 1)
+        if name == "oob_read":  # a plain-pointer read, so the stray row really leaves the buffer
+            text = text.replace("__builtin_amdgcn_raw_buffer_load_b32(rA, fl, 0, 0)",
+                                "*reinterpret_cast<const uint32_t*>(a.Aq + fl)", 1)
+        (src / fname).write_text(text)
+        env = dict(os.environ, KEMU_CSRC=str(src), KEMU_OUT=str(tmp_path / name / "build"))
+        r = subprocess.run([sys.executable, str(KEMU / "kemu_build.py")], capture_output=True, text=True, env=env,
+                           timeout=900)
+        assert r.returncode == 0, r.stderr[-2000:]
+        return _run(dict(spec, schedules=BOTH + [4]), env=env)
+
+    with ThreadPoolExecutor(2) as ex:
+        results = dict(zip(PLANTED, ex.map(build_and_run, PLANTED)))
+    for name, r in results.items():
+        print(f"{name}: rc={r.returncode} {(r.stdout + r.stderr).strip().splitlines()[-1][:160]}")
+        assert r.returncode != 0, f"planted mistake {name} went unnoticed"
+    clean = [dict(PLANTED[n][3], schedules=BOTH + [4]) for n in PLANTED]
+    with ThreadPoolExecutor(_workers()) as ex:
+        for spec, r in zip(clean, ex.map(_run, clean)):
+            assert r.returncode == 0, f"unmodified sources fail {spec}: {r.stderr[-1500:]}"
