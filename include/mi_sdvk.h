@@ -99,7 +99,9 @@ int mi_q8_0_quantize(const float* w, void* blocks, uint64_t n, void* stream);
  *   A      fp32 row-major, row stride lda (0 -> K), batch stride sA
  *   C      fp32 row-major, row stride ldc (0 -> N), batch stride sC
  *   mode 0 stores acc (+ bias[n] when bias != NULL); mode 1 adds acc to C and
- *          ignores bias (gemm_nt_q8_v.comp:115-127)
+ *          ignores bias (gemm_nt_q8_v.comp:115-127); mode 2 (no reference
+ *          counterpart: a residual add fused into the GEMM, replacing the
+ *          linear + add2 pair of sdvkgen.cpp:1746,1751,1762) adds acc + bias[n]
  *   batch  grid z: item z reads A + z*sA and writes C + z*sC; W (and bias)
  *          are shared by every item (the reference never offsets B)
  * Arithmetic: A is rounded to fp16, the weight d*q is rounded to fp16, the
@@ -132,6 +134,17 @@ int mi_gemm_nt_q8_split(const float* A, const uint32_t* payload, const float* sc
                         const float* bias, float* C, uint32_t M, uint32_t N, uint32_t K,
                         uint32_t mode, uint32_t lda, uint32_t ldc, uint32_t batch, uint64_t sA,
                         uint64_t sC, void* stream);
+
+/* GEGLU fused into the FF-up projection: W holds 2F Q8_0 rows (GEGLU's value
+ * rows 0..F-1, then its gate rows F..2F-1: the proj layout of diffusers'
+ * GEGLU), bias 2F floats or NULL, and
+ *   G[m, j] = (A.W[j]^T + bias[j]) * gelu(A.W[F + j]^T + bias[F + j])
+ * with the erf GELU of unary_fwd.comp:28-36, for j < F; G row stride ldg
+ * (0 -> F). Replaces linear(ff_up) + geglu (sdvkgen.cpp:1709-1720): the
+ * [M, 2F] intermediate never reaches memory. K % 32 == 0, K > 0; alignment
+ * as mi_gemm_nt_q8_0; G must not overlap A, W or bias.                      */
+int mi_gemm_nt_q8_0_geglu(const float* A, const void* W, const float* bias, float* G, uint32_t M,
+                          uint32_t F, uint32_t K, uint32_t lda, uint32_t ldg, void* stream);
 
 /* Q8 NN GEMM (the conv / 1x1 paths' weights-left product):
  *   C[M,N] (=|+=) deq(A[M,K]) . B[K,N]

@@ -72,6 +72,7 @@ SIGNATURES = {
                                        _u64, _u64, _vp]),
     "mi_gemm_nt_q8_split": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32,
                                            _u32, _u64, _u64, _vp]),
+    "mi_gemm_nt_q8_0_geglu": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp]),
     "mi_gemm_nn_q8_split": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32,
                                            _u64, _u64, _u64, _vp]),
     "mi_fused_attn_supported": (ctypes.c_int, [_u32, _u32]),

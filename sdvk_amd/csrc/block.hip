@@ -10,6 +10,16 @@
 // per batch item through the batched attention entry. All intermediates live
 // in a caller-provided workspace (nothing is allocated), every launch is
 // ordered on the caller's stream.
+//
+// Fused epilogues (MI_BLOCK_EPILOGUE=fused): the out-projections and FF-down
+// add their product and bias straight into x (GEMM mode 2) and FF-up applies
+// GEGLU in its epilogue (mi_gemm_nt_q8_0_geglu), which removes the three
+// residual-add passes and the [rows, 2 ff_inner] intermediate. Off by default
+// until timed on the GPU; results agree with the separate path to fp32
+// rounding.
+#include <cstdlib>
+#include <cstring>
+
 #include "common.hpp"
 
 namespace mi {
@@ -72,6 +82,11 @@ int attention(const mi_block_dims& d, const float* q, const float* k, const floa
     return mi_fused_attention_ex(&x, s);
 }
 
+bool fused_epilogues() {
+    const char* e = std::getenv("MI_BLOCK_EPILOGUE");
+    return e && std::strcmp(e, "fused") == 0;
+}
+
 int check_weights(const mi_block_weights& w, const char* fn) {
     const void* mats[10] = {w.attn1_q, w.attn1_k, w.attn1_v, w.attn1_out, w.attn2_q,
                             w.attn2_k, w.attn2_v, w.attn2_out, w.ff_up, w.ff_down};
@@ -109,6 +124,13 @@ int forward(const mi_block_weights& w, const mi_block_dims& d, float* x, const f
     auto gemm = [&](const float* A, const void* W, const float* bias, float* out, uint32_t M, uint32_t N, uint32_t K) {
         return mi_gemm_nt_q8_0(A, W, bias, out, M, N, K, 0, 0, 0, 1, 0, 0, s);
     };
+    const bool fused = fused_epilogues();
+    // x += A . W^T + bias: one GEMM with the residual epilogue, or GEMM + add
+    auto residual = [&](const float* A, const void* W, const float* bias, uint32_t K) {
+        if (fused) return mi_gemm_nt_q8_0(A, W, bias, x, rows, C, K, 2, 0, 0, 1, 0, 0, s);
+        const int st = gemm(A, W, bias, ws.a, rows, C, K);
+        return st != MI_OK ? st : mi_add_inplace(x, ws.a, nx, s);
+    };
 
     // self-attention
     MI_TRY(mi_layernorm(x, w.norm1_w, w.norm1_b, ws.n, rows, C, 1e-5f, s));
@@ -116,8 +138,7 @@ int forward(const mi_block_weights& w, const mi_block_dims& d, float* x, const f
     MI_TRY(gemm(ws.n, w.attn1_k, nullptr, ws.k, rows, C, C));
     MI_TRY(gemm(ws.n, w.attn1_v, nullptr, ws.v, rows, C, C));
     MI_TRY(attention(d, ws.q, ws.k, ws.v, ws.o, d.tokens, nullptr, s));
-    MI_TRY(gemm(ws.o, w.attn1_out, w.attn1_out_b, ws.a, rows, C, C));
-    MI_TRY(mi_add_inplace(x, ws.a, nx, s));
+    MI_TRY(residual(ws.o, w.attn1_out, w.attn1_out_b, C));
     // cross-attention over the context
     MI_TRY(mi_layernorm(x, w.norm2_w, w.norm2_b, ws.n, rows, C, 1e-5f, s));
     MI_TRY(gemm(ws.n, w.attn2_q, nullptr, ws.q, rows, C, C));
@@ -129,14 +150,16 @@ int forward(const mi_block_weights& w, const mi_block_dims& d, float* x, const f
         MI_TRY(ctx_kv(w, d, ctx, ws.k, ws.v, s));
     }
     MI_TRY(attention(d, ws.q, ck, cv, ws.o, d.ctx_tokens, ctx_len, s));
-    MI_TRY(gemm(ws.o, w.attn2_out, w.attn2_out_b, ws.a, rows, C, C));
-    MI_TRY(mi_add_inplace(x, ws.a, nx, s));
+    MI_TRY(residual(ws.o, w.attn2_out, w.attn2_out_b, C));
     // GEGLU feed-forward
     MI_TRY(mi_layernorm(x, w.norm3_w, w.norm3_b, ws.n, rows, C, 1e-5f, s));
-    MI_TRY(gemm(ws.n, w.ff_up, w.ff_up_b, ws.h, rows, 2 * d.ff_inner, C));
-    MI_TRY(mi_geglu(ws.h, ws.g, rows, d.ff_inner, s));
-    MI_TRY(gemm(ws.g, w.ff_down, w.ff_down_b, ws.a, rows, C, d.ff_inner));
-    MI_TRY(mi_add_inplace(x, ws.a, nx, s));
+    if (fused) {
+        MI_TRY(mi_gemm_nt_q8_0_geglu(ws.n, w.ff_up, w.ff_up_b, ws.g, rows, d.ff_inner, C, 0, 0, s));
+    } else {
+        MI_TRY(gemm(ws.n, w.ff_up, w.ff_up_b, ws.h, rows, 2 * d.ff_inner, C));
+        MI_TRY(mi_geglu(ws.h, ws.g, rows, d.ff_inner, s));
+    }
+    MI_TRY(residual(ws.g, w.ff_down, w.ff_down_b, d.ff_inner));
     return MI_OK;
 }
 

@@ -52,6 +52,19 @@ __device__ __forceinline__ float fp16_bits_to_f32(uint32_t h) {
     return __uint_as_float(bits);
 }
 
+// erf GELU, Abramowitz & Stegun 7.1.26 (the published rational approximation
+// the reference shader uses): erf(z) ~ 1 - (a1 t + ... + a5 t^5) exp(-z^2),
+// t = 1 / (1 + p z), z >= 0, odd extension.
+__device__ __forceinline__ float gelu_erf(float v) {
+    const float xs = v * 0.70710678118654752440f;
+    const float ax = fabsf(xs);
+    const float t = 1.0f / (1.0f + 0.3275911f * ax);
+    const float poly = ((((1.061405429f * t - 1.453152027f) * t + 1.421413741f) * t - 0.284496736f) * t + 0.254829592f) * t;
+    const float e = 1.0f - poly * expf(-ax * ax);
+    const float erf = xs >= 0.0f ? e : -e;
+    return 0.5f * v * (1.0f + erf);
+}
+
 // Remaps a linear workgroup id so that consecutive logical tiles land on the
 // same XCD. The dispatcher hands workgroup b to XCD b % 8; tiles that share an
 // operand should share that XCD's L2.

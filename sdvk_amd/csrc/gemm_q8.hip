@@ -46,7 +46,25 @@ struct GemmArgs {
     uint32_t group_m;       // tile order: groups of group_m row panels, column-major inside a group
     uint32_t cvec;          // C rows 16-byte aligned (C % 16 == 0, ldc % 4 == 0, sC % 4 == 0)
     uint32_t bvec;          // bias 16-byte aligned
+    uint32_t F;             // GEGLU epilogue: output columns (W has 2F rows: value rows, then gate rows)
 };
+
+// Epilogues. kEpiPlain: the reference's modes (0 stores acc + bias, 1 adds acc
+// to C). kEpiResidual: C += acc + bias (a residual add fused into the GEMM).
+// kEpiGeglu: W holds 2F rows (GEGLU's value rows, then its gate rows) and
+// C[m, j] = (v + bias[j]) * gelu(g + bias[F + j]) for the value / gate
+// products v, g of output column j: each 32-wide MFMA column tile holds 16
+// value columns and the 16 gate columns that pair with them, so the
+// epilogue combines them in registers and only F columns reach memory.
+enum Epi { kEpiPlain = 0, kEpiGeglu = 1, kEpiResidual = 2 };
+
+// W row of tile column c (0 <= c < BN) for an output tile starting at column
+// o0: the first 16 columns of every 32 are value rows, the next 16 the gate
+// rows of the same outputs; outputs past F read the last valid rows.
+__device__ __forceinline__ uint32_t geglu_wrow(uint32_t o0, uint32_t c, uint32_t F) {
+    const uint32_t o = min(o0 + 16u * (c >> 5) + (c & 15u), F - 1u);
+    return (c & 16u) ? F + o : o;
+}
 
 GemmArgs make_args(const float* A, const uint8_t* W, const float* scales, const float* bias, float* C, uint32_t M,
                    uint32_t N, uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldc, uint64_t sA, uint64_t sC,
@@ -137,12 +155,16 @@ __device__ __forceinline__ void interleave_step() {
 constexpr int kStageLd = 36;                       // floats per staged row (16-byte pad)
 constexpr int kStageFloats = 32 * kStageLd;        // per wave
 
-template <int FM, int FN, bool SPLITK>
+// GEGLU (EPI == kEpiGeglu): nw is the wave's first output column; tile b
+// yields output columns nw + 16 (b % FN) + 0..15 from its value columns 0..15
+// and gate columns 16..31.
+template <int FM, int FN, bool SPLITK, int EPI = kEpiPlain>
 __device__ __forceinline__ void store_tiles(const GemmArgs& a, float* C, float* stage, uint32_t mw, uint32_t nw,
                                             const floatx16 (&acc)[FM][FN], int lane) {
+    static_assert(!(SPLITK && EPI == kEpiGeglu), "the GEGLU epilogue needs the whole K sum");
     const int l32 = lane & 31, g = lane >> 5;
     const bool vec = a.cvec != 0;
-    const bool use_bias = !SPLITK && a.mode == 0 && a.bias != nullptr;
+    const bool use_bias = !SPLITK && (EPI == kEpiResidual ? true : a.mode == 0) && a.bias != nullptr;
     const bool vec_bias = !use_bias || a.bvec != 0;
     if constexpr (SPLITK) {
         // no staging: one atomic instruction covers 32 consecutive floats of a row
@@ -175,6 +197,36 @@ __device__ __forceinline__ void store_tiles(const GemmArgs& a, float* C, float* 
         // the staged tile is read back by other lanes of the wave: keep every
         // write of the wave ahead of every read (no instruction is emitted)
         __builtin_amdgcn_wave_barrier();
+        if constexpr (EPI == kEpiGeglu) {
+            // 32 rows x 4 groups of 4 output columns: value at column 4 c4, gate at 16 + 4 c4
+            const uint32_t mb = mw + 32 * (b / FN), ob = nw + 16 * (b % FN);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int u = lane + 64 * i;
+                const int row = u >> 2, col = (u & 3) * 4;
+                const floatx4 v = *reinterpret_cast<const floatx4*>(&stage[row * kStageLd + col]);
+                const floatx4 gt = *reinterpret_cast<const floatx4*>(&stage[row * kStageLd + 16 + col]);
+                const uint32_t m = mb + row, n = ob + col;
+                if (m >= a.M) continue;
+                float* c = C + static_cast<uint64_t>(m) * a.ldc + n;
+                floatx4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t j = min(n + e, a.F - 1);  // columns past F are computed, never stored
+                    const float bv = a.bias ? a.bias[j] : 0.0f, bg = a.bias ? a.bias[a.F + j] : 0.0f;
+                    o[e] = (v[e] + bv) * gelu_erf(gt[e] + bg);
+                }
+                if (vec && n + 3 < a.F) {
+                    __builtin_nontemporal_store(o, reinterpret_cast<floatx4*>(c));
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (n + e < a.F) c[e] = o[e];
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+            continue;
+        }
         const uint32_t mb = mw + 32 * (b / FN), nb = nw + 32 * (b % FN);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -185,7 +237,12 @@ __device__ __forceinline__ void store_tiles(const GemmArgs& a, float* C, float* 
             if (m >= a.M) continue;
             float* c = C + static_cast<uint64_t>(m) * a.ldc + n;
             if (vec && vec_bias && n + 3 < a.N) {
-                if (a.mode == 0) {
+                if (EPI == kEpiResidual) {
+                    // x + (acc + bias): the rounding of the separate GEMM + add
+                    floatx4 o = v;
+                    if (use_bias) o += *reinterpret_cast<const floatx4*>(a.bias + n);
+                    *reinterpret_cast<floatx4*>(c) = *reinterpret_cast<const floatx4*>(c) + o;
+                } else if (a.mode == 0) {
                     floatx4 o = v;
                     if (use_bias) o += *reinterpret_cast<const floatx4*>(a.bias + n);
                     // C is written once and not re-read here: streaming stores keep
@@ -198,7 +255,8 @@ __device__ __forceinline__ void store_tiles(const GemmArgs& a, float* C, float* 
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     if (n + e >= a.N) continue;
-                    if (a.mode == 0) c[e] = v[e] + (use_bias ? a.bias[n + e] : 0.0f);
+                    if (EPI == kEpiResidual) c[e] += v[e] + (use_bias ? a.bias[n + e] : 0.0f);
+                    else if (a.mode == 0) c[e] = v[e] + (use_bias ? a.bias[n + e] : 0.0f);
                     else c[e] += v[e];
                 }
             }
@@ -208,7 +266,7 @@ __device__ __forceinline__ void store_tiles(const GemmArgs& a, float* C, float* 
     }
 }
 
-template <int BM, int BN, int WM, int WN, int KB, int WK, bool SPLITK, bool KTAIL, int PF>
+template <int BM, int BN, int WM, int WN, int KB, int WK, bool SPLITK, bool KTAIL, int PF, int EPI = kEpiPlain>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     constexpr int NT = WM * WN * 64;
     constexpr int BK = 32 * KB;
@@ -250,7 +308,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     const uint32_t grp = lin / gsz, rem = lin % gsz;
     const uint32_t rows_in = min(a.group_m, a.tiles_m - grp * a.group_m);
     const uint32_t m0 = __builtin_amdgcn_readfirstlane((grp * a.group_m + rem % rows_in) * BM);
-    const uint32_t n0 = __builtin_amdgcn_readfirstlane((rem / rows_in) * BN);
+    // GEGLU: n0 is the tile's first output column (BN / 2 outputs per tile)
+    const uint32_t n0 = __builtin_amdgcn_readfirstlane((rem / rows_in) * (EPI == kEpiGeglu ? BN / 2 : BN));
     const uint32_t s_begin = SPLITK ? blockIdx.y * a.steps_per_split : 0;
     const uint32_t s_end = SPLITK ? min(a.ksteps, s_begin + a.steps_per_split) : a.ksteps;
 
@@ -281,7 +340,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < W_IT; ++i) {
         const int u = tid + i * NT;
-        const uint32_t n = min(n0 + u / (BK / 8), a.N - 1);
+        const uint32_t n = EPI == kEpiGeglu ? geglu_wrow(n0, u / (BK / 8), a.F) : min(n0 + u / (BK / 8), a.N - 1);
         w_k[i] = (u % (BK / 8)) * 8;
         if constexpr (WK == kBlocks34) {
             w_aux[i] = n * a.rowbytes + (w_k[i] / 32) * 34;
@@ -318,7 +377,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < WB_IT; ++i) {
         const int wb = tid + i * NT;
-        const uint32_t n = min(n0 + wb % BN, a.N - 1);
+        const uint32_t n = EPI == kEpiGeglu ? geglu_wrow(n0, wb % BN, a.F) : min(n0 + wb % BN, a.N - 1);
         const uint32_t byte = n * a.rowbytes + (wb / BN) * 34;
         wb_off[i] = byte & ~3u;
         wb_qsel[i] = (byte & 2u) ? 0x07060504u : 0x05040302u;  // bytes 4..7 or 2..5 of (x[j+1]:x[j])
@@ -537,8 +596,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
 
     float* C = a.C + static_cast<uint64_t>(blockIdx.z) * a.sC;
     __syncthreads();  // every wave is done with the operand tiles before LDS is reused
-    store_tiles<FM, FN, SPLITK>(a, C, reinterpret_cast<float*>(smem) + wave * kStageFloats, m0 + wm * TM,
-                                n0 + wn * TN, acc, lane);
+    store_tiles<FM, FN, SPLITK, EPI>(a, C, reinterpret_cast<float*>(smem) + wave * kStageFloats, m0 + wm * TM,
+                                     EPI == kEpiGeglu ? n0 + wn * TN / 2 : n0 + wn * TN, acc, lane);
 }
 
 // ---- row-stationary kernel --------------------------------------------------------
@@ -591,7 +650,7 @@ __device__ __forceinline__ void quad_transpose4(uint32_t (&e)[4], int lane) {
 //   fp16 conversion) then leaves lane l holding chunks 4 g .. 4 g + 3 of row
 //   l % 32 -- the same operand layout as AQ = false, so W, the MFMAs and the
 //   epilogue are shared.
-template <int FN, int WK, bool SPLITK, bool AQ = false>
+template <int FN, int WK, bool SPLITK, bool AQ = false, int EPI = kEpiPlain>
 __global__ __launch_bounds__(256) void gemm_q8_rows_kernel(GemmArgs a) {
     constexpr int BM = 256, BN = 32 * FN, FM = 2, LDW = 40;  // LDW: 32 halves + 16-byte pad per column
     // every thread stages one W column (threads t >= BN a clamped column into
@@ -610,7 +669,8 @@ __global__ __launch_bounds__(256) void gemm_q8_rows_kernel(GemmArgs a) {
     const uint32_t grp = lin / gsz, rem = lin % gsz;
     const uint32_t rows_in = min(a.group_m, a.tiles_m - grp * a.group_m);
     const uint32_t m0 = __builtin_amdgcn_readfirstlane((grp * a.group_m + rem % rows_in) * BM);
-    const uint32_t n0 = __builtin_amdgcn_readfirstlane((rem / rows_in) * BN);
+    // GEGLU: n0 is the tile's first output column (BN / 2 outputs per tile)
+    const uint32_t n0 = __builtin_amdgcn_readfirstlane((rem / rows_in) * (EPI == kEpiGeglu ? BN / 2 : BN));
     // split K: steps_per_split is even, so a split starts on an even step and
     // step parity = register set = LDS stage
     const uint32_t s_begin = SPLITK ? blockIdx.y * a.steps_per_split : 0;
@@ -646,7 +706,8 @@ __global__ __launch_bounds__(256) void gemm_q8_rows_kernel(GemmArgs a) {
     // starts at byte wb + 34 ks; even steps read the window at
     // (wb & ~3) + 68 (ks / 2), odd steps at ((wb + 34) & ~3) + 68 (ks / 2), and
     // the block sits 0 or 2 bytes into its window (v_perm selectors per parity).
-    const uint32_t wn = min(n0 + static_cast<uint32_t>(tid), a.N - 1);
+    const uint32_t wn = EPI == kEpiGeglu ? geglu_wrow(n0, min(static_cast<uint32_t>(tid), BN - 1u), a.F)
+                                         : min(n0 + static_cast<uint32_t>(tid), a.N - 1);
     uint32_t w_vo[2], w_qsel[2], w_dsel[2];
     if constexpr (WK == kBlocks34) {
         const uint32_t wb = wn * a.rowbytes;
@@ -867,8 +928,8 @@ __global__ __launch_bounds__(256) void gemm_q8_rows_kernel(GemmArgs a) {
 
     float* C = a.C + static_cast<uint64_t>(blockIdx.z) * a.sC;
     __syncthreads();  // every wave is done with the W tiles before LDS is reused
-    store_tiles<FM, FN, SPLITK>(a, C, reinterpret_cast<float*>(smem) + wave * kStageFloats, m0 + 64 * wave, n0, acc,
-                                lane);
+    store_tiles<FM, FN, SPLITK, EPI>(a, C, reinterpret_cast<float*>(smem) + wave * kStageFloats, m0 + 64 * wave, n0,
+                                     acc, lane);
 }
 
 // C[m, n] = bias[n] (or 0) for the split-K accumulation (mode 0 only).
@@ -884,6 +945,34 @@ __global__ __launch_bounds__(256) void gemm_init_kernel(float* C, const float* b
 void launch_init(float* C, const float* bias, uint32_t M, uint32_t N, uint32_t ldc, uint64_t sC, uint32_t batch,
                  hipStream_t s) {
     gemm_init_kernel<<<dim3(ceil_div(N, 256), std::min<uint32_t>(M, 4096), batch), 256, 0, s>>>(C, bias, M, N, ldc, sC);
+}
+
+// C[m, n] += bias[n]: the bias of a residual-epilogue GEMM whose K splits add
+// their partial products with atomics.
+__global__ __launch_bounds__(256) void gemm_bias_add_kernel(float* C, const float* bias, uint32_t M, uint32_t N,
+                                                            uint32_t ldc, uint64_t sC) {
+    const uint32_t n = blockIdx.x * 256 + threadIdx.x;
+    if (n >= N) return;
+    const float v = bias[n];
+    float* c = C + static_cast<uint64_t>(blockIdx.z) * sC + n;
+    for (uint32_t m = blockIdx.y; m < M; m += gridDim.y) c[static_cast<uint64_t>(m) * ldc] += v;
+}
+
+void launch_bias_add(float* C, const float* bias, uint32_t M, uint32_t N, uint32_t ldc, uint64_t sC, uint32_t batch,
+                     hipStream_t s) {
+    gemm_bias_add_kernel<<<dim3(ceil_div(N, 256), std::min<uint32_t>(M, 4096), batch), 256, 0, s>>>(C, bias, M, N,
+                                                                                                     ldc, sC);
+}
+
+// Before the K splits add into C: mode 0 writes bias (or 0), the residual
+// epilogue adds bias once, mode 1 leaves C as it is.
+template <int EPI>
+void prepare_split(const GemmArgs& a, uint32_t batch, hipStream_t s) {
+    if (EPI == kEpiResidual) {
+        if (a.bias) launch_bias_add(a.C, a.bias, a.M, a.N, a.ldc, a.sC, batch, s);
+    } else if (a.mode == 0) {
+        launch_init(a.C, a.bias, a.M, a.N, a.ldc, a.sC, batch, s);
+    }
 }
 
 // ---- configurations -------------------------------------------------------------
@@ -947,10 +1036,12 @@ uint32_t pick_group(uint32_t tm, uint32_t tn, uint32_t BM, uint32_t BN, uint32_t
     return best;
 }
 
-template <int BM, int BN, int WM, int WN, int KB, int WK, bool KTAIL, int PF = 2>
+template <int BM, int BN, int WM, int WN, int KB, int WK, bool KTAIL, int PF = 2, int EPI = kEpiPlain>
 void launch_cfg(const GemmArgs& a0, uint32_t batch, uint32_t splits, hipStream_t s) {
     GemmArgs a = a0;
-    a.tiles_n = ceil_div(a.N, BN);
+    // GEGLU: BN / 2 outputs per tile, and the epilogue needs the whole K sum
+    a.tiles_n = EPI == kEpiGeglu ? ceil_div(a.F, BN / 2) : ceil_div(a.N, BN);
+    if (EPI == kEpiGeglu) splits = 1;
     a.tiles_m = ceil_div(a.M, BM);
     a.group_m = pick_group(a.tiles_m, a.tiles_n, BM, BN, a.K);
     a.ksteps = ceil_div(a.K, 32 * KB);
@@ -960,21 +1051,23 @@ void launch_cfg(const GemmArgs& a0, uint32_t batch, uint32_t splits, hipStream_t
         splits = ceil_div(a.ksteps, a.steps_per_split);
     }
     if (splits > 1) {
-        if (a.mode == 0) launch_init(a.C, a.bias, a.M, a.N, a.ldc, a.sC, batch, s);
-        gemm_q8_kernel<BM, BN, WM, WN, KB, WK, true, KTAIL, PF><<<dim3(tiles, splits, batch), WM * WN * 64, 0, s>>>(a);
+        prepare_split<EPI>(a, batch, s);
+        if constexpr (EPI != kEpiGeglu)
+            gemm_q8_kernel<BM, BN, WM, WN, KB, WK, true, KTAIL, PF><<<dim3(tiles, splits, batch), WM * WN * 64, 0, s>>>(a);
     } else {
         a.steps_per_split = a.ksteps;
-        gemm_q8_kernel<BM, BN, WM, WN, KB, WK, false, KTAIL, PF><<<dim3(tiles, 1, batch), WM * WN * 64, 0, s>>>(a);
+        gemm_q8_kernel<BM, BN, WM, WN, KB, WK, false, KTAIL, PF, EPI><<<dim3(tiles, 1, batch), WM * WN * 64, 0, s>>>(a);
     }
 }
 
 // Row-stationary kernel: 256 x (32 FN) tiles, K % 32 == 0. A K split covers an
 // even number of 32-wide steps.
-template <int FN, int WK, bool AQ = false>
+template <int FN, int WK, bool AQ = false, int EPI = kEpiPlain>
 void launch_rows(const GemmArgs& a0, uint32_t batch, uint32_t splits, hipStream_t s) {
     GemmArgs a = a0;
     constexpr uint32_t BM = 256, BN = 32 * FN;
-    a.tiles_n = ceil_div(a.N, BN);
+    a.tiles_n = EPI == kEpiGeglu ? ceil_div(a.F, BN / 2) : ceil_div(a.N, BN);
+    if (EPI == kEpiGeglu) splits = 1;
     a.tiles_m = ceil_div(a.M, BM);
     a.group_m = pick_group(a.tiles_m, a.tiles_n, BM, BN, a.K);
     a.ksteps = a.K / 32;
@@ -984,37 +1077,38 @@ void launch_rows(const GemmArgs& a0, uint32_t batch, uint32_t splits, hipStream_
         splits = ceil_div(a.ksteps, a.steps_per_split);
     }
     if (splits > 1) {
-        if (a.mode == 0) launch_init(a.C, a.bias, a.M, a.N, a.ldc, a.sC, batch, s);
-        gemm_q8_rows_kernel<FN, WK, true, AQ><<<dim3(tiles, splits, batch), 256, 0, s>>>(a);
+        prepare_split<EPI>(a, batch, s);
+        if constexpr (EPI != kEpiGeglu)
+            gemm_q8_rows_kernel<FN, WK, true, AQ><<<dim3(tiles, splits, batch), 256, 0, s>>>(a);
     } else {
         a.steps_per_split = a.ksteps;
-        gemm_q8_rows_kernel<FN, WK, false, AQ><<<dim3(tiles, 1, batch), 256, 0, s>>>(a);
+        gemm_q8_rows_kernel<FN, WK, false, AQ, EPI><<<dim3(tiles, 1, batch), 256, 0, s>>>(a);
     }
 }
 
-template <int WK>
+template <int WK, int EPI = kEpiPlain>
 void launch(int cfg, const GemmArgs& a, uint32_t batch, uint32_t splits, hipStream_t s) {
     switch (cfg) {
-        case kR256x256: launch_rows<8, WK>(a, batch, splits, s); break;
-        case kR256x256Q: launch_rows<8, WK, true>(a, batch, splits, s); break;
-        case kR256x192Q: launch_rows<6, WK, true>(a, batch, splits, s); break;
-        case kR256x160Q: launch_rows<5, WK, true>(a, batch, splits, s); break;
-        case kR256x128Q: launch_rows<4, WK, true>(a, batch, splits, s); break;
-        case kR256x128: launch_rows<4, WK>(a, batch, splits, s); break;
-        case kC256x128: launch_cfg<256, 128, 4, 2, 2, WK, false>(a, batch, splits, s); break;
-        case kC128x128: launch_cfg<128, 128, 2, 2, 2, WK, false>(a, batch, splits, s); break;
-        case kC128x64: launch_cfg<128, 64, 2, 2, 2, WK, false>(a, batch, splits, s); break;
-        case kC256x256: launch_cfg<256, 256, 4, 2, 2, WK, false, 1>(a, batch, splits, s); break;
-        default: launch_cfg<64, 64, 2, 2, 2, WK, false>(a, batch, splits, s); break;
+        case kR256x256: launch_rows<8, WK, false, EPI>(a, batch, splits, s); break;
+        case kR256x256Q: launch_rows<8, WK, true, EPI>(a, batch, splits, s); break;
+        case kR256x192Q: launch_rows<6, WK, true, EPI>(a, batch, splits, s); break;
+        case kR256x160Q: launch_rows<5, WK, true, EPI>(a, batch, splits, s); break;
+        case kR256x128Q: launch_rows<4, WK, true, EPI>(a, batch, splits, s); break;
+        case kR256x128: launch_rows<4, WK, false, EPI>(a, batch, splits, s); break;
+        case kC256x128: launch_cfg<256, 128, 4, 2, 2, WK, false, 2, EPI>(a, batch, splits, s); break;
+        case kC128x128: launch_cfg<128, 128, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, s); break;
+        case kC128x64: launch_cfg<128, 64, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, s); break;
+        case kC256x256: launch_cfg<256, 256, 4, 2, 2, WK, false, 1, EPI>(a, batch, splits, s); break;
+        default: launch_cfg<64, 64, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, s); break;
     }
 }
 
 // General K (K % 64 != 0): one block column per step, 64x64 tiles; the split
 // layout with K % 32 != 0 also zero-fills the partial last step.
-template <int WK>
+template <int WK, int EPI = kEpiPlain>
 void launch_general(const GemmArgs& a, uint32_t batch, uint32_t splits, hipStream_t s) {
-    if (a.K % 32 == 0) launch_cfg<64, 64, 2, 2, 1, WK, false>(a, batch, splits, s);
-    else launch_cfg<64, 64, 2, 2, 1, WK, true>(a, batch, splits, s);
+    if (a.K % 32 == 0) launch_cfg<64, 64, 2, 2, 1, WK, false, 2, EPI>(a, batch, splits, s);
+    else launch_cfg<64, 64, 2, 2, 1, WK, true, 2, EPI>(a, batch, splits, s);
 }
 
 constexpr int kCUs = 256;
@@ -1060,19 +1154,20 @@ void choose(uint32_t M, uint32_t N, uint32_t K, uint32_t batch, int& cfg, uint32
     }
 }
 
-template <int WK>
+template <int WK, int EPI = kEpiPlain>
 void dispatch(const GemmArgs& a, uint32_t batch, hipStream_t s) {
     int cfg;
     uint32_t splits;
-    choose(a.M, a.N, a.K, batch, cfg, splits);
-    if (a.K % 64 != 0) launch_general<WK>(a, batch, splits, s);
-    else launch<WK>(cfg, a, batch, splits, s);
+    choose(a.M, a.N, a.K, batch, cfg, splits);  // GEGLU: N = 2F weight rows, the same MFMA work
+    if (a.K % 64 != 0) launch_general<WK, EPI>(a, batch, splits, s);
+    else launch<WK, EPI>(cfg, a, batch, splits, s);
 }
 
 int validate(const char* fn, const float* A, const void* W, const float* C, uint32_t M, uint32_t N, uint32_t K,
              uint32_t mode, uint32_t& lda, uint32_t& ldc, uint32_t batch, uint64_t sA, uint64_t sC) {
     if (!A || !W || !C) return fail(MI_ERR_INVALID_ARG, "%s: null pointer", fn);
-    if (mode > 1) return fail(MI_ERR_INVALID_ARG, "%s: mode %u (0 = store, 1 = accumulate)", fn, mode);
+    if (mode > 2)
+        return fail(MI_ERR_INVALID_ARG, "%s: mode %u (0 = store, 1 = accumulate, 2 = accumulate + bias)", fn, mode);
     if (batch == 0) return fail(MI_ERR_INVALID_ARG, "%s: batch 0", fn);
     if (batch > 65535) return fail(MI_ERR_UNSUPPORTED, "%s: batch %u > 65535", fn, batch);
     if (lda == 0) lda = K;
@@ -1108,11 +1203,13 @@ extern "C" int mi_gemm_nt_q8_0(const float* A, const void* W, const float* bias,
         return fail(MI_ERR_ALIASING, "%s: C overlaps an input", fn);
     if (K == 0) {
         if (mode == 0) launch_init(C, bias, M, N, ldc, sC, batch, static_cast<hipStream_t>(stream));
+        if (mode == 2 && bias) launch_bias_add(C, bias, M, N, ldc, sC, batch, static_cast<hipStream_t>(stream));
         return check_launch(fn);
     }
     GemmArgs a = make_args(A, static_cast<const uint8_t*>(W), nullptr, bias, C, M, N, K, mode, lda, ldc, sA, sC,
                            (K / 32) * 34);
-    dispatch<kBlocks34>(a, batch, static_cast<hipStream_t>(stream));
+    if (mode == 2) dispatch<kBlocks34, kEpiResidual>(a, batch, static_cast<hipStream_t>(stream));
+    else dispatch<kBlocks34>(a, batch, static_cast<hipStream_t>(stream));
     return check_launch(fn);
 }
 
@@ -1135,10 +1232,36 @@ extern "C" int mi_gemm_nt_q8_split(const float* A, const uint32_t* payload, cons
         return fail(MI_ERR_ALIASING, "%s: C overlaps an input", fn);
     if (K == 0) {
         if (mode == 0) launch_init(C, bias, M, N, ldc, sC, batch, static_cast<hipStream_t>(stream));
+        if (mode == 2 && bias) launch_bias_add(C, bias, M, N, ldc, sC, batch, static_cast<hipStream_t>(stream));
         return check_launch(fn);
     }
     GemmArgs a = make_args(A, reinterpret_cast<const uint8_t*>(payload), scales, bias, C, M, N, K, mode, lda, ldc, sA,
                            sC, 0);
-    dispatch<kSplit>(a, batch, static_cast<hipStream_t>(stream));
+    if (mode == 2) dispatch<kSplit, kEpiResidual>(a, batch, static_cast<hipStream_t>(stream));
+    else dispatch<kSplit>(a, batch, static_cast<hipStream_t>(stream));
+    return check_launch(fn);
+}
+
+extern "C" int mi_gemm_nt_q8_0_geglu(const float* A, const void* W, const float* bias, float* G, uint32_t M, uint32_t F,
+                                     uint32_t K, uint32_t lda, uint32_t ldg, void* stream) {
+    const char* fn = "mi_gemm_nt_q8_0_geglu";
+    if (M == 0 || F == 0) return MI_OK;
+    if (K == 0 || K % 32) return fail(MI_ERR_UNSUPPORTED, "%s: K=%u must be a positive multiple of 32", fn, K);
+    if (F > (1u << 30)) return fail(MI_ERR_UNSUPPORTED, "%s: F=%u too large", fn, F);
+    const uint32_t N = 2 * F;
+    uint32_t ldc = ldg, mode = 0;
+    int st = validate(fn, A, W, G, M, F, K, mode, lda, ldc, 1, 0, 0);
+    if (st) return st;
+    if (!aligned(W, 16)) return fail(MI_ERR_ALIGNMENT, "%s: W must be 16-byte aligned", fn);
+    const uint64_t wbytes = static_cast<uint64_t>(N) * (K / 32) * 34;
+    if (wbytes + 16 >= (uint64_t(1) << 32)) return fail(MI_ERR_UNSUPPORTED, "%s: weight >= 4 GiB", fn);
+    const uint64_t gbytes = (static_cast<uint64_t>(M - 1) * ldc + F) * 4;
+    const uint64_t abytes = (static_cast<uint64_t>(M - 1) * lda + K) * 4;
+    if (overlaps(G, gbytes, A, abytes) || overlaps(G, gbytes, W, wbytes) || overlaps(G, gbytes, bias, uint64_t(N) * 4))
+        return fail(MI_ERR_ALIASING, "%s: G overlaps an input", fn);
+    GemmArgs a = make_args(A, static_cast<const uint8_t*>(W), nullptr, bias, G, M, N, K, 0, lda, ldc, 0, 0,
+                           (K / 32) * 34);
+    a.F = F;
+    dispatch<kBlocks34, kEpiGeglu>(a, 1, static_cast<hipStream_t>(stream));
     return check_launch(fn);
 }

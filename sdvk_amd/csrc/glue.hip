@@ -104,19 +104,6 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict_
     }
 }
 
-// erf GELU, Abramowitz & Stegun 7.1.26 (the published rational approximation
-// the reference shader uses): erf(z) ~ 1 - (a1 t + ... + a5 t^5) exp(-z^2),
-// t = 1 / (1 + p z), z >= 0, odd extension.
-__device__ __forceinline__ float gelu_erf(float v) {
-    const float xs = v * 0.70710678118654752440f;
-    const float ax = fabsf(xs);
-    const float t = 1.0f / (1.0f + 0.3275911f * ax);
-    const float poly = ((((1.061405429f * t - 1.453152027f) * t + 1.421413741f) * t - 0.284496736f) * t + 0.254829592f) * t;
-    const float e = 1.0f - poly * expf(-ax * ax);
-    const float erf = xs >= 0.0f ? e : -e;
-    return 0.5f * v * (1.0f + erf);
-}
-
 // y[r, j] = h[r, j] * gelu(h[r, F + j]); F % 4 == 0 and 16-byte aligned rows.
 __global__ __launch_bounds__(256) void geglu_vec_kernel(const float* __restrict__ h, float* __restrict__ y, uint32_t rows,
                                                         uint32_t F) {

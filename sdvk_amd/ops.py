@@ -32,7 +32,7 @@ from ._lib import MI_F16, MI_F32, MiAttnArgs, MiBlockDims, MiBlockWeights, MiErr
 
 __all__ = [
     "MiError", "MI_F32", "MI_F16", "FusedAttnArgs", "fused_attn_supported", "fused_attention",
-    "fused_attention_ex", "gemm_nt_q8", "gemm_nt_q8_bias", "gemm_nt_q8_0", "gemm_nn_q8", "q8_0_dequant",
+    "fused_attention_ex", "gemm_nt_q8", "gemm_nt_q8_bias", "gemm_nt_q8_0", "gemm_nt_q8_0_geglu", "gemm_nn_q8", "q8_0_dequant",
     "q8_split_dequant", "q8_0_to_split", "q8_0_quantize", "Pg", "dispatch", "KERNELS", "layernorm", "geglu", "add2",
     "BlockWeights", "BlockDims", "block_workspace_bytes", "sdxl_block_forward", "block_ctx_kv_bytes", "block_ctx_kv",
     "sdxl_block_forward_kv",
@@ -93,6 +93,13 @@ def gemm_nt_q8(A, Bq, C, Bs, M: int, N: int, K: int, *, mode: int = 0, lda: int 
     """sdvkgen.cpp:917-926 gemmNtQ8: C = A . deq(Bq, Bs)^T on the split layout."""
     call("mi_gemm_nt_q8_split", ptr(A), ptr(Bq), ptr(Bs), None, ptr(C), M, N, K, mode, lda, ldc,
          batch, sA, sC, _s(stream))
+
+
+def gemm_nt_q8_0_geglu(A, W, G, M: int, F: int, K: int, *, bias=None, lda: int = 0, ldg: int = 0,
+                       stream=None) -> None:
+    """linear(ff_up) + geglu (sdvkgen.cpp:1709-1720) in one GEMM: W has 2F Q8_0 rows (value, then gate),
+    G[M, F] = (A.W[:F]^T + b[:F]) * gelu(A.W[F:]^T + b[F:])."""
+    call("mi_gemm_nt_q8_0_geglu", ptr(A), ptr(W), ptr(bias), ptr(G), M, F, K, lda, ldg, _s(stream))
 
 
 def gemm_nn_q8(Aq, As, B, C, M: int, N: int, K: int, *, mode: int = 0, lda: int = 0, ldb: int = 0, ldc: int = 0,

@@ -62,28 +62,79 @@ def gemm_nt(E, *, M, N, K, layout="q8_0", cfg=None, mode=0, bias=True, batch=1, 
     A = ob.normal(seed, a_el)
     blocks = q8_weights(ob, seed + 1, N, K)
     b = ob.normal(seed + 2, N, 0.0, 0.02) if bias else None
-    C0 = ob.normal(seed + 3, c_el) if mode == 1 else np.full(c_el, SENTINEL, dtype=np.float32)
+    C0 = ob.normal(seed + 3, c_el) if mode in (1, 2) else np.full(c_el, SENTINEL, dtype=np.float32)
     dA, dC = E.buf(A, front=front), E.buf(C0, front=front)
     dB = E.buf(b, front=front) if bias else None
+    # mode 2 (C += acc + bias) = C0 + the mode-0 product with bias
+    omode, oC = (0, np.zeros_like(C0)) if mode == 2 else (mode, C0.copy())
     if layout == "q8_0":
         dW = E.buf(blocks, front=front)
         E.call("mi_gemm_nt_q8_0", dA.ptr, dW.ptr, dB.ptr if dB else None, dC.ptr, M, N, K, mode, lda, ldc, batch,
                sA, sC, None)
-        want = ob.gemm_nt_q8_0(A, blocks, M, N, K, bias=b, C=C0.copy(), mode=mode, lda=lda, ldc=ldc, batch=batch,
+        want = ob.gemm_nt_q8_0(A, blocks, M, N, K, bias=b, C=oC, mode=omode, lda=lda, ldc=ldc, batch=batch,
                                sA=sA, sC=sC, threads=ob.max_threads())
     else:
         payload, scales = ob.q8_0_to_split(blocks, N * K)
         dP, dS = E.buf(payload, front=front), E.buf(scales, front=front)
         E.call("mi_gemm_nt_q8_split", dA.ptr, dP.ptr, dS.ptr, dB.ptr if dB else None, dC.ptr, M, N, K, mode, lda,
                ldc, batch, sA, sC, None)
-        want = ob.gemm_nt_q8_split(A, payload, scales, M, N, K, bias=b, C=C0.copy(), mode=mode, lda=lda, ldc=ldc,
+        want = ob.gemm_nt_q8_split(A, payload, scales, M, N, K, bias=b, C=oC, mode=omode, lda=lda, ldc=ldc,
                                    batch=batch, sA=sA, sC=sC, threads=ob.max_threads())
+    if mode == 2:
+        want = want + C0
     got = dC.get(np.float32, c_el)
     mask = _logical_mask(M, N, ldc_e, batch, sC, c_el)
     assert np.array_equal(got[~mask], C0[~mask]), "elements outside the logical output changed"
-    if mode == 1:
-        return assert_parity(got[mask] - C0[mask], want[mask] - C0[mask], tol=tol, what="gemm_nt mode 1")
+    if mode in (1, 2):
+        return assert_parity(got[mask] - C0[mask], want[mask] - C0[mask], tol=tol, what=f"gemm_nt mode {mode}")
     return assert_parity(got[mask], want[mask], tol=tol, what="gemm_nt")
+
+
+def gemm_geglu(E, *, M, F, K, cfg=None, bias=True, lda=0, ldg=0, seed=1, front=False, order=0, tol=2e-3):
+    """mi_gemm_nt_q8_0_geglu: against the separate path on the same build
+    (mi_gemm_nt_q8_0 into [M, 2F], then mi_geglu) to fp32 rounding, and
+    against the oracle's GEMM + GEGLU."""
+    _set_cfg(cfg)
+    E.order(order)
+    lda_e, ldg_e = lda or K, ldg or F
+    a_el, g_el = (M - 1) * lda_e + K, (M - 1) * ldg_e + F
+    A = ob.normal(seed, a_el)
+    blocks = q8_weights(ob, seed + 1, 2 * F, K)
+    b = ob.normal(seed + 2, 2 * F, 0.0, 0.5) if bias else None
+    dA, dW = E.buf(A, front=front), E.buf(blocks, front=front)
+    dB = E.buf(b, front=front) if bias else None
+    dG = E.buf(np.full(g_el, SENTINEL, np.float32), front=front)
+    E.call("mi_gemm_nt_q8_0_geglu", dA.ptr, dW.ptr, dB.ptr if dB else None, dG.ptr, M, F, K, lda, ldg, None)
+    got = dG.get(np.float32, g_el)
+    mask = _logical_mask(M, F, ldg_e, 1, 0, g_el)
+    assert np.array_equal(got[~mask], np.full((~mask).sum(), SENTINEL, np.float32)), "padding of G changed"
+    got = got[mask].reshape(M, F)
+    # separate path on the same build: same MFMA sums (no K split), fp32 epilogue arithmetic
+    os.environ["MI_GEMM_CFG"] = (cfg.split(":")[0] if cfg else os.environ.get("MI_GEMM_CFG", "")) or "0"
+    if cfg is None:
+        os.environ.pop("MI_GEMM_CFG", None)
+    dH, dY = E.buf(nbytes=M * 2 * F * 4), E.buf(nbytes=M * F * 4)
+    E.call("mi_gemm_nt_q8_0", dA.ptr, dW.ptr, dB.ptr if dB else None, dH.ptr, M, 2 * F, K, 0, lda, 0, 1, 0, 0, None)
+    E.call("mi_geglu", dH.ptr, dY.ptr, M, F, None)
+    sep = dY.get(np.float32, M * F).reshape(M, F)
+    d_sep = float(np.max(np.abs(got - sep)) / max(rms(sep), 1e-30))
+    h = ob.gemm_nt_q8_0(A, blocks, M, 2 * F, K, bias=b, lda=lda, threads=ob.max_threads())
+    want = ob.geglu(h, M, F).reshape(M, F)
+    # GEGLU multiplies two GEMM outputs: the GEMM bar (tol x RMS(h) on v and g)
+    # propagates to |dG| <= tol RMS(h) (|gelu(g)| + |v gelu'(g)|) per element
+    h2 = h.reshape(M, 2 * F).astype(np.float64)
+    v, g = h2[:, :F], h2[:, F:]
+    from math import erf as _erf
+    cdf = 0.5 * (1.0 + np.vectorize(_erf)(g / np.sqrt(2.0)))
+    dgelu = cdf + g * np.exp(-0.5 * g * g) / np.sqrt(2.0 * np.pi)
+    bound = tol * rms(h2) * (np.abs(g * cdf) + np.abs(v * dgelu)) + 1e-6 * np.abs(want)
+    assert np.all(np.isfinite(got)), "gemm_geglu: non-finite output"
+    worst = float(np.max(np.abs(got - want) / bound))
+    assert worst <= 1.0, f"gemm_geglu: error {worst:.2f} x the propagated GEMM bound"
+    e = float(np.max(np.abs(got - want)) / rms(want))
+    if cfg is None or ":" not in cfg:  # no K split in the separate path: same sums
+        assert d_sep <= 2e-6, f"fused vs separate GEGLU: {d_sep:.3e} x RMS"
+    return e
 
 
 def gemm_nn(E, *, M, N, K, mode=0, batch=1, lda=0, ldb=0, ldc=0, sA=0, sB=0, sC=0, seed=1, front=False,
@@ -145,11 +196,15 @@ def attention(E, *, batch=1, Tq, Tk, C, heads, causal=False, f16_in=False, f16_o
     return assert_parity(got, want, tol=tol, what="attention")
 
 
-def block(E, *, B, T, C, H, Tc, Cc, F, masked=False, blocks=2, order=0, front=False):
+def block(E, *, B, T, C, H, Tc, Cc, F, masked=False, blocks=2, order=0, front=False, fused=False):
     """Two applications of one SDXL transformer block: uncached
     (mi_sdxl_block_forward) vs context K / V projected once (mi_block_ctx_kv,
     mi_sdxl_block_forward_kv), both against the oracle's block."""
     E.order(order)
+    if fused:
+        os.environ["MI_BLOCK_EPILOGUE"] = "fused"
+    else:
+        os.environ.pop("MI_BLOCK_EPILOGUE", None)
     w = make_weights(ob, C, Cc, F, seed=500)
     dw = {k: E.buf(v, front=front) for k, v in w.items()}
     bw = MiBlockWeights(*[dw[f[0]].ptr for f in MiBlockWeights._fields_])
@@ -180,6 +235,23 @@ def block(E, *, B, T, C, H, Tc, Cc, F, masked=False, blocks=2, order=0, front=Fa
     assert e_kv <= 1e-5, f"cached vs fresh K / V: {e_kv:.3e} x RMS(update)"
     e = float(np.max(np.abs(fresh - want)) / rms(want - x))
     assert e <= blocks * BLOCK_TOL, f"block vs oracle: {e:.3e} x RMS(update)"
+    if fused:
+        # one block, fused vs separate epilogues on the same build: they differ
+        # only in the rounding order of the residual adds of K-split GEMMs
+        # ((x + b) + partials vs x + (b + partials)), a few ulps of |x|
+        outs = []
+        for mode in ("fused", None):
+            if mode:
+                os.environ["MI_BLOCK_EPILOGUE"] = mode
+            else:
+                os.environ.pop("MI_BLOCK_EPILOGUE", None)
+            d1 = E.buf(x, front=front)
+            E.call("mi_sdxl_block_forward", ctypes.byref(bw), ctypes.byref(dims), d1.ptr, dc.ptr,
+                   dl.ptr if dl else None, ws.ptr, ws_bytes, None)
+            outs.append(d1.get(np.float32))
+        diff = float(np.max(np.abs(outs[0] - outs[1])))
+        ulp = float(np.spacing(np.float32(np.max(np.abs(outs[1])))))
+        assert diff <= 4 * ulp, f"fused vs separate epilogues: {diff:.3e} > 4 ulp ({ulp:.3e}) of max|x|"
     return e
 
 
@@ -241,7 +313,7 @@ def gguf_upload(E, *, big_rows=10240, big_cols=1280, order=0, front=False):
     return 0.0
 
 
-CASES = {"gemm_nt": gemm_nt, "gemm_nn": gemm_nn, "attention": attention, "block": block, "gguf_upload": gguf_upload}
+CASES = {"gemm_nt": gemm_nt, "gemm_geglu": gemm_geglu, "gemm_nn": gemm_nn, "attention": attention, "block": block, "gguf_upload": gguf_upload}
 
 
 def main(argv):

@@ -71,9 +71,18 @@ def test_errors_are_returned_not_raised_through_the_abi():
     # C overlapping A
     st = lib.mi_gemm_nt_q8_0(fake, fake * 2, None, fake + 64, 8, 8, 32, 0, 0, 0, 1, 0, 0, None)
     assert st == _lib.MI_ERR_ALIASING
-    # bad mode
-    st = lib.mi_gemm_nt_q8_split(fake, fake * 2, fake * 4, None, fake * 3, 8, 8, 32, 2, 0, 0, 1, 0, 0, None)
-    assert st == _lib.MI_ERR_INVALID_ARG
+    # bad mode (0 store, 1 accumulate, 2 accumulate + bias)
+    for entry_mode in (3, 7):
+        st = lib.mi_gemm_nt_q8_split(fake, fake * 2, fake * 4, None, fake * 3, 8, 8, 32, entry_mode, 0, 0, 1, 0, 0,
+                                     None)
+        assert st == _lib.MI_ERR_INVALID_ARG
+        st = lib.mi_gemm_nt_q8_0(fake, fake * 2, None, fake * 3, 8, 8, 32, entry_mode, 0, 0, 1, 0, 0, None)
+        assert st == _lib.MI_ERR_INVALID_ARG
+    # GEGLU GEMM: K must be a positive multiple of 32; G must not overlap A
+    assert lib.mi_gemm_nt_q8_0_geglu(fake, fake * 2, None, fake * 3, 8, 8, 48, 0, 0, None) == _lib.MI_ERR_UNSUPPORTED
+    assert lib.mi_gemm_nt_q8_0_geglu(fake, fake * 2, None, fake * 3, 8, 8, 0, 0, 0, None) == _lib.MI_ERR_UNSUPPORTED
+    assert lib.mi_gemm_nt_q8_0_geglu(fake, fake * 2, None, fake + 64, 8, 8, 32, 0, 0, None) == _lib.MI_ERR_ALIASING
+    assert lib.mi_gemm_nt_q8_0_geglu(None, None, None, None, 0, 8, 32, 0, 0, None) == _lib.MI_OK
     # split entry rejects K % 4 != 0 (the reference's 4-wide staging zero-fills there)
     st = lib.mi_gemm_nt_q8_split(fake, fake * 2, fake * 4, None, fake * 3, 8, 8, 30, 0, 0, 0, 1, 0, 0, None)
     assert st == _lib.MI_ERR_UNSUPPORTED

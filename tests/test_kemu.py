@@ -12,7 +12,8 @@ wave operation per wave per pass, and wave-major with lanes and waves
 reversed, so a missing barrier changes the result under one of them.
 
 This is where paths are checked before they reach a GPU (the coalesced-A row
-kernel configurations, the NN GEMM, the cached-K/V block, the GGUF uploads);
+kernel configurations, the NN GEMM, the cached-K/V block, the GGUF uploads,
+the fused GEGLU / residual epilogues);
 it does not measure anything and nothing in the product loads the emulation
 build. test_emulator_catches_planted_faults pins the checker itself: copies
 of the sources with one planted mistake each (compiled for the host only)
@@ -58,6 +59,16 @@ FAMILIES = {
         dict(M=70, N=36, K=128, batch=2, lda=132, ldc=40, sA=9300, sC=3000, cfg="8"),
         dict(M=70, N=36, K=256, batch=2, lda=260, ldc=40, sA=18300, sC=3000, cfg="10:2", layout="split"),
     ],
+    # fused epilogues: residual mode 2 (C += A W^T + bias) and the GEGLU GEMM
+    "gemm_fused": [
+        dict(case="gemm_nt", M=77, N=96, K=64, mode=2), dict(case="gemm_nt", M=130, N=257, K=320, mode=2),
+        dict(case="gemm_nt", M=300, N=200, K=256, cfg="7:2", mode=2, layout="split"),
+        dict(case="gemm_nt", M=60, N=40, K=100, layout="split", mode=2),
+        dict(case="gemm_geglu", M=77, F=48, K=64), dict(case="gemm_geglu", M=300, F=200, K=256, cfg="4"),
+        dict(case="gemm_geglu", M=130, F=100, K=96), dict(case="gemm_geglu", M=300, F=130, K=256, cfg="7", ldg=136),
+        dict(case="gemm_geglu", M=260, F=96, K=128, cfg="9", front=True),
+        dict(case="gemm_geglu", M=70, F=40, K=128, cfg="1", bias=False),
+    ],
     "gemm_nn": [
         dict(M=64, N=64, K=32), dict(M=100, N=72, K=96), dict(M=130, N=260, K=100, mode=1),
         dict(M=60, N=36, K=44, batch=3, lda=48, ldb=40, ldc=44, sA=3000, sB=1800, sC=2800),
@@ -74,6 +85,8 @@ FAMILIES = {
     "block": [
         dict(B=1, T=33, C=64, H=1, Tc=5, Cc=96, F=160),
         dict(B=2, T=64, C=128, H=2, Tc=77, Cc=256, F=256, masked=True),
+        dict(B=1, T=33, C=64, H=1, Tc=5, Cc=96, F=160, fused=True),
+        dict(B=2, T=64, C=128, H=2, Tc=77, Cc=256, F=256, masked=True, fused=True),
     ],
     "gguf_upload": [dict()],
 }
@@ -102,7 +115,7 @@ def emulator():
 
 @pytest.mark.parametrize("family", list(FAMILIES))
 def test_kernels_on_emulator(emulator, family):
-    specs = [dict(case=CASE_OF.get(family, family), schedules=BOTH, **s) for s in FAMILIES[family]]
+    specs = [dict({"case": CASE_OF.get(family, family)}, schedules=BOTH, **s) for s in FAMILIES[family]]
     with ThreadPoolExecutor(_workers()) as ex:
         results = list(ex.map(_run, specs))
     failed = []
