@@ -313,7 +313,8 @@ def gguf_upload(E, *, big_rows=10240, big_cols=1280, order=0, front=False):
     return 0.0
 
 
-CASES = {"gemm_nt": gemm_nt, "gemm_geglu": gemm_geglu, "gemm_nn": gemm_nn, "attention": attention, "block": block, "gguf_upload": gguf_upload}
+CASES = {"gemm_nt": gemm_nt, "gemm_geglu": gemm_geglu, "gemm_nn": gemm_nn, "attention": attention, "block": block,
+         "gguf_upload": gguf_upload}
 
 
 def main(argv):

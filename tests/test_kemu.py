@@ -134,7 +134,8 @@ PLANTED = {
                     dict(case="gemm_nt", M=300, N=200, K=128, cfg="7")),
     # the row kernel's per-step barrier removed (stage Q read before other waves wrote it)
     "missing_barrier": ("gemm_q8.hip",
-                        "        __syncthreads();\n#pragma unroll\n        for (int fn = 0; fn < FN - kTail; ++fn) wf[fn]",
+                        "        __syncthreads();\n#pragma unroll\n"
+                        "        for (int fn = 0; fn < FN - kTail; ++fn) wf[fn]",
                         "#pragma unroll\n        for (int fn = 0; fn < FN - kTail; ++fn) wf[fn]",
                         dict(case="gemm_nt", M=300, N=200, K=256, cfg="5")),
     # staged epilogue without the wave barrier between its LDS writes and reads
