@@ -255,6 +255,63 @@ def block(E, *, B, T, C, H, Tc, Cc, F, masked=False, blocks=2, order=0, front=Fa
     return e
 
 
+def q8(E, *, n, seed=1, front=False, order=0):
+    """Q8_0 decode (fp32 bit-exact, fp16 = RNE of it), repack to the split
+    layout and its decode, and the device quantiser, against the oracle."""
+    E.order(order)
+    w = ob.normal(seed, n, 0.0, 0.02)
+    if n >= 64:
+        w[:32] = 0.0                                   # an all-zero block
+        w[32:64] = np.arange(32, dtype=np.float32) - 15.5
+    blocks = ob.q8_0_quantize(w)
+    db = E.buf(blocks, front=front)
+    want = ob.q8_0_dequant(blocks, n)
+    o32, o16 = E.buf(nbytes=n * 4, front=front), E.buf(nbytes=n * 2, front=front)
+    E.call("mi_q8_0_dequant", db.ptr, o32.ptr, MI_F32, n, None)
+    E.call("mi_q8_0_dequant", db.ptr, o16.ptr, MI_F16, n, None)
+    assert np.array_equal(o32.get(np.uint32, n), want.view(np.uint32)), "q8_0 dequant fp32"
+    assert np.array_equal(o16.get(np.uint16, n), want.astype(np.float16).view(np.uint16)), "q8_0 dequant fp16"
+    dp, ds = E.buf(nbytes=n, front=front), E.buf(nbytes=n // 32 * 4, front=front)
+    E.call("mi_q8_0_to_split", db.ptr, dp.ptr, ds.ptr, n, None)
+    payload, scales = ob.q8_0_to_split(blocks, n)
+    assert np.array_equal(dp.get(np.int8, n), payload.view(np.int8)[:n]), "to_split payload"
+    assert np.array_equal(ds.get(np.uint32, n // 32), scales.view(np.uint32)), "to_split scales"
+    E.call("mi_q8_split_dequant", dp.ptr, ds.ptr, o32.ptr, MI_F32, n, None)
+    assert np.array_equal(o32.get(np.uint32, n), want.view(np.uint32)), "split dequant"
+    dw, dq = E.buf(w, front=front), E.buf(nbytes=n // 32 * 34, front=front)
+    E.call("mi_q8_0_quantize", dw.ptr, dq.ptr, n, None)
+    assert np.array_equal(dq.get(np.uint8, n // 32 * 34), blocks), "quantize"
+    return 0.0
+
+
+def glue(E, *, rows, d, affine=True, seed=1, front=False, order=0):
+    """LayerNorm (also in place), GEGLU (F = d / 2) and the residual add
+    against the oracle, to the GPU tests' bars."""
+    E.order(order)
+    x = ob.normal(seed, rows * d, 0.5, 3.0)
+    g = ob.normal(seed + 1, d, 1.0, 0.2) if affine else None
+    b = ob.normal(seed + 2, d, 0.0, 0.2) if affine else None
+    want = ob.layernorm(x, g, b, rows, d)
+    dx, dy = E.buf(x, front=front), E.buf(nbytes=x.nbytes, front=front)
+    dg, dbb = (E.buf(g, front=front), E.buf(b, front=front)) if affine else (None, None)
+    E.call("mi_layernorm", dx.ptr, dg.ptr if dg else None, dbb.ptr if dbb else None, dy.ptr, rows, d, 1e-5, None)
+    assert np.max(np.abs(dy.get(np.float32) - want)) <= 4e-6, "layernorm"
+    E.call("mi_layernorm", dx.ptr, dg.ptr if dg else None, dbb.ptr if dbb else None, dx.ptr, rows, d, 1e-5, None)
+    assert np.max(np.abs(dx.get(np.float32) - want)) <= 4e-6, "layernorm in place"
+    if d % 2 == 0:
+        F = d // 2
+        h = ob.normal(seed + 3, rows * 2 * F, 0.0, 2.0)
+        dh, dg2 = E.buf(h, front=front), E.buf(nbytes=rows * F * 4, front=front)
+        E.call("mi_geglu", dh.ptr, dg2.ptr, rows, F, None)
+        wg = ob.geglu(h, rows, F)
+        assert np.all(np.abs(dg2.get(np.float32) - wg) <= 2e-6 * (1 + np.abs(wg))), "geglu"
+    a1, a2 = ob.normal(seed + 4, rows * d), ob.normal(seed + 5, rows * d)
+    d1, d2 = E.buf(a1, front=front), E.buf(a2, front=front)
+    E.call("mi_add_inplace", d1.ptr, d2.ptr, rows * d, None)
+    assert np.array_equal(d1.get(np.float32), ob.add(a1, a2)), "add"
+    return 0.0
+
+
 def gguf_upload(E, *, big_rows=10240, big_cols=1280, order=0, front=False):
     """mi_gguf_upload_raw / _f32 / _q8_split of every tensor of the sample
     checkpoint plus a Q8_0 weight that crosses the 8 MiB staging buffers
@@ -314,7 +371,7 @@ def gguf_upload(E, *, big_rows=10240, big_cols=1280, order=0, front=False):
 
 
 CASES = {"gemm_nt": gemm_nt, "gemm_geglu": gemm_geglu, "gemm_nn": gemm_nn, "attention": attention, "block": block,
-         "gguf_upload": gguf_upload}
+         "gguf_upload": gguf_upload, "q8": q8, "glue": glue}
 
 
 def main(argv):

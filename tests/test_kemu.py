@@ -89,6 +89,9 @@ FAMILIES = {
         dict(B=2, T=64, C=128, H=2, Tc=77, Cc=256, F=256, masked=True, fused=True),
     ],
     "gguf_upload": [dict()],
+    "q8": [dict(n=32), dict(n=4096), dict(n=224, front=True)],
+    "glue": [dict(rows=9, d=1280), dict(rows=3, d=37, affine=False), dict(rows=1, d=4, affine=False),
+             dict(rows=5, d=4096, front=True)],
 }
 CASE_OF = {"gemm_lds": "gemm_nt", "gemm_rows": "gemm_nt"}
 
