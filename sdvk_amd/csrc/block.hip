@@ -64,12 +64,16 @@ int check_dims(const mi_block_dims& d, const char* fn) {
         if (st_ != MI_OK) return st_; \
     } while (0)
 
-int attention(const mi_block_dims& d, const float* q, const float* k, const float* v, float* o, uint32_t tk,
-              const int32_t* kv_len, hipStream_t s) {
+// ld: token stride of q, k and v (C, or 3C for the joint Q/K/V projection)
+int attention(const mi_block_dims& d, const float* q, const float* k, const float* v, uint64_t ld, float* o,
+              uint32_t tk, const int32_t* kv_len, hipStream_t s) {
     mi_attn_args x{};
     x.q = q;
     x.k = k;
     x.v = v;
+    x.ldq = ld;
+    x.ldk = ld;
+    x.ldv = ld;
     x.out = o;
     x.batch = d.batch;
     x.Tq = d.tokens;
@@ -80,6 +84,14 @@ int attention(const mi_block_dims& d, const float* q, const float* k, const floa
     x.out_dtype = MI_F32;
     x.kv_len = kv_len;
     return mi_fused_attention_ex(&x, s);
+}
+
+// Q, K and V weights stored back to back ([Wq; Wk; Wv], one 3C x C Q8_0
+// matrix) take one projection GEMM with N = 3C instead of three (a grid three
+// times wider: larger tiles fill the CUs); attention then reads Q / K / V from
+// the [rows, 3C] result at token stride 3C.
+bool adjacent(const void* a, const void* b, uint64_t bytes) {
+    return static_cast<const char*>(a) + bytes == static_cast<const char*>(b);
 }
 
 bool fused_epilogues() {
@@ -134,10 +146,18 @@ int forward(const mi_block_weights& w, const mi_block_dims& d, float* x, const f
 
     // self-attention
     MI_TRY(mi_layernorm(x, w.norm1_w, w.norm1_b, ws.n, rows, C, 1e-5f, s));
-    MI_TRY(gemm(ws.n, w.attn1_q, nullptr, ws.q, rows, C, C));
-    MI_TRY(gemm(ws.n, w.attn1_k, nullptr, ws.k, rows, C, C));
-    MI_TRY(gemm(ws.n, w.attn1_v, nullptr, ws.v, rows, C, C));
-    MI_TRY(attention(d, ws.q, ws.k, ws.v, ws.o, d.tokens, nullptr, s));
+    const uint64_t wcc = static_cast<uint64_t>(C) * (C / 32) * 34;  // bytes of one C x C Q8_0 matrix
+    // the joint result [rows, 3C] goes to the FF-up region, free until the FF stage
+    if (adjacent(w.attn1_q, w.attn1_k, wcc) && adjacent(w.attn1_k, w.attn1_v, wcc) &&
+        2ull * d.ff_inner >= 3ull * C) {
+        MI_TRY(gemm(ws.n, w.attn1_q, nullptr, ws.h, rows, 3 * C, C));
+        MI_TRY(attention(d, ws.h, ws.h + C, ws.h + 2 * C, 3ull * C, ws.o, d.tokens, nullptr, s));
+    } else {
+        MI_TRY(gemm(ws.n, w.attn1_q, nullptr, ws.q, rows, C, C));
+        MI_TRY(gemm(ws.n, w.attn1_k, nullptr, ws.k, rows, C, C));
+        MI_TRY(gemm(ws.n, w.attn1_v, nullptr, ws.v, rows, C, C));
+        MI_TRY(attention(d, ws.q, ws.k, ws.v, C, ws.o, d.tokens, nullptr, s));
+    }
     MI_TRY(residual(ws.o, w.attn1_out, w.attn1_out_b, C));
     // cross-attention over the context
     MI_TRY(mi_layernorm(x, w.norm2_w, w.norm2_b, ws.n, rows, C, 1e-5f, s));
@@ -149,7 +169,7 @@ int forward(const mi_block_weights& w, const mi_block_dims& d, float* x, const f
     } else {
         MI_TRY(ctx_kv(w, d, ctx, ws.k, ws.v, s));
     }
-    MI_TRY(attention(d, ws.q, ck, cv, ws.o, d.ctx_tokens, ctx_len, s));
+    MI_TRY(attention(d, ws.q, ck, cv, C, ws.o, d.ctx_tokens, ctx_len, s));
     MI_TRY(residual(ws.o, w.attn2_out, w.attn2_out_b, C));
     // GEGLU feed-forward
     MI_TRY(mi_layernorm(x, w.norm3_w, w.norm3_b, ws.n, rows, C, 1e-5f, s));

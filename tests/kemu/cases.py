@@ -196,7 +196,7 @@ def attention(E, *, batch=1, Tq, Tk, C, heads, causal=False, f16_in=False, f16_o
     return assert_parity(got, want, tol=tol, what="attention")
 
 
-def block(E, *, B, T, C, H, Tc, Cc, F, masked=False, blocks=2, order=0, front=False, fused=False):
+def block(E, *, B, T, C, H, Tc, Cc, F, masked=False, blocks=2, order=0, front=False, fused=False, qkv_joint=False):
     """Two applications of one SDXL transformer block: uncached
     (mi_sdxl_block_forward) vs context K / V projected once (mi_block_ctx_kv,
     mi_sdxl_block_forward_kv), both against the oracle's block."""
@@ -207,7 +207,15 @@ def block(E, *, B, T, C, H, Tc, Cc, F, masked=False, blocks=2, order=0, front=Fa
         os.environ.pop("MI_BLOCK_EPILOGUE", None)
     w = make_weights(ob, C, Cc, F, seed=500)
     dw = {k: E.buf(v, front=front) for k, v in w.items()}
-    bw = MiBlockWeights(*[dw[f[0]].ptr for f in MiBlockWeights._fields_])
+    ptrs = {k: b.ptr for k, b in dw.items()}
+    if qkv_joint:  # to_q / to_k / to_v back to back: the block takes one projection GEMM
+        joint = E.buf(np.concatenate([w["attn1_q"], w["attn1_k"], w["attn1_v"]]), front=front)
+        dw["_joint"] = joint
+        nb = w["attn1_q"].nbytes
+        ptrs.update(attn1_q=joint.ptr, attn1_k=joint.ptr + nb, attn1_v=joint.ptr + 2 * nb)
+    bw = MiBlockWeights(*[ptrs[f[0]] for f in MiBlockWeights._fields_])
+    # the same weights stored apart (three projection GEMMs)
+    bw_apart = MiBlockWeights(*[dw[f[0]].ptr for f in MiBlockWeights._fields_])
     dims = MiBlockDims(B, T, C, H, Tc, Cc, F)
     x = ob.normal(3, B * T * C)
     ctx = ob.normal(4, B * Tc * Cc).astype(np.float16).astype(np.float32)
@@ -235,6 +243,18 @@ def block(E, *, B, T, C, H, Tc, Cc, F, masked=False, blocks=2, order=0, front=Fa
     assert e_kv <= 1e-5, f"cached vs fresh K / V: {e_kv:.3e} x RMS(update)"
     e = float(np.max(np.abs(fresh - want)) / rms(want - x))
     assert e <= blocks * BLOCK_TOL, f"block vs oracle: {e:.3e} x RMS(update)"
+    if qkv_joint:
+        # one block: joint vs separate Q/K/V projections on the same build (the
+        # same MFMA sums unless a K split differs: a few ulps of |x|)
+        outs = []
+        for wts in (bw, bw_apart):
+            d1 = E.buf(x, front=front)
+            E.call("mi_sdxl_block_forward", ctypes.byref(wts), ctypes.byref(dims), d1.ptr, dc.ptr,
+                   dl.ptr if dl else None, ws.ptr, ws_bytes, None)
+            outs.append(d1.get(np.float32))
+        diff = float(np.max(np.abs(outs[0] - outs[1])))
+        ulp = float(np.spacing(np.float32(np.max(np.abs(outs[1])))))
+        assert diff <= 4 * ulp, f"joint vs separate Q/K/V: {diff:.3e} > 4 ulp ({ulp:.3e}) of max|x|"
     if fused:
         # one block, fused vs separate epilogues on the same build: they differ
         # only in the rounding order of the residual adds of K-split GEMMs

@@ -1,6 +1,7 @@
 """GPU checks of the fused block epilogues: GEMM mode 2 (C += A.W^T + bias,
 the residual add of sdvkgen.cpp:1746,1751,1762 folded into the GEMM) and the
-GEGLU GEMM (linear(ff_up) + geglu, sdvkgen.cpp:1709-1720, in one kernel).
+GEGLU GEMM (linear(ff_up) + geglu, sdvkgen.cpp:1709-1720, in one kernel); and
+the block's joint Q/K/V projection (to_q / to_k / to_v stored back to back).
 
 Bars: mode 2 to the GEMM bar on the update (C - C0); GEGLU against the
 oracle within the GEMM bar propagated through v * gelu(g), and against the
@@ -105,3 +106,38 @@ def test_block_fused_epilogues(gpu, oracle, monkeypatch, B, T, C, H, Tc, Cc, F, 
     print(f"  fused vs oracle err/rms(update) = {e:.3e}", flush=True)
     assert np.all(np.isfinite(outs["fused"])) and e <= BLOCK_TOL
     assert diff <= 4 * ulp
+
+
+def test_block_joint_qkv(gpu, oracle):
+    """to_q / to_k / to_v in one allocation, back to back: one projection GEMM
+    (N = 3C) and attention at token stride 3C; equal to the block with the
+    weights stored apart within 4 ulp of max|x|, and to the oracle's block."""
+    B, T, C, H, Tc, Cc, F = 2, 1024, 1280, 20, 77, 2048, 5120
+    print(f"[case] block joint qkv B={B} T={T} C={C}", flush=True)
+    w = make_weights(oracle, C, Cc, F, seed=500)
+    x = oracle.normal(3, B * T * C)
+    ctx = oracle.normal(4, B * Tc * Cc).astype(np.float16).astype(np.float32)
+    dims = ops.BlockDims(B, T, C, H, Tc, Cc, F)
+    dev, bw = to_device(w)
+    joint = DeviceBuffer.from_array(np.concatenate([w["attn1_q"], w["attn1_k"], w["attn1_v"]]))
+    nb = w["attn1_q"].nbytes
+    bw_joint = ops.BlockWeights(**dict(dev, attn1_q=joint.value, attn1_k=joint.value + nb,
+                                       attn1_v=joint.value + 2 * nb))
+    dc = DeviceBuffer.from_array(ctx)
+    ws = DeviceBuffer(ops.block_workspace_bytes(dims))
+    outs = []
+    for weights in (bw_joint, bw):
+        dx = DeviceBuffer.from_array(x)
+        ops.sdxl_block_forward(weights, dims, dx, dc, ws)
+        synchronize()
+        outs.append(dx.download(np.float32, x.size))
+    diff = float(np.max(np.abs(outs[0] - outs[1])))
+    ulp = float(np.spacing(np.float32(np.max(np.abs(outs[1])))))
+    print(f"  joint vs apart: {diff / ulp:.1f} ulp of max|x|", flush=True)
+    want = oracle.sdxl_block(w, x, ctx, batch=B, tokens=T, channels=C, heads=H, ctx_tokens=Tc, ctx_channels=Cc,
+                             ff_inner=F, threads=oracle.max_threads())
+    e = float(np.max(np.abs(outs[0] - want)) / rms(want - x))
+    print(f"  joint vs oracle err/rms(update) = {e:.3e}", flush=True)
+    assert np.all(np.isfinite(outs[0])) and e <= BLOCK_TOL
+    assert diff <= 4 * ulp
+

@@ -87,6 +87,9 @@ FAMILIES = {
         dict(B=2, T=64, C=128, H=2, Tc=77, Cc=256, F=256, masked=True),
         dict(B=1, T=33, C=64, H=1, Tc=5, Cc=96, F=160, fused=True),
         dict(B=2, T=64, C=128, H=2, Tc=77, Cc=256, F=256, masked=True, fused=True),
+        dict(B=2, T=64, C=128, H=2, Tc=77, Cc=256, F=256, masked=True, qkv_joint=True),
+        dict(B=1, T=33, C=64, H=1, Tc=5, Cc=96, F=160, qkv_joint=True, fused=True),
+        dict(B=1, T=33, C=64, H=1, Tc=5, Cc=96, F=64, qkv_joint=True),
     ],
     "gguf_upload": [dict()],
     "q8": [dict(n=32), dict(n=4096), dict(n=224, front=True)],
