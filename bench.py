@@ -147,7 +147,9 @@ class BlockStack:
 
     DIMS = (2, 1024, 1280, 20, 77, 2048, 5120)  # batch, tokens, channels, heads, ctx_tokens, ctx_channels, ff_inner
 
-    def __init__(self, rng, hip, ops, nblocks=10):
+    def __init__(self, rng, hip, ops, nblocks=10, joint_qkv=False):
+        """joint_qkv: each block's to_q / to_k / to_v weights in one allocation,
+        back to back, so the block runs one Q/K/V projection GEMM (N = 3C)."""
         B, T, C, H, Tc, Cc, F = self.DIMS
         self.ops, self.hip, self.nblocks = ops, hip, nblocks
         self.dims = ops.BlockDims(*self.DIMS)
@@ -161,18 +163,24 @@ class BlockStack:
         self.weights = []
         for i in range(nblocks):
             d = {}
+            qkv = hip.DeviceBuffer(3 * C * C // 32 * 34) if joint_qkv else None
             for j, (nm, (n, k)) in enumerate(shapes.items()):
                 cnt = n * k
                 off = ((i * len(shapes) + j) * 1000003 * 32) % (pool_n - cnt) // 32 * 32
-                d[nm] = hip.DeviceBuffer(cnt // 32 * 34)
+                if qkv is not None and nm in ("attn1_q", "attn1_k", "attn1_v"):
+                    d[nm] = qkv.value + ("attn1_q", "attn1_k", "attn1_v").index(nm) * (cnt // 32 * 34)
+                else:
+                    d[nm] = hip.DeviceBuffer(cnt // 32 * 34)
                 ops.q8_0_quantize(pool.value + 4 * off, d[nm], cnt)
+            if qkv is not None:
+                d["_qkv"] = qkv
             for nm, n in {"attn1_out_b": C, "attn2_out_b": C, "ff_up_b": 2 * F, "ff_down_b": C}.items():
                 d[nm] = hip.DeviceBuffer.from_array(rng.standard_normal(n, dtype=np.float32) * np.float32(0.02))
             for nm in ("norm1", "norm2", "norm3"):
                 d[nm + "_w"] = hip.DeviceBuffer.from_array(ones)
                 d[nm + "_b"] = hip.DeviceBuffer.from_array(zeros)
             self.keep.append(d)
-            self.weights.append(ops.BlockWeights(**d))
+            self.weights.append(ops.BlockWeights(**{k: v for k, v in d.items() if not k.startswith("_")}))
         self.x = hip.DeviceBuffer.from_array(rng.standard_normal(B * T * C, dtype=np.float32))
         self.ctx = hip.DeviceBuffer.from_array(
             rng.standard_normal(B * Tc * Cc, dtype=np.float32).astype(np.float16).astype(np.float32))
@@ -239,33 +247,104 @@ def time_case(c, stream, hip, reps):
                  "gbs": round(c.bytes / sec / 1e9, 1)}
 
 
-def extras(rng, hip, ops, stream, reps, stack):
-    """Measurements outside the step metric (after the timed region): BASELINE
-    config 0 (the reference harness's GEMM shape), the NN GEMM at the SDXL conv
-    shapes, and the config-4 stack with the context's K / V cached. Each part
-    reports its error instead of stopping the bench."""
-    out = {}
+# Row-stationary GEMM builds with row-coalesced A (MI_GEMM_CFG 7-10: 256 x 256,
+# 256 x 192, 256 x 160, 256 x 128 tiles): candidates for the default tile rules,
+# timed on every shape of the step and on config 0.
+GEMM_CANDIDATES = ["7", "8", "9", "10"]
+
+
+def _part(out, name, fn):
+    """out[name] = fn(), or the error it raised (reported, not fatal)."""
+    print(f"[bench:extras] {name}", file=sys.stderr, flush=True)
     try:
-        c = GemmCase(*CONFIG0, rng, hip, ops)
-        out["config0_gemm"] = time_case(c, stream, hip, reps)[1]
-        del c
+        out[name] = fn()
     except Exception as e:  # noqa: BLE001 -- reported, not fatal
-        out["config0_gemm"] = {"error": str(e)}
-    try:
-        nn = []
+        out[name] = {"error": f"{type(e).__name__}: {e}"}
+
+
+def extras(rng, hip, ops, stream, reps):
+    """Measurements outside the step metric: BASELINE config 0 (the reference
+    harness's GEMM shape), the NN GEMM at the SDXL conv shapes, the config-4
+    stack with the context's K / V cached, with the fused epilogues
+    (MI_BLOCK_EPILOGUE=fused), with joint Q/K/V weights and with all three, and
+    the candidate GEMM tile builds on every GEMM shape of the step. These
+    paths run in a child process (bench.py --extras-child): a failure there
+    cannot cost the step measurement."""
+    out = {}
+
+    def cfg0():
+        c = GemmCase(*CONFIG0, rng, hip, ops)
+        return time_case(c, stream, hip, reps)[1]
+
+    def nn():
+        res = []
         for t, M, N, K in NN_SHAPES:
-            c = NnCase(t, M, N, K, rng, hip, ops)
-            nn.append(time_case(c, stream, hip, reps)[1])
-            del c
-        out["nn_gemm"] = nn
-    except Exception as e:  # noqa: BLE001
-        out["nn_gemm"] = {"error": str(e)}
-    if stack is not None:
-        try:
-            out["block_stack_cached_kv"] = stack.measure(stream, 5, cached_kv=True)
-        except Exception as e:  # noqa: BLE001
-            out["block_stack_cached_kv"] = {"error": str(e)}
+            res.append(time_case(NnCase(t, M, N, K, rng, hip, ops), stream, hip, reps)[1])
+        return res
+
+    def stack(cached_kv=False, fused=False, joint_qkv=False):
+        def run():
+            prev = os.environ.get("MI_BLOCK_EPILOGUE")
+            if fused:
+                os.environ["MI_BLOCK_EPILOGUE"] = "fused"
+            try:
+                st = BlockStack(rng, hip, ops, joint_qkv=joint_qkv)
+                res = st.measure(stream, 5, cached_kv=cached_kv)
+                res["variant"] = {"cached_kv": cached_kv, "fused_epilogues": fused, "joint_qkv": joint_qkv}
+                del st
+                return res
+            finally:
+                if prev is None:
+                    os.environ.pop("MI_BLOCK_EPILOGUE", None)
+                else:
+                    os.environ["MI_BLOCK_EPILOGUE"] = prev
+        return run
+
+    def candidates():
+        cases = [GemmCase(t, M, N, K, rng, hip, ops) for t, M, N, K in GEMM_SHAPES + [CONFIG0]]
+        res = {}
+        for cfg in GEMM_CANDIDATES:
+            os.environ["MI_GEMM_CFG"] = cfg
+            try:
+                res[cfg] = [{"shape": c.tag, "us": e["us"], "pct_of_roofline": e["pct_of_roofline"]}
+                            for c in cases for e in [time_case(c, stream, hip, reps)[1]]]
+            finally:
+                os.environ.pop("MI_GEMM_CFG", None)
+        return res
+
+    _part(out, "config0_gemm", cfg0)
+    _part(out, "nn_gemm", nn)
+    _part(out, "block_stack_cached_kv", stack(cached_kv=True))
+    _part(out, "block_stack_fused_epilogues", stack(fused=True))
+    _part(out, "block_stack_joint_qkv", stack(joint_qkv=True))
+    _part(out, "block_stack_fused_joint_cached", stack(cached_kv=True, fused=True, joint_qkv=True))
+    _part(out, "gemm_candidates", candidates)
     return out
+
+
+def extras_child_main(reps: int) -> int:
+    from sdvk_amd import _lib, hip, ops
+
+    _lib.load()
+    rng = np.random.default_rng(2)
+    stream = hip.Stream()
+    print(json.dumps(extras(rng, hip, ops, stream, reps)), flush=True)
+    return 0
+
+
+def run_extras_child(reps: int, timeout_s: int = 420) -> dict:
+    """bench.py --extras-child in a child process; its JSON line, or the error."""
+    import subprocess
+
+    cmd = [sys.executable, str(Path(__file__).resolve()), "--extras-child", "--reps", str(reps)]
+    try:
+        r = subprocess.run(cmd, stdout=subprocess.PIPE, text=True, timeout=timeout_s, cwd=str(ROOT))
+    except subprocess.TimeoutExpired:
+        return {"error": f"extras child exceeded {timeout_s} s"}
+    lines = [l for l in r.stdout.splitlines() if l.startswith("{")]
+    if r.returncode != 0 or not lines:
+        return {"error": f"extras child exited with status {r.returncode}"}
+    return json.loads(lines[-1])
 
 
 def roofline_pct(c, seconds):
@@ -324,9 +403,13 @@ def main() -> int:
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run one device-to-device copy of this many MiB first (profiler byte calibration)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true", help="skip the measurements outside the step metric")
+    ap.add_argument("--extras-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--only", choices=["gemm", "attention", "block"], default=None,
                     help="run one part only (profiling): a kernel family, or the config-4 block stack")
     args = ap.parse_args()
+    if args.extras_child:
+        return extras_child_main(args.reps)
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (multi-GPU sharding is "
                                    "design-only, see DESIGN.md)"}))
@@ -443,17 +526,19 @@ def main() -> int:
         print(f"[bench] block stack: {block['latency_ms']:.3f} ms for {block['blocks']} blocks "
               f"({block['tflops']:.1f} TFLOP/s)", file=sys.stderr, flush=True)
 
-    more = None
-    if args.only is None:
-        print("[bench] extras: config 0, NN GEMM conv shapes, cached-K/V block stack", file=sys.stderr, flush=True)
-        more = extras(rng, hip, ops, stream, args.reps, stack)
-        del stack
+    del stack
 
     cpu = None
     if not args.no_cpu_baseline and args.only is None:
         threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
         print(f"[bench] cpu baseline on {threads} threads", file=sys.stderr, flush=True)
         cpu = cpu_baseline(threads)
+
+    more = None
+    if args.only is None and not args.no_extras:
+        print("[bench] extras (child process): config 0, NN GEMM conv shapes, block-stack variants, candidate "
+              "GEMM tiles", file=sys.stderr, flush=True)
+        more = run_extras_child(args.reps)
 
     out = {
         "metric": "Q8_0 GEMM & fused-attn TFLOP/s at SDXL-1024 shapes; % of MFMA peak",

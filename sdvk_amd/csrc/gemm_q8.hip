@@ -138,6 +138,31 @@ __device__ __forceinline__ void interleave_step() {
     }
 }
 
+// One register set (PF = 1): the store phase consumes the loads issued at the
+// start of the same step, so it may only begin after the first NHEAD MFMAs
+// (which carry the fragment reads); the rest of the MFMAs each carry a share
+// of the conversions, dequantisation and LDS writes. Left to itself the
+// compiler hoists the conversions next to the loads and the wave waits out the
+// whole memory latency with one MFMA issued.
+template <int NMFMA, int NHEAD, int NREAD0, int NREAD, int NVALU, int NWRITE>
+__device__ __forceinline__ void interleave_step_tail() {
+    static_assert(NHEAD > 0 && NHEAD < NMFMA, "head and tail both hold MFMAs");
+    constexpr int kTail = NMFMA - NHEAD;
+    __builtin_amdgcn_sched_group_barrier(0x100, NREAD0, 0);
+#pragma unroll
+    for (int i = 0; i < NHEAD; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, (NREAD + NMFMA - 1) / NMFMA, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < kTail; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, (NREAD + NMFMA - 1) / NMFMA, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, (NVALU + kTail - 1) / kTail, 0);
+        __builtin_amdgcn_sched_group_barrier(0x200, (NWRITE + kTail - 1) / kTail, 0);
+    }
+}
+
 // ---- epilogue ---------------------------------------------------------------------
 //
 // Non-split: a wave's FM x FN accumulator tiles (32 x 32 each, transposed
@@ -372,11 +397,15 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     // start; the row stride is 0 mod 4 (K % 64 == 0) and a step advances 68
     // bytes, so a block's position inside its window (0 or 2 bytes) is fixed
     // for the lane. v_perm selectors pick d and the eight q dwords for either.
+    // Threads past the step's W_BLOCKS blocks load a duplicate (block
+    // wb mod W_BLOCKS) and store nothing: a load under a branch makes the
+    // compiler's wait counts assume it was skipped, so every later wait would
+    // also retire the loads of the step just issued.
     uint32_t wb_off[WB_IT], wb_qsel[WB_IT], wb_dsel[WB_IT];
     uint32_t wbx_[PF][WB_IT][9];
 #pragma unroll
     for (int i = 0; i < WB_IT; ++i) {
-        const int wb = tid + i * NT;
+        const int wb = (tid + i * NT) % W_BLOCKS;
         const uint32_t n = EPI == kEpiGeglu ? geglu_wrow(n0, wb % BN, a.F) : min(n0 + wb % BN, a.N - 1);
         const uint32_t byte = n * a.rowbytes + (wb / BN) * 34;
         wb_off[i] = byte & ~3u;
@@ -403,15 +432,13 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
             const uint32_t soff = ks * (KB * 34);
 #pragma unroll
             for (int i = 0; i < WB_IT; ++i) {
-                if (W_BLOCKS % NT == 0 || tid + i * NT < W_BLOCKS) {
-                    const auto x0 = __builtin_amdgcn_raw_buffer_load_b128(rW, wb_off[i], soff, 0);
-                    const auto x1 = __builtin_amdgcn_raw_buffer_load_b128(rW, wb_off[i] + 16, soff, 0);
-                    wbx_[rs][i][8] = __builtin_amdgcn_raw_buffer_load_b32(rW, wb_off[i] + 32, soff, 0);
+                const auto x0 = __builtin_amdgcn_raw_buffer_load_b128(rW, wb_off[i], soff, 0);
+                const auto x1 = __builtin_amdgcn_raw_buffer_load_b128(rW, wb_off[i] + 16, soff, 0);
+                wbx_[rs][i][8] = __builtin_amdgcn_raw_buffer_load_b32(rW, wb_off[i] + 32, soff, 0);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        wbx_[rs][i][e] = x0[e];
-                        wbx_[rs][i][4 + e] = x1[e];
-                    }
+                for (int e = 0; e < 4; ++e) {
+                    wbx_[rs][i][e] = x0[e];
+                    wbx_[rs][i][4 + e] = x1[e];
                 }
             }
         }
@@ -578,17 +605,13 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
             __builtin_amdgcn_sched_barrier(0);
             compute(S0{});
             store_step(S0{}, S1{});
-#ifdef MI_GEMM_PF1_INTERLEAVE
-            interleave_step<kMfma, kRead0, kReads - kRead0, kValu, kWrites>();
-#endif
+            interleave_step_tail<kMfma, kMfma * 3 / 4, kRead0, kReads - kRead0, kValu, kWrites>();
             __syncthreads();
             load_step(phys(min(j + 2, last)), S0{});
             __builtin_amdgcn_sched_barrier(0);
             compute(S1{});
             store_step(S0{}, S0{});
-#ifdef MI_GEMM_PF1_INTERLEAVE
-            interleave_step<kMfma, kRead0, kReads - kRead0, kValu, kWrites>();
-#endif
+            interleave_step_tail<kMfma, kMfma * 3 / 4, kRead0, kReads - kRead0, kValu, kWrites>();
             __syncthreads();
         }
     }
@@ -1098,7 +1121,17 @@ void launch(int cfg, const GemmArgs& a, uint32_t batch, uint32_t splits, hipStre
         case kC256x128: launch_cfg<256, 128, 4, 2, 2, WK, false, 2, EPI>(a, batch, splits, s); break;
         case kC128x128: launch_cfg<128, 128, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, s); break;
         case kC128x64: launch_cfg<128, 64, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, s); break;
-        case kC256x256: launch_cfg<256, 256, 4, 2, 2, WK, false, 1, EPI>(a, batch, splits, s); break;
+        case kC256x256:
+            // The split layout's and the GEGLU epilogue's 256x256 builds need
+            // more than the 256 VGPRs of a wave at two waves per SIMD: the
+            // compiler spills LDS addresses inside the K loop, and every
+            // scratch reload waits for all global loads in flight. They run
+            // 256x128 tiles instead.
+            if constexpr (WK == kSplit || EPI == kEpiGeglu)
+                launch_cfg<256, 128, 4, 2, 2, WK, false, 2, EPI>(a, batch, splits, s);
+            else
+                launch_cfg<256, 256, 4, 2, 2, WK, false, 1, EPI>(a, batch, splits, s);
+            break;
         default: launch_cfg<64, 64, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, s); break;
     }
 }

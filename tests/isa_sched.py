@@ -1,0 +1,95 @@
+"""Static checks of the gfx950 code the compiler makes of the product kernels.
+
+Parity tests cannot see a software pipeline that the compiler has undone: a
+load hoisted next to its consumer, a wait count made conservative by a load
+under a branch, a register spill inside the K loop (a scratch reload waits for
+every global load in flight). Those show up only as time on the GPU. This
+module compiles a source to gfx950 assembly (the same flags as the product
+build) and measures, for every loop that issues MFMAs, how many MFMAs the wave
+issues between each global load and the `s_waitcnt vmcnt` that retires it
+(vector-memory counters retire in issue order), and whether the loop touches
+scratch.
+"""
+from __future__ import annotations
+
+import re
+import subprocess
+import sys
+from dataclasses import dataclass
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parents[1]
+CSRC = ROOT / "sdvk_amd" / "csrc"
+sys.path.insert(0, str(ROOT))
+
+
+@dataclass
+class Loop:
+    kernel: str          # mangled name
+    label: str
+    instructions: int
+    mfma: int
+    loads: int
+    scratch: int
+    distances: list      # MFMAs issued between a load and the wait that retires it (steady state)
+
+    @property
+    def min_distance(self) -> int | None:
+        return min(self.distances) if self.distances else None
+
+
+def compile_asm(source: str, out: Path) -> Path:
+    """gfx950 assembly of one product source, built with the product's flags."""
+    from sdvk_amd import build as b
+
+    flags = [f for f in b.HIPCC_FLAGS if f not in ("-shared", "-fPIC")]
+    cmd = [b.hipcc(), *flags, *b.EXTRA_FLAGS.get(source, []), "--cuda-device-only", "-S", f"-I{ROOT / 'include'}",
+           f"-I{CSRC}", str(CSRC / source), "-o", str(out)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc -S {source} failed:\n{r.stderr[-3000:]}")
+    return out
+
+
+def _is_load(ins: str) -> bool:
+    return ins.startswith(("buffer_load", "global_load", "scratch_load", "flat_load"))
+
+
+def loops(asm_path: Path) -> list[Loop]:
+    """Every loop (LLVM's 'Loop Header' blocks, up to the branch back) that issues MFMAs."""
+    text = asm_path.read_text()
+    found = []
+    for part in re.split(r"\n(?=_Z\S+:\s*; @)", text):
+        m = re.match(r"(_Z\S+):", part)
+        if not m:
+            continue
+        body = part.split(".Lfunc_end")[0].split("\n")
+        for i, line in enumerate(body):
+            if "Loop Header" not in line:
+                continue
+            label = line.split(":")[0]
+            j = i + 1
+            while j < len(body) and not (re.match(r"\s*s_c?branch", body[j]) and body[j].strip().endswith(label)):
+                j += 1
+            ins = [x.strip() for x in body[i + 1:j]]
+            ins = [x for x in ins if x and not x.startswith((";", "."))]
+            nm = sum("v_mfma" in x for x in ins)
+            if nm == 0:
+                continue
+            # two passes over the body: the second one is the steady state
+            outstanding, mf, dist = [], 0, []
+            for k, x in enumerate(ins + ins):
+                if _is_load(x):
+                    outstanding.append(mf)
+                elif "v_mfma" in x:
+                    mf += 1
+                else:
+                    w = re.search(r"vmcnt\((\d+)\)", x)
+                    if w:
+                        while len(outstanding) > int(w.group(1)):
+                            issued = outstanding.pop(0)
+                            if k >= len(ins):
+                                dist.append(mf - issued)
+            found.append(Loop(m.group(1), label, len(ins), nm, sum(_is_load(x) for x in ins),
+                              sum("scratch_" in x for x in ins), dist))
+    return found

@@ -1,0 +1,160 @@
+"""bench.py's host logic on the CPU, over a stand-in device layer.
+
+No GPU here, so the bench's own Python (case set-up, the timed loop's event
+bookkeeping, the roofline / breakdown / block-stack / extras assembly and the
+JSON line) would otherwise first run at the end of a round. The stand-in
+`hip` hands out fake device addresses and fixed event times; every `ops` call
+is bound against the real `sdvk_amd.ops` signature, so a wrong argument name
+or count fails here. Nothing is computed.
+"""
+from __future__ import annotations
+
+import inspect
+import json
+import sys
+import types
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+sys.path.insert(0, str(ROOT))
+
+
+class _Buf:
+    _next = 1 << 32
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        self.value = _Buf._next
+        _Buf._next += (self.nbytes + 255) // 256 * 256 + 256
+
+    @classmethod
+    def from_array(cls, a):
+        return cls(np.asarray(a).nbytes)
+
+    def fill_zero(self, stream=None):
+        pass
+
+    def copy_from(self, src, nbytes, stream=None):
+        assert nbytes <= self.nbytes
+
+    def upload(self, a, offset=0):
+        pass
+
+
+class _Stream:
+    def synchronize(self):
+        pass
+
+
+class _Event:
+    t = 0.0
+
+    def __init__(self):
+        self.at = None
+
+    def record(self, stream=None):
+        _Event.t += 0.25
+        self.at = _Event.t
+
+    def synchronize(self):
+        pass
+
+    def elapsed_ms(self, end):
+        assert self.at is not None and end.at is not None
+        return end.at - self.at
+
+
+def _fake_hip():
+    m = types.SimpleNamespace(DeviceBuffer=_Buf, Stream=_Stream, Event=_Event, device_count=lambda: 1,
+                              device_name=lambda d=0: "stand-in", synchronize=lambda: None)
+    return m
+
+
+def _fake_ops(calls):
+    from sdvk_amd import ops as real
+
+    def wrap(name):
+        sig = inspect.signature(getattr(real, name))
+
+        def f(*a, **k):
+            sig.bind(*a, **k)
+            calls.append(name)
+            if name in ("block_workspace_bytes", "block_ctx_kv_bytes"):
+                return 1 << 20
+            return None
+        return f
+
+    names = [n for n, v in vars(real).items() if inspect.isfunction(v) and v.__module__ == real.__name__]
+    ns = {n: wrap(n) for n in names}
+    ns.update(BlockDims=real.BlockDims, BlockWeights=real.BlockWeights)
+    return types.SimpleNamespace(**ns)
+
+
+@pytest.fixture
+def fake_device(monkeypatch):
+    import sdvk_amd
+    from sdvk_amd import _lib
+
+    calls = []
+    monkeypatch.setattr(sdvk_amd, "hip", _fake_hip(), raising=False)
+    monkeypatch.setattr(sdvk_amd, "ops", _fake_ops(calls), raising=False)
+    monkeypatch.setattr(_lib, "load", lambda: None)
+    return calls
+
+
+def test_bench_line_on_stand_in_device(fake_device, monkeypatch, capsys):
+    import bench
+
+    # the extras child runs in-process here (same code path, no subprocess)
+    def child(reps, timeout_s=420):
+        from sdvk_amd import hip, ops
+        return bench.extras(np.random.default_rng(2), hip, ops, hip.Stream(), reps)
+
+    monkeypatch.setattr(bench, "run_extras_child", child)
+    monkeypatch.setattr(sys, "argv", ["bench.py", "--steps", "2", "--warmup", "1", "--reps", "2",
+                                      "--no-cpu-baseline"])
+    assert bench.main() == 0
+    lines = [l for l in capsys.readouterr().out.splitlines() if l.startswith("{")]
+    assert len(lines) == 1
+    out = json.loads(lines[0])
+    for key in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better",
+                "scaling", "vs_baseline", "dtype", "data", "config", "roofline", "cpu_baseline"):
+        assert key in out, key
+    assert out["n_gpus"] == 1 and out["steps"] == 2 and out["value"] > 0
+    r = out["roofline"]
+    assert r["bound"] == "mfma" and r["unit"] == "TFLOP/s" and 0 < r["frac"] == pytest.approx(r["achieved"] / r["peak"],
+                                                                                            rel=1e-3)
+    assert len(out["breakdown"]) == len(bench.GEMM_SHAPES) + len(bench.ATTN_SHAPES)
+    assert out["block_stack"]["blocks"] == 10
+    ex = out["extras"]
+    for part in ("config0_gemm", "nn_gemm", "block_stack_cached_kv", "block_stack_fused_epilogues",
+                 "block_stack_joint_qkv", "block_stack_fused_joint_cached", "gemm_candidates"):
+        assert part in ex and "error" not in ex[part], (part, ex.get(part))
+    assert set(ex["gemm_candidates"]) == set(bench.GEMM_CANDIDATES)
+    assert ex["block_stack_fused_joint_cached"]["variant"] == {"cached_kv": True, "fused_epilogues": True,
+                                                               "joint_qkv": True}
+    for name in ("gemm_nt_q8_0", "fused_attention_ex", "gemm_nn_q8", "sdxl_block_forward", "block_ctx_kv",
+                 "sdxl_block_forward_kv", "q8_0_quantize"):
+        assert name in fake_device, name
+
+
+def test_joint_qkv_weights_are_back_to_back(fake_device):
+    import bench
+    from sdvk_amd import hip, ops
+
+    st = bench.BlockStack(np.random.default_rng(0), hip, ops, nblocks=2, joint_qkv=True)
+    C = bench.BlockStack.DIMS[2]
+    nb = C * C // 32 * 34
+    for w in st.weights:
+        assert w.attn1_k == w.attn1_q + nb and w.attn1_v == w.attn1_k + nb
+
+
+def test_gpus_above_one_exits_with_a_message(monkeypatch, capsys):
+    import bench
+
+    monkeypatch.setattr(sys, "argv", ["bench.py", "--gpus", "2"])
+    assert bench.main() == 2
+    assert "one GPU" in capsys.readouterr().out

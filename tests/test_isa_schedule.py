@@ -1,0 +1,56 @@
+"""The compiled K loops keep their software pipelines (CPU: gfx950 assembly of
+the product sources, analysed by tests/isa_sched.py).
+
+For every loop that issues MFMAs in the GEMM and attention kernels:
+  * no scratch access (a spilled register reloaded inside the loop waits for
+    every global load in flight);
+  * every global load has at least a quarter of the loop's MFMAs (half a K
+    step: the loops run two steps per trip) issued between it and the wait
+    that retires it. A load under a branch, or a consumer hoisted next to its
+    load, drops this to 0-2 and the wave then sits out the memory latency.
+Excluded: the attention kernel's scalar-load build (head dims that are not a
+multiple of 8, or unaligned tensors; no SDXL shape takes it).
+"""
+from __future__ import annotations
+
+import shutil
+
+import pytest
+
+import isa_sched
+
+CASES = {
+    "gemm_q8.hip": ("gemm_q8_kernel", "gemm_q8_rows_kernel"),
+    "attention.hip": ("attn_f16_kernel", "attn_kernel"),
+}
+
+
+def _excluded(kernel: str) -> bool:
+    # attn_kernel<TI, TO, VEC = false>: element-wise loads for unaligned inputs
+    return "attn_kernel" in kernel and kernel.endswith("Lb0EEEvNS0_8AttnArgsE")
+
+
+@pytest.fixture(scope="module")
+def asm(tmp_path_factory):
+    from sdvk_amd import build as b
+
+    if shutil.which(b.hipcc()) is None:
+        pytest.skip("no hipcc for the gfx950 assembly")
+    d = tmp_path_factory.mktemp("isa")
+    return {src: isa_sched.loops(isa_sched.compile_asm(src, d / (src + ".s"))) for src in CASES}
+
+
+@pytest.mark.parametrize("src", list(CASES))
+def test_k_loops_keep_loads_ahead_of_their_waits(asm, src):
+    loops = [l for l in asm[src] if any(k in l.kernel for k in CASES[src]) and not _excluded(l.kernel)]
+    assert loops, f"no MFMA loops found in {src}"
+    bad = []
+    for l in loops:
+        need = max(1, l.mfma // 4)
+        if l.scratch:
+            bad.append(f"{l.kernel} {l.label}: {l.scratch} scratch accesses in the loop")
+        if l.loads and (l.min_distance is None or l.min_distance < need):
+            bad.append(f"{l.kernel} {l.label}: a load is waited for {l.min_distance} MFMAs after issue "
+                       f"(loop of {l.mfma} MFMAs; want >= {need})")
+    print(f"{src}: {len(loops)} loops checked")
+    assert not bad, "\n".join(bad)
