@@ -247,10 +247,11 @@ def time_case(c, stream, hip, reps):
                  "gbs": round(c.bytes / sec / 1e9, 1)}
 
 
-# Row-stationary GEMM builds with row-coalesced A (MI_GEMM_CFG 7-10: 256 x 256,
-# 256 x 192, 256 x 160, 256 x 128 tiles): candidates for the default tile rules,
-# timed on every shape of the step and on config 0.
-GEMM_CANDIDATES = ["7", "8", "9", "10"]
+# Candidates for the default tile rules, timed on every shape of the step and on
+# config 0: the row-stationary builds with row-coalesced A (MI_GEMM_CFG 7-10:
+# 256 x 256, 256 x 192, 256 x 160, 256 x 128 tiles) and the 4-wave 256 x 256 LDS
+# build (11); "4" is the 8-wave 256 x 256 LDS build the rules pick for tall grids.
+GEMM_CANDIDATES = ["7", "8", "9", "10", "11", "4"]
 
 
 def _part(out, name, fn):

@@ -1006,6 +1006,7 @@ enum CfgId {
     kC256x128 = 0, kC128x128, kC128x64, kC64x64, kC256x256,  // LDS kernel (gemm_q8_kernel)
     kR256x256, kR256x128,                                     // row kernel, per-lane-row A loads
     kR256x256Q, kR256x192Q, kR256x160Q, kR256x128Q,           // row kernel, row-coalesced A
+    kC256x256W4,                                              // LDS kernel, 4 waves of 128x128, two sets in flight
     kNumCfg
 };
 
@@ -1059,12 +1060,14 @@ uint32_t pick_group(uint32_t tm, uint32_t tn, uint32_t BM, uint32_t BN, uint32_t
     return best;
 }
 
-template <int BM, int BN, int WM, int WN, int KB, int WK, bool KTAIL, int PF = 2, int EPI = kEpiPlain>
+// SPLIT = false: a build without a K-split variant (requested splits are ignored).
+template <int BM, int BN, int WM, int WN, int KB, int WK, bool KTAIL, int PF = 2, int EPI = kEpiPlain,
+          bool SPLIT = true>
 void launch_cfg(const GemmArgs& a0, uint32_t batch, uint32_t splits, hipStream_t s) {
     GemmArgs a = a0;
     // GEGLU: BN / 2 outputs per tile, and the epilogue needs the whole K sum
     a.tiles_n = EPI == kEpiGeglu ? ceil_div(a.F, BN / 2) : ceil_div(a.N, BN);
-    if (EPI == kEpiGeglu) splits = 1;
+    if (EPI == kEpiGeglu || !SPLIT) splits = 1;
     a.tiles_m = ceil_div(a.M, BM);
     a.group_m = pick_group(a.tiles_m, a.tiles_n, BM, BN, a.K);
     a.ksteps = ceil_div(a.K, 32 * KB);
@@ -1075,7 +1078,7 @@ void launch_cfg(const GemmArgs& a0, uint32_t batch, uint32_t splits, hipStream_t
     }
     if (splits > 1) {
         prepare_split<EPI>(a, batch, s);
-        if constexpr (EPI != kEpiGeglu)
+        if constexpr (EPI != kEpiGeglu && SPLIT)
             gemm_q8_kernel<BM, BN, WM, WN, KB, WK, true, KTAIL, PF><<<dim3(tiles, splits, batch), WM * WN * 64, 0, s>>>(a);
     } else {
         a.steps_per_split = a.ksteps;
@@ -1120,6 +1123,11 @@ void launch(int cfg, const GemmArgs& a, uint32_t batch, uint32_t splits, hipStre
         case kR256x128: launch_rows<4, WK, false, EPI>(a, batch, splits, s); break;
         case kC256x128: launch_cfg<256, 128, 4, 2, 2, WK, false, 2, EPI>(a, batch, splits, s); break;
         case kC128x128: launch_cfg<128, 128, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, s); break;
+        case kC256x256W4:
+            // one wave per SIMD with 128 x 128 per wave (256 accumulator AGPRs)
+            // and one register set; its K-split build would spill in the loop
+            launch_cfg<256, 256, 2, 2, 2, WK, false, 1, EPI, false>(a, batch, splits, s);
+            break;
         case kC128x64: launch_cfg<128, 64, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, s); break;
         case kC256x256:
             // The split layout's and the GEGLU epilogue's 256x256 builds need

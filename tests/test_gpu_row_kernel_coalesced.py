@@ -1,7 +1,9 @@
-"""GPU parity of the row-stationary Q8_0 GEMM with row-coalesced A loads and
-the quad transpose (MI_GEMM_CFG=7..10: 256 x 256 / 192 / 160 / 128 tiles; not
-chosen by the tile rules until measured faster), against the CPU oracle: the same bar and cases as the other
-tile configurations (tests/test_gpu_gemm.py)."""
+"""GPU parity of the candidate Q8_0 GEMM builds that the tile rules do not
+choose until measured faster, against the CPU oracle (the same bar and cases as
+the other tile configurations, tests/test_gpu_gemm.py): the row-stationary
+kernel with row-coalesced A loads and the quad transpose (MI_GEMM_CFG=7..10:
+256 x 256 / 192 / 160 / 128 tiles) and the 4-wave 256 x 256 LDS kernel
+(MI_GEMM_CFG=11, one wave per SIMD, no K split)."""
 import numpy as np
 import pytest
 
@@ -13,7 +15,7 @@ from test_gpu_gemm import run_q8_0
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("cfg", ["7", "7:2", "8", "9:3", "10"])  # 256x256, 256x192, 256x160, 256x128
+@pytest.mark.parametrize("cfg", ["7", "7:2", "8", "9:3", "10", "11"])  # 256x256, 256x192, 256x160, 256x128; 4-wave 256x256
 @pytest.mark.parametrize("M,N,K", [(300, 200, 640), (1030, 130, 256), (257, 512, 128)])
 def test_coalesced_rows_config(gpu, oracle, monkeypatch, cfg, M, N, K):
     print(f"[case] cfg={cfg} M={M} N={N} K={K}", flush=True)
@@ -35,10 +37,11 @@ def test_coalesced_rows_config(gpu, oracle, monkeypatch, cfg, M, N, K):
     assert_parity(dC.download(np.float32, M * N).reshape(M, N), want, what=f"cfg {cfg} split layout")
 
 
-def test_coalesced_rows_baseline_shape(gpu, oracle, monkeypatch):
+@pytest.mark.parametrize("cfg", ["7", "11"])
+def test_candidate_config_baseline_shape(gpu, oracle, monkeypatch, cfg):
     M, N, K = 9216, 1280, 1280
-    print(f"[case] cfg=7 baseline M={M} N={N} K={K}", flush=True)
-    monkeypatch.setenv("MI_GEMM_CFG", "7")
+    print(f"[case] cfg={cfg} baseline M={M} N={N} K={K}", flush=True)
+    monkeypatch.setenv("MI_GEMM_CFG", cfg)
     A = oracle.normal(1, M * K)
     blocks = q8_weights(oracle, 2, N, K)
     got = run_q8_0(A, blocks, M, N, K).reshape(M, N)

@@ -49,6 +49,9 @@ FAMILIES = {
         dict(M=300, N=300, K=256, cfg="4"), dict(M=200, N=300, K=512, cfg="0:3"),
         dict(M=70, N=36, K=64, batch=3, lda=72, ldc=40, sA=5200, sC=3000),
         dict(M=70, N=36, K=128, batch=2, lda=132, ldc=40, sA=9300, sC=3000, cfg="4:2", mode=1),
+        # 4-wave 256x256 (one wave per SIMD, 128x128 per wave); a requested split is ignored
+        dict(M=300, N=300, K=256, cfg="11"), dict(M=260, N=130, K=192, cfg="11:2", layout="split", mode=1),
+        dict(M=70, N=36, K=128, batch=2, lda=132, ldc=40, sA=9300, sC=3000, cfg="11", front=True),
     ],
     # row-stationary kernel: per-lane-row A (5, 6) and row-coalesced A (7-10)
     "gemm_rows": [
@@ -68,6 +71,7 @@ FAMILIES = {
         dict(case="gemm_geglu", M=130, F=100, K=96), dict(case="gemm_geglu", M=300, F=130, K=256, cfg="7", ldg=136),
         dict(case="gemm_geglu", M=260, F=96, K=128, cfg="9", front=True),
         dict(case="gemm_geglu", M=70, F=40, K=128, cfg="1", bias=False),
+        dict(case="gemm_nt", M=300, N=200, K=256, cfg="11", mode=2), dict(case="gemm_geglu", M=300, F=130, K=256, cfg="11"),
     ],
     "gemm_nn": [
         dict(M=64, N=64, K=32), dict(M=100, N=72, K=96), dict(M=130, N=260, K=100, mode=1),
