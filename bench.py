@@ -247,11 +247,13 @@ def time_case(c, stream, hip, reps):
                  "gbs": round(c.bytes / sec / 1e9, 1)}
 
 
-# Candidates for the default tile rules, timed on every shape of the step and on
-# config 0: the row-stationary builds with row-coalesced A (MI_GEMM_CFG 7-10:
-# 256 x 256, 256 x 192, 256 x 160, 256 x 128 tiles) and the 4-wave 256 x 256 LDS
-# build (11); "4" is the 8-wave 256 x 256 LDS build the rules pick for tall grids.
-GEMM_CANDIDATES = ["7", "8", "9", "10", "11", "4"]
+# Every tile build (MI_GEMM_CFG "<cfg>[:<K splits>]"), timed on every GEMM shape
+# of the step and on config 0, so the tile rules can be re-derived from one run:
+# the LDS kernel's 256x128 / 128x128 / 128x64 / 64x64 / 256x256 tiles (0-4) with
+# and without K splits, the row-stationary builds (5, 6; row-coalesced A 7-10)
+# and the 4-wave 256x256 LDS build (11).
+GEMM_CANDIDATES = ["0", "0:2", "0:4", "1", "1:2", "2", "2:2", "3", "3:2", "3:4", "3:8", "4", "4:2", "5", "6",
+                   "7", "8", "9", "10", "11"]
 
 
 def _part(out, name, fn):
@@ -302,15 +304,21 @@ def extras(rng, hip, ops, stream, reps):
         return run
 
     def candidates():
+        """{"shapes": [tag], "us": {cfg: [us per shape]}, "default_us": [...], "best": [[cfg, us] per shape]}"""
         cases = [GemmCase(t, M, N, K, rng, hip, ops) for t, M, N, K in GEMM_SHAPES + [CONFIG0]]
-        res = {}
+        res = {"shapes": [c.tag for c in cases], "us": {}}
+        res["default_us"] = [time_case(c, stream, hip, reps)[1]["us"] for c in cases]
         for cfg in GEMM_CANDIDATES:
             os.environ["MI_GEMM_CFG"] = cfg
             try:
-                res[cfg] = [{"shape": c.tag, "us": e["us"], "pct_of_roofline": e["pct_of_roofline"]}
-                            for c in cases for e in [time_case(c, stream, hip, reps)[1]]]
+                res["us"][cfg] = [time_case(c, stream, hip, reps)[1]["us"] for c in cases]
+            except Exception as e:  # noqa: BLE001 -- one build's failure keeps the others
+                res["us"][cfg] = f"{type(e).__name__}: {e}"
             finally:
                 os.environ.pop("MI_GEMM_CFG", None)
+        timed = {k: v for k, v in res["us"].items() if isinstance(v, list)}
+        res["best"] = [min(([k, v[i]] for k, v in timed.items()), key=lambda kv: kv[1]) if timed else None
+                       for i in range(len(cases))]
         return res
 
     _part(out, "config0_gemm", cfg0)

@@ -133,7 +133,8 @@ def test_bench_line_on_stand_in_device(fake_device, monkeypatch, capsys):
     for part in ("config0_gemm", "nn_gemm", "block_stack_cached_kv", "block_stack_fused_epilogues",
                  "block_stack_joint_qkv", "block_stack_fused_joint_cached", "gemm_candidates"):
         assert part in ex and "error" not in ex[part], (part, ex.get(part))
-    assert set(ex["gemm_candidates"]) == set(bench.GEMM_CANDIDATES)
+    assert set(ex["gemm_candidates"]["us"]) == set(bench.GEMM_CANDIDATES)
+    assert len(ex["gemm_candidates"]["best"]) == len(bench.GEMM_SHAPES) + 1
     assert ex["block_stack_fused_joint_cached"]["variant"] == {"cached_kv": True, "fused_epilogues": True,
                                                                "joint_qkv": True}
     for name in ("gemm_nt_q8_0", "fused_attention_ex", "gemm_nn_q8", "sdxl_block_forward", "block_ctx_kv",
