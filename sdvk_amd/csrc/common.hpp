@@ -65,6 +65,24 @@ __device__ __forceinline__ float gelu_erf(float v) {
     return 0.5f * v * (1.0f + erf);
 }
 
+// Scheduling groups for one K step (instruction-class masks of
+// __builtin_amdgcn_sched_group_barrier: 0x008 MFMA, 0x002 VALU, 0x100 LDS read,
+// 0x200 LDS write). The step's first fragment reads go first; then every MFMA
+// is followed by a share of the next fragment reads and of the store phase
+// (conversions, dequantisation, LDS writes of the other stage), so that work
+// issues in the MFMA shadow instead of between MFMA bursts.
+template <int NMFMA, int NREAD0, int NREAD, int NVALU, int NWRITE>
+__device__ __forceinline__ void interleave_step() {
+    __builtin_amdgcn_sched_group_barrier(0x100, NREAD0, 0);
+#pragma unroll
+    for (int i = 0; i < NMFMA; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, (NREAD + NMFMA - 1) / NMFMA, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, (NVALU + NMFMA - 1) / NMFMA, 0);
+        __builtin_amdgcn_sched_group_barrier(0x200, (NWRITE + NMFMA - 1) / NMFMA, 0);
+    }
+}
+
 // Remaps a linear workgroup id so that consecutive logical tiles land on the
 // same XCD. The dispatcher hands workgroup b to XCD b % 8; tiles that share an
 // operand should share that XCD's L2.

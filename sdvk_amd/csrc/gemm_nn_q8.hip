@@ -9,17 +9,36 @@
 // 54-64), B fp32 row-major, mode 0 stores / mode 1 accumulates, batch on z
 // offsets A, B and C, zero leading dimensions default to K, N, N (:38-40).
 //
-// This is the first MFMA version (not yet tuned): a workgroup computes a
-// 64 x 64 tile of C with four waves of one 32 x 32 v_mfma_f32_32x32x16_f16
-// tile each, 32 k per step. W is dequantised to fp16 per 4-element group with
-// that group's flat scale (exactly the shader's staging unit), B is rounded to
-// fp16 and stored transposed ([n][k]) so both MFMA operands are 8 consecutive
-// k per lane. Small LDS (10 KB) and registers let eight workgroups share a CU,
-// which hides the unpipelined load -> store -> barrier -> MFMA sequence.
-// Every global access goes through a buffer resource whose range is exactly
-// the operand's extent: a read outside it returns zeros and a write outside
-// it is dropped.
+// Two kernels:
+//
+//   * gemm_nn_q8_tiled_kernel (weights 16-byte aligned with lda, sA multiples
+//     of 16, K a multiple of 64: every SDXL conv): 128 x 256 tiles, eight
+//     waves of 64 x 64 v_mfma_f32_32x32x16_f16 tiles, 64 k per step, two LDS
+//     stages and two register sets in flight (the loads of step j + 2 are
+//     issued before step j's MFMAs; step j + 1's dequantisation and B
+//     conversion run between them). W is dequantised once per workgroup: 16
+//     bytes of one row per thread, which lie inside one 32-element scale block
+//     (16-aligned flat index), as fp16(float(q) * s) computed exactly as
+//     fma(float(q + 128), s, -128 s). B is read as row-coalesced 16-byte pieces
+//     of four k rows and transposed in registers (a 4 x 4 block of k by n per
+//     thread) so LDS holds [n][k] and both MFMA operands are 8 consecutive k
+//     per lane. Grids that would leave CUs idle split K; the splits add their
+//     partial tiles with fp32 atomics after a fill kernel has cleared C
+//     (mode 0), so the summation order varies run to run (last bits only).
+//   * gemm_nn_q8_kernel (every other shape): 64 x 64 tiles, four waves of one
+//     32 x 32 tile, 32 k per step, no software pipelining; W is dequantised per
+//     4-element group with that group's flat scale (exactly the shader's
+//     staging unit), B is rounded to fp16 and stored transposed ([n][k]).
+//
+// Every global read goes through a buffer resource whose range is exactly the
+// operand's extent with the whole offset in the lane offset: a read outside it
+// returns zeros. The general kernel's writes go through such a resource too.
 #include "common.hpp"
+
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+#include <type_traits>
 
 namespace mi {
 namespace {
@@ -32,6 +51,7 @@ struct NnArgs {
     uint32_t M, N, K, mode, lda, ldb, ldc;
     uint32_t sA, sB, sC;                      // batch strides (elements), < 2^31 by validation
     uint32_t a_bytes, s_bytes, b_bytes, c_bytes;  // whole-buffer extents
+    uint32_t splits, steps_per_split;         // tiled kernel: K splits (blockIdx.z = batch * splits + split)
 };
 
 constexpr int kTM = 64, kTN = 64, kTK = 32;
@@ -121,6 +141,174 @@ __global__ __launch_bounds__(256) void gemm_nn_q8_kernel(NnArgs a) {
     }
 }
 
+// ---- tiled kernel --------------------------------------------------------------
+
+constexpr int kBM2 = 128, kBN2 = 256, kBK2 = 64;
+constexpr int kLd2 = kBK2 + 8;   // LDS row stride in halves (16-byte pad: conflict-free reads and writes)
+constexpr int kNT2 = 512;        // eight waves: 2 (m) x 4 (n), 64 x 64 each
+constexpr uint32_t kCUs = 256;
+
+// C[z] rows m < M, columns n < N = 0 (mode 0 before K splits add into C).
+__global__ __launch_bounds__(256) void gemm_nn_zero_kernel(float* C, uint32_t M, uint32_t N, uint32_t ldc,
+                                                           uint32_t sC) {
+    const uint32_t n = blockIdx.x * 256 + threadIdx.x;
+    if (n >= N) return;
+    float* c = C + static_cast<uint64_t>(blockIdx.z) * sC + n;
+    for (uint32_t m = blockIdx.y; m < M; m += gridDim.y) c[static_cast<uint64_t>(m) * ldc] = 0.0f;
+}
+
+template <bool SPLITK>
+__global__ __launch_bounds__(kNT2) void gemm_nn_q8_tiled_kernel(NnArgs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 smem[2 * (kBM2 + kBN2) * kLd2];
+    auto Ws = reinterpret_cast<_Float16 (*)[kBM2 * kLd2]>(smem);              // [m][k]
+    auto Bs = reinterpret_cast<_Float16 (*)[kBN2 * kLd2]>(smem + 2 * kBM2 * kLd2);  // [n][k]
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, g = lane >> 5;
+    const int wm = wave & 1, wn = wave >> 1;
+    const uint32_t n0 = blockIdx.x * kBN2, m0 = blockIdx.y * kBM2;
+    const uint32_t z = blockIdx.z / a.splits, split = blockIdx.z % a.splits;
+    const uint32_t ksteps = a.K / kBK2;
+    const uint32_t s_begin = SPLITK ? split * a.steps_per_split : 0;
+    const uint32_t s_end = SPLITK ? min(ksteps, s_begin + a.steps_per_split) : ksteps;
+
+    const __amdgpu_buffer_rsrc_t rA =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.Aq), 0, static_cast<int>(a.a_bytes), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rS =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.S), 0, static_cast<int>(a.s_bytes), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rB =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.B), 0, static_cast<int>(a.b_bytes), 0x00020000);
+
+    // W: thread -> row wr, 16 k at wq; flat index of the step's first byte
+    // (rows past M read other rows or zeros: they feed outputs never stored)
+    const uint32_t wr = tid >> 2, wq = (tid & 3) * 16;
+    const uint32_t w_fl = z * a.sA + (m0 + wr) * a.lda + wq;
+    // B: thread -> k block kb (4 rows), n quad bq; pass p adds 32 rows
+    const uint32_t kb = tid & 7, bq = tid >> 3;
+    const uint32_t b_el = z * a.sB + (4 * kb) * a.ldb + n0 + 4 * bq;
+
+    uint32_t wraw[2][4];
+    float wsc[2];
+    floatx4 braw[2][2][4];
+    auto load = [&](uint32_t ks_in, auto RS) {
+        constexpr int rs = decltype(RS)::value;
+        const uint32_t ks = __builtin_amdgcn_readfirstlane(ks_in);
+        const uint32_t fl = w_fl + ks * kBK2;
+        const auto w = __builtin_amdgcn_raw_buffer_load_b128(rA, fl, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) wraw[rs][e] = w[e];
+        wsc[rs] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rS, (fl >> 5) * 4, 0, 0));
+        const uint32_t b0 = b_el + ks * kBK2 * a.ldb;
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                braw[rs][p][i] = __builtin_bit_cast(
+                    floatx4, __builtin_amdgcn_raw_buffer_load_b128(rB, (b0 + (32 * p + i) * a.ldb) * 4, 0, 0));
+    };
+    auto store = [&](auto RS, auto ST) {
+        constexpr int rs = decltype(RS)::value;
+        constexpr int st = decltype(ST)::value;
+        // fp16(float(q) * s) = fp16(fma(float(q + 128), s, -128 s)): one fp32 rounding of the exact product
+        const float s = wsc[rs], ms = -128.0f * s;
+        half8 h[2];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t u = wraw[rs][e] ^ 0x80808080u;
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb)
+                h[e >> 1][4 * (e & 1) + bb] =
+                    static_cast<_Float16>(__builtin_fmaf(static_cast<float>((u >> (8 * bb)) & 0xffu), s, ms));
+        }
+        *reinterpret_cast<half8*>(&Ws[st][wr * kLd2 + wq]) = h[0];
+        *reinterpret_cast<half8*>(&Ws[st][wr * kLd2 + wq + 8]) = h[1];
+        // B: the 4 x 4 block (k rows i, n columns e) goes to LDS rows n as 4 consecutive k
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                *reinterpret_cast<half4*>(&Bs[st][(4 * bq + e) * kLd2 + 32 * p + 4 * kb]) =
+                    half4{static_cast<_Float16>(braw[rs][p][0][e]), static_cast<_Float16>(braw[rs][p][1][e]),
+                          static_cast<_Float16>(braw[rs][p][2][e]), static_cast<_Float16>(braw[rs][p][3][e])};
+    };
+
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    auto compute = [&](auto ST) {
+        constexpr int st = decltype(ST)::value;
+#pragma unroll
+        for (int s = 0; s < kBK2 / 16; ++s) {
+            half8 af[2], bf[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                af[i] = *reinterpret_cast<const half8*>(&Ws[st][(wm * 64 + 32 * i + l32) * kLd2 + 16 * s + 8 * g]);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                bf[j] = *reinterpret_cast<const half8*>(&Bs[st][(wn * 64 + 32 * j + l32) * kLd2 + 16 * s + 8 * g]);
+            // D[i][j] = sum_k af(row i)[k] bf(col j)[k]: i = m, j = n
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    constexpr int kMfma = 2 * 2 * (kBK2 / 16), kRead0 = 4, kReads = 4 * (kBK2 / 16);
+    constexpr int kValu = 4 + 16 * 2 + 8 + 16, kWrites = 2 + 8;
+
+    // Step j computes from LDS stage j & 1 while the loads of step j + 2 (into
+    // register set j & 1) are in flight and set (j + 1) & 1 is stored; loads
+    // past the last step re-read it (unused), so the loop has no load branches.
+    const uint32_t n_steps = s_end - s_begin, last = s_end - 1;
+    if (n_steps > 0) {
+        load(s_begin, S0{});
+        store(S0{}, S0{});
+        load(min(s_begin + 1, last), S1{});
+    }
+    __syncthreads();
+    uint32_t j = 0;
+    for (; j + 2 <= n_steps; j += 2) {
+        load(min(s_begin + j + 2, last), S0{});
+        __builtin_amdgcn_sched_barrier(0);
+        compute(S0{});
+        store(S1{}, S1{});
+        interleave_step<kMfma, kRead0, kReads - kRead0, kValu, kWrites>();
+        __syncthreads();
+        load(min(s_begin + j + 3, last), S1{});
+        __builtin_amdgcn_sched_barrier(0);
+        compute(S1{});
+        store(S0{}, S0{});
+        interleave_step<kMfma, kRead0, kReads - kRead0, kValu, kWrites>();
+        __syncthreads();
+    }
+    if (j < n_steps) compute(S0{});
+
+    // lane holds column n = l32 and rows 8 (r / 4) + 4 g + r % 4 of each
+    // 32 x 32 tile: for each r, 32 lanes cover 32 consecutive floats of a row
+    float* C = a.C + static_cast<uint64_t>(z) * a.sC;
+#pragma unroll
+    for (int jt = 0; jt < 2; ++jt) {
+        const uint32_t n = n0 + wn * 64 + 32 * jt + l32;
+        if (n >= a.N) continue;
+#pragma unroll
+        for (int it = 0; it < 2; ++it)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t m = m0 + wm * 64 + 32 * it + 8 * (r >> 2) + 4 * g + (r & 3);
+                if (m >= a.M) continue;
+                float* c = C + static_cast<uint64_t>(m) * a.ldc + n;
+                if constexpr (SPLITK) unsafeAtomicAdd(c, acc[it][jt][r]);  // native global_atomic_add_f32
+                else *c = a.mode != 0 ? *c + acc[it][jt][r] : acc[it][jt][r];
+            }
+    }
+}
+
 }  // namespace
 }  // namespace mi
 
@@ -179,7 +367,35 @@ extern "C" int mi_gemm_nn_q8_split(const uint32_t* payload, const float* scales,
     a.s_bytes = static_cast<uint32_t>(s_el * 4);
     a.b_bytes = static_cast<uint32_t>(b_el * 4);
     a.c_bytes = static_cast<uint32_t>(c_el * 4);
-    const dim3 grid(ceil_div(N, kTN), ceil_div(M, kTM), batch);
-    gemm_nn_q8_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(a);
+    a.splits = 1;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const char* env = std::getenv("MI_NN_KERNEL");  // "general": the untiled kernel for every shape (tests)
+    const bool tiled = K > 0 && K % kBK2 == 0 && aligned(payload, 16) && lda % 16 == 0 && sA % 16 == 0 &&
+                       !(env && std::strcmp(env, "general") == 0);
+    if (!tiled) {
+        const dim3 grid(ceil_div(N, kTN), ceil_div(M, kTM), batch);
+        gemm_nn_q8_kernel<<<grid, 256, 0, st>>>(a);
+        return check_launch(fn);
+    }
+    // One 8-wave workgroup per CU: split K until the grid covers the CUs, keeping
+    // at least four 64-wide steps per split.
+    const uint64_t tiles = static_cast<uint64_t>(ceil_div(N, kBN2)) * ceil_div(M, kBM2) * batch;
+    const uint32_t ksteps = K / kBK2;
+    uint32_t splits = 1;
+    while (tiles * splits < kCUs && splits * 2 * 4 <= ksteps && batch * splits * 2 <= 65535) splits *= 2;
+    if (splits > 1) {
+        a.steps_per_split = ceil_div(ksteps, splits);
+        splits = ceil_div(ksteps, a.steps_per_split);
+    }
+    a.splits = splits;
+    if (splits > 1) {
+        if (mode == 0)
+            gemm_nn_zero_kernel<<<dim3(ceil_div(N, 256), std::min<uint32_t>(M, 4096), batch), 256, 0, st>>>(C, M, N, ldc,
+                                                                                                         a.sC);
+        gemm_nn_q8_tiled_kernel<true><<<dim3(ceil_div(N, kBN2), ceil_div(M, kBM2), batch * splits), kNT2, 0, st>>>(a);
+    } else {
+        a.steps_per_split = ksteps;
+        gemm_nn_q8_tiled_kernel<false><<<dim3(ceil_div(N, kBN2), ceil_div(M, kBM2), batch), kNT2, 0, st>>>(a);
+    }
     return check_launch(fn);
 }

@@ -138,9 +138,14 @@ def gemm_geglu(E, *, M, F, K, cfg=None, bias=True, lda=0, ldg=0, seed=1, front=F
 
 
 def gemm_nn(E, *, M, N, K, mode=0, batch=1, lda=0, ldb=0, ldc=0, sA=0, sB=0, sC=0, seed=1, front=False,
-            order=0, tol=2e-3):
-    """mi_gemm_nn_q8_split against the oracle (flat-index scales)."""
+            order=0, tol=2e-3, kernel=None):
+    """mi_gemm_nn_q8_split against the oracle (flat-index scales). kernel="general"
+    forces the untiled kernel (MI_NN_KERNEL) on shapes the tiled one would take."""
     E.order(order)
+    if kernel:
+        os.environ["MI_NN_KERNEL"] = kernel
+    else:
+        os.environ.pop("MI_NN_KERNEL", None)
     lda_e, ldb_e, ldc_e = lda or K, ldb or N, ldc or N
     a_el = (batch - 1) * sA + (M - 1) * lda_e + K
     b_el = (batch - 1) * sB + (K - 1) * ldb_e + N if K else N

@@ -67,6 +67,49 @@ def test_nn_batch_strides_and_flat_scales(gpu, oracle):
     assert np.array_equal(got[M * ldc: sC], C0[M * ldc: sC])
 
 
+@pytest.mark.parametrize("kernel", ["tiled", "general"])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_nn_tiled_strides_and_k_splits(gpu, oracle, monkeypatch, kernel, mode):
+    """The tiled kernel (K % 64 == 0, lda and sA multiples of 16) with batch /
+    leading dimensions, and with K split across workgroups (64 x 64 x 1024: one
+    tile, four splits adding with atomics); MI_NN_KERNEL=general runs the same
+    cases on the untiled kernel."""
+    if kernel == "general":
+        monkeypatch.setenv("MI_NN_KERNEL", "general")
+    else:
+        monkeypatch.delenv("MI_NN_KERNEL", raising=False)
+    M, N, K, batch = 70, 36, 256, 3
+    lda, ldb, ldc = 272, 40, 44
+    sA, sB, sC = 19056, 10248, 3100
+    print(f"[case] nn {kernel} mode={mode} batch={batch} strides", flush=True)
+    na = (batch - 1) * sA + (M - 1) * lda + K
+    payload, scales = oracle.q8_0_to_split(q8_weights(oracle, 61, 1, (na + 31) // 32 * 32), (na + 31) // 32 * 32)
+    B = oracle.normal(62, (batch - 1) * sB + (K - 1) * ldb + N)
+    C0 = oracle.normal(63, (batch - 1) * sC + M * ldc)
+    kw = dict(lda=lda, ldb=ldb, ldc=ldc, batch=batch, sA=sA, sB=sB, sC=sC, mode=mode)
+    want = oracle.gemm_nn_q8_split(payload, scales, B, M, N, K, C=C0.copy(), threads=oracle.max_threads(), **kw)
+    got = run_nn(payload, scales, B, M, N, K, C0=C0, **kw)
+    for z in range(batch):
+        g = got[z * sC: z * sC + M * ldc].reshape(M, ldc)
+        w = want[z * sC: z * sC + M * ldc].reshape(M, ldc)
+        c0 = C0[z * sC: z * sC + M * ldc].reshape(M, ldc)
+        if mode == 1:
+            assert_parity(g[:, :N] - c0[:, :N], w[:, :N] - c0[:, :N], what=f"{kernel} batch {z} mode 1")
+        else:
+            assert_parity(g[:, :N], w[:, :N], what=f"{kernel} batch {z}")
+        assert np.array_equal(g[:, N:], c0[:, N:])
+    M, N, K = 64, 64, 1024
+    payload, scales = split_weight(oracle, 64, M, K)
+    B = oracle.normal(65, K * N)
+    C0 = oracle.normal(66, M * N)
+    want = oracle.gemm_nn_q8_split(payload, scales, B, M, N, K, C=C0.copy(), mode=mode, threads=oracle.max_threads())
+    got = run_nn(payload, scales, B, M, N, K, C0=C0, mode=mode)
+    if mode == 1:
+        assert_parity(got - C0, want - C0, what=f"{kernel} K split mode 1")
+    else:
+        assert_parity(got, want, what=f"{kernel} K split")
+
+
 # SDXL 1024^2 conv shapes: level-0 3x3 (320 -> 320 over a 4096-pixel chunk of the
 # 128 x 128 latent), level-1 3x3 (640 -> 640, 64 x 64), level-2 3x3 (1280 -> 1280,
 # 32 x 32), a 1x1 shortcut (640 -> 1280, 32 x 32)

@@ -9,7 +9,8 @@ For every loop that issues MFMAs in the GEMM and attention kernels:
     that retires it. A load under a branch, or a consumer hoisted next to its
     load, drops this to 0-2 and the wave then sits out the memory latency.
 Excluded: the attention kernel's scalar-load build (head dims that are not a
-multiple of 8, or unaligned tensors; no SDXL shape takes it).
+multiple of 8, or unaligned tensors; no SDXL shape takes it) and the NN GEMM's
+untiled kernel (the general path for unaligned shapes; not pipelined).
 """
 from __future__ import annotations
 
@@ -22,6 +23,7 @@ import isa_sched
 CASES = {
     "gemm_q8.hip": ("gemm_q8_kernel", "gemm_q8_rows_kernel"),
     "attention.hip": ("attn_f16_kernel", "attn_kernel"),
+    "gemm_nn_q8.hip": ("gemm_nn_q8_tiled_kernel",),
 }
 
 

@@ -78,6 +78,10 @@ FAMILIES = {
         dict(M=60, N=36, K=44, batch=3, lda=48, ldb=40, ldc=44, sA=3000, sB=1800, sC=2800),
         dict(M=5, N=4, K=4), dict(M=64, N=64, K=0), dict(M=64, N=64, K=0, mode=1),
         dict(M=33, N=68, K=36, front=True),
+        # tiled kernel (K % 64 == 0, lda / sA multiples of 16): edges, K splits (mode 0 / 1), batch / strides
+        dict(M=130, N=260, K=128), dict(M=300, N=520, K=640, mode=1), dict(M=64, N=64, K=1024),
+        dict(M=70, N=36, K=256, batch=3, lda=272, ldb=40, ldc=44, sA=19056, sB=10248, sC=3100),
+        dict(M=129, N=300, K=256, front=True), dict(M=130, N=260, K=128, kernel="general"),
     ],
     "attention": [
         dict(Tq=100, Tk=300, C=128, heads=2), dict(Tq=100, Tk=300, C=128, heads=2, causal=True),
@@ -154,6 +158,14 @@ PLANTED = {
     # NN GEMM weight rows past M read through a plain pointer (out of bounds)
     "oob_read": ("gemm_nn_q8.hip", "if (wm_row < a.M && k < a.K) {", "if (k < a.K) {",
                  dict(case="gemm_nn", M=60, N=64, K=32)),
+    # tiled NN GEMM: B's 4 x 4 register transpose taken the wrong way round
+    "nn_transpose": ("gemm_nn_q8.hip", "static_cast<_Float16>(braw[rs][p][1][e])",
+                     "static_cast<_Float16>(braw[rs][p][e][1])", dict(case="gemm_nn", M=130, N=260, K=128)),
+    # tiled NN GEMM: the barrier between storing stage 1 and reading it removed
+    "nn_missing_barrier": ("gemm_nn_q8.hip",
+                           "        __syncthreads();\n        load(min(s_begin + j + 3, last), S1{});",
+                           "        load(min(s_begin + j + 3, last), S1{});",
+                           dict(case="gemm_nn", M=130, N=260, K=256)),
     # GGUF upload refills a staging buffer without waiting for its last copy
     "staging_reuse": ("gguf.cpp",
                       "    if (g->stage_used[i] && hipEventSynchronize(g->done[i]) != hipSuccess)\n"
