@@ -17,6 +17,8 @@
 // grid-stride loop.
 #include "common.hpp"
 
+#include <algorithm>
+
 namespace mi {
 namespace {
 
@@ -105,18 +107,20 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict_
 }
 
 // y[r, j] = h[r, j] * gelu(h[r, F + j]); F % 4 == 0 and 16-byte aligned rows.
+// Thread (x, y) of the grid takes float4 column blockIdx.x * 256 + tid of rows
+// blockIdx.y, blockIdx.y + gridDim.y, ... (no index division per element).
 __global__ __launch_bounds__(256) void geglu_vec_kernel(const float* __restrict__ h, float* __restrict__ y, uint32_t rows,
                                                         uint32_t F) {
     const uint32_t f4 = F / 4;
-    const uint64_t total = static_cast<uint64_t>(rows) * f4;
-    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < total; i += static_cast<uint64_t>(gridDim.x) * 256) {
-        const uint64_t r = i / f4, j = i % f4;
-        const floatx4* hr = reinterpret_cast<const floatx4*>(h + r * 2 * F);
+    const uint32_t j = blockIdx.x * 256 + threadIdx.x;
+    if (j >= f4) return;
+    for (uint32_t r = blockIdx.y; r < rows; r += gridDim.y) {
+        const floatx4* hr = reinterpret_cast<const floatx4*>(h + static_cast<uint64_t>(r) * 2 * F);
         const floatx4 a = hr[j], b = hr[f4 + j];
         floatx4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[e] = a[e] * gelu_erf(b[e]);
-        reinterpret_cast<floatx4*>(y + r * F)[j] = o;
+        reinterpret_cast<floatx4*>(y + static_cast<uint64_t>(r) * F)[j] = o;
     }
 }
 
@@ -180,8 +184,12 @@ extern "C" int mi_geglu(const float* h, float* y, uint32_t rows, uint32_t F, voi
     if (overlaps(h, static_cast<uint64_t>(rows) * 2 * F * 4, y, static_cast<uint64_t>(rows) * F * 4))
         return fail(MI_ERR_ALIASING, "%s: y overlaps h", fn);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (F % 4 == 0 && aligned(h, 16) && aligned(y, 16))
-        geglu_vec_kernel<<<stride_grid(static_cast<uint64_t>(rows) * F / 4), 256, 0, s>>>(h, y, rows, F);
+    if (F % 4 == 0 && aligned(h, 16) && aligned(y, 16)) {
+        // ~2048 workgroups in all: the rows are strided over grid.y
+        const unsigned gx = ceil_div(F / 4, 256);
+        const unsigned gy = static_cast<unsigned>(std::min<uint64_t>(rows, std::max<uint64_t>(1, 2048 / gx)));
+        geglu_vec_kernel<<<dim3(gx, gy), 256, 0, s>>>(h, y, rows, F);
+    }
     else
         geglu_kernel<<<stride_grid(static_cast<uint64_t>(rows) * F), 256, 0, s>>>(h, y, rows, F);
     return check_launch(fn);
