@@ -988,7 +988,8 @@ enum CfgId {
     kC256x128 = 0, kC128x128, kC128x64, kC64x64, kC256x256,  // LDS kernel (gemm_q8_kernel)
     kR256x256, kR256x128,                                     // row kernel, per-lane-row A loads
     kR256x256Q, kR256x192Q, kR256x160Q, kR256x128Q,           // row kernel, row-coalesced A
-    kC256x256W4,                                              // LDS kernel, 4 waves of 128x128, two sets in flight
+    kC256x256W4,                                              // LDS kernel, 4 waves of 128x128, one set in flight
+    kC256x128W4, kC128x256W4,                                 // LDS kernel, 4 waves of 128x64 / 64x128
     kNumCfg
 };
 
@@ -1105,6 +1106,8 @@ void launch(int cfg, const GemmArgs& a, uint32_t batch, uint32_t splits, hipStre
         case kR256x128: launch_rows<4, WK, false, EPI>(a, batch, splits, s); break;
         case kC256x128: launch_cfg<256, 128, 4, 2, 2, WK, false, 2, EPI>(a, batch, splits, s); break;
         case kC128x128: launch_cfg<128, 128, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, s); break;
+        case kC256x128W4: launch_cfg<256, 128, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, s); break;
+        case kC128x256W4: launch_cfg<128, 256, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, s); break;
         case kC256x256W4:
             // one wave per SIMD with 128 x 128 per wave (256 accumulator AGPRs)
             // and one register set; its K-split build would spill in the loop

@@ -52,6 +52,9 @@ FAMILIES = {
         # 4-wave 256x256 (one wave per SIMD, 128x128 per wave); a requested split is ignored
         dict(M=300, N=300, K=256, cfg="11"), dict(M=260, N=130, K=192, cfg="11:2", layout="split", mode=1),
         dict(M=70, N=36, K=128, batch=2, lda=132, ldc=40, sA=9300, sC=3000, cfg="11", front=True),
+        # 4-wave 256x128 / 128x256 (128x64 / 64x128 per wave), K splits and the split layout
+        dict(M=300, N=300, K=256, cfg="12"), dict(M=260, N=130, K=320, cfg="12:3", layout="split", mode=1),
+        dict(M=300, N=300, K=256, cfg="13:2"), dict(M=130, N=520, K=192, cfg="13", layout="split", front=True),
     ],
     # row-stationary kernel: per-lane-row A (5, 6) and row-coalesced A (7-10)
     "gemm_rows": [
@@ -72,6 +75,7 @@ FAMILIES = {
         dict(case="gemm_geglu", M=260, F=96, K=128, cfg="9", front=True),
         dict(case="gemm_geglu", M=70, F=40, K=128, cfg="1", bias=False),
         dict(case="gemm_nt", M=300, N=200, K=256, cfg="11", mode=2), dict(case="gemm_geglu", M=300, F=130, K=256, cfg="11"),
+        dict(case="gemm_nt", M=200, N=300, K=256, cfg="12:2", mode=2), dict(case="gemm_geglu", M=200, F=260, K=128, cfg="13"),
     ],
     "gemm_nn": [
         dict(M=64, N=64, K=32), dict(M=100, N=72, K=96), dict(M=130, N=260, K=100, mode=1),
