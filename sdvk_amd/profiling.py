@@ -4,8 +4,9 @@ Two reports, both plain text so they can be kept next to the source:
 
 * ``stats``: a ``*_kernel_stats.csv`` (``rocprofv3 --kernel-trace --stats``)
   turned into a markdown table per kernel plus per-family aggregates
-  (``gemm_q8`` = the GEMM kernels with their split-K init fills, one entry per
-  API call; ``attention`` = the fused attention kernel).
+  (``gemm_q8`` = the NT GEMM kernels with their split-K init / bias fills, one
+  entry per API call; ``attention`` = the fused attention kernels;
+  ``gemm_nn_q8`` = the NN GEMM kernels with their split-K clear).
 * ``traffic``: two ``*_counter_collection.csv`` files (``--pmc FETCH_SIZE``,
   then ``--pmc WRITE_SIZE``) turned into HBM bytes per launch of a family.
   Each counter (KiB per dispatch) is scaled by what it reads for the runtime's
@@ -29,9 +30,11 @@ import subprocess
 import sys
 from pathlib import Path
 
+# family -> (main kernels: one launch per API call, helper kernels of the same calls)
 FAMILIES = {
-    "gemm_q8": ("gemm_q8_kernel", "gemm_init_kernel"),
-    "attention": ("attn_kernel",),
+    "gemm_q8": (("gemm_q8_kernel", "gemm_q8_rows_kernel"), ("gemm_init_kernel", "gemm_bias_add_kernel")),
+    "attention": (("attn_kernel", "attn_f16_kernel"), ()),
+    "gemm_nn_q8": (("gemm_nn_q8_kernel", "gemm_nn_q8_tiled_kernel"), ("gemm_nn_zero_kernel",)),
 }
 COPY_KERNEL = re.compile(r"copyBuffer", re.I)
 
@@ -42,20 +45,33 @@ def short_name(name: str) -> str:
         tool = shutil.which("c++filt") or shutil.which("llvm-cxxfilt")
         if tool:
             name = subprocess.run([tool, name], capture_output=True, text=True).stdout.strip() or name
-        m = re.search(r"\d([a-z][a-z_0-9]*?_kernel)I((?:DF16_|f|Lb[01]E)+)E", name) if name.startswith("_Z") else None
+        m = re.search(r"\d([a-z][a-z_0-9]*?_kernel)I((?:DF16_|f|Lb[01]E|Li\d+E)+)E", name) if name.startswith("_Z") \
+            else None
         if m:  # template arguments this library uses that binutils' demangler may not know (_Float16)
-            toks = re.findall(r"DF16_|f|Lb[01]E", m.group(2))
+            toks = re.findall(r"DF16_|f|Lb[01]E|Li\d+E", m.group(2))
             conv = {"DF16_": "_Float16", "f": "float", "Lb0E": "false", "Lb1E": "true"}
-            name = f"{m.group(1)}<{', '.join(conv[t] for t in toks)}>"
+            name = f"{m.group(1)}<{', '.join(conv.get(t, t[2:-1]) for t in toks)}>"
     n = re.sub(r"^void\s+", "", name)
     n = n.replace("mi::(anonymous namespace)::", "")
     n = re.sub(r"\(.*\)$", "", n)
     return n
 
 
+def _has(name: str, key: str) -> bool:
+    """key as a whole identifier of a kernel name: mangled (length-prefixed,
+    `...15attn_f16_kernelI...`) or demangled (`...::attn_f16_kernel<...`)."""
+    if name.startswith("_Z"):
+        return f"{len(key)}{key}" in name
+    return re.search(r"(?<![A-Za-z0-9_])" + re.escape(key) + r"(?![A-Za-z0-9_])", name) is not None
+
+
+def is_main(name: str, family: str) -> bool:
+    return any(_has(name, k) for k in FAMILIES[family][0])
+
+
 def family_of(name: str) -> str | None:
-    for fam, keys in FAMILIES.items():
-        if any(k in name for k in keys):
+    for fam, (main, helpers) in FAMILIES.items():
+        if any(_has(name, k) for k in main + helpers):
             return fam
     return None
 
@@ -72,7 +88,7 @@ def stats_report(csv_path: str, command: str) -> str:
                      f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.2f} |")
         f = family_of(name)
         if f:
-            if FAMILIES[f][0] in name:
+            if is_main(name, f):
                 fam[f][0] += calls
             fam[f][1] += tot
     lines += ["", "Family aggregates (total time of the family's kernels / calls of its main kernel, i.e. per API "
@@ -104,9 +120,8 @@ def traffic_report(fetch_csv: str, write_csv: str, copy_mib: int, family: str, c
         factor = nbytes / (max(copies) * 1024.0)
         result[f"{counter.lower()}_factor"] = round(factor, 5)
         result[f"{counter.lower()}_copy_kib"] = max(copies)
-        main_key = FAMILIES[family][0]
         for n, grid, v in rows:
-            if main_key in n:
+            if is_main(n, family):
                 d = per_shape.setdefault((short_name(n), grid), {"fetch": [], "write": []})
                 d["fetch" if counter == "FETCH_SIZE" else "write"].append(v * 1024.0 * factor)
     shapes = []
