@@ -155,8 +155,12 @@ int mi_gemm_nt_q8_0_geglu(const float* A, const void* W, const float* bias, floa
  * K and N must be multiples of 4 (the shader's 4-wide staging zero-fills a
  * partial group, :58,79: rejected, not emulated). payload 4-byte aligned with
  * lda, sA % 4 == 0; B 16-byte aligned with ldb, sB % 4 == 0; each operand
- * below 2 GiB. Replaces Engine::dispatch("gemm_nn_q8_v" / "gemm_nn_q8",
- * {Aq, B, C, S}, Pg) (vk_engine.cpp:57,63) behind gemmNnQ8 (sdvkgen.cpp:944-948). */
+ * below 2 GiB. payload 16-byte aligned with lda, sA % 16 == 0 and
+ * K % 64 == 0 (every SDXL conv) take the pipelined tiled kernel, which may
+ * split K and add the splits with atomics (last bits then vary run to run);
+ * other shapes take the untiled kernel. Replaces Engine::dispatch("gemm_nn_q8_v"
+ * / "gemm_nn_q8", {Aq, B, C, S}, Pg) (vk_engine.cpp:57,63) behind gemmNnQ8
+ * (sdvkgen.cpp:944-948). */
 int mi_gemm_nn_q8_split(const uint32_t* payload, const float* scales, const float* B, float* C,
                         uint32_t M, uint32_t N, uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldb,
                         uint32_t ldc, uint32_t batch, uint64_t sA, uint64_t sB, uint64_t sC, void* stream);
