@@ -290,6 +290,12 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     constexpr bool WBLK = WK == kBlocks34 && KB == 2 && !KTAIL;
     constexpr int W_BLOCKS = BN * KB;
     constexpr int WB_IT = (W_BLOCKS + NT - 1) / NT;
+    // Twice as many threads as blocks (the 4-wave 64x64 and 128x64 tiles, the
+    // 8-wave 256x128 tile): thread t dequantises half h = t / W_BLOCKS of block
+    // t % W_BLOCKS (every thread loads its block's window), so the
+    // dequantisation is spread over all waves instead of half of them, which
+    // on a 4-wave workgroup would be half of the SIMDs.
+    constexpr bool WHALF = WBLK && 2 * W_BLOCKS == NT;
     // Buffer-load fast path: two blocks per step keep each lane's byte
     // alignment fixed (68 = 0 mod 4), so the step advance is a scalar offset.
     constexpr bool FAST = KB == 2 && !KTAIL;
@@ -476,7 +482,23 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
             h[3] = static_cast<_Float16>(areg_[rs][i][3]);
             *reinterpret_cast<half4*>(&As[st][(f / (BK / 4)) * LDK + (f % (BK / 4)) * 4]) = h;
         }
-        if constexpr (WBLK) {
+        if constexpr (WHALF) {
+            const uint32_t* x = wbx_[rs][0];
+            const bool hi = tid >= W_BLOCKS;  // wave-uniform: W_BLOCKS is a multiple of 64
+            uint32_t xs[5];
+#pragma unroll
+            for (int j = 0; j < 5; ++j) xs[j] = hi ? x[4 + j] : x[j];
+            const _Float16 d = __builtin_bit_cast(
+                _Float16, static_cast<uint16_t>(__builtin_amdgcn_perm(x[0], x[0], wb_dsel[0])));
+            uint32_t q[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) q[j] = __builtin_amdgcn_perm(xs[j + 1], xs[j], wb_qsel[0]);
+            const int wb = hi ? tid - W_BLOCKS : tid;
+            _Float16* dst = &Ws[st][(wb % BN) * LDK + (wb / BN) * 32 + (hi ? 16 : 0)];
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                *reinterpret_cast<half8*>(dst + 8 * j) = dequant8_f16(q[2 * j], q[2 * j + 1], d);
+        } else if constexpr (WBLK) {
 #pragma unroll
             for (int i = 0; i < WB_IT; ++i) {
                 const int wb = tid + i * NT;
@@ -554,8 +576,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     constexpr int kMfma = FM * FN * (BK / 16);       // MFMAs per step
     constexpr int kRead0 = FM + FN;                  // fragment reads of the first k16 slice
     constexpr int kReads = (FM + FN) * (BK / 16);    // all fragment reads of a step
-    constexpr int kWrites = A_IT + (WBLK ? 4 * WB_IT : W_IT);            // LDS writes of the store phase
-    constexpr int kValu = A_IT * 2 + (WBLK ? 60 * WB_IT : W_IT * 16);     // conversions + dequantisation (approx.)
+    constexpr int kWrites = A_IT + (WHALF ? 2 : WBLK ? 4 * WB_IT : W_IT);              // LDS writes of the store phase
+    constexpr int kValu = A_IT * 2 + (WHALF ? 36 : WBLK ? 60 * WB_IT : W_IT * 16);   // conversions + dequant (approx.)
     // Every workgroup sweeps K in the same order, so the workgroups that share
     // a panel read the same K slice at about the same time (L2 reuse).
     const uint32_t n_steps = s_end - s_begin;
