@@ -241,7 +241,8 @@ def time_case(c, stream, hip, reps):
     b.synchronize()
     sec = a.elapsed_ms(b) / 1e3 / reps
     tf, roof, frac = roofline_pct(c, sec)
-    return sec, {"shape": c.tag, "kernel": c.kernel, "M_N_K": [c.M, c.N, c.K], "us": round(sec * 1e6, 2),
+    dims = {"M_N_K": [c.M, c.N, c.K]} if hasattr(c, "M") else {"B_H_Tq_Tk": [c.B, c.H, c.Tq, c.Tk]}
+    return sec, {"shape": c.tag, "kernel": c.kernel, **dims, "us": round(sec * 1e6, 2),
                  "tflops": round(tf, 2), "pct_mfma_peak": round(100 * tf / PEAK_FP16_TFLOPS, 2),
                  "roofline_tflops": round(roof, 1), "pct_of_roofline": round(100 * frac, 2),
                  "gbs": round(c.bytes / sec / 1e9, 1)}
@@ -270,7 +271,8 @@ def extras(rng, hip, ops, stream, reps):
     harness's GEMM shape), the NN GEMM at the SDXL conv shapes, the config-4
     stack with the context's K / V cached, with the fused epilogues
     (MI_BLOCK_EPILOGUE=fused), with joint Q/K/V weights and with all three, and
-    the candidate GEMM tile builds on every GEMM shape of the step. These
+    the candidate GEMM tile builds on every GEMM shape of the step, and both
+    workgroup sizes of the fp16 attention kernel on every attention shape. These
     paths run in a child process (bench.py --extras-child): a failure there
     cannot cost the step measurement."""
     out = {}
@@ -327,7 +329,22 @@ def extras(rng, hip, ops, stream, reps):
     _part(out, "block_stack_fused_epilogues", stack(fused=True))
     _part(out, "block_stack_joint_qkv", stack(joint_qkv=True))
     _part(out, "block_stack_fused_joint_cached", stack(cached_kv=True, fused=True, joint_qkv=True))
+    def attn_candidates():
+        """{"shapes": [tag], "us": {"default" | "nw2" | "nw4": [us per shape]}}: the fp16 attention
+        kernel's 2- and 4-wave workgroups (MI_ATTN_NW) on every attention shape of the step."""
+        cases = [AttnCase(t, B, H, Tq, Tk, m, rng, hip, ops) for t, B, H, Tq, Tk, m in ATTN_SHAPES]
+        res = {"shapes": [c.tag for c in cases], "us": {}}
+        for key, nw in (("default", None), ("nw2", "2"), ("nw4", "4")):
+            if nw:
+                os.environ["MI_ATTN_NW"] = nw
+            try:
+                res["us"][key] = [time_case(c, stream, hip, reps)[1]["us"] for c in cases]
+            finally:
+                os.environ.pop("MI_ATTN_NW", None)
+        return res
+
     _part(out, "gemm_candidates", candidates)
+    _part(out, "attention_candidates", attn_candidates)
     return out
 
 

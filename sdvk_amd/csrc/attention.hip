@@ -28,6 +28,8 @@
 //     MFMA per product.
 #include "common.hpp"
 
+#include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 namespace mi {
@@ -712,10 +714,14 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
 
 template <typename TO>
 void launch_f16(const AttnArgs& a, uint32_t batch, hipStream_t s) {
-    // 4-wave workgroups when they give at least two per CU, else 2-wave ones
+    // 4-wave workgroups when they give at least two per CU, else 2-wave ones;
+    // MI_ATTN_NW = 2 or 4 pins one (tuning sweeps)
     const uint32_t q4 = ceil_div(a.Tq, 128u), q2 = ceil_div(a.Tq, 64u);
     const uint64_t groups = static_cast<uint64_t>(a.heads) * batch;
-    if (q4 * groups >= 512) attn_f16_kernel<TO, 4><<<static_cast<unsigned>(q4 * groups), 256, 0, s>>>(a, q4);
+    const char* env = std::getenv("MI_ATTN_NW");
+    const int nw = env && std::strcmp(env, "2") == 0 ? 2 : env && std::strcmp(env, "4") == 0 ? 4
+                   : q4 * groups >= 512 ? 4 : 2;
+    if (nw == 4) attn_f16_kernel<TO, 4><<<static_cast<unsigned>(q4 * groups), 256, 0, s>>>(a, q4);
     else attn_f16_kernel<TO, 2><<<static_cast<unsigned>(q2 * groups), 128, 0, s>>>(a, q2);
 }
 

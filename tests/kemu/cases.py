@@ -173,9 +173,14 @@ def gemm_nn(E, *, M, N, K, mode=0, batch=1, lda=0, ldb=0, ldc=0, sA=0, sB=0, sC=
 
 
 def attention(E, *, batch=1, Tq, Tk, C, heads, causal=False, f16_in=False, f16_out=False, kv_len=None, seed=1,
-              front=False, order=0, tol=2e-3):
-    """mi_fused_attention_ex (contiguous [batch, T, C]) against the oracle."""
+              front=False, order=0, tol=2e-3, nw=None):
+    """mi_fused_attention_ex (contiguous [batch, T, C]) against the oracle;
+    nw pins the fp16 kernel's workgroup size (MI_ATTN_NW)."""
     E.order(order)
+    if nw:
+        os.environ["MI_ATTN_NW"] = str(nw)
+    else:
+        os.environ.pop("MI_ATTN_NW", None)
     idt = np.float16 if f16_in else np.float32
     q = ob.normal(seed, batch * Tq * C).astype(idt)
     k = ob.normal(seed + 1, batch * Tk * C).astype(idt)

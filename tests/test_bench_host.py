@@ -131,7 +131,8 @@ def test_bench_line_on_stand_in_device(fake_device, monkeypatch, capsys):
     assert out["block_stack"]["blocks"] == 10
     ex = out["extras"]
     for part in ("config0_gemm", "nn_gemm", "block_stack_cached_kv", "block_stack_fused_epilogues",
-                 "block_stack_joint_qkv", "block_stack_fused_joint_cached", "gemm_candidates"):
+                 "block_stack_joint_qkv", "block_stack_fused_joint_cached", "gemm_candidates",
+                 "attention_candidates"):
         assert part in ex and "error" not in ex[part], (part, ex.get(part))
     assert set(ex["gemm_candidates"]["us"]) == set(bench.GEMM_CANDIDATES)
     assert len(ex["gemm_candidates"]["best"]) == len(bench.GEMM_SHAPES) + 1

@@ -93,6 +93,9 @@ FAMILIES = {
         dict(batch=2, Tq=70, Tk=77, C=640, heads=10, f16_in=True, f16_out=True, kv_len=[77, 40]),
         dict(batch=2, Tq=130, Tk=200, C=128, heads=2, f16_in=True, f16_out=True, causal=True),
         dict(batch=2, Tq=33, Tk=70, C=320, heads=5, f16_in=True, f16_out=False, kv_len=[1, 70]),
+        # the 4-wave fp16 kernel (chosen for large grids) on small shapes
+        dict(batch=2, Tq=200, Tk=300, C=128, heads=2, f16_in=True, f16_out=True, causal=True, nw=4),
+        dict(batch=2, Tq=130, Tk=77, C=640, heads=10, f16_in=True, f16_out=False, kv_len=[77, 13], nw=4),
     ],
     "block": [
         dict(B=1, T=33, C=64, H=1, Tc=5, Cc=96, F=160),
