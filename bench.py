@@ -252,9 +252,10 @@ def time_case(c, stream, hip, reps):
 # of the step and on config 0, so the tile rules can be re-derived from one run:
 # the LDS kernel's 256x128 / 128x128 / 128x64 / 64x64 / 256x256 tiles (0-4) with
 # and without K splits, the row-stationary builds (5, 6; row-coalesced A 7-10)
-# and the 4-wave LDS builds: 256x256 (11), 256x128 (12) and 128x256 (13).
+# the 4-wave LDS builds: 256x256 (11), 256x128 (12) and 128x256 (13), and the
+# 8-wave 192x256 LDS build (14).
 GEMM_CANDIDATES = ["0", "0:2", "0:4", "1", "1:2", "2", "2:2", "3", "3:2", "3:4", "3:8", "4", "4:2", "5", "6",
-                   "7", "8", "9", "10", "11", "12", "12:2", "13", "13:2"]
+                   "7", "8", "9", "10", "11", "12", "12:2", "13", "13:2", "14", "14:2"]
 
 
 def _part(out, name, fn):

@@ -1012,6 +1012,7 @@ enum CfgId {
     kR256x256Q, kR256x192Q, kR256x160Q, kR256x128Q,           // row kernel, row-coalesced A
     kC256x256W4,                                              // LDS kernel, 4 waves of 128x128, one set in flight
     kC256x128W4, kC128x256W4,                                 // LDS kernel, 4 waves of 128x64 / 64x128
+    kC192x256,                                                // LDS kernel, 8 waves of 96x64
     kNumCfg
 };
 
@@ -1129,6 +1130,7 @@ void launch(int cfg, const GemmArgs& a, uint32_t batch, uint32_t splits, hipStre
         case kC256x128: launch_cfg<256, 128, 4, 2, 2, WK, false, 2, EPI>(a, batch, splits, s); break;
         case kC128x128: launch_cfg<128, 128, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, s); break;
         case kC256x128W4: launch_cfg<256, 128, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, s); break;
+        case kC192x256: launch_cfg<192, 256, 2, 4, 2, WK, false, 2, EPI>(a, batch, splits, s); break;
         case kC128x256W4: launch_cfg<128, 256, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, s); break;
         case kC256x256W4:
             // one wave per SIMD with 128 x 128 per wave (256 accumulator AGPRs)

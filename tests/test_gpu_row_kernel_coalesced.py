@@ -4,7 +4,8 @@ the other tile configurations, tests/test_gpu_gemm.py): the row-stationary
 kernel with row-coalesced A loads and the quad transpose (MI_GEMM_CFG=7..10:
 256 x 256 / 192 / 160 / 128 tiles) and the 4-wave 256 x 256 LDS kernel
 (MI_GEMM_CFG=11, one wave per SIMD, no K split), and the 4-wave 256 x 128 and
-128 x 256 LDS builds (12, 13: 128 x 64 / 64 x 128 per wave)."""
+128 x 256 LDS builds (12, 13: 128 x 64 / 64 x 128 per wave), and the 8-wave
+192 x 256 LDS build (14: 96 x 64 per wave)."""
 import numpy as np
 import pytest
 
@@ -16,7 +17,7 @@ from test_gpu_gemm import run_q8_0
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("cfg", ["7", "7:2", "8", "9:3", "10", "11", "12", "12:2", "13", "13:3"])
+@pytest.mark.parametrize("cfg", ["7", "7:2", "8", "9:3", "10", "11", "12", "12:2", "13", "13:3", "14", "14:2"])
 @pytest.mark.parametrize("M,N,K", [(300, 200, 640), (1030, 130, 256), (257, 512, 128)])
 def test_coalesced_rows_config(gpu, oracle, monkeypatch, cfg, M, N, K):
     print(f"[case] cfg={cfg} M={M} N={N} K={K}", flush=True)
@@ -38,7 +39,7 @@ def test_coalesced_rows_config(gpu, oracle, monkeypatch, cfg, M, N, K):
     assert_parity(dC.download(np.float32, M * N).reshape(M, N), want, what=f"cfg {cfg} split layout")
 
 
-@pytest.mark.parametrize("cfg", ["7", "11", "12", "13"])
+@pytest.mark.parametrize("cfg", ["7", "11", "12", "13", "14"])
 def test_candidate_config_baseline_shape(gpu, oracle, monkeypatch, cfg):
     M, N, K = 9216, 1280, 1280
     print(f"[case] cfg={cfg} baseline M={M} N={N} K={K}", flush=True)

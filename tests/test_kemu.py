@@ -55,6 +55,8 @@ FAMILIES = {
         # 4-wave 256x128 / 128x256 (128x64 / 64x128 per wave), K splits and the split layout
         dict(M=300, N=300, K=256, cfg="12"), dict(M=260, N=130, K=320, cfg="12:3", layout="split", mode=1),
         dict(M=300, N=300, K=256, cfg="13:2"), dict(M=130, N=520, K=192, cfg="13", layout="split", front=True),
+        # 192x256 (8 waves of 96x64)
+        dict(M=400, N=300, K=256, cfg="14"), dict(M=200, N=260, K=320, cfg="14:2", layout="split", mode=1),
     ],
     # row-stationary kernel: per-lane-row A (5, 6) and row-coalesced A (7-10)
     "gemm_rows": [
@@ -76,6 +78,7 @@ FAMILIES = {
         dict(case="gemm_geglu", M=70, F=40, K=128, cfg="1", bias=False),
         dict(case="gemm_nt", M=300, N=200, K=256, cfg="11", mode=2), dict(case="gemm_geglu", M=300, F=130, K=256, cfg="11"),
         dict(case="gemm_nt", M=200, N=300, K=256, cfg="12:2", mode=2), dict(case="gemm_geglu", M=200, F=260, K=128, cfg="13"),
+        dict(case="gemm_geglu", M=200, F=130, K=128, cfg="14"),
     ],
     "gemm_nn": [
         dict(M=64, N=64, K=32), dict(M=100, N=72, K=96), dict(M=130, N=260, K=100, mode=1),
