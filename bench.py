@@ -272,8 +272,9 @@ def extras(rng, hip, ops, stream, reps):
     harness's GEMM shape), the NN GEMM at the SDXL conv shapes, the config-4
     stack with the context's K / V cached, with the fused epilogues
     (MI_BLOCK_EPILOGUE=fused), with joint Q/K/V weights and with all three, and
-    the candidate GEMM tile builds on every GEMM shape of the step, and both
-    workgroup sizes of the fp16 attention kernel on every attention shape. These
+    the candidate GEMM tile builds on every GEMM shape of the step, both
+    workgroup sizes of the fp16 attention kernel on every attention shape, and
+    the step replayed from a HIP graph next to the eager step. These
     paths run in a child process (bench.py --extras-child): a failure there
     cannot cost the step measurement."""
     out = {}
@@ -344,8 +345,42 @@ def extras(rng, hip, ops, stream, reps):
                 os.environ.pop("MI_ATTN_NW", None)
         return res
 
+    def step_graph():
+        """The step (every GEMM and attention shape, in order) issued eagerly and
+        replayed from a HIP graph captured once: the gap between the two is the
+        host launch overhead the eager step pays."""
+        cases = [GemmCase(t, M, N, K, rng, hip, ops) for t, M, N, K in GEMM_SHAPES]
+        cases += [AttnCase(t, B, H, Tq, Tk, m, rng, hip, ops) for t, B, H, Tq, Tk, m in ATTN_SHAPES]
+        flops = sum(c.flops for c in cases)
+        steps = 20
+
+        def timed(run):
+            run()
+            stream.synchronize()
+            a, b = hip.Event(), hip.Event()
+            a.record(stream)
+            for _ in range(steps):
+                run()
+            b.record(stream)
+            b.synchronize()
+            return a.elapsed_ms(b) / steps
+
+        def eager():
+            for c in cases:
+                c.run(stream)
+
+        g = hip.Graph(stream)
+        g.begin()
+        eager()
+        g.end()
+        ms_e, ms_g = timed(eager), timed(g.launch)
+        return {"ms_per_step_eager": round(ms_e, 4), "ms_per_step_graph": round(ms_g, 4),
+                "tflops_eager": round(flops / (ms_e / 1e3) / 1e12, 2),
+                "tflops_graph": round(flops / (ms_g / 1e3) / 1e12, 2), "steps": steps}
+
     _part(out, "gemm_candidates", candidates)
     _part(out, "attention_candidates", attn_candidates)
+    _part(out, "step_graph", step_graph)
     return out
 
 

@@ -47,6 +47,12 @@ def lib() -> ctypes.CDLL:
         h.hipGetDeviceCount.argtypes = [ctypes.POINTER(ctypes.c_int)]
         h.hipDeviceGetAttribute.argtypes = [ctypes.POINTER(ctypes.c_int), ctypes.c_int, ctypes.c_int]
         h.hipDeviceGetName.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_int]
+        h.hipStreamBeginCapture.argtypes = [vp, ctypes.c_int]
+        h.hipStreamEndCapture.argtypes = [vp, ctypes.POINTER(vp)]
+        h.hipGraphInstantiate.argtypes = [ctypes.POINTER(vp), vp, vp, ctypes.c_char_p, sz]
+        h.hipGraphLaunch.argtypes = [vp, vp]
+        h.hipGraphExecDestroy.argtypes = [vp]
+        h.hipGraphDestroy.argtypes = [vp]
         _hip = h
     return _hip
 
@@ -170,5 +176,38 @@ class Event:
         try:
             if self.handle.value:
                 lib().hipEventDestroy(self.handle)
+        except Exception:
+            pass
+
+
+class Graph:
+    """A stream capture turned into an executable graph (hipStreamBeginCapture /
+    hipStreamEndCapture / hipGraphInstantiate): the launches issued on `stream`
+    between begin() and end() are recorded, not run, and launch() replays them.
+    Only kernel launches belong in a graph here (no hipMemsetAsync nodes)."""
+
+    CAPTURE_THREAD_LOCAL = 1  # hipStreamCaptureModeThreadLocal
+
+    def __init__(self, stream: Stream):
+        self.stream = stream
+        self.graph = ctypes.c_void_p()
+        self.exec = ctypes.c_void_p()
+
+    def begin(self) -> None:
+        check(lib().hipStreamBeginCapture(self.stream.handle, self.CAPTURE_THREAD_LOCAL), "hipStreamBeginCapture")
+
+    def end(self) -> None:
+        check(lib().hipStreamEndCapture(self.stream.handle, ctypes.byref(self.graph)), "hipStreamEndCapture")
+        check(lib().hipGraphInstantiate(ctypes.byref(self.exec), self.graph, None, None, 0), "hipGraphInstantiate")
+
+    def launch(self) -> None:
+        check(lib().hipGraphLaunch(self.exec, self.stream.handle), "hipGraphLaunch")
+
+    def __del__(self):
+        try:
+            if self.exec.value:
+                lib().hipGraphExecDestroy(self.exec)
+            if self.graph.value:
+                lib().hipGraphDestroy(self.graph)
         except Exception:
             pass

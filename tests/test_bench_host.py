@@ -67,8 +67,22 @@ class _Event:
         return end.at - self.at
 
 
+class _Graph:
+    def __init__(self, stream):
+        self.stream = stream
+
+    def begin(self):
+        pass
+
+    def end(self):
+        pass
+
+    def launch(self):
+        pass
+
+
 def _fake_hip():
-    m = types.SimpleNamespace(DeviceBuffer=_Buf, Stream=_Stream, Event=_Event, device_count=lambda: 1,
+    m = types.SimpleNamespace(DeviceBuffer=_Buf, Stream=_Stream, Event=_Event, Graph=_Graph, device_count=lambda: 1,
                               device_name=lambda d=0: "stand-in", synchronize=lambda: None)
     return m
 
@@ -132,7 +146,7 @@ def test_bench_line_on_stand_in_device(fake_device, monkeypatch, capsys):
     ex = out["extras"]
     for part in ("config0_gemm", "nn_gemm", "block_stack_cached_kv", "block_stack_fused_epilogues",
                  "block_stack_joint_qkv", "block_stack_fused_joint_cached", "gemm_candidates",
-                 "attention_candidates"):
+                 "attention_candidates", "step_graph"):
         assert part in ex and "error" not in ex[part], (part, ex.get(part))
     assert set(ex["gemm_candidates"]["us"]) == set(bench.GEMM_CANDIDATES)
     assert len(ex["gemm_candidates"]["best"]) == len(bench.GEMM_SHAPES) + 1
