@@ -348,8 +348,13 @@ inline void buffer_load_lds(Rsrc r, void* lds, int size, uint32_t voff, uint32_t
         case 12: buf_load<3>(r, voff, soff, x, "raw_ptr_buffer_load_lds"); break;
         default: buf_load<4>(r, voff, soff, x, "raw_ptr_buffer_load_lds"); break;
     }
-    std::memcpy(static_cast<unsigned char*>(lds) + offset + static_cast<size_t>(size) * lane_id(), x, size);
+    dma_enqueue(static_cast<unsigned char*>(lds) + offset + static_cast<size_t>(size) * lane_id(), x, size);
 }
+
+// s_waitcnt: only the vector-memory count matters here (loads into registers
+// complete at once in this emulation; LDS DMA writes wait in a queue).
+// gfx9 encoding: vmcnt = imm[3:0] | imm[15:14] << 4.
+inline void s_waitcnt(int imm) { dma_wait_vmcnt((imm & 0xF) | (((imm >> 14) & 3) << 4)); }
 
 // wave vote: nonzero in every lane when the predicate holds in any lane
 inline void any_fn(const unsigned char (*ins)[256], unsigned char (*outs)[256], const void*) {
@@ -406,5 +411,5 @@ inline T __shfl_xor(T v, int mask, int width = 64) {
 #define __builtin_amdgcn_raw_ptr_buffer_load_lds ::kemu::buffer_load_lds
 #define __builtin_amdgcn_sched_barrier(...) ((void)0)
 #define __builtin_amdgcn_sched_group_barrier(...) ((void)0)
-#define __builtin_amdgcn_s_waitcnt(...) ((void)0)
+#define __builtin_amdgcn_s_waitcnt ::kemu::s_waitcnt
 #define __builtin_amdgcn_s_setprio(...) ((void)0)

@@ -34,11 +34,18 @@ struct Wave {
 
 }  // namespace
 
+struct PendingDma {
+    void* dst;
+    unsigned char data[16];
+    int size;
+};
+
 struct Thread {
     ucontext_t ctx;
     dim3v idx;
     int linear = 0, lane = 0, wave = 0;
     int state = kRun;
+    std::deque<PendingDma> dma;  // LDS DMA writes not yet retired by a vmcnt wait
 };
 
 namespace {
@@ -117,9 +124,18 @@ void release_barrier(Block& b) {
 
 void yield_to_scheduler(Thread* t) { swapcontext(&t->ctx, &g_sched); }
 
+void retire_dma(Thread* t, size_t keep) {
+    while (t->dma.size() > keep) {
+        const PendingDma& d = t->dma.front();
+        std::memcpy(d.dst, d.data, static_cast<size_t>(d.size));
+        t->dma.pop_front();
+    }
+}
+
 void thread_entry() {
     g_blk->body->run();
     Thread* t = g_cur;
+    retire_dma(t, 0);
     Block& b = *g_blk;
     Wave& w = b.waves[t->wave];
     t->state = kDone;
@@ -203,6 +219,14 @@ void die(const char* fmt, ...) {
     fflush(stderr);
     _exit(70);
 }
+
+void dma_enqueue(void* lds_dst, const void* data, int size) {
+    if (size <= 0 || size > 16) die("LDS DMA of %d bytes", size);
+    PendingDma d{lds_dst, {}, size};
+    std::memcpy(d.data, data, static_cast<size_t>(size));
+    g_cur->dma.push_back(d);
+}
+void dma_wait_vmcnt(int n) { retire_dma(g_cur, static_cast<size_t>(n < 0 ? 0 : n)); }
 
 void enqueue_copy(void* dst, const void* src, size_t n) { g_copies.push_back(Copy{dst, src, n}); }
 uint64_t copy_seq() { return g_copy_base + g_copies.size(); }

@@ -16,6 +16,8 @@
 //     written shows up in the results;
 //   * buffer resources range-check every dword like the hardware's raw buffer
 //     loads (out of range: loads return 0, stores are dropped);
+//   * a DMA load into LDS writes LDS only when an s_waitcnt vmcnt of the
+//     issuing work-item retires it (or the work-item exits);
 //   * device memory is host memory; tests allocate it with kemu_alloc, which
 //     places the buffer against a PROT_NONE guard page, so an access past its
 //     end faults and the fault handler names the kernel, workgroup and lane.
@@ -55,6 +57,15 @@ void syncthreads();
 typedef void (*WaveFn)(const unsigned char (*ins)[256], unsigned char (*outs)[256], const void* ctx);
 void wave_op(const char* name, const void* in, size_t n_in, void* out, size_t n_out, WaveFn fn, const void* ctx);
 int lane_id();
+
+// ---- LDS DMA (buffer_load ... lds) ----------------------------------------------------
+// The LDS write of a DMA load lands when the issuing work-item's
+// s_waitcnt vmcnt(n) retires it (oldest first, until n remain), or when the
+// work-item exits -- not at a barrier (the hardware's s_barrier does not wait
+// for vector memory), so a read of a DMA target that no wait covers sees the
+// old LDS contents.
+void dma_enqueue(void* lds_dst, const void* data, int size);
+void dma_wait_vmcnt(int n);
 
 // ---- deferred copies -------------------------------------------------------------
 void enqueue_copy(void* dst, const void* src, size_t n);

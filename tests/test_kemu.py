@@ -176,6 +176,10 @@ PLANTED = {
                            "        __syncthreads();\n        load(min(s_begin + j + 3, last), S1{});",
                            "        load(min(s_begin + j + 3, last), S1{});",
                            dict(case="gemm_nn", M=130, N=260, K=256)),
+    # fp16 attention: the vmcnt wait for the iteration's K / V DMA removed before the barrier
+    "attn_dma_wait": ("attention.hip", "            dma_wait();\n            __syncthreads();\n        };",
+                      "            __syncthreads();\n        };",
+                      dict(case="attention", batch=2, Tq=130, Tk=200, C=128, heads=2, f16_in=True, f16_out=True)),
     # GGUF upload refills a staging buffer without waiting for its last copy
     "staging_reuse": ("gguf.cpp",
                       "    if (g->stage_used[i] && hipEventSynchronize(g->done[i]) != hipSuccess)\n"
