@@ -206,6 +206,160 @@ def attention(E, *, batch=1, Tq, Tk, C, heads, causal=False, f16_in=False, f16_o
     return assert_parity(got, want, tol=tol, what="attention")
 
 
+# ---- full-size shapes with sampled workgroups ----------------------------------
+# The benchmark's shapes at their real size, with only a few workgroups
+# emulated (kemu_set_sample): the first one and the one that takes the last
+# tile in the kernel's order (the bottom-right corner), with every K split and
+# batch of those tiles. Inputs are the full tensors on guarded buffers, so the
+# grids, tile counts, split choices and offsets are those of the GPU run;
+# every element the sampled workgroups wrote is compared with the oracle's
+# rows, and the written region must consist of whole 32-aligned MFMA tiles.
+
+def _block_of_tile(t: int, nb: int) -> int:
+    """blockIdx.x that the kernels' XCD swizzle (8 contiguous chunks of the
+    tile order, chunk i on blockIdx.x % 8 == i) maps to linear tile t."""
+    per, rem = divmod(nb, 8)
+    if t < rem * (per + 1):
+        xcd, local = divmod(t, per + 1)
+    else:
+        xcd, local = rem + (t - rem * (per + 1)) // per, (t - rem * (per + 1)) % per
+    return local * 8 + xcd
+
+
+def _probe_grid(E, spec_none: str, call) -> tuple[str, tuple[int, int, int]]:
+    """Launches with no workgroup emulated and returns the main launch's grid."""
+    E.sample(spec_none)
+    call()
+    return E.last_launch()
+
+
+def _whole_tiles(mask: np.ndarray, what: str) -> None:
+    """Runs of written elements along rows and along columns start at a
+    multiple of 32 and span a multiple of 32 unless they end at the edge."""
+    for m in (mask, mask.T):
+        pad = np.zeros((m.shape[0], 1), dtype=np.int8)
+        d = np.diff(np.concatenate([pad, m.astype(np.int8), pad], axis=1), axis=1)
+        _, s = np.nonzero(d == 1)
+        _, e = np.nonzero(d == -1)
+        bad = (s % 32 != 0) | (((e - s) % 32 != 0) & (e != m.shape[1]))
+        assert not bad.any(), f"{what}: written region is not whole 32-aligned tiles ({int(bad.sum())} runs)"
+
+
+def gemm_full(E, *, M, N, K, cfg=None, layout="q8_0", seed=1, order=0, tol=2e-3):
+    """mi_gemm_nt_q8_0 / _split at a full benchmark shape, sampled workgroups."""
+    _set_cfg(cfg)
+    E.order(order)
+    A = ob.normal(seed, M * K)
+    blocks = q8_weights(ob, seed + 1, N, K)
+    dA, dC = E.buf(A), E.buf(np.zeros(M * N, np.float32))
+    if layout == "q8_0":
+        dW = E.buf(blocks)
+        call = lambda: E.call("mi_gemm_nt_q8_0", dA.ptr, dW.ptr, None, dC.ptr, M, N, K, 0, 0, 0, 1, 0, 0, None)
+    else:
+        payload, scales = ob.q8_0_to_split(blocks, N * K)
+        dP, dS = E.buf(payload), E.buf(scales)
+        call = lambda: E.call("mi_gemm_nt_q8_split", dA.ptr, dP.ptr, dS.ptr, None, dC.ptr, M, N, K, 0, 0, 0, 1, 0, 0,
+                              None)
+    helpers = "gemm_init_kernel|-|-|-;gemm_bias_add_kernel|-|-|-"
+    kern, grid = _probe_grid(E, f"gemm_q8_kernel|-|-|-;gemm_q8_rows_kernel|-|-|-;{helpers}", call)
+    assert not np.any(dC.get(np.float32, M * N)), "a launch with no workgroup wrote C"
+    xs = sorted({0, _block_of_tile(grid[0] - 1, grid[0])})
+    x = ",".join(map(str, xs))
+    print(f"  {kern} grid {grid}, blockIdx.x {xs}", flush=True)
+    E.sample(f"gemm_q8_kernel|{x}|*|*;gemm_q8_rows_kernel|{x}|*|*;{helpers}")
+    before = E.lib.kemu_blocks_run()
+    call()
+    ran = E.lib.kemu_blocks_run() - before
+    assert ran == len(xs) * grid[1] * grid[2], f"{ran} workgroups ran, expected {len(xs)} x {grid[1]} x {grid[2]}"
+    got = dC.get(np.float32, M * N).reshape(M, N)
+    mask = got != 0
+    assert mask.any(), "the sampled workgroups wrote nothing"
+    _whole_tiles(mask, f"gemm {kern} {grid}")
+    rows = np.flatnonzero(mask.any(axis=1))
+    want = ob.gemm_rows(A, blocks, M, N, K, rows, threads=ob.max_threads())
+    sub = mask[rows]
+    e = assert_parity(got[rows][sub], want[sub], tol=tol, what=f"gemm full {kern} grid {grid}")
+    # the corner tile is among those written
+    assert mask[M - 1, N - 1], "the bottom-right tile was not sampled"
+    return e
+
+
+def gemm_nn_full(E, *, M, N, K, seed=1, order=0, tol=2e-3):
+    """mi_gemm_nn_q8_split at a full SDXL conv shape, sampled workgroups (the
+    first and last column tiles of the last row tile, every K split)."""
+    E.order(order)
+    os.environ.pop("MI_NN_KERNEL", None)
+    w = ob.normal(seed, M * K, 0.0, 0.02)
+    payload, scales = ob.q8_0_to_split(ob.q8_0_quantize(w), M * K)
+    B = ob.normal(seed + 1, K * N)
+    dP, dS, dB, dC = E.buf(payload), E.buf(scales), E.buf(B), E.buf(np.zeros(M * N, np.float32))
+    call = lambda: E.call("mi_gemm_nn_q8_split", dP.ptr, dS.ptr, dB.ptr, dC.ptr, M, N, K, 0, 0, 0, 0, 1, 0, 0, 0,
+                          None)
+    kern, grid = _probe_grid(E, "gemm_nn_q8_tiled_kernel|-|-|-;gemm_nn_q8_kernel|-|-|-;gemm_nn_zero_kernel|-|-|-",
+                             call)
+    print(f"  {kern} grid {grid}", flush=True)
+    E.sample("gemm_nn_q8_tiled_kernel|0,-1|-1|*;gemm_nn_q8_kernel|0,-1|-1|*;gemm_nn_zero_kernel|-|-|-")
+    call()
+    got = dC.get(np.float32, M * N).reshape(M, N)
+    mask = got != 0
+    assert mask.any() and mask[M - 1, N - 1], "the sampled workgroups did not write the corner tile"
+    _whole_tiles(mask, f"gemm_nn {kern} {grid}")
+    rows = np.flatnonzero(mask.any(axis=1))
+    want = ob.gemm_nn_q8_split(payload.reshape(M, -1)[rows].reshape(-1), scales.reshape(M, -1)[rows].reshape(-1),
+                               B, len(rows), N, K, threads=ob.max_threads()).reshape(len(rows), N)
+    sub = mask[rows]
+    return assert_parity(got[rows][sub], want[sub], tol=tol, what=f"gemm_nn full {kern} grid {grid}")
+
+
+def attention_full(E, *, batch, Tq, Tk, C, heads, masked=False, nw=None, seed=1, order=0, tol=2e-3):
+    """fp16 mi_fused_attention_ex at a full benchmark shape, sampled workgroups
+    (the first and the last in the kernel's order)."""
+    E.order(order)
+    if nw:
+        os.environ["MI_ATTN_NW"] = str(nw)
+    else:
+        os.environ.pop("MI_ATTN_NW", None)
+    q = ob.normal(seed, batch * Tq * C).astype(np.float16)
+    k = ob.normal(seed + 1, batch * Tk * C).astype(np.float16)
+    v = ob.normal(seed + 2, batch * Tk * C).astype(np.float16)
+    kv_len = ob.uniform_int(seed + 6, 1, Tk, batch).astype(np.int32) if masked else None
+    sentinel = np.float16(7.0)
+    dq, dk, dv = E.buf(q), E.buf(k), E.buf(v)
+    do = E.buf(np.full(batch * Tq * C, sentinel, np.float16))
+    dl = E.buf(kv_len) if masked else None
+    x = MiAttnArgs(q=dq.ptr, k=dk.ptr, v=dv.ptr, out=do.ptr, batch=batch, Tq=Tq, Tk=Tk, C=C, heads=heads, causal=0,
+                   in_dtype=MI_F16, out_dtype=MI_F16, kv_len=dl.ptr if dl else None)
+    call = lambda: E.call("mi_fused_attention_ex", ctypes.byref(x), None)
+    kern, grid = _probe_grid(E, "attn_f16_kernel|-|-|-;attn_kernel|-|-|-", call)
+    xs = sorted({0, _block_of_tile(grid[0] - 1, grid[0])})
+    xl = ",".join(map(str, xs))
+    print(f"  {kern} grid {grid}, blockIdx.x {xs}", flush=True)
+    E.sample(f"attn_f16_kernel|{xl}|*|*;attn_kernel|{xl}|*|*")
+    call()
+    hd = C // heads
+    got = do.get(np.float16, batch * Tq * C).reshape(batch, Tq, heads, hd)
+    mask = got != sentinel
+    head_written = mask.any(axis=3)
+    assert head_written.any() and head_written[batch - 1, Tq - 1, heads - 1], "last query tile not sampled"
+    assert np.array_equal(mask, np.repeat(head_written[..., None], hd, axis=3)), "partially written head rows"
+    for b in range(batch):
+        for h in range(heads):
+            r = np.flatnonzero(head_written[b, :, h])
+            if r.size:
+                assert r[0] % 32 == 0 and (r.size % 32 == 0 or r[-1] == Tq - 1) and np.all(np.diff(r) == 1), \
+                    f"written query rows of (batch {b}, head {h}) are not whole tiles"
+    rows = np.flatnonzero(head_written.any(axis=(0, 2)))
+    want = ob.fused_attention_ex(q, k, v, batch=batch, Tq=Tq, Tk=Tk, C=C, heads=heads, in_dtype=ob.OR_F16,
+                                 out_dtype=ob.OR_F32, kv_len=kv_len, rows=rows,
+                                 threads=ob.max_threads()).reshape(batch, len(rows), heads, hd)
+    sel = mask[:, rows]
+    g = got[:, rows].astype(np.float64)[sel]
+    w = want.astype(np.float64)[sel]
+    bound = tol * rms(w) + fp16_half_ulp(w)
+    assert np.all(np.abs(g - w) <= bound), f"attention full {kern} grid {grid}: beyond tol x RMS + half an ulp"
+    return float(np.max(np.abs(g - w)) / rms(w))
+
+
 def block(E, *, B, T, C, H, Tc, Cc, F, masked=False, blocks=2, order=0, front=False, fused=False, qkv_joint=False):
     """Two applications of one SDXL transformer block: uncached
     (mi_sdxl_block_forward) vs context K / V projected once (mi_block_ctx_kv,
@@ -401,7 +555,8 @@ def gguf_upload(E, *, big_rows=10240, big_cols=1280, order=0, front=False):
 
 
 CASES = {"gemm_nt": gemm_nt, "gemm_geglu": gemm_geglu, "gemm_nn": gemm_nn, "attention": attention, "block": block,
-         "gguf_upload": gguf_upload, "q8": q8, "glue": glue}
+         "gguf_upload": gguf_upload, "q8": q8, "glue": glue, "gemm_full": gemm_full, "gemm_nn_full": gemm_nn_full,
+         "attention_full": attention_full}
 
 
 def main(argv):

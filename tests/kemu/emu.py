@@ -53,6 +53,10 @@ class Emu:
         self.lib.kemu_alloc.restype, self.lib.kemu_alloc.argtypes = ctypes.c_void_p, [ctypes.c_size_t, ctypes.c_int]
         self.lib.kemu_set_order.argtypes = [ctypes.c_int, ctypes.c_int]
         self.lib.kemu_launches.restype = ctypes.c_uint64
+        self.lib.kemu_blocks_run.restype = ctypes.c_uint64
+        self.lib.kemu_set_sample.argtypes = [ctypes.c_char_p]
+        self.lib.kemu_last_grid.argtypes = [ctypes.POINTER(ctypes.c_uint32)]
+        self.lib.kemu_last_kernel.restype = ctypes.c_char_p
         self.lib.kemu_sync.restype = None
 
     def buf(self, arr=None, *, nbytes: int | None = None, front: bool = False) -> Buf:
@@ -70,6 +74,18 @@ class Emu:
 
     def status(self, name: str, *args) -> int:
         return getattr(self.lib, name)(*args)
+
+    def sample(self, spec: str = "") -> None:
+        """Emulate only some workgroups: rules "kernel|x|y|z" joined by ';', each
+        dimension '*' (all), '-' (none) or indices (negative: from the end);
+        kernels that no rule names run in full. "" runs everything."""
+        self.lib.kemu_set_sample(spec.encode())
+
+    def last_launch(self) -> tuple[str, tuple[int, int, int]]:
+        """(kernel text, grid) of the most recent launch."""
+        g = (ctypes.c_uint32 * 3)()
+        self.lib.kemu_last_grid(g)
+        return self.lib.kemu_last_kernel().decode(), (g[0], g[1], g[2])
 
     def order(self, order: int, reverse_blocks: bool = False) -> None:
         """order bits: 1 lanes reversed, 2 waves reversed, 4 wave-major."""

@@ -12,8 +12,10 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <deque>
 #include <map>
+#include <string>
 #include <vector>
 
 extern "C" __attribute__((weak)) char __start_kemu_lds[];
@@ -68,7 +70,17 @@ constexpr size_t kPage = 4096;
 // the next wave starts) instead of one wave operation per wave per pass
 enum { kRevLanes = 1, kRevWaves = 2, kWaveMajor = 4 };
 int g_order = 0, g_rev_blocks = 0;
-uint64_t g_launches = 0;
+uint64_t g_launches = 0, g_blocks_run = 0;
+// workgroup sampling (kemu_set_sample): the first rule whose kernel text is
+// part of the launched kernel's name picks, per grid dimension, every index
+// (all) or a list (negative entries count from the end; an empty list runs
+// no workgroup of that kernel)
+struct SampleRule {
+    std::string kernel;
+    bool all[3] = {true, true, true};
+    std::vector<long> idx[3];
+};
+std::vector<SampleRule> g_sample;
 const char* g_kernel = "";
 std::map<void*, std::pair<void*, size_t>> g_allocs;
 bool g_handler = false;
@@ -285,11 +297,31 @@ void run_grid(const char* name, dim3v grid, dim3v block, Body& body) {
     b.body = &body;
     b.th.resize(nthreads);
     b.waves.resize((nthreads + 63) / 64);
+    const SampleRule* rule = nullptr;
+    for (const SampleRule& r : g_sample)
+        if (std::strstr(name, r.kernel.c_str())) {
+            rule = &r;
+            break;
+        }
+    const uint32_t dims[3] = {grid.x, grid.y, grid.z};
+    auto sampled = [&](const dim3v& bi) {
+        if (!rule) return true;
+        const uint32_t at[3] = {bi.x, bi.y, bi.z};
+        for (int d = 0; d < 3; ++d) {
+            if (rule->all[d]) continue;
+            bool hit = false;
+            for (long v : rule->idx[d]) hit |= (v < 0 ? static_cast<long>(dims[d]) + v : v) == static_cast<long>(at[d]);
+            if (!hit) return false;
+        }
+        return true;
+    };
     const uint64_t nblocks = static_cast<uint64_t>(grid.x) * grid.y * grid.z;
     for (uint64_t bi = 0; bi < nblocks; ++bi) {
         const uint64_t lin = g_rev_blocks ? nblocks - 1 - bi : bi;
         g_block_idx = dim3v{static_cast<uint32_t>(lin % grid.x), static_cast<uint32_t>(lin / grid.x % grid.y),
                             static_cast<uint32_t>(lin / grid.x / grid.y)};
+        if (!sampled(g_block_idx)) continue;
+        ++g_blocks_run;
         for (uint64_t i = 0; i < nthreads; ++i) {
             Thread& t = b.th[i];
             t.linear = static_cast<int>(i);
@@ -346,5 +378,52 @@ extern "C" void kemu_set_order(int order, int reverse_blocks) {
 }
 
 extern "C" uint64_t kemu_launches(void) { return g_launches; }
+extern "C" uint64_t kemu_blocks_run(void) { return g_blocks_run; }
+extern "C" void kemu_last_grid(uint32_t* xyz) {
+    xyz[0] = g_grid_dim.x;
+    xyz[1] = g_grid_dim.y;
+    xyz[2] = g_grid_dim.z;
+}
+
+// spec: rules separated by ';', each "kernel|x|y|z" where a dimension is '*'
+// (every index), '-' (none) or comma-separated indices (negative: from the
+// end). An empty spec runs every workgroup of every kernel.
+extern "C" void kemu_set_sample(const char* spec) {
+    g_sample.clear();
+    std::string s = spec ? spec : "";
+    size_t pos = 0;
+    while (pos < s.size()) {
+        size_t end = s.find(';', pos);
+        if (end == std::string::npos) end = s.size();
+        const std::string item = s.substr(pos, end - pos);
+        pos = end + 1;
+        if (item.empty()) continue;
+        std::vector<std::string> f;
+        size_t a = 0;
+        for (size_t b; (b = item.find('|', a)) != std::string::npos; a = b + 1) f.push_back(item.substr(a, b - a));
+        f.push_back(item.substr(a));
+        if (f.size() != 4 || f[0].empty()) die("kemu_set_sample: bad rule '%s'", item.c_str());
+        SampleRule r;
+        r.kernel = f[0];
+        for (int d = 0; d < 3; ++d) {
+            const std::string& v = f[d + 1];
+            if (v == "*") continue;
+            r.all[d] = false;
+            if (v == "-") continue;
+            size_t c = 0;
+            while (c <= v.size()) {
+                size_t e = v.find(',', c);
+                if (e == std::string::npos) e = v.size();
+                char* stop = nullptr;
+                const std::string num = v.substr(c, e - c);
+                const long x = std::strtol(num.c_str(), &stop, 10);
+                if (num.empty() || *stop) die("kemu_set_sample: bad index '%s' in '%s'", num.c_str(), item.c_str());
+                r.idx[d].push_back(x);
+                c = e + 1;
+            }
+        }
+        g_sample.push_back(std::move(r));
+    }
+}
 extern "C" void kemu_sync(void) { flush_copies(~0ull); }
 extern "C" const char* kemu_last_kernel(void) { return g_kernel; }

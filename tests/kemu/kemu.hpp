@@ -93,6 +93,9 @@ void* kemu_alloc(size_t bytes, int guard_front);
 void kemu_free(void* p);
 void kemu_set_order(int order, int reverse_blocks);
 uint64_t kemu_launches(void);
+uint64_t kemu_blocks_run(void);  // workgroups emulated so far
+void kemu_set_sample(const char* spec);  // run only some workgroups (kemu.cpp)
+void kemu_last_grid(uint32_t* xyz);      // grid of the last launch
 void kemu_sync(void);  // runs every deferred copy
 const char* kemu_last_kernel(void);
 }

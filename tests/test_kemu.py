@@ -13,7 +13,11 @@ reversed, so a missing barrier changes the result under one of them.
 
 This is where paths are checked before they reach a GPU (the coalesced-A row
 kernel configurations, the NN GEMM, the cached-K/V block, the GGUF uploads,
-the fused GEGLU / residual epilogues);
+the fused GEGLU / residual epilogues). The "fullsize" family runs every
+kernel build the benchmark launches at the benchmark's own shapes, with a
+few workgroups emulated per launch (the first and the bottom-right tile,
+every K split of them): grids, split choices and offsets are those of the
+GPU run, and the written tiles are compared with the oracle's rows;
 it does not measure anything and nothing in the product loads the emulation
 build. test_emulator_catches_planted_faults pins the checker itself: copies
 of the sources with one planted mistake each (compiled for the host only)
@@ -117,6 +121,36 @@ FAMILIES = {
 CASE_OF = {"gemm_lds": "gemm_nt", "gemm_rows": "gemm_nt"}
 
 
+def _fullsize() -> list[dict]:
+    """The benchmark's shapes at full size with sampled workgroups (cases.py
+    gemm_full / gemm_nn_full / attention_full): every GEMM shape through the
+    tile rules, every build of the benchmark's GEMM candidate sweep (shapes in
+    rotation; the 4-wave and 192-row builds also on the widest-output and the
+    deepest-K shape), the NN GEMM at the SDXL conv shapes, and every attention
+    shape with the default and both pinned workgroup sizes."""
+    sys.path.insert(0, str(ROOT))
+    import bench
+    g = [(M, N, K) for _, M, N, K in bench.GEMM_SHAPES + [bench.CONFIG0]]
+    specs = [dict(case="gemm_full", M=M, N=N, K=K) for M, N, K in g]
+    specs.append(dict(case="gemm_full", M=9216, N=1280, K=1280, layout="split"))
+    for i, cfg in enumerate(bench.GEMM_CANDIDATES):
+        M, N, K = g[i % len(g)]
+        specs.append(dict(case="gemm_full", M=M, N=N, K=K, cfg=cfg))
+    for cfg in ("11", "12", "13", "14"):
+        for M, N, K in ((8192, 5120, 640), (2048, 1280, 5120)):
+            specs.append(dict(case="gemm_full", M=M, N=N, K=K, cfg=cfg))
+    specs += [dict(case="gemm_nn_full", M=M, N=N, K=K) for _, M, N, K in bench.NN_SHAPES]
+    for _, b, h, tq, tk, masked in bench.ATTN_SHAPES:
+        for nw in (None, 2, 4):
+            specs.append(dict(case="attention_full", batch=b, Tq=tq, Tk=tk, C=64 * h, heads=h, masked=masked, nw=nw))
+    unique = {json.dumps(s, sort_keys=True): s for s in specs}
+    return list(unique.values())
+
+
+FAMILIES["fullsize"] = _fullsize()
+SCHEDULES = {"fullsize": [0]}  # the barrier-sensitive schedules run at the small shapes above
+
+
 def _workers() -> int:
     return max(1, min(8, os.cpu_count() or 1))
 
@@ -139,12 +173,13 @@ def emulator():
 
 @pytest.mark.parametrize("family", list(FAMILIES))
 def test_kernels_on_emulator(emulator, family):
-    specs = [dict({"case": CASE_OF.get(family, family)}, schedules=BOTH, **s) for s in FAMILIES[family]]
+    sched = SCHEDULES.get(family, BOTH)
+    specs = [dict({"case": CASE_OF.get(family, family)}, schedules=sched, **s) for s in FAMILIES[family]]
     with ThreadPoolExecutor(_workers()) as ex:
         results = list(ex.map(_run, specs))
     failed = []
     for spec, r in zip(specs, results):
-        ok = r.returncode == 0 and r.stdout.count("OK ") == len(BOTH)
+        ok = r.returncode == 0 and r.stdout.count("OK ") == len(sched)
         print(f"{json.dumps(spec)}: {r.stdout.strip() if ok else 'FAILED'}")
         if not ok:
             failed.append(f"{json.dumps(spec)}\n{(r.stdout + r.stderr).strip()[-1500:]}")
