@@ -439,6 +439,51 @@ def block(E, *, B, T, C, H, Tc, Cc, F, masked=False, blocks=2, order=0, front=Fa
     return e
 
 
+def block_full(E, *, fused=False, qkv_joint=False, cached=False, order=0):
+    """The config-4 block (level 2: 2 x 1024 tokens, C 1280, 20 heads, context
+    2 x 77 x 2048, FF 1280 -> 2 x 5120 -> 1280) at full size with the first and
+    last workgroup of every grid dimension of every launch emulated: a bounds
+    check of the workspace carve-up, the joint Q / K / V placement, the cached
+    context K / V buffer and every kernel's offsets at the real sizes (the
+    tensors the skipped workgroups would write stay unwritten, so no values
+    are compared here; the small-shape block cases compare them)."""
+    E.order(order)
+    if fused:
+        os.environ["MI_BLOCK_EPILOGUE"] = "fused"
+    else:
+        os.environ.pop("MI_BLOCK_EPILOGUE", None)
+    B, T, C, H, Tc, Cc, F = 2, 1024, 1280, 20, 77, 2048, 5120
+    w = make_weights(ob, C, Cc, F, seed=500)
+    dw = {k: E.buf(v) for k, v in w.items()}
+    ptrs = {k: b.ptr for k, b in dw.items()}
+    if qkv_joint:
+        joint = E.buf(np.concatenate([w["attn1_q"], w["attn1_k"], w["attn1_v"]]))
+        dw["_joint"] = joint
+        nb = w["attn1_q"].nbytes
+        ptrs.update(attn1_q=joint.ptr, attn1_k=joint.ptr + nb, attn1_v=joint.ptr + 2 * nb)
+    bw = MiBlockWeights(*[ptrs[f[0]] for f in MiBlockWeights._fields_])
+    dims = MiBlockDims(B, T, C, H, Tc, Cc, F)
+    dx = E.buf(ob.normal(3, B * T * C))
+    dc = E.buf(ob.normal(4, B * Tc * Cc).astype(np.float16).astype(np.float32))
+    dl = E.buf(ob.uniform_int(8, 1, Tc, B).astype(np.int32))
+    ws_bytes = E.lib.mi_block_workspace_bytes(ctypes.byref(dims))
+    kv_bytes = E.lib.mi_block_ctx_kv_bytes(ctypes.byref(dims))
+    ws, kv = E.buf(nbytes=ws_bytes).fill(0), E.buf(nbytes=kv_bytes).fill(0)
+    E.sample("*|0,-1|0,-1|0,-1")
+    before = E.lib.kemu_launches()
+    if cached:
+        E.call("mi_block_ctx_kv", ctypes.byref(bw), ctypes.byref(dims), dc.ptr, kv.ptr, kv_bytes, None)
+        E.call("mi_sdxl_block_forward_kv", ctypes.byref(bw), ctypes.byref(dims), dx.ptr, kv.ptr, kv_bytes, dl.ptr,
+               ws.ptr, ws_bytes, None)
+    else:
+        E.call("mi_sdxl_block_forward", ctypes.byref(bw), ctypes.byref(dims), dx.ptr, dc.ptr, dl.ptr, ws.ptr,
+               ws_bytes, None)
+    n = E.lib.kemu_launches() - before
+    print(f"  {n} launches, workspace {ws_bytes} B, context K/V {kv_bytes} B", flush=True)
+    assert n >= 8, f"only {n} launches"
+    return 0.0
+
+
 def q8(E, *, n, seed=1, front=False, order=0):
     """Q8_0 decode (fp32 bit-exact, fp16 = RNE of it), repack to the split
     layout and its decode, and the device quantiser, against the oracle."""
@@ -556,7 +601,7 @@ def gguf_upload(E, *, big_rows=10240, big_cols=1280, order=0, front=False):
 
 CASES = {"gemm_nt": gemm_nt, "gemm_geglu": gemm_geglu, "gemm_nn": gemm_nn, "attention": attention, "block": block,
          "gguf_upload": gguf_upload, "q8": q8, "glue": glue, "gemm_full": gemm_full, "gemm_nn_full": gemm_nn_full,
-         "attention_full": attention_full}
+         "attention_full": attention_full, "block_full": block_full}
 
 
 def main(argv):

@@ -299,7 +299,7 @@ void run_grid(const char* name, dim3v grid, dim3v block, Body& body) {
     b.waves.resize((nthreads + 63) / 64);
     const SampleRule* rule = nullptr;
     for (const SampleRule& r : g_sample)
-        if (std::strstr(name, r.kernel.c_str())) {
+        if (r.kernel == "*" || std::strstr(name, r.kernel.c_str())) {
             rule = &r;
             break;
         }
@@ -385,7 +385,7 @@ extern "C" void kemu_last_grid(uint32_t* xyz) {
     xyz[2] = g_grid_dim.z;
 }
 
-// spec: rules separated by ';', each "kernel|x|y|z" where a dimension is '*'
+// spec: rules separated by ';', each "kernel|x|y|z" (kernel "*": any) where a dimension is '*'
 // (every index), '-' (none) or comma-separated indices (negative: from the
 // end). An empty spec runs every workgroup of every kernel.
 extern "C" void kemu_set_sample(const char* spec) {

@@ -17,7 +17,8 @@ the fused GEGLU / residual epilogues). The "fullsize" family runs every
 kernel build the benchmark launches at the benchmark's own shapes, with a
 few workgroups emulated per launch (the first and the bottom-right tile,
 every K split of them): grids, split choices and offsets are those of the
-GPU run, and the written tiles are compared with the oracle's rows;
+GPU run, and the written tiles are compared with the oracle's rows (the
+config-4 block at full size is a bounds check only);
 it does not measure anything and nothing in the product loads the emulation
 build. test_emulator_catches_planted_faults pins the checker itself: copies
 of the sources with one planted mistake each (compiled for the host only)
@@ -143,6 +144,9 @@ def _fullsize() -> list[dict]:
     for _, b, h, tq, tk, masked in bench.ATTN_SHAPES:
         for nw in (None, 2, 4):
             specs.append(dict(case="attention_full", batch=b, Tq=tq, Tk=tk, C=64 * h, heads=h, masked=masked, nw=nw))
+    # the config-4 block: bounds only (first / last workgroups of every launch)
+    specs += [dict(case="block_full"), dict(case="block_full", cached=True),
+              dict(case="block_full", fused=True, qkv_joint=True)]
     unique = {json.dumps(s, sort_keys=True): s for s in specs}
     return list(unique.values())
 
