@@ -267,7 +267,7 @@ def _part(out, name, fn):
         out[name] = {"error": f"{type(e).__name__}: {e}"}
 
 
-def extras(rng, hip, ops, stream, reps):
+def extras(rng, hip, ops, stream, reps, emit=None):
     """Measurements outside the step metric: BASELINE config 0 (the reference
     harness's GEMM shape), the NN GEMM at the SDXL conv shapes, the config-4
     stack with the context's K / V cached, with the fused epilogues
@@ -276,8 +276,15 @@ def extras(rng, hip, ops, stream, reps):
     workgroup sizes of the fp16 attention kernel on every attention shape, and
     the step replayed from a HIP graph next to the eager step. These
     paths run in a child process (bench.py --extras-child): a failure there
-    cannot cost the step measurement."""
+    cannot cost the step measurement. `emit(out)` is called after every part
+    (and after every GEMM candidate build), so a child that is stopped early
+    still leaves what it measured."""
     out = {}
+
+    def part(name, fn):
+        _part(out, name, fn)
+        if emit:
+            emit(out)
 
     def cfg0():
         c = GemmCase(*CONFIG0, rng, hip, ops)
@@ -312,6 +319,11 @@ def extras(rng, hip, ops, stream, reps):
         cases = [GemmCase(t, M, N, K, rng, hip, ops) for t, M, N, K in GEMM_SHAPES + [CONFIG0]]
         res = {"shapes": [c.tag for c in cases], "us": {}}
         res["default_us"] = [time_case(c, stream, hip, reps)[1]["us"] for c in cases]
+        def best():
+            timed = {k: v for k, v in res["us"].items() if isinstance(v, list)}
+            res["best"] = [min(([k, v[i]] for k, v in timed.items()), key=lambda kv: kv[1]) if timed else None
+                           for i in range(len(cases))]
+
         for cfg in GEMM_CANDIDATES:
             os.environ["MI_GEMM_CFG"] = cfg
             try:
@@ -320,17 +332,12 @@ def extras(rng, hip, ops, stream, reps):
                 res["us"][cfg] = f"{type(e).__name__}: {e}"
             finally:
                 os.environ.pop("MI_GEMM_CFG", None)
-        timed = {k: v for k, v in res["us"].items() if isinstance(v, list)}
-        res["best"] = [min(([k, v[i]] for k, v in timed.items()), key=lambda kv: kv[1]) if timed else None
-                       for i in range(len(cases))]
+            best()
+            if emit:
+                emit(dict(out, gemm_candidates=res))
+        best()
         return res
 
-    _part(out, "config0_gemm", cfg0)
-    _part(out, "nn_gemm", nn)
-    _part(out, "block_stack_cached_kv", stack(cached_kv=True))
-    _part(out, "block_stack_fused_epilogues", stack(fused=True))
-    _part(out, "block_stack_joint_qkv", stack(joint_qkv=True))
-    _part(out, "block_stack_fused_joint_cached", stack(cached_kv=True, fused=True, joint_qkv=True))
     def attn_candidates():
         """{"shapes": [tag], "us": {"default" | "nw2" | "nw4": [us per shape]}}: the fp16 attention
         kernel's 2- and 4-wave workgroups (MI_ATTN_NW) on every attention shape of the step."""
@@ -378,9 +385,16 @@ def extras(rng, hip, ops, stream, reps):
                 "tflops_eager": round(flops / (ms_e / 1e3) / 1e12, 2),
                 "tflops_graph": round(flops / (ms_g / 1e3) / 1e12, 2), "steps": steps}
 
-    _part(out, "gemm_candidates", candidates)
-    _part(out, "attention_candidates", attn_candidates)
-    _part(out, "step_graph", step_graph)
+    # the tile-rule data first: it is what the next kernel decisions need
+    part("config0_gemm", cfg0)
+    part("gemm_candidates", candidates)
+    part("attention_candidates", attn_candidates)
+    part("nn_gemm", nn)
+    part("block_stack_cached_kv", stack(cached_kv=True))
+    part("block_stack_fused_epilogues", stack(fused=True))
+    part("block_stack_joint_qkv", stack(joint_qkv=True))
+    part("block_stack_fused_joint_cached", stack(cached_kv=True, fused=True, joint_qkv=True))
+    part("step_graph", step_graph)
     return out
 
 
@@ -390,7 +404,8 @@ def extras_child_main(reps: int) -> int:
     _lib.load()
     rng = np.random.default_rng(2)
     stream = hip.Stream()
-    print(json.dumps(extras(rng, hip, ops, stream, reps)), flush=True)
+    emit = lambda out: print(json.dumps(out), flush=True)  # noqa: E731
+    emit(extras(rng, hip, ops, stream, reps, emit=emit))
     return 0
 
 
@@ -401,12 +416,24 @@ def run_extras_child(reps: int, timeout_s: int = 420) -> dict:
     cmd = [sys.executable, str(Path(__file__).resolve()), "--extras-child", "--reps", str(reps)]
     try:
         r = subprocess.run(cmd, stdout=subprocess.PIPE, text=True, timeout=timeout_s, cwd=str(ROOT))
-    except subprocess.TimeoutExpired:
-        return {"error": f"extras child exceeded {timeout_s} s"}
-    lines = [l for l in r.stdout.splitlines() if l.startswith("{")]
-    if r.returncode != 0 or not lines:
-        return {"error": f"extras child exited with status {r.returncode}"}
-    return json.loads(lines[-1])
+        stdout, error = r.stdout, None if r.returncode == 0 else f"extras child exited with status {r.returncode}"
+    except subprocess.TimeoutExpired as e:
+        stdout, error = e.stdout or "", f"extras child exceeded {timeout_s} s"
+    if isinstance(stdout, bytes):
+        stdout = stdout.decode(errors="replace")
+    # the child prints its results so far after every part: keep the last complete line
+    last = None
+    for line in stdout.splitlines():
+        if line.startswith("{"):
+            try:
+                last = json.loads(line)
+            except ValueError:
+                pass
+    if last is None:
+        return {"error": error or "extras child printed no result"}
+    if error:
+        last["error"] = error + " (results measured before it stopped)"
+    return last
 
 
 def roofline_pct(c, seconds):

@@ -157,6 +157,43 @@ def test_bench_line_on_stand_in_device(fake_device, monkeypatch, capsys):
         assert name in fake_device, name
 
 
+def test_extras_emit_partial_results(fake_device):
+    """Every emitted line is a growing prefix of the final extras (so a child
+    stopped early leaves what it measured), one line per GEMM candidate build."""
+    import bench
+    from sdvk_amd import hip, ops
+
+    seen = []
+    final = bench.extras(np.random.default_rng(2), hip, ops, hip.Stream(), 2, emit=lambda o: seen.append(json.dumps(o)))
+    emitted = [json.loads(x) for x in seen]
+    assert len(emitted) >= len(bench.GEMM_CANDIDATES) + 9
+    for a, b in zip(emitted, emitted[1:]):
+        assert set(a) <= set(b)
+    assert emitted[-1] == json.loads(json.dumps(final))
+    cand = [e["gemm_candidates"] for e in emitted if "gemm_candidates" in e]
+    assert [len(c["us"]) for c in cand[:3]] == [1, 2, 3]
+
+
+@pytest.mark.parametrize("how", ["timeout", "crash", "ok"])
+def test_extras_child_keeps_the_last_complete_line(monkeypatch, how):
+    import subprocess
+
+    import bench
+
+    partial = '{"config0_gemm": {"us": 1.0}}\n{"config0_gemm": {"us": 1.0}, "nn_gemm": []}\n{"trunc'
+
+    def fake_run(cmd, **kw):
+        assert "--extras-child" in cmd
+        if how == "timeout":
+            raise subprocess.TimeoutExpired(cmd, kw["timeout"], output=partial.encode())
+        return subprocess.CompletedProcess(cmd, 0 if how == "ok" else -11, stdout=partial)
+
+    monkeypatch.setattr(subprocess, "run", fake_run)
+    r = bench.run_extras_child(2, timeout_s=5)
+    assert r["nn_gemm"] == [] and r["config0_gemm"] == {"us": 1.0}
+    assert ("error" in r) == (how != "ok")
+
+
 def test_joint_qkv_weights_are_back_to_back(fake_device):
     import bench
     from sdvk_amd import hip, ops
