@@ -500,8 +500,8 @@ def main() -> int:
     if args.extras_child:
         return extras_child_main(args.reps)
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (multi-GPU sharding is "
-                                   "design-only, see DESIGN.md)"}))
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (sharding the GEMM by N or "
+                                   "M and attention by batch / head is designed, not built)"}))
         return 2
 
     from sdvk_amd import _lib, hip, ops
