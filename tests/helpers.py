@@ -43,3 +43,14 @@ def q8_weights(oracle, seed: int, N: int, K: int, std: float = 0.02) -> np.ndarr
 def split_from_blocks(oracle, blocks: np.ndarray, n: int):
     payload, scales = oracle.q8_0_to_split(blocks, n)
     return payload, scales
+
+
+def residual_split_ulps(C: int, F: int) -> float:
+    """Bound, in ulp of max|x|, on fused vs separate residual epilogues of one
+    block: each of the three residual GEMMs (two out-projections with K = C,
+    FF-down with K = F) adds at most one partial per 64-wide K step into x
+    with atomics, each rounding by at most half an ulp of |x|, where the
+    separate path rounds once; 2 ulp more for the changed LayerNorm inputs
+    downstream."""
+    steps = lambda k: -(-k // 64)  # noqa: E731
+    return 0.5 * (2 * (steps(C) + 1) + steps(F) + 1) + 2.0
