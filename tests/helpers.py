@@ -54,3 +54,12 @@ def residual_split_ulps(C: int, F: int) -> float:
     downstream."""
     steps = lambda k: -(-k // 64)  # noqa: E731
     return 0.5 * (2 * (steps(C) + 1) + steps(F) + 1) + 2.0
+
+
+def split_order_ulps(blocks: int) -> float:
+    """Bound, in ulp of max|x|, on two runs of the same block path whose K-split
+    GEMMs add their partials with atomics in a different order: a GEMM output
+    then differs in its last bits, which can move each of the block's three
+    residual adds (x + sublayer) by one ulp of |x|, plus at most one more ulp
+    per add from the changed LayerNorm inputs downstream; per block applied."""
+    return 2.0 * 3 * blocks

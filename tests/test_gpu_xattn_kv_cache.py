@@ -6,7 +6,7 @@ context's to_k / to_v projections that crossAttention recomputes on every call
 import numpy as np
 import pytest
 
-from helpers import rms
+from helpers import rms, split_order_ulps
 from sdvk_amd import ops
 from sdvk_amd.hip import DeviceBuffer, synchronize
 from test_gpu_block import BLOCK_TOL, make_weights, run_block, to_device
@@ -19,8 +19,9 @@ pytestmark = pytest.mark.gpu
 def test_block_cached_ctx_kv(gpu, oracle, B, T, C, H, Tc, Cc, F, masked):
     """K / V of the context projected once (mi_block_ctx_kv) and reused by two
     block applications (mi_sdxl_block_forward_kv) match two uncached calls; the
-    K / V GEMMs add split-K partials with atomics, so the two paths may differ
-    in the last bits of K / V: 1e-5 x RMS of the update."""
+    K-split GEMMs of both runs add their partials with atomics in run-dependent
+    order, so the two may differ by a few ulps of |x| (helpers.split_order_ulps),
+    five orders of magnitude below a wrong K / V (RMS of the update)."""
     print(f"[case] block cached kv B={B} T={T} C={C} Tc={Tc} Cc={Cc}", flush=True)
     w = make_weights(oracle, C, Cc, F, seed=500)
     x = oracle.normal(3, B * T * C)
@@ -38,9 +39,11 @@ def test_block_cached_ctx_kv(gpu, oracle, B, T, C, H, Tc, Cc, F, masked):
         ops.sdxl_block_forward_kv(bw, dims, dx, kv, ws, ctx_len=dl)
     synchronize()
     got = dx.download(np.float32, x.size)
-    e = np.max(np.abs(got - fresh)) / rms(fresh - x)
-    print(f"  cached vs fresh err/rms = {e:.3e}", flush=True)
-    assert np.all(np.isfinite(got)) and e <= 1e-5
+    diff = float(np.max(np.abs(got - fresh)))
+    ulp = float(np.spacing(np.float32(np.max(np.abs(fresh)))))
+    print(f"  cached vs fresh: {diff / ulp:.1f} ulp of max|x| ({diff / rms(fresh - x):.3e} x RMS(update))",
+          flush=True)
+    assert np.all(np.isfinite(got)) and diff <= split_order_ulps(2) * ulp
     once = oracle.sdxl_block(w, x, ctx, batch=B, tokens=T, channels=C, heads=H, ctx_tokens=Tc, ctx_channels=Cc,
                              ff_inner=F, ctx_len=kl, threads=oracle.max_threads())
     want = oracle.sdxl_block(w, once, ctx, batch=B, tokens=T, channels=C, heads=H, ctx_tokens=Tc, ctx_channels=Cc,
