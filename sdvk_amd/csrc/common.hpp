@@ -86,6 +86,13 @@ __device__ __forceinline__ void interleave_step() {
 // Remaps a linear workgroup id so that consecutive logical tiles land on the
 // same XCD. The dispatcher hands workgroup b to XCD b % 8; tiles that share an
 // operand should share that XCD's L2.
+// Lane index within the wave from the exec-mask bit counts (v_mbcnt), not from
+// threadIdx.x: a kernel that needs the lane again after a long loop computes it
+// there instead of keeping threadIdx-derived values live across the loop.
+__device__ __forceinline__ int lane_id() {
+    return static_cast<int>(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)));
+}
+
 __device__ __forceinline__ unsigned xcd_swizzle(unsigned b, unsigned nb) {
     constexpr unsigned kXcd = 8;
     unsigned xcd = b % kXcd, local = b / kXcd;

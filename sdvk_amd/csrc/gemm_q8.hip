@@ -312,6 +312,14 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     const int lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, g = lane >> 5;
     const int wm = wave % WM, wn = wave / WM;
+    // 8-wave builds: the epilogue takes the wave index from this SGPR copy and
+    // the lane from v_mbcnt, so fewer threadIdx-derived VGPRs stay live across
+    // the K loop (the 256x256 build, at its 256-register limit, spilled six of
+    // them around the loop; three with this). The 4-wave builds keep the
+    // prologue's values: with the same change the register allocator moved a
+    // spill of the 4-wave 256x256 build into its K loop.
+    constexpr bool kFreshLane = NT == 512;
+    const int wave_s = kFreshLane ? __builtin_amdgcn_readfirstlane(wave) : wave;
 
     // Tile order: each XCD takes a contiguous chunk of a grouped order (groups
     // of group_m row panels, column-major inside a group), so the chunk is a
@@ -623,8 +631,10 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
 
     float* C = a.C + static_cast<uint64_t>(blockIdx.z) * a.sC;
     __syncthreads();  // every wave is done with the operand tiles before LDS is reused
-    store_tiles<FM, FN, SPLITK, EPI>(a, C, reinterpret_cast<float*>(smem) + wave * kStageFloats, m0 + wm * TM,
-                                     EPI == kEpiGeglu ? n0 + wn * TN / 2 : n0 + wn * TN, acc, lane);
+    const int wm_s = kFreshLane ? wave_s % WM : wm, wn_s = kFreshLane ? wave_s / WM : wn;
+    store_tiles<FM, FN, SPLITK, EPI>(a, C, reinterpret_cast<float*>(smem) + wave_s * kStageFloats, m0 + wm_s * TM,
+                                     EPI == kEpiGeglu ? n0 + wn_s * TN / 2 : n0 + wn_s * TN, acc,
+                                     kFreshLane ? lane_id() : lane);
 }
 
 // ---- row-stationary kernel --------------------------------------------------------

@@ -93,3 +93,42 @@ def loops(asm_path: Path) -> list[Loop]:
             found.append(Loop(m.group(1), label, len(ins), nm, sum(_is_load(x) for x in ins),
                               sum("scratch_" in x for x in ins), dist))
     return found
+
+
+@dataclass
+class Resources:
+    kernel: str          # mangled name
+    vgpr: int            # arch VGPRs
+    agpr: int            # accumulation VGPRs
+    sgpr: int
+    lds: int             # static LDS bytes per workgroup
+    scratch: int         # private segment bytes per work-item
+    vgpr_spills: int
+    sgpr_spills: int
+    max_threads: int     # launch bound (work-items per workgroup)
+
+    @property
+    def waves_per_simd(self) -> int:
+        """Waves of this kernel one SIMD can hold by registers: 512 unified
+        registers per lane, allocated in granules of 8 (the metadata's
+        vgpr_count already includes the AGPRs)."""
+        used = max(8, -(-self.vgpr // 8) * 8)
+        return min(8, 512 // used)
+
+
+def resources(asm_path: Path) -> list[Resources]:
+    """Register, LDS and scratch use of every kernel, from the code object's
+    metadata (the amdhsa.kernels list of .amdgpu_metadata)."""
+    import yaml
+
+    text = asm_path.read_text()
+    meta = text.split("\n\t.amdgpu_metadata", 1)[1].split("\n\t.end_amdgpu_metadata", 1)[0]
+    doc = yaml.safe_load(meta.split("---", 1)[1].split("\n...", 1)[0])
+    out = []
+    for k in doc["amdhsa.kernels"]:
+        out.append(Resources(kernel=k[".name"], vgpr=k[".vgpr_count"], agpr=k.get(".agpr_count", 0),
+                             sgpr=k[".sgpr_count"], lds=k[".group_segment_fixed_size"],
+                             scratch=k[".private_segment_fixed_size"], vgpr_spills=k.get(".vgpr_spill_count", 0),
+                             sgpr_spills=k.get(".sgpr_spill_count", 0),
+                             max_threads=k.get(".max_flat_workgroup_size", 1024)))
+    return out

@@ -372,6 +372,19 @@ inline int vote_any(int pred) {
     return r;
 }
 
+// v_mbcnt_lo / _hi: base + the set bits of mask that belong to lanes below
+// this one, in lanes 0-31 (lo) or 32-63 (hi)
+inline unsigned mbcnt_lo(unsigned mask, unsigned base) {
+    const int l = lane_id();
+    const unsigned below = l >= 32 ? mask : mask & ((1u << l) - 1u);
+    return base + static_cast<unsigned>(__builtin_popcount(below));
+}
+inline unsigned mbcnt_hi(unsigned mask, unsigned base) {
+    const int l = lane_id() - 32;
+    const unsigned below = l <= 0 ? 0u : mask & ((1u << l) - 1u);
+    return base + static_cast<unsigned>(__builtin_popcount(below));
+}
+
 inline void nop_fn(const unsigned char (*)[256], unsigned char (*)[256], const void*) {}
 inline void wave_barrier() { wave_op("wave_barrier", nullptr, 0, nullptr, 0, nop_fn, nullptr); }
 
@@ -402,6 +415,8 @@ inline T __shfl_xor(T v, int mask, int width = 64) {
 #define __builtin_amdgcn_mfma_f32_32x32x16_f16 ::kemu::mfma_32x32x16_f16
 #define __builtin_amdgcn_mov_dpp ::kemu::mov_dpp
 #define __builtin_amdgcn_readfirstlane ::kemu::readfirstlane
+#define __builtin_amdgcn_mbcnt_lo ::kemu::mbcnt_lo
+#define __builtin_amdgcn_mbcnt_hi ::kemu::mbcnt_hi
 #define __builtin_amdgcn_wave_barrier ::kemu::wave_barrier
 #define __builtin_amdgcn_perm ::kemu::perm
 #define __builtin_amdgcn_alignbit ::kemu::alignbit

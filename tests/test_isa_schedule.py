@@ -8,6 +8,9 @@ For every loop that issues MFMAs in the GEMM and attention kernels:
     step: the loops run two steps per trip) issued between it and the wait
     that retires it. A load under a branch, or a consumer hoisted next to its
     load, drops this to 0-2 and the wave then sits out the memory latency.
+And for every kernel of those sources (test_register_budgets): the 8-wave
+builds fit two waves per SIMD, LDS fits the CU, and scratch is used only by
+the listed build, within its budget.
 Excluded: the attention kernel's scalar-load build (head dims that are not a
 multiple of 8, or unaligned tensors; no SDXL shape takes it) and the NN GEMM's
 untiled kernel (the general path for unaligned shapes; not pipelined).
@@ -39,7 +42,9 @@ def asm(tmp_path_factory):
     if shutil.which(b.hipcc()) is None:
         pytest.skip("no hipcc for the gfx950 assembly")
     d = tmp_path_factory.mktemp("isa")
-    return {src: isa_sched.loops(isa_sched.compile_asm(src, d / (src + ".s"))) for src in CASES}
+    paths = {src: isa_sched.compile_asm(src, d / (src + ".s")) for src in CASES}
+    return {src: isa_sched.loops(path) for src, path in paths.items()} | {
+        ("resources", src): isa_sched.resources(path) for src, path in paths.items()}
 
 
 @pytest.mark.parametrize("src", list(CASES))
@@ -55,4 +60,29 @@ def test_k_loops_keep_loads_ahead_of_their_waits(asm, src):
             bad.append(f"{l.kernel} {l.label}: a load is waited for {l.min_distance} MFMAs after issue "
                        f"(loop of {l.mfma} MFMAs; want >= {need})")
     print(f"{src}: {len(loops)} loops checked")
+    assert not bad, "\n".join(bad)
+
+
+# Kernels that may keep values in scratch around (never inside) their K loop,
+# and how many bytes per lane: the 8-wave 256x256 LDS build at its 256-register
+# limit (epilogue indices across the loop).
+SCRATCH_ALLOWED = {"gemm_q8_kernelILi256ELi256ELi4ELi2E": 16}
+
+
+@pytest.mark.parametrize("src", list(CASES))
+def test_register_budgets(asm, src):
+    """Every 8-wave (512-thread) build fits two waves per SIMD, every kernel's
+    LDS fits the CU, and scratch appears only where listed, within its budget."""
+    res = asm[("resources", src)]
+    assert res, f"no kernels in {src}"
+    bad = []
+    for r in res:
+        allowed = max([v for k, v in SCRATCH_ALLOWED.items() if k in r.kernel], default=0)
+        if r.scratch > allowed:
+            bad.append(f"{r.kernel}: {r.scratch} B of scratch per lane (allowed {allowed})")
+        if r.lds > 160 * 1024:
+            bad.append(f"{r.kernel}: {r.lds} B of LDS")
+        if r.max_threads == 512 and r.waves_per_simd < 2:
+            bad.append(f"{r.kernel}: {r.vgpr} registers, under two waves per SIMD")
+    print(f"{src}: {len(res)} kernels checked")
     assert not bad, "\n".join(bad)

@@ -219,6 +219,9 @@ PLANTED = {
     "attn_dma_wait": ("attention.hip", "            dma_wait();\n            __syncthreads();\n        };",
                       "            __syncthreads();\n        };",
                       dict(case="attention", batch=2, Tq=130, Tk=200, C=128, heads=2, f16_in=True, f16_out=True)),
+    # the lane index the 8-wave GEMM epilogue takes from v_mbcnt, off by one
+    "lane_id": ("common.hpp", "__builtin_amdgcn_mbcnt_lo(~0u, 0u)", "__builtin_amdgcn_mbcnt_lo(~0u, 1u)",
+                dict(case="gemm_nt", M=300, N=300, K=256, cfg="0")),
     # GGUF upload refills a staging buffer without waiting for its last copy
     "staging_reuse": ("gguf.cpp",
                       "    if (g->stage_used[i] && hipEventSynchronize(g->done[i]) != hipSuccess)\n"
