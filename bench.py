@@ -436,6 +436,26 @@ def run_extras_child(reps: int, timeout_s: int = 420) -> dict:
     return last
 
 
+def profiled_traffic(family: str):
+    """(traffic, note): HBM bytes per launch of the family from its committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary when that summary was measured on
+    these kernel sources (same sources_sha256), else None, with a note that
+    names the file and the figure it holds."""
+    from sdvk_amd.profiling import sources_digest
+
+    tfile = ROOT / "profiles" / f"traffic_{family}_sdxl1024.json"
+    if not tfile.exists():
+        return None, None
+    try:
+        prof = json.loads(tfile.read_text())
+    except ValueError:
+        return None, {"file": str(tfile.relative_to(ROOT)), "note": "unreadable"}
+    note = {"file": str(tfile.relative_to(ROOT)), "bytes_per_launch": prof.get("bytes_per_launch")}
+    if prof.get("sources_sha256") == sources_digest(ROOT):
+        return prof.get("bytes_per_launch"), dict(note, build="these kernel sources")
+    return None, dict(note, build="an earlier build of the kernels (not used as traffic)")
+
+
 def roofline_pct(c, seconds):
     ai = c.flops / c.bytes
     roof = min(PEAK_FP16_TFLOPS, ai * PEAK_HBM_GBS / 1e3)
@@ -594,15 +614,10 @@ def main() -> int:
     dom = max(fam_time, key=fam_time.get)
     avg_launch = fam_time[dom] / fam_launch[dom]
     achieved = fam_flops[dom] / fam_launch[dom] / avg_launch / 1e12
-    traffic = None
-    tfile = ROOT / "profiles" / f"traffic_{dom}_sdxl1024.json"
-    if tfile.exists():
-        try:
-            traffic = json.loads(tfile.read_text()).get("bytes_per_launch")
-        except Exception:
-            traffic = None
+    traffic, traffic_profile = profiled_traffic(dom)
     roofline = {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4), "traffic": traffic,
+                "traffic_profile": traffic_profile,
                 "avg_launch_us": round(avg_launch * 1e6, 2),
                 "algorithmic_flop_per_launch": fam_flops[dom] / fam_launch[dom],
                 "algorithmic_bytes_per_launch": fam_bytes[dom] / fam_launch[dom]}

@@ -108,9 +108,23 @@ def _per_dispatch(csv_path: str, counter: str):
     return out
 
 
+def sources_digest(root: Path | None = None) -> str:
+    """sha256 over the kernel sources and the C-ABI header (names and contents):
+    identifies the build a counter profile was measured on."""
+    import hashlib
+
+    root = Path(root) if root else Path(__file__).resolve().parents[1]
+    h = hashlib.sha256()
+    files = sorted((root / "sdvk_amd" / "csrc").glob("*")) + sorted((root / "include").glob("*.h"))
+    for f in files:
+        if f.suffix in (".hip", ".hpp", ".cpp", ".h"):
+            h.update(f.name.encode() + b"\0" + f.read_bytes() + b"\0")
+    return h.hexdigest()
+
+
 def traffic_report(fetch_csv: str, write_csv: str, copy_mib: int, family: str, command: str) -> dict:
     nbytes = copy_mib << 20
-    result = {"family": family, "copy_probe_bytes": nbytes, "command": command}
+    result = {"family": family, "copy_probe_bytes": nbytes, "command": command, "sources_sha256": sources_digest()}
     per_shape = collections.OrderedDict()
     for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
         rows = _per_dispatch(path, counter)

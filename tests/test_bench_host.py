@@ -194,6 +194,28 @@ def test_extras_child_keeps_the_last_complete_line(monkeypatch, how):
     assert ("error" in r) == (how != "ok")
 
 
+def test_traffic_only_from_a_profile_of_these_sources(tmp_path, monkeypatch):
+    """roofline.traffic comes from the committed counter profile only when that
+    profile was measured on the current kernel sources."""
+    import bench
+    from sdvk_amd.profiling import sources_digest
+
+    (tmp_path / "profiles").mkdir()
+    monkeypatch.setattr(bench, "ROOT", tmp_path)
+    assert bench.profiled_traffic("gemm_q8") == (None, None)
+    f = tmp_path / "profiles" / "traffic_gemm_q8_sdxl1024.json"
+    f.write_text(json.dumps({"bytes_per_launch": 123, "sources_sha256": "0" * 64}))
+    t, note = bench.profiled_traffic("gemm_q8")
+    assert t is None and note["bytes_per_launch"] == 123 and "earlier" in note["build"]
+    for d in ("sdvk_amd/csrc", "include"):
+        (tmp_path / d).mkdir(parents=True)
+    (tmp_path / "sdvk_amd/csrc/k.hip").write_text("kernel")
+    f.write_text(json.dumps({"bytes_per_launch": 123, "sources_sha256": sources_digest(tmp_path)}))
+    assert bench.profiled_traffic("gemm_q8")[0] == 123
+    (tmp_path / "sdvk_amd/csrc/k.hip").write_text("kernel, changed")
+    assert bench.profiled_traffic("gemm_q8")[0] is None
+
+
 def test_joint_qkv_weights_are_back_to_back(fake_device):
     import bench
     from sdvk_amd import hip, ops

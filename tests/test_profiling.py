@@ -74,3 +74,4 @@ def test_traffic_report_scales_by_the_copy_probe(tmp_path):
     assert k["dispatches"] == 2
     assert k["fetch_bytes"] == round(2000 * 1024 * 2.0) and k["write_bytes"] == round(100 * 1024)
     assert r["bytes_per_launch"] == round(2000 * 1024 * 2.0 + 100 * 1024)
+    assert r["sources_sha256"] == p.sources_digest()  # the build the counters were read on
