@@ -442,6 +442,42 @@ def block(E, *, B, T, C, H, Tc, Cc, F, masked=False, blocks=2, order=0, front=Fa
     return e
 
 
+def routing(E, *, table, order=0):
+    """Host routing (tile / split choice, attention workgroup size): each
+    entry [op, dims, grid, threads] is launched with no workgroup emulated and
+    its main launch must have that grid and block size."""
+    E.order(order)
+    for var in ("MI_GEMM_CFG", "MI_NN_KERNEL", "MI_ATTN_NW"):
+        os.environ.pop(var, None)
+    E.sample("*|-|-|-")
+    bad = []
+    for op, dims, grid, threads in table:
+        if op == "gemm":
+            M, N, K = dims
+            A, W, C = E.buf(nbytes=M * K * 4), E.buf(nbytes=N * K // 32 * 34), E.buf(nbytes=M * N * 4)
+            E.call("mi_gemm_nt_q8_0", A.ptr, W.ptr, None, C.ptr, M, N, K, 0, 0, 0, 1, 0, 0, None)
+        elif op == "nn":
+            M, N, K = dims
+            P, S, B, C = E.buf(nbytes=M * K), E.buf(nbytes=M * K // 32 * 4), E.buf(nbytes=K * N * 4), \
+                E.buf(nbytes=M * N * 4)
+            E.call("mi_gemm_nn_q8_split", P.ptr, S.ptr, B.ptr, C.ptr, M, N, K, 0, 0, 0, 0, 1, 0, 0, 0, None)
+        else:
+            b, h, tq, tk = dims
+            C = 64 * h
+            q, k, v = E.buf(nbytes=b * tq * C * 2), E.buf(nbytes=b * tk * C * 2), E.buf(nbytes=b * tk * C * 2)
+            o = E.buf(nbytes=b * tq * C * 2)
+            x = MiAttnArgs(q=q.ptr, k=k.ptr, v=v.ptr, out=o.ptr, batch=b, Tq=tq, Tk=tk, C=C, heads=h, causal=0,
+                           in_dtype=MI_F16, out_dtype=MI_F16, kv_len=None)
+            E.call("mi_fused_attention_ex", ctypes.byref(x), None)
+        kern, g = E.last_launch()
+        got = [list(g), E.last_block_threads()]
+        if got != [list(grid), threads]:
+            bad.append(f"{op} {dims}: {kern} grid {got[0]} x {got[1]} threads, expected {list(grid)} x {threads}")
+    E.sample("")
+    assert not bad, "\n".join(bad)
+    return 0.0
+
+
 def block_full(E, *, fused=False, qkv_joint=False, cached=False, order=0):
     """The config-4 block (level 2: 2 x 1024 tokens, C 1280, 20 heads, context
     2 x 77 x 2048, FF 1280 -> 2 x 5120 -> 1280) at full size with the first and
@@ -604,7 +640,7 @@ def gguf_upload(E, *, big_rows=10240, big_cols=1280, order=0, front=False):
 
 CASES = {"gemm_nt": gemm_nt, "gemm_geglu": gemm_geglu, "gemm_nn": gemm_nn, "attention": attention, "block": block,
          "gguf_upload": gguf_upload, "q8": q8, "glue": glue, "gemm_full": gemm_full, "gemm_nn_full": gemm_nn_full,
-         "attention_full": attention_full, "block_full": block_full}
+         "attention_full": attention_full, "block_full": block_full, "routing": routing}
 
 
 def main(argv):

@@ -83,9 +83,14 @@ class Emu:
 
     def last_launch(self) -> tuple[str, tuple[int, int, int]]:
         """(kernel text, grid) of the most recent launch."""
-        g = (ctypes.c_uint32 * 3)()
+        g = (ctypes.c_uint32 * 4)()
         self.lib.kemu_last_grid(g)
         return self.lib.kemu_last_kernel().decode(), (g[0], g[1], g[2])
+
+    def last_block_threads(self) -> int:
+        g = (ctypes.c_uint32 * 4)()
+        self.lib.kemu_last_grid(g)
+        return g[3]
 
     def order(self, order: int, reverse_blocks: bool = False) -> None:
         """order bits: 1 lanes reversed, 2 waves reversed, 4 wave-major."""

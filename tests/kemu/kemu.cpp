@@ -383,6 +383,7 @@ extern "C" void kemu_last_grid(uint32_t* xyz) {
     xyz[0] = g_grid_dim.x;
     xyz[1] = g_grid_dim.y;
     xyz[2] = g_grid_dim.z;
+    xyz[3] = g_block_dim.x * g_block_dim.y * g_block_dim.z;
 }
 
 // spec: rules separated by ';', each "kernel|x|y|z" (kernel "*": any) where a dimension is '*'

@@ -190,6 +190,34 @@ def test_kernels_on_emulator(emulator, family):
     assert not failed, "\n\n".join(failed)
 
 
+# The tile rules at the SDXL shapes of the benchmark: (op, dims, grid, work-items
+# per workgroup). GEMM (choose in gemm_q8.hip): 256x256 with 8 waves when it gives
+# >= 160 tiles, M >= 4096 and K <= 2048; 128x128 (4 waves) when that gives
+# >= 1024 tiles and K <= 2048; 256x128 (8 waves) for >= 128 tiles; K >= 4096
+# with >= 64 such tiles: 256x128 with two K splits; 64x64 (4 waves) for >= 512
+# tiles; else 64x64 with K split to about 256 workgroups (powers of two, >= 128 k
+# per split). Grid = (tiles, splits, batch). NN GEMM: 128x256 tiles (8 waves),
+# grid (N tiles, M tiles, splits), K splits doubled while tiles x splits < 256
+# and each split keeps >= 4 steps of 64. fp16 attention: 4-wave workgroups of
+# 128 queries when that gives >= 512 workgroups, else 2-wave ones of 64.
+ROUTING = [
+    ["gemm", [8192, 640, 640], [160, 1, 1], 512], ["gemm", [8192, 5120, 640], [640, 1, 1], 512],
+    ["gemm", [8192, 640, 2560], [160, 1, 1], 512], ["gemm", [2048, 1280, 1280], [640, 1, 1], 256],
+    ["gemm", [2048, 10240, 1280], [1280, 1, 1], 256], ["gemm", [2048, 1280, 5120], [80, 2, 1], 512],
+    ["gemm", [154, 640, 2048], [30, 8, 1], 256], ["gemm", [154, 1280, 2048], [60, 4, 1], 256],
+    ["gemm", [9216, 1280, 1280], [180, 1, 1], 512],
+    ["nn", [320, 4096, 2880], [16, 3, 8], 512], ["nn", [640, 4096, 5760], [16, 5, 4], 512],
+    ["nn", [1280, 1024, 11520], [4, 10, 8], 512], ["nn", [1280, 1024, 640], [4, 10, 2], 512],
+    ["attn", [2, 10, 4096, 4096], [640, 1, 1], 256], ["attn", [2, 20, 1024, 1024], [640, 1, 1], 128],
+    ["attn", [2, 10, 4096, 77], [640, 1, 1], 256], ["attn", [2, 20, 1024, 77], [640, 1, 1], 128],
+]
+
+
+def test_routing_at_sdxl_shapes(emulator):
+    r = _run({"case": "routing", "table": ROUTING})
+    assert r.returncode == 0 and "OK routing" in r.stdout, (r.stdout + r.stderr)[-3000:]
+
+
 # One planted mistake per copy of the sources: (file, text, replacement, case).
 PLANTED = {
     # DPP quad permute of the wrong pattern in the row-coalesced A transpose
