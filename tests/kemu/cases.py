@@ -52,8 +52,9 @@ def _logical_mask(M, N, ldc, batch, sC, size):
 
 
 def gemm_nt(E, *, M, N, K, layout="q8_0", cfg=None, mode=0, bias=True, batch=1, lda=0, ldc=0, sA=0, sC=0,
-            seed=1, front=False, order=0, tol=2e-3):
-    """mi_gemm_nt_q8_0 / mi_gemm_nt_q8_split against the oracle."""
+            seed=1, front=False, order=0, tol=2e-3, bias_off=0):
+    """mi_gemm_nt_q8_0 / mi_gemm_nt_q8_split against the oracle; bias_off
+    shifts the bias pointer by that many floats (an unaligned bias)."""
     _set_cfg(cfg)
     E.order(order)
     lda_e, ldc_e = lda or K, ldc or N
@@ -64,7 +65,9 @@ def gemm_nt(E, *, M, N, K, layout="q8_0", cfg=None, mode=0, bias=True, batch=1, 
     b = ob.normal(seed + 2, N, 0.0, 0.02) if bias else None
     C0 = ob.normal(seed + 3, c_el) if mode in (1, 2) else np.full(c_el, SENTINEL, dtype=np.float32)
     dA, dC = E.buf(A, front=front), E.buf(C0, front=front)
-    dB = E.buf(b, front=front) if bias else None
+    dB = E.buf(np.concatenate([np.zeros(bias_off, np.float32), b]), front=front) if bias else None
+    if dB is not None and bias_off:
+        dB.ptr += 4 * bias_off
     # mode 2 (C += acc + bias) = C0 + the mode-0 product with bias
     omode, oC = (0, np.zeros_like(C0)) if mode == 2 else (mode, C0.copy())
     if layout == "q8_0":
@@ -260,7 +263,7 @@ def gemm_full(E, *, M, N, K, cfg=None, layout="q8_0", seed=1, order=0, tol=2e-3)
         dP, dS = E.buf(payload), E.buf(scales)
         call = lambda: E.call("mi_gemm_nt_q8_split", dA.ptr, dP.ptr, dS.ptr, None, dC.ptr, M, N, K, 0, 0, 0, 1, 0, 0,
                               None)
-    helpers = "gemm_init_kernel|-|-|-;gemm_bias_add_kernel|-|-|-"
+    helpers = "gemm_init|-|-|-;gemm_bias_add_kernel|-|-|-"  # both fill kernels
     kern, grid = _probe_grid(E, f"gemm_q8_kernel|-|-|-;gemm_q8_rows_kernel|-|-|-;{helpers}", call)
     assert not np.any(dC.get(np.float32, M * N)), "a launch with no workgroup wrote C"
     xs = sorted({0, _block_of_tile(grid[0] - 1, grid[0])})

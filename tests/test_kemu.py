@@ -50,6 +50,8 @@ FAMILIES = {
         dict(M=130, N=257, K=320), dict(M=130, N=257, K=320, mode=1), dict(M=154, N=96, K=2048),
         dict(M=60, N=40, K=100, layout="split"), dict(M=77, N=96, K=64, layout="split", mode=1),
         dict(M=300, N=300, K=256, cfg="0"), dict(M=300, N=200, K=256, cfg="1", layout="split"),
+        # K splits: the 16-byte fill of C with an unaligned bias, and the scalar fill (N % 4 != 0)
+        dict(M=154, N=96, K=2048, bias_off=1), dict(M=154, N=98, K=2048, mode=0),
         dict(M=130, N=100, K=128, cfg="2"), dict(M=70, N=70, K=128, cfg="3", front=True),
         dict(M=300, N=300, K=256, cfg="4"), dict(M=200, N=300, K=512, cfg="0:3"),
         dict(M=70, N=36, K=64, batch=3, lda=72, ldc=40, sA=5200, sC=3000),
