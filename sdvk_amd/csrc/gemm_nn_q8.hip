@@ -157,6 +157,29 @@ __global__ __launch_bounds__(256) void gemm_nn_zero_kernel(float* C, uint32_t M,
     for (uint32_t m = blockIdx.y; m < M; m += gridDim.y) c[static_cast<uint64_t>(m) * ldc] = 0.0f;
 }
 
+// The same clear with one 16-byte store per work-item step over the flattened
+// [M, N / 4] index of each batch item (blockIdx.y), for 16-byte aligned rows.
+__global__ __launch_bounds__(256) void gemm_nn_zero_vec_kernel(float* C, uint32_t M, uint32_t N4, uint32_t ldc,
+                                                               uint32_t sC) {
+    float* c = C + static_cast<uint64_t>(blockIdx.y) * sC;
+    const uint64_t total = static_cast<uint64_t>(M) * N4;
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * 256;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x; i < total; i += stride) {
+        const uint32_t m = static_cast<uint32_t>(i / N4), n = static_cast<uint32_t>(i % N4) * 4;
+        *reinterpret_cast<floatx4*>(c + static_cast<uint64_t>(m) * ldc + n) = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+}
+
+void launch_zero(float* C, uint32_t M, uint32_t N, uint32_t ldc, uint32_t sC, uint32_t batch, hipStream_t st) {
+    if (reinterpret_cast<uintptr_t>(C) % 16 == 0 && N % 4 == 0 && ldc % 4 == 0 && sC % 4 == 0) {
+        const uint64_t n4 = static_cast<uint64_t>(M) * (N / 4);
+        const unsigned gx = static_cast<unsigned>(std::min<uint64_t>(std::max<uint64_t>(ceil_div(n4, 256ull), 1), 1024));
+        gemm_nn_zero_vec_kernel<<<dim3(gx, batch), 256, 0, st>>>(C, M, N / 4, ldc, sC);
+        return;
+    }
+    gemm_nn_zero_kernel<<<dim3(ceil_div(N, 256), std::min<uint32_t>(M, 4096), batch), 256, 0, st>>>(C, M, N, ldc, sC);
+}
+
 template <bool SPLITK>
 __global__ __launch_bounds__(kNT2) void gemm_nn_q8_tiled_kernel(NnArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 smem[2 * (kBM2 + kBN2) * kLd2];
@@ -390,8 +413,7 @@ extern "C" int mi_gemm_nn_q8_split(const uint32_t* payload, const float* scales,
     a.splits = splits;
     if (splits > 1) {
         if (mode == 0)
-            gemm_nn_zero_kernel<<<dim3(ceil_div(N, 256), std::min<uint32_t>(M, 4096), batch), 256, 0, st>>>(C, M, N, ldc,
-                                                                                                         a.sC);
+            launch_zero(C, M, N, ldc, a.sC, batch, st);
         gemm_nn_q8_tiled_kernel<true><<<dim3(ceil_div(N, kBN2), ceil_div(M, kBM2), batch * splits), kNT2, 0, st>>>(a);
     } else {
         a.steps_per_split = ksteps;

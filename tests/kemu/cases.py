@@ -298,10 +298,10 @@ def gemm_nn_full(E, *, M, N, K, seed=1, order=0, tol=2e-3):
     dP, dS, dB, dC = E.buf(payload), E.buf(scales), E.buf(B), E.buf(np.zeros(M * N, np.float32))
     call = lambda: E.call("mi_gemm_nn_q8_split", dP.ptr, dS.ptr, dB.ptr, dC.ptr, M, N, K, 0, 0, 0, 0, 1, 0, 0, 0,
                           None)
-    kern, grid = _probe_grid(E, "gemm_nn_q8_tiled_kernel|-|-|-;gemm_nn_q8_kernel|-|-|-;gemm_nn_zero_kernel|-|-|-",
+    kern, grid = _probe_grid(E, "gemm_nn_q8_tiled_kernel|-|-|-;gemm_nn_q8_kernel|-|-|-;gemm_nn_zero|-|-|-",
                              call)
     print(f"  {kern} grid {grid}", flush=True)
-    E.sample("gemm_nn_q8_tiled_kernel|0,-1|-1|*;gemm_nn_q8_kernel|0,-1|-1|*;gemm_nn_zero_kernel|-|-|-")
+    E.sample("gemm_nn_q8_tiled_kernel|0,-1|-1|*;gemm_nn_q8_kernel|0,-1|-1|*;gemm_nn_zero|-|-|-")
     call()
     got = dC.get(np.float32, M * N).reshape(M, N)
     mask = got != 0

@@ -96,6 +96,7 @@ FAMILIES = {
         dict(M=130, N=260, K=128), dict(M=300, N=520, K=640, mode=1), dict(M=64, N=64, K=1024),
         dict(M=70, N=36, K=256, batch=3, lda=272, ldb=40, ldc=44, sA=19056, sB=10248, sC=3100),
         dict(M=129, N=300, K=256, front=True), dict(M=130, N=260, K=128, kernel="general"),
+        dict(M=129, N=300, K=256, ldc=302),  # K splits, ldc % 4 != 0: the per-column clear of C
     ],
     "attention": [
         dict(Tq=100, Tk=300, C=128, heads=2), dict(Tq=100, Tk=300, C=128, heads=2, causal=True),
