@@ -1020,8 +1020,32 @@ __global__ __launch_bounds__(256) void gemm_bias_add_kernel(float* C, const floa
     for (uint32_t m = blockIdx.y; m < M; m += gridDim.y) c[static_cast<uint64_t>(m) * ldc] += v;
 }
 
+// The same add with 16-byte accesses over the flattened [M, N / 4] index (rows
+// 16-byte aligned, N % 4 == 0).
+__global__ __launch_bounds__(256) void gemm_bias_add_vec_kernel(float* C, const float* bias, uint32_t M, uint32_t N4,
+                                                                uint32_t ldc, uint64_t sC, uint32_t bvec) {
+    float* c = C + static_cast<uint64_t>(blockIdx.y) * sC;
+    const uint64_t total = static_cast<uint64_t>(M) * N4;
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * 256;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x; i < total; i += stride) {
+        const uint32_t m = static_cast<uint32_t>(i / N4), n = static_cast<uint32_t>(i % N4) * 4;
+        const floatx4 b = bvec ? *reinterpret_cast<const floatx4*>(bias + n)
+                               : floatx4{bias[n], bias[n + 1], bias[n + 2], bias[n + 3]};
+        floatx4* p = reinterpret_cast<floatx4*>(c + static_cast<uint64_t>(m) * ldc + n);
+        const floatx4 x = *p;
+        *p = floatx4{x[0] + b[0], x[1] + b[1], x[2] + b[2], x[3] + b[3]};
+    }
+}
+
 void launch_bias_add(float* C, const float* bias, uint32_t M, uint32_t N, uint32_t ldc, uint64_t sC, uint32_t batch,
                      hipStream_t s) {
+    if (reinterpret_cast<uintptr_t>(C) % 16 == 0 && N % 4 == 0 && ldc % 4 == 0 && sC % 4 == 0 && batch <= 65535) {
+        const uint64_t n4 = static_cast<uint64_t>(M) * (N / 4);
+        const unsigned gx = static_cast<unsigned>(std::min<uint64_t>(std::max<uint64_t>(ceil_div(n4, 256ull), 1), 1024));
+        gemm_bias_add_vec_kernel<<<dim3(gx, batch), 256, 0, s>>>(C, bias, M, N / 4, ldc, sC,
+                                                                 reinterpret_cast<uintptr_t>(bias) % 16 == 0 ? 1u : 0u);
+        return;
+    }
     gemm_bias_add_kernel<<<dim3(ceil_div(N, 256), std::min<uint32_t>(M, 4096), batch), 256, 0, s>>>(C, bias, M, N,
                                                                                                      ldc, sC);
 }

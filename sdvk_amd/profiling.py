@@ -33,7 +33,7 @@ from pathlib import Path
 # family -> (main kernels: one launch per API call, helper kernels of the same calls)
 FAMILIES = {
     "gemm_q8": (("gemm_q8_kernel", "gemm_q8_rows_kernel"),
-                ("gemm_init_kernel", "gemm_init_vec_kernel", "gemm_bias_add_kernel")),
+                ("gemm_init_kernel", "gemm_init_vec_kernel", "gemm_bias_add_kernel", "gemm_bias_add_vec_kernel")),
     "attention": (("attn_kernel", "attn_f16_kernel"), ()),
     "gemm_nn_q8": (("gemm_nn_q8_kernel", "gemm_nn_q8_tiled_kernel"), ("gemm_nn_zero_kernel", "gemm_nn_zero_vec_kernel")),
 }

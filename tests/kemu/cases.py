@@ -263,7 +263,7 @@ def gemm_full(E, *, M, N, K, cfg=None, layout="q8_0", seed=1, order=0, tol=2e-3)
         dP, dS = E.buf(payload), E.buf(scales)
         call = lambda: E.call("mi_gemm_nt_q8_split", dA.ptr, dP.ptr, dS.ptr, None, dC.ptr, M, N, K, 0, 0, 0, 1, 0, 0,
                               None)
-    helpers = "gemm_init|-|-|-;gemm_bias_add_kernel|-|-|-"  # both fill kernels
+    helpers = "gemm_init|-|-|-;gemm_bias_add|-|-|-"  # the fill and bias-add kernels, both forms
     kern, grid = _probe_grid(E, f"gemm_q8_kernel|-|-|-;gemm_q8_rows_kernel|-|-|-;{helpers}", call)
     assert not np.any(dC.get(np.float32, M * N)), "a launch with no workgroup wrote C"
     xs = sorted({0, _block_of_tile(grid[0] - 1, grid[0])})

@@ -79,6 +79,7 @@ FAMILIES = {
         dict(case="gemm_nt", M=77, N=96, K=64, mode=2), dict(case="gemm_nt", M=130, N=257, K=320, mode=2),
         dict(case="gemm_nt", M=300, N=200, K=256, cfg="7:2", mode=2, layout="split"),
         dict(case="gemm_nt", M=60, N=40, K=100, layout="split", mode=2),
+        dict(case="gemm_nt", M=154, N=96, K=2048, mode=2, bias_off=1),  # K splits: 16-byte bias add, unaligned bias
         dict(case="gemm_geglu", M=77, F=48, K=64), dict(case="gemm_geglu", M=300, F=200, K=256, cfg="4"),
         dict(case="gemm_geglu", M=130, F=100, K=96), dict(case="gemm_geglu", M=300, F=130, K=256, cfg="7", ldg=136),
         dict(case="gemm_geglu", M=260, F=96, K=128, cfg="9", front=True),

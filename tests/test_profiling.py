@@ -14,6 +14,7 @@ GEMM = "_ZN2mi12_GLOBAL__N_114gemm_q8_kernelILi256ELi128ELi4ELi2ELi2ELi0ELb0ELb0
 ROWS = "_ZN2mi12_GLOBAL__N_119gemm_q8_rows_kernelILi8ELi0ELb0ELb1ELi0EEEvNS0_8GemmArgsE"
 INIT = "_ZN2mi12_GLOBAL__N_116gemm_init_kernelEPfPKfjjjm"
 INIT_VEC = "_ZN2mi12_GLOBAL__N_120gemm_init_vec_kernelEPfPKfjjjmj"
+BIAS_VEC = "_ZN2mi12_GLOBAL__N_124gemm_bias_add_vec_kernelEPfPKfjjjmj"
 NN = "_ZN2mi12_GLOBAL__N_123gemm_nn_q8_tiled_kernelILb1EEEvNS0_6NnArgsE"
 NN_ZERO = "_ZN2mi12_GLOBAL__N_119gemm_nn_zero_kernelEPfjjjj"
 NN_ZERO_VEC = "_ZN2mi12_GLOBAL__N_123gemm_nn_zero_vec_kernelEPfjjjj"
@@ -22,7 +23,7 @@ COPY = "__amd_rocclr_copyBuffer"
 
 @pytest.mark.parametrize("name,family,main", [
     (ATTN_F16, "attention", True), (GEMM, "gemm_q8", True), (ROWS, "gemm_q8", True), (INIT, "gemm_q8", False),
-    (INIT_VEC, "gemm_q8", False),
+    (INIT_VEC, "gemm_q8", False), (BIAS_VEC, "gemm_q8", False),
     (NN, "gemm_nn_q8", True), (NN_ZERO, "gemm_nn_q8", False), (NN_ZERO_VEC, "gemm_nn_q8", False),
     (COPY, None, None),
     ("void mi::(anonymous namespace)::gemm_q8_kernel<64, 64, 2, 2, 2, 0, true, false, 2, 0>(mi::GemmArgs)",
