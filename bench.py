@@ -68,19 +68,31 @@ def quantize_q8_0(w: np.ndarray) -> np.ndarray:
 
 
 class GemmCase:
+    """mi_gemm_nt_q8_0_ws with the workspace the library asks for (the
+    reference's caller keeps such scratch in its step arena): small grids split
+    K there, summed in a fixed order. The workspace is (re)allocated by the
+    first call after the plan changes -- a warm-up call, never a timed one."""
     kernel = "gemm_q8"
 
     def __init__(self, tag, M, N, K, rng, hip, ops):
         self.tag, self.M, self.N, self.K = tag, M, N, K
-        self.ops = ops
+        self.ops, self.hip = ops, hip
         self.A = hip.DeviceBuffer.from_array(rng.standard_normal(M * K, dtype=np.float32))
         self.W = hip.DeviceBuffer.from_array(quantize_q8_0(rng.standard_normal(N * K, dtype=np.float32) * 0.02))
         self.C = hip.DeviceBuffer(M * N * 4)
+        self.ws = None
         self.flops = 2.0 * M * N * K
         self.bytes = 4.0 * M * K + 34.0 / 32.0 * N * K + 4.0 * M * N
 
+    def workspace(self):
+        n = self.ops.gemm_workspace_bytes(self.M, self.N, self.K)
+        if n and (self.ws is None or self.ws.nbytes < n):
+            self.ws = self.hip.DeviceBuffer(n)
+        return self.ws if n else None
+
     def run(self, stream):
-        self.ops.gemm_nt_q8_0(self.A, self.W, self.C, self.M, self.N, self.K, stream=stream)
+        self.ops.gemm_nt_q8_0(self.A, self.W, self.C, self.M, self.N, self.K, workspace=self.workspace(),
+                              stream=stream)
 
 
 class AttnCase:
@@ -130,11 +142,14 @@ class NnCase:
         self.As = hip.DeviceBuffer.from_array(blk[:, :2].copy().view(np.float16).astype(np.float32).reshape(-1))
         self.B = hip.DeviceBuffer.from_array(rng.standard_normal(K * N, dtype=np.float32))
         self.C = hip.DeviceBuffer(M * N * 4)
+        n = ops.gemm_nn_workspace_bytes(M, N, K)
+        self.ws = hip.DeviceBuffer(n) if n else None
         self.flops = 2.0 * M * N * K
         self.bytes = M * K * (1.0 + 4.0 / 32.0) + 4.0 * K * N + 4.0 * M * N
 
     def run(self, stream):
-        self.ops.gemm_nn_q8(self.Aq, self.As, self.B, self.C, self.M, self.N, self.K, stream=stream)
+        self.ops.gemm_nn_q8(self.Aq, self.As, self.B, self.C, self.M, self.N, self.K, workspace=self.ws,
+                            stream=stream)
 
 
 class BlockStack:
@@ -147,12 +162,15 @@ class BlockStack:
 
     DIMS = (2, 1024, 1280, 20, 77, 2048, 5120)  # batch, tokens, channels, heads, ctx_tokens, ctx_channels, ff_inner
 
-    def __init__(self, rng, hip, ops, nblocks=10, joint_qkv=False):
+    def __init__(self, rng, hip, ops, nblocks=10, joint_qkv=False, fused=False):
         """joint_qkv: each block's to_q / to_k / to_v weights in one allocation,
-        back to back, so the block runs one Q/K/V projection GEMM (N = 3C)."""
+        back to back, and MI_BLOCK_JOINT_QKV: one Q/K/V projection GEMM (N = 3C);
+        fused: MI_BLOCK_FUSED_EPILOGUES (residual adds and GEGLU in the GEMM
+        epilogues)."""
         B, T, C, H, Tc, Cc, F = self.DIMS
         self.ops, self.hip, self.nblocks = ops, hip, nblocks
-        self.dims = ops.BlockDims(*self.DIMS)
+        flags = (ops.MI_BLOCK_JOINT_QKV if joint_qkv else 0) | (ops.MI_BLOCK_FUSED_EPILOGUES if fused else 0)
+        self.dims = ops.BlockDims(*self.DIMS, flags)
         shapes = {"attn1_q": (C, C), "attn1_k": (C, C), "attn1_v": (C, C), "attn1_out": (C, C),
                   "attn2_q": (C, C), "attn2_k": (C, Cc), "attn2_v": (C, Cc), "attn2_out": (C, C),
                   "ff_up": (2 * F, C), "ff_down": (C, F)}
@@ -271,7 +289,7 @@ def extras(rng, hip, ops, stream, reps, emit=None):
     """Measurements outside the step metric: BASELINE config 0 (the reference
     harness's GEMM shape), the NN GEMM at the SDXL conv shapes, the config-4
     stack with the context's K / V cached, with the fused epilogues
-    (MI_BLOCK_EPILOGUE=fused), with joint Q/K/V weights and with all three, and
+    (MI_BLOCK_FUSED_EPILOGUES), with joint Q/K/V weights and with all three, and
     the candidate GEMM tile builds on every GEMM shape of the step, both
     workgroup sizes of the fp16 attention kernel on every attention shape, and
     the step replayed from a HIP graph next to the eager step. These
@@ -298,20 +316,11 @@ def extras(rng, hip, ops, stream, reps, emit=None):
 
     def stack(cached_kv=False, fused=False, joint_qkv=False):
         def run():
-            prev = os.environ.get("MI_BLOCK_EPILOGUE")
-            if fused:
-                os.environ["MI_BLOCK_EPILOGUE"] = "fused"
-            try:
-                st = BlockStack(rng, hip, ops, joint_qkv=joint_qkv)
-                res = st.measure(stream, 5, cached_kv=cached_kv)
-                res["variant"] = {"cached_kv": cached_kv, "fused_epilogues": fused, "joint_qkv": joint_qkv}
-                del st
-                return res
-            finally:
-                if prev is None:
-                    os.environ.pop("MI_BLOCK_EPILOGUE", None)
-                else:
-                    os.environ["MI_BLOCK_EPILOGUE"] = prev
+            st = BlockStack(rng, hip, ops, joint_qkv=joint_qkv, fused=fused)
+            res = st.measure(stream, 5, cached_kv=cached_kv)
+            res["variant"] = {"cached_kv": cached_kv, "fused_epilogues": fused, "joint_qkv": joint_qkv}
+            del st
+            return res
         return run
 
     def candidates():

@@ -107,10 +107,17 @@ int mi_q8_0_quantize(const float* w, void* blocks, uint64_t n, void* stream);
  * Arithmetic: A is rounded to fp16, the weight d*q is rounded to fp16, the
  * products are summed in fp32 by the gfx950 MFMA units; accuracy vs the
  * reference's fp32 shader is max|err| <= 2e-3 x RMS(C) at the SDXL shapes.
- * Activations must lie within the fp16 range (|a| < 65504).
+ * Activations must lie within the fp16 range (|a| < 65504): a larger |a| rounds
+ * to an infinite fp16 operand and its output row becomes inf / NaN.
  * Alignment: A 16-byte aligned with lda % 4 == 0 and sA % 4 == 0; C 4-byte
  * aligned. C must not overlap A, W or bias.
  * Returns MI_OK for M == 0 || N == 0 (nothing to do); K == 0 stores bias/0.
+ * Determinism: every entry sums in a fixed order, so a call repeats bit for
+ * bit. The entries without a workspace never split K, and every such call
+ * gives the same bits whatever tile build runs it. The *_ws entries may split
+ * K into the caller's workspace (partials summed in split order by a second
+ * kernel): bit-identical from run to run, but grouped differently from the
+ * unsplit sum (last-bit differences from the entry without a workspace).
  */
 
 /* North-star entry: W is the raw GGUF stream of 34-byte Q8_0 blocks, row n's
@@ -123,17 +130,39 @@ int mi_gemm_nt_q8_0(const float* A, const void* W, const float* bias, float* C, 
                     uint32_t N, uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldc,
                     uint32_t batch, uint64_t sA, uint64_t sC, void* stream);
 
+/* Workspace variants (no reference counterpart: the reference never splits K;
+ * the reference caller's step arena, sdvkgen.cpp:1080, is where such scratch
+ * lives). Grids too small to fill the GPU split K when `workspace` (device
+ * memory, 16-byte aligned, disjoint from every operand, caller-owned, used only
+ * in stream order) holds mi_gemm_nt_q8_workspace_bytes(M, N, K, batch) bytes;
+ * with less (or NULL) they run exactly as the entries without a workspace.
+ * Calls sharing a workspace must be ordered (same stream). */
+uint64_t mi_gemm_nt_q8_workspace_bytes(uint32_t M, uint32_t N, uint32_t K, uint32_t batch);
+int mi_gemm_nt_q8_0_ws(const float* A, const void* W, const float* bias, float* C, uint32_t M,
+                       uint32_t N, uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldc,
+                       uint32_t batch, uint64_t sA, uint64_t sC, void* workspace,
+                       uint64_t workspace_bytes, void* stream);
+
 /* Reference device layout: payload (int8 x4 per uint32, flat [N,K] order) +
  * fp32 scale per 32 flat elements (any fp32 value: LoRA requantisation writes
- * non-fp16 scales, sdvkgen.cpp:536-538). K % 4 == 0 (the reference's 4-wide
- * staging zero-fills otherwise, gemm_nt_q8_v.comp:69,86; rejected here).
- * Replaces Engine::dispatch("gemm_nt_q8_v[_bm128][_b]", {A, Bq, C, S[, bias]},
- * Pg{M,N,K,mode,sA,0,sC,batch,lda,0,ldc,0}) (vk_engine.cpp:55-63,
- * sdvkgen.cpp:917-936).                                                     */
+ * non-fp16 scales, sdvkgen.cpp:536-538). Any K, like the reference's scalar
+ * gemm_nt_q8 (gemm_nt_q8.comp:52-80): shapes with K % 4 != 0, lda or sA not a
+ * multiple of 4, or A not 16-byte aligned run on an untiled kernel that
+ * stages element by element (A 4-byte aligned). (The reference's vectorised
+ * gemm_nt_q8_v zero-fills a partial 4-group instead, gemm_nt_q8_v.comp:69,86;
+ * that quirk is not reproduced.)
+ * Replaces Engine::dispatch("gemm_nt_q8_v[_bm128][_b]" / "gemm_nt_q8",
+ * {A, Bq, C, S[, bias]}, Pg{M,N,K,mode,sA,0,sC,batch,lda,0,ldc,0})
+ * (vk_engine.cpp:55-63, sdvkgen.cpp:917-936, tests/gemm_q8_bench.cpp:32-38). */
 int mi_gemm_nt_q8_split(const float* A, const uint32_t* payload, const float* scales,
                         const float* bias, float* C, uint32_t M, uint32_t N, uint32_t K,
                         uint32_t mode, uint32_t lda, uint32_t ldc, uint32_t batch, uint64_t sA,
                         uint64_t sC, void* stream);
+/* Workspace variant of mi_gemm_nt_q8_split (as mi_gemm_nt_q8_0_ws). */
+int mi_gemm_nt_q8_split_ws(const float* A, const uint32_t* payload, const float* scales,
+                           const float* bias, float* C, uint32_t M, uint32_t N, uint32_t K,
+                           uint32_t mode, uint32_t lda, uint32_t ldc, uint32_t batch, uint64_t sA,
+                           uint64_t sC, void* workspace, uint64_t workspace_bytes, void* stream);
 
 /* GEGLU fused into the FF-up projection: W holds 2F Q8_0 rows (GEGLU's value
  * rows 0..F-1, then its gate rows F..2F-1: the proj layout of diffusers'
@@ -156,14 +185,22 @@ int mi_gemm_nt_q8_0_geglu(const float* A, const void* W, const float* bias, floa
  * partial group, :58,79: rejected, not emulated). payload 4-byte aligned with
  * lda, sA % 4 == 0; B 16-byte aligned with ldb, sB % 4 == 0; each operand
  * below 2 GiB. payload 16-byte aligned with lda, sA % 16 == 0 and
- * K % 64 == 0 (every SDXL conv) take the pipelined tiled kernel, which may
- * split K and add the splits with atomics (last bits then vary run to run);
- * other shapes take the untiled kernel. Replaces Engine::dispatch("gemm_nn_q8_v"
- * / "gemm_nn_q8", {Aq, B, C, S}, Pg) (vk_engine.cpp:57,63) behind gemmNnQ8
- * (sdvkgen.cpp:944-948). */
+ * K % 64 == 0 (every SDXL conv) take the pipelined tiled kernel; other shapes
+ * take the untiled kernel. Sums in a fixed order (results repeat bit for bit).
+ * Replaces Engine::dispatch("gemm_nn_q8_v" / "gemm_nn_q8", {Aq, B, C, S}, Pg)
+ * (vk_engine.cpp:57,63) behind gemmNnQ8 (sdvkgen.cpp:944-948). */
 int mi_gemm_nn_q8_split(const uint32_t* payload, const float* scales, const float* B, float* C,
                         uint32_t M, uint32_t N, uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldb,
                         uint32_t ldc, uint32_t batch, uint64_t sA, uint64_t sB, uint64_t sC, void* stream);
+/* Workspace variant (no reference counterpart): the tiled kernel splits K when
+ * its grid would leave CUs idle and `workspace` holds
+ * mi_gemm_nn_q8_workspace_bytes(M, N, K, batch) bytes (16-byte aligned,
+ * disjoint from the operands); the partials are summed in split order. */
+uint64_t mi_gemm_nn_q8_workspace_bytes(uint32_t M, uint32_t N, uint32_t K, uint32_t batch);
+int mi_gemm_nn_q8_split_ws(const uint32_t* payload, const float* scales, const float* B, float* C,
+                           uint32_t M, uint32_t N, uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldb,
+                           uint32_t ldc, uint32_t batch, uint64_t sA, uint64_t sB, uint64_t sC,
+                           void* workspace, uint64_t workspace_bytes, void* stream);
 
 /* ----------------------------------------------------------- attention -- *
  * O = softmax(Q K^T / sqrt(hd) + mask) V per head, hd = C / heads <= 64,
@@ -231,7 +268,16 @@ int mi_add_inplace(float* x, const float* a, uint64_t n, void* stream);
  * ctx_len: device int32[batch] key-padding lengths for the cross-attention,
  * or NULL. workspace: device memory of mi_block_workspace_bytes() bytes,
  * 256-byte aligned; nothing is allocated. Calls sharing a workspace must be
- * ordered (same stream).                                                   */
+ * ordered (same stream).
+ * dims.flags (0 = the reference's sequence of separate operators):
+ *   MI_BLOCK_FUSED_EPILOGUES: the residual adds run in the out-projection /
+ *     FF-down GEMM epilogues (mode 2) and GEGLU in the FF-up epilogue;
+ *   MI_BLOCK_JOINT_QKV: attn1_q / attn1_k / attn1_v are the three C x C parts
+ *     of one [3C, C] Q8_0 matrix (attn1_k = attn1_q + C*(C/32)*34 bytes,
+ *     attn1_v = attn1_k + as much; else MI_ERR_INVALID_ARG), projected by one
+ *     GEMM.
+ * Every flag combination computes the same bits (the block sums in a fixed
+ * order, and the GEMMs that differ between the variants never split K).   */
 typedef struct mi_block_weights {
     const float *norm1_w, *norm1_b, *norm2_w, *norm2_b, *norm3_w, *norm3_b; /* [channels] */
     const void *attn1_q, *attn1_k, *attn1_v, *attn1_out;    /* [channels, channels] */
@@ -246,8 +292,11 @@ typedef struct mi_block_weights {
     const float* ff_down_b;                                  /* [channels] or NULL */
 } mi_block_weights;
 
+enum { MI_BLOCK_FUSED_EPILOGUES = 1, MI_BLOCK_JOINT_QKV = 2 };
+
 typedef struct mi_block_dims {
     uint32_t batch, tokens, channels, heads, ctx_tokens, ctx_channels, ff_inner;
+    uint32_t flags;       /* MI_BLOCK_* bits */
 } mi_block_dims;
 
 uint64_t mi_block_workspace_bytes(const mi_block_dims* dims);
@@ -262,9 +311,9 @@ int mi_sdxl_block_forward(const mi_block_weights* w, const mi_block_dims* dims, 
  * into `kv` (K, then V at byte offset mi_block_ctx_kv_bytes / 2; each
  * [batch * ctx_tokens, channels] fp32; 256-byte aligned, caller-owned);
  * mi_sdxl_block_forward_kv then runs the block exactly like
- * mi_sdxl_block_forward but reads K / V from `kv` instead of projecting ctx.
- * The K / V GEMMs split K with fp32 atomics, so a fresh projection and a
- * cached one may differ in the last bits.                                   */
+ * mi_sdxl_block_forward but reads K / V from `kv` instead of projecting ctx;
+ * both project with the same unsplit GEMMs, so cached and fresh results are
+ * bit-identical.                                                            */
 uint64_t mi_block_ctx_kv_bytes(const mi_block_dims* dims);
 int mi_block_ctx_kv(const mi_block_weights* w, const mi_block_dims* dims, const float* ctx, float* kv,
                     uint64_t kv_bytes, void* stream);

@@ -45,7 +45,10 @@ class MiBlockWeights(ctypes.Structure):
 class MiBlockDims(ctypes.Structure):
     """Mirror of mi_block_dims (include/mi_sdvk.h)."""
     _fields_ = [(n, _u32) for n in ("batch", "tokens", "channels", "heads", "ctx_tokens", "ctx_channels",
-                                    "ff_inner")]
+                                    "ff_inner", "flags")]
+
+
+MI_BLOCK_FUSED_EPILOGUES, MI_BLOCK_JOINT_QKV = 1, 2
 
 
 class MiGgufTensorInfo(ctypes.Structure):
@@ -72,9 +75,17 @@ SIGNATURES = {
                                        _u64, _u64, _vp]),
     "mi_gemm_nt_q8_split": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32,
                                            _u32, _u64, _u64, _vp]),
+    "mi_gemm_nt_q8_workspace_bytes": (_u64, [_u32, _u32, _u32, _u32]),
+    "mi_gemm_nt_q8_0_ws": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32,
+                                          _u64, _u64, _vp, _u64, _vp]),
+    "mi_gemm_nt_q8_split_ws": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32,
+                                              _u32, _u64, _u64, _vp, _u64, _vp]),
     "mi_gemm_nt_q8_0_geglu": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp]),
     "mi_gemm_nn_q8_split": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32,
                                            _u64, _u64, _u64, _vp]),
+    "mi_gemm_nn_q8_workspace_bytes": (_u64, [_u32, _u32, _u32, _u32]),
+    "mi_gemm_nn_q8_split_ws": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32,
+                                              _u64, _u64, _u64, _vp, _u64, _vp]),
     "mi_fused_attn_supported": (ctypes.c_int, [_u32, _u32]),
     "mi_fused_attention": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, ctypes.c_int, _vp]),
     "mi_fused_attention_ex": (ctypes.c_int, [ctypes.POINTER(MiAttnArgs), _vp]),

@@ -11,15 +11,18 @@
 // in a caller-provided workspace (nothing is allocated), every launch is
 // ordered on the caller's stream.
 //
-// Fused epilogues (MI_BLOCK_EPILOGUE=fused): the out-projections and FF-down
-// add their product and bias straight into x (GEMM mode 2) and FF-up applies
-// GEGLU in its epilogue (mi_gemm_nt_q8_0_geglu), which removes the three
-// residual-add passes and the [rows, 2 ff_inner] intermediate. Off by default
-// until timed on the GPU; results agree with the separate path to fp32
-// rounding.
-#include <cstdlib>
-#include <cstring>
-
+// mi_block_dims.flags:
+//   MI_BLOCK_FUSED_EPILOGUES: the out-projections and FF-down add their product
+//     and bias straight into x (GEMM mode 2) and FF-up applies GEGLU in its
+//     epilogue (mi_gemm_nt_q8_0_geglu), which removes the three residual-add
+//     passes and the [rows, 2 ff_inner] intermediate;
+//   MI_BLOCK_JOINT_QKV: attn1 to_q / to_k / to_v are one [3C, C] Q8_0 matrix
+//     (the three pointers must be C x C matrices apart), projected by one GEMM.
+// Every variant computes the same bits: the GEMMs whose results must agree
+// across variants (Q / K / V, context K / V, FF-up) never split K, the
+// residual GEMMs split K the same way in both epilogue forms (partials in the
+// workspace, summed in a fixed order), and an unsplit GEMM's sums do not
+// depend on the tile build.
 #include "common.hpp"
 
 namespace mi {
@@ -27,23 +30,40 @@ namespace {
 
 struct Workspace {
     float *n, *q, *k, *v, *o, *a, *h, *g;
+    float* split;           // K-split partials of the residual GEMMs
+    uint64_t split_bytes;
 };
 
 uint64_t round256(uint64_t b) { return (b + 255) / 256 * 256; }
 
-// Byte layout of the workspace; returns the total.
+// Workspace the residual GEMMs' K splits use (out-projections: K = C,
+// FF-down: K = ff_inner; both N = C).
+uint64_t split_bytes(const mi_block_dims& d) {
+    const uint32_t rows = d.batch * d.tokens;
+    const uint64_t a = mi_gemm_nt_q8_workspace_bytes(rows, d.channels, d.channels, 1);
+    const uint64_t b = mi_gemm_nt_q8_workspace_bytes(rows, d.channels, d.ff_inner, 1);
+    return a > b ? a : b;
+}
+
+// Byte layout of the workspace; returns the total. h holds FF-up's
+// [rows, 2 ff_inner] output and, before the FF stage, the joint Q/K/V
+// projection's [rows, 3C].
 uint64_t layout(const mi_block_dims& d, char* base, Workspace* w) {
     const uint64_t rows = static_cast<uint64_t>(d.batch) * d.tokens;
     const uint64_t crow = static_cast<uint64_t>(d.batch) * d.ctx_tokens;
     const uint64_t kvrows = rows > crow ? rows : crow;
+    const uint64_t hcols = 2ull * d.ff_inner > 3ull * d.channels ? 2ull * d.ff_inner : 3ull * d.channels;
     const uint64_t sizes[8] = {rows * d.channels, rows * d.channels, kvrows * d.channels, kvrows * d.channels,
-                               rows * d.channels, rows * d.channels, rows * 2ull * d.ff_inner, rows * d.ff_inner};
+                               rows * d.channels, rows * d.channels, rows * hcols, rows * d.ff_inner};
     float** slots[8] = {&w->n, &w->q, &w->k, &w->v, &w->o, &w->a, &w->h, &w->g};
     uint64_t off = 0;
     for (int i = 0; i < 8; ++i) {
         if (base) *slots[i] = reinterpret_cast<float*>(base + off);
         off += round256(sizes[i] * 4);
     }
+    w->split_bytes = split_bytes(d);
+    w->split = base && w->split_bytes ? reinterpret_cast<float*>(base + off) : nullptr;
+    off += round256(w->split_bytes);
     return off;
 }
 
@@ -55,6 +75,8 @@ int check_dims(const mi_block_dims& d, const char* fn) {
                     d.heads);
     if (d.channels % 32 || d.ctx_channels % 32 || d.ff_inner % 32)
         return fail(MI_ERR_UNSUPPORTED, "%s: channels, ctx_channels and ff_inner must be multiples of 32 (Q8_0 K)", fn);
+    if (d.flags & ~static_cast<uint32_t>(MI_BLOCK_FUSED_EPILOGUES | MI_BLOCK_JOINT_QKV))
+        return fail(MI_ERR_INVALID_ARG, "%s: unknown flags 0x%x", fn, d.flags);
     return MI_OK;
 }
 
@@ -86,24 +108,24 @@ int attention(const mi_block_dims& d, const float* q, const float* k, const floa
     return mi_fused_attention_ex(&x, s);
 }
 
-// Q, K and V weights stored back to back ([Wq; Wk; Wv], one 3C x C Q8_0
-// matrix) take one projection GEMM with N = 3C instead of three (a grid three
-// times wider: larger tiles fill the CUs); attention then reads Q / K / V from
-// the [rows, 3C] result at token stride 3C.
+// MI_BLOCK_JOINT_QKV: Q, K and V weights stored back to back ([Wq; Wk; Wv],
+// one 3C x C Q8_0 matrix) take one projection GEMM with N = 3C instead of three
+// (a grid three times wider: larger tiles fill the CUs); attention then reads
+// Q / K / V from the [rows, 3C] result at token stride 3C.
 bool adjacent(const void* a, const void* b, uint64_t bytes) {
     return static_cast<const char*>(a) + bytes == static_cast<const char*>(b);
 }
 
-bool fused_epilogues() {
-    const char* e = std::getenv("MI_BLOCK_EPILOGUE");
-    return e && std::strcmp(e, "fused") == 0;
-}
-
-int check_weights(const mi_block_weights& w, const char* fn) {
+int check_weights(const mi_block_weights& w, const mi_block_dims& d, const char* fn) {
     const void* mats[10] = {w.attn1_q, w.attn1_k, w.attn1_v, w.attn1_out, w.attn2_q,
                             w.attn2_k, w.attn2_v, w.attn2_out, w.ff_up, w.ff_down};
     for (const void* m : mats)
         if (!m) return fail(MI_ERR_INVALID_ARG, "%s: null weight", fn);
+    const uint64_t wcc = static_cast<uint64_t>(d.channels) * (d.channels / 32) * 34;  // one C x C Q8_0 matrix
+    if ((d.flags & MI_BLOCK_JOINT_QKV) && !(adjacent(w.attn1_q, w.attn1_k, wcc) && adjacent(w.attn1_k, w.attn1_v, wcc)))
+        return fail(MI_ERR_INVALID_ARG, "%s: MI_BLOCK_JOINT_QKV needs attn1_k = attn1_q + %llu bytes and attn1_v = "
+                    "attn1_k + %llu bytes (one [3C, C] matrix)", fn, static_cast<unsigned long long>(wcc),
+                    static_cast<unsigned long long>(wcc));
     return MI_OK;
 }
 
@@ -123,7 +145,7 @@ int ctx_kv(const mi_block_weights& w, const mi_block_dims& d, const float* ctx, 
 int forward(const mi_block_weights& w, const mi_block_dims& d, float* x, const float* ctx, const float* kv,
             const int32_t* ctx_len, void* workspace, uint64_t workspace_bytes, hipStream_t s, const char* fn) {
     MI_TRY(check_dims(d, fn));
-    MI_TRY(check_weights(w, fn));
+    MI_TRY(check_weights(w, d, fn));
     Workspace ws;
     const uint64_t need = layout(d, static_cast<char*>(workspace), &ws);
     if (workspace_bytes < need)
@@ -136,20 +158,19 @@ int forward(const mi_block_weights& w, const mi_block_dims& d, float* x, const f
     auto gemm = [&](const float* A, const void* W, const float* bias, float* out, uint32_t M, uint32_t N, uint32_t K) {
         return mi_gemm_nt_q8_0(A, W, bias, out, M, N, K, 0, 0, 0, 1, 0, 0, s);
     };
-    const bool fused = fused_epilogues();
-    // x += A . W^T + bias: one GEMM with the residual epilogue, or GEMM + add
+    const bool fused = (d.flags & MI_BLOCK_FUSED_EPILOGUES) != 0;
+    // x += A . W^T + bias: one GEMM with the residual epilogue, or GEMM + add;
+    // both split K the same way (the workspace's partials region)
     auto residual = [&](const float* A, const void* W, const float* bias, uint32_t K) {
-        if (fused) return mi_gemm_nt_q8_0(A, W, bias, x, rows, C, K, 2, 0, 0, 1, 0, 0, s);
-        const int st = gemm(A, W, bias, ws.a, rows, C, K);
+        if (fused) return mi_gemm_nt_q8_0_ws(A, W, bias, x, rows, C, K, 2, 0, 0, 1, 0, 0, ws.split, ws.split_bytes, s);
+        const int st = mi_gemm_nt_q8_0_ws(A, W, bias, ws.a, rows, C, K, 0, 0, 0, 1, 0, 0, ws.split, ws.split_bytes, s);
         return st != MI_OK ? st : mi_add_inplace(x, ws.a, nx, s);
     };
 
     // self-attention
     MI_TRY(mi_layernorm(x, w.norm1_w, w.norm1_b, ws.n, rows, C, 1e-5f, s));
-    const uint64_t wcc = static_cast<uint64_t>(C) * (C / 32) * 34;  // bytes of one C x C Q8_0 matrix
     // the joint result [rows, 3C] goes to the FF-up region, free until the FF stage
-    if (adjacent(w.attn1_q, w.attn1_k, wcc) && adjacent(w.attn1_k, w.attn1_v, wcc) &&
-        2ull * d.ff_inner >= 3ull * C) {
+    if (d.flags & MI_BLOCK_JOINT_QKV) {
         MI_TRY(gemm(ws.n, w.attn1_q, nullptr, ws.h, rows, 3 * C, C));
         MI_TRY(attention(d, ws.h, ws.h + C, ws.h + 2 * C, 3ull * C, ws.o, d.tokens, nullptr, s));
     } else {
@@ -209,7 +230,7 @@ extern "C" int mi_block_ctx_kv(const mi_block_weights* wt, const mi_block_dims* 
     const char* fn = "mi_block_ctx_kv";
     if (!wt || !dims || !ctx || !kv) return fail(MI_ERR_INVALID_ARG, "%s: null pointer", fn);
     MI_TRY(check_dims(*dims, fn));
-    MI_TRY(check_weights(*wt, fn));
+    MI_TRY(check_weights(*wt, *dims, fn));
     if (kv_bytes < ctx_kv_bytes(*dims))
         return fail(MI_ERR_INVALID_ARG, "%s: kv buffer %llu bytes < %llu needed", fn,
                     static_cast<unsigned long long>(kv_bytes), static_cast<unsigned long long>(ctx_kv_bytes(*dims)));

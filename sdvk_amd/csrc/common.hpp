@@ -36,6 +36,14 @@ inline bool overlaps(const void* a, uint64_t na, const void* b, uint64_t nb) {
 
 inline unsigned ceil_div(uint64_t a, uint64_t b) { return static_cast<unsigned>((a + b - 1) / b); }
 
+// Sums the partial planes of a K-split GEMM in split order into C (gemm_q8.hip).
+// P holds batch * splits planes of [M, N] floats (row stride N): batch item z,
+// split s at P + (z * splits + s) * M * N. op 0: C = sum + bias (bias may be
+// NULL); op 1: C += sum; op 2: C += sum + bias. The order of the additions is
+// fixed, so results repeat bit for bit.
+void launch_splitk_reduce(const float* P, uint32_t splits, float* C, const float* bias, uint32_t M, uint32_t N,
+                          uint32_t ldc, uint64_t sC, uint32_t batch, int op, hipStream_t s);
+
 // ----------------------------------------------------------- device helpers --
 
 // fp16 bit pattern -> fp32, exact for every pattern (subnormals scaled by
@@ -55,7 +63,11 @@ __device__ __forceinline__ float fp16_bits_to_f32(uint32_t h) {
 // erf GELU, Abramowitz & Stegun 7.1.26 (the published rational approximation
 // the reference shader uses): erf(z) ~ 1 - (a1 t + ... + a5 t^5) exp(-z^2),
 // t = 1 / (1 + p z), z >= 0, odd extension.
+// Contraction is off: every multiply and add rounds on its own, so the GELU
+// computes the same bits in every kernel it is inlined into (the GEGLU GEMM
+// epilogue and the separate GEGLU kernel agree exactly).
 __device__ __forceinline__ float gelu_erf(float v) {
+#pragma clang fp contract(off)
     const float xs = v * 0.70710678118654752440f;
     const float ax = fabsf(xs);
     const float t = 1.0f / (1.0f + 0.3275911f * ax);

@@ -22,9 +22,10 @@
 //     fma(float(q + 128), s, -128 s). B is read as row-coalesced 16-byte pieces
 //     of four k rows and transposed in registers (a 4 x 4 block of k by n per
 //     thread) so LDS holds [n][k] and both MFMA operands are 8 consecutive k
-//     per lane. Grids that would leave CUs idle split K; the splits add their
-//     partial tiles with fp32 atomics after a fill kernel has cleared C
-//     (mode 0), so the summation order varies run to run (last bits only).
+//     per lane. With a caller workspace (mi_gemm_nn_q8_split_ws), grids that
+//     would leave CUs idle split K: each split stores its partial tile into the
+//     workspace and a reduce kernel adds them in split order (fixed, so a call
+//     repeats bit for bit).
 //   * gemm_nn_q8_kernel (every other shape): 64 x 64 tiles, four waves of one
 //     32 x 32 tile, 32 k per step, no software pipelining; W is dequantised per
 //     4-element group with that group's flat scale (exactly the shader's
@@ -52,6 +53,7 @@ struct NnArgs {
     uint32_t sA, sB, sC;                      // batch strides (elements), < 2^31 by validation
     uint32_t a_bytes, s_bytes, b_bytes, c_bytes;  // whole-buffer extents
     uint32_t splits, steps_per_split;         // tiled kernel: K splits (blockIdx.z = batch * splits + split)
+    uint64_t plane;                           // K splits: floats per partial plane (C = workspace, ldc = N)
 };
 
 constexpr int kTM = 64, kTN = 64, kTK = 32;
@@ -147,38 +149,6 @@ constexpr int kBM2 = 128, kBN2 = 256, kBK2 = 64;
 constexpr int kLd2 = kBK2 + 8;   // LDS row stride in halves (16-byte pad: conflict-free reads and writes)
 constexpr int kNT2 = 512;        // eight waves: 2 (m) x 4 (n), 64 x 64 each
 constexpr uint32_t kCUs = 256;
-
-// C[z] rows m < M, columns n < N = 0 (mode 0 before K splits add into C).
-__global__ __launch_bounds__(256) void gemm_nn_zero_kernel(float* C, uint32_t M, uint32_t N, uint32_t ldc,
-                                                           uint32_t sC) {
-    const uint32_t n = blockIdx.x * 256 + threadIdx.x;
-    if (n >= N) return;
-    float* c = C + static_cast<uint64_t>(blockIdx.z) * sC + n;
-    for (uint32_t m = blockIdx.y; m < M; m += gridDim.y) c[static_cast<uint64_t>(m) * ldc] = 0.0f;
-}
-
-// The same clear with one 16-byte store per work-item step over the flattened
-// [M, N / 4] index of each batch item (blockIdx.y), for 16-byte aligned rows.
-__global__ __launch_bounds__(256) void gemm_nn_zero_vec_kernel(float* C, uint32_t M, uint32_t N4, uint32_t ldc,
-                                                               uint32_t sC) {
-    float* c = C + static_cast<uint64_t>(blockIdx.y) * sC;
-    const uint64_t total = static_cast<uint64_t>(M) * N4;
-    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * 256;
-    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x; i < total; i += stride) {
-        const uint32_t m = static_cast<uint32_t>(i / N4), n = static_cast<uint32_t>(i % N4) * 4;
-        *reinterpret_cast<floatx4*>(c + static_cast<uint64_t>(m) * ldc + n) = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
-}
-
-void launch_zero(float* C, uint32_t M, uint32_t N, uint32_t ldc, uint32_t sC, uint32_t batch, hipStream_t st) {
-    if (reinterpret_cast<uintptr_t>(C) % 16 == 0 && N % 4 == 0 && ldc % 4 == 0 && sC % 4 == 0) {
-        const uint64_t n4 = static_cast<uint64_t>(M) * (N / 4);
-        const unsigned gx = static_cast<unsigned>(std::min<uint64_t>(std::max<uint64_t>(ceil_div(n4, 256ull), 1), 1024));
-        gemm_nn_zero_vec_kernel<<<dim3(gx, batch), 256, 0, st>>>(C, M, N / 4, ldc, sC);
-        return;
-    }
-    gemm_nn_zero_kernel<<<dim3(ceil_div(N, 256), std::min<uint32_t>(M, 4096), batch), 256, 0, st>>>(C, M, N, ldc, sC);
-}
 
 template <bool SPLITK>
 __global__ __launch_bounds__(kNT2) void gemm_nn_q8_tiled_kernel(NnArgs a) {
@@ -314,7 +284,8 @@ __global__ __launch_bounds__(kNT2) void gemm_nn_q8_tiled_kernel(NnArgs a) {
 
     // lane holds column n = l32 and rows 8 (r / 4) + 4 g + r % 4 of each
     // 32 x 32 tile: for each r, 32 lanes cover 32 consecutive floats of a row
-    float* C = a.C + static_cast<uint64_t>(z) * a.sC;
+    // split K: the split's partial plane of the workspace (row stride ldc = N)
+    float* C = a.C + (SPLITK ? (static_cast<uint64_t>(z) * a.splits + split) * a.plane : static_cast<uint64_t>(z) * a.sC);
 #pragma unroll
     for (int jt = 0; jt < 2; ++jt) {
         const uint32_t n = n0 + wn * 64 + 32 * jt + l32;
@@ -326,7 +297,7 @@ __global__ __launch_bounds__(kNT2) void gemm_nn_q8_tiled_kernel(NnArgs a) {
                 const uint32_t m = m0 + wm * 64 + 32 * it + 8 * (r >> 2) + 4 * g + (r & 3);
                 if (m >= a.M) continue;
                 float* c = C + static_cast<uint64_t>(m) * a.ldc + n;
-                if constexpr (SPLITK) unsafeAtomicAdd(c, acc[it][jt][r]);  // native global_atomic_add_f32
+                if constexpr (SPLITK) *c = acc[it][jt][r];
                 else *c = a.mode != 0 ? *c + acc[it][jt][r] : acc[it][jt][r];
             }
     }
@@ -337,10 +308,29 @@ __global__ __launch_bounds__(kNT2) void gemm_nn_q8_tiled_kernel(NnArgs a) {
 
 using namespace mi;
 
-extern "C" int mi_gemm_nn_q8_split(const uint32_t* payload, const float* scales, const float* B, float* C, uint32_t M,
-                                   uint32_t N, uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldb, uint32_t ldc,
-                                   uint32_t batch, uint64_t sA, uint64_t sB, uint64_t sC, void* stream) {
-    const char* fn = "mi_gemm_nn_q8_split";
+namespace mi {
+namespace {
+
+bool nn_tiled(const uint32_t* payload, uint32_t K, uint32_t lda, uint64_t sA) {
+    const char* env = std::getenv("MI_NN_KERNEL");  // "general": the untiled kernel for every shape (tests)
+    return K > 0 && K % kBK2 == 0 && aligned(payload, 16) && lda % 16 == 0 && sA % 16 == 0 &&
+           !(env && std::strcmp(env, "general") == 0);
+}
+
+// K splits of the tiled kernel: one 8-wave workgroup per CU; split K until the
+// grid covers the CUs, keeping at least four 64-wide steps per split.
+uint32_t nn_splits(uint32_t M, uint32_t N, uint32_t K, uint32_t batch) {
+    const uint64_t tiles = static_cast<uint64_t>(ceil_div(N, kBN2)) * ceil_div(M, kBM2) * batch;
+    const uint32_t ksteps = K / kBK2;
+    uint32_t splits = 1;
+    while (tiles * splits < kCUs && splits * 2 * 4 <= ksteps && batch * splits * 2 <= 65535) splits *= 2;
+    if (splits > 1) splits = ceil_div(ksteps, ceil_div(ksteps, splits));
+    return splits;
+}
+
+int gemm_nn(const char* fn, const uint32_t* payload, const float* scales, const float* B, float* C, uint32_t M,
+            uint32_t N, uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t batch,
+            uint64_t sA, uint64_t sB, uint64_t sC, void* ws, uint64_t ws_bytes, hipStream_t st) {
     if (M == 0 || N == 0) return MI_OK;
     if (!payload || !scales || !B || !C) return fail(MI_ERR_INVALID_ARG, "%s: null pointer", fn);
     if (mode > 1) return fail(MI_ERR_INVALID_ARG, "%s: mode %u (0 = store, 1 = accumulate)", fn, mode);
@@ -391,33 +381,62 @@ extern "C" int mi_gemm_nn_q8_split(const uint32_t* payload, const float* scales,
     a.b_bytes = static_cast<uint32_t>(b_el * 4);
     a.c_bytes = static_cast<uint32_t>(c_el * 4);
     a.splits = 1;
-    const hipStream_t st = static_cast<hipStream_t>(stream);
-    const char* env = std::getenv("MI_NN_KERNEL");  // "general": the untiled kernel for every shape (tests)
-    const bool tiled = K > 0 && K % kBK2 == 0 && aligned(payload, 16) && lda % 16 == 0 && sA % 16 == 0 &&
-                       !(env && std::strcmp(env, "general") == 0);
+    if (ws && ws_bytes) {
+        if (!aligned(ws, 16)) return fail(MI_ERR_ALIGNMENT, "%s: workspace must be 16-byte aligned", fn);
+        if (overlaps(ws, ws_bytes, payload, a_el) || overlaps(ws, ws_bytes, scales, s_el * 4) ||
+            overlaps(ws, ws_bytes, B, b_el * 4) || overlaps(ws, ws_bytes, C, c_el * 4))
+            return fail(MI_ERR_ALIASING, "%s: workspace overlaps an operand", fn);
+    }
+    const bool tiled = nn_tiled(payload, K, lda, sA);
     if (!tiled) {
         const dim3 grid(ceil_div(N, kTN), ceil_div(M, kTM), batch);
         gemm_nn_q8_kernel<<<grid, 256, 0, st>>>(a);
         return check_launch(fn);
     }
-    // One 8-wave workgroup per CU: split K until the grid covers the CUs, keeping
-    // at least four 64-wide steps per split.
-    const uint64_t tiles = static_cast<uint64_t>(ceil_div(N, kBN2)) * ceil_div(M, kBM2) * batch;
     const uint32_t ksteps = K / kBK2;
-    uint32_t splits = 1;
-    while (tiles * splits < kCUs && splits * 2 * 4 <= ksteps && batch * splits * 2 <= 65535) splits *= 2;
+    uint32_t splits = ws ? nn_splits(M, N, K, batch) : 1;
+    const uint64_t plane = static_cast<uint64_t>(M) * N;
+    if (splits > 1 && static_cast<uint64_t>(batch) * splits * plane * 4 > ws_bytes) splits = 1;
     if (splits > 1) {
-        a.steps_per_split = ceil_div(ksteps, splits);
-        splits = ceil_div(ksteps, a.steps_per_split);
-    }
-    a.splits = splits;
-    if (splits > 1) {
-        if (mode == 0)
-            launch_zero(C, M, N, ldc, a.sC, batch, st);
-        gemm_nn_q8_tiled_kernel<true><<<dim3(ceil_div(N, kBN2), ceil_div(M, kBM2), batch * splits), kNT2, 0, st>>>(a);
+        // partial planes into the workspace, then their sum in split order
+        NnArgs p = a;
+        p.steps_per_split = ceil_div(ksteps, splits);
+        p.splits = splits;
+        p.C = static_cast<float*>(ws);
+        p.ldc = N;
+        p.plane = plane;
+        p.mode = 0;
+        gemm_nn_q8_tiled_kernel<true><<<dim3(ceil_div(N, kBN2), ceil_div(M, kBM2), batch * splits), kNT2, 0, st>>>(p);
+        launch_splitk_reduce(static_cast<const float*>(ws), splits, C, nullptr, M, N, ldc, sC, batch, mode == 0 ? 0 : 1,
+                             st);
     } else {
         a.steps_per_split = ksteps;
         gemm_nn_q8_tiled_kernel<false><<<dim3(ceil_div(N, kBN2), ceil_div(M, kBM2), batch), kNT2, 0, st>>>(a);
     }
     return check_launch(fn);
+}
+
+}  // namespace
+}  // namespace mi
+
+extern "C" int mi_gemm_nn_q8_split(const uint32_t* payload, const float* scales, const float* B, float* C, uint32_t M,
+                                   uint32_t N, uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldb, uint32_t ldc,
+                                   uint32_t batch, uint64_t sA, uint64_t sB, uint64_t sC, void* stream) {
+    return mi::gemm_nn("mi_gemm_nn_q8_split", payload, scales, B, C, M, N, K, mode, lda, ldb, ldc, batch, sA, sB, sC,
+                       nullptr, 0, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mi_gemm_nn_q8_split_ws(const uint32_t* payload, const float* scales, const float* B, float* C,
+                                      uint32_t M, uint32_t N, uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldb,
+                                      uint32_t ldc, uint32_t batch, uint64_t sA, uint64_t sB, uint64_t sC,
+                                      void* workspace, uint64_t workspace_bytes, void* stream) {
+    return mi::gemm_nn("mi_gemm_nn_q8_split_ws", payload, scales, B, C, M, N, K, mode, lda, ldb, ldc, batch, sA, sB,
+                       sC, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" uint64_t mi_gemm_nn_q8_workspace_bytes(uint32_t M, uint32_t N, uint32_t K, uint32_t batch) {
+    // the tiled kernel's split plan (shapes the untiled kernel serves use none of it)
+    if (M == 0 || N == 0 || batch == 0 || K == 0 || K % mi::kBK2) return 0;
+    const uint32_t splits = mi::nn_splits(M, N, K, batch);
+    return splits > 1 ? static_cast<uint64_t>(batch) * splits * M * N * 4 : 0;
 }

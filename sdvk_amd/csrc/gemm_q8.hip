@@ -17,9 +17,11 @@
 //   * workgroup ids are remapped so that each XCD runs a compact block of
 //     tiles (a grouped tile order cut into one contiguous chunk per XCD) and
 //     its workgroups share A and W panels in that XCD's L2;
-//   * grids too small to fill 256 CUs split K: each split adds its partial tile
-//     into C with fp32 atomics after a fill kernel has written bias / 0.
-//     Summation order then varies run to run (last-bit differences only).
+//   * grids too small to fill 256 CUs may split K when the caller passes a
+//     workspace (the *_ws entries): each split stores its partial tile into
+//     the workspace and a reduce kernel adds the partials in split order, then
+//     applies bias / accumulate. Every plan sums in a fixed order, so a call
+//     repeats bit for bit; entries without a workspace never split K.
 #include <algorithm>
 #include <type_traits>
 #include <cstdlib>
@@ -47,6 +49,7 @@ struct GemmArgs {
     uint32_t cvec;          // C rows 16-byte aligned (C % 16 == 0, ldc % 4 == 0, sC % 4 == 0)
     uint32_t bvec;          // bias 16-byte aligned
     uint32_t F;             // GEGLU epilogue: output columns (W has 2F rows: value rows, then gate rows)
+    uint64_t split_stride;  // K-split partials: elements between the planes of consecutive splits
 };
 
 // Epilogues. kEpiPlain: the reference's modes (0 stores acc + bias, 1 adds acc
@@ -156,9 +159,9 @@ __device__ __forceinline__ void interleave_step_tail() {
 // edge branches is tens of KB of code that every workgroup runs once, cold in
 // the instruction cache).
 // Split K: the plain product (a lane holds column l32 and rows
-// 8 (r / 4) + 4 g + r % 4) is added with fp32 atomics straight from the
-// registers, 32 consecutive floats per instruction; bias came from the fill
-// kernel.
+// 8 (r / 4) + 4 g + r % 4) is stored straight from the registers into the
+// split's partial plane (row stride ldc = N), 32 consecutive floats per
+// instruction; the reduce kernel adds the planes and applies bias / mode.
 constexpr int kStageLd = 36;                       // floats per staged row (16-byte pad)
 constexpr int kStageFloats = 32 * kStageLd;        // per wave
 
@@ -174,7 +177,7 @@ __device__ __forceinline__ void store_tiles(const GemmArgs& a, float* C, float* 
     const bool use_bias = !SPLITK && (EPI == kEpiResidual ? true : a.mode == 0) && a.bias != nullptr;
     const bool vec_bias = !use_bias || a.bvec != 0;
     if constexpr (SPLITK) {
-        // no staging: one atomic instruction covers 32 consecutive floats of a row
+        // no staging: one store instruction covers 32 consecutive floats of a row
 #pragma unroll
         for (int fn = 0; fn < FN; ++fn) {
             const uint32_t n = nw + 32 * fn + l32;
@@ -184,7 +187,7 @@ __device__ __forceinline__ void store_tiles(const GemmArgs& a, float* C, float* 
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const uint32_t m = mw + 32 * fm + 8 * (r >> 2) + 4 * g + (r & 3);
-                    if (m < a.M) unsafeAtomicAdd(C + static_cast<uint64_t>(m) * a.ldc + n, acc[fm][fn][r]);  // native global_atomic_add_f32
+                    if (m < a.M) C[static_cast<uint64_t>(m) * a.ldc + n] = acc[fm][fn][r];
                 }
         }
         return;
@@ -629,7 +632,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     }
     if (j < n_steps) compute(S0{});
 
-    float* C = a.C + static_cast<uint64_t>(blockIdx.z) * a.sC;
+    float* C = a.C + static_cast<uint64_t>(blockIdx.z) * a.sC + (SPLITK ? blockIdx.y * a.split_stride : 0);
     __syncthreads();  // every wave is done with the operand tiles before LDS is reused
     const int wm_s = kFreshLane ? wave_s % WM : wm, wn_s = kFreshLane ? wave_s / WM : wn;
     store_tiles<FM, FN, SPLITK, EPI>(a, C, reinterpret_cast<float*>(smem) + wave_s * kStageFloats, m0 + wm_s * TM,
@@ -963,103 +966,101 @@ __global__ __launch_bounds__(256) void gemm_q8_rows_kernel(GemmArgs a) {
         for (int fn = 0; fn < FN; ++fn) mfma1(P0{}, 1, fn, wf[fn]);
     }
 
-    float* C = a.C + static_cast<uint64_t>(blockIdx.z) * a.sC;
+    float* C = a.C + static_cast<uint64_t>(blockIdx.z) * a.sC + (SPLITK ? blockIdx.y * a.split_stride : 0);
     __syncthreads();  // every wave is done with the W tiles before LDS is reused
     store_tiles<FM, FN, SPLITK, EPI>(a, C, reinterpret_cast<float*>(smem) + wave * kStageFloats, m0 + 64 * wave, n0,
                                      acc, lane);
 }
 
-// C[m, n] = bias[n] (or 0) for the split-K accumulation (mode 0 only).
-__global__ __launch_bounds__(256) void gemm_init_kernel(float* C, const float* bias, uint32_t M, uint32_t N,
-                                                        uint32_t ldc, uint64_t sC) {
+// K == 0: C[m, n] = bias[n] (or 0) in mode 0, C[m, n] += bias[n] in mode 2.
+__global__ __launch_bounds__(256) void gemm_fill_kernel(float* C, const float* bias, uint32_t M, uint32_t N,
+                                                        uint32_t ldc, uint64_t sC, uint32_t add) {
     const uint32_t n = blockIdx.x * 256 + threadIdx.x;
     if (n >= N) return;
     const float v = bias ? bias[n] : 0.0f;
     float* c = C + static_cast<uint64_t>(blockIdx.z) * sC + n;
-    for (uint32_t m = blockIdx.y; m < M; m += gridDim.y) c[static_cast<uint64_t>(m) * ldc] = v;
+    for (uint32_t m = blockIdx.y; m < M; m += gridDim.y) {
+        float* p = c + static_cast<uint64_t>(m) * ldc;
+        *p = add ? *p + v : v;
+    }
 }
 
-// The same fill with one 16-byte store per work-item step, grid-stride over
-// the flattened [M, N / 4] index of each batch item (blockIdx.y): for C rows
-// that are 16-byte aligned with N % 4 == 0. A few hundred workgroups instead of
-// one per (256 columns, row).
-__global__ __launch_bounds__(256) void gemm_init_vec_kernel(float* C, const float* bias, uint32_t M, uint32_t N4,
-                                                            uint32_t ldc, uint64_t sC, uint32_t bvec) {
+void launch_fill(float* C, const float* bias, uint32_t M, uint32_t N, uint32_t ldc, uint64_t sC, uint32_t batch,
+                 bool add, hipStream_t s) {
+    gemm_fill_kernel<<<dim3(ceil_div(N, 256), std::min<uint32_t>(M, 4096), batch), 256, 0, s>>>(C, bias, M, N, ldc,
+                                                                                                sC, add ? 1u : 0u);
+}
+
+// The K splits' partial planes P[z][s] ([M, N], row stride N, `plane` floats
+// apart; batch item z's planes start at z * splits * plane) are added in split
+// order -- ((P0 + P1) + P2) + ... -- so the sum never depends on timing:
+//   OP 0: C = sum + bias[n]   (mode 0; bias may be NULL)
+//   OP 1: C = C + sum         (mode 1)
+//   OP 2: C = C + (sum + bias[n])   (mode 2, the residual epilogue)
+// VEC: 16-byte accesses over the flattened [M, N / 4] index (N % 4 == 0, C rows
+// 16-byte aligned); a capped grid strides over the tile.
+template <int OP, bool VEC>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* P, uint64_t plane, uint32_t splits, float* C,
+                                                            const float* bias, uint32_t M, uint32_t N, uint32_t ldc,
+                                                            uint64_t sC, uint32_t bvec) {
+    const float* p = P + static_cast<uint64_t>(blockIdx.y) * splits * plane;
     float* c = C + static_cast<uint64_t>(blockIdx.y) * sC;
-    const uint64_t total = static_cast<uint64_t>(M) * N4;
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * 256;
-    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x; i < total; i += stride) {
-        const uint32_t m = static_cast<uint32_t>(i / N4), n = static_cast<uint32_t>(i % N4) * 4;
-        floatx4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (bias) v = bvec ? *reinterpret_cast<const floatx4*>(bias + n)
-                           : floatx4{bias[n], bias[n + 1], bias[n + 2], bias[n + 3]};
-        *reinterpret_cast<floatx4*>(c + static_cast<uint64_t>(m) * ldc + n) = v;
+    if constexpr (VEC) {
+        const uint32_t N4 = N / 4;
+        const uint64_t total = static_cast<uint64_t>(M) * N4;
+        for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x; i < total; i += stride) {
+            const uint32_t m = static_cast<uint32_t>(i / N4), n = static_cast<uint32_t>(i % N4) * 4;
+            const float* q = p + static_cast<uint64_t>(m) * N + n;
+            floatx4 v = *reinterpret_cast<const floatx4*>(q);
+            for (uint32_t sp = 1; sp < splits; ++sp) v += *reinterpret_cast<const floatx4*>(q + sp * plane);
+            floatx4 b = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (OP != 1 && bias)
+                b = bvec ? *reinterpret_cast<const floatx4*>(bias + n)
+                         : floatx4{bias[n], bias[n + 1], bias[n + 2], bias[n + 3]};
+            floatx4* o = reinterpret_cast<floatx4*>(c + static_cast<uint64_t>(m) * ldc + n);
+            if (OP == 0) *o = bias ? v + b : v;
+            else if (OP == 1) *o = *o + v;
+            else *o = *o + (bias ? v + b : v);
+        }
+    } else {
+        const uint64_t total = static_cast<uint64_t>(M) * N;
+        for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x; i < total; i += stride) {
+            const uint32_t m = static_cast<uint32_t>(i / N), n = static_cast<uint32_t>(i % N);
+            const float* q = p + i;
+            float v = *q;
+            for (uint32_t sp = 1; sp < splits; ++sp) v += q[sp * plane];
+            const float b = (OP != 1 && bias) ? bias[n] : 0.0f;
+            float* o = c + static_cast<uint64_t>(m) * ldc + n;
+            if (OP == 0) *o = bias ? v + b : v;
+            else if (OP == 1) *o = *o + v;
+            else *o = *o + (bias ? v + b : v);
+        }
     }
 }
 
-void launch_init(float* C, const float* bias, uint32_t M, uint32_t N, uint32_t ldc, uint64_t sC, uint32_t batch,
-                 hipStream_t s) {
-    if (reinterpret_cast<uintptr_t>(C) % 16 == 0 && N % 4 == 0 && ldc % 4 == 0 && sC % 4 == 0 && batch <= 65535) {
-        const uint64_t n4 = static_cast<uint64_t>(M) * (N / 4);
-        const unsigned gx = static_cast<unsigned>(std::min<uint64_t>(std::max<uint64_t>(ceil_div(n4, 256ull), 1), 1024));
-        gemm_init_vec_kernel<<<dim3(gx, batch), 256, 0, s>>>(C, bias, M, N / 4, ldc, sC,
-                                                             reinterpret_cast<uintptr_t>(bias) % 16 == 0 ? 1u : 0u);
-        return;
-    }
-    gemm_init_kernel<<<dim3(ceil_div(N, 256), std::min<uint32_t>(M, 4096), batch), 256, 0, s>>>(C, bias, M, N, ldc, sC);
+template <int OP>
+void launch_reduce_op(const float* P, uint64_t plane, uint32_t splits, float* C, const float* bias, uint32_t M,
+                      uint32_t N, uint32_t ldc, uint64_t sC, uint32_t batch, hipStream_t s) {
+    const bool vec = reinterpret_cast<uintptr_t>(C) % 16 == 0 && N % 4 == 0 && ldc % 4 == 0 && sC % 4 == 0;
+    const uint64_t units = static_cast<uint64_t>(M) * (vec ? N / 4 : N);
+    const unsigned gx = static_cast<unsigned>(std::min<uint64_t>(std::max<uint64_t>(ceil_div(units, 256ull), 1), 1024));
+    const uint32_t bvec = reinterpret_cast<uintptr_t>(bias) % 16 == 0 ? 1u : 0u;
+    if (vec) splitk_reduce_kernel<OP, true><<<dim3(gx, batch), 256, 0, s>>>(P, plane, splits, C, bias, M, N, ldc, sC, bvec);
+    else splitk_reduce_kernel<OP, false><<<dim3(gx, batch), 256, 0, s>>>(P, plane, splits, C, bias, M, N, ldc, sC, bvec);
 }
 
-// C[m, n] += bias[n]: the bias of a residual-epilogue GEMM whose K splits add
-// their partial products with atomics.
-__global__ __launch_bounds__(256) void gemm_bias_add_kernel(float* C, const float* bias, uint32_t M, uint32_t N,
-                                                            uint32_t ldc, uint64_t sC) {
-    const uint32_t n = blockIdx.x * 256 + threadIdx.x;
-    if (n >= N) return;
-    const float v = bias[n];
-    float* c = C + static_cast<uint64_t>(blockIdx.z) * sC + n;
-    for (uint32_t m = blockIdx.y; m < M; m += gridDim.y) c[static_cast<uint64_t>(m) * ldc] += v;
+}  // namespace
+
+void launch_splitk_reduce(const float* P, uint32_t splits, float* C, const float* bias, uint32_t M, uint32_t N,
+                          uint32_t ldc, uint64_t sC, uint32_t batch, int op, hipStream_t s) {
+    const uint64_t plane = static_cast<uint64_t>(M) * N;
+    if (op == 0) launch_reduce_op<0>(P, plane, splits, C, bias, M, N, ldc, sC, batch, s);
+    else if (op == 1) launch_reduce_op<1>(P, plane, splits, C, bias, M, N, ldc, sC, batch, s);
+    else launch_reduce_op<2>(P, plane, splits, C, bias, M, N, ldc, sC, batch, s);
 }
 
-// The same add with 16-byte accesses over the flattened [M, N / 4] index (rows
-// 16-byte aligned, N % 4 == 0).
-__global__ __launch_bounds__(256) void gemm_bias_add_vec_kernel(float* C, const float* bias, uint32_t M, uint32_t N4,
-                                                                uint32_t ldc, uint64_t sC, uint32_t bvec) {
-    float* c = C + static_cast<uint64_t>(blockIdx.y) * sC;
-    const uint64_t total = static_cast<uint64_t>(M) * N4;
-    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * 256;
-    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x; i < total; i += stride) {
-        const uint32_t m = static_cast<uint32_t>(i / N4), n = static_cast<uint32_t>(i % N4) * 4;
-        const floatx4 b = bvec ? *reinterpret_cast<const floatx4*>(bias + n)
-                               : floatx4{bias[n], bias[n + 1], bias[n + 2], bias[n + 3]};
-        floatx4* p = reinterpret_cast<floatx4*>(c + static_cast<uint64_t>(m) * ldc + n);
-        const floatx4 x = *p;
-        *p = floatx4{x[0] + b[0], x[1] + b[1], x[2] + b[2], x[3] + b[3]};
-    }
-}
-
-void launch_bias_add(float* C, const float* bias, uint32_t M, uint32_t N, uint32_t ldc, uint64_t sC, uint32_t batch,
-                     hipStream_t s) {
-    if (reinterpret_cast<uintptr_t>(C) % 16 == 0 && N % 4 == 0 && ldc % 4 == 0 && sC % 4 == 0 && batch <= 65535) {
-        const uint64_t n4 = static_cast<uint64_t>(M) * (N / 4);
-        const unsigned gx = static_cast<unsigned>(std::min<uint64_t>(std::max<uint64_t>(ceil_div(n4, 256ull), 1), 1024));
-        gemm_bias_add_vec_kernel<<<dim3(gx, batch), 256, 0, s>>>(C, bias, M, N / 4, ldc, sC,
-                                                                 reinterpret_cast<uintptr_t>(bias) % 16 == 0 ? 1u : 0u);
-        return;
-    }
-    gemm_bias_add_kernel<<<dim3(ceil_div(N, 256), std::min<uint32_t>(M, 4096), batch), 256, 0, s>>>(C, bias, M, N,
-                                                                                                     ldc, sC);
-}
-
-// Before the K splits add into C: mode 0 writes bias (or 0), the residual
-// epilogue adds bias once, mode 1 leaves C as it is.
-template <int EPI>
-void prepare_split(const GemmArgs& a, uint32_t batch, hipStream_t s) {
-    if (EPI == kEpiResidual) {
-        if (a.bias) launch_bias_add(a.C, a.bias, a.M, a.N, a.ldc, a.sC, batch, s);
-    } else if (a.mode == 0) {
-        launch_init(a.C, a.bias, a.M, a.N, a.ldc, a.sC, batch, s);
-    }
-}
+namespace {
 
 // ---- configurations -------------------------------------------------------------
 
@@ -1125,14 +1126,33 @@ uint32_t pick_group(uint32_t tm, uint32_t tn, uint32_t BM, uint32_t BN, uint32_t
     return best;
 }
 
+// The partial planes of a K split: the kernel's C becomes the workspace
+// (row stride N, split planes M * N apart, batch items splits planes apart).
+GemmArgs partial_args(const GemmArgs& a, uint32_t splits, float* ws) {
+    GemmArgs p = a;
+    p.C = ws;
+    p.ldc = a.N;
+    p.split_stride = static_cast<uint64_t>(a.M) * a.N;
+    p.sC = p.split_stride * splits;
+    return p;
+}
+
+// Adds the partial planes into C in split order (reduce op from the epilogue / mode).
+template <int EPI>
+void finish_split(const GemmArgs& a, uint32_t splits, const float* ws, uint32_t batch, hipStream_t s) {
+    const int op = EPI == kEpiResidual ? 2 : a.mode == 0 ? 0 : 1;
+    launch_splitk_reduce(ws, splits, a.C, a.bias, a.M, a.N, a.ldc, a.sC, batch, op, s);
+}
+
 // SPLIT = false: a build without a K-split variant (requested splits are ignored).
+// splits > 1 needs ws: batch * splits * M * N floats (split_workspace_floats).
 template <int BM, int BN, int WM, int WN, int KB, int WK, bool KTAIL, int PF = 2, int EPI = kEpiPlain,
           bool SPLIT = true>
-void launch_cfg(const GemmArgs& a0, uint32_t batch, uint32_t splits, hipStream_t s) {
+void launch_cfg(const GemmArgs& a0, uint32_t batch, uint32_t splits, float* ws, hipStream_t s) {
     GemmArgs a = a0;
     // GEGLU: BN / 2 outputs per tile, and the epilogue needs the whole K sum
     a.tiles_n = EPI == kEpiGeglu ? ceil_div(a.F, BN / 2) : ceil_div(a.N, BN);
-    if (EPI == kEpiGeglu || !SPLIT) splits = 1;
+    if (EPI == kEpiGeglu || !SPLIT || !ws) splits = 1;
     a.tiles_m = ceil_div(a.M, BM);
     a.group_m = pick_group(a.tiles_m, a.tiles_n, BM, BN, a.K);
     a.ksteps = ceil_div(a.K, 32 * KB);
@@ -1142,9 +1162,11 @@ void launch_cfg(const GemmArgs& a0, uint32_t batch, uint32_t splits, hipStream_t
         splits = ceil_div(a.ksteps, a.steps_per_split);
     }
     if (splits > 1) {
-        prepare_split<EPI>(a, batch, s);
-        if constexpr (EPI != kEpiGeglu && SPLIT)
-            gemm_q8_kernel<BM, BN, WM, WN, KB, WK, true, KTAIL, PF><<<dim3(tiles, splits, batch), WM * WN * 64, 0, s>>>(a);
+        if constexpr (EPI != kEpiGeglu && SPLIT) {
+            const GemmArgs p = partial_args(a, splits, ws);
+            gemm_q8_kernel<BM, BN, WM, WN, KB, WK, true, KTAIL, PF><<<dim3(tiles, splits, batch), WM * WN * 64, 0, s>>>(p);
+            finish_split<EPI>(a, splits, ws, batch, s);
+        }
     } else {
         a.steps_per_split = a.ksteps;
         gemm_q8_kernel<BM, BN, WM, WN, KB, WK, false, KTAIL, PF, EPI><<<dim3(tiles, 1, batch), WM * WN * 64, 0, s>>>(a);
@@ -1154,11 +1176,11 @@ void launch_cfg(const GemmArgs& a0, uint32_t batch, uint32_t splits, hipStream_t
 // Row-stationary kernel: 256 x (32 FN) tiles, K % 32 == 0. A K split covers an
 // even number of 32-wide steps.
 template <int FN, int WK, bool AQ = false, int EPI = kEpiPlain>
-void launch_rows(const GemmArgs& a0, uint32_t batch, uint32_t splits, hipStream_t s) {
+void launch_rows(const GemmArgs& a0, uint32_t batch, uint32_t splits, float* ws, hipStream_t s) {
     GemmArgs a = a0;
     constexpr uint32_t BM = 256, BN = 32 * FN;
     a.tiles_n = EPI == kEpiGeglu ? ceil_div(a.F, BN / 2) : ceil_div(a.N, BN);
-    if (EPI == kEpiGeglu) splits = 1;
+    if (EPI == kEpiGeglu || !ws) splits = 1;
     a.tiles_m = ceil_div(a.M, BM);
     a.group_m = pick_group(a.tiles_m, a.tiles_n, BM, BN, a.K);
     a.ksteps = a.K / 32;
@@ -1168,9 +1190,11 @@ void launch_rows(const GemmArgs& a0, uint32_t batch, uint32_t splits, hipStream_
         splits = ceil_div(a.ksteps, a.steps_per_split);
     }
     if (splits > 1) {
-        prepare_split<EPI>(a, batch, s);
-        if constexpr (EPI != kEpiGeglu)
-            gemm_q8_rows_kernel<FN, WK, true, AQ><<<dim3(tiles, splits, batch), 256, 0, s>>>(a);
+        if constexpr (EPI != kEpiGeglu) {
+            const GemmArgs p = partial_args(a, splits, ws);
+            gemm_q8_rows_kernel<FN, WK, true, AQ><<<dim3(tiles, splits, batch), 256, 0, s>>>(p);
+            finish_split<EPI>(a, splits, ws, batch, s);
+        }
     } else {
         a.steps_per_split = a.ksteps;
         gemm_q8_rows_kernel<FN, WK, false, AQ, EPI><<<dim3(tiles, 1, batch), 256, 0, s>>>(a);
@@ -1178,25 +1202,25 @@ void launch_rows(const GemmArgs& a0, uint32_t batch, uint32_t splits, hipStream_
 }
 
 template <int WK, int EPI = kEpiPlain>
-void launch(int cfg, const GemmArgs& a, uint32_t batch, uint32_t splits, hipStream_t s) {
+void launch(int cfg, const GemmArgs& a, uint32_t batch, uint32_t splits, float* ws, hipStream_t s) {
     switch (cfg) {
-        case kR256x256: launch_rows<8, WK, false, EPI>(a, batch, splits, s); break;
-        case kR256x256Q: launch_rows<8, WK, true, EPI>(a, batch, splits, s); break;
-        case kR256x192Q: launch_rows<6, WK, true, EPI>(a, batch, splits, s); break;
-        case kR256x160Q: launch_rows<5, WK, true, EPI>(a, batch, splits, s); break;
-        case kR256x128Q: launch_rows<4, WK, true, EPI>(a, batch, splits, s); break;
-        case kR256x128: launch_rows<4, WK, false, EPI>(a, batch, splits, s); break;
-        case kC256x128: launch_cfg<256, 128, 4, 2, 2, WK, false, 2, EPI>(a, batch, splits, s); break;
-        case kC128x128: launch_cfg<128, 128, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, s); break;
-        case kC256x128W4: launch_cfg<256, 128, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, s); break;
-        case kC192x256: launch_cfg<192, 256, 2, 4, 2, WK, false, 2, EPI>(a, batch, splits, s); break;
-        case kC128x256W4: launch_cfg<128, 256, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, s); break;
+        case kR256x256: launch_rows<8, WK, false, EPI>(a, batch, splits, ws, s); break;
+        case kR256x256Q: launch_rows<8, WK, true, EPI>(a, batch, splits, ws, s); break;
+        case kR256x192Q: launch_rows<6, WK, true, EPI>(a, batch, splits, ws, s); break;
+        case kR256x160Q: launch_rows<5, WK, true, EPI>(a, batch, splits, ws, s); break;
+        case kR256x128Q: launch_rows<4, WK, true, EPI>(a, batch, splits, ws, s); break;
+        case kR256x128: launch_rows<4, WK, false, EPI>(a, batch, splits, ws, s); break;
+        case kC256x128: launch_cfg<256, 128, 4, 2, 2, WK, false, 2, EPI>(a, batch, splits, ws, s); break;
+        case kC128x128: launch_cfg<128, 128, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, ws, s); break;
+        case kC256x128W4: launch_cfg<256, 128, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, ws, s); break;
+        case kC192x256: launch_cfg<192, 256, 2, 4, 2, WK, false, 2, EPI>(a, batch, splits, ws, s); break;
+        case kC128x256W4: launch_cfg<128, 256, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, ws, s); break;
         case kC256x256W4:
             // one wave per SIMD with 128 x 128 per wave (256 accumulator AGPRs)
             // and one register set; its K-split build would spill in the loop
-            launch_cfg<256, 256, 2, 2, 2, WK, false, 1, EPI, false>(a, batch, splits, s);
+            launch_cfg<256, 256, 2, 2, 2, WK, false, 1, EPI, false>(a, batch, splits, ws, s);
             break;
-        case kC128x64: launch_cfg<128, 64, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, s); break;
+        case kC128x64: launch_cfg<128, 64, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, ws, s); break;
         case kC256x256:
             // The split layout's and the GEGLU epilogue's 256x256 builds need
             // more than the 256 VGPRs of a wave at two waves per SIMD: the
@@ -1204,76 +1228,155 @@ void launch(int cfg, const GemmArgs& a, uint32_t batch, uint32_t splits, hipStre
             // scratch reload waits for all global loads in flight. They run
             // 256x128 tiles instead.
             if constexpr (WK == kSplit || EPI == kEpiGeglu)
-                launch_cfg<256, 128, 4, 2, 2, WK, false, 2, EPI>(a, batch, splits, s);
+                launch_cfg<256, 128, 4, 2, 2, WK, false, 2, EPI>(a, batch, splits, ws, s);
             else
-                launch_cfg<256, 256, 4, 2, 2, WK, false, 1, EPI>(a, batch, splits, s);
+                launch_cfg<256, 256, 4, 2, 2, WK, false, 1, EPI>(a, batch, splits, ws, s);
             break;
-        default: launch_cfg<64, 64, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, s); break;
+        default: launch_cfg<64, 64, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, ws, s); break;
     }
 }
 
 // General K (K % 64 != 0): one block column per step, 64x64 tiles; the split
 // layout with K % 32 != 0 also zero-fills the partial last step.
 template <int WK, int EPI = kEpiPlain>
-void launch_general(const GemmArgs& a, uint32_t batch, uint32_t splits, hipStream_t s) {
-    if (a.K % 32 == 0) launch_cfg<64, 64, 2, 2, 1, WK, false, 2, EPI>(a, batch, splits, s);
-    else launch_cfg<64, 64, 2, 2, 1, WK, true, 2, EPI>(a, batch, splits, s);
+void launch_general(const GemmArgs& a, uint32_t batch, uint32_t splits, float* ws, hipStream_t s) {
+    if (a.K % 32 == 0) launch_cfg<64, 64, 2, 2, 1, WK, false, 2, EPI>(a, batch, splits, ws, s);
+    else launch_cfg<64, 64, 2, 2, 1, WK, true, 2, EPI>(a, batch, splits, ws, s);
 }
 
 constexpr int kCUs = 256;
 
-// Picks the tile and K split for a shape (rules from sweeps of every tile on
-// MI355X over the SDXL shapes): 256x256 tiles for tall grids that nearly fill
-// the CUs; 128x128 (two workgroups per CU) for wide grids with few row
-// panels; 256x128 once that gives half a wave of workgroups; long-K shapes
-// with fewer tiles split K in two; 64x64 when that alone fills the CUs twice;
-// smaller grids split K on 64x64 tiles until ~256 workgroups are resident.
-void choose(uint32_t M, uint32_t N, uint32_t K, uint32_t batch, int& cfg, uint32_t& splits) {
+struct Plan {
+    int cfg;
+    uint32_t splits;
+};
+
+// Picks the tile and K split for a shape (rules from per-shape sweeps of every
+// tile build on MI355X over the SDXL shapes): the 192x256 tile (8 waves, one
+// workgroup per CU) where it yields a wave or more of long-K tiles; 128x128
+// (4 waves, two workgroups per CU) for mid-size grids; 64x64 for the rest.
+// With a workspace (allow_split), long-K 128x128 grids below one wave split
+// K in two and small 64x64 grids split K until ~256 workgroups run.
+Plan choose(uint32_t M, uint32_t N, uint32_t K, uint32_t batch, bool allow_split) {
+    Plan p{kC64x64, 1};
     const char* env = std::getenv("MI_GEMM_CFG");  // "<cfg>[:<splits>]" overrides (tuning sweeps)
     if (env && *env) {
-        cfg = std::atoi(env);
+        p.cfg = std::atoi(env);
         const char* c = std::strchr(env, ':');
-        splits = c ? static_cast<uint32_t>(std::atoi(c + 1)) : 1u;
-        if (cfg < 0 || cfg >= kNumCfg) cfg = kC64x64;
-        if (splits < 1) splits = 1;
-        return;
+        p.splits = c ? static_cast<uint32_t>(std::atoi(c + 1)) : 1u;
+        if (p.cfg < 0 || p.cfg >= kNumCfg) p.cfg = kC64x64;
+        if (p.splits < 1 || !allow_split) p.splits = 1;
+        return p;
     }
     auto tiles = [&](uint32_t bm, uint32_t bn) {
         return static_cast<uint64_t>(ceil_div(M, bm)) * ceil_div(N, bn) * batch;
     };
-    const uint64_t tsq = tiles(256, 256), t128 = tiles(128, 128), t256 = tiles(256, 128), t64 = tiles(64, 64);
-    splits = 1;
-    if (tsq >= 160 && M >= 4096 && K <= 2048) {
-        cfg = kC256x256;
-    } else if (t128 >= 4 * kCUs && K <= 2048) {
-        cfg = kC128x128;
-    } else if (t256 >= kCUs / 2) {
-        cfg = kC256x128;
-    } else if (K >= 4096 && t256 * 2 >= kCUs / 2) {
-        cfg = kC256x128;
-        splits = 2;
-    } else if (t64 >= 2 * kCUs) {
-        cfg = kC64x64;
+    const uint64_t t192 = tiles(192, 256), t128 = tiles(128, 128), t64 = tiles(64, 64);
+    if (t192 >= 120 && K >= 1280) {
+        p.cfg = kC192x256;
+    } else if (t128 >= 160) {
+        p.cfg = kC128x128;
+        if (allow_split && t128 < kCUs && K >= 4096) p.splits = 2;
     } else {
-        cfg = kC64x64;
-        const uint64_t want = (kCUs + t64 - 1) / t64;
-        uint32_t s = 1;
-        while (s * 2 <= want && s * 2 * 128 <= K) s *= 2;
-        splits = s;
+        p.cfg = kC64x64;
+        if (allow_split && t64 < 2 * kCUs) {
+            const uint64_t want = (kCUs + t64 - 1) / t64;
+            uint32_t sp = 1;
+            while (sp * 2 <= want && sp * 2 * 128 <= K) sp *= 2;
+            p.splits = sp;
+        }
     }
+    return p;
+}
+
+// Floats of workspace a K-split plan uses: one [M, N] partial plane per split
+// and batch item.
+uint64_t split_floats(uint32_t M, uint32_t N, uint32_t batch, uint32_t splits) {
+    return splits > 1 ? static_cast<uint64_t>(batch) * splits * M * N : 0;
+}
+
+// The plan for a call: a split plan only when the caller's workspace holds
+// its partials, else the best plan without a split.
+Plan plan_for(uint32_t M, uint32_t N, uint32_t K, uint32_t batch, const void* ws, uint64_t ws_bytes) {
+    Plan p = choose(M, N, K, batch, ws != nullptr);
+    if (p.splits > 1 && split_floats(M, N, batch, p.splits) * 4 > ws_bytes) p = choose(M, N, K, batch, false);
+    return p;
 }
 
 template <int WK, int EPI = kEpiPlain>
-void dispatch(const GemmArgs& a, uint32_t batch, hipStream_t s) {
-    int cfg;
-    uint32_t splits;
-    choose(a.M, a.N, a.K, batch, cfg, splits);  // GEGLU: N = 2F weight rows, the same MFMA work
-    if (a.K % 64 != 0) launch_general<WK, EPI>(a, batch, splits, s);
-    else launch<WK, EPI>(cfg, a, batch, splits, s);
+void dispatch(const GemmArgs& a, uint32_t batch, const Plan& p, float* ws, hipStream_t s) {
+    if (a.K % 64 != 0) launch_general<WK, EPI>(a, batch, p.splits, ws, s);
+    else launch<WK, EPI>(p.cfg, a, batch, p.splits, ws, s);
 }
 
+// ---- any-K kernel (split layout) ---------------------------------------------------
+//
+// The reference's scalar gemm_nt_q8 accepts any K and any row stride
+// (gemm_nt_q8.comp:52-80 stages element by element with bounds checks). Shapes
+// the tiled kernels do not take (K % 4 != 0, lda or sA not a multiple of 4, A
+// not 16-byte aligned) run here: 64 x 64 tiles, four waves of one 32 x 32 MFMA
+// tile, 32 k per step, every element staged with its own bounds check
+// (zero past K). The arithmetic is the tiled kernels': A rounded to fp16, the
+// weight fp16(q * s), fp32 MFMA sums.
+__global__ __launch_bounds__(256) void gemm_q8_any_kernel(GemmArgs a) {
+    constexpr int LD = 40;  // halves per staged row: 32 k + 16-byte pad
+    __shared__ __attribute__((aligned(16))) _Float16 As[64 * LD];
+    __shared__ __attribute__((aligned(16))) _Float16 Ws[64 * LD];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, g = lane >> 5;
+    const int wm = wave & 1, wn = wave >> 1;
+    const uint32_t n0 = blockIdx.x * 64, m0 = blockIdx.y * 64;
+    const float* A = a.A + static_cast<uint64_t>(blockIdx.z) * a.sA;
+    const int8_t* q = reinterpret_cast<const int8_t*>(a.W);
+    floatx16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    // this thread stages row (tid / 4) of both tiles, k = 8 (tid % 4) .. + 7
+    const uint32_t sr = tid >> 2, sk = (tid & 3) * 8;
+    const uint32_t am = min(m0 + sr, a.M - 1), wr = min(n0 + sr, a.N - 1);
+    for (uint32_t k0 = 0; k0 < a.K; k0 += 32) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t k = k0 + sk + e;
+            float av = 0.0f, wv = 0.0f;
+            if (k < a.K) {
+                av = A[static_cast<uint64_t>(am) * a.lda + k];
+                const uint64_t f = static_cast<uint64_t>(wr) * a.K + k;
+                wv = static_cast<float>(q[f]) * a.scales[f >> 5];
+            }
+            As[sr * LD + sk + e] = static_cast<_Float16>(av);
+            Ws[sr * LD + sk + e] = static_cast<_Float16>(wv);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int sl = 0; sl < 2; ++sl) {
+            const half8 af = *reinterpret_cast<const half8*>(&As[(wm * 32 + l32) * LD + 16 * sl + 8 * g]);
+            const half8 bf = *reinterpret_cast<const half8*>(&Ws[(wn * 32 + l32) * LD + 16 * sl + 8 * g]);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, acc, 0, 0, 0);
+        }
+        __syncthreads();
+    }
+    // lane holds column n = l32 and rows 8 (r / 4) + 4 g + r % 4 of the wave's tile
+    const uint32_t n = n0 + wn * 32 + l32;
+    if (n >= a.N) return;
+    float* C = a.C + static_cast<uint64_t>(blockIdx.z) * a.sC;
+    const float b = a.bias ? a.bias[n] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const uint32_t m = m0 + wm * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+        if (m >= a.M) continue;
+        float* c = C + static_cast<uint64_t>(m) * a.ldc + n;
+        if (a.mode == 0) *c = a.bias ? acc[r] + b : acc[r];
+        else if (a.mode == 1) *c = *c + acc[r];
+        else *c = *c + (a.bias ? acc[r] + b : acc[r]);
+    }
+}
+
+// vec_a: the tiled kernels' A path (16-byte loads) -- A 16-byte aligned, lda
+// and sA multiples of 4; otherwise A only needs 4-byte alignment (the any-K
+// kernel of the split layout).
 int validate(const char* fn, const float* A, const void* W, const float* C, uint32_t M, uint32_t N, uint32_t K,
-             uint32_t mode, uint32_t& lda, uint32_t& ldc, uint32_t batch, uint64_t sA, uint64_t sC) {
+             uint32_t mode, uint32_t& lda, uint32_t& ldc, uint32_t batch, uint64_t sA, uint64_t sC, bool vec_a) {
     if (!A || !W || !C) return fail(MI_ERR_INVALID_ARG, "%s: null pointer", fn);
     if (mode > 2)
         return fail(MI_ERR_INVALID_ARG, "%s: mode %u (0 = store, 1 = accumulate, 2 = accumulate + bias)", fn, mode);
@@ -1282,7 +1385,9 @@ int validate(const char* fn, const float* A, const void* W, const float* C, uint
     if (lda == 0) lda = K;
     if (ldc == 0) ldc = N;
     if (lda < K || ldc < N) return fail(MI_ERR_INVALID_ARG, "%s: lda %u < K %u or ldc %u < N %u", fn, lda, K, ldc, N);
-    if (!aligned(A, 16) || lda % 4 || sA % 4) return fail(MI_ERR_ALIGNMENT, "%s: A must be 16-byte aligned, lda and sA multiples of 4", fn);
+    if (vec_a && (!aligned(A, 16) || lda % 4 || sA % 4))
+        return fail(MI_ERR_ALIGNMENT, "%s: A must be 16-byte aligned, lda and sA multiples of 4", fn);
+    if (!aligned(A, 4)) return fail(MI_ERR_ALIGNMENT, "%s: A must be 4-byte aligned", fn);
     if (!aligned(C, 4)) return fail(MI_ERR_ALIGNMENT, "%s: C must be 4-byte aligned", fn);
     // per-workgroup A offsets are 32-bit: a 256-row panel must stay below 4 GiB
     if (static_cast<uint64_t>(lda) * 4 * 256 >= (uint64_t(1) << 32))
@@ -1290,18 +1395,23 @@ int validate(const char* fn, const float* A, const void* W, const float* C, uint
     return MI_OK;
 }
 
-}  // namespace
-}  // namespace mi
+// Workspace of a *_ws call: 16-byte aligned, disjoint from every operand.
+int check_ws(const char* fn, const void* ws, uint64_t ws_bytes, const void* A, uint64_t abytes, const void* W,
+             uint64_t wbytes, const void* C, uint64_t cbytes, const float* bias, uint32_t N) {
+    if (!ws || ws_bytes == 0) return MI_OK;
+    if (!aligned(ws, 16)) return fail(MI_ERR_ALIGNMENT, "%s: workspace must be 16-byte aligned", fn);
+    if (overlaps(ws, ws_bytes, A, abytes) || overlaps(ws, ws_bytes, W, wbytes) || overlaps(ws, ws_bytes, C, cbytes) ||
+        overlaps(ws, ws_bytes, bias, uint64_t(N) * 4))
+        return fail(MI_ERR_ALIASING, "%s: workspace overlaps an operand", fn);
+    return MI_OK;
+}
 
-using namespace mi;
-
-extern "C" int mi_gemm_nt_q8_0(const float* A, const void* W, const float* bias, float* C, uint32_t M, uint32_t N,
-                               uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldc, uint32_t batch, uint64_t sA,
-                               uint64_t sC, void* stream) {
-    const char* fn = "mi_gemm_nt_q8_0";
+int gemm_blocks(const char* fn, const float* A, const void* W, const float* bias, float* C, uint32_t M, uint32_t N,
+                uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldc, uint32_t batch, uint64_t sA, uint64_t sC,
+                void* ws, uint64_t ws_bytes, hipStream_t stream) {
     if (M == 0 || N == 0) return MI_OK;
     if (K % 32) return fail(MI_ERR_UNSUPPORTED, "%s: K=%u is not a multiple of 32 (Q8_0 block)", fn, K);
-    int st = validate(fn, A, W, C, M, N, K, mode, lda, ldc, batch, sA, sC);
+    int st = validate(fn, A, W, C, M, N, K, mode, lda, ldc, batch, sA, sC, true);
     if (st) return st;
     if (!aligned(W, 16)) return fail(MI_ERR_ALIGNMENT, "%s: W must be 16-byte aligned", fn);
     const uint64_t wbytes = static_cast<uint64_t>(N) * (K / 32) * 34;
@@ -1310,25 +1420,28 @@ extern "C" int mi_gemm_nt_q8_0(const float* A, const void* W, const float* bias,
     const uint64_t abytes = (static_cast<uint64_t>(batch - 1) * sA + static_cast<uint64_t>(M - 1) * lda + K) * 4;
     if (overlaps(C, cbytes, A, abytes) || overlaps(C, cbytes, W, wbytes) || overlaps(C, cbytes, bias, uint64_t(N) * 4))
         return fail(MI_ERR_ALIASING, "%s: C overlaps an input", fn);
+    st = check_ws(fn, ws, ws_bytes, A, abytes, W, wbytes, C, cbytes, bias, N);
+    if (st) return st;
     if (K == 0) {
-        if (mode == 0) launch_init(C, bias, M, N, ldc, sC, batch, static_cast<hipStream_t>(stream));
-        if (mode == 2 && bias) launch_bias_add(C, bias, M, N, ldc, sC, batch, static_cast<hipStream_t>(stream));
+        if (mode == 0 || (mode == 2 && bias)) launch_fill(C, bias, M, N, ldc, sC, batch, mode == 2, stream);
         return check_launch(fn);
     }
     GemmArgs a = make_args(A, static_cast<const uint8_t*>(W), nullptr, bias, C, M, N, K, mode, lda, ldc, sA, sC,
                            (K / 32) * 34);
-    if (mode == 2) dispatch<kBlocks34, kEpiResidual>(a, batch, static_cast<hipStream_t>(stream));
-    else dispatch<kBlocks34>(a, batch, static_cast<hipStream_t>(stream));
+    const Plan p = plan_for(M, N, K, batch, ws, ws_bytes);
+    if (mode == 2) dispatch<kBlocks34, kEpiResidual>(a, batch, p, static_cast<float*>(ws), stream);
+    else dispatch<kBlocks34>(a, batch, p, static_cast<float*>(ws), stream);
     return check_launch(fn);
 }
 
-extern "C" int mi_gemm_nt_q8_split(const float* A, const uint32_t* payload, const float* scales, const float* bias,
-                                   float* C, uint32_t M, uint32_t N, uint32_t K, uint32_t mode, uint32_t lda,
-                                   uint32_t ldc, uint32_t batch, uint64_t sA, uint64_t sC, void* stream) {
-    const char* fn = "mi_gemm_nt_q8_split";
+int gemm_split(const char* fn, const float* A, const uint32_t* payload, const float* scales, const float* bias,
+               float* C, uint32_t M, uint32_t N, uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldc,
+               uint32_t batch, uint64_t sA, uint64_t sC, void* ws, uint64_t ws_bytes, hipStream_t stream) {
     if (M == 0 || N == 0) return MI_OK;
-    if (K % 4) return fail(MI_ERR_UNSUPPORTED, "%s: K=%u is not a multiple of 4", fn, K);
-    int st = validate(fn, A, payload, C, M, N, K, mode, lda, ldc, batch, sA, sC);
+    const uint32_t lda_e = lda ? lda : K;
+    // the tiled kernels stage A 16 bytes at a time; other shapes take the any-K kernel
+    const bool tiled = K % 4 == 0 && lda_e % 4 == 0 && sA % 4 == 0 && aligned(A, 16);
+    int st = validate(fn, A, payload, C, M, N, K, mode, lda, ldc, batch, sA, sC, false);
     if (st) return st;
     if (!scales) return fail(MI_ERR_INVALID_ARG, "%s: null scales", fn);
     if (!aligned(payload, 4) || !aligned(scales, 4)) return fail(MI_ERR_ALIGNMENT, "%s: payload/scales alignment", fn);
@@ -1339,16 +1452,62 @@ extern "C" int mi_gemm_nt_q8_split(const float* A, const uint32_t* payload, cons
     if (overlaps(C, cbytes, A, abytes) || overlaps(C, cbytes, payload, nk) ||
         overlaps(C, cbytes, scales, (nk + 31) / 32 * 4) || overlaps(C, cbytes, bias, uint64_t(N) * 4))
         return fail(MI_ERR_ALIASING, "%s: C overlaps an input", fn);
+    st = check_ws(fn, ws, ws_bytes, A, abytes, payload, nk, C, cbytes, bias, N);
+    if (st) return st;
     if (K == 0) {
-        if (mode == 0) launch_init(C, bias, M, N, ldc, sC, batch, static_cast<hipStream_t>(stream));
-        if (mode == 2 && bias) launch_bias_add(C, bias, M, N, ldc, sC, batch, static_cast<hipStream_t>(stream));
+        if (mode == 0 || (mode == 2 && bias)) launch_fill(C, bias, M, N, ldc, sC, batch, mode == 2, stream);
         return check_launch(fn);
     }
     GemmArgs a = make_args(A, reinterpret_cast<const uint8_t*>(payload), scales, bias, C, M, N, K, mode, lda, ldc, sA,
                            sC, 0);
-    if (mode == 2) dispatch<kSplit, kEpiResidual>(a, batch, static_cast<hipStream_t>(stream));
-    else dispatch<kSplit>(a, batch, static_cast<hipStream_t>(stream));
+    if (!tiled) {
+        gemm_q8_any_kernel<<<dim3(ceil_div(N, 64), ceil_div(M, 64), batch), 256, 0, stream>>>(a);
+        return check_launch(fn);
+    }
+    const Plan p = plan_for(M, N, K, batch, ws, ws_bytes);
+    if (mode == 2) dispatch<kSplit, kEpiResidual>(a, batch, p, static_cast<float*>(ws), stream);
+    else dispatch<kSplit>(a, batch, p, static_cast<float*>(ws), stream);
     return check_launch(fn);
+}
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" int mi_gemm_nt_q8_0(const float* A, const void* W, const float* bias, float* C, uint32_t M, uint32_t N,
+                               uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldc, uint32_t batch, uint64_t sA,
+                               uint64_t sC, void* stream) {
+    return gemm_blocks("mi_gemm_nt_q8_0", A, W, bias, C, M, N, K, mode, lda, ldc, batch, sA, sC, nullptr, 0,
+                       static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mi_gemm_nt_q8_0_ws(const float* A, const void* W, const float* bias, float* C, uint32_t M, uint32_t N,
+                                  uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldc, uint32_t batch, uint64_t sA,
+                                  uint64_t sC, void* workspace, uint64_t workspace_bytes, void* stream) {
+    return gemm_blocks("mi_gemm_nt_q8_0_ws", A, W, bias, C, M, N, K, mode, lda, ldc, batch, sA, sC, workspace,
+                       workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mi_gemm_nt_q8_split(const float* A, const uint32_t* payload, const float* scales, const float* bias,
+                                   float* C, uint32_t M, uint32_t N, uint32_t K, uint32_t mode, uint32_t lda,
+                                   uint32_t ldc, uint32_t batch, uint64_t sA, uint64_t sC, void* stream) {
+    return gemm_split("mi_gemm_nt_q8_split", A, payload, scales, bias, C, M, N, K, mode, lda, ldc, batch, sA, sC,
+                      nullptr, 0, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mi_gemm_nt_q8_split_ws(const float* A, const uint32_t* payload, const float* scales,
+                                      const float* bias, float* C, uint32_t M, uint32_t N, uint32_t K, uint32_t mode,
+                                      uint32_t lda, uint32_t ldc, uint32_t batch, uint64_t sA, uint64_t sC,
+                                      void* workspace, uint64_t workspace_bytes, void* stream) {
+    return gemm_split("mi_gemm_nt_q8_split_ws", A, payload, scales, bias, C, M, N, K, mode, lda, ldc, batch, sA, sC,
+                      workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" uint64_t mi_gemm_nt_q8_workspace_bytes(uint32_t M, uint32_t N, uint32_t K, uint32_t batch) {
+    if (M == 0 || N == 0 || K == 0 || batch == 0) return 0;
+    const Plan p = choose(M, N, K, batch, true);
+    return split_floats(M, N, batch, p.splits) * 4;
 }
 
 extern "C" int mi_gemm_nt_q8_0_geglu(const float* A, const void* W, const float* bias, float* G, uint32_t M, uint32_t F,
@@ -1359,7 +1518,7 @@ extern "C" int mi_gemm_nt_q8_0_geglu(const float* A, const void* W, const float*
     if (F > (1u << 30)) return fail(MI_ERR_UNSUPPORTED, "%s: F=%u too large", fn, F);
     const uint32_t N = 2 * F;
     uint32_t ldc = ldg, mode = 0;
-    int st = validate(fn, A, W, G, M, F, K, mode, lda, ldc, 1, 0, 0);
+    int st = validate(fn, A, W, G, M, F, K, mode, lda, ldc, 1, 0, 0, true);
     if (st) return st;
     if (!aligned(W, 16)) return fail(MI_ERR_ALIGNMENT, "%s: W must be 16-byte aligned", fn);
     const uint64_t wbytes = static_cast<uint64_t>(N) * (K / 32) * 34;
@@ -1371,6 +1530,7 @@ extern "C" int mi_gemm_nt_q8_0_geglu(const float* A, const void* W, const float*
     GemmArgs a = make_args(A, static_cast<const uint8_t*>(W), nullptr, bias, G, M, N, K, 0, lda, ldc, 0, 0,
                            (K / 32) * 34);
     a.F = F;
-    dispatch<kBlocks34, kEpiGeglu>(a, 1, static_cast<hipStream_t>(stream));
+    // the GEGLU epilogue needs the whole K sum: never split
+    dispatch<kBlocks34, kEpiGeglu>(a, 1, plan_for(M, N, K, 1, nullptr, 0), nullptr, static_cast<hipStream_t>(stream));
     return check_launch(fn);
 }

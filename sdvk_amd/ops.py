@@ -28,11 +28,13 @@ from dataclasses import dataclass
 from typing import Optional, Sequence
 
 from . import _lib
-from ._lib import MI_F16, MI_F32, MiAttnArgs, MiBlockDims, MiBlockWeights, MiError, call, ptr
+from ._lib import (MI_BLOCK_FUSED_EPILOGUES, MI_BLOCK_JOINT_QKV, MI_F16, MI_F32, MiAttnArgs, MiBlockDims,
+                   MiBlockWeights, MiError, call, ptr)
 
 __all__ = [
-    "MiError", "MI_F32", "MI_F16", "FusedAttnArgs", "fused_attn_supported", "fused_attention",
+    "MiError", "MI_F32", "MI_F16", "MI_BLOCK_FUSED_EPILOGUES", "MI_BLOCK_JOINT_QKV", "FusedAttnArgs", "fused_attn_supported", "fused_attention",
     "fused_attention_ex", "gemm_nt_q8", "gemm_nt_q8_bias", "gemm_nt_q8_0", "gemm_nt_q8_0_geglu", "gemm_nn_q8",
+    "gemm_workspace_bytes", "gemm_nn_workspace_bytes",
     "q8_0_dequant",
     "q8_split_dequant", "q8_0_to_split", "q8_0_quantize", "Pg", "dispatch", "KERNELS", "layernorm", "geglu", "add2",
     "BlockWeights", "BlockDims", "block_workspace_bytes", "sdxl_block_forward", "block_ctx_kv_bytes", "block_ctx_kv",
@@ -89,9 +91,28 @@ def fused_attention_ex(q, k, v, out, *, batch: int, Tq: int, Tk: int, C: int, he
 
 # ------------------------------------------------------------------------ GEMM --
 
+def _ws(workspace):
+    """(pointer, bytes) of an optional workspace buffer."""
+    return (ptr(workspace), getattr(workspace, "nbytes", 0)) if workspace is not None else (None, 0)
+
+
+def gemm_workspace_bytes(M: int, N: int, K: int, batch: int = 1) -> int:
+    """Workspace the *_ws NT GEMM entries use for this shape's K-split plan (0: no split)."""
+    return int(_lib.load().mi_gemm_nt_q8_workspace_bytes(M, N, K, batch))
+
+
+def gemm_nn_workspace_bytes(M: int, N: int, K: int, batch: int = 1) -> int:
+    """Workspace mi_gemm_nn_q8_split_ws uses for this shape's K-split plan (0: no split)."""
+    return int(_lib.load().mi_gemm_nn_q8_workspace_bytes(M, N, K, batch))
+
+
 def gemm_nt_q8(A, Bq, C, Bs, M: int, N: int, K: int, *, mode: int = 0, lda: int = 0, ldc: int = 0,
-               batch: int = 1, sA: int = 0, sC: int = 0, stream=None) -> None:
-    """sdvkgen.cpp:917-926 gemmNtQ8: C = A . deq(Bq, Bs)^T on the split layout."""
+               batch: int = 1, sA: int = 0, sC: int = 0, workspace=None, stream=None) -> None:
+    """sdvkgen.cpp:917-926 gemmNtQ8: C = A . deq(Bq, Bs)^T on the split layout (any K)."""
+    if workspace is not None:
+        call("mi_gemm_nt_q8_split_ws", ptr(A), ptr(Bq), ptr(Bs), None, ptr(C), M, N, K, mode, lda, ldc,
+             batch, sA, sC, *_ws(workspace), _s(stream))
+        return
     call("mi_gemm_nt_q8_split", ptr(A), ptr(Bq), ptr(Bs), None, ptr(C), M, N, K, mode, lda, ldc,
          batch, sA, sC, _s(stream))
 
@@ -104,22 +125,35 @@ def gemm_nt_q8_0_geglu(A, W, G, M: int, F: int, K: int, *, bias=None, lda: int =
 
 
 def gemm_nn_q8(Aq, As, B, C, M: int, N: int, K: int, *, mode: int = 0, lda: int = 0, ldb: int = 0, ldc: int = 0,
-               batch: int = 1, sA: int = 0, sB: int = 0, sC: int = 0, stream=None) -> None:
+               batch: int = 1, sA: int = 0, sB: int = 0, sC: int = 0, workspace=None, stream=None) -> None:
     """sdvkgen.cpp:944-948 gemmNnQ8: C[M,N] = deq(Aq, As)[M,K] . B[K,N] (the conv paths' weights-left GEMM)."""
+    if workspace is not None:
+        call("mi_gemm_nn_q8_split_ws", ptr(Aq), ptr(As), ptr(B), ptr(C), M, N, K, mode, lda, ldb, ldc, batch, sA,
+             sB, sC, *_ws(workspace), _s(stream))
+        return
     call("mi_gemm_nn_q8_split", ptr(Aq), ptr(As), ptr(B), ptr(C), M, N, K, mode, lda, ldb, ldc, batch, sA, sB, sC,
          _s(stream))
 
 
 def gemm_nt_q8_bias(A, Bq, C, Bs, bias, M: int, N: int, K: int, *, mode: int = 0, lda: int = 0,
-                    ldc: int = 0, batch: int = 1, sA: int = 0, sC: int = 0, stream=None) -> None:
+                    ldc: int = 0, batch: int = 1, sA: int = 0, sC: int = 0, workspace=None, stream=None) -> None:
     """sdvkgen.cpp:928-936 gemmNtQ8Bias: as gemm_nt_q8, + bias[n] in mode 0."""
+    if workspace is not None:
+        call("mi_gemm_nt_q8_split_ws", ptr(A), ptr(Bq), ptr(Bs), ptr(bias), ptr(C), M, N, K, mode, lda,
+             ldc, batch, sA, sC, *_ws(workspace), _s(stream))
+        return
     call("mi_gemm_nt_q8_split", ptr(A), ptr(Bq), ptr(Bs), ptr(bias), ptr(C), M, N, K, mode, lda,
          ldc, batch, sA, sC, _s(stream))
 
 
 def gemm_nt_q8_0(A, W, C, M: int, N: int, K: int, *, bias=None, mode: int = 0, lda: int = 0,
-                 ldc: int = 0, batch: int = 1, sA: int = 0, sC: int = 0, stream=None) -> None:
-    """North-star entry: W is the raw stream of 34-byte GGUF Q8_0 blocks."""
+                 ldc: int = 0, batch: int = 1, sA: int = 0, sC: int = 0, workspace=None, stream=None) -> None:
+    """North-star entry: W is the raw stream of 34-byte GGUF Q8_0 blocks. With a workspace
+    (gemm_workspace_bytes) small grids may split K (mi_gemm_nt_q8_0_ws)."""
+    if workspace is not None:
+        call("mi_gemm_nt_q8_0_ws", ptr(A), ptr(W), ptr(bias), ptr(C), M, N, K, mode, lda, ldc, batch, sA,
+             sC, *_ws(workspace), _s(stream))
+        return
     call("mi_gemm_nt_q8_0", ptr(A), ptr(W), ptr(bias), ptr(C), M, N, K, mode, lda, ldc, batch, sA,
          sC, _s(stream))
 
@@ -171,10 +205,11 @@ class BlockDims:
     ctx_tokens: int
     ctx_channels: int
     ff_inner: int
+    flags: int = 0   # MI_BLOCK_FUSED_EPILOGUES | MI_BLOCK_JOINT_QKV
 
     def c(self) -> MiBlockDims:
         return MiBlockDims(self.batch, self.tokens, self.channels, self.heads, self.ctx_tokens,
-                           self.ctx_channels, self.ff_inner)
+                           self.ctx_channels, self.ff_inner, self.flags)
 
 
 @dataclass

@@ -31,11 +31,12 @@ import sys
 from pathlib import Path
 
 # family -> (main kernels: one launch per API call, helper kernels of the same calls)
+# (the K-split reduce pass is shared by both GEMMs; it is counted with gemm_q8)
 FAMILIES = {
-    "gemm_q8": (("gemm_q8_kernel", "gemm_q8_rows_kernel"),
-                ("gemm_init_kernel", "gemm_init_vec_kernel", "gemm_bias_add_kernel", "gemm_bias_add_vec_kernel")),
+    "gemm_q8": (("gemm_q8_kernel", "gemm_q8_rows_kernel", "gemm_q8_any_kernel"),
+                ("gemm_fill_kernel", "splitk_reduce_kernel")),
     "attention": (("attn_kernel", "attn_f16_kernel"), ()),
-    "gemm_nn_q8": (("gemm_nn_q8_kernel", "gemm_nn_q8_tiled_kernel"), ("gemm_nn_zero_kernel", "gemm_nn_zero_vec_kernel")),
+    "gemm_nn_q8": (("gemm_nn_q8_kernel", "gemm_nn_q8_tiled_kernel"), ()),
 }
 COPY_KERNEL = re.compile(r"copyBuffer", re.I)
 
@@ -93,7 +94,7 @@ def stats_report(csv_path: str, command: str) -> str:
                 fam[f][0] += calls
             fam[f][1] += tot
     lines += ["", "Family aggregates (total time of the family's kernels / calls of its main kernel, i.e. per API "
-                  "call; the GEMM family includes the split-K init fills):", "",
+                  "call; the GEMM family includes its K-split reduce passes):", "",
               "| family | calls | avg us per call |", "|---|---:|---:|"]
     for f, (calls, tot) in fam.items():
         if calls:

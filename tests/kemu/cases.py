@@ -25,9 +25,10 @@ sys.path.insert(0, str(HERE))
 import ctypes  # noqa: E402
 
 import emu as kemu  # noqa: E402
-from helpers import assert_parity, fp16_half_ulp, q8_weights, residual_split_ulps, rms, split_order_ulps  # noqa: E402
+from helpers import assert_parity, fp16_half_ulp, q8_weights, rms  # noqa: E402
 from oracle import binding as ob  # noqa: E402
-from sdvk_amd._lib import MI_F16, MI_F32, MiAttnArgs, MiBlockDims, MiBlockWeights  # noqa: E402
+from sdvk_amd._lib import (MI_BLOCK_FUSED_EPILOGUES, MI_BLOCK_JOINT_QKV, MI_F16, MI_F32, MiAttnArgs,  # noqa: E402
+                           MiBlockDims, MiBlockWeights)
 from test_gpu_block import BLOCK_TOL, make_weights  # noqa: E402
 import gguf_writer as gw  # noqa: E402
 from sdvk_amd._lib import MiGgufTensorInfo  # noqa: E402
@@ -51,36 +52,57 @@ def _logical_mask(M, N, ldc, batch, sC, size):
     return mask
 
 
+def _workspace(E, nbytes, front):
+    """(pointer, bytes) of a guarded workspace filled with NaN, or (None, 0)."""
+    if not nbytes:
+        return None, 0, None
+    b = E.buf(nbytes=nbytes, front=front).fill(0xFF)
+    return b.ptr, nbytes, b
+
+
 def gemm_nt(E, *, M, N, K, layout="q8_0", cfg=None, mode=0, bias=True, batch=1, lda=0, ldc=0, sA=0, sC=0,
-            seed=1, front=False, order=0, tol=2e-3, bias_off=0):
-    """mi_gemm_nt_q8_0 / mi_gemm_nt_q8_split against the oracle; bias_off
-    shifts the bias pointer by that many floats (an unaligned bias)."""
+            seed=1, front=False, order=0, tol=2e-3, bias_off=0, ws=True, a_off=0):
+    """mi_gemm_nt_q8_0[_ws] / mi_gemm_nt_q8_split[_ws] against the oracle;
+    bias_off shifts the bias pointer by that many floats (an unaligned bias),
+    a_off the A pointer (an A that is only 4-byte aligned); ws: through the
+    workspace entry with the workspace the library asks for (K splits)."""
     _set_cfg(cfg)
     E.order(order)
     lda_e, ldc_e = lda or K, ldc or N
     a_el = (batch - 1) * sA + (M - 1) * lda_e + K
     c_el = (batch - 1) * sC + (M - 1) * ldc_e + N
     A = ob.normal(seed, a_el)
-    blocks = q8_weights(ob, seed + 1, N, K)
+    if K % 32:  # split layout only: int8 values and flat-index scales drawn directly
+        assert layout == "split", "the 34-byte block layout needs K % 32 == 0"
+        blocks = None
+        q = ob.uniform_int(seed + 1, -127, 127, N * K).astype(np.int8)
+        payload = np.concatenate([q, np.zeros((-q.size) % 4, np.int8)]).view(np.uint32)
+        scales = ob.normal(seed + 4, (N * K + 31) // 32, 0.01, 0.002)
+    else:
+        blocks = q8_weights(ob, seed + 1, N, K)
     b = ob.normal(seed + 2, N, 0.0, 0.02) if bias else None
     C0 = ob.normal(seed + 3, c_el) if mode in (1, 2) else np.full(c_el, SENTINEL, dtype=np.float32)
-    dA, dC = E.buf(A, front=front), E.buf(C0, front=front)
+    dA, dC = E.buf(np.concatenate([np.zeros(a_off, np.float32), A]), front=front), E.buf(C0, front=front)
+    dA.ptr += 4 * a_off
     dB = E.buf(np.concatenate([np.zeros(bias_off, np.float32), b]), front=front) if bias else None
     if dB is not None and bias_off:
         dB.ptr += 4 * bias_off
     # mode 2 (C += acc + bias) = C0 + the mode-0 product with bias
     omode, oC = (0, np.zeros_like(C0)) if mode == 2 else (mode, C0.copy())
+    wsp, wsn, _keep = _workspace(E, E.lib.mi_gemm_nt_q8_workspace_bytes(M, N, K, batch) if ws else 0, front)
+    sfx, extra = ("_ws", (wsp, wsn)) if ws else ("", ())
     if layout == "q8_0":
         dW = E.buf(blocks, front=front)
-        E.call("mi_gemm_nt_q8_0", dA.ptr, dW.ptr, dB.ptr if dB else None, dC.ptr, M, N, K, mode, lda, ldc, batch,
-               sA, sC, None)
+        E.call("mi_gemm_nt_q8_0" + sfx, dA.ptr, dW.ptr, dB.ptr if dB else None, dC.ptr, M, N, K, mode, lda, ldc,
+               batch, sA, sC, *extra, None)
         want = ob.gemm_nt_q8_0(A, blocks, M, N, K, bias=b, C=oC, mode=omode, lda=lda, ldc=ldc, batch=batch,
                                sA=sA, sC=sC, threads=ob.max_threads())
     else:
-        payload, scales = ob.q8_0_to_split(blocks, N * K)
+        if blocks is not None:
+            payload, scales = ob.q8_0_to_split(blocks, N * K)
         dP, dS = E.buf(payload, front=front), E.buf(scales, front=front)
-        E.call("mi_gemm_nt_q8_split", dA.ptr, dP.ptr, dS.ptr, dB.ptr if dB else None, dC.ptr, M, N, K, mode, lda,
-               ldc, batch, sA, sC, None)
+        E.call("mi_gemm_nt_q8_split" + sfx, dA.ptr, dP.ptr, dS.ptr, dB.ptr if dB else None, dC.ptr, M, N, K, mode,
+               lda, ldc, batch, sA, sC, *extra, None)
         want = ob.gemm_nt_q8_split(A, payload, scales, M, N, K, bias=b, C=oC, mode=omode, lda=lda, ldc=ldc,
                                    batch=batch, sA=sA, sC=sC, threads=ob.max_threads())
     if mode == 2:
@@ -141,7 +163,7 @@ def gemm_geglu(E, *, M, F, K, cfg=None, bias=True, lda=0, ldg=0, seed=1, front=F
 
 
 def gemm_nn(E, *, M, N, K, mode=0, batch=1, lda=0, ldb=0, ldc=0, sA=0, sB=0, sC=0, seed=1, front=False,
-            order=0, tol=2e-3, kernel=None):
+            order=0, tol=2e-3, kernel=None, ws=True):
     """mi_gemm_nn_q8_split against the oracle (flat-index scales). kernel="general"
     forces the untiled kernel (MI_NN_KERNEL) on shapes the tiled one would take."""
     E.order(order)
@@ -163,8 +185,10 @@ def gemm_nn(E, *, M, N, K, mode=0, batch=1, lda=0, ldb=0, ldc=0, sA=0, sB=0, sC=
     C0 = ob.normal(seed + 3, c_el) if mode == 1 else np.full(c_el, SENTINEL, dtype=np.float32)
     dP, dS, dB, dC = (E.buf(payload, front=front), E.buf(scales, front=front), E.buf(B, front=front),
                       E.buf(C0, front=front))
-    E.call("mi_gemm_nn_q8_split", dP.ptr, dS.ptr, dB.ptr, dC.ptr, M, N, K, mode, lda, ldb, ldc, batch, sA, sB, sC,
-           None)
+    wsp, wsn, _keep = _workspace(E, E.lib.mi_gemm_nn_q8_workspace_bytes(M, N, K, batch) if ws else 0, front)
+    sfx, extra = ("_ws", (wsp, wsn)) if ws else ("", ())
+    E.call("mi_gemm_nn_q8_split" + sfx, dP.ptr, dS.ptr, dB.ptr, dC.ptr, M, N, K, mode, lda, ldb, ldc, batch, sA, sB,
+           sC, *extra, None)
     want = ob.gemm_nn_q8_split(payload, scales, B, M, N, K, C=C0.copy(), mode=mode, lda=lda, ldb=ldb, ldc=ldc,
                                batch=batch, sA=sA, sB=sB, sC=sC, threads=ob.max_threads())
     got = dC.get(np.float32, c_el)
@@ -248,32 +272,41 @@ def _whole_tiles(mask: np.ndarray, what: str) -> None:
         assert not bad.any(), f"{what}: written region is not whole 32-aligned tiles ({int(bad.sum())} runs)"
 
 
-def gemm_full(E, *, M, N, K, cfg=None, layout="q8_0", seed=1, order=0, tol=2e-3):
-    """mi_gemm_nt_q8_0 / _split at a full benchmark shape, sampled workgroups."""
+def gemm_full(E, *, M, N, K, cfg=None, layout="q8_0", seed=1, order=0, tol=2e-3, ws=True):
+    """mi_gemm_nt_q8_0[_ws] / _split[_ws] at a full benchmark shape, sampled
+    workgroups (with ws: the K-split plan the benchmark runs; the reduce pass
+    runs whole over a zeroed workspace, so unsampled tiles read back as 0)."""
     _set_cfg(cfg)
     E.order(order)
     A = ob.normal(seed, M * K)
     blocks = q8_weights(ob, seed + 1, N, K)
     dA, dC = E.buf(A), E.buf(np.zeros(M * N, np.float32))
+    nws = E.lib.mi_gemm_nt_q8_workspace_bytes(M, N, K, 1) if ws else 0
+    dws = E.buf(nbytes=nws).fill(0) if nws else None
+    sfx, extra = ("_ws", (dws.ptr if dws else None, nws)) if ws else ("", ())
     if layout == "q8_0":
         dW = E.buf(blocks)
-        call = lambda: E.call("mi_gemm_nt_q8_0", dA.ptr, dW.ptr, None, dC.ptr, M, N, K, 0, 0, 0, 1, 0, 0, None)
+        call = lambda: E.call("mi_gemm_nt_q8_0" + sfx, dA.ptr, dW.ptr, None, dC.ptr, M, N, K, 0, 0, 0, 1, 0, 0,
+                              *extra, None)
     else:
         payload, scales = ob.q8_0_to_split(blocks, N * K)
         dP, dS = E.buf(payload), E.buf(scales)
-        call = lambda: E.call("mi_gemm_nt_q8_split", dA.ptr, dP.ptr, dS.ptr, None, dC.ptr, M, N, K, 0, 0, 0, 1, 0, 0,
-                              None)
-    helpers = "gemm_init|-|-|-;gemm_bias_add|-|-|-"  # the fill and bias-add kernels, both forms
+        call = lambda: E.call("mi_gemm_nt_q8_split" + sfx, dA.ptr, dP.ptr, dS.ptr, None, dC.ptr, M, N, K, 0, 0, 0, 1,
+                              0, 0, *extra, None)
+    helpers = "gemm_fill|-|-|-;splitk_reduce|-|-|-"  # the K == 0 fill and the split reduce pass
     kern, grid = _probe_grid(E, f"gemm_q8_kernel|-|-|-;gemm_q8_rows_kernel|-|-|-;{helpers}", call)
     assert not np.any(dC.get(np.float32, M * N)), "a launch with no workgroup wrote C"
     xs = sorted({0, _block_of_tile(grid[0] - 1, grid[0])})
     x = ",".join(map(str, xs))
     print(f"  {kern} grid {grid}, blockIdx.x {xs}", flush=True)
-    E.sample(f"gemm_q8_kernel|{x}|*|*;gemm_q8_rows_kernel|{x}|*|*;{helpers}")
+    E.sample(f"gemm_q8_kernel|{x}|*|*;gemm_q8_rows_kernel|{x}|*|*;gemm_fill|-|-|-")
     before = E.lib.kemu_blocks_run()
     call()
     ran = E.lib.kemu_blocks_run() - before
-    assert ran == len(xs) * grid[1] * grid[2], f"{ran} workgroups ran, expected {len(xs)} x {grid[1]} x {grid[2]}"
+    # a split plan's reduce pass runs whole: a capped grid over the [M, N / 4] units
+    reduce = min(max(-(-(M * N // 4) // 256), 1), 1024) if grid[1] > 1 else 0
+    assert ran == len(xs) * grid[1] * grid[2] + reduce, \
+        f"{ran} workgroups ran, expected {len(xs)} x {grid[1]} x {grid[2]} + {reduce} (reduce)"
     got = dC.get(np.float32, M * N).reshape(M, N)
     mask = got != 0
     assert mask.any(), "the sampled workgroups wrote nothing"
@@ -296,12 +329,14 @@ def gemm_nn_full(E, *, M, N, K, seed=1, order=0, tol=2e-3):
     payload, scales = ob.q8_0_to_split(ob.q8_0_quantize(w), M * K)
     B = ob.normal(seed + 1, K * N)
     dP, dS, dB, dC = E.buf(payload), E.buf(scales), E.buf(B), E.buf(np.zeros(M * N, np.float32))
-    call = lambda: E.call("mi_gemm_nn_q8_split", dP.ptr, dS.ptr, dB.ptr, dC.ptr, M, N, K, 0, 0, 0, 0, 1, 0, 0, 0,
-                          None)
-    kern, grid = _probe_grid(E, "gemm_nn_q8_tiled_kernel|-|-|-;gemm_nn_q8_kernel|-|-|-;gemm_nn_zero|-|-|-",
+    nws = E.lib.mi_gemm_nn_q8_workspace_bytes(M, N, K, 1)
+    dws = E.buf(nbytes=nws).fill(0) if nws else None
+    call = lambda: E.call("mi_gemm_nn_q8_split_ws", dP.ptr, dS.ptr, dB.ptr, dC.ptr, M, N, K, 0, 0, 0, 0, 1, 0, 0, 0,
+                          dws.ptr if dws else None, nws, None)
+    kern, grid = _probe_grid(E, "gemm_nn_q8_tiled_kernel|-|-|-;gemm_nn_q8_kernel|-|-|-;splitk_reduce|-|-|-",
                              call)
     print(f"  {kern} grid {grid}", flush=True)
-    E.sample("gemm_nn_q8_tiled_kernel|0,-1|-1|*;gemm_nn_q8_kernel|0,-1|-1|*;gemm_nn_zero|-|-|-")
+    E.sample("gemm_nn_q8_tiled_kernel|0,-1|-1|*;gemm_nn_q8_kernel|0,-1|-1|*")
     call()
     got = dC.get(np.float32, M * N).reshape(M, N)
     mask = got != 0
@@ -366,12 +401,12 @@ def attention_full(E, *, batch, Tq, Tk, C, heads, masked=False, nw=None, seed=1,
 def block(E, *, B, T, C, H, Tc, Cc, F, masked=False, blocks=2, order=0, front=False, fused=False, qkv_joint=False):
     """Two applications of one SDXL transformer block: uncached
     (mi_sdxl_block_forward) vs context K / V projected once (mi_block_ctx_kv,
-    mi_sdxl_block_forward_kv), both against the oracle's block."""
+    mi_sdxl_block_forward_kv), against the oracle's block; cached and fresh
+    runs must be bit-identical (same GEMM plans, fixed summation order). With
+    fused / qkv_joint: one block with those flags against the plain block,
+    bit for bit (every flag combination computes the same sums)."""
     E.order(order)
-    if fused:
-        os.environ["MI_BLOCK_EPILOGUE"] = "fused"
-    else:
-        os.environ.pop("MI_BLOCK_EPILOGUE", None)
+    flags = (MI_BLOCK_FUSED_EPILOGUES if fused else 0) | (MI_BLOCK_JOINT_QKV if qkv_joint else 0)
     w = make_weights(ob, C, Cc, F, seed=500)
     dw = {k: E.buf(v, front=front) for k, v in w.items()}
     ptrs = {k: b.ptr for k, b in dw.items()}
@@ -383,7 +418,8 @@ def block(E, *, B, T, C, H, Tc, Cc, F, masked=False, blocks=2, order=0, front=Fa
     bw = MiBlockWeights(*[ptrs[f[0]] for f in MiBlockWeights._fields_])
     # the same weights stored apart (three projection GEMMs)
     bw_apart = MiBlockWeights(*[dw[f[0]].ptr for f in MiBlockWeights._fields_])
-    dims = MiBlockDims(B, T, C, H, Tc, Cc, F)
+    dims = MiBlockDims(B, T, C, H, Tc, Cc, F, flags)
+    plain = MiBlockDims(B, T, C, H, Tc, Cc, F, 0)
     x = ob.normal(3, B * T * C)
     ctx = ob.normal(4, B * Tc * Cc).astype(np.float16).astype(np.float32)
     kl = ob.uniform_int(8, 1, Tc, B) if masked else None
@@ -406,42 +442,20 @@ def block(E, *, B, T, C, H, Tc, Cc, F, masked=False, blocks=2, order=0, front=Fa
         want = ob.sdxl_block(w, want, ctx, batch=B, tokens=T, channels=C, heads=H, ctx_tokens=Tc, ctx_channels=Cc,
                              ff_inner=F, ctx_len=kl, threads=ob.max_threads())
     assert np.all(np.isfinite(cached)) and np.all(np.isfinite(fresh)), "block: non-finite output"
-    d_kv = float(np.max(np.abs(cached - fresh)))
-    ulp_x = float(np.spacing(np.float32(np.max(np.abs(fresh)))))
-    assert d_kv <= split_order_ulps(blocks) * ulp_x, f"cached vs fresh K / V: {d_kv / ulp_x:.1f} ulp of max|x|"
     e = float(np.max(np.abs(fresh - want)) / rms(want - x))
     assert e <= blocks * BLOCK_TOL, f"block vs oracle: {e:.3e} x RMS(update)"
-    if qkv_joint:
-        # one block: joint vs separate Q/K/V projections on the same build (the
-        # same MFMA sums unless a K split differs: a few ulps of |x|)
+    assert np.array_equal(cached, fresh), \
+        f"cached vs fresh K / V differ by {float(np.max(np.abs(cached - fresh))):.3e}"
+    if flags:
+        # one block with the flags vs the plain block (weights apart, separate epilogues)
         outs = []
-        for wts in (bw, bw_apart):
+        for wts, dd in ((bw, dims), (bw_apart, plain)):
             d1 = E.buf(x, front=front)
-            E.call("mi_sdxl_block_forward", ctypes.byref(wts), ctypes.byref(dims), d1.ptr, dc.ptr,
+            E.call("mi_sdxl_block_forward", ctypes.byref(wts), ctypes.byref(dd), d1.ptr, dc.ptr,
                    dl.ptr if dl else None, ws.ptr, ws_bytes, None)
             outs.append(d1.get(np.float32))
-        diff = float(np.max(np.abs(outs[0] - outs[1])))
-        ulp = float(np.spacing(np.float32(np.max(np.abs(outs[1])))))
-        assert diff <= 4 * ulp, f"joint vs separate Q/K/V: {diff:.3e} > 4 ulp ({ulp:.3e}) of max|x|"
-    if fused:
-        # one block, fused vs separate epilogues on the same build: they differ
-        # only in the rounding order of the residual adds of K-split GEMMs
-        # ((x + b) + partials vs x + (b + partials)), a few ulps of |x|
-        # (bound: helpers.residual_split_ulps)
-        outs = []
-        for mode in ("fused", None):
-            if mode:
-                os.environ["MI_BLOCK_EPILOGUE"] = mode
-            else:
-                os.environ.pop("MI_BLOCK_EPILOGUE", None)
-            d1 = E.buf(x, front=front)
-            E.call("mi_sdxl_block_forward", ctypes.byref(bw), ctypes.byref(dims), d1.ptr, dc.ptr,
-                   dl.ptr if dl else None, ws.ptr, ws_bytes, None)
-            outs.append(d1.get(np.float32))
-        diff = float(np.max(np.abs(outs[0] - outs[1])))
-        ulp = float(np.spacing(np.float32(np.max(np.abs(outs[1])))))
-        lim = residual_split_ulps(C, F)
-        assert diff <= lim * ulp, f"fused vs separate epilogues: {diff / ulp:.1f} > {lim} ulp of max|x|"
+        assert np.array_equal(outs[0], outs[1]), \
+            f"flags {flags:#x} vs plain block differ by {float(np.max(np.abs(outs[0] - outs[1]))):.3e}"
     return e
 
 
@@ -455,15 +469,26 @@ def routing(E, *, table, order=0):
     E.sample("*|-|-|-")
     bad = []
     for op, dims, grid, threads in table:
-        if op == "gemm":
+        if op in ("gemm", "gemm_ws"):
             M, N, K = dims
             A, W, C = E.buf(nbytes=M * K * 4), E.buf(nbytes=N * K // 32 * 34), E.buf(nbytes=M * N * 4)
-            E.call("mi_gemm_nt_q8_0", A.ptr, W.ptr, None, C.ptr, M, N, K, 0, 0, 0, 1, 0, 0, None)
-        elif op == "nn":
+            if op == "gemm":
+                E.call("mi_gemm_nt_q8_0", A.ptr, W.ptr, None, C.ptr, M, N, K, 0, 0, 0, 1, 0, 0, None)
+            else:
+                n = E.lib.mi_gemm_nt_q8_workspace_bytes(M, N, K, 1)
+                ws = E.buf(nbytes=max(n, 16))
+                E.call("mi_gemm_nt_q8_0_ws", A.ptr, W.ptr, None, C.ptr, M, N, K, 0, 0, 0, 1, 0, 0, ws.ptr, n, None)
+        elif op in ("nn", "nn_ws"):
             M, N, K = dims
             P, S, B, C = E.buf(nbytes=M * K), E.buf(nbytes=M * K // 32 * 4), E.buf(nbytes=K * N * 4), \
                 E.buf(nbytes=M * N * 4)
-            E.call("mi_gemm_nn_q8_split", P.ptr, S.ptr, B.ptr, C.ptr, M, N, K, 0, 0, 0, 0, 1, 0, 0, 0, None)
+            if op == "nn":
+                E.call("mi_gemm_nn_q8_split", P.ptr, S.ptr, B.ptr, C.ptr, M, N, K, 0, 0, 0, 0, 1, 0, 0, 0, None)
+            else:
+                n = E.lib.mi_gemm_nn_q8_workspace_bytes(M, N, K, 1)
+                ws = E.buf(nbytes=max(n, 16))
+                E.call("mi_gemm_nn_q8_split_ws", P.ptr, S.ptr, B.ptr, C.ptr, M, N, K, 0, 0, 0, 0, 1, 0, 0, 0, ws.ptr,
+                       n, None)
         else:
             b, h, tq, tk = dims
             C = 64 * h
@@ -490,10 +515,6 @@ def block_full(E, *, fused=False, qkv_joint=False, cached=False, order=0):
     tensors the skipped workgroups would write stay unwritten, so no values
     are compared here; the small-shape block cases compare them)."""
     E.order(order)
-    if fused:
-        os.environ["MI_BLOCK_EPILOGUE"] = "fused"
-    else:
-        os.environ.pop("MI_BLOCK_EPILOGUE", None)
     B, T, C, H, Tc, Cc, F = 2, 1024, 1280, 20, 77, 2048, 5120
     w = make_weights(ob, C, Cc, F, seed=500)
     dw = {k: E.buf(v) for k, v in w.items()}
@@ -504,7 +525,8 @@ def block_full(E, *, fused=False, qkv_joint=False, cached=False, order=0):
         nb = w["attn1_q"].nbytes
         ptrs.update(attn1_q=joint.ptr, attn1_k=joint.ptr + nb, attn1_v=joint.ptr + 2 * nb)
     bw = MiBlockWeights(*[ptrs[f[0]] for f in MiBlockWeights._fields_])
-    dims = MiBlockDims(B, T, C, H, Tc, Cc, F)
+    flags = (MI_BLOCK_FUSED_EPILOGUES if fused else 0) | (MI_BLOCK_JOINT_QKV if qkv_joint else 0)
+    dims = MiBlockDims(B, T, C, H, Tc, Cc, F, flags)
     dx = E.buf(ob.normal(3, B * T * C))
     dc = E.buf(ob.normal(4, B * Tc * Cc).astype(np.float16).astype(np.float32))
     dl = E.buf(ob.uniform_int(8, 1, Tc, B).astype(np.int32))

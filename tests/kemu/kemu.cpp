@@ -216,6 +216,9 @@ void run_block(Block& b) {
 
 Thread* g_cur = nullptr;
 dim3v g_block_idx{0, 0, 0}, g_block_dim{1, 1, 1}, g_grid_dim{1, 1, 1};
+// the last launch other than a K-split reduce pass (kemu_last_grid / kemu_last_kernel)
+const char* g_rec_kernel = "";
+dim3v g_rec_grid{1, 1, 1}, g_rec_block{1, 1, 1};
 
 const dim3v& thread_idx() { return g_cur->idx; }
 int lane_id() { return g_cur->lane; }
@@ -293,6 +296,12 @@ void run_grid(const char* name, dim3v grid, dim3v block, Body& body) {
     if (grid.y > 65535 || grid.z > 65535) die("grid (%u,%u,%u) beyond the launch limits", grid.x, grid.y, grid.z);
     g_grid_dim = grid;
     g_block_dim = block;
+    // the routing record skips the K-split reduce pass that follows a split GEMM
+    if (!std::strstr(name, "splitk_reduce")) {
+        g_rec_kernel = name;
+        g_rec_grid = grid;
+        g_rec_block = block;
+    }
     Block b;
     b.body = &body;
     b.th.resize(nthreads);
@@ -380,10 +389,10 @@ extern "C" void kemu_set_order(int order, int reverse_blocks) {
 extern "C" uint64_t kemu_launches(void) { return g_launches; }
 extern "C" uint64_t kemu_blocks_run(void) { return g_blocks_run; }
 extern "C" void kemu_last_grid(uint32_t* xyz) {
-    xyz[0] = g_grid_dim.x;
-    xyz[1] = g_grid_dim.y;
-    xyz[2] = g_grid_dim.z;
-    xyz[3] = g_block_dim.x * g_block_dim.y * g_block_dim.z;
+    xyz[0] = g_rec_grid.x;
+    xyz[1] = g_rec_grid.y;
+    xyz[2] = g_rec_grid.z;
+    xyz[3] = g_rec_block.x * g_rec_block.y * g_rec_block.z;
 }
 
 // spec: rules separated by ';', each "kernel|x|y|z" (kernel "*": any) where a dimension is '*'
@@ -427,4 +436,4 @@ extern "C" void kemu_set_sample(const char* spec) {
     }
 }
 extern "C" void kemu_sync(void) { flush_copies(~0ull); }
-extern "C" const char* kemu_last_kernel(void) { return g_kernel; }
+extern "C" const char* kemu_last_kernel(void) { return g_rec_kernel; }

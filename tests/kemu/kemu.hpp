@@ -96,6 +96,7 @@ uint64_t kemu_launches(void);
 uint64_t kemu_blocks_run(void);  // workgroups emulated so far
 void kemu_set_sample(const char* spec);  // run only some workgroups (kemu.cpp)
 void kemu_last_grid(uint32_t* xyz);      // grid (x, y, z) and work-items per block of the last launch
+                                        // (a K-split reduce pass is not recorded)
 void kemu_sync(void);  // runs every deferred copy
 const char* kemu_last_kernel(void);
 }

@@ -83,9 +83,22 @@ def test_errors_are_returned_not_raised_through_the_abi():
     assert lib.mi_gemm_nt_q8_0_geglu(fake, fake * 2, None, fake * 3, 8, 8, 0, 0, 0, None) == _lib.MI_ERR_UNSUPPORTED
     assert lib.mi_gemm_nt_q8_0_geglu(fake, fake * 2, None, fake + 64, 8, 8, 32, 0, 0, None) == _lib.MI_ERR_ALIASING
     assert lib.mi_gemm_nt_q8_0_geglu(None, None, None, None, 0, 8, 32, 0, 0, None) == _lib.MI_OK
-    # split entry rejects K % 4 != 0 (the reference's 4-wide staging zero-fills there)
-    st = lib.mi_gemm_nt_q8_split(fake, fake * 2, fake * 4, None, fake * 3, 8, 8, 30, 0, 0, 0, 1, 0, 0, None)
-    assert st == _lib.MI_ERR_UNSUPPORTED
+    # the split entry takes any K (the scalar gemm_nt_q8 does, gemm_nt_q8.comp:52-80) and an A that is only
+    # 4-byte aligned; a 2-byte-aligned A is an alignment error
+    st = lib.mi_gemm_nt_q8_split(fake + 2, fake * 2, fake * 4, None, fake * 3, 8, 8, 30, 0, 0, 0, 1, 0, 0, None)
+    assert st == _lib.MI_ERR_ALIGNMENT
+    # workspace entries: a workspace overlapping an operand, or misaligned
+    st = lib.mi_gemm_nt_q8_0_ws(fake, fake * 2, None, fake * 3, 8, 8, 32, 0, 0, 0, 1, 0, 0, fake * 3 + 16, 4096,
+                                None)
+    assert st == _lib.MI_ERR_ALIASING
+    st = lib.mi_gemm_nt_q8_0_ws(fake, fake * 2, None, fake * 3, 8, 8, 32, 0, 0, 0, 1, 0, 0, fake * 5 + 4, 4096, None)
+    assert st == _lib.MI_ERR_ALIGNMENT
+    # the workspace a plan needs: none for a grid that fills the GPU, split planes for a small one
+    assert lib.mi_gemm_nt_q8_workspace_bytes(8192, 5120, 640, 1) == 0
+    assert lib.mi_gemm_nt_q8_workspace_bytes(154, 640, 2048, 1) == 8 * 154 * 640 * 4
+    assert lib.mi_gemm_nt_q8_workspace_bytes(154, 640, 2048, 2) == 2 * 4 * 154 * 640 * 4
+    assert lib.mi_gemm_nn_q8_workspace_bytes(1280, 1024, 640, 1) == 2 * 1280 * 1024 * 4
+    assert lib.mi_gemm_nn_q8_workspace_bytes(1280, 1024, 100, 1) == 0  # K % 64 != 0: the untiled kernel
     # unsupported attention head dim: the reference exit(1)s; here an error code
     st = lib.mi_fused_attention(fake, fake * 2, fake * 3, fake * 4, 8, 8, 130, 1, 0, None)
     assert st == _lib.MI_ERR_UNSUPPORTED

@@ -98,12 +98,15 @@ def _fake_ops(calls):
             calls.append(name)
             if name in ("block_workspace_bytes", "block_ctx_kv_bytes"):
                 return 1 << 20
+            if name in ("gemm_workspace_bytes", "gemm_nn_workspace_bytes"):
+                return 1 << 16
             return None
         return f
 
     names = [n for n, v in vars(real).items() if inspect.isfunction(v) and v.__module__ == real.__name__]
     ns = {n: wrap(n) for n in names}
-    ns.update(BlockDims=real.BlockDims, BlockWeights=real.BlockWeights)
+    ns.update(BlockDims=real.BlockDims, BlockWeights=real.BlockWeights,
+              MI_BLOCK_FUSED_EPILOGUES=real.MI_BLOCK_FUSED_EPILOGUES, MI_BLOCK_JOINT_QKV=real.MI_BLOCK_JOINT_QKV)
     return types.SimpleNamespace(**ns)
 
 

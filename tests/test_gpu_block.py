@@ -9,7 +9,7 @@ what those errors are relative to: max |err| <= 5e-3 x RMS(update).
 import numpy as np
 import pytest
 
-from helpers import rms
+from helpers import record, rms
 from sdvk_amd import ops
 from sdvk_amd.hip import DeviceBuffer, synchronize
 
@@ -66,6 +66,7 @@ def test_block_small(gpu, oracle, B, T, C, H, Tc, Cc, F, masked):
     upd = want - x
     e = np.max(np.abs(got - want)) / rms(upd)
     print(f"  update err/rms = {e:.3e}", flush=True)
+    record(e, BLOCK_TOL)
     assert np.all(np.isfinite(got)) and e <= BLOCK_TOL
 
 
@@ -83,6 +84,7 @@ def test_block_config4_full(gpu, oracle):
                              ff_inner=F, threads=oracle.max_threads())
     e = np.max(np.abs(got - want)) / rms(want - x)
     print(f"  update err/rms = {e:.3e}", flush=True)
+    record(e, BLOCK_TOL)
     assert np.all(np.isfinite(got)) and e <= BLOCK_TOL
 
 

@@ -17,13 +17,22 @@ pytestmark = pytest.mark.gpu
 GOLDEN = Path(__file__).parent / "golden"
 
 
-def run_q8_0(A, blocks, M, N, K, bias=None, C0=None, mode=0, lda=0, ldc=0, batch=1, sA=0, sC=0):
+def workspace(M, N, K, batch=1):
+    """The workspace the *_ws entries ask for (None when the plan does not split K)."""
+    n = ops.gemm_workspace_bytes(M, N, K, batch)
+    return DeviceBuffer(n) if n else None
+
+
+def run_q8_0(A, blocks, M, N, K, bias=None, C0=None, mode=0, lda=0, ldc=0, batch=1, sA=0, sC=0, ws=False):
+    """ws: through mi_gemm_nt_q8_0_ws with the workspace the library asks for."""
     ldc_e = ldc or N
     csize = ((batch - 1) * sC + (M - 1) * ldc_e + N) if batch > 1 else M * ldc_e
     dA, dW = DeviceBuffer.from_array(A), DeviceBuffer.from_array(blocks)
     dB = DeviceBuffer.from_array(bias) if bias is not None else None
     dC = DeviceBuffer.from_array(C0) if C0 is not None else DeviceBuffer(csize * 4)
-    ops.gemm_nt_q8_0(dA, dW, dC, M, N, K, bias=dB, mode=mode, lda=lda, ldc=ldc, batch=batch, sA=sA, sC=sC)
+    dws = workspace(M, N, K, batch) if ws else None
+    ops.gemm_nt_q8_0(dA, dW, dC, M, N, K, bias=dB, mode=mode, lda=lda, ldc=ldc, batch=batch, sA=sA, sC=sC,
+                     workspace=dws)
     synchronize()
     return dC.download(np.float32, C0.size if C0 is not None else csize)
 
@@ -46,28 +55,48 @@ def test_reference_bench_case_every_variant(gpu):
         assert_parity(got, want, what=kernel)
 
 
+@pytest.mark.parametrize("ws", [False, True])
 @pytest.mark.parametrize("M,N,K", [(1, 1, 32), (77, 96, 64), (100, 100, 96), (130, 257, 320),
                                    (1024, 96, 64), (1100, 130, 128), (2048, 640, 640), (154, 1280, 2048)])
-def test_q8_0_shapes_bias_and_accumulate(gpu, oracle, M, N, K):
-    print(f"[case] q8_0 M={M} N={N} K={K}", flush=True)
+def test_q8_0_shapes_bias_and_accumulate(gpu, oracle, M, N, K, ws):
+    print(f"[case] q8_0 M={M} N={N} K={K} ws={ws}", flush=True)
     A = oracle.normal(M + 1, M * K)
     blocks = q8_weights(oracle, N + 2, N, K)
     bias = oracle.normal(3, N, 0.0, 0.02)
     want = oracle.gemm_nt_q8_0(A, blocks, M, N, K, bias=bias, threads=oracle.max_threads()).reshape(M, N)
-    got = run_q8_0(A, blocks, M, N, K, bias=bias).reshape(M, N)
+    got = run_q8_0(A, blocks, M, N, K, bias=bias, ws=ws).reshape(M, N)
     e = assert_parity(got, want, what=f"{M}x{N}x{K} mode0")
     # mode 1: C += A W^T, no bias (gemm_nt_q8_v.comp:121-125)
     C0 = oracle.normal(4, M * N)
     want1 = oracle.gemm_nt_q8_0(A, blocks, M, N, K, threads=oracle.max_threads()).reshape(M, N) + C0.reshape(M, N)
-    got1 = run_q8_0(A, blocks, M, N, K, bias=bias, C0=C0, mode=1).reshape(M, N)
+    got1 = run_q8_0(A, blocks, M, N, K, bias=bias, C0=C0, mode=1, ws=ws).reshape(M, N)
     assert_parity(got1 - C0.reshape(M, N), want1 - C0.reshape(M, N), what="mode1")
+    # mode 2: C += A W^T + bias (the residual epilogue)
+    got2 = run_q8_0(A, blocks, M, N, K, bias=bias, C0=C0, mode=2, ws=ws).reshape(M, N)
+    assert_parity(got2 - C0.reshape(M, N), want, what="mode2")
     print(f"  err/rms = {e:.3e}", flush=True)
 
 
-def test_q8_0_and_split_entries_agree_bitwise(gpu, oracle, monkeypatch):
-    """Both entries dequantise w = fp16(fp32(d) * q): identical results (on a
-    configuration without K splitting, whose fp32 atomics reorder the sum)."""
-    monkeypatch.setenv("MI_GEMM_CFG", "1")
+def test_activation_beyond_fp16_range(gpu, oracle):
+    """Documented limit: A is rounded to fp16, so |a| >= 65520 becomes an
+    infinite operand and only the output rows that read it go inf / NaN;
+    |a| up to 65504 (the largest fp16) stays finite and within the bar."""
+    M, N, K = 64, 64, 64
+    A = oracle.normal(1, M * K).reshape(M, K)
+    A[3, 5] = 65504.0
+    A[7, 9] = 1.0e6
+    blocks = q8_weights(oracle, 2, N, K)
+    got = run_q8_0(A.reshape(-1), blocks, M, N, K).reshape(M, N)
+    want = oracle.gemm_nt_q8_0(A.reshape(-1), blocks, M, N, K).reshape(M, N)
+    bad = ~np.isfinite(got)
+    assert bad[7].all() and not np.delete(bad, 7, axis=0).any(), "only the row with |a| = 1e6 is non-finite"
+    ok = [r for r in range(M) if r != 7]
+    assert_parity(got[ok], want[ok], what="rows within the fp16 range")
+
+
+def test_q8_0_and_split_entries_agree_bitwise(gpu, oracle):
+    """Both entries dequantise w = fp16(fp32(d) * q) and sum in the same order:
+    identical results."""
     M, N, K = 1100, 320, 640
     A = oracle.normal(1, M * K)
     blocks = q8_weights(oracle, 2, N, K)
@@ -80,12 +109,15 @@ def test_q8_0_and_split_entries_agree_bitwise(gpu, oracle, monkeypatch):
     assert np.array_equal(dC.download(np.float32, M * N), got_blocks)
 
 
-@pytest.mark.parametrize("K", [100, 36, 4, 132])
+@pytest.mark.parametrize("K", [100, 36, 4, 132, 37, 5, 1, 70])
 def test_split_general_k(gpu, oracle, K):
-    """Split layout with K % 32 != 0: scales follow the flat element index."""
+    """Split layout with K % 32 != 0 (scales follow the flat element index),
+    including K % 4 != 0, which the scalar gemm_nt_q8 accepts
+    (gemm_nt_q8.comp:52-80) and the untiled any-K kernel serves."""
     M, N = 70, 45
     A = oracle.normal(K, M * K)
     payload = oracle.uniform_int(K + 1, -127, 127, N * K).astype(np.int8)
+    payload = np.concatenate([payload, np.zeros((-payload.size) % 4, np.int8)])
     scales = oracle.normal(K + 2, (N * K + 31) // 32, 0.01, 0.002)
     bias = oracle.normal(5, N)
     want = oracle.gemm_nt_q8_split(A, payload, scales, M, N, K, bias=bias).reshape(M, N)
@@ -94,6 +126,22 @@ def test_split_general_k(gpu, oracle, K):
                         DeviceBuffer.from_array(scales), DeviceBuffer.from_array(bias), M, N, K)
     synchronize()
     assert_parity(dC.download(np.float32, M * N).reshape(M, N), want, what=f"split K={K}")
+
+
+def test_split_unaligned_a_and_odd_lda(gpu, oracle):
+    """A only 4-byte aligned with lda % 4 != 0 (the any-K kernel), modes 0 / 1."""
+    M, N, K, lda = 90, 70, 64, 67
+    A = oracle.normal(3, M * lda + 1)
+    blocks = q8_weights(oracle, 4, N, K)
+    payload, scales = oracle.q8_0_to_split(blocks, N * K)
+    bias = oracle.normal(5, N, 0.0, 0.02)
+    want = oracle.gemm_nt_q8_split(A[1:], payload, scales, M, N, K, bias=bias, lda=lda).reshape(M, N)
+    dA = DeviceBuffer.from_array(A)
+    dC = DeviceBuffer(M * N * 4)
+    ops.gemm_nt_q8_bias(dA.value + 4, DeviceBuffer.from_array(payload), dC, DeviceBuffer.from_array(scales),
+                        DeviceBuffer.from_array(bias), M, N, K, lda=lda)
+    synchronize()
+    assert_parity(dC.download(np.float32, M * N).reshape(M, N), want, what="unaligned A")
 
 
 @pytest.mark.parametrize("ldc_pad,sc_pad,K,cfg", [(8, 8, 96, ""), (3, 5, 96, ""), (8, 8, 128, ""), (1, 0, 256, ""),
@@ -110,7 +158,7 @@ def test_batch_and_strides(gpu, oracle, monkeypatch, ldc_pad, sc_pad, K, cfg):
     blocks = q8_weights(oracle, 2, N, K)
     C0 = oracle.normal(3, (batch - 1) * sC + M * ldc)
     want = oracle.gemm_nt_q8_0(A, blocks, M, N, K, C=C0.copy(), lda=lda, ldc=ldc, batch=batch, sA=sA, sC=sC)
-    got = run_q8_0(A, blocks, M, N, K, C0=C0, lda=lda, ldc=ldc, batch=batch, sA=sA, sC=sC)
+    got = run_q8_0(A, blocks, M, N, K, C0=C0, lda=lda, ldc=ldc, batch=batch, sA=sA, sC=sC, ws=True)
     for z in range(batch):
         g = got[z * sC: z * sC + M * ldc].reshape(M, ldc)
         w = want[z * sC: z * sC + M * ldc].reshape(M, ldc)
@@ -141,25 +189,27 @@ def test_baseline_shapes_sampled_rows(gpu, oracle, M, N, K):
     assert e <= REL_RMS_TOL
 
 
-@pytest.mark.parametrize("cfg", ["0", "1", "2", "3", "4", "5", "6", "0:3", "1:2", "2:5", "3:16", "4:2", "5:2",
-                                 "6:3"])
+@pytest.mark.parametrize("cfg", ["0", "1", "2", "3", "4", "5", "6", "12", "13", "14", "0:3", "1:2", "2:5",
+                                 "3:16", "4:2", "5:2", "6:3", "14:2"])
 @pytest.mark.parametrize("M,N,K", [(300, 200, 640), (1030, 130, 256)])
 def test_every_tile_config_and_split_k(gpu, oracle, monkeypatch, cfg, M, N, K):
-    """Forces each tile configuration / K split (MI_GEMM_CFG="<cfg>[:<splits>]")."""
+    """Forces each tile configuration / K split (MI_GEMM_CFG="<cfg>[:<splits>]";
+    the splits run through the workspace entries)."""
     print(f"[case] cfg={cfg} M={M} N={N} K={K}", flush=True)
     monkeypatch.setenv("MI_GEMM_CFG", cfg)
     A = oracle.normal(11, M * K)
     blocks = q8_weights(oracle, 12, N, K)
     bias = oracle.normal(13, N, 0.0, 0.02)
     want = oracle.gemm_nt_q8_0(A, blocks, M, N, K, bias=bias, threads=oracle.max_threads()).reshape(M, N)
-    got = run_q8_0(A, blocks, M, N, K, bias=bias).reshape(M, N)
+    got = run_q8_0(A, blocks, M, N, K, bias=bias, ws=True).reshape(M, N)
     assert_parity(got, want, what=f"cfg {cfg} mode0")
     C0 = oracle.normal(14, M * N)
-    got1 = run_q8_0(A, blocks, M, N, K, C0=C0, mode=1).reshape(M, N)
+    got1 = run_q8_0(A, blocks, M, N, K, C0=C0, mode=1, ws=True).reshape(M, N)
     assert_parity(got1 - C0.reshape(M, N), want - bias, what=f"cfg {cfg} mode1")
     payload, scales = oracle.q8_0_to_split(blocks, N * K)
     dC = DeviceBuffer(M * N * 4)
     ops.gemm_nt_q8_bias(DeviceBuffer.from_array(A), DeviceBuffer.from_array(payload), dC,
-                        DeviceBuffer.from_array(scales), DeviceBuffer.from_array(bias), M, N, K)
+                        DeviceBuffer.from_array(scales), DeviceBuffer.from_array(bias), M, N, K,
+                        workspace=workspace(M, N, K))
     synchronize()
     assert_parity(dC.download(np.float32, M * N).reshape(M, N), want, what=f"cfg {cfg} split layout")

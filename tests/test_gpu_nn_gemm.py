@@ -20,9 +20,13 @@ def split_weight(oracle, seed, M, K):
     return oracle.q8_0_to_split(q8_weights(oracle, seed, M, K), M * K)
 
 
-def run_nn(payload, scales, B, M, N, K, C0=None, csize=None, **kw):
+def run_nn(payload, scales, B, M, N, K, C0=None, csize=None, ws=False, **kw):
+    """ws: through mi_gemm_nn_q8_split_ws with the workspace the library asks for (K splits)."""
     dq, ds, dB = DeviceBuffer.from_array(payload), DeviceBuffer.from_array(scales), DeviceBuffer.from_array(B)
     dC = DeviceBuffer.from_array(C0) if C0 is not None else DeviceBuffer(csize * 4)
+    if ws:
+        n = ops.gemm_nn_workspace_bytes(M, N, K, kw.get("batch", 1))
+        kw["workspace"] = DeviceBuffer(n) if n else None
     ops.gemm_nn_q8(dq, ds, dB, dC, M, N, K, **kw)
     synchronize()
     return dC.download(np.float32, C0.size if C0 is not None else csize)
@@ -71,9 +75,10 @@ def test_nn_batch_strides_and_flat_scales(gpu, oracle):
 @pytest.mark.parametrize("mode", [0, 1])
 def test_nn_tiled_strides_and_k_splits(gpu, oracle, monkeypatch, kernel, mode):
     """The tiled kernel (K % 64 == 0, lda and sA multiples of 16) with batch /
-    leading dimensions, and with K split across workgroups (64 x 64 x 1024: one
-    tile, four splits adding with atomics); MI_NN_KERNEL=general runs the same
-    cases on the untiled kernel."""
+    leading dimensions, and with K split across workgroups through the
+    workspace (64 x 64 x 1024: one tile, four splits summed in order by the
+    reduce pass); MI_NN_KERNEL=general runs the same cases on the untiled
+    kernel."""
     if kernel == "general":
         monkeypatch.setenv("MI_NN_KERNEL", "general")
     else:
@@ -88,7 +93,7 @@ def test_nn_tiled_strides_and_k_splits(gpu, oracle, monkeypatch, kernel, mode):
     C0 = oracle.normal(63, (batch - 1) * sC + M * ldc)
     kw = dict(lda=lda, ldb=ldb, ldc=ldc, batch=batch, sA=sA, sB=sB, sC=sC, mode=mode)
     want = oracle.gemm_nn_q8_split(payload, scales, B, M, N, K, C=C0.copy(), threads=oracle.max_threads(), **kw)
-    got = run_nn(payload, scales, B, M, N, K, C0=C0, **kw)
+    got = run_nn(payload, scales, B, M, N, K, C0=C0, ws=True, **kw)
     for z in range(batch):
         g = got[z * sC: z * sC + M * ldc].reshape(M, ldc)
         w = want[z * sC: z * sC + M * ldc].reshape(M, ldc)
@@ -103,7 +108,7 @@ def test_nn_tiled_strides_and_k_splits(gpu, oracle, monkeypatch, kernel, mode):
     B = oracle.normal(65, K * N)
     C0 = oracle.normal(66, M * N)
     want = oracle.gemm_nn_q8_split(payload, scales, B, M, N, K, C=C0.copy(), mode=mode, threads=oracle.max_threads())
-    got = run_nn(payload, scales, B, M, N, K, C0=C0, mode=mode)
+    got = run_nn(payload, scales, B, M, N, K, C0=C0, mode=mode, ws=True)
     if mode == 1:
         assert_parity(got - C0, want - C0, what=f"{kernel} K split mode 1")
     else:
@@ -121,7 +126,7 @@ def test_nn_conv_shapes_sampled_rows(gpu, oracle, M, N, K):
     print(f"[case] nn conv M={M} N={N} K={K}", flush=True)
     payload, scales = split_weight(oracle, 31, M, K)
     B = oracle.normal(32, K * N)
-    got = run_nn(payload, scales, B, M, N, K, csize=M * N).reshape(M, N)
+    got = run_nn(payload, scales, B, M, N, K, csize=M * N, ws=True).reshape(M, N)
     rng = np.random.default_rng(M + N + K)
     rows = np.unique(np.concatenate([[0, M - 1, min(63, M - 1), min(64, M - 1)], rng.integers(0, M, 24)]))
     # the oracle on the selected weight rows only (rows of C depend on rows of A)

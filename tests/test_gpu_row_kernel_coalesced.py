@@ -12,7 +12,7 @@ import pytest
 from helpers import REL_RMS_TOL, assert_parity, err_vs_rms, q8_weights
 from sdvk_amd import ops
 from sdvk_amd.hip import DeviceBuffer, synchronize
-from test_gpu_gemm import run_q8_0
+from test_gpu_gemm import run_q8_0, workspace
 
 pytestmark = pytest.mark.gpu
 
@@ -26,15 +26,16 @@ def test_coalesced_rows_config(gpu, oracle, monkeypatch, cfg, M, N, K):
     blocks = q8_weights(oracle, 12, N, K)
     bias = oracle.normal(13, N, 0.0, 0.02)
     want = oracle.gemm_nt_q8_0(A, blocks, M, N, K, bias=bias, threads=oracle.max_threads()).reshape(M, N)
-    got = run_q8_0(A, blocks, M, N, K, bias=bias).reshape(M, N)
+    got = run_q8_0(A, blocks, M, N, K, bias=bias, ws=True).reshape(M, N)
     assert_parity(got, want, what=f"cfg {cfg} mode0")
     C0 = oracle.normal(14, M * N)
-    got1 = run_q8_0(A, blocks, M, N, K, C0=C0, mode=1).reshape(M, N)
+    got1 = run_q8_0(A, blocks, M, N, K, C0=C0, mode=1, ws=True).reshape(M, N)
     assert_parity(got1 - C0.reshape(M, N), want - bias, what=f"cfg {cfg} mode1")
     payload, scales = oracle.q8_0_to_split(blocks, N * K)
     dC = DeviceBuffer(M * N * 4)
     ops.gemm_nt_q8_bias(DeviceBuffer.from_array(A), DeviceBuffer.from_array(payload), dC,
-                        DeviceBuffer.from_array(scales), DeviceBuffer.from_array(bias), M, N, K)
+                        DeviceBuffer.from_array(scales), DeviceBuffer.from_array(bias), M, N, K,
+                        workspace=workspace(M, N, K))
     synchronize()
     assert_parity(dC.download(np.float32, M * N).reshape(M, N), want, what=f"cfg {cfg} split layout")
 

@@ -50,8 +50,13 @@ FAMILIES = {
         dict(M=130, N=257, K=320), dict(M=130, N=257, K=320, mode=1), dict(M=154, N=96, K=2048),
         dict(M=60, N=40, K=100, layout="split"), dict(M=77, N=96, K=64, layout="split", mode=1),
         dict(M=300, N=300, K=256, cfg="0"), dict(M=300, N=200, K=256, cfg="1", layout="split"),
-        # K splits: the 16-byte fill of C with an unaligned bias, and the scalar fill (N % 4 != 0)
+        # K splits (partials in the workspace, fixed-order reduce): 16-byte reduce with an unaligned
+        # bias, the scalar reduce (N % 4 != 0), mode 1; the same shape without a workspace (no split)
         dict(M=154, N=96, K=2048, bias_off=1), dict(M=154, N=98, K=2048, mode=0),
+        dict(M=154, N=96, K=2048, mode=1), dict(M=154, N=96, K=2048, ws=False),
+        # the any-K kernel (split layout): K % 4 != 0, an A only 4-byte aligned, modes 1 / 2
+        dict(M=70, N=50, K=37, layout="split"), dict(M=100, N=100, K=96, layout="split", a_off=1),
+        dict(M=65, N=33, K=70, layout="split", mode=1, lda=75), dict(M=65, N=33, K=5, layout="split", mode=2),
         dict(M=130, N=100, K=128, cfg="2"), dict(M=70, N=70, K=128, cfg="3", front=True),
         dict(M=300, N=300, K=256, cfg="4"), dict(M=200, N=300, K=512, cfg="0:3"),
         dict(M=70, N=36, K=64, batch=3, lda=72, ldc=40, sA=5200, sC=3000),
@@ -97,7 +102,8 @@ FAMILIES = {
         dict(M=130, N=260, K=128), dict(M=300, N=520, K=640, mode=1), dict(M=64, N=64, K=1024),
         dict(M=70, N=36, K=256, batch=3, lda=272, ldb=40, ldc=44, sA=19056, sB=10248, sC=3100),
         dict(M=129, N=300, K=256, front=True), dict(M=130, N=260, K=128, kernel="general"),
-        dict(M=129, N=300, K=256, ldc=302),  # K splits, ldc % 4 != 0: the per-column clear of C
+        dict(M=129, N=300, K=256, ldc=302),  # K splits, ldc % 4 != 0: the scalar reduce pass
+        dict(M=300, N=520, K=640, mode=1, ws=False),  # no workspace: no split
     ],
     "attention": [
         dict(Tq=100, Tk=300, C=128, heads=2), dict(Tq=100, Tk=300, C=128, heads=2, causal=True),
@@ -195,23 +201,26 @@ def test_kernels_on_emulator(emulator, family):
 
 
 # The tile rules at the SDXL shapes of the benchmark: (op, dims, grid, work-items
-# per workgroup). GEMM (choose in gemm_q8.hip): 256x256 with 8 waves when it gives
-# >= 160 tiles, M >= 4096 and K <= 2048; 128x128 (4 waves) when that gives
-# >= 1024 tiles and K <= 2048; 256x128 (8 waves) for >= 128 tiles; K >= 4096
-# with >= 64 such tiles: 256x128 with two K splits; 64x64 (4 waves) for >= 512
-# tiles; else 64x64 with K split to about 256 workgroups (powers of two, >= 128 k
-# per split). Grid = (tiles, splits, batch). NN GEMM: 128x256 tiles (8 waves),
-# grid (N tiles, M tiles, splits), K splits doubled while tiles x splits < 256
+# per workgroup). GEMM (choose in gemm_q8.hip): 192x256 (8 waves) when that gives
+# >= 120 tiles and K >= 1280; 128x128 (4 waves) when that gives >= 160 tiles;
+# else 64x64 (4 waves). Grid = (tiles, splits, batch). With a workspace
+# ("gemm_ws"): 128x128 grids under 256 tiles with K >= 4096 split K in two, 64x64
+# grids under 512 tiles split K (powers of two) to about 256 workgroups with
+# >= 128 k per split. NN GEMM: 128x256 tiles (8 waves), grid (N tiles, M tiles,
+# splits); with a workspace ("nn_ws") K splits double while tiles x splits < 256
 # and each split keeps >= 4 steps of 64. fp16 attention: 4-wave workgroups of
 # 128 queries when that gives >= 512 workgroups, else 2-wave ones of 64.
 ROUTING = [
-    ["gemm", [8192, 640, 640], [160, 1, 1], 512], ["gemm", [8192, 5120, 640], [640, 1, 1], 512],
-    ["gemm", [8192, 640, 2560], [160, 1, 1], 512], ["gemm", [2048, 1280, 1280], [640, 1, 1], 256],
-    ["gemm", [2048, 10240, 1280], [1280, 1, 1], 256], ["gemm", [2048, 1280, 5120], [80, 2, 1], 512],
-    ["gemm", [154, 640, 2048], [30, 8, 1], 256], ["gemm", [154, 1280, 2048], [60, 4, 1], 256],
-    ["gemm", [9216, 1280, 1280], [180, 1, 1], 512],
-    ["nn", [320, 4096, 2880], [16, 3, 8], 512], ["nn", [640, 4096, 5760], [16, 5, 4], 512],
-    ["nn", [1280, 1024, 11520], [4, 10, 8], 512], ["nn", [1280, 1024, 640], [4, 10, 2], 512],
+    ["gemm", [8192, 640, 640], [320, 1, 1], 256], ["gemm", [8192, 5120, 640], [2560, 1, 1], 256],
+    ["gemm", [8192, 640, 2560], [129, 1, 1], 512], ["gemm", [2048, 1280, 1280], [160, 1, 1], 256],
+    ["gemm", [2048, 10240, 1280], [440, 1, 1], 512], ["gemm", [2048, 1280, 5120], [160, 1, 1], 256],
+    ["gemm_ws", [2048, 1280, 5120], [160, 2, 1], 256],
+    ["gemm", [154, 640, 2048], [30, 1, 1], 256], ["gemm_ws", [154, 640, 2048], [30, 8, 1], 256],
+    ["gemm", [154, 1280, 2048], [60, 1, 1], 256], ["gemm_ws", [154, 1280, 2048], [60, 4, 1], 256],
+    ["gemm", [9216, 1280, 1280], [240, 1, 1], 512], ["gemm_ws", [9216, 1280, 1280], [240, 1, 1], 512],
+    ["nn_ws", [320, 4096, 2880], [16, 3, 8], 512], ["nn_ws", [640, 4096, 5760], [16, 5, 4], 512],
+    ["nn_ws", [1280, 1024, 11520], [4, 10, 8], 512], ["nn_ws", [1280, 1024, 640], [4, 10, 2], 512],
+    ["nn", [1280, 1024, 11520], [4, 10, 1], 512],
     ["attn", [2, 10, 4096, 4096], [640, 1, 1], 256], ["attn", [2, 20, 1024, 1024], [640, 1, 1], 128],
     ["attn", [2, 10, 4096, 77], [640, 1, 1], 256], ["attn", [2, 20, 1024, 77], [640, 1, 1], 128],
 ]

@@ -12,19 +12,16 @@ from sdvk_amd import profiling as p
 ATTN_F16 = "_ZN2mi12_GLOBAL__N_115attn_f16_kernelIDF16_Li4EEEvNS0_8AttnArgsEj"
 GEMM = "_ZN2mi12_GLOBAL__N_114gemm_q8_kernelILi256ELi128ELi4ELi2ELi2ELi0ELb0ELb0ELi2ELi0EEEvNS0_8GemmArgsE"
 ROWS = "_ZN2mi12_GLOBAL__N_119gemm_q8_rows_kernelILi8ELi0ELb0ELb1ELi0EEEvNS0_8GemmArgsE"
-INIT = "_ZN2mi12_GLOBAL__N_116gemm_init_kernelEPfPKfjjjm"
-INIT_VEC = "_ZN2mi12_GLOBAL__N_120gemm_init_vec_kernelEPfPKfjjjmj"
-BIAS_VEC = "_ZN2mi12_GLOBAL__N_124gemm_bias_add_vec_kernelEPfPKfjjjmj"
+INIT = "_ZN2mi12_GLOBAL__N_116gemm_fill_kernelEPfPKfjjjmj"
+REDUCE = "_ZN2mi12_GLOBAL__N_120splitk_reduce_kernelILi0ELb1EEEvPKfmjPfS3_jjjmj"
+ANY = "_ZN2mi12_GLOBAL__N_118gemm_q8_any_kernelENS0_8GemmArgsE"
 NN = "_ZN2mi12_GLOBAL__N_123gemm_nn_q8_tiled_kernelILb1EEEvNS0_6NnArgsE"
-NN_ZERO = "_ZN2mi12_GLOBAL__N_119gemm_nn_zero_kernelEPfjjjj"
-NN_ZERO_VEC = "_ZN2mi12_GLOBAL__N_123gemm_nn_zero_vec_kernelEPfjjjj"
 COPY = "__amd_rocclr_copyBuffer"
 
 
 @pytest.mark.parametrize("name,family,main", [
     (ATTN_F16, "attention", True), (GEMM, "gemm_q8", True), (ROWS, "gemm_q8", True), (INIT, "gemm_q8", False),
-    (INIT_VEC, "gemm_q8", False), (BIAS_VEC, "gemm_q8", False),
-    (NN, "gemm_nn_q8", True), (NN_ZERO, "gemm_nn_q8", False), (NN_ZERO_VEC, "gemm_nn_q8", False),
+    (REDUCE, "gemm_q8", False), (ANY, "gemm_q8", True), (NN, "gemm_nn_q8", True),
     (COPY, None, None),
     ("void mi::(anonymous namespace)::gemm_q8_kernel<64, 64, 2, 2, 2, 0, true, false, 2, 0>(mi::GemmArgs)",
      "gemm_q8", True),
@@ -54,14 +51,14 @@ def test_stats_report_aggregates_per_call(tmp_path):
                     [INIT, 2, 20000, 10000, 2, 9000, 11000],
                     [ROWS, 2, 100000, 50000, 10, 50000, 50000],
                     [ATTN_F16, 3, 300000, 100000, 30, 100000, 100000],
-                    [NN, 1, 50000, 50000, 5, 50000, 50000], [NN_ZERO, 1, 5000, 5000, 0.5, 5000, 5000],
+                    [NN, 1, 50000, 50000, 5, 50000, 50000],
                     [COPY, 1, 1000, 1000, 0.1, 1000, 1000]])
     md = p.stats_report(str(f), "cmd")
     agg = {l.split("|")[1].strip(): float(l.split("|")[3]) for l in md.splitlines()
            if l.startswith("| ") and l.count("|") == 4 and not l.startswith("| family")}
     assert agg["gemm_q8"] == pytest.approx((400000 + 20000 + 100000) / 6 / 1e3, abs=0.01)  # 6 calls, helpers timed
     assert agg["attention"] == pytest.approx(100.0, abs=0.01)
-    assert agg["gemm_nn_q8"] == pytest.approx(55.0, abs=0.01)
+    assert agg["gemm_nn_q8"] == pytest.approx(50.0, abs=0.01)
     assert "attn_f16_kernel<_Float16, 4>" in md
 
 
