@@ -972,6 +972,244 @@ __global__ __launch_bounds__(256) void gemm_q8_rows_kernel(GemmArgs a) {
                                      acc, lane);
 }
 
+// ---- producer / consumer kernel -------------------------------------------------------
+//
+// One workgroup = 8 waves, two per SIMD, for a 192 x 256 tile (BM x BN), one
+// Q8_0 block (32 k) per step:
+//   * waves 4-7 (producers) only move data: each of their 256 threads keeps
+//     three register sets of raw loads in flight (A: six 16-byte pieces, W:
+//     one whole block, 36-byte window) and, one step at a time, rounds A to
+//     fp16 and dequantises its W block into an LDS stage;
+//   * waves 0-3 (consumers, 2 x 2, 96 x 128 each) only read fragments and
+//     issue v_mfma_f32_32x32x16_f16 (3 x 4 accumulator tiles per wave).
+// Two waves share each SIMD, so the producers' VALU work and memory waits
+// overlap the consumers' MFMAs in hardware instead of in one instruction
+// stream. Three LDS stages: step t lives in stage t % 3, written by the
+// producers two steps ahead of its use, so the consumers read the first
+// fragments of step t + 1 before the barrier that ends step t (stage
+// (t + 1) % 3 was complete one barrier earlier). One barrier per step; both
+// roles pass the same number of barriers. The sums run over k16 slices in
+// the same order as every other build, so an unsplit call gives the same bits.
+template <int WK, bool SPLITK, int EPI = kEpiPlain>
+__global__ __launch_bounds__(512) void gemm_q8_pc_kernel(GemmArgs a) {
+    constexpr int BM = 192, BN = 256, BK = 32, LDK = 40;  // LDS row stride in halves (32 k + 16-byte pad)
+    constexpr int WMC = 96, WNC = 128, FM = 3, FN = 4;   // consumer wave tile, 32x32 MFMA tiles per wave
+    constexpr int NP = 256;                              // producer threads
+    constexpr int A_IT = BM * BK / 4 / NP;               // 16-byte A pieces per producer thread and step (6)
+    constexpr int kStage = (BM + BN) * LDK;              // halves per LDS stage
+    constexpr int kOperandHalves = 3 * kStage;
+    constexpr int kStageHalves = 2 * 4 * kStageFloats;   // epilogue staging of the 4 consumer waves
+    static_assert(BN == NP, "one W block per producer thread and step");
+    __shared__ __attribute__((aligned(16))) _Float16 smem[kOperandHalves > kStageHalves ? kOperandHalves : kStageHalves];
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+
+    const unsigned lin = xcd_swizzle(blockIdx.x, gridDim.x);
+    const uint32_t gsz = a.group_m * a.tiles_n;
+    const uint32_t grp = lin / gsz, rem = lin % gsz;
+    const uint32_t rows_in = min(a.group_m, a.tiles_m - grp * a.group_m);
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((grp * a.group_m + rem % rows_in) * BM);
+    const uint32_t n0 = __builtin_amdgcn_readfirstlane((rem / rows_in) * (EPI == kEpiGeglu ? BN / 2 : BN));
+    const uint32_t s_begin = SPLITK ? blockIdx.y * a.steps_per_split : 0;
+    const uint32_t s_end = SPLITK ? min(a.ksteps, s_begin + a.steps_per_split) : a.ksteps;
+    const uint32_t n_steps = s_end - s_begin;  // >= 1
+
+    if (wave >= 4) {
+        // ---------------- producers ----------------
+        const int pt = tid - 256;  // 0..255
+        const float* Apanel = a.A + static_cast<uint64_t>(blockIdx.z) * a.sA + static_cast<uint64_t>(m0) * a.lda;
+        const uint32_t a_bytes = ((min(a.M - m0, static_cast<uint32_t>(BM)) - 1) * a.lda + a.K) * 4;
+        const __amdgpu_buffer_rsrc_t rA =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Apanel), 0, static_cast<int>(a_bytes), 0x00020000);
+        const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t*>(a.W), 0, WK == kBlocks34 ? static_cast<int>((a.N * a.rowbytes + 15u) & ~15u) : -1,
+            0x00020000);
+        const __amdgpu_buffer_rsrc_t rS =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(WK == kSplit ? a.scales : a.A), 0, -1, 0x00020000);
+        // A piece i of a step: row (pt + 256 i) / 8, 16-byte chunk (pt + 256 i) % 8
+        uint32_t a_off[A_IT];
+#pragma unroll
+        for (int i = 0; i < A_IT; ++i) {
+            const int u = pt + NP * i;
+            const uint32_t row = min(m0 + u / 8, a.M - 1) - m0;
+            a_off[i] = (row * a.lda + (u % 8) * 4) * 4;
+        }
+        // W: column n0 + pt (GEGLU: value / gate rows interleaved per 32 columns)
+        const uint32_t wn = EPI == kEpiGeglu ? geglu_wrow(n0, pt, a.F) : min(n0 + static_cast<uint32_t>(pt), a.N - 1);
+        // 34-byte layout: block of step ks at byte wn * rowbytes + 34 ks; the 36-byte window starts at its
+        // 4-byte-aligned floor and the block sits 0 or 2 bytes into it (v_perm selectors per step)
+        const uint32_t wrow = WK == kBlocks34 ? wn * a.rowbytes : wn * a.K;
+
+        floatx4 ar[3][A_IT];
+        uint32_t wx[3][9];
+        auto load = [&](uint32_t ks_in, auto R) {
+            constexpr int r = decltype(R)::value;
+            const uint32_t ks = __builtin_amdgcn_readfirstlane(ks_in);
+#pragma unroll
+            for (int i = 0; i < A_IT; ++i)
+                ar[r][i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rA, a_off[i], ks * BK * 4, 0));
+            if constexpr (WK == kBlocks34) {
+                const uint32_t w0 = (wrow + 34u * ks) & ~3u;
+                const auto x0 = __builtin_amdgcn_raw_buffer_load_b128(rW, w0, 0, 0);
+                const auto x1 = __builtin_amdgcn_raw_buffer_load_b128(rW, w0 + 16, 0, 0);
+                wx[r][8] = __builtin_amdgcn_raw_buffer_load_b32(rW, w0 + 32, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    wx[r][e] = x0[e];
+                    wx[r][4 + e] = x1[e];
+                }
+            } else {
+                const uint32_t w0 = wrow + 32u * ks;
+                const auto x0 = __builtin_amdgcn_raw_buffer_load_b128(rW, w0, 0, 0);
+                const auto x1 = __builtin_amdgcn_raw_buffer_load_b128(rW, w0 + 16, 0, 0);
+                wx[r][8] = __builtin_amdgcn_raw_buffer_load_b32(rS, (w0 >> 5) * 4, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    wx[r][e] = x0[e];
+                    wx[r][4 + e] = x1[e];
+                }
+            }
+        };
+        auto store = [&](uint32_t ks, auto R) {
+            constexpr int r = decltype(R)::value;  // register set = LDS stage
+            _Float16* As = smem + r * kStage;
+            _Float16* Ws = As + BM * LDK;
+#pragma unroll
+            for (int i = 0; i < A_IT; ++i) {
+                const int u = pt + NP * i;
+                half4 h;
+                h[0] = static_cast<_Float16>(ar[r][i][0]);
+                h[1] = static_cast<_Float16>(ar[r][i][1]);
+                h[2] = static_cast<_Float16>(ar[r][i][2]);
+                h[3] = static_cast<_Float16>(ar[r][i][3]);
+                *reinterpret_cast<half4*>(&As[(u / 8) * LDK + (u % 8) * 4]) = h;
+            }
+            const uint32_t* x = wx[r];
+            _Float16* dst = &Ws[pt * LDK];
+            if constexpr (WK == kBlocks34) {
+                const bool sh = ((wrow + 34u * ks) & 2u) != 0;
+                const uint32_t qsel = sh ? 0x07060504u : 0x05040302u;  // bytes 4..7 or 2..5 of (x[j+1]:x[j])
+                const uint32_t dsel = sh ? 0x0c0c0302u : 0x0c0c0100u;  // bytes 2,3 or 0,1 of x[0]; 0x0c = zero
+                const _Float16 d = __builtin_bit_cast(_Float16, static_cast<uint16_t>(__builtin_amdgcn_perm(x[0], x[0], dsel)));
+                uint32_t q[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) q[j] = __builtin_amdgcn_perm(x[j + 1], x[j], qsel);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) *reinterpret_cast<half8*>(dst + 8 * j) = dequant8_f16(q[2 * j], q[2 * j + 1], d);
+            } else {
+                const float sc = __builtin_bit_cast(float, x[8]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) *reinterpret_cast<half8*>(dst + 8 * j) = dequant8_f32(x[2 * j], x[2 * j + 1], sc, sc);
+            }
+        };
+        using R0 = std::integral_constant<int, 0>;
+        using R1 = std::integral_constant<int, 1>;
+        using R2 = std::integral_constant<int, 2>;
+        const uint32_t last = s_end - 1;
+        auto ph = [&](uint32_t t) { return min(s_begin + t, last); };  // clamped step (loads past the end re-read it)
+        // A step's work stays between its barriers (sched_barrier): left free, the compiler moves the
+        // conversions of later register sets up across the barriers, and the waits for their loads
+        // then take the prefetch lead away.
+        auto barrier = [] {
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        // Each step first consumes its register set completely (the oldest loads in flight, so the
+        // in-order vmcnt wait retires only them), then refills it: a refill hoisted above the
+        // consumption makes the wait retire the newer sets' loads as well.
+        auto step = [&](uint32_t t_store, uint32_t t_load, auto R) {
+            store(t_store, R);
+            __builtin_amdgcn_sched_barrier(0);
+            load(t_load, R);
+        };
+        load(ph(0), R0{});
+        load(ph(1), R1{});
+        load(ph(2), R2{});
+        step(ph(0), ph(3), R0{});
+        __builtin_amdgcn_sched_barrier(0);
+        step(ph(1), ph(4), R1{});
+        barrier();
+        // iteration j converts step j + 2 into stage (j + 2) % 3 (harmless past the end: that stage is
+        // never read again) and refills its register set with step j + 5
+        uint32_t j = 0;
+        for (; j + 3 <= n_steps; j += 3) {
+            step(ph(j + 2), ph(j + 5), R2{});
+            barrier();
+            step(ph(j + 3), ph(j + 6), R0{});
+            barrier();
+            step(ph(j + 4), ph(j + 7), R1{});
+            barrier();
+        }
+        // the last one or two steps were stored by earlier iterations: only the barriers remain
+        for (; j < n_steps; ++j) __syncthreads();
+        return;
+    }
+
+    // ---------------- consumers ----------------
+    const int wm = wave & 1, wn = wave >> 1;
+    const int l32 = lane & 31, g = lane >> 5;
+    floatx16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int jn = 0; jn < FN; ++jn)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][jn][r] = 0.0f;
+
+    half8 fa[2][FM], fb[2][FN];  // fragments of a k16 slice: [slice parity]
+    auto read = [&](int stage, int s, int p) {
+        const _Float16* As = smem + stage * kStage;
+        const _Float16* Ws = As + BM * LDK;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+            fa[p][i] = *reinterpret_cast<const half8*>(&As[(wm * WMC + 32 * i + l32) * LDK + 16 * s + 8 * g]);
+#pragma unroll
+        for (int jn = 0; jn < FN; ++jn)
+            fb[p][jn] = *reinterpret_cast<const half8*>(&Ws[(wn * WNC + 32 * jn + l32) * LDK + 16 * s + 8 * g]);
+    };
+    auto mfma = [&](int p) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int jn = 0; jn < FN; ++jn)
+                if constexpr (SPLITK)
+                    acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[p][i], fb[p][jn], acc[i][jn], 0, 0, 0);
+                else
+                    acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[p][jn], fa[p][i], acc[i][jn], 0, 0, 0);
+    };
+    __syncthreads();
+    read(0, 0, 0);
+    int st = 0;
+    for (uint32_t j = 0; j < n_steps; ++j) {
+        const int nx = st == 2 ? 0 : st + 1;
+        read(st, 1, 1);
+        mfma(0);
+        // step j + 1 was stored one barrier ago: its first slice is read before this step's barrier
+        // (after the last step this reads a stage no producer writes any more; the values go unused)
+        read(nx, 0, 0);
+        mfma(1);
+        // slice 0's MFMAs carry slice 1's fragment reads, slice 1's MFMAs the next step's slice 0
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < FM * FN; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if (i < FM + FN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+        __builtin_amdgcn_sched_barrier(0);  // every MFMA of the step is issued before the barrier
+        __syncthreads();
+        st = nx;
+    }
+
+    float* C = a.C + static_cast<uint64_t>(blockIdx.z) * a.sC + (SPLITK ? blockIdx.y * a.split_stride : 0);
+    // the producers' last LDS writes precede the loop's last barrier: the staging area is free
+    store_tiles<FM, FN, SPLITK, EPI>(a, C, reinterpret_cast<float*>(smem) + wave * kStageFloats, m0 + wm * WMC,
+                                     EPI == kEpiGeglu ? n0 + wn * WNC / 2 : n0 + wn * WNC, acc, lane);
+}
+
 // K == 0: C[m, n] = bias[n] (or 0) in mode 0, C[m, n] += bias[n] in mode 2.
 __global__ __launch_bounds__(256) void gemm_fill_kernel(float* C, const float* bias, uint32_t M, uint32_t N,
                                                         uint32_t ldc, uint64_t sC, uint32_t add) {
@@ -1073,6 +1311,7 @@ enum CfgId {
     kC256x256W4,                                              // LDS kernel, 4 waves of 128x128, one set in flight
     kC256x128W4, kC128x256W4,                                 // LDS kernel, 4 waves of 128x64 / 64x128
     kC192x256,                                                // LDS kernel, 8 waves of 96x64
+    kP192x256,                                                // producer / consumer kernel
     kNumCfg
 };
 
@@ -1201,9 +1440,37 @@ void launch_rows(const GemmArgs& a0, uint32_t batch, uint32_t splits, float* ws,
     }
 }
 
+// Producer / consumer kernel: 192 x 256 tiles, one Q8_0 block per step (K % 32 == 0).
+template <int WK, int EPI = kEpiPlain>
+void launch_pc(const GemmArgs& a0, uint32_t batch, uint32_t splits, float* ws, hipStream_t s) {
+    GemmArgs a = a0;
+    constexpr uint32_t BM = 192, BN = 256;
+    a.tiles_n = EPI == kEpiGeglu ? ceil_div(a.F, BN / 2) : ceil_div(a.N, BN);
+    if (EPI == kEpiGeglu || !ws) splits = 1;
+    a.tiles_m = ceil_div(a.M, BM);
+    a.group_m = pick_group(a.tiles_m, a.tiles_n, BM, BN, a.K);
+    a.ksteps = a.K / 32;
+    const unsigned tiles = a.tiles_m * a.tiles_n;
+    if (splits > 1) {
+        a.steps_per_split = ceil_div(a.ksteps, splits);
+        splits = ceil_div(a.ksteps, a.steps_per_split);
+    }
+    if (splits > 1) {
+        if constexpr (EPI != kEpiGeglu) {
+            const GemmArgs p = partial_args(a, splits, ws);
+            gemm_q8_pc_kernel<WK, true><<<dim3(tiles, splits, batch), 512, 0, s>>>(p);
+            finish_split<EPI>(a, splits, ws, batch, s);
+        }
+    } else {
+        a.steps_per_split = a.ksteps;
+        gemm_q8_pc_kernel<WK, false, EPI><<<dim3(tiles, 1, batch), 512, 0, s>>>(a);
+    }
+}
+
 template <int WK, int EPI = kEpiPlain>
 void launch(int cfg, const GemmArgs& a, uint32_t batch, uint32_t splits, float* ws, hipStream_t s) {
     switch (cfg) {
+        case kP192x256: launch_pc<WK, EPI>(a, batch, splits, ws, s); break;
         case kR256x256: launch_rows<8, WK, false, EPI>(a, batch, splits, ws, s); break;
         case kR256x256Q: launch_rows<8, WK, true, EPI>(a, batch, splits, ws, s); break;
         case kR256x192Q: launch_rows<6, WK, true, EPI>(a, batch, splits, ws, s); break;

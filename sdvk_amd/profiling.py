@@ -14,9 +14,14 @@ Two reports, both plain text so they can be kept next to the source:
   --copy-probe-mib``): the copy reads and writes exactly that many bytes, so
   ``factor = bytes / (counter x 1024)``.
 
+* ``counters``: ``*_counter_collection.csv`` files of other ``--pmc`` passes
+  (MFMA / VALU busy cycles, LDS bank conflicts, wait cycles) averaged per
+  kernel and grid, with the derived busy fractions.
+
 Usage:
   python -m sdvk_amd.profiling stats  <kernel_stats.csv> <out.md> --command "<cmd>"
   python -m sdvk_amd.profiling traffic <fetch.csv> <write.csv> <copy_mib> <family> <out.json> --command "<cmd>"
+  python -m sdvk_amd.profiling counters <out.md> <counter_collection.csv>... --command "<cmd>"
 """
 from __future__ import annotations
 
@@ -154,6 +159,49 @@ def traffic_report(fetch_csv: str, write_csv: str, copy_mib: int, family: str, c
     return result
 
 
+# Derived figures of the counter report (per dispatch; the counters are summed
+# over the whole GPU). MFMA and VALU issue cycles are per SIMD, so the busy
+# fractions divide by the SIMD-cycles the dispatch had: GRBM_GUI_ACTIVE (GPU
+# busy cycles of the dispatch) x 256 CUs x 4 SIMDs.
+SIMDS = 256 * 4
+
+
+def counters_report(csv_paths: list[str], command: str, flops: dict | None = None) -> str:
+    """Per (kernel, grid): the average of every counter over the dispatches,
+    and MFMA busy / VALU busy / LDS bank conflicts per LDS instruction where
+    the counters are present. flops: {"kernel substring|grid": FLOP per dispatch}
+    adds the MFMA busy fraction implied by the algorithmic FLOP (1024 fp16 FLOP
+    per SIMD-cycle for v_mfma_f32_32x32x16_f16) for comparison."""
+    acc = collections.OrderedDict()
+    for path in csv_paths:
+        for r in csv.DictReader(open(path)):
+            key = (short_name(r["Kernel_Name"]), int(r["Grid_Size"]))
+            d = acc.setdefault(key, collections.defaultdict(list))
+            d[r["Counter_Name"]].append(float(r["Counter_Value"]))
+    names = sorted({c for d in acc.values() for c in d})
+    lines = ["# rocprofv3 counters per kernel and grid", "", f"Command: `{command}`", "",
+             "Averages per dispatch. mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 1024 SIMDs); "
+             "valu_busy = SQ_ACTIVE_INST_VALU / (GRBM_GUI_ACTIVE x 1024); lds_conflict_per_lds = "
+             "SQ_LDS_BANK_CONFLICT / SQ_INSTS_LDS; wait_frac = SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES.", ""]
+    hdr = ["kernel", "grid", "dispatches"] + names + ["mfma_busy", "valu_busy", "lds_conflict_per_lds", "wait_frac"]
+    lines += ["| " + " | ".join(hdr) + " |", "|" + "---|" * len(hdr)]
+    for (name, grid), d in acc.items():
+        avg = {c: sum(v) / len(v) for c, v in d.items()}
+        n = max(len(v) for v in d.values())
+        gui = avg.get("GRBM_GUI_ACTIVE")
+
+        def frac(num):
+            return f"{avg[num] / (gui * SIMDS):.3f}" if gui and num in avg else ""
+        conf = (f"{avg['SQ_LDS_BANK_CONFLICT'] / avg['SQ_INSTS_LDS']:.3f}"
+                if avg.get("SQ_INSTS_LDS") and "SQ_LDS_BANK_CONFLICT" in avg else "")
+        wait = (f"{avg['SQ_WAIT_INST_ANY'] / avg['SQ_WAVE_CYCLES']:.3f}"
+                if avg.get("SQ_WAVE_CYCLES") and "SQ_WAIT_INST_ANY" in avg else "")
+        row = [f"`{name}`", str(grid), str(n)] + [f"{avg[c]:.4g}" if c in avg else "" for c in names]
+        row += [frac("SQ_VALU_MFMA_BUSY_CYCLES"), frac("SQ_ACTIVE_INST_VALU"), conf, wait]
+        lines.append("| " + " | ".join(row) + " |")
+    return "\n".join(lines) + "\n"
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -168,8 +216,14 @@ def main(argv=None) -> int:
     t.add_argument("family", choices=sorted(FAMILIES))
     t.add_argument("out")
     t.add_argument("--command", required=True)
+    c = sub.add_parser("counters")
+    c.add_argument("out")
+    c.add_argument("csvs", nargs="+")
+    c.add_argument("--command", required=True)
     a = ap.parse_args(argv)
-    if a.cmd == "stats":
+    if a.cmd == "counters":
+        Path(a.out).write_text(counters_report(a.csvs, a.command))
+    elif a.cmd == "stats":
         Path(a.out).write_text(stats_report(a.csv, a.command))
     else:
         Path(a.out).write_text(json.dumps(traffic_report(a.fetch_csv, a.write_csv, a.copy_mib, a.family,

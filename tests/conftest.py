@@ -35,7 +35,7 @@ def oracle():
 
 
 def pytest_terminal_summary(terminalreporter):
-    """Worst parity error per test module (max |err| over the module's checks,
+    """Worst parity error per test function (max |err| over its checks,
     relative to RMS of the reference, and the share of its bar it used), so
     the margins show in a -q run's record."""
     from helpers import WORST
@@ -43,6 +43,7 @@ def pytest_terminal_summary(terminalreporter):
     if not WORST:
         return
     tr = terminalreporter
-    tr.write_sep("-", "parity margins: worst max|err| / RMS per test module")
-    for mod, (e, tol, test) in sorted(WORST.items()):
-        tr.write_line(f"{mod:<34} {e:.3e}  bar {tol:.1e}  ({100 * e / tol:5.1f}% of the bar)  {test}")
+    tr.write_sep("-", "parity margins: worst max|err| / RMS per test function")
+    for key, (e, tol, test) in sorted(WORST.items()):
+        case = test.split("::")[-1]
+        tr.write_line(f"{key:<64} {e:.3e}  bar {tol:.1e}  ({100 * e / tol:5.1f}% of the bar)  {case}")

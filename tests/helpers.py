@@ -15,15 +15,16 @@ def rms(x: np.ndarray) -> float:
     return float(np.sqrt(np.mean(x * x))) if x.size else 0.0
 
 
-# Worst parity error of this session per test module, {module: (err, bar, test)};
-# tests/conftest.py prints it in the terminal summary (visible under -q).
+# Worst parity error of this session per test function, {module::function:
+# (err, bar, test id)}; tests/conftest.py prints it in the terminal summary
+# (visible under -q).
 WORST: dict[str, tuple[float, float, str]] = {}
 
 
 def record(e: float, tol: float = REL_RMS_TOL) -> float:
     """Notes an error (relative to its bar `tol`) for the end-of-session summary."""
     test = os.environ.get("PYTEST_CURRENT_TEST", "").split(" ")[0]
-    mod = test.split("::")[0].rsplit("/", 1)[-1].removesuffix(".py") if test else "?"
+    mod = test.rsplit("/", 1)[-1].replace(".py", "").split("[")[0] if test else "?"
     prev = WORST.get(mod)
     if prev is None or e / tol > prev[0] / prev[1]:
         WORST[mod] = (float(e), float(tol), test)

@@ -294,12 +294,13 @@ def gemm_full(E, *, M, N, K, cfg=None, layout="q8_0", seed=1, order=0, tol=2e-3,
         call = lambda: E.call("mi_gemm_nt_q8_split" + sfx, dA.ptr, dP.ptr, dS.ptr, None, dC.ptr, M, N, K, 0, 0, 0, 1,
                               0, 0, *extra, None)
     helpers = "gemm_fill|-|-|-;splitk_reduce|-|-|-"  # the K == 0 fill and the split reduce pass
-    kern, grid = _probe_grid(E, f"gemm_q8_kernel|-|-|-;gemm_q8_rows_kernel|-|-|-;{helpers}", call)
+    kern, grid = _probe_grid(E, f"gemm_q8_kernel|-|-|-;gemm_q8_rows_kernel|-|-|-;gemm_q8_pc_kernel|-|-|-;{helpers}",
+                             call)
     assert not np.any(dC.get(np.float32, M * N)), "a launch with no workgroup wrote C"
     xs = sorted({0, _block_of_tile(grid[0] - 1, grid[0])})
     x = ",".join(map(str, xs))
     print(f"  {kern} grid {grid}, blockIdx.x {xs}", flush=True)
-    E.sample(f"gemm_q8_kernel|{x}|*|*;gemm_q8_rows_kernel|{x}|*|*;gemm_fill|-|-|-")
+    E.sample(f"gemm_q8_kernel|{x}|*|*;gemm_q8_rows_kernel|{x}|*|*;gemm_q8_pc_kernel|{x}|*|*;gemm_fill|-|-|-")
     before = E.lib.kemu_blocks_run()
     call()
     ran = E.lib.kemu_blocks_run() - before

@@ -51,6 +51,7 @@ typedef enum hipMemcpyKind {
 #define hipHostMallocDefault 0x0u
 
 inline hipError_t hipGetLastError() { return hipSuccess; }
+
 inline const char* hipGetErrorString(hipError_t e) { return e == hipSuccess ? "no error" : "emulated HIP error"; }
 // Asynchronous copies are deferred: they run at the event synchronisation that
 // covers them, before the next kernel launch, or at kemu_sync(), so a source

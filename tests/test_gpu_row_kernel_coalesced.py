@@ -40,7 +40,7 @@ def test_coalesced_rows_config(gpu, oracle, monkeypatch, cfg, M, N, K):
     assert_parity(dC.download(np.float32, M * N).reshape(M, N), want, what=f"cfg {cfg} split layout")
 
 
-@pytest.mark.parametrize("cfg", ["7", "11", "12", "13", "14"])
+@pytest.mark.parametrize("cfg", ["7", "11", "12", "13", "14", "15"])
 def test_candidate_config_baseline_shape(gpu, oracle, monkeypatch, cfg):
     M, N, K = 9216, 1280, 1280
     print(f"[case] cfg={cfg} baseline M={M} N={N} K={K}", flush=True)

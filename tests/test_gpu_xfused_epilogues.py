@@ -48,7 +48,7 @@ def test_residual_mode(gpu, oracle, monkeypatch, M, N, K, cfg):
 
 
 @pytest.mark.parametrize("M,F,K,cfg", [(77, 48, 64, None), (300, 200, 256, "4"), (130, 100, 96, None),
-                                       (2048, 5120, 1280, None), (300, 130, 256, "7")])
+                                       (2048, 5120, 1280, None), (300, 130, 256, "7"), (300, 130, 256, "15")])
 def test_geglu_gemm(gpu, oracle, monkeypatch, M, F, K, cfg):
     print(f"[case] gemm geglu M={M} F={F} K={K} cfg={cfg}", flush=True)
     if cfg:

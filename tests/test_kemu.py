@@ -69,6 +69,12 @@ FAMILIES = {
         dict(M=300, N=300, K=256, cfg="13:2"), dict(M=130, N=520, K=192, cfg="13", layout="split", front=True),
         # 192x256 (8 waves of 96x64)
         dict(M=400, N=300, K=256, cfg="14"), dict(M=200, N=260, K=320, cfg="14:2", layout="split", mode=1),
+        # producer / consumer 192x256 (4 loading waves, 4 MFMA waves, 3 LDS stages): 1, 2, 3 and more
+        # steps (the barrier bookkeeping of short K), K splits, the split layout, batch / strides
+        dict(M=300, N=520, K=32, cfg="15"), dict(M=193, N=257, K=64, cfg="15", mode=2),
+        dict(M=400, N=300, K=96, cfg="15", front=True), dict(M=400, N=300, K=256, cfg="15"),
+        dict(M=200, N=300, K=640, cfg="15:3"), dict(M=200, N=260, K=320, cfg="15", layout="split", mode=1),
+        dict(M=70, N=36, K=128, batch=2, lda=132, ldc=40, sA=9300, sC=3000, cfg="15:2", layout="split"),
     ],
     # row-stationary kernel: per-lane-row A (5, 6) and row-coalesced A (7-10)
     "gemm_rows": [
@@ -91,7 +97,8 @@ FAMILIES = {
         dict(case="gemm_geglu", M=70, F=40, K=128, cfg="1", bias=False),
         dict(case="gemm_nt", M=300, N=200, K=256, cfg="11", mode=2), dict(case="gemm_geglu", M=300, F=130, K=256, cfg="11"),
         dict(case="gemm_nt", M=200, N=300, K=256, cfg="12:2", mode=2), dict(case="gemm_geglu", M=200, F=260, K=128, cfg="13"),
-        dict(case="gemm_geglu", M=200, F=130, K=128, cfg="14"),
+        dict(case="gemm_geglu", M=200, F=130, K=128, cfg="14"), dict(case="gemm_geglu", M=200, F=130, K=128, cfg="15"),
+        dict(case="gemm_nt", M=200, N=300, K=256, cfg="15:2", mode=2),
     ],
     "gemm_nn": [
         dict(M=64, N=64, K=32), dict(M=100, N=72, K=96), dict(M=130, N=260, K=100, mode=1),
@@ -147,7 +154,7 @@ def _fullsize() -> list[dict]:
     for i, cfg in enumerate(bench.GEMM_CANDIDATES):
         M, N, K = g[i % len(g)]
         specs.append(dict(case="gemm_full", M=M, N=N, K=K, cfg=cfg))
-    for cfg in ("11", "12", "13", "14"):
+    for cfg in ("11", "12", "13", "14", "15"):
         for M, N, K in ((8192, 5120, 640), (2048, 1280, 5120)):
             specs.append(dict(case="gemm_full", M=M, N=N, K=K, cfg=cfg))
     specs += [dict(case="gemm_nn_full", M=M, N=N, K=K) for _, M, N, K in bench.NN_SHAPES]
