@@ -143,6 +143,25 @@ int mi_gemm_nt_q8_0_ws(const float* A, const void* W, const float* bias, float* 
                        uint32_t batch, uint64_t sA, uint64_t sC, void* workspace,
                        uint64_t workspace_bytes, void* stream);
 
+/* No-allocation variant of mi_gemm_nt_q8_0_ws (no counterpart in the
+ * reference). For callers that cannot allocate device memory: code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc. Same
+ * arguments, semantics and results (bit for bit) as mi_gemm_nt_q8_0_ws given a
+ * workspace of mi_gemm_nt_q8_workspace_bytes(M, N, K, batch) bytes, but the
+ * K-split partials go to a scratch array inside the library, one per GPU,
+ * of MI_GEMM_NOALLOC_SCRATCH_BYTES, held until the process ends. A shape whose
+ * plan needs more scratch than that returns MI_ERR_UNSUPPORTED (no shape does
+ * under the built-in tile rules: they split only grids of fewer than 256
+ * 128 x 128 tiles into at most 2 parts, or fewer than 512 64 x 64 tiles into
+ * about 256 workgroups, at most 32 MiB of partials). Calls on one GPU share
+ * the scratch: calls that overlap on one GPU (unordered streams) race, so
+ * order them (one stream). Calls no hipMalloc / hipFree; the scratch's device
+ * address is looked up once per GPU, on the first call made there.          */
+#define MI_GEMM_NOALLOC_SCRATCH_BYTES (32ull << 20)
+int mi_gemm_nt_q8_0_noalloc(const float* A, const void* W, const float* bias, float* C, uint32_t M,
+                            uint32_t N, uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldc,
+                            uint32_t batch, uint64_t sA, uint64_t sC, void* stream);
+
 /* Reference device layout: payload (int8 x4 per uint32, flat [N,K] order) +
  * fp32 scale per 32 flat elements (any fp32 value: LoRA requantisation writes
  * non-fp16 scales, sdvkgen.cpp:536-538). Any K, like the reference's scalar

@@ -78,6 +78,8 @@ SIGNATURES = {
     "mi_gemm_nt_q8_workspace_bytes": (_u64, [_u32, _u32, _u32, _u32]),
     "mi_gemm_nt_q8_0_ws": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32,
                                           _u64, _u64, _vp, _u64, _vp]),
+    "mi_gemm_nt_q8_0_noalloc": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32,
+                                               _u64, _u64, _vp]),
     "mi_gemm_nt_q8_split_ws": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32,
                                               _u32, _u64, _u64, _vp, _u64, _vp]),
     "mi_gemm_nt_q8_0_geglu": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp]),

@@ -26,6 +26,7 @@
 #include <type_traits>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 #include "common.hpp"
 
@@ -1673,9 +1674,12 @@ int check_ws(const char* fn, const void* ws, uint64_t ws_bytes, const void* A, u
     return MI_OK;
 }
 
+// fixed_ws: `ws` is the library's fixed-size scratch (the no-allocation
+// entry): a plan whose K-split partials exceed it is an error, not a reason to
+// run unsplit, so that the entry's results always equal the workspace entry's.
 int gemm_blocks(const char* fn, const float* A, const void* W, const float* bias, float* C, uint32_t M, uint32_t N,
                 uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldc, uint32_t batch, uint64_t sA, uint64_t sC,
-                void* ws, uint64_t ws_bytes, hipStream_t stream) {
+                void* ws, uint64_t ws_bytes, hipStream_t stream, bool fixed_ws = false) {
     if (M == 0 || N == 0) return MI_OK;
     if (K % 32) return fail(MI_ERR_UNSUPPORTED, "%s: K=%u is not a multiple of 32 (Q8_0 block)", fn, K);
     int st = validate(fn, A, W, C, M, N, K, mode, lda, ldc, batch, sA, sC, true);
@@ -1692,6 +1696,16 @@ int gemm_blocks(const char* fn, const float* A, const void* W, const float* bias
     if (K == 0) {
         if (mode == 0 || (mode == 2 && bias)) launch_fill(C, bias, M, N, ldc, sC, batch, mode == 2, stream);
         return check_launch(fn);
+    }
+    if (fixed_ws) {
+        const Plan want = choose(M, N, K, batch, true);
+        const uint64_t need = split_floats(M, N, batch, want.splits) * 4;
+        if (need > ws_bytes)
+            return fail(MI_ERR_UNSUPPORTED,
+                        "%s: M=%u N=%u K=%u batch=%u plans %u K splits whose partials need %llu bytes of scratch; "
+                        "the maximum is %llu bytes (use mi_gemm_nt_q8_0_ws with a larger workspace)",
+                        fn, M, N, K, batch, want.splits, static_cast<unsigned long long>(need),
+                        static_cast<unsigned long long>(ws_bytes));
     }
     GemmArgs a = make_args(A, static_cast<const uint8_t*>(W), nullptr, bias, C, M, N, K, mode, lda, ldc, sA, sC,
                            (K / 32) * 34);
@@ -1737,10 +1751,59 @@ int gemm_split(const char* fn, const float* A, const uint32_t* payload, const fl
     return check_launch(fn);
 }
 
+// ---- no-allocation entry -------------------------------------------------------------
+//
+// Scratch of mi_gemm_nt_q8_0_noalloc: the K-split partial planes live in this
+// file-scope device array instead of a caller workspace. The runtime gives
+// each GPU its own copy when the code object loads there, and it stays until
+// the process ends. Host code never passes `scratch` itself to a kernel (on
+// the host the name is only a stand-in, not a device address): the entry
+// looks up the device address once per GPU with hipGetSymbolAddress and uses
+// that pointer everywhere. Every call on a GPU shares its copy, so calls that
+// overlap on one GPU (different streams without ordering) race. Nothing in it
+// must start at zero: each split stores every element of its partial plane
+// before the reduce kernel reads it.
+constexpr uint64_t kScratchBytes = MI_GEMM_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) float scratch[kScratchBytes / 4];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current GPU's scratch (looked up on its first use).
+int scratch_on_current_device(const char* fn, void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(MI_ERR_HIP, "%s: hipGetDevice: %s", fn, hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return fail(MI_ERR_UNSUPPORTED, "%s: device index %d >= %d", fn, dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(MI_ERR_HIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", fn, dev, hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return MI_OK;
+}
+
 }  // namespace
 }  // namespace mi
 
 using namespace mi;
+
+extern "C" int mi_gemm_nt_q8_0_noalloc(const float* A, const void* W, const float* bias, float* C, uint32_t M,
+                                       uint32_t N, uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldc,
+                                       uint32_t batch, uint64_t sA, uint64_t sC, void* stream) {
+    const char* fn = "mi_gemm_nt_q8_0_noalloc";
+    if (M == 0 || N == 0) return MI_OK;
+    void* ws = nullptr;
+    const int st = scratch_on_current_device(fn, &ws);
+    if (st) return st;
+    return gemm_blocks(fn, A, W, bias, C, M, N, K, mode, lda, ldc, batch, sA, sC, ws, kScratchBytes,
+                       static_cast<hipStream_t>(stream), true);
+}
 
 extern "C" int mi_gemm_nt_q8_0(const float* A, const void* W, const float* bias, float* C, uint32_t M, uint32_t N,
                                uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldc, uint32_t batch, uint64_t sA,
