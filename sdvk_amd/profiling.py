@@ -159,46 +159,81 @@ def traffic_report(fetch_csv: str, write_csv: str, copy_mib: int, family: str, c
     return result
 
 
-# Derived figures of the counter report (per dispatch; the counters are summed
-# over the whole GPU). MFMA and VALU issue cycles are per SIMD, so the busy
-# fractions divide by the SIMD-cycles the dispatch had: GRBM_GUI_ACTIVE (GPU
-# busy cycles of the dispatch) x 256 CUs x 4 SIMDs.
+# Derived figures of the counter report (per dispatch; rocprofv3's CSV sums each
+# counter over all its instances). GRBM_GUI_ACTIVE is counted once per XCD, so
+# the dispatch's active cycles are its sum / 8. SQ_VALU_MFMA_BUSY_CYCLES sums
+# the busy cycles of every SIMD, so MFMA busy = that / (active cycles x 1024
+# SIMDs); for v_mfma_f32_32x32x16_f16 it equals 32 cycles x the MFMA count, i.e.
+# FLOP / 1024 (checked against the 9216x1280x1280 GEMM: 29.49 M = 30.2 GFLOP /
+# 1024). SQ_ACTIVE_INST_VALU and SQ_WAVE_CYCLES are per-wave sums in quad-cycles.
+XCDS = 8
 SIMDS = 256 * 4
 
 
-def counters_report(csv_paths: list[str], command: str, flops: dict | None = None) -> str:
-    """Per (kernel, grid): the average of every counter over the dispatches,
-    and MFMA busy / VALU busy / LDS bank conflicts per LDS instruction where
-    the counters are present. flops: {"kernel substring|grid": FLOP per dispatch}
-    adds the MFMA busy fraction implied by the algorithmic FLOP (1024 fp16 FLOP
-    per SIMD-cycle for v_mfma_f32_32x32x16_f16) for comparison."""
-    acc = collections.OrderedDict()
+def _duration_classes(items):
+    """Splits dispatches [(duration_ns, counters)] into classes at gaps of more
+    than 2x in duration: one (kernel, grid) can serve shapes of very different
+    cost (the attention kernel's self- and cross-attention shapes share a grid)."""
+    items = sorted(items, key=lambda x: x[0])
+    out, cur = [], []
+    for it in items:
+        if cur and it[0] > 2.0 * cur[-1][0]:
+            out.append(cur)
+            cur = []
+        cur.append(it)
+    if cur:
+        out.append(cur)
+    return out
+
+
+def counters_report(csv_paths: list[str], command: str) -> str:
+    """Per (kernel, grid, duration class): the average of every counter over the
+    dispatches, with MFMA busy / VALU busy / LDS bank conflicts per LDS
+    instruction / wait fraction where the counters are present."""
+    disp = collections.OrderedDict()  # (path, dispatch id) -> (name, grid, duration, {counter: value})
     for path in csv_paths:
         for r in csv.DictReader(open(path)):
-            key = (short_name(r["Kernel_Name"]), int(r["Grid_Size"]))
-            d = acc.setdefault(key, collections.defaultdict(list))
-            d[r["Counter_Name"]].append(float(r["Counter_Value"]))
-    names = sorted({c for d in acc.values() for c in d})
+            k = (path, r["Dispatch_Id"])
+            if k not in disp:
+                dur = float(r["End_Timestamp"]) - float(r["Start_Timestamp"])
+                disp[k] = (short_name(r["Kernel_Name"]), int(r["Grid_Size"]), dur, {})
+            disp[k][3][r["Counter_Name"]] = float(r["Counter_Value"])
+    groups = collections.OrderedDict()
+    for name, grid, dur, cnt in disp.values():
+        groups.setdefault((name, grid), []).append((dur, cnt))
+    names = sorted({c for _, _, _, cnt in disp.values() for c in cnt})
     lines = ["# rocprofv3 counters per kernel and grid", "", f"Command: `{command}`", "",
-             "Averages per dispatch. mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 1024 SIMDs); "
-             "valu_busy = SQ_ACTIVE_INST_VALU / (GRBM_GUI_ACTIVE x 1024); lds_conflict_per_lds = "
-             "SQ_LDS_BANK_CONFLICT / SQ_INSTS_LDS; wait_frac = SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES.", ""]
-    hdr = ["kernel", "grid", "dispatches"] + names + ["mfma_busy", "valu_busy", "lds_conflict_per_lds", "wait_frac"]
+             "Averages per dispatch (each counter summed over its instances by rocprofv3); dispatches of one "
+             "kernel and grid are split where their durations differ by more than 2x (shapes of different cost "
+             "on one grid). active = GRBM_GUI_ACTIVE / 8 (one count per XCD); mfma_busy = "
+             "SQ_VALU_MFMA_BUSY_CYCLES / (active x 1024 SIMDs); valu_busy = 4 x SQ_ACTIVE_INST_VALU "
+             "(quad-cycles, summed over waves) / (active x 1024); lds_conflict_per_lds = SQ_LDS_BANK_CONFLICT "
+             "cycles / SQ_INSTS_LDS; wait_frac = SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES (both quad-cycles summed "
+             "over waves). Durations are those of the profiled (serialised) dispatches.", ""]
+    hdr = ["kernel", "grid", "dispatches", "avg us"] + names + ["mfma_busy", "valu_busy", "lds_conflict_per_lds",
+                                                               "wait_frac"]
     lines += ["| " + " | ".join(hdr) + " |", "|" + "---|" * len(hdr)]
-    for (name, grid), d in acc.items():
-        avg = {c: sum(v) / len(v) for c, v in d.items()}
-        n = max(len(v) for v in d.values())
-        gui = avg.get("GRBM_GUI_ACTIVE")
+    for (name, grid), items in groups.items():
+        for cls in _duration_classes(items):
+            avg = {}
+            for c in names:
+                vals = [cnt[c] for _, cnt in cls if c in cnt]
+                if vals:
+                    avg[c] = sum(vals) / len(vals)
+            us = sum(d for d, _ in cls) / len(cls) / 1e3
+            gui = avg.get("GRBM_GUI_ACTIVE")
+            active = gui / XCDS if gui else None
 
-        def frac(num):
-            return f"{avg[num] / (gui * SIMDS):.3f}" if gui and num in avg else ""
-        conf = (f"{avg['SQ_LDS_BANK_CONFLICT'] / avg['SQ_INSTS_LDS']:.3f}"
-                if avg.get("SQ_INSTS_LDS") and "SQ_LDS_BANK_CONFLICT" in avg else "")
-        wait = (f"{avg['SQ_WAIT_INST_ANY'] / avg['SQ_WAVE_CYCLES']:.3f}"
-                if avg.get("SQ_WAVE_CYCLES") and "SQ_WAIT_INST_ANY" in avg else "")
-        row = [f"`{name}`", str(grid), str(n)] + [f"{avg[c]:.4g}" if c in avg else "" for c in names]
-        row += [frac("SQ_VALU_MFMA_BUSY_CYCLES"), frac("SQ_ACTIVE_INST_VALU"), conf, wait]
-        lines.append("| " + " | ".join(row) + " |")
+            def frac(num, scale=1.0):
+                return f"{scale * avg[num] / (active * SIMDS):.3f}" if active and num in avg else ""
+            conf = (f"{avg['SQ_LDS_BANK_CONFLICT'] / avg['SQ_INSTS_LDS']:.3f}"
+                    if avg.get("SQ_INSTS_LDS") and "SQ_LDS_BANK_CONFLICT" in avg else "")
+            wait = (f"{avg['SQ_WAIT_INST_ANY'] / avg['SQ_WAVE_CYCLES']:.3f}"
+                    if avg.get("SQ_WAVE_CYCLES") and "SQ_WAIT_INST_ANY" in avg else "")
+            row = [f"`{name}`", str(grid), str(len(cls)), f"{us:.2f}"]
+            row += [f"{avg[c]:.4g}" if c in avg else "" for c in names]
+            row += [frac("SQ_VALU_MFMA_BUSY_CYCLES"), frac("SQ_ACTIVE_INST_VALU", 4.0), conf, wait]
+            lines.append("| " + " | ".join(row) + " |")
     return "\n".join(lines) + "\n"
 
 

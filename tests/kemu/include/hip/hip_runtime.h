@@ -51,6 +51,18 @@ typedef enum hipMemcpyKind {
 #define hipHostMallocDefault 0x0u
 
 inline hipError_t hipGetLastError() { return hipSuccess; }
+// File-scope __device__ arrays are host globals here: a symbol's device address
+// is its host address, on the one emulated device 0.
+#define __align__(n) __attribute__((aligned(n)))
+#define HIP_SYMBOL(x) (&(x))
+inline hipError_t hipGetDevice(int* d) {
+    *d = 0;
+    return hipSuccess;
+}
+inline hipError_t hipGetSymbolAddress(void** p, const void* sym) {
+    *p = const_cast<void*>(sym);
+    return hipSuccess;
+}
 
 inline const char* hipGetErrorString(hipError_t e) { return e == hipSuccess ? "no error" : "emulated HIP error"; }
 // Asynchronous copies are deferred: they run at the event synchronisation that
