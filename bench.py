@@ -152,6 +152,15 @@ class NnCase:
                             stream=stream)
 
 
+# The block stack of the bench line runs the library's fastest block path:
+# context K / V projected once per job (mi_block_ctx_kv), joint Q/K/V weights
+# (MI_BLOCK_JOINT_QKV) and the residual / GEGLU epilogues fused into the GEMMs
+# (MI_BLOCK_FUSED_EPILOGUES). Every flag combination computes the same bits as
+# the plain block (tests/test_gpu_xfused_epilogues.py, test_gpu_xattn_kv_cache.py);
+# the extras time the plain block and each flag alone.
+BLOCK_VARIANT = {"cached_kv": True, "fused_epilogues": True, "joint_qkv": True}
+
+
 class BlockStack:
     """ten SDXL BasicTransformerBlocks at level 2 (1280
     channels, 2 x 1024 tokens, 20 heads, context 2 x 77 x 2048, FF 1280 ->
@@ -405,10 +414,10 @@ def extras(rng, hip, ops, stream, reps, emit=None):
     part("gemm_candidates", candidates)
     part("attention_candidates", attn_candidates)
     part("nn_gemm", nn)
+    part("block_stack_plain", stack())
     part("block_stack_cached_kv", stack(cached_kv=True))
     part("block_stack_fused_epilogues", stack(fused=True))
     part("block_stack_joint_qkv", stack(joint_qkv=True))
-    part("block_stack_fused_joint_cached", stack(cached_kv=True, fused=True, joint_qkv=True))
     part("step_graph", step_graph)
     return out
 
@@ -548,8 +557,9 @@ def main() -> int:
     rng = np.random.default_rng(1)
     stream = hip.Stream()
     if args.only == "block":
-        stack = BlockStack(rng, hip, ops)
-        res = stack.measure(stream, max(args.steps // 4, 1))
+        stack = BlockStack(rng, hip, ops, joint_qkv=True, fused=True)
+        res = stack.measure(stream, max(args.steps // 4, 1), cached_kv=True)
+        res["variant"] = BLOCK_VARIANT
         print(json.dumps({"block_stack": res}), flush=True)
         return 0
     cases = []
@@ -643,8 +653,9 @@ def main() -> int:
     block, stack = None, None
     if args.only is None:
         print("[bench] config-4 block stack", file=sys.stderr, flush=True)
-        stack = BlockStack(rng, hip, ops)
-        block = stack.measure(stream, 5)
+        stack = BlockStack(rng, hip, ops, joint_qkv=True, fused=True)
+        block = stack.measure(stream, 5, cached_kv=True)
+        block["variant"] = BLOCK_VARIANT
         print(f"[bench] block stack: {block['latency_ms']:.3f} ms for {block['blocks']} blocks "
               f"({block['tflops']:.1f} TFLOP/s)", file=sys.stderr, flush=True)
 

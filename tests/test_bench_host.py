@@ -146,15 +146,15 @@ def test_bench_line_on_stand_in_device(fake_device, monkeypatch, capsys):
                                                                                             rel=1e-3)
     assert len(out["breakdown"]) == len(bench.GEMM_SHAPES) + len(bench.ATTN_SHAPES)
     assert out["block_stack"]["blocks"] == 10
+    assert out["block_stack"]["variant"] == {"cached_kv": True, "fused_epilogues": True, "joint_qkv": True}
     ex = out["extras"]
-    for part in ("config0_gemm", "nn_gemm", "block_stack_cached_kv", "block_stack_fused_epilogues",
-                 "block_stack_joint_qkv", "block_stack_fused_joint_cached", "gemm_candidates",
+    for part in ("config0_gemm", "nn_gemm", "block_stack_plain", "block_stack_cached_kv",
+                 "block_stack_fused_epilogues", "block_stack_joint_qkv", "gemm_candidates",
                  "attention_candidates", "step_graph"):
         assert part in ex and "error" not in ex[part], (part, ex.get(part))
     assert set(ex["gemm_candidates"]["us"]) == set(bench.GEMM_CANDIDATES)
     assert len(ex["gemm_candidates"]["best"]) == len(bench.GEMM_SHAPES) + 1
-    assert ex["block_stack_fused_joint_cached"]["variant"] == {"cached_kv": True, "fused_epilogues": True,
-                                                               "joint_qkv": True}
+    assert ex["block_stack_plain"]["variant"] == {"cached_kv": False, "fused_epilogues": False, "joint_qkv": False}
     for name in ("gemm_nt_q8_0", "fused_attention_ex", "gemm_nn_q8", "sdxl_block_forward", "block_ctx_kv",
                  "sdxl_block_forward_kv", "q8_0_quantize"):
         assert name in fake_device, name
