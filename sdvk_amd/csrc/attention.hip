@@ -21,7 +21,9 @@
 //     layout is, key for key, the B-operand layout the PV product needs); V is
 //     stored in LDS grouped by the PV step that consumes each key, so each A
 //     fragment is one 16-byte read; the row sums of P come from the same MFMA
-//     (an all-ones A operand);
+//     (an all-ones A operand) in the fp32-input kernel, and from v_dot2_f32_f16
+//     on the fp16 P values in the fp16 kernel (VALU instead of a fifth of its
+//     MFMAs);
 //   * fp32 inputs (the reference layout) are carried as fp16 hi + lo pairs
 //     (x = hi + lo to 2^-22): S = K_hi Q_hi + K_lo Q_hi + K_hi Q_lo and
 //     O = V_hi P + V_lo P, so only P is rounded to fp16. fp16 inputs take one
@@ -569,10 +571,10 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
             m1 = fmaxf(m1, fmaxf(sc[1][r], sc[1][r + 1]));
         }
         const float mx = fmaxf(m0, m1);
-        // the partner lane (lane ^ 32) holds the query's other 32 keys
-        const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, mx),
-                                                          __builtin_bit_cast(unsigned, mx), false, false);
-        return fmaxf(__builtin_bit_cast(float, sw[0]), __builtin_bit_cast(float, sw[1]));
+        // the partner lane (lane ^ 32) holds the query's other 32 keys. (Not
+        // v_permlane32_swap with mx as both operands: the compiler then takes
+        // the two results for equal and keeps this half's max only.)
+        return fmaxf(mx, __shfl_xor(mx, 32));
     };
     auto exp_pack = [&](const floatx16 (&sc)[2], half8 (&pf)[2][2]) {
 #pragma unroll
@@ -583,21 +585,33 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
                 for (int i = 0; i < 8; ++i) pf[t][sp][i] = static_cast<_Float16>(__builtin_amdgcn_exp2f(sc[t][8 * sp + i]));
     };
 
-    floatx16 o[3];  // O^T for d in [0, 32), [32, 64); row sums of P (all-ones A operand)
+    floatx16 o[2];  // O^T for d in [0, 32), [32, 64)
 #pragma unroll
-    for (int u = 0; u < 3; ++u)
+    for (int u = 0; u < 2; ++u)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[u][r] = 0.0f;
-    const half8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+    // Row sum of P over this lane's 32 keys of every tile (the partner lane,
+    // lane ^ 32, holds the query's other 32): the fp16 P values the PV product
+    // uses, summed in fp32 two at a time by v_dot2_f32_f16 (p0 * 1 + p1 * 1),
+    // on the VALU instead of an all-ones MFMA operand.
+    float lsum = 0.0f;
+    const half2 one2 = {1, 1};
+    auto row_sum = [&](const half8 (&pf)[2][2]) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int sp = 0; sp < 2; ++sp)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    lsum = __builtin_amdgcn_fdot2(half2{pf[t][sp][2 * i], pf[t][sp][2 * i + 1]}, one2, lsum, false);
+    };
     auto pv = [&](const half8 (&pf)[2][2]) {
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int sp = 0; sp < 2; ++sp) {
-                o[2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones, pf[t][sp], o[2], 0, 0, 0);
+            for (int sp = 0; sp < 2; ++sp)
 #pragma unroll
                 for (int u = 0; u < 2; ++u) o[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[t][sp][u], pf[t][sp], o[u], 0, 0, 0);
-            }
     };
 
     if (ntiles > 0) {
@@ -648,8 +662,9 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
             }
             __builtin_amdgcn_sched_barrier(0);
 
-            // phase B: PV of tile j (12 MFMA) || mask + scale + max of tile j+1
+            // phase B: PV of tile j (8 MFMA) || row sum of tile j + mask + scale + max of tile j+1
             pv(pf);
+            row_sum(pf);
             if constexpr (kMasked) mask(s1, kv1);
 #pragma unroll
             for (int t = 0; t < 2; ++t)
@@ -657,17 +672,18 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
                 for (int r = 0; r < 16; ++r) s1[t][r] = __builtin_fmaf(s1[t][r], a.c, -m);
             const float mx = lane_max(s1);
 #pragma unroll
-            for (int i = 0; i < 12; ++i) {
+            for (int i = 0; i < 8; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, kMasked ? 10 : 4, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, kMasked ? 16 : 8, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
             if (__any(mx > kLazy)) {  // raise the running max (rare)
                 const float d = fmaxf(mx, 0.0f);
                 const float alpha = __builtin_amdgcn_exp2f(-d);
                 m += d;
+                lsum *= alpha;
 #pragma unroll
-                for (int u = 0; u < 3; ++u)
+                for (int u = 0; u < 2; ++u)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) o[u][r] *= alpha;
 #pragma unroll
@@ -689,9 +705,12 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
         half8 pf[2][2];
         exp_pack(s0, pf);
         pv(pf);
+        row_sum(pf);
     }
 
-    const float lt = o[2][0];
+    // the query's row sum: this lane's 32 keys of every tile plus the partner
+    // lane's (one rounding, the same in both lanes: fp32 addition commutes)
+    const float lt = lsum + __shfl_xor(lsum, 32);
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
     if (qi >= a.Tq) return;
     TO* Op = static_cast<TO*>(a.o) + b * a.so + static_cast<uint64_t>(qi) * a.ldo + static_cast<uint64_t>(h) * a.hd;

@@ -200,9 +200,11 @@ def gemm_nn(E, *, M, N, K, mode=0, batch=1, lda=0, ldb=0, ldc=0, sA=0, sB=0, sC=
 
 
 def attention(E, *, batch=1, Tq, Tk, C, heads, causal=False, f16_in=False, f16_out=False, kv_len=None, seed=1,
-              front=False, order=0, tol=2e-3, nw=None):
+              front=False, order=0, tol=2e-3, nw=None, outliers=None):
     """mi_fused_attention_ex (contiguous [batch, T, C]) against the oracle;
-    nw pins the fp16 kernel's workgroup size (MI_ATTN_NW)."""
+    nw pins the fp16 kernel's workgroup size (MI_ATTN_NW); outliers: key
+    indices whose scores stand far above the rest (q ~ 1, k ~ 0.1 N(0, 1),
+    those keys 3.0), so that a running max that misses them overflows."""
     E.order(order)
     if nw:
         os.environ["MI_ATTN_NW"] = str(nw)
@@ -212,6 +214,11 @@ def attention(E, *, batch=1, Tq, Tk, C, heads, causal=False, f16_in=False, f16_o
     q = ob.normal(seed, batch * Tq * C).astype(idt)
     k = ob.normal(seed + 1, batch * Tk * C).astype(idt)
     v = ob.normal(seed + 2, batch * Tk * C).astype(idt)
+    if outliers:
+        q = (q.astype(np.float32) * np.float32(0.1) + np.float32(1.0)).astype(idt)
+        kk = (k.astype(np.float32) * np.float32(0.1)).reshape(batch, Tk, C)
+        kk[:, outliers, :] = 3.0
+        k = kk.reshape(-1).astype(idt)
     odt = np.float16 if f16_out else np.float32
     n_out = batch * Tq * C
     dq, dk, dv = E.buf(q, front=front), E.buf(k, front=front), E.buf(v, front=front)

@@ -398,6 +398,16 @@ inline unsigned mbcnt_hi(unsigned mask, unsigned base) {
     return base + static_cast<unsigned>(__builtin_popcount(below));
 }
 
+// v_dot2_f32_f16: a.x * b.x + a.y * b.y + c, rounded once to fp32 (the fp16
+// products and their sum with c are exact in double for the kernels' operands).
+typedef _Float16 kemu_h2 __attribute__((ext_vector_type(2)));
+inline float fdot2(kemu_h2 a, kemu_h2 b, float c, bool clamp) {
+    if (clamp) die("fdot2: clamp not emulated");
+    const double r = static_cast<double>(a[0]) * static_cast<double>(b[0]) +
+                     static_cast<double>(a[1]) * static_cast<double>(b[1]) + static_cast<double>(c);
+    return static_cast<float>(r);
+}
+
 inline void nop_fn(const unsigned char (*)[256], unsigned char (*)[256], const void*) {}
 inline void wave_barrier() { wave_op("wave_barrier", nullptr, 0, nullptr, 0, nop_fn, nullptr); }
 
@@ -436,6 +446,7 @@ inline T __shfl_xor(T v, int mask, int width = 64) {
 #define __builtin_amdgcn_exp2f exp2f
 #define __builtin_amdgcn_ds_read_tr16_b64_v4f16 ::kemu::ds_read_tr16_b64
 #define __builtin_amdgcn_permlane32_swap ::kemu::permlane32_swap
+#define __builtin_amdgcn_fdot2 ::kemu::fdot2
 #define __builtin_amdgcn_raw_ptr_buffer_load_lds ::kemu::buffer_load_lds
 #define __builtin_amdgcn_sched_barrier(...) ((void)0)
 #define __builtin_amdgcn_sched_group_barrier(...) ((void)0)

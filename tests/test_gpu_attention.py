@@ -91,6 +91,25 @@ def test_special_cases(gpu, oracle):
     assert_parity(got[1], want[1], what="kv_len full")
 
 
+def test_outlier_key_in_either_lane_half(gpu, oracle):
+    """One key per tile scores far above the others (s * log2(e) / 8 ~ 35
+    above them): the running max must take both lane halves of a tile into
+    account (keys 8j + 0..3 sit in one lane of a query, 8j + 4..7 in its
+    partner), or exp2 of that key overflows fp16. Both halves, fp16 path."""
+    B, Tq, Tk, C, heads = 1, 64, 192, 128, 2
+    rng = np.random.default_rng(11)
+    q = (rng.standard_normal(Tq * C) * 0.1 + 1.0).astype(np.float16)
+    k = (rng.standard_normal((Tk, C)) * 0.1).astype(np.float16)
+    v = rng.standard_normal(Tk * C).astype(np.float16)
+    k[5] = 3.0      # tile 0: a key of the upper lane half
+    k[64 + 2] = 3.0  # tile 1: a key of the lower lane half
+    k[128 + 70 - 64] = 2.5
+    k = k.reshape(-1)
+    got = run_ex(q, k, v, batch=B, Tq=Tq, Tk=Tk, C=C, heads=heads, in_dtype=MI_F16, out_dtype=MI_F32)
+    want = oracle.fused_attention_ex(q, k, v, batch=B, Tq=Tq, Tk=Tk, C=C, heads=heads, in_dtype=1)
+    assert_parity(got, want, what="outlier keys")
+
+
 def _sample_rows(Tq, n, seed):
     rng = np.random.default_rng(seed)
     return np.unique(np.concatenate([[0, Tq - 1, 127, 128], rng.integers(0, Tq, n)])).astype(np.uint32)

@@ -121,6 +121,9 @@ FAMILIES = {
         # the 4-wave fp16 kernel (chosen for large grids) on small shapes
         dict(batch=2, Tq=200, Tk=300, C=128, heads=2, f16_in=True, f16_out=True, causal=True, nw=4),
         dict(batch=2, Tq=130, Tk=77, C=640, heads=10, f16_in=True, f16_out=False, kv_len=[77, 13], nw=4),
+        # one far-outlying key per tile, in either lane half of a query (the running max spans both)
+        dict(Tq=64, Tk=192, C=128, heads=2, f16_in=True, outliers=[5, 66, 134]),
+        dict(Tq=64, Tk=192, C=128, heads=2, outliers=[5, 66, 134]),
     ],
     "block": [
         dict(B=1, T=33, C=64, H=1, Tc=5, Cc=96, F=160),
