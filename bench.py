@@ -538,8 +538,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip the measurements outside the step metric")
     ap.add_argument("--extras-child", action="store_true", help=argparse.SUPPRESS)
-    ap.add_argument("--only", choices=["gemm", "attention", "block", "cfg0"], default=None,
-                    help="run one part only (profiling): a kernel family, the config-4 block stack, or the "
+    ap.add_argument("--only", choices=["step", "gemm", "attention", "block", "cfg0"], default=None,
+                    help="run one part only (profiling): the step's kernels (GEMM and attention shapes, no block "
+                         "stack, CPU baseline or extras), a kernel family, the config-4 block stack, or the "
                          "config-0 GEMM alone")
     args = ap.parse_args()
     if args.extras_child:
@@ -565,9 +566,9 @@ def main() -> int:
     cases = []
     if args.only == "cfg0":
         cases.append(GemmCase(*CONFIG0, rng, hip, ops))
-    if args.only in (None, "gemm"):
+    if args.only in (None, "step", "gemm"):
         cases += [GemmCase(t, M, N, K, rng, hip, ops) for t, M, N, K in GEMM_SHAPES]
-    if args.only in (None, "attention"):
+    if args.only in (None, "step", "attention"):
         cases += [AttnCase(t, B, H, Tq, Tk, m, rng, hip, ops) for t, B, H, Tq, Tk, m in ATTN_SHAPES]
     hip.synchronize()
     print(f"[bench] {hip.device_name(0)}: {len(cases)} shapes resident", file=sys.stderr, flush=True)
@@ -689,10 +690,10 @@ def main() -> int:
         "pct_mfma_peak": round(100 * value / PEAK_FP16_TFLOPS, 2),
         "config": {"workload": "sdxl1024: Q8_0 GEMM sweep (BASELINE config 1) + fused self/cross attention "
                                "(configs 2-3), fp32 GEMM I/O, fp16 attention I/O, one pass = 1 step",
-                   "gemm_shapes_MNK": ([[M, N, K] for _, M, N, K in GEMM_SHAPES] if args.only in (None, "gemm")
+                   "gemm_shapes_MNK": ([[M, N, K] for _, M, N, K in GEMM_SHAPES] if args.only in (None, "step", "gemm")
                                        else [list(CONFIG0[1:])] if args.only == "cfg0" else []),
                    "attn_shapes_B_H_Tq_Tk": [[B, H, Tq, Tk] for _, B, H, Tq, Tk, _ in ATTN_SHAPES]
-                   if args.only in (None, "attention") else [],
+                   if args.only in (None, "step", "attention") else [],
                    "step_gflop": round(step_flops / 1e9, 3)},
         "roofline": roofline,
         "cpu_baseline": cpu,

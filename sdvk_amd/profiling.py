@@ -83,7 +83,10 @@ def family_of(name: str) -> str | None:
     return None
 
 
-def stats_report(csv_path: str, command: str) -> str:
+def stats_report(csv_path: str, command: str, flops: dict | None = None) -> str:
+    """flops: {family: algorithmic FLOP per API call}; adds the achieved rate of
+    each such family (FLOP per call / its average time per call) and its
+    fraction of the 2500 TFLOP/s fp16 MFMA peak."""
     rows = list(csv.DictReader(open(csv_path)))
     lines = [f"# rocprofv3 kernel statistics", "", f"Command: `{command}`", "",
              "| kernel | calls | avg us | min us | max us | total % |", "|---|---:|---:|---:|---:|---:|"]
@@ -104,6 +107,12 @@ def stats_report(csv_path: str, command: str) -> str:
     for f, (calls, tot) in fam.items():
         if calls:
             lines.append(f"| {f} | {calls} | {tot / calls / 1e3:.2f} |")
+    for f, fl in (flops or {}).items():
+        calls, tot = fam.get(f, (0, 0.0))
+        if calls:
+            tf = fl / (tot / calls * 1e-9) / 1e12
+            lines += ["", f"{f}: {fl:.6g} algorithmic FLOP per call / {tot / calls / 1e3:.2f} us per call = "
+                          f"{tf:.1f} TFLOP/s = {tf / 2500.0:.4f} of the 2500 TFLOP/s fp16 MFMA peak"]
     return "\n".join(lines) + "\n"
 
 
@@ -244,6 +253,8 @@ def main(argv=None) -> int:
     s.add_argument("csv")
     s.add_argument("out")
     s.add_argument("--command", required=True)
+    s.add_argument("--flops", action="append", default=[], metavar="FAMILY=FLOP",
+                   help="algorithmic FLOP per API call of a family (adds its achieved rate)")
     t = sub.add_parser("traffic")
     t.add_argument("fetch_csv")
     t.add_argument("write_csv")
@@ -259,7 +270,8 @@ def main(argv=None) -> int:
     if a.cmd == "counters":
         Path(a.out).write_text(counters_report(a.csvs, a.command))
     elif a.cmd == "stats":
-        Path(a.out).write_text(stats_report(a.csv, a.command))
+        fl = {k: float(v) for k, v in (x.split("=", 1) for x in a.flops)}
+        Path(a.out).write_text(stats_report(a.csv, a.command, fl))
     else:
         Path(a.out).write_text(json.dumps(traffic_report(a.fetch_csv, a.write_csv, a.copy_mib, a.family,
                                                          a.command), indent=1) + "\n")
