@@ -151,6 +151,10 @@ __device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0F7
 // a tile's max exceeds it by more than this, so P = exp2(s - m) <= 2^8 stays
 // far inside fp16 range while the O / l rescale runs on few tiles.
 constexpr float kLazy = 8.0f;
+// The fp16 kernel checks the same bound after the exponentials: a lane's sum
+// of a tile's P values bounds each of them, so a sum <= 2^kLazy keeps every
+// P <= 2^kLazy.
+constexpr float kLazySum = 256.0f;
 
 template <typename TI, typename TO, bool VEC>
 __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
@@ -424,9 +428,12 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
 // Same math as attn_kernel, arranged so that matrix and vector work overlap
 // inside each wave (a wave issues in order, so an MFMA only hides VALU work
 // placed between MFMAs; waves sharing a SIMD do not overlap them): iteration
-// j issues the S MFMAs of tile j+1 between the exp2 / fp16 packing of tile j,
-// then the PV MFMAs of tile j between the scale / max of tile j+1. Every LDS
-// fragment of an iteration is read up front.
+// j issues the S MFMAs of tile j+1 between the exp2 / fp16 packing / row sum
+// of tile j, then the PV MFMAs of tile j between the scale of tile j+1. The
+// lazy-rescale test needs no row max per tile: it runs on the tile's row sums
+// after the exponentials (a sum over 2^8 is rare and sends the wave through a
+// rescale that recomputes the tile's P). Every LDS fragment of an iteration is
+// read up front.
 //
 // K and V tiles travel from memory straight into LDS (buffer loads with the
 // LDS-DMA bit: no registers, no conversion, no LDS store instructions), as
@@ -566,9 +573,9 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
     auto lane_max = [&](const floatx16 (&sc)[2]) {
         float m0 = fmaxf(sc[0][0], sc[0][1]), m1 = fmaxf(sc[1][0], sc[1][1]);
 #pragma unroll
-        for (int r = 2; r < 16; r += 2) {
-            m0 = fmaxf(m0, fmaxf(sc[0][r], sc[0][r + 1]));
-            m1 = fmaxf(m1, fmaxf(sc[1][r], sc[1][r + 1]));
+        for (int r = 2; r < 16; r += 2) {  // v_max3_f32 chains
+            m0 = fmaxf(fmaxf(m0, sc[0][r]), sc[0][r + 1]);
+            m1 = fmaxf(fmaxf(m1, sc[1][r]), sc[1][r + 1]);
         }
         const float mx = fmaxf(m0, m1);
         // the partner lane (lane ^ 32) holds the query's other 32 keys. (Not
@@ -594,16 +601,42 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
     // lane ^ 32, holds the query's other 32): the fp16 P values the PV product
     // uses, summed in fp32 two at a time by v_dot2_f32_f16 (p0 * 1 + p1 * 1),
     // on the VALU instead of an all-ones MFMA operand.
-    float lsum = 0.0f;
+    float lsum = 0.0f, m = 0.0f;
     const half2 one2 = {1, 1};
-    auto row_sum = [&](const half8 (&pf)[2][2]) {
+    auto tile_sum = [&](const half8 (&pf)[2][2]) {
+        float ts = 0.0f;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int sp = 0; sp < 2; ++sp)
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    lsum = __builtin_amdgcn_fdot2(half2{pf[t][sp][2 * i], pf[t][sp][2 * i + 1]}, one2, lsum, false);
+                    ts = __builtin_amdgcn_fdot2(half2{pf[t][sp][2 * i], pf[t][sp][2 * i + 1]}, one2, ts, false);
+        return ts;
+    };
+    // Adds tile j's row sum (ts, from its fp16 P in pf, computed from the
+    // scaled scores sc) after the lazy-rescale test: when some lane's sum
+    // exceeds 2^8 (rare), the running max rises by the tile's excess over it
+    // (the same amount in both lanes of a query), O and l are rescaled and
+    // the tile's P are recomputed.
+    auto settle = [&](floatx16 (&sc)[2], half8 (&pf)[2][2], float ts) {
+        if (__any(ts > kLazySum)) {
+            const float d = fmaxf(lane_max(sc), 0.0f);
+            const float alpha = __builtin_amdgcn_exp2f(-d);
+            m += d;
+            lsum *= alpha;
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[u][r] *= alpha;
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sc[t][r] -= d;
+            exp_pack(sc, pf);
+            ts = tile_sum(pf);
+        }
+        lsum += ts;
     };
     auto pv = [&](const half8 (&pf)[2][2]) {
 #pragma unroll
@@ -628,7 +661,7 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
         qk(s0);
         if (0 >= kfull) mask(s0, 0);
         const float mx0 = lane_max(s0);
-        float m = mx0 == -INFINITY ? 0.0f : mx0 * a.c;
+        m = mx0 == -INFINITY ? 0.0f : mx0 * a.c;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -650,47 +683,33 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
             dma_v(kv1, (j + 1) & 1);
             __builtin_amdgcn_sched_barrier(0);
 
-            // phase A: S of tile j+1 (8 MFMA) || exp2 + fp16 pack of tile j
+            // phase A: S of tile j+1 (8 MFMA) || exp2 + fp16 pack + row sum of tile j
             floatx16 s1[2];
             half8 pf[2][2];
             qk(s1);
             exp_pack(s0, pf);
+            const float ts = tile_sum(pf);
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
+            settle(s0, pf, ts);
 
-            // phase B: PV of tile j (8 MFMA) || row sum of tile j + mask + scale + max of tile j+1
+            // phase B: PV of tile j (8 MFMA) || mask + scale of tile j+1
             pv(pf);
-            row_sum(pf);
             if constexpr (kMasked) mask(s1, kv1);
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) s1[t][r] = __builtin_fmaf(s1[t][r], a.c, -m);
-            const float mx = lane_max(s1);
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, kMasked ? 16 : 8, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, kMasked ? 12 : 4, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
-            if (__any(mx > kLazy)) {  // raise the running max (rare)
-                const float d = fmaxf(mx, 0.0f);
-                const float alpha = __builtin_amdgcn_exp2f(-d);
-                m += d;
-                lsum *= alpha;
-#pragma unroll
-                for (int u = 0; u < 2; ++u)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) o[u][r] *= alpha;
-#pragma unroll
-                for (int t = 0; t < 2; ++t)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) s1[t][r] -= d;
-            }
 #pragma unroll
             for (int t = 0; t < 2; ++t) s0[t] = s1[t];
             dma_wait();
@@ -704,8 +723,8 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
         read_v((ntiles - 1) & 1);
         half8 pf[2][2];
         exp_pack(s0, pf);
+        settle(s0, pf, tile_sum(pf));
         pv(pf);
-        row_sum(pf);
     }
 
     // the query's row sum: this lane's 32 keys of every tile plus the partner
