@@ -56,6 +56,7 @@ struct AttnArgs {
     uint64_t ldq, ldk, ldv, ldo, sq, sk, sv, so;
     const int32_t* kv_len;
     float c;  // scale * log2(e)
+    int ostage;  // output rows and head columns 16-byte aligned: store O through LDS (store_o_rows)
 };
 
 // 8 consecutive elements as fp16 (hi); for fp32 sources also the residual
@@ -147,6 +148,45 @@ __device__ __forceinline__ half4 lds_read_tr16(const _Float16* p) {
 
 __device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// Writes one wave's O^T accumulators (32 queries x 64 d, times inv) as output
+// rows. In the MFMA layout a lane holds 4-element runs of one query's row, so
+// a direct store touches 32 rows with 8 or 16 bytes each per instruction; here
+// the wave transposes through its own LDS region (32 rows, the 16-byte chunks
+// of row q XOR-swizzled by q) and then stores 16 bytes per lane, whole rows
+// per instruction. Rows at or past nrows and chunks at or past hd are skipped.
+// Needs 16-byte aligned rows and head offsets; lds: 32 * 64 * sizeof(TO) bytes.
+template <typename TO>
+__device__ __forceinline__ void store_o_rows(const floatx16* o, float inv, char* lds, TO* Ob, int nrows, int hd,
+                                             uint64_t ldo, int lane) {
+    constexpr int E = sizeof(TO), RB = 64 * E, NC = RB / 16;
+    const int q = lane & 31, g = lane >> 5;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int run = 0; run < 4; ++run) {
+            const int byte = (32 * u + 8 * run + 4 * g) * E;
+            char* p = lds + q * RB + (((byte >> 4) ^ (q & (NC - 1))) << 4) + (byte & 15);
+            if constexpr (E == 4) {
+                *reinterpret_cast<floatx4*>(p) =
+                    floatx4{o[u][4 * run] * inv, o[u][4 * run + 1] * inv, o[u][4 * run + 2] * inv, o[u][4 * run + 3] * inv};
+            } else {
+                *reinterpret_cast<half4*>(p) =
+                    half4{static_cast<_Float16>(o[u][4 * run] * inv), static_cast<_Float16>(o[u][4 * run + 1] * inv),
+                          static_cast<_Float16>(o[u][4 * run + 2] * inv), static_cast<_Float16>(o[u][4 * run + 3] * inv)};
+            }
+        }
+    __builtin_amdgcn_wave_barrier();
+    constexpr int RPI = 64 / NC;  // rows per store instruction
+    const int c = lane % NC, r0 = lane / NC;
+#pragma unroll
+    for (int i = 0; i < 32 / RPI; ++i) {
+        const int r = i * RPI + r0;
+        const floatx4 v = *reinterpret_cast<const floatx4*>(lds + r * RB + ((c ^ (r & (NC - 1))) << 4));
+        if (r < nrows && c * (16 / E) < hd)
+            *reinterpret_cast<floatx4*>(reinterpret_cast<char*>(Ob + static_cast<uint64_t>(r) * ldo) + c * 16) = v;
+    }
+}
+
 // Lazy rescaling threshold (exp2 domain): the running max is only raised when
 // a tile's max exceeds it by more than this, so P = exp2(s - m) <= 2^8 stays
 // far inside fp16 range while the O / l rescale runs on few tiles.
@@ -160,8 +200,8 @@ template <typename TI, typename TO, bool VEC>
 __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
     constexpr bool kSplit = sizeof(TI) == 4;  // fp32 inputs: hi + lo planes
     constexpr int NP = kSplit ? 2 : 1;
-    __shared__ _Float16 Ks[2][NP][kBKV * kKld];
-    __shared__ _Float16 Vs[2][NP][8 * kVG * 8];
+    __shared__ __attribute__((aligned(16))) _Float16 Ks[2][NP][kBKV * kKld];
+    __shared__ __attribute__((aligned(16))) _Float16 Vs[2][NP][8 * kVG * 8];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -398,6 +438,16 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
 
     const float lt = o[2][0];
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    constexpr int kWaveBytes = 32 * 64 * static_cast<int>(sizeof(TO));
+    if constexpr (VEC && static_cast<int>(sizeof(Ks)) >= (kThreads / 64) * kWaveBytes) {
+        if (a.ostage) {  // through LDS (the K stages, free after every wave's last tile)
+            __syncthreads();
+            const int nrows = qwave >= a.Tq ? 0 : static_cast<int>(min(a.Tq - qwave, 32u));
+            TO* Ob = static_cast<TO*>(a.o) + b * a.so + static_cast<uint64_t>(qwave) * a.ldo + static_cast<uint64_t>(h) * a.hd;
+            store_o_rows<TO>(o, inv, reinterpret_cast<char*>(&Ks[0][0][0]) + wave * kWaveBytes, Ob, nrows, hd, a.ldo, lane);
+            return;
+        }
+    }
     if (qi >= a.Tq) return;
     TO* Op = static_cast<TO*>(a.o) + b * a.so + static_cast<uint64_t>(qi) * a.ldo + static_cast<uint64_t>(h) * a.hd;
 #pragma unroll
@@ -731,6 +781,19 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
     // lane's (one rounding, the same in both lanes: fp32 addition commutes)
     const float lt = lsum + __shfl_xor(lsum, 32);
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    if (a.ostage) {
+        // every wave is done with the K / V stages: each takes 32 * 64 * sizeof(TO)
+        // bytes of them (waves 0, 1 of Ks and 2, 3 of Vs for fp32 output)
+        __syncthreads();
+        constexpr int kWaveBytes = 32 * 64 * static_cast<int>(sizeof(TO));
+        constexpr int kStage = static_cast<int>(sizeof(Ks));
+        char* st = wave * kWaveBytes < kStage ? reinterpret_cast<char*>(&Ks[0][0]) + wave * kWaveBytes
+                                              : reinterpret_cast<char*>(&Vs[0][0]) + (wave * kWaveBytes - kStage);
+        const int nrows = qwave >= a.Tq ? 0 : static_cast<int>(min(a.Tq - qwave, 32u));
+        TO* Ob = static_cast<TO*>(a.o) + b * a.so + static_cast<uint64_t>(qwave) * a.ldo + static_cast<uint64_t>(h) * a.hd;
+        store_o_rows<TO>(o, inv, st, Ob, nrows, hd, a.ldo, lane);
+        return;
+    }
     if (qi >= a.Tq) return;
     TO* Op = static_cast<TO*>(a.o) + b * a.so + static_cast<uint64_t>(qi) * a.ldo + static_cast<uint64_t>(h) * a.hd;
 #pragma unroll
@@ -807,6 +870,8 @@ int run(const mi_attn_args& x, hipStream_t s, const char* fn) {
     a.kv_len = x.kv_len;
     const float scale = x.scale != 0.0f ? x.scale : 1.0f / sqrtf(static_cast<float>(a.hd));
     a.c = scale * 1.4426950408889634f;
+    a.ostage = aligned(x.out, 16) && (ldo * eo) % 16 == 0 && (so * eo) % 16 == 0 && (a.hd * eo) % 16 == 0 &&
+               !std::getenv("MI_ATTN_DIRECT_STORE");
 
     // 16-byte vector path: every 8-element chunk of every row is 16-byte aligned.
     const uintptr_t vin = 8 * ei, vout = 4 * eo;
