@@ -252,7 +252,7 @@ typedef struct mi_attn_args {
     int32_t causal;
     int32_t in_dtype;     /* mi_dtype of q, k, v */
     int32_t out_dtype;    /* mi_dtype of out */
-    uint64_t ldq, ldk, ldv, ldo;   /* token stride, 0 -> C */
+    uint64_t ldq, ldk, ldv, ldo;   /* token stride, 0 -> C; ldq, ldk, ldv < 2^22 elements */
     uint64_t sq, sk, sv, so;       /* batch stride, 0 -> T * ld */
     const int32_t* kv_len;         /* device int32[batch] or NULL (all Tk keys) */
     float scale;                   /* 0 -> 1/sqrt(C/heads) (fused_attn.cpp:55) */

@@ -527,13 +527,10 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
     const _Float16* Kp = static_cast<const _Float16*>(a.k) + b * a.sk + static_cast<uint64_t>(h) * a.hd;
     const _Float16* Vp = static_cast<const _Float16*>(a.v) + b * a.sv + static_cast<uint64_t>(h) * a.hd;
 
+    // Q rows of this wave go through LDS like the K tiles (4 DMA pieces of 8
+    // rows: 128-byte row segments per instruction instead of 32 rows x 32 bytes)
+    __shared__ __attribute__((aligned(16))) _Float16 Qs[BQ * 64];
     half8 qf[4];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-        const int d0 = 16 * s + 8 * g;
-        qf[s] = qi < a.Tq && d0 < hd ? *reinterpret_cast<const half8*>(Qp + static_cast<uint64_t>(qi) * a.ldq + d0)
-                                     : zero8();
-    }
 
     // Chunk slots: K row k keeps chunk c at slot c ^ ((k / 2) % 8), V row k at
     // c ^ 4 ((k / 2) % 2) (conflict-free for the K reads and the transposing V
@@ -701,11 +698,26 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
         // prologue: K tiles 0, 1 and V tile 0 in LDS; S of tile 0; the running
         // max starts at tile 0's max (every query has a valid key in tile 0:
         // key 0 < L, and key 0 <= qi under the causal mask)
+        {
+            const uint32_t nq = qwave < a.Tq ? min(a.Tq - qwave, 32u) : 0u;
+            const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<_Float16*>(Qp + static_cast<uint64_t>(qwave) * a.ldq), 0,
+                nq ? static_cast<int>(((nq - 1) * a.ldq + a.hd) * 2) : 0, 0x00020000);
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const uint32_t row = 8 * p + (lane >> 3), c = (lane & 7) ^ ((row >> 1) & 7);
+                lds_dma16(rq, &Qs[wave * 2048 + p * 512],
+                          static_cast<int>(c * 8) < hd ? (row * static_cast<uint32_t>(a.ldq) + c * 8) * 2u : kOob);
+            }
+        }
         dma_k(0, 0);
         dma_v(0, 0);
         if (ntiles > 1) dma_k(kBKV, 1);
         dma_wait();
         __syncthreads();
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            qf[s] = *reinterpret_cast<const half8*>(&Qs[wave * 2048 + l32 * 64 + (((2 * s + g) ^ ((l32 >> 1) & 7)) * 8)]);
         read_k(0);
         floatx16 s0[2];
         qk(s0);
@@ -846,8 +858,8 @@ int run(const mi_attn_args& x, hipStream_t s, const char* fn) {
                    ldo = x.ldo ? x.ldo : x.C;
     if (ldq < x.C || ldk < x.C || ldv < x.C || ldo < x.C) return fail(MI_ERR_INVALID_ARG, "%s: token stride < C", fn);
     // a 64-row K/V tile must span under 2^30 bytes (32-bit buffer offsets)
-    if (ldk * 64 * 4 >= (1ull << 30) || ldv * 64 * 4 >= (1ull << 30))
-        return fail(MI_ERR_UNSUPPORTED, "%s: K/V token stride too large", fn);
+    if (ldq * 64 * 4 >= (1ull << 30) || ldk * 64 * 4 >= (1ull << 30) || ldv * 64 * 4 >= (1ull << 30))
+        return fail(MI_ERR_UNSUPPORTED, "%s: Q/K/V token stride too large", fn);
     const uint64_t sq = x.sq ? x.sq : x.Tq * ldq, sk = x.sk ? x.sk : x.Tk * ldk, sv = x.sv ? x.sv : x.Tk * ldv,
                    so = x.so ? x.so : x.Tq * ldo;
     const uint64_t ei = x.in_dtype == MI_F32 ? 4 : 2, eo = x.out_dtype == MI_F32 ? 4 : 2;
