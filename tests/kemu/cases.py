@@ -200,16 +200,22 @@ def gemm_nn(E, *, M, N, K, mode=0, batch=1, lda=0, ldb=0, ldc=0, sA=0, sB=0, sC=
 
 
 def attention(E, *, batch=1, Tq, Tk, C, heads, causal=False, f16_in=False, f16_out=False, kv_len=None, seed=1,
-              front=False, order=0, tol=2e-3, nw=None, outliers=None):
+              front=False, order=0, tol=2e-3, nw=None, outliers=None, direct_store=False):
     """mi_fused_attention_ex (contiguous [batch, T, C]) against the oracle;
     nw pins the fp16 kernel's workgroup size (MI_ATTN_NW); outliers: key
     indices whose scores stand far above the rest (q ~ 1, k ~ 0.1 N(0, 1),
-    those keys 3.0), so that a running max that misses them overflows."""
+    those keys 3.0), so that a running max that misses them overflows;
+    direct_store: output stores straight from the MFMA layout
+    (MI_ATTN_DIRECT_STORE) instead of whole rows through LDS."""
     E.order(order)
     if nw:
         os.environ["MI_ATTN_NW"] = str(nw)
     else:
         os.environ.pop("MI_ATTN_NW", None)
+    if direct_store:
+        os.environ["MI_ATTN_DIRECT_STORE"] = "1"
+    else:
+        os.environ.pop("MI_ATTN_DIRECT_STORE", None)
     idt = np.float16 if f16_in else np.float32
     q = ob.normal(seed, batch * Tq * C).astype(idt)
     k = ob.normal(seed + 1, batch * Tk * C).astype(idt)
@@ -365,6 +371,7 @@ def attention_full(E, *, batch, Tq, Tk, C, heads, masked=False, nw=None, seed=1,
         os.environ["MI_ATTN_NW"] = str(nw)
     else:
         os.environ.pop("MI_ATTN_NW", None)
+    os.environ.pop("MI_ATTN_DIRECT_STORE", None)
     q = ob.normal(seed, batch * Tq * C).astype(np.float16)
     k = ob.normal(seed + 1, batch * Tk * C).astype(np.float16)
     v = ob.normal(seed + 2, batch * Tk * C).astype(np.float16)

@@ -181,3 +181,46 @@ def test_strided_layouts_and_scale(gpu, oracle):
             p = np.exp(s - s.max(1, keepdims=True))
             want[:, h * hd:(h + 1) * hd] = (p @ V[:, h * hd:(h + 1) * hd]) / p.sum(1, keepdims=True)
         assert_parity(got[b], want, what=f"strided b={b}")
+
+
+@pytest.mark.parametrize("C,heads", [(128, 2), (80, 2)])
+def test_staged_and_direct_output_stores_agree(gpu, oracle, monkeypatch, C, heads):
+    """Output rows go through LDS (16-byte stores of whole rows) when the rows and head columns are 16-byte
+    aligned, else straight from the MFMA layout: both give the same bits, in both kernels (fp16 and fp32
+    inputs), for both output types, with a partial last row block and key padding. MI_ATTN_DIRECT_STORE
+    forces the direct stores; an output 8 bytes off 16-byte alignment takes them by itself (fp16)."""
+    B, Tq, Tk = 2, 130, 150
+    kv_len = np.array([150, 61], dtype=np.int32)
+    dl = DeviceBuffer.from_array(kv_len)
+    for in_dtype, idt in ((MI_F16, np.float16), (MI_F32, np.float32)):
+        q = oracle.normal(21, B * Tq * C).astype(idt)
+        k = oracle.normal(22, B * Tk * C).astype(idt)
+        v = oracle.normal(23, B * Tk * C).astype(idt)
+        dq, dk, dv = (DeviceBuffer.from_array(x) for x in (q, k, v))
+        for out_dtype, odt in ((MI_F16, np.float16), (MI_F32, np.float32)):
+            n = B * Tq * C
+            do = DeviceBuffer(n * odt().itemsize + 16)
+            outs = []
+            for direct, off in ((False, 0), (True, 0), (False, 8)):
+                if off and odt is np.float32:
+                    continue
+                print(f"[case] C={C} in={in_dtype} out={out_dtype} direct={direct} offset={off}", flush=True)
+                if direct:
+                    monkeypatch.setenv("MI_ATTN_DIRECT_STORE", "1")
+                else:
+                    monkeypatch.delenv("MI_ATTN_DIRECT_STORE", raising=False)
+                ops.fused_attention_ex(dq, dk, dv, do.value + off, batch=B, Tq=Tq, Tk=Tk, C=C, heads=heads,
+                                       in_dtype=in_dtype, out_dtype=out_dtype, kv_len=dl)
+                synchronize()
+                outs.append(do.download(odt, n, offset=off))
+            monkeypatch.delenv("MI_ATTN_DIRECT_STORE", raising=False)
+            for o in outs[1:]:
+                assert np.array_equal(o.view(np.uint8), outs[0].view(np.uint8)), "staged and direct stores differ"
+            want = oracle.fused_attention_ex(q, k, v, batch=B, Tq=Tq, Tk=Tk, C=C, heads=heads,
+                                             in_dtype=oracle.OR_F16 if in_dtype == MI_F16 else oracle.OR_F32,
+                                             kv_len=kv_len).reshape(-1).astype(np.float64)
+            got = outs[0].astype(np.float64)
+            if odt is np.float16:
+                assert np.all(np.abs(got - want) <= REL_RMS_TOL * rms(want) + fp16_half_ulp(want))
+            else:
+                assert_parity(got, want, what="staged store")

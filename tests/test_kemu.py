@@ -124,6 +124,9 @@ FAMILIES = {
         # one far-outlying key per tile, in either lane half of a query (the running max spans both)
         dict(Tq=64, Tk=192, C=128, heads=2, f16_in=True, outliers=[5, 66, 134]),
         dict(Tq=64, Tk=192, C=128, heads=2, outliers=[5, 66, 134]),
+        # output stores straight from the MFMA layout (the path for rows not 16-byte aligned), both kernels
+        dict(batch=2, Tq=70, Tk=77, C=640, heads=10, f16_in=True, f16_out=True, kv_len=[77, 40], direct_store=True),
+        dict(Tq=100, Tk=300, C=128, heads=2, causal=True, direct_store=True),
     ],
     "block": [
         dict(B=1, T=33, C=64, H=1, Tc=5, Cc=96, F=160),
@@ -270,6 +273,11 @@ PLANTED = {
     "attn_dma_wait": ("attention.hip", "            dma_wait();\n            __syncthreads();\n        };",
                       "            __syncthreads();\n        };",
                       dict(case="attention", batch=2, Tq=130, Tk=200, C=128, heads=2, f16_in=True, f16_out=True)),
+    # attention: output rows read back from LDS without the wave barrier after the wave's writes
+    "attn_store_wave_barrier": ("attention.hip", "    __builtin_amdgcn_wave_barrier();\n    constexpr int RPI",
+                                "    constexpr int RPI",
+                                dict(case="attention", batch=2, Tq=130, Tk=77, C=640, heads=10, f16_in=True,
+                                     f16_out=False, kv_len=[77, 13], nw=4)),
     # the lane index the 8-wave GEMM epilogue takes from v_mbcnt, off by one
     "lane_id": ("common.hpp", "__builtin_amdgcn_mbcnt_lo(~0u, 0u)", "__builtin_amdgcn_mbcnt_lo(~0u, 1u)",
                 dict(case="gemm_nt", M=300, N=300, K=256, cfg="0")),
