@@ -1479,7 +1479,12 @@ void launch(int cfg, const GemmArgs& a, uint32_t batch, uint32_t splits, float* 
         case kR256x128Q: launch_rows<4, WK, true, EPI>(a, batch, splits, ws, s); break;
         case kR256x128: launch_rows<4, WK, false, EPI>(a, batch, splits, ws, s); break;
         case kC256x128: launch_cfg<256, 128, 4, 2, 2, WK, false, 2, EPI>(a, batch, splits, ws, s); break;
-        case kC128x128: launch_cfg<128, 128, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, ws, s); break;
+        case kC128x128:
+            // one register set: the loop then issues most of a step's MFMAs before
+            // converting the next step's loads (8192x640x2560 58 vs 68 us with two
+            // sets, 2048x1280x5120 71 vs 76, 8192x640x640 20 vs 22, the rest equal)
+            launch_cfg<128, 128, 2, 2, 2, WK, false, 1, EPI>(a, batch, splits, ws, s);
+            break;
         case kC256x128W4: launch_cfg<256, 128, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, ws, s); break;
         case kC192x256: launch_cfg<192, 256, 2, 4, 2, WK, false, 2, EPI>(a, batch, splits, ws, s); break;
         case kC128x256W4: launch_cfg<128, 256, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, ws, s); break;
