@@ -113,8 +113,13 @@ class AttnCase:
         self.flops = 4.0 * B * H * Tq * Tk * 64
         self.bytes = 2.0 * B * (2 * Tq * self.C + 2 * Tk * self.C) + (4 * B if masked else 0)
 
+        # the key-split plan's workspace (mi_fused_attention_ws), when the shape has one
+        self.ws_bytes = ops.fused_attention_ws_bytes(batch=B, Tq=Tq, Tk=Tk, C=self.C, heads=H, in_dtype=1,
+                                                     out_dtype=1, kv_len=self.kv_len)
+        self.ws = hip.DeviceBuffer(self.ws_bytes) if self.ws_bytes else None
+
     def run(self, stream):
-        self.ops.fused_attention_ex(self.q, self.k, self.v, self.o, batch=self.B, Tq=self.Tq, Tk=self.Tk,
+        self.ops.fused_attention_ws(self.q, self.k, self.v, self.o, self.ws, batch=self.B, Tq=self.Tq, Tk=self.Tk,
                                     C=self.C, heads=self.H, in_dtype=1, out_dtype=1, kv_len=self.kv_len,
                                     stream=stream)
 

@@ -260,6 +260,21 @@ typedef struct mi_attn_args {
 
 int mi_fused_attention_ex(const mi_attn_args* args, void* stream);
 
+/* mi_fused_attention_ex with a caller workspace (extension; the reference
+ * launches one dispatch per call). When the fp16 kernel's grid ends in a
+ * partial round of query blocks (e.g. 2 x 10 heads x 4096 queries: 640 blocks
+ * of 128 queries against 512 resident), the blocks of that round run as
+ * several workgroups over consecutive key ranges whose partial results are
+ * added, in a fixed order, by a second kernel; the last round then fills the
+ * GPU. Only unmasked, non-causal fp16 calls split. mi_fused_attention_ws_bytes
+ * gives the bytes the call's plan needs (0: no split); a smaller workspace (or
+ * NULL) runs mi_fused_attention_ex's plan. The workspace: 16-byte aligned,
+ * disjoint from q, k, v and out; calls sharing one must not overlap in time.
+ * Results differ from mi_fused_attention_ex's in the last bits (a different
+ * summation order) and repeat bit for bit.                                   */
+uint64_t mi_fused_attention_ws_bytes(const mi_attn_args* args);
+int mi_fused_attention_ws(const mi_attn_args* args, void* workspace, uint64_t workspace_bytes, void* stream);
+
 /* --------------------------------------------------------- block glue -- *
  * The SDXL transformer block's row / elementwise operators, fp32.          */
 

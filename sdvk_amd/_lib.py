@@ -91,6 +91,8 @@ SIGNATURES = {
     "mi_fused_attn_supported": (ctypes.c_int, [_u32, _u32]),
     "mi_fused_attention": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, ctypes.c_int, _vp]),
     "mi_fused_attention_ex": (ctypes.c_int, [ctypes.POINTER(MiAttnArgs), _vp]),
+    "mi_fused_attention_ws_bytes": (ctypes.c_uint64, [ctypes.POINTER(MiAttnArgs)]),
+    "mi_fused_attention_ws": (ctypes.c_int, [ctypes.POINTER(MiAttnArgs), _vp, ctypes.c_uint64, _vp]),
     "mi_layernorm": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, ctypes.c_float, _vp]),
     "mi_geglu": (ctypes.c_int, [_vp, _vp, _u32, _u32, _vp]),
     "mi_add_inplace": (ctypes.c_int, [_vp, _vp, _u64, _vp]),

@@ -30,6 +30,7 @@
 //     MFMA per product.
 #include "common.hpp"
 
+#include <atomic>
 #include <cstdlib>
 #include <cstring>
 #include <type_traits>
@@ -45,6 +46,9 @@ constexpr int kKld = 72;   // K tile LDS row stride (halves): 64 d + 8 pad
 // then spread over the banks instead of hitting one bank in four.
 constexpr int kVG = 66;
 constexpr int kThreads = 256;
+// floats per key-split piece in the workspace: O rows [kBQ][64], then the running max and the row sum of
+// each of the kBQ queries
+constexpr uint32_t kPartFloats = kBQ * 64 + 2 * kBQ;
 
 struct AttnArgs {
     const void* q;
@@ -57,6 +61,11 @@ struct AttnArgs {
     const int32_t* kv_len;
     float c;  // scale * log2(e)
     int ostage;  // output rows and head columns 16-byte aligned: store O through LDS (store_o_rows)
+    // Key-split plan of the fp16 kernel (mi_fused_attention_ws): the first nfull query blocks run
+    // whole; each later one runs as `pieces` workgroups over consecutive key-tile ranges that write
+    // unnormalised partials to `part` (kPartFloats floats per piece), merged by attn_merge_kernel.
+    uint32_t nfull, pieces;
+    float* part;
 };
 
 // 8 consecutive elements as fp16 (hi); for fp32 sources also the residual
@@ -503,7 +512,18 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
     __shared__ __attribute__((aligned(16))) _Float16 Ks[2][kBKV * 64];
     __shared__ __attribute__((aligned(16))) _Float16 Vs[2][kBKV * 64];
 
-    const unsigned blk = xcd_swizzle(blockIdx.x, gridDim.x);
+    // block -> query block (and key range of a piece)
+    unsigned blk;
+    uint32_t piece = 0;
+    bool split = false;
+    if (a.pieces > 1 && blockIdx.x >= a.nfull) {
+        const unsigned j = xcd_swizzle(blockIdx.x - a.nfull, gridDim.x - a.nfull);
+        blk = a.nfull + j / a.pieces;
+        piece = j % a.pieces;
+        split = true;
+    } else {
+        blk = xcd_swizzle(blockIdx.x, a.pieces > 1 ? a.nfull : gridDim.x);
+    }
     const uint32_t qt = blk % qtiles, bh = blk / qtiles;
     const uint32_t h = bh % a.heads, b = bh / a.heads;
     const int tid = threadIdx.x;
@@ -521,7 +541,10 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
     if (a.causal) kend = min(kend, qcta + BQ);
     uint32_t kfull = L / kBKV * kBKV;
     if (a.causal) kfull = min(kfull, (qwave + 1) / kBKV * kBKV);
-    const uint32_t ntiles = (kend + kBKV - 1) / kBKV;
+    const uint32_t ntiles_all = (kend + kBKV - 1) / kBKV;
+    // key tiles [t0, ntiles) of this workgroup (a piece: its share, in piece order)
+    const uint32_t t0 = split ? ntiles_all * piece / a.pieces : 0u;
+    const uint32_t ntiles = split ? ntiles_all * (piece + 1) / a.pieces : ntiles_all;
 
     const _Float16* Qp = static_cast<const _Float16*>(a.q) + b * a.sq + static_cast<uint64_t>(h) * a.hd;
     const _Float16* Kp = static_cast<const _Float16*>(a.k) + b * a.sk + static_cast<uint64_t>(h) * a.hd;
@@ -694,10 +717,11 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
                 for (int u = 0; u < 2; ++u) o[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[t][sp][u], pf[t][sp], o[u], 0, 0, 0);
     };
 
-    if (ntiles > 0) {
-        // prologue: K tiles 0, 1 and V tile 0 in LDS; S of tile 0; the running
-        // max starts at tile 0's max (every query has a valid key in tile 0:
-        // key 0 < L, and key 0 <= qi under the causal mask)
+    if (t0 < ntiles) {
+        // prologue: K tiles t0, t0+1 and V tile t0 in LDS; S of tile t0; the
+        // running max starts at that tile's max (every query has a valid key in
+        // it: key 0 < L and key 0 <= qi under the causal mask for t0 = 0, and
+        // key-split plans have no mask)
         {
             const uint32_t nq = qwave < a.Tq ? min(a.Tq - qwave, 32u) : 0u;
             const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
@@ -710,25 +734,25 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
                           static_cast<int>(c * 8) < hd ? (row * static_cast<uint32_t>(a.ldq) + c * 8) * 2u : kOob);
             }
         }
-        dma_k(0, 0);
-        dma_v(0, 0);
-        if (ntiles > 1) dma_k(kBKV, 1);
+        dma_k(t0 * kBKV, t0 & 1);
+        dma_v(t0 * kBKV, t0 & 1);
+        if (t0 + 1 < ntiles) dma_k((t0 + 1) * kBKV, (t0 + 1) & 1);
         dma_wait();
         __syncthreads();
 #pragma unroll
         for (int s = 0; s < 4; ++s)
             qf[s] = *reinterpret_cast<const half8*>(&Qs[wave * 2048 + l32 * 64 + (((2 * s + g) ^ ((l32 >> 1) & 7)) * 8)]);
-        read_k(0);
+        read_k(t0 & 1);
         floatx16 s0[2];
         qk(s0);
-        if (0 >= kfull) mask(s0, 0);
+        if (t0 * kBKV >= kfull) mask(s0, t0 * kBKV);
         const float mx0 = lane_max(s0);
         m = mx0 == -INFINITY ? 0.0f : mx0 * a.c;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int r = 0; r < 16; ++r) s0[t][r] = __builtin_fmaf(s0[t][r], a.c, -m);
-        __syncthreads();  // every wave has read K tile 0 before it is overwritten
+        __syncthreads();  // every wave has read K tile t0 before it is overwritten
 
         // One pipelined iteration; boundary tiles (key padding, Tk end, causal
         // diagonal) take the masked instantiation so that neither body branches
@@ -777,7 +801,7 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
             dma_wait();
             __syncthreads();
         };
-        for (uint32_t j = 0; j + 1 < ntiles; ++j) {
+        for (uint32_t j = t0; j + 1 < ntiles; ++j) {
             if ((j + 1) * kBKV >= kfull) step(j, std::true_type{});
             else step(j, std::false_type{});
         }
@@ -792,6 +816,22 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
     // the query's row sum: this lane's 32 keys of every tile plus the partner
     // lane's (one rounding, the same in both lanes: fp32 addition commutes)
     const float lt = lsum + __shfl_xor(lsum, 32);
+    if (split) {
+        // a piece: the unnormalised O rows (fp32, through the K / V stages like the
+        // output), the running max and the row sum of each query, for attn_merge_kernel
+        __syncthreads();
+        constexpr int kWB = 32 * 64 * 4;
+        constexpr int kStage = static_cast<int>(sizeof(Ks));
+        char* st = wave * kWB < kStage ? reinterpret_cast<char*>(&Ks[0][0]) + wave * kWB
+                                       : reinterpret_cast<char*>(&Vs[0][0]) + (wave * kWB - kStage);
+        float* P = a.part + static_cast<uint64_t>((blk - a.nfull) * a.pieces + piece) * kPartFloats;
+        store_o_rows<float>(o, 1.0f, st, P + wave * 32 * 64, 32, 64, 64, lane);
+        if (lane < 32) {
+            P[kBQ * 64 + wave * 32 + lane] = m;
+            P[kBQ * 64 + kBQ + wave * 32 + lane] = lt;
+        }
+        return;
+    }
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
     if (a.ostage) {
         // every wave is done with the K / V stages: each takes 32 * 64 * sizeof(TO)
@@ -825,16 +865,123 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
         }
 }
 
+
+// Adds the key-split pieces of a query block (mi_fused_attention_ws): O = sum_i 2^(m_i - M) O_i /
+// sum_i 2^(m_i - M) l_i with M = max_i m_i, pieces in order (a call repeats bit for bit). One
+// workgroup per split query block; thread t takes query t / 2 and half t % 2 of its 64 columns.
+template <typename TO>
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, uint32_t qtiles) {
+    const uint32_t rb = blockIdx.x, blk = a.nfull + rb;
+    const uint32_t qt = blk % qtiles, bh = blk / qtiles;
+    const uint32_t h = bh % a.heads, b = bh / a.heads;
+    const int q = threadIdx.x >> 1, dh = (threadIdx.x & 1) * 32;
+    const uint32_t qi = qt * kBQ + q;
+    if (qi >= a.Tq) return;
+    const float* P = a.part + static_cast<uint64_t>(rb) * a.pieces * kPartFloats;
+    float M = -INFINITY;
+    for (uint32_t i = 0; i < a.pieces; ++i) M = fmaxf(M, P[i * kPartFloats + kBQ * 64 + q]);
+    float l = 0.0f;
+    float acc[32];
+#pragma unroll
+    for (int d = 0; d < 32; ++d) acc[d] = 0.0f;
+    for (uint32_t i = 0; i < a.pieces; ++i) {
+        const float* Pi = P + i * kPartFloats;
+        const float mi = Pi[kBQ * 64 + q];
+        const float sc = mi == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mi - M);
+        l += sc * Pi[kBQ * 64 + kBQ + q];
+        const floatx4* row = reinterpret_cast<const floatx4*>(Pi + q * 64 + dh);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const floatx4 v = row[c];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[4 * c + e] += sc * v[e];
+        }
+    }
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    const int hd = static_cast<int>(a.hd);
+    TO* Op = static_cast<TO*>(a.o) + b * a.so + static_cast<uint64_t>(qi) * a.ldo + static_cast<uint64_t>(h) * a.hd;
+#pragma unroll
+    for (int d = 0; d < 32; ++d)
+        if (dh + d < hd) Op[dh + d] = static_cast<TO>(acc[d] * inv);
+}
+
+// Waves per workgroup of the fp16 kernel: 4 when that gives at least two
+// workgroups per CU, else 2; MI_ATTN_NW = 2 or 4 pins one (tuning sweeps).
+int f16_waves(const AttnArgs& a, uint32_t batch) {
+    const uint64_t q4 = ceil_div(a.Tq, 128u), groups = static_cast<uint64_t>(a.heads) * batch;
+    const char* env = std::getenv("MI_ATTN_NW");
+    return env && std::strcmp(env, "2") == 0 ? 2 : env && std::strcmp(env, "4") == 0 ? 4 : q4 * groups >= 512 ? 4 : 2;
+}
+
+// Compute units of the current device (queried once per device).
+uint32_t cu_count() {
+    constexpr int kMaxDevices = 64;
+    static std::atomic<int> cache[kMaxDevices];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n > 0) return static_cast<uint32_t>(n);
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+    return static_cast<uint32_t>(n);
+}
+
+// Key split of the grid's last partial round (mi_fused_attention_ws): with W
+// 4-wave query blocks and S = 2 per CU resident at once, W = r S + rest runs
+// r full rounds and then `rest` blocks alone on part of the GPU. Those rest
+// blocks instead run as `pieces` workgroups each over consecutive key-tile
+// ranges (pieces = S / rest, >= 8 tiles each, at most 8), so the last round
+// fills the GPU for a fraction of a round; attn_merge_kernel adds the pieces.
+// Plans of fewer than 4 pieces are not taken: measured, 2 x 12 heads x 4096
+// (256 rest blocks in 2 pieces) ran 141 us against 131 unsplit, while 2 x 10
+// heads (128 in 4) ran 120 against 126.
+// Only unmasked, non-causal fp16 launches split. MI_ATTN_SPLIT="<rest>:<pieces>"
+// forces a plan (tests).
+struct SplitPlan {
+    uint32_t nfull = 0, pieces = 1, rest = 0;
+};
+
+SplitPlan plan_split(const AttnArgs& a, uint32_t batch) {
+    SplitPlan p;
+    if (a.causal || a.kv_len || a.Tk == 0 || f16_waves(a, batch) != 4) return p;
+    const uint64_t W = static_cast<uint64_t>(ceil_div(a.Tq, kBQ)) * a.heads * batch;
+    const uint32_t nt = ceil_div(a.Tk, kBKV);
+    uint64_t rest = 0, pieces = 1;
+    const char* env = std::getenv("MI_ATTN_SPLIT");
+    if (env && *env) {
+        rest = std::strtoull(env, nullptr, 10);
+        const char* c = std::strchr(env, ':');
+        pieces = c ? std::strtoull(c + 1, nullptr, 10) : 2;
+        rest = rest < W ? rest : W;
+        if (pieces > nt) pieces = nt;
+    } else {
+        const uint64_t S = 2ull * cu_count();
+        if (W <= S || W % S == 0) return p;
+        rest = W % S;
+        pieces = S / rest;
+        if (pieces > nt / 8) pieces = nt / 8;
+        if (pieces > 8) pieces = 8;
+    }
+    if (rest == 0 || pieces < 2 || (!(env && *env) && pieces < 4)) return p;
+    p.rest = static_cast<uint32_t>(rest);
+    p.pieces = static_cast<uint32_t>(pieces);
+    p.nfull = static_cast<uint32_t>(W - rest);
+    return p;
+}
+
+uint64_t split_bytes(const SplitPlan& p) { return static_cast<uint64_t>(p.rest) * p.pieces * kPartFloats * 4; }
+
 template <typename TO>
 void launch_f16(const AttnArgs& a, uint32_t batch, hipStream_t s) {
-    // 4-wave workgroups when they give at least two per CU, else 2-wave ones;
-    // MI_ATTN_NW = 2 or 4 pins one (tuning sweeps)
     const uint32_t q4 = ceil_div(a.Tq, 128u), q2 = ceil_div(a.Tq, 64u);
     const uint64_t groups = static_cast<uint64_t>(a.heads) * batch;
-    const char* env = std::getenv("MI_ATTN_NW");
-    const int nw = env && std::strcmp(env, "2") == 0 ? 2 : env && std::strcmp(env, "4") == 0 ? 4
-                   : q4 * groups >= 512 ? 4 : 2;
-    if (nw == 4) attn_f16_kernel<TO, 4><<<static_cast<unsigned>(q4 * groups), 256, 0, s>>>(a, q4);
+    if (a.pieces > 1) {  // a key-split plan (4-wave workgroups)
+        const uint32_t rest = static_cast<uint32_t>(q4 * groups - a.nfull);
+        attn_f16_kernel<TO, 4><<<a.nfull + rest * a.pieces, 256, 0, s>>>(a, q4);
+        attn_merge_kernel<TO><<<rest, 256, 0, s>>>(a, q4);
+        return;
+    }
+    if (f16_waves(a, batch) == 4) attn_f16_kernel<TO, 4><<<static_cast<unsigned>(q4 * groups), 256, 0, s>>>(a, q4);
     else attn_f16_kernel<TO, 2><<<static_cast<unsigned>(q2 * groups), 128, 0, s>>>(a, q2);
 }
 
@@ -845,7 +992,10 @@ void launch_typed(const AttnArgs& a, uint32_t batch, bool vec, hipStream_t s) {
     else attn_kernel<TI, TO, false><<<grid, kThreads, 0, s>>>(a);
 }
 
-int run(const mi_attn_args& x, hipStream_t s, const char* fn) {
+// need: when set, only the workspace bytes a split plan would use are stored
+// (no launch); ws / ws_bytes: the caller's workspace (mi_fused_attention_ws).
+int run(const mi_attn_args& x, hipStream_t s, const char* fn, void* ws = nullptr, uint64_t ws_bytes = 0,
+        uint64_t* need = nullptr) {
     if (!x.q || !x.k || !x.v || !x.out) return fail(MI_ERR_INVALID_ARG, "%s: null pointer", fn);
     if (x.in_dtype != MI_F32 && x.in_dtype != MI_F16) return fail(MI_ERR_INVALID_ARG, "%s: in_dtype %d", fn, x.in_dtype);
     if (x.out_dtype != MI_F32 && x.out_dtype != MI_F16) return fail(MI_ERR_INVALID_ARG, "%s: out_dtype %d", fn, x.out_dtype);
@@ -895,6 +1045,29 @@ int run(const mi_attn_args& x, hipStream_t s, const char* fn) {
     // 64 or 128 queries of one (batch, head), 1-D grid)
     const bool fast = vec && x.in_dtype == MI_F16 &&
                       static_cast<uint64_t>(ceil_div(x.Tq, 64u)) * x.heads * x.batch < (1ull << 31);
+    a.nfull = 0;
+    a.pieces = 1;
+    a.part = nullptr;
+    if (fast && (need || ws)) {
+        const SplitPlan p = plan_split(a, x.batch);
+        const uint64_t bytes = p.pieces > 1 ? split_bytes(p) : 0;
+        if (need) {
+            *need = bytes;
+            return MI_OK;
+        }
+        if (bytes && ws_bytes >= bytes) {
+            if (!aligned(ws, 16)) return fail(MI_ERR_ALIGNMENT, "%s: workspace must be 16-byte aligned", fn);
+            if (overlaps(ws, bytes, x.out, obytes) || overlaps(ws, bytes, x.q, qbytes) ||
+                overlaps(ws, bytes, x.k, kbytes) || overlaps(ws, bytes, x.v, vbytes))
+                return fail(MI_ERR_ALIASING, "%s: workspace overlaps q, k, v or out", fn);
+            a.nfull = p.nfull;
+            a.pieces = p.pieces;
+            a.part = static_cast<float*>(ws);
+        }
+    } else if (need) {
+        *need = 0;
+        return MI_OK;
+    }
     if (fast && x.out_dtype == MI_F16) launch_f16<_Float16>(a, x.batch, s);
     else if (fast) launch_f16<float>(a, x.batch, s);
     else if (x.in_dtype == MI_F16 && x.out_dtype == MI_F16) launch_typed<_Float16, _Float16>(a, x.batch, vec, s);
@@ -927,4 +1100,16 @@ extern "C" int mi_fused_attention(const float* q, const float* k, const float* v
 extern "C" int mi_fused_attention_ex(const mi_attn_args* args, void* stream) {
     if (!args) return fail(MI_ERR_INVALID_ARG, "mi_fused_attention_ex: null args");
     return run(*args, static_cast<hipStream_t>(stream), "mi_fused_attention_ex");
+}
+
+extern "C" uint64_t mi_fused_attention_ws_bytes(const mi_attn_args* args) {
+    if (!args) return 0;
+    uint64_t need = 0;
+    return run(*args, nullptr, "mi_fused_attention_ws_bytes", nullptr, 0, &need) == MI_OK ? need : 0;
+}
+
+extern "C" int mi_fused_attention_ws(const mi_attn_args* args, void* workspace, uint64_t workspace_bytes,
+                                     void* stream) {
+    if (!args) return fail(MI_ERR_INVALID_ARG, "mi_fused_attention_ws: null args");
+    return run(*args, static_cast<hipStream_t>(stream), "mi_fused_attention_ws", workspace, workspace_bytes);
 }

@@ -89,6 +89,34 @@ def fused_attention_ex(q, k, v, out, *, batch: int, Tq: int, Tk: int, C: int, he
     call("mi_fused_attention_ex", ctypes.byref(x), _s(stream))
 
 
+def _attn_args(q, k, v, out, batch, Tq, Tk, C, heads, causal, in_dtype, out_dtype, ldq, ldk, ldv, ldo, sq, sk, sv, so,
+               kv_len, scale) -> MiAttnArgs:
+    return MiAttnArgs(q=ptr(q), k=ptr(k), v=ptr(v), out=ptr(out), batch=batch, Tq=Tq, Tk=Tk, C=C,
+                      heads=heads, causal=1 if causal else 0, in_dtype=in_dtype, out_dtype=out_dtype,
+                      ldq=ldq, ldk=ldk, ldv=ldv, ldo=ldo, sq=sq, sk=sk, sv=sv, so=so,
+                      kv_len=ptr(kv_len), scale=scale)
+
+
+def fused_attention_ws_bytes(*, batch: int, Tq: int, Tk: int, C: int, heads: int, causal: bool = False,
+                             in_dtype: int = MI_F32, out_dtype: int = MI_F32, kv_len=None) -> int:
+    """Workspace mi_fused_attention_ws uses for this call's key-split plan (0: no split); contiguous tensors
+    with 16-byte aligned rows assumed (the plan does not depend on the addresses otherwise)."""
+    x = _attn_args(0x1000, 0x2000_0000_000, 0x4000_0000_000, 0x6000_0000_000, batch, Tq, Tk, C, heads, causal,
+                   in_dtype, out_dtype, 0, 0, 0, 0, 0, 0, 0, 0, kv_len, 0.0)
+    return int(_lib.load().mi_fused_attention_ws_bytes(ctypes.byref(x)))
+
+
+def fused_attention_ws(q, k, v, out, workspace, *, batch: int, Tq: int, Tk: int, C: int, heads: int,
+                       causal: bool = False, in_dtype: int = MI_F32, out_dtype: int = MI_F32, ldq: int = 0,
+                       ldk: int = 0, ldv: int = 0, ldo: int = 0, sq: int = 0, sk: int = 0, sv: int = 0, so: int = 0,
+                       kv_len=None, scale: float = 0.0, stream=None) -> None:
+    """mi_fused_attention_ws: fused_attention_ex with a workspace for the key-split plan."""
+    x = _attn_args(q, k, v, out, batch, Tq, Tk, C, heads, causal, in_dtype, out_dtype, ldq, ldk, ldv, ldo, sq, sk,
+                   sv, so, kv_len, scale)
+    wp, wn = _ws(workspace)
+    call("mi_fused_attention_ws", ctypes.byref(x), wp, wn, _s(stream))
+
+
 # ------------------------------------------------------------------------ GEMM --
 
 def _ws(workspace):

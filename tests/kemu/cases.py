@@ -200,8 +200,10 @@ def gemm_nn(E, *, M, N, K, mode=0, batch=1, lda=0, ldb=0, ldc=0, sA=0, sB=0, sC=
 
 
 def attention(E, *, batch=1, Tq, Tk, C, heads, causal=False, f16_in=False, f16_out=False, kv_len=None, seed=1,
-              front=False, order=0, tol=2e-3, nw=None, outliers=None, direct_store=False):
+              front=False, order=0, tol=2e-3, nw=None, outliers=None, direct_store=False, split=None):
     """mi_fused_attention_ex (contiguous [batch, T, C]) against the oracle;
+    split "<rest>:<pieces>": through mi_fused_attention_ws with that key-split
+    plan forced (MI_ATTN_SPLIT) and the workspace the library asks for;
     nw pins the fp16 kernel's workgroup size (MI_ATTN_NW); outliers: key
     indices whose scores stand far above the rest (q ~ 1, k ~ 0.1 N(0, 1),
     those keys 3.0), so that a running max that misses them overflows;
@@ -216,6 +218,10 @@ def attention(E, *, batch=1, Tq, Tk, C, heads, causal=False, f16_in=False, f16_o
         os.environ["MI_ATTN_DIRECT_STORE"] = "1"
     else:
         os.environ.pop("MI_ATTN_DIRECT_STORE", None)
+    if split:
+        os.environ["MI_ATTN_SPLIT"] = split
+    else:
+        os.environ.pop("MI_ATTN_SPLIT", None)
     idt = np.float16 if f16_in else np.float32
     q = ob.normal(seed, batch * Tq * C).astype(idt)
     k = ob.normal(seed + 1, batch * Tk * C).astype(idt)
@@ -233,7 +239,14 @@ def attention(E, *, batch=1, Tq, Tk, C, heads, causal=False, f16_in=False, f16_o
     x = MiAttnArgs(q=dq.ptr, k=dk.ptr, v=dv.ptr, out=do.ptr, batch=batch, Tq=Tq, Tk=Tk, C=C, heads=heads,
                    causal=1 if causal else 0, in_dtype=MI_F16 if f16_in else MI_F32,
                    out_dtype=MI_F16 if f16_out else MI_F32, kv_len=dl.ptr if dl else None)
-    E.call("mi_fused_attention_ex", ctypes.byref(x), None)
+    if split:
+        nws = E.lib.mi_fused_attention_ws_bytes(ctypes.byref(x))
+        assert nws > 0, f"attention: split {split} planned no workspace"
+        dws = E.buf(nbytes=nws, front=front).fill(0xFF)  # NaN bytes: every partial read must have been written
+        E.call("mi_fused_attention_ws", ctypes.byref(x), dws.ptr, nws, None)
+        os.environ.pop("MI_ATTN_SPLIT", None)
+    else:
+        E.call("mi_fused_attention_ex", ctypes.byref(x), None)
     got = do.get(odt, n_out).astype(np.float64)
     want = ob.fused_attention_ex(q, k, v, batch=batch, Tq=Tq, Tk=Tk, C=C, heads=heads, causal=causal,
                                  in_dtype=ob.OR_F16 if f16_in else ob.OR_F32, out_dtype=ob.OR_F32, kv_len=kv_len,

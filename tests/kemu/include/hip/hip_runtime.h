@@ -59,6 +59,12 @@ inline hipError_t hipGetDevice(int* d) {
     *d = 0;
     return hipSuccess;
 }
+// The emulated device reports an MI355X's 256 compute units.
+enum hipDeviceAttribute_t { hipDeviceAttributeMultiprocessorCount = 1 };
+inline hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t attr, int) {
+    *v = attr == hipDeviceAttributeMultiprocessorCount ? 256 : 0;
+    return hipSuccess;
+}
 inline hipError_t hipGetSymbolAddress(void** p, const void* sym) {
     *p = const_cast<void*>(sym);
     return hipSuccess;

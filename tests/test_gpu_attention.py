@@ -224,3 +224,64 @@ def test_staged_and_direct_output_stores_agree(gpu, oracle, monkeypatch, C, head
                 assert np.all(np.abs(got - want) <= REL_RMS_TOL * rms(want) + fp16_half_ulp(want))
             else:
                 assert_parity(got, want, what="staged store")
+
+
+def test_key_split_workspace_entry(gpu, oracle, monkeypatch):
+    """mi_fused_attention_ws: the key-split plan of the last partial round of query blocks (2 x 10 heads x 4096,
+    640 blocks against 512 resident: 128 blocks in 4 key ranges) against the oracle on sampled rows, its repeat
+    bit for bit, and agreement with mi_fused_attention_ex; a workspace below the plan's size (and none) runs
+    mi_fused_attention_ex's plan exactly; forced plans on small shapes (uneven pieces, partial query block,
+    hd = 40) against the oracle."""
+    monkeypatch.delenv("MI_ATTN_SPLIT", raising=False)
+    B, H, T = 2, 10, 4096
+    C = H * 64
+    kw = dict(batch=B, Tq=T, Tk=T, C=C, heads=H, in_dtype=MI_F16, out_dtype=MI_F16)
+    nws = ops.fused_attention_ws_bytes(**kw)
+    assert nws == 128 * 4 * (128 * 64 + 2 * 128) * 4, nws
+    q, k, v = (oracle.normal(31 + i, B * T * C).astype(np.float16) for i in range(3))
+    dq, dk, dv = (DeviceBuffer.from_array(x) for x in (q, k, v))
+    ws = DeviceBuffer(nws)
+    outs = []
+    for w in (ws, ws, None, DeviceBuffer(nws - 16)):
+        print(f"[case] key split workspace {w.nbytes if w is not None else 0} B", flush=True)
+        do = DeviceBuffer(B * T * C * 2)
+        ops.fused_attention_ws(dq, dk, dv, do, w, **kw)
+        synchronize()
+        outs.append(do.download(np.float16, B * T * C))
+    assert np.array_equal(outs[0].view(np.uint16), outs[1].view(np.uint16)), "split plan does not repeat"
+    assert np.array_equal(outs[2].view(np.uint16), outs[3].view(np.uint16)), "small workspace changed the plan"
+    # the split blocks are the grid's last 128 (b = 1, heads 6..9): sample rows of both halves
+    rows = np.unique(np.concatenate([np.arange(0, T, 151), np.arange(T - 40, T)])).astype(np.uint32)
+    want = oracle.fused_attention_ex(q, k, v, batch=B, Tq=T, Tk=T, C=C, heads=H, in_dtype=oracle.OR_F16,
+                                     rows=rows, threads=oracle.max_threads()).astype(np.float64)
+    for o in (outs[0], outs[2]):
+        got = o.reshape(B, T, C)[:, rows].astype(np.float64)
+        assert np.all(np.abs(got - want) <= REL_RMS_TOL * rms(want) + fp16_half_ulp(want))
+    # everywhere (not only the sampled rows): split and unsplit each within the bar of the exact result
+    a0, a2 = outs[0].astype(np.float64), outs[2].astype(np.float64)
+    d = np.abs(a0 - a2)
+    print(f"  split vs unsplit max |diff| / RMS = {d.max() / rms(want):.2e}", flush=True)
+    assert np.all(d <= 2 * REL_RMS_TOL * rms(want) + 2 * fp16_half_ulp(np.maximum(np.abs(a0), np.abs(a2))))
+    for (B, Tq, Tk, C, heads, split, odt) in [(2, 300, 1000, 128, 2, "3:3", MI_F32), (1, 200, 130, 80, 2, "1:2", MI_F32),
+                                             (1, 256, 512, 128, 2, "2:4", MI_F16)]:
+        print(f"[case] forced split {split} B={B} Tq={Tq} Tk={Tk} C={C} heads={heads}", flush=True)
+        monkeypatch.setenv("MI_ATTN_SPLIT", split)
+        monkeypatch.setenv("MI_ATTN_NW", "4")
+        kw = dict(batch=B, Tq=Tq, Tk=Tk, C=C, heads=heads, in_dtype=MI_F16, out_dtype=odt)
+        nws = ops.fused_attention_ws_bytes(**kw)
+        assert nws > 0
+        q, k, v = (oracle.normal(41 + i, B * n * C).astype(np.float16) for i, n in enumerate((Tq, Tk, Tk)))
+        dq, dk, dv = (DeviceBuffer.from_array(x) for x in (q, k, v))
+        osz = 4 if odt == MI_F32 else 2
+        do = DeviceBuffer(B * Tq * C * osz)
+        ops.fused_attention_ws(dq, dk, dv, do, DeviceBuffer(nws), **kw)
+        synchronize()
+        got = do.download(np.float32 if odt == MI_F32 else np.float16, B * Tq * C).astype(np.float64)
+        want = oracle.fused_attention_ex(q, k, v, batch=B, Tq=Tq, Tk=Tk, C=C, heads=heads,
+                                         in_dtype=oracle.OR_F16).reshape(-1).astype(np.float64)
+        if odt == MI_F32:
+            assert_parity(got, want, what=f"forced split {split}")
+        else:
+            assert np.all(np.abs(got - want) <= REL_RMS_TOL * rms(want) + fp16_half_ulp(want))
+    monkeypatch.delenv("MI_ATTN_SPLIT", raising=False)
+    monkeypatch.delenv("MI_ATTN_NW", raising=False)

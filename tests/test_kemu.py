@@ -127,6 +127,12 @@ FAMILIES = {
         # output stores straight from the MFMA layout (the path for rows not 16-byte aligned), both kernels
         dict(batch=2, Tq=70, Tk=77, C=640, heads=10, f16_in=True, f16_out=True, kv_len=[77, 40], direct_store=True),
         dict(Tq=100, Tk=300, C=128, heads=2, causal=True, direct_store=True),
+        # key-split plans (mi_fused_attention_ws, forced): pieces of uneven tile counts, a partial query
+        # block, hd = 40, fp16 / fp32 output, an outlying key inside one piece
+        dict(batch=1, Tq=256, Tk=512, C=128, heads=2, f16_in=True, f16_out=True, split="2:4", nw=4),
+        dict(batch=2, Tq=300, Tk=1000, C=128, heads=2, f16_in=True, f16_out=False, split="3:3", nw=4),
+        dict(Tq=200, Tk=130, C=80, heads=2, f16_in=True, f16_out=False, split="1:2", nw=4),
+        dict(Tq=128, Tk=256, C=64, heads=1, f16_in=True, split="1:4", nw=4, outliers=[5, 70, 200]),
     ],
     "block": [
         dict(B=1, T=33, C=64, H=1, Tc=5, Cc=96, F=160),
