@@ -98,7 +98,7 @@ def _fake_ops(calls):
             calls.append(name)
             if name in ("block_workspace_bytes", "block_ctx_kv_bytes"):
                 return 1 << 20
-            if name in ("gemm_workspace_bytes", "gemm_nn_workspace_bytes"):
+            if name in ("gemm_workspace_bytes", "gemm_nn_workspace_bytes", "fused_attention_ws_bytes"):
                 return 1 << 16
             return None
         return f
@@ -155,7 +155,7 @@ def test_bench_line_on_stand_in_device(fake_device, monkeypatch, capsys):
     assert set(ex["gemm_candidates"]["us"]) == set(bench.GEMM_CANDIDATES)
     assert len(ex["gemm_candidates"]["best"]) == len(bench.GEMM_SHAPES) + 1
     assert ex["block_stack_plain"]["variant"] == {"cached_kv": False, "fused_epilogues": False, "joint_qkv": False}
-    for name in ("gemm_nt_q8_0", "fused_attention_ex", "gemm_nn_q8", "sdxl_block_forward", "block_ctx_kv",
+    for name in ("gemm_nt_q8_0", "fused_attention_ws", "gemm_nn_q8", "sdxl_block_forward", "block_ctx_kv",
                  "sdxl_block_forward_kv", "q8_0_quantize"):
         assert name in fake_device, name
 
