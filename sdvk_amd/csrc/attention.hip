@@ -867,42 +867,60 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
 
 
 // Adds the key-split pieces of a query block (mi_fused_attention_ws): O = sum_i 2^(m_i - M) O_i /
-// sum_i 2^(m_i - M) l_i with M = max_i m_i, pieces in order (a call repeats bit for bit). One
-// workgroup per split query block; thread t takes query t / 2 and half t % 2 of its 64 columns.
+// sum_i 2^(m_i - M) l_i with M = max_i m_i, pieces in order (a call repeats bit for bit). Four
+// workgroups per split query block; thread t of a workgroup takes query t / 8 of its 32 and the 8
+// columns 8 (t % 8) of the head, so a warp-wide access covers whole 256-byte partial rows and whole
+// output rows (one 16-byte store per thread for fp16 output when rows are 16-byte aligned).
 template <typename TO>
 __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, uint32_t qtiles) {
-    const uint32_t rb = blockIdx.x, blk = a.nfull + rb;
+    const uint32_t rb = blockIdx.x / 4, blk = a.nfull + rb;
     const uint32_t qt = blk % qtiles, bh = blk / qtiles;
     const uint32_t h = bh % a.heads, b = bh / a.heads;
-    const int q = threadIdx.x >> 1, dh = (threadIdx.x & 1) * 32;
+    const int q = static_cast<int>(blockIdx.x % 4) * 32 + static_cast<int>(threadIdx.x >> 3);
+    const int c = static_cast<int>(threadIdx.x & 7) * 8;
     const uint32_t qi = qt * kBQ + q;
-    if (qi >= a.Tq) return;
+    const int hd = static_cast<int>(a.hd);
+    if (qi >= a.Tq || c >= hd) return;
     const float* P = a.part + static_cast<uint64_t>(rb) * a.pieces * kPartFloats;
     float M = -INFINITY;
     for (uint32_t i = 0; i < a.pieces; ++i) M = fmaxf(M, P[i * kPartFloats + kBQ * 64 + q]);
     float l = 0.0f;
-    float acc[32];
-#pragma unroll
-    for (int d = 0; d < 32; ++d) acc[d] = 0.0f;
+    floatx4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
     for (uint32_t i = 0; i < a.pieces; ++i) {
         const float* Pi = P + i * kPartFloats;
         const float mi = Pi[kBQ * 64 + q];
         const float sc = mi == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mi - M);
         l += sc * Pi[kBQ * 64 + kBQ + q];
-        const floatx4* row = reinterpret_cast<const floatx4*>(Pi + q * 64 + dh);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const floatx4 v = row[c];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[4 * c + e] += sc * v[e];
-        }
+        const floatx4* row = reinterpret_cast<const floatx4*>(Pi + q * 64 + c);
+        acc0 += sc * row[0];
+        acc1 += sc * row[1];
     }
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    const int hd = static_cast<int>(a.hd);
-    TO* Op = static_cast<TO*>(a.o) + b * a.so + static_cast<uint64_t>(qi) * a.ldo + static_cast<uint64_t>(h) * a.hd;
+    acc0 *= inv;
+    acc1 *= inv;
+    TO* Op = static_cast<TO*>(a.o) + b * a.so + static_cast<uint64_t>(qi) * a.ldo + static_cast<uint64_t>(h) * a.hd + c;
+    if constexpr (sizeof(TO) == 2) {
+        const half8 v = {static_cast<_Float16>(acc0[0]), static_cast<_Float16>(acc0[1]), static_cast<_Float16>(acc0[2]),
+                         static_cast<_Float16>(acc0[3]), static_cast<_Float16>(acc1[0]), static_cast<_Float16>(acc1[1]),
+                         static_cast<_Float16>(acc1[2]), static_cast<_Float16>(acc1[3])};
+        if (a.ostage) {
+            *reinterpret_cast<half8*>(Op) = v;
+        } else {
 #pragma unroll
-    for (int d = 0; d < 32; ++d)
-        if (dh + d < hd) Op[dh + d] = static_cast<TO>(acc[d] * inv);
+            for (int e = 0; e < 8; ++e) Op[e] = v[e];
+        }
+    } else {
+        if (a.ostage) {
+            reinterpret_cast<floatx4*>(Op)[0] = acc0;
+            reinterpret_cast<floatx4*>(Op)[1] = acc1;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                Op[e] = acc0[e];
+                Op[4 + e] = acc1[e];
+            }
+        }
+    }
 }
 
 // Waves per workgroup of the fp16 kernel: 4 when that gives at least two
@@ -978,7 +996,7 @@ void launch_f16(const AttnArgs& a, uint32_t batch, hipStream_t s) {
     if (a.pieces > 1) {  // a key-split plan (4-wave workgroups)
         const uint32_t rest = static_cast<uint32_t>(q4 * groups - a.nfull);
         attn_f16_kernel<TO, 4><<<a.nfull + rest * a.pieces, 256, 0, s>>>(a, q4);
-        attn_merge_kernel<TO><<<rest, 256, 0, s>>>(a, q4);
+        attn_merge_kernel<TO><<<rest * 4, 256, 0, s>>>(a, q4);
         return;
     }
     if (f16_waves(a, batch) == 4) attn_f16_kernel<TO, 4><<<static_cast<unsigned>(q4 * groups), 256, 0, s>>>(a, q4);
