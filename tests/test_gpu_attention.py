@@ -154,6 +154,38 @@ def test_config3_cross_attention(gpu, oracle, heads, T):
     print(f"  kv_len={kv_len.tolist()} err/rms = {e:.3e}", flush=True)
 
 
+@pytest.mark.parametrize("nw", ["2", "4"])
+@pytest.mark.parametrize("B,Tq,Tk,C,heads,causal,kv_len", [
+    (2, 300, 1000, 128, 2, False, None),
+    (2, 200, 300, 128, 2, True, None),
+    (2, 130, 77, 640, 10, False, [77, 13]),
+    (1, 1024, 1024, 1280, 20, False, None),
+])
+def test_two_and_four_wave_workgroups(gpu, oracle, monkeypatch, nw, B, Tq, Tk, C, heads, causal, kv_len):
+    """The fp16 kernel's 64-query (2-wave) and 128-query (4-wave) workgroups,
+    pinned with MI_ATTN_NW, each against the oracle (the default rule takes
+    4 waves unless Tq <= 64)."""
+    print(f"[case] nw={nw} B={B} Tq={Tq} Tk={Tk} C={C} H={heads} causal={causal} kv_len={kv_len}", flush=True)
+    monkeypatch.setenv("MI_ATTN_NW", nw)
+    q = oracle.normal(21, B * Tq * C).astype(np.float16)
+    k = oracle.normal(22, B * Tk * C).astype(np.float16)
+    v = oracle.normal(23, B * Tk * C).astype(np.float16)
+    kl = np.asarray(kv_len, dtype=np.int32) if kv_len is not None else None
+    rows = _sample_rows(Tq, 40, 5) if Tq > 512 else None
+    want = oracle.fused_attention_ex(q, k, v, batch=B, Tq=Tq, Tk=Tk, C=C, heads=heads, in_dtype=1, causal=causal,
+                                     kv_len=kl, rows=rows, threads=oracle.max_threads())
+    for out_dtype in (MI_F32, MI_F16):
+        got = run_ex(q, k, v, batch=B, Tq=Tq, Tk=Tk, C=C, heads=heads, in_dtype=MI_F16, out_dtype=out_dtype,
+                     kv_len=kl, causal=causal)
+        g = (got[:, rows] if rows is not None else got).astype(np.float64)
+        w = want.reshape(g.shape)
+        if out_dtype == MI_F32:
+            assert_parity(g, w, what=f"nw={nw}")
+        else:
+            bound = REL_RMS_TOL * rms(w) + fp16_half_ulp(w)
+            assert np.all(np.abs(g - w) <= bound), f"nw={nw}: fp16 output beyond parity + storage rounding"
+
+
 def test_strided_layouts_and_scale(gpu, oracle):
     """Token strides > C (e.g. fused QKV buffers), batch strides with gaps, custom scale."""
     B, Tq, Tk, C, heads = 2, 150, 200, 128, 2

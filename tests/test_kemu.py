@@ -240,8 +240,8 @@ ROUTING = [
     ["nn_ws", [320, 4096, 2880], [16, 3, 8], 512], ["nn_ws", [640, 4096, 5760], [16, 5, 4], 512],
     ["nn_ws", [1280, 1024, 11520], [4, 10, 8], 512], ["nn_ws", [1280, 1024, 640], [4, 10, 2], 512],
     ["nn", [1280, 1024, 11520], [4, 10, 1], 512],
-    ["attn", [2, 10, 4096, 4096], [640, 1, 1], 256], ["attn", [2, 20, 1024, 1024], [640, 1, 1], 128],
-    ["attn", [2, 10, 4096, 77], [640, 1, 1], 256], ["attn", [2, 20, 1024, 77], [640, 1, 1], 128],
+    ["attn", [2, 10, 4096, 4096], [640, 1, 1], 256], ["attn", [2, 20, 1024, 1024], [320, 1, 1], 256],
+    ["attn", [2, 10, 4096, 77], [640, 1, 1], 256], ["attn", [2, 20, 1024, 77], [320, 1, 1], 256],
 ]
 
 
