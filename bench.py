@@ -10,7 +10,10 @@ resident in HBM:
     d = 64, fp16 in/out, no mask) and cross-attention (config 3: 77 context
     tokens, key-padding lengths U{1..77}).
 value = algorithmic FLOP of one step x steps / elapsed (HIP events on the
-launch stream), in TFLOP/s. The roofline of the dominant kernel family uses its
+launch stream), in TFLOP/s. By default each timed step replays one HIP graph
+per kernel family, captured once after the warm-up (the same launches on the
+same buffers; the replayed outputs are checked bit for bit against an eager
+pass afterwards); --launch eager issues every launch from the host instead. The roofline of the dominant kernel family uses its
 launch durations inside the timed steps (events at the family boundaries). The
 JSON line also carries a per-shape breakdown (each shape launched back to back
 after the timed region) and a CPU baseline (the oracle's OpenMP fp32
@@ -94,6 +97,9 @@ class GemmCase:
         self.ops.gemm_nt_q8_0(self.A, self.W, self.C, self.M, self.N, self.K, workspace=self.workspace(),
                               stream=stream)
 
+    def output(self):
+        return self.C.download(np.float32, self.M * self.N)
+
 
 class AttnCase:
     kernel = "attention"
@@ -122,6 +128,9 @@ class AttnCase:
         self.ops.fused_attention_ws(self.q, self.k, self.v, self.o, self.ws, batch=self.B, Tq=self.Tq, Tk=self.Tk,
                                     C=self.C, heads=self.H, in_dtype=1, out_dtype=1, kv_len=self.kv_len,
                                     stream=stream)
+
+    def output(self):
+        return self.o.download(np.float16, self.B * self.Tq * self.C)
 
 
 # SDXL 1024^2 convolutions as the NN GEMM sees them after im2col (M = output
@@ -540,6 +549,10 @@ def main() -> int:
     ap.add_argument("--reps", type=int, default=10, help="back-to-back launches per shape for the breakdown")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run one device-to-device copy of this many MiB first (profiler byte calibration)")
+    ap.add_argument("--launch", choices=["graph", "eager"], default="graph",
+                    help="timed steps replay one HIP graph per kernel family (captured once after the warm-up, "
+                         "checked bit for bit against an eager pass afterwards), or issue every launch from the "
+                         "host")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip the measurements outside the step metric")
     ap.add_argument("--extras-child", action="store_true", help=argparse.SUPPRESS)
@@ -603,20 +616,50 @@ def main() -> int:
             groups[-1][1].append(c)
         else:
             groups.append((c.kernel, [c]))
+    # With --launch graph each family's launches are captured once into a HIP
+    # graph (the warm-up has sized every workspace: nothing allocates under
+    # capture) and every timed step replays the graphs, with the events between
+    # them: the same kernels on the same buffers, without the host's per-launch
+    # cost between them.
+    graphs = []
+    if args.launch == "graph":
+        for _, members in groups:
+            gr = hip.Graph(stream)
+            gr.begin()
+            for c in members:
+                c.run(stream)
+            gr.end()
+            graphs.append(gr)
     marks = [[hip.Event() for _ in range(len(groups) + 1)] for _ in range(args.steps)]
     hip.synchronize()
     for st in range(args.steps):
         marks[st][0].record(stream)
         for g, (_, members) in enumerate(groups):
-            for c in members:
-                c.run(stream)
+            if graphs:
+                graphs[g].launch()
+            else:
+                for c in members:
+                    c.run(stream)
             marks[st][g + 1].record(stream)
     marks[-1][-1].synchronize()
     hip.synchronize()
     ms_total = marks[0][0].elapsed_ms(marks[-1][-1])
     step_flops = sum(c.flops for c in cases)
     value = step_flops * args.steps / (ms_total / 1e3) / 1e12
-    print(f"[bench] timed {args.steps} steps: {ms_total:.3f} ms", file=sys.stderr, flush=True)
+    print(f"[bench] timed {args.steps} steps ({args.launch}): {ms_total:.3f} ms", file=sys.stderr, flush=True)
+    launch_check = None
+    if graphs:
+        # the replayed steps' outputs must equal an eager pass bit for bit
+        # (every kernel stores plain values in a fixed order)
+        replayed = [c.output() for c in cases]
+        for c in cases:
+            c.run(stream)
+        stream.synchronize()
+        bad = [c.tag for c, r in zip(cases, replayed) if not np.array_equal(r.view(np.uint8), c.output().view(np.uint8))]
+        if bad:
+            raise SystemExit(f"graph replay differs from the eager launches: {bad}")
+        launch_check = "graph replay outputs bitwise equal to an eager pass"
+        del graphs
 
     fam_time, fam_flops, fam_bytes, fam_launch = {}, {}, {}, {}
     for g, (fam, members) in enumerate(groups):
@@ -699,7 +742,10 @@ def main() -> int:
                                        else [list(CONFIG0[1:])] if args.only == "cfg0" else []),
                    "attn_shapes_B_H_Tq_Tk": [[B, H, Tq, Tk] for _, B, H, Tq, Tk, _ in ATTN_SHAPES]
                    if args.only in (None, "step", "attention") else [],
-                   "step_gflop": round(step_flops / 1e9, 3)},
+                   "step_gflop": round(step_flops / 1e9, 3),
+                   "launch": ("one HIP graph per kernel family, captured once, replayed each step" if args.launch ==
+                              "graph" else "eager (every launch issued from the host)"),
+                   "launch_check": launch_check},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "block_stack": block,

@@ -43,6 +43,9 @@ class _Buf:
     def upload(self, a, offset=0):
         pass
 
+    def download(self, dtype, count):
+        return np.zeros(count, dtype=dtype)
+
 
 class _Stream:
     def synchronize(self):
@@ -122,7 +125,8 @@ def fake_device(monkeypatch):
     return calls
 
 
-def test_bench_line_on_stand_in_device(fake_device, monkeypatch, capsys):
+@pytest.mark.parametrize("launch", [None, "eager"])
+def test_bench_line_on_stand_in_device(fake_device, monkeypatch, capsys, launch):
     import bench
 
     # the extras child runs in-process here (same code path, no subprocess)
@@ -132,7 +136,7 @@ def test_bench_line_on_stand_in_device(fake_device, monkeypatch, capsys):
 
     monkeypatch.setattr(bench, "run_extras_child", child)
     monkeypatch.setattr(sys, "argv", ["bench.py", "--steps", "2", "--warmup", "1", "--reps", "2",
-                                      "--no-cpu-baseline"])
+                                      "--no-cpu-baseline"] + (["--launch", launch] if launch else []))
     assert bench.main() == 0
     lines = [l for l in capsys.readouterr().out.splitlines() if l.startswith("{")]
     assert len(lines) == 1
@@ -141,6 +145,11 @@ def test_bench_line_on_stand_in_device(fake_device, monkeypatch, capsys):
                 "scaling", "vs_baseline", "dtype", "data", "config", "roofline", "cpu_baseline"):
         assert key in out, key
     assert out["n_gpus"] == 1 and out["steps"] == 2 and out["value"] > 0
+    if launch is None:  # the default: graph replays, checked against an eager pass
+        assert out["config"]["launch"].startswith("one HIP graph per kernel family")
+        assert out["config"]["launch_check"] == "graph replay outputs bitwise equal to an eager pass"
+    else:
+        assert out["config"]["launch"].startswith("eager") and out["config"]["launch_check"] is None
     r = out["roofline"]
     assert r["bound"] == "mfma" and r["unit"] == "TFLOP/s" and 0 < r["frac"] == pytest.approx(r["achieved"] / r["peak"],
                                                                                             rel=1e-3)

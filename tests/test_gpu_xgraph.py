@@ -2,8 +2,9 @@
 C-ABI launches) and replayed give the eager results.
 
 The sequence holds a GEMM without K splits, a K-split GEMM (partials in a
-workspace, then the reduce pass), a K-split tiled NN GEMM (the same) and a
-key-padded fp16 attention. The graph is replayed three times with eager work
+workspace, then the reduce pass), a K-split tiled NN GEMM (the same), a
+key-padded fp16 attention and a key-split fp16 attention (pieces in a
+workspace, then the merge pass; the split forced with MI_ATTN_SPLIT). The graph is replayed three times with eager work
 and a synchronisation between the replays; every replay must equal the eager
 results bit for bit (every sum has a fixed order).
 """
@@ -17,7 +18,7 @@ from sdvk_amd.hip import DeviceBuffer
 pytestmark = pytest.mark.gpu
 
 
-def test_graph_replays_match_eager(gpu, oracle):
+def test_graph_replays_match_eager(gpu, oracle, monkeypatch):
     print("[case] graph capture / replay of GEMM, split-K GEMM, NN GEMM, attention", flush=True)
     st = hip.Stream()
     M1, N1, K1 = 2048, 1280, 1280            # no K split
@@ -36,8 +37,17 @@ def test_graph_replays_match_eager(gpu, oracle):
     k = DeviceBuffer.from_array(oracle.normal(8, B * Tk * C).astype(np.float16))
     v = DeviceBuffer.from_array(oracle.normal(9, B * Tk * C).astype(np.float16))
     kv_len = DeviceBuffer.from_array(np.array([77, 30], dtype=np.int32))
+    Ts, Tks, Hs = 256, 512, 2
+    qs = DeviceBuffer.from_array(oracle.normal(10, Ts * Hs * 64).astype(np.float16))
+    ks = DeviceBuffer.from_array(oracle.normal(11, Tks * Hs * 64).astype(np.float16))
+    vs = DeviceBuffer.from_array(oracle.normal(12, Tks * Hs * 64).astype(np.float16))
+    skw = dict(batch=1, Tq=Ts, Tk=Tks, C=Hs * 64, heads=Hs, in_dtype=MI_F16, out_dtype=MI_F16)
+    monkeypatch.setenv("MI_ATTN_NW", "4")
+    monkeypatch.setenv("MI_ATTN_SPLIT", "2:4")
+    ws4 = DeviceBuffer(ops.fused_attention_ws_bytes(**skw))
+    assert ws4.nbytes > 0, "the forced key split has no workspace"
     outs = [DeviceBuffer(M1 * N1 * 4), DeviceBuffer(M2 * N2 * 4), DeviceBuffer(M3 * N3 * 4),
-            DeviceBuffer(B * T * C * 4)]
+            DeviceBuffer(B * T * C * 4), DeviceBuffer(Ts * Hs * 64 * 2)]
     ws2 = DeviceBuffer(ops.gemm_workspace_bytes(M2, N2, K2))
     ws3 = DeviceBuffer(ops.gemm_nn_workspace_bytes(M3, N3, K3))
     assert ws2.nbytes > 0 and ws3.nbytes > 0, "the shapes no longer split K"
@@ -48,6 +58,7 @@ def test_graph_replays_match_eager(gpu, oracle):
         ops.gemm_nn_q8(P3, S3, B3, outs[2], M3, N3, K3, workspace=ws3, stream=st)
         ops.fused_attention_ex(q, k, v, outs[3], batch=B, Tq=T, Tk=Tk, C=C, heads=H, in_dtype=MI_F16,
                                out_dtype=MI_F32, kv_len=kv_len, stream=st)
+        ops.fused_attention_ws(qs, ks, vs, outs[4], ws4, stream=st, **skw)
 
     def read():
         st.synchronize()
@@ -74,6 +85,6 @@ def test_graph_replays_match_eager(gpu, oracle):
         got = read()
         ops.gemm_nt_q8_0(A1, W1, other, M1, N1, K1, stream=st)  # eager work between replays
         st.synchronize()
-        for i, what in enumerate(("GEMM", "K-split GEMM", "K-split NN GEMM", "attention")):
+        for i, what in enumerate(("GEMM", "K-split GEMM", "K-split NN GEMM", "attention", "key-split attention")):
             assert np.array_equal(got[i], eager[i]), f"replay {rep}: {what} differs from eager"
         print(f"  replay {rep} ok", flush=True)
