@@ -152,8 +152,8 @@ int mi_gemm_nt_q8_0_ws(const float* A, const void* W, const float* bias, float* 
  * of MI_GEMM_NOALLOC_SCRATCH_BYTES, held until the process ends. A shape whose
  * plan needs more scratch than that returns MI_ERR_UNSUPPORTED (no shape does
  * under the built-in tile rules: they split only grids of fewer than 256
- * 128 x 128 tiles into at most 2 parts, or fewer than 512 64 x 64 tiles into
- * about 256 workgroups, at most 32 MiB of partials). Calls on one GPU share
+ * 128 x 128 tiles, into at most 512 / tiles parts, or fewer than 512 64 x 64
+ * tiles into about 256 workgroups, at most 32 MiB of partials). Calls on one GPU share
  * the scratch: calls that overlap on one GPU (unordered streams) race, so
  * order them (one stream). Calls no hipMalloc / hipFree; the scratch's device
  * address is looked up once per GPU, on the first call made there.          */

@@ -233,7 +233,7 @@ ROUTING = [
     ["gemm", [8192, 640, 640], [320, 1, 1], 256], ["gemm", [8192, 5120, 640], [2560, 1, 1], 256],
     ["gemm", [8192, 640, 2560], [320, 1, 1], 256], ["gemm", [2048, 1280, 1280], [160, 1, 1], 256],
     ["gemm", [2048, 10240, 1280], [440, 1, 1], 512], ["gemm", [2048, 1280, 5120], [160, 1, 1], 256],
-    ["gemm_ws", [2048, 1280, 5120], [160, 2, 1], 256],
+    ["gemm_ws", [2048, 1280, 5120], [160, 3, 1], 256],
     ["gemm", [154, 640, 2048], [30, 1, 1], 256], ["gemm_ws", [154, 640, 2048], [30, 8, 1], 256],
     ["gemm", [154, 1280, 2048], [60, 1, 1], 256], ["gemm_ws", [154, 1280, 2048], [60, 4, 1], 256],
     ["gemm", [9216, 1280, 1280], [240, 1, 1], 512], ["gemm_ws", [9216, 1280, 1280], [240, 1, 1], 512],
