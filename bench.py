@@ -272,14 +272,25 @@ class BlockStack:
 
 
 def time_case(c, stream, hip, reps):
-    """Average launch time of `reps` back-to-back launches of case c (seconds) and its breakdown entry."""
-    c.run(stream)
+    """Average launch time of `reps` back-to-back launches of case c (seconds) and its breakdown entry.
+    The launches are captured into a HIP graph and timed on its second replay, so the time is the GPU's:
+    a kernel shorter than the host's per-call cost (ctypes, argument checks) would otherwise be timed
+    with the gaps between launches, and the first replay warms the clocks and caches."""
+    c.run(stream)  # sizes the workspaces: nothing allocates under capture
+    g = hip.Graph(stream)
+    g.begin()
+    try:
+        for _ in range(reps):
+            c.run(stream)
+    finally:
+        g.end()
+    g.launch()
     a, b = hip.Event(), hip.Event()
     a.record(stream)
-    for _ in range(reps):
-        c.run(stream)
+    g.launch()
     b.record(stream)
     b.synchronize()
+    del g
     sec = a.elapsed_ms(b) / 1e3 / reps
     tf, roof, frac = roofline_pct(c, sec)
     dims = {"M_N_K": [c.M, c.N, c.K]} if hasattr(c, "M") else {"B_H_Tq_Tk": [c.B, c.H, c.Tq, c.Tk]}
@@ -347,45 +358,60 @@ def extras(rng, hip, ops, stream, reps, emit=None):
         return run
 
     def candidates():
-        """{"shapes": [tag], "us": {cfg: [us per shape]}, "default_us": [...], "best": [[cfg, us] per shape]}"""
+        """{"shapes": [tag], "us": {cfg: [us per shape]}, "default_us": [...], "best": [[cfg, us] per shape]}:
+        the default plan ("default", no MI_GEMM_CFG) and every build, timed in two passes (forward, then
+        reverse order) and kept at the per-shape minimum, so no build gains from its place in the order."""
         cases = [GemmCase(t, M, N, K, rng, hip, ops) for t, M, N, K in GEMM_SHAPES + [CONFIG0]]
         res = {"shapes": [c.tag for c in cases], "us": {}}
         for c in cases:  # warm-up pass: the first timed build must not pay the clock ramp
             for _ in range(reps):
                 c.run(stream)
         stream.synchronize()
-        res["default_us"] = [time_case(c, stream, hip, reps)[1]["us"] for c in cases]
+
         def best():
-            timed = {k: v for k, v in res["us"].items() if isinstance(v, list)}
+            timed = {k: v for k, v in res["us"].items() if isinstance(v, list) and k != "default"}
             res["best"] = [min(([k, v[i]] for k, v in timed.items()), key=lambda kv: kv[1]) if timed else None
                            for i in range(len(cases))]
 
-        for cfg in GEMM_CANDIDATES:
-            os.environ["MI_GEMM_CFG"] = cfg
+        order = ["default"] + GEMM_CANDIDATES
+        for cfg in order + order[::-1]:
+            if cfg != "default":
+                os.environ["MI_GEMM_CFG"] = cfg
             try:
-                res["us"][cfg] = [time_case(c, stream, hip, reps)[1]["us"] for c in cases]
+                us = [time_case(c, stream, hip, reps)[1]["us"] for c in cases]
+                prev = res["us"].get(cfg)
+                res["us"][cfg] = [min(a, b) for a, b in zip(prev, us)] if isinstance(prev, list) else (
+                    prev if isinstance(prev, str) else us)
             except Exception as e:  # noqa: BLE001 -- one build's failure keeps the others
                 res["us"][cfg] = f"{type(e).__name__}: {e}"
             finally:
                 os.environ.pop("MI_GEMM_CFG", None)
             best()
+            if isinstance(res["us"].get("default"), list):
+                res["default_us"] = res["us"]["default"]
             if emit:
                 emit(dict(out, gemm_candidates=res))
         best()
         return res
 
     def attn_candidates():
-        """{"shapes": [tag], "us": {"default" | "nw2" | "nw4": [us per shape]}}: the fp16 attention
-        kernel's 2- and 4-wave workgroups (MI_ATTN_NW) on every attention shape of the step."""
+        """{"shapes": [tag], "us": {"default" | "nw2" | "nw4" | "nosplit": [us per shape]}}: the fp16
+        attention kernel's 2- and 4-wave workgroups (MI_ATTN_NW) and the default plan without its key
+        split (MI_ATTN_SPLIT=0) on every attention shape of the step, timed in two passes (forward, then
+        reverse order) and kept at the per-shape minimum."""
         cases = [AttnCase(t, B, H, Tq, Tk, m, rng, hip, ops) for t, B, H, Tq, Tk, m in ATTN_SHAPES]
         res = {"shapes": [c.tag for c in cases], "us": {}}
-        for key, nw in (("default", None), ("nw2", "2"), ("nw4", "4")):
-            if nw:
-                os.environ["MI_ATTN_NW"] = nw
+        variants = [("default", {}), ("nw2", {"MI_ATTN_NW": "2"}), ("nw4", {"MI_ATTN_NW": "4"}),
+                    ("nosplit", {"MI_ATTN_SPLIT": "0"})]
+        for key, env in variants + variants[::-1]:
+            os.environ.update(env)
             try:
-                res["us"][key] = [time_case(c, stream, hip, reps)[1]["us"] for c in cases]
+                us = [time_case(c, stream, hip, reps)[1]["us"] for c in cases]
             finally:
-                os.environ.pop("MI_ATTN_NW", None)
+                for k in env:
+                    os.environ.pop(k, None)
+            prev = res["us"].get(key)
+            res["us"][key] = [min(a, b) for a, b in zip(prev, us)] if prev else us
         return res
 
     def step_graph():
@@ -659,7 +685,7 @@ def main() -> int:
         if bad:
             raise SystemExit(f"graph replay differs from the eager launches: {bad}")
         launch_check = "graph replay outputs bitwise equal to an eager pass"
-        del graphs
+        del graphs, gr, replayed
 
     fam_time, fam_flops, fam_bytes, fam_launch = {}, {}, {}, {}
     for g, (fam, members) in enumerate(groups):
@@ -669,22 +695,21 @@ def main() -> int:
         fam_bytes[fam] = fam_bytes.get(fam, 0.0) + sum(c.bytes for c in members)
         fam_launch[fam] = fam_launch.get(fam, 0) + len(members)
 
-    # Per-shape breakdown (after the timed region): each shape launched `reps`
-    # times back to back between two events.
+    # Per-shape breakdown (after the timed region): each shape's `reps`
+    # back-to-back launches replayed from a graph between two events (time_case).
+    # The output check above leaves the GPU idle for a while (host copies), so
+    # ~50 ms of eager steps first bring its clocks back to where the timed
+    # steps ran.
+    t_end = time.perf_counter() + 0.05
+    while time.perf_counter() < t_end:
+        for c in cases:
+            c.run(stream)
+        stream.synchronize()
     breakdown = []
     for c in cases:
-        a, b = hip.Event(), hip.Event()
-        a.record(stream)
-        for _ in range(args.reps):
-            c.run(stream)
-        b.record(stream)
-        b.synchronize()
-        sec = a.elapsed_ms(b) / 1e3 / args.reps
+        sec, entry = time_case(c, stream, hip, args.reps)
         tf, roof, frac = roofline_pct(c, sec)
-        breakdown.append({"shape": c.tag, "kernel": c.kernel, "us": round(sec * 1e6, 2), "tflops": round(tf, 2),
-                          "pct_mfma_peak": round(100 * tf / PEAK_FP16_TFLOPS, 2),
-                          "roofline_tflops": round(roof, 1), "pct_of_roofline": round(100 * frac, 2),
-                          "gbs": round(c.bytes / sec / 1e9, 1)})
+        breakdown.append({k: v for k, v in entry.items() if k not in ("M_N_K", "B_H_Tq_Tk")})
         print(f"[bench] {c.tag:<28} {sec * 1e6:9.2f} us {tf:8.1f} TFLOP/s {100 * frac:6.1f}% of roofline",
               file=sys.stderr, flush=True)
 

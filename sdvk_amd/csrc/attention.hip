@@ -956,7 +956,7 @@ uint32_t cu_count() {
 // (256 rest blocks in 2 pieces) ran 141 us against 131 unsplit, while 2 x 10
 // heads (128 in 4) ran 120 against 126.
 // Only unmasked, non-causal fp16 launches split. MI_ATTN_SPLIT="<rest>:<pieces>"
-// forces a plan (tests).
+// forces a plan (tests; "0" turns the split off).
 struct SplitPlan {
     uint32_t nfull = 0, pieces = 1, rest = 0;
 };

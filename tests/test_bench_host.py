@@ -161,7 +161,9 @@ def test_bench_line_on_stand_in_device(fake_device, monkeypatch, capsys, launch)
                  "block_stack_fused_epilogues", "block_stack_joint_qkv", "gemm_candidates",
                  "attention_candidates", "step_graph"):
         assert part in ex and "error" not in ex[part], (part, ex.get(part))
-    assert set(ex["gemm_candidates"]["us"]) == set(bench.GEMM_CANDIDATES)
+    assert set(ex["gemm_candidates"]["us"]) == set(bench.GEMM_CANDIDATES) | {"default"}
+    assert len(ex["gemm_candidates"]["default_us"]) == len(bench.GEMM_SHAPES) + 1
+    assert set(ex["attention_candidates"]["us"]) == {"default", "nw2", "nw4", "nosplit"}
     assert len(ex["gemm_candidates"]["best"]) == len(bench.GEMM_SHAPES) + 1
     assert ex["block_stack_plain"]["variant"] == {"cached_kv": False, "fused_epilogues": False, "joint_qkv": False}
     for name in ("gemm_nt_q8_0", "fused_attention_ws", "gemm_nn_q8", "sdxl_block_forward", "block_ctx_kv",
