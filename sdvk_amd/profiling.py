@@ -40,7 +40,7 @@ from pathlib import Path
 FAMILIES = {
     "gemm_q8": (("gemm_q8_kernel", "gemm_q8_rows_kernel", "gemm_q8_any_kernel"),
                 ("gemm_fill_kernel", "splitk_reduce_kernel")),
-    "attention": (("attn_kernel", "attn_f16_kernel"), ()),
+    "attention": (("attn_kernel", "attn_f16_kernel"), ("attn_merge_kernel",)),
     "gemm_nn_q8": (("gemm_nn_q8_kernel", "gemm_nn_q8_tiled_kernel"), ()),
 }
 COPY_KERNEL = re.compile(r"copyBuffer", re.I)
@@ -102,7 +102,7 @@ def stats_report(csv_path: str, command: str, flops: dict | None = None) -> str:
                 fam[f][0] += calls
             fam[f][1] += tot
     lines += ["", "Family aggregates (total time of the family's kernels / calls of its main kernel, i.e. per API "
-                  "call; the GEMM family includes its K-split reduce passes):", "",
+                  "call; the GEMM family includes its K-split reduce passes, attention its key-split merge passes):", "",
               "| family | calls | avg us per call |", "|---|---:|---:|"]
     for f, (calls, tot) in fam.items():
         if calls:

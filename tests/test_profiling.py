@@ -16,11 +16,12 @@ INIT = "_ZN2mi12_GLOBAL__N_116gemm_fill_kernelEPfPKfjjjmj"
 REDUCE = "_ZN2mi12_GLOBAL__N_120splitk_reduce_kernelILi0ELb1EEEvPKfmjPfS3_jjjmj"
 ANY = "_ZN2mi12_GLOBAL__N_118gemm_q8_any_kernelENS0_8GemmArgsE"
 NN = "_ZN2mi12_GLOBAL__N_123gemm_nn_q8_tiled_kernelILb1EEEvNS0_6NnArgsE"
+MERGE = "_ZN2mi12_GLOBAL__N_117attn_merge_kernelIDF16_EEvNS0_8AttnArgsEj"
 COPY = "__amd_rocclr_copyBuffer"
 
 
 @pytest.mark.parametrize("name,family,main", [
-    (ATTN_F16, "attention", True), (GEMM, "gemm_q8", True), (ROWS, "gemm_q8", True), (INIT, "gemm_q8", False),
+    (ATTN_F16, "attention", True), (MERGE, "attention", False), (GEMM, "gemm_q8", True), (ROWS, "gemm_q8", True), (INIT, "gemm_q8", False),
     (REDUCE, "gemm_q8", False), (ANY, "gemm_q8", True), (NN, "gemm_nn_q8", True),
     (COPY, None, None),
     ("void mi::(anonymous namespace)::gemm_q8_kernel<64, 64, 2, 2, 2, 0, true, false, 2, 0>(mi::GemmArgs)",
