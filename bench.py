@@ -10,10 +10,10 @@ resident in HBM:
     d = 64, fp16 in/out, no mask) and cross-attention (config 3: 77 context
     tokens, key-padding lengths U{1..77}).
 value = algorithmic FLOP of one step x steps / elapsed (HIP events on the
-launch stream), in TFLOP/s. By default each timed step replays one HIP graph
-per kernel family, captured once after the warm-up (the same launches on the
-same buffers; the replayed outputs are checked bit for bit against an eager
-pass afterwards); --launch eager issues every launch from the host instead. The roofline of the dominant kernel family uses its
+launch stream), in TFLOP/s. The timed steps issue their launches from the
+host; --launch graph replays one HIP graph per kernel family instead, captured
+once after the warm-up (the same launches on the same buffers; the replayed
+outputs are checked bit for bit against an eager pass afterwards). The roofline of the dominant kernel family uses its
 launch durations inside the timed steps (events at the family boundaries). The
 JSON line also carries a per-shape breakdown (each shape launched back to back
 after the timed region) and a CPU baseline (the oracle's OpenMP fp32
@@ -37,6 +37,7 @@ sys.path.insert(0, str(ROOT))
 
 PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA (published)
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E (published)
+TIMING_EVENT = 0x40000000   # hipEventReleaseToDevice: no system-scope fence in the timed stream
 
 GEMM_SHAPES = [  # (tag, M, N, K)
     ("L1 q/k/v/out 640->640", 8192, 640, 640),
@@ -253,7 +254,7 @@ class BlockStack:
             run = self.run_cached
         run(stream)
         stream.synchronize()
-        a, b = self.hip.Event(), self.hip.Event()
+        a, b = self.hip.Event(TIMING_EVENT), self.hip.Event(TIMING_EVENT)
         a.record(stream)
         for _ in range(reps):
             run(stream)
@@ -285,7 +286,7 @@ def time_case(c, stream, hip, reps):
     finally:
         g.end()
     g.launch()
-    a, b = hip.Event(), hip.Event()
+    a, b = hip.Event(TIMING_EVENT), hip.Event(TIMING_EVENT)
     a.record(stream)
     g.launch()
     b.record(stream)
@@ -426,7 +427,7 @@ def extras(rng, hip, ops, stream, reps, emit=None):
         def timed(run):
             run()
             stream.synchronize()
-            a, b = hip.Event(), hip.Event()
+            a, b = hip.Event(TIMING_EVENT), hip.Event(TIMING_EVENT)
             a.record(stream)
             for _ in range(steps):
                 run()
@@ -571,14 +572,15 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=100,
+                    help="untimed steps first (~60 ms: the GPU's clocks settle over the first few dozen)")
     ap.add_argument("--reps", type=int, default=10, help="back-to-back launches per shape for the breakdown")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run one device-to-device copy of this many MiB first (profiler byte calibration)")
-    ap.add_argument("--launch", choices=["graph", "eager"], default="graph",
-                    help="timed steps replay one HIP graph per kernel family (captured once after the warm-up, "
-                         "checked bit for bit against an eager pass afterwards), or issue every launch from the "
-                         "host")
+    ap.add_argument("--launch", choices=["eager", "graph"], default="eager",
+                    help="timed steps issue every launch from the host, or replay one HIP graph per kernel "
+                         "family (captured once after the warm-up, checked bit for bit against an eager pass "
+                         "afterwards)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip the measurements outside the step metric")
     ap.add_argument("--extras-child", action="store_true", help=argparse.SUPPRESS)
@@ -656,7 +658,7 @@ def main() -> int:
                 c.run(stream)
             gr.end()
             graphs.append(gr)
-    marks = [[hip.Event() for _ in range(len(groups) + 1)] for _ in range(args.steps)]
+    marks = [[hip.Event(TIMING_EVENT) for _ in range(len(groups) + 1)] for _ in range(args.steps)]
     hip.synchronize()
     for st in range(args.steps):
         marks[st][0].record(stream)

@@ -40,6 +40,7 @@ def lib() -> ctypes.CDLL:
         h.hipStreamDestroy.argtypes = [vp]
         h.hipStreamSynchronize.argtypes = [vp]
         h.hipEventCreate.argtypes = [ctypes.POINTER(vp)]
+        h.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(vp), ctypes.c_uint]
         h.hipEventDestroy.argtypes = [vp]
         h.hipEventRecord.argtypes = [vp, vp]
         h.hipEventSynchronize.argtypes = [vp]
@@ -156,10 +157,19 @@ class Stream:
             pass
 
 
+# hipEventReleaseToDevice: the event's completion releases at device scope
+# only (no system-scope fence, which writes the L2 back to memory), the flag
+# HIP documents for timing the commands between events.
+EVENT_RELEASE_TO_DEVICE = 0x40000000
+
+
 class Event:
-    def __init__(self):
+    def __init__(self, flags: int = 0):
         self.handle = ctypes.c_void_p()
-        check(lib().hipEventCreate(ctypes.byref(self.handle)), "hipEventCreate")
+        if flags:
+            check(lib().hipEventCreateWithFlags(ctypes.byref(self.handle), flags), "hipEventCreateWithFlags")
+        else:
+            check(lib().hipEventCreate(ctypes.byref(self.handle)), "hipEventCreate")
 
     def record(self, stream: Stream | None = None) -> None:
         check(lib().hipEventRecord(self.handle, stream.handle if stream else None), "hipEventRecord")

@@ -55,7 +55,7 @@ class _Stream:
 class _Event:
     t = 0.0
 
-    def __init__(self):
+    def __init__(self, flags=0):
         self.at = None
 
     def record(self, stream=None):
@@ -125,7 +125,7 @@ def fake_device(monkeypatch):
     return calls
 
 
-@pytest.mark.parametrize("launch", [None, "eager"])
+@pytest.mark.parametrize("launch", [None, "graph"])
 def test_bench_line_on_stand_in_device(fake_device, monkeypatch, capsys, launch):
     import bench
 
@@ -145,10 +145,10 @@ def test_bench_line_on_stand_in_device(fake_device, monkeypatch, capsys, launch)
                 "scaling", "vs_baseline", "dtype", "data", "config", "roofline", "cpu_baseline"):
         assert key in out, key
     assert out["n_gpus"] == 1 and out["steps"] == 2 and out["value"] > 0
-    if launch is None:  # the default: graph replays, checked against an eager pass
+    if launch == "graph":  # graph replays, checked against an eager pass
         assert out["config"]["launch"].startswith("one HIP graph per kernel family")
         assert out["config"]["launch_check"] == "graph replay outputs bitwise equal to an eager pass"
-    else:
+    else:  # the default
         assert out["config"]["launch"].startswith("eager") and out["config"]["launch_check"] is None
     r = out["roofline"]
     assert r["bound"] == "mfma" and r["unit"] == "TFLOP/s" and 0 < r["frac"] == pytest.approx(r["achieved"] / r["peak"],
