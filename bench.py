@@ -361,20 +361,25 @@ def extras(rng, hip, ops, stream, reps, emit=None):
     def candidates():
         """{"shapes": [tag], "us": {cfg: [us per shape]}, "default_us": [...], "best": [[cfg, us] per shape]}:
         the default plan ("default", no MI_GEMM_CFG) and every build, timed in two passes (forward, then
-        reverse order) and kept at the per-shape minimum, so no build gains from its place in the order."""
+        reverse order) and kept at the per-shape minimum, so no build gains from its place in the order
+        (the default in the middle of both)."""
         cases = [GemmCase(t, M, N, K, rng, hip, ops) for t, M, N, K in GEMM_SHAPES + [CONFIG0]]
         res = {"shapes": [c.tag for c in cases], "us": {}}
-        for c in cases:  # warm-up pass: the first timed build must not pay the clock ramp
-            for _ in range(reps):
+        t_end = time.perf_counter() + 0.3  # warm-up: the first timed build must not pay the clock ramp
+        while time.perf_counter() < t_end:
+            for c in cases:
                 c.run(stream)
-        stream.synchronize()
+            stream.synchronize()
 
         def best():
             timed = {k: v for k, v in res["us"].items() if isinstance(v, list) and k != "default"}
             res["best"] = [min(([k, v[i]] for k, v in timed.items()), key=lambda kv: kv[1]) if timed else None
                            for i in range(len(cases))]
 
-        order = ["default"] + GEMM_CANDIDATES
+        # the default plan sits in the middle of both passes (the ends of a long
+        # sweep run at other clocks: ~8% apart for one build timed first and last)
+        half = len(GEMM_CANDIDATES) // 2
+        order = GEMM_CANDIDATES[:half] + ["default"] + GEMM_CANDIDATES[half:]
         for cfg in order + order[::-1]:
             if cfg != "default":
                 os.environ["MI_GEMM_CFG"] = cfg
