@@ -110,6 +110,41 @@ def test_errors_are_returned_not_raised_through_the_abi():
     assert lib.mi_q8_0_dequant(fake, fake * 2, 7, 32, None) == _lib.MI_ERR_INVALID_ARG
 
 
+def test_attention_workspace_entry_plans_and_errors():
+    """mi_fused_attention_ws_bytes / mi_fused_attention_ws on the host side: the
+    key-split plan's size for self-attention L1 (640 query blocks of 128 for
+    2 x 256 resident: the last 128 in 4 key ranges, 128 x 64 fp32 O rows plus
+    a max and a sum per query and piece), none for the shapes without a plan,
+    and the workspace's own argument errors, all before any device work."""
+    import ctypes
+    lib = _lib.load()
+    fake = 1 << 24
+
+    def args(B, H, Tq, Tk, causal=0, kv_len=None):
+        x = _lib.MiAttnArgs()
+        C = 64 * H
+        x.q, x.k, x.v, x.out = fake, fake * 4, fake * 8, fake * 12
+        x.batch, x.Tq, x.Tk, x.C, x.heads, x.causal = B, Tq, Tk, C, H, causal
+        x.in_dtype = x.out_dtype = _lib.MI_F16
+        x.ldq = x.ldk = x.ldv = x.ldo = C
+        x.sq, x.so, x.sk, x.sv = Tq * C, Tq * C, Tk * C, Tk * C
+        x.kv_len = kv_len
+        return x
+
+    assert lib.mi_fused_attention_ws_bytes(None) == 0
+    l1 = args(2, 10, 4096, 4096)
+    assert lib.mi_fused_attention_ws_bytes(ctypes.byref(l1)) == 128 * 4 * (128 * 64 + 2 * 128) * 4
+    for other in (args(2, 20, 1024, 1024), args(2, 10, 4096, 77), args(2, 10, 4096, 4096, causal=1),
+                  args(2, 10, 4096, 4096, kv_len=fake * 16)):
+        assert lib.mi_fused_attention_ws_bytes(ctypes.byref(other)) == 0
+    need = 128 * 4 * (128 * 64 + 2 * 128) * 4
+    # a workspace overlapping the output, or not 16-byte aligned
+    st = lib.mi_fused_attention_ws(ctypes.byref(l1), fake * 12 + 64, need, None)
+    assert st == _lib.MI_ERR_ALIASING
+    st = lib.mi_fused_attention_ws(ctypes.byref(l1), fake * 20 + 8, need, None)
+    assert st == _lib.MI_ERR_ALIGNMENT
+
+
 def test_python_mirror_raises_mi_error():
     with pytest.raises(ops.MiError) as e:
         ops.fused_attention(ops.FusedAttnArgs(1 << 20, 2 << 20, 3 << 20, 4 << 20, 8, 8, 130, 1))
