@@ -317,13 +317,25 @@ bool nn_tiled(const uint32_t* payload, uint32_t K, uint32_t lda, uint64_t sA) {
            !(env && std::strcmp(env, "general") == 0);
 }
 
-// K splits of the tiled kernel: one 8-wave workgroup per CU; split K until the
-// grid covers the CUs, keeping at least four 64-wide steps per split.
+// K splits of the tiled kernel: one 8-wave workgroup per CU; the most splits
+// whose workgroups all run at once (tiles x splits <= CUs), keeping at least
+// four 64-wide steps per split. Measured on MI355X against the doubling rule
+// (split until the grid covers the CUs): 320x4096x2880 48 tiles x 5 splits
+// 33.2 us against x 8 48.6 us; 640x4096x5760 80 x 3 73.9 against x 4 103.7;
+// 1280x1024x11520 40 x 6 73.8 against x 8 111.6 (a second partial round of
+// workgroups costs a whole round).
 uint32_t nn_splits(uint32_t M, uint32_t N, uint32_t K, uint32_t batch) {
     const uint64_t tiles = static_cast<uint64_t>(ceil_div(N, kBN2)) * ceil_div(M, kBM2) * batch;
     const uint32_t ksteps = K / kBK2;
     uint32_t splits = 1;
-    while (tiles * splits < kCUs && splits * 2 * 4 <= ksteps && batch * splits * 2 <= 65535) splits *= 2;
+    const char* env = std::getenv("MI_NN_SPLITS");  // a fixed split count (tuning sweeps)
+    if (env && *env) {
+        splits = static_cast<uint32_t>(std::max(1, std::atoi(env)));
+        splits = std::min<uint32_t>({splits, std::max(1u, ksteps), 65535u / std::max(1u, batch)});
+    } else if (tiles < kCUs) {
+        splits = static_cast<uint32_t>(std::min<uint64_t>({kCUs / tiles, ksteps / 4, 65535u / std::max(1u, batch)}));
+        splits = std::max(1u, splits);
+    }
     if (splits > 1) splits = ceil_div(ksteps, ceil_div(ksteps, splits));
     return splits;
 }

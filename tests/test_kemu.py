@@ -223,12 +223,13 @@ def test_kernels_on_emulator(emulator, family):
 # per workgroup). GEMM (choose in gemm_q8.hip): 192x256 (8 waves) when that gives
 # >= 120 tiles and K >= 1280; 128x128 (4 waves) when that gives >= 160 tiles;
 # else 64x64 (4 waves). Grid = (tiles, splits, batch). With a workspace
-# ("gemm_ws"): 128x128 grids under 256 tiles with K >= 4096 split K in two, 64x64
+# ("gemm_ws"): 128x128 grids under 256 tiles with K >= 4096 split K into the most
+# parts (2-4, >= 1024 k each) with tiles x parts <= 512, 64x64
 # grids under 512 tiles split K (powers of two) to about 256 workgroups with
 # >= 128 k per split. NN GEMM: 128x256 tiles (8 waves), grid (N tiles, M tiles,
-# splits); with a workspace ("nn_ws") K splits double while tiles x splits < 256
+# splits); with a workspace ("nn_ws") the most K splits with tiles x splits <= 256
 # and each split keeps >= 4 steps of 64. fp16 attention: 4-wave workgroups of
-# 128 queries when that gives >= 512 workgroups, else 2-wave ones of 64.
+# 128 queries, 2-wave ones of 64 when Tq <= 64.
 ROUTING = [
     ["gemm", [8192, 640, 640], [320, 1, 1], 256], ["gemm", [8192, 5120, 640], [2560, 1, 1], 256],
     ["gemm", [8192, 640, 2560], [320, 1, 1], 256], ["gemm", [2048, 1280, 1280], [160, 1, 1], 256],
@@ -237,8 +238,8 @@ ROUTING = [
     ["gemm", [154, 640, 2048], [30, 1, 1], 256], ["gemm_ws", [154, 640, 2048], [30, 8, 1], 256],
     ["gemm", [154, 1280, 2048], [60, 1, 1], 256], ["gemm_ws", [154, 1280, 2048], [60, 4, 1], 256],
     ["gemm", [9216, 1280, 1280], [240, 1, 1], 512], ["gemm_ws", [9216, 1280, 1280], [240, 1, 1], 512],
-    ["nn_ws", [320, 4096, 2880], [16, 3, 8], 512], ["nn_ws", [640, 4096, 5760], [16, 5, 4], 512],
-    ["nn_ws", [1280, 1024, 11520], [4, 10, 8], 512], ["nn_ws", [1280, 1024, 640], [4, 10, 2], 512],
+    ["nn_ws", [320, 4096, 2880], [16, 3, 5], 512], ["nn_ws", [640, 4096, 5760], [16, 5, 3], 512],
+    ["nn_ws", [1280, 1024, 11520], [4, 10, 6], 512], ["nn_ws", [1280, 1024, 640], [4, 10, 2], 512],
     ["nn", [1280, 1024, 11520], [4, 10, 1], 512],
     ["attn", [2, 10, 4096, 4096], [640, 1, 1], 256], ["attn", [2, 20, 1024, 1024], [320, 1, 1], 256],
     ["attn", [2, 10, 4096, 77], [640, 1, 1], 256], ["attn", [2, 20, 1024, 77], [320, 1, 1], 256],
