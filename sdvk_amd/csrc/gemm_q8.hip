@@ -1531,10 +1531,10 @@ struct Plan {
 // faster: 8192x640x2560 61.6 vs 66.0 us); 128x128 (4 waves, two workgroups per
 // CU) for mid-size grids; 64x64 for the rest.
 // With a workspace (allow_split), long-K 128x128 grids of fewer tiles than
-// CUs split K into the most parts (2 to 4, >= 1024 k each) whose workgroups
-// all fit two per CU (2048x1280x5120: 160 tiles x 3 = 480 workgroups,
-// 55.2 us against 67.7 us for 2 parts and 69.4 us for 4), and small 64x64
-// grids split K until ~256 workgroups run.
+// CUs split K into the most parts (>= 1024 k each; 2 or 3, as these grids
+// have >= 160 tiles) whose workgroups all fit two per CU (2048x1280x5120:
+// 160 tiles x 3 = 480 workgroups, 55.2 us against 67.7 us for 2 parts and
+// 69.4 us for 4), and small 64x64 grids split K until ~256 workgroups run.
 Plan choose(uint32_t M, uint32_t N, uint32_t K, uint32_t batch, bool allow_split) {
     Plan p{kC64x64, 1};
     const char* env = std::getenv("MI_GEMM_CFG");  // "<cfg>[:<splits>]" overrides (tuning sweeps)

@@ -224,7 +224,7 @@ def test_kernels_on_emulator(emulator, family):
 # >= 120 tiles and K >= 1280; 128x128 (4 waves) when that gives >= 160 tiles;
 # else 64x64 (4 waves). Grid = (tiles, splits, batch). With a workspace
 # ("gemm_ws"): 128x128 grids under 256 tiles with K >= 4096 split K into the most
-# parts (2-4, >= 1024 k each) with tiles x parts <= 512, 64x64
+# parts (2 or 3, >= 1024 k each) with tiles x parts <= 512, 64x64
 # grids under 512 tiles split K (powers of two) to about 256 workgroups with
 # >= 128 k per split. NN GEMM: 128x256 tiles (8 waves), grid (N tiles, M tiles,
 # splits); with a workspace ("nn_ws") the most K splits with tiles x splits <= 256
