@@ -653,13 +653,16 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
         // the two results for equal and keeps this half's max only.)
         return fmaxf(mx, __shfl_xor(mx, 32));
     };
+    // exp2 + fp16 pack of key block t (keys 32t .. 32t + 31 of the tile)
+    auto exp_half = [&](const floatx16 (&sc)[2], half8 (&pf)[2][2], int t) {
+#pragma unroll
+        for (int sp = 0; sp < 2; ++sp)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) pf[t][sp][i] = static_cast<_Float16>(__builtin_amdgcn_exp2f(sc[t][8 * sp + i]));
+    };
     auto exp_pack = [&](const floatx16 (&sc)[2], half8 (&pf)[2][2]) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int sp = 0; sp < 2; ++sp)
-#pragma unroll
-                for (int i = 0; i < 8; ++i) pf[t][sp][i] = static_cast<_Float16>(__builtin_amdgcn_exp2f(sc[t][8 * sp + i]));
+        exp_half(sc, pf, 0);
+        exp_half(sc, pf, 1);
     };
 
     floatx16 o[2];  // O^T for d in [0, 32), [32, 64)
@@ -752,6 +755,11 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int r = 0; r < 16; ++r) s0[t][r] = __builtin_fmaf(s0[t][r], a.c, -m);
+        // P of the tile's first 32 keys; each iteration computes the second
+        // half in phase A and the next tile's first half in phase B, which
+        // splits the exp2 work between the two MFMA phases
+        half8 pf[2][2];
+        exp_half(s0, pf, 0);
         __syncthreads();  // every wave has read K tile t0 before it is overwritten
 
         // One pipelined iteration; boundary tiles (key padding, Tk end, causal
@@ -769,35 +777,40 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
             dma_v(kv1, (j + 1) & 1);
             __builtin_amdgcn_sched_barrier(0);
 
-            // phase A: S of tile j+1 (8 MFMA) || exp2 + fp16 pack + row sum of tile j
+            // phase A: S of tile j+1 (8 MFMA) || exp2 + fp16 pack of tile j's
+            // second half, row sum of tile j
             floatx16 s1[2];
-            half8 pf[2][2];
             qk(s1);
-            exp_pack(s0, pf);
+            exp_half(s0, pf, 1);
             const float ts = tile_sum(pf);
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
             settle(s0, pf, ts);
 
-            // phase B: PV of tile j (8 MFMA) || mask + scale of tile j+1
+            // phase B: PV of tile j (8 MFMA) || mask + scale of tile j+1, exp2 +
+            // fp16 pack of its first half
             pv(pf);
             if constexpr (kMasked) mask(s1, kv1);
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) s1[t][r] = __builtin_fmaf(s1[t][r], a.c, -m);
+            half8 pn[2][2];
+            exp_half(s1, pn, 0);
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, kMasked ? 12 : 4, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, kMasked ? 15 : 7, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int t = 0; t < 2; ++t) s0[t] = s1[t];
+#pragma unroll
+            for (int sp = 0; sp < 2; ++sp) pf[0][sp] = pn[0][sp];
             dma_wait();
             __syncthreads();
         };
@@ -807,8 +820,7 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
         }
         // last tile
         read_v((ntiles - 1) & 1);
-        half8 pf[2][2];
-        exp_pack(s0, pf);
+        exp_half(s0, pf, 1);
         settle(s0, pf, tile_sum(pf));
         pv(pf);
     }
