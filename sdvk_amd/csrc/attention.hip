@@ -962,11 +962,13 @@ uint32_t cu_count() {
 // 4-wave query blocks and S = 2 per CU resident at once, W = r S + rest runs
 // r full rounds and then `rest` blocks alone on part of the GPU. Those rest
 // blocks instead run as `pieces` workgroups each over consecutive key-tile
-// ranges (pieces = S / rest, >= 8 tiles each, at most 8), so the last round
-// fills the GPU for a fraction of a round; attn_merge_kernel adds the pieces.
-// Plans of fewer than 4 pieces are not taken: measured, 2 x 12 heads x 4096
-// (256 rest blocks in 2 pieces) ran 141 us against 131 unsplit, while 2 x 10
-// heads (128 in 4) ran 120 against 126.
+// ranges, one piece per CU (pieces = CUs / rest, >= 8 tiles each, at most 8),
+// so the last round fills the GPU for a fraction of a round; attn_merge_kernel
+// adds the pieces. Measured on MI355X (graph-timed, interleaved): 2 x 10 heads
+// x 4096 (128 rest blocks) unsplit 119.4 us, 2 pieces 104.7, 4 pieces 106.6,
+// 8 pieces 110.3; 2 x 9 heads (64 rest) unsplit 116.4, 2 / 4 / 8 pieces 119.5 /
+// 110.0 / 113.4; 2 x 12 heads (256 rest: no plan, CUs / rest = 1) 131 unsplit
+// against 141 in 2 pieces.
 // Only unmasked, non-causal fp16 launches split. MI_ATTN_SPLIT="<rest>:<pieces>"
 // forces a plan (tests; "0" turns the split off).
 struct SplitPlan {
@@ -990,11 +992,11 @@ SplitPlan plan_split(const AttnArgs& a, uint32_t batch) {
         const uint64_t S = 2ull * cu_count();
         if (W <= S || W % S == 0) return p;
         rest = W % S;
-        pieces = S / rest;
+        pieces = cu_count() / rest;
         if (pieces > nt / 8) pieces = nt / 8;
         if (pieces > 8) pieces = 8;
     }
-    if (rest == 0 || pieces < 2 || (!(env && *env) && pieces < 4)) return p;
+    if (rest == 0 || pieces < 2) return p;
     p.rest = static_cast<uint32_t>(rest);
     p.pieces = static_cast<uint32_t>(pieces);
     p.nfull = static_cast<uint32_t>(W - rest);

@@ -113,7 +113,7 @@ def test_errors_are_returned_not_raised_through_the_abi():
 def test_attention_workspace_entry_plans_and_errors():
     """mi_fused_attention_ws_bytes / mi_fused_attention_ws on the host side: the
     key-split plan's size for self-attention L1 (640 query blocks of 128 for
-    2 x 256 resident: the last 128 in 4 key ranges, 128 x 64 fp32 O rows plus
+    2 x 256 resident: the last 128 in 2 key ranges, one per CU, 128 x 64 fp32 O rows plus
     a max and a sum per query and piece), none for the shapes without a plan,
     and the workspace's own argument errors, all before any device work."""
     import ctypes
@@ -133,11 +133,14 @@ def test_attention_workspace_entry_plans_and_errors():
 
     assert lib.mi_fused_attention_ws_bytes(None) == 0
     l1 = args(2, 10, 4096, 4096)
-    assert lib.mi_fused_attention_ws_bytes(ctypes.byref(l1)) == 128 * 4 * (128 * 64 + 2 * 128) * 4
-    for other in (args(2, 20, 1024, 1024), args(2, 10, 4096, 77), args(2, 10, 4096, 4096, causal=1),
+    assert lib.mi_fused_attention_ws_bytes(ctypes.byref(l1)) == 128 * 2 * (128 * 64 + 2 * 128) * 4
+    # 2 x 9 heads: 576 blocks, the last 64 in 4 ranges; 2 x 12 heads: 768, the last 256 (one per CU) unsplit
+    assert lib.mi_fused_attention_ws_bytes(ctypes.byref(args(2, 9, 4096, 4096))) == 64 * 4 * (128 * 64 + 2 * 128) * 4
+    for other in (args(2, 20, 1024, 1024), args(2, 12, 4096, 4096), args(2, 10, 4096, 77),
+                  args(2, 10, 4096, 4096, causal=1),
                   args(2, 10, 4096, 4096, kv_len=fake * 16)):
         assert lib.mi_fused_attention_ws_bytes(ctypes.byref(other)) == 0
-    need = 128 * 4 * (128 * 64 + 2 * 128) * 4
+    need = 128 * 2 * (128 * 64 + 2 * 128) * 4
     # a workspace overlapping the output, or not 16-byte aligned
     st = lib.mi_fused_attention_ws(ctypes.byref(l1), fake * 12 + 64, need, None)
     assert st == _lib.MI_ERR_ALIASING

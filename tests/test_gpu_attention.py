@@ -259,17 +259,17 @@ def test_staged_and_direct_output_stores_agree(gpu, oracle, monkeypatch, C, head
 
 
 def test_key_split_workspace_entry(gpu, oracle, monkeypatch):
-    """mi_fused_attention_ws: the key-split plan of the last partial round of query blocks (2 x 10 heads x 4096,
-    640 blocks against 512 resident: 128 blocks in 4 key ranges) against the oracle on sampled rows, its repeat
-    bit for bit, and agreement with mi_fused_attention_ex; a workspace below the plan's size (and none) runs
-    mi_fused_attention_ex's plan exactly; forced plans on small shapes (uneven pieces, partial query block,
-    hd = 40) against the oracle."""
+    """mi_fused_attention_ws: the key-split plan of the last partial round of query blocks (2 x 10 heads x
+    4096, 640 blocks against 512 resident: 128 blocks in 2 key ranges, one per CU) against the oracle on
+    sampled rows, its repeat bit for bit, and agreement with mi_fused_attention_ex; a workspace below the
+    plan's size (and none) runs mi_fused_attention_ex's plan exactly; the 4-range plan of 2 x 9 heads;
+    forced plans on small shapes (uneven pieces, partial query block, hd = 40) against the oracle."""
     monkeypatch.delenv("MI_ATTN_SPLIT", raising=False)
     B, H, T = 2, 10, 4096
     C = H * 64
     kw = dict(batch=B, Tq=T, Tk=T, C=C, heads=H, in_dtype=MI_F16, out_dtype=MI_F16)
     nws = ops.fused_attention_ws_bytes(**kw)
-    assert nws == 128 * 4 * (128 * 64 + 2 * 128) * 4, nws
+    assert nws == 128 * 2 * (128 * 64 + 2 * 128) * 4, nws
     q, k, v = (oracle.normal(31 + i, B * T * C).astype(np.float16) for i in range(3))
     dq, dk, dv = (DeviceBuffer.from_array(x) for x in (q, k, v))
     ws = DeviceBuffer(nws)
@@ -294,6 +294,21 @@ def test_key_split_workspace_entry(gpu, oracle, monkeypatch):
     d = np.abs(a0 - a2)
     print(f"  split vs unsplit max |diff| / RMS = {d.max() / rms(want):.2e}", flush=True)
     assert np.all(d <= 2 * REL_RMS_TOL * rms(want) + 2 * fp16_half_ulp(np.maximum(np.abs(a0), np.abs(a2))))
+    # 2 x 9 heads: 576 blocks, the last 64 in 4 key ranges
+    H9 = 9
+    kw9 = dict(batch=B, Tq=T, Tk=T, C=H9 * 64, heads=H9, in_dtype=MI_F16, out_dtype=MI_F32)
+    n9 = ops.fused_attention_ws_bytes(**kw9)
+    assert n9 == 64 * 4 * (128 * 64 + 2 * 128) * 4, n9
+    print("[case] key split 2 x 9 heads, 4 ranges", flush=True)
+    q9, k9, v9 = (oracle.normal(41 + i, B * T * H9 * 64).astype(np.float16) for i in range(3))
+    d9 = [DeviceBuffer.from_array(x) for x in (q9, k9, v9)]
+    o9 = DeviceBuffer(B * T * H9 * 64 * 4)
+    ops.fused_attention_ws(*d9, o9, DeviceBuffer(n9), **kw9)
+    synchronize()
+    got9 = o9.download(np.float32, B * T * H9 * 64).reshape(B, T, H9 * 64)[:, rows].astype(np.float64)
+    want9 = oracle.fused_attention_ex(q9, k9, v9, batch=B, Tq=T, Tk=T, C=H9 * 64, heads=H9, in_dtype=oracle.OR_F16,
+                                      rows=rows, threads=oracle.max_threads()).astype(np.float64)
+    assert_parity(got9, want9, what="2 x 9 heads key split")
     for (B, Tq, Tk, C, heads, split, odt) in [(2, 300, 1000, 128, 2, "3:3", MI_F32), (1, 200, 130, 80, 2, "1:2", MI_F32),
                                              (1, 256, 512, 128, 2, "2:4", MI_F16)]:
         print(f"[case] forced split {split} B={B} Tq={Tq} Tk={Tk} C={C} heads={heads}", flush=True)
