@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import inspect
 import json
+import os
 import sys
 import types
 from pathlib import Path
@@ -247,3 +248,14 @@ def test_gpus_above_one_exits_with_a_message(monkeypatch, capsys):
     monkeypatch.setattr(sys, "argv", ["bench.py", "--gpus", "2"])
     assert bench.main() == 2
     assert "one GPU" in capsys.readouterr().out
+
+
+def test_cpu_baseline_one_pass():
+    """The CPU baseline leg (the oracle's OpenMP restatement over one full step
+    of the same shapes) reports a positive rate with its sample description."""
+    import bench
+
+    r = bench.cpu_baseline(threads=max(1, (os.cpu_count() or 1)), min_seconds=0.0, max_passes=1)
+    assert r["kind"] == "port" and r["unit"] == "TFLOP/s" and r["passes"] == 1
+    assert r["value"] > 0 and r["seconds"] > 0 and r["cores"] >= 1
+    assert "8 config-1 GEMM shapes" in r["sample"]
