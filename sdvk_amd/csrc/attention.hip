@@ -440,6 +440,33 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
                 }
             }
         }
+        if (a.causal && kv0 >= kfull) {
+            // causal diagonal tile: P's fp16 residual as a second product (the
+            // first queries average a handful of keys; see attn_f16_kernel)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+#pragma unroll
+                for (int sp = 0; sp < 2; ++sp) {
+                    half8 plo;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[t][8 * sp + i], a.c, -m_use));
+                        plo[i] = static_cast<_Float16>(e - static_cast<float>(static_cast<_Float16>(e)));
+                    }
+                    o[2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones, plo, o[2], 0, 0, 0);
+                    const int G = t * 4 + sp * 2 + g;
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const int d = 32 * u + l32;
+#pragma unroll
+                        for (int pl = 0; pl < NP; ++pl) {
+                            const half8 vf = *reinterpret_cast<const half8*>(&Vs[st][pl][(G * kVG + d) * 8]);
+                            o[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, plo, o[u], 0, 0, 0);
+                        }
+                    }
+                }
+            }
+        }
 
         store_tile(st ^ 1);
         __syncthreads();
@@ -719,6 +746,25 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
 #pragma unroll
                 for (int u = 0; u < 2; ++u) o[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[t][sp][u], pf[t][sp], o[u], 0, 0, 0);
     };
+    // Causal diagonal tiles: the rows of the first queries average a handful
+    // of keys, so their |O| is several times the output's RMS and P's fp16
+    // rounding (2^-11 of each weight) would reach the 2e-3 x RMS bar. On those
+    // tiles P also enters as the fp16 residual exp2(s) - fp16(exp2(s)): O gets
+    // V P_lo as a second product and l the residuals' sum, which leaves P's
+    // error at ~2^-22. Other tiles (and non-causal launches) keep one product.
+    auto pv_residual = [&](const floatx16 (&sc)[2], const half8 (&pf)[2][2]) {
+        half8 plo[2][2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int sp = 0; sp < 2; ++sp)
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    plo[t][sp][i] = static_cast<_Float16>(__builtin_amdgcn_exp2f(sc[t][8 * sp + i]) -
+                                                          static_cast<float>(pf[t][sp][i]));
+        lsum += tile_sum(plo);
+        pv(plo);
+    };
 
     if (t0 < ntiles) {
         // prologue: K tiles t0, t0+1 and V tile t0 in LDS; S of tile t0; the
@@ -790,6 +836,7 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
             }
             __builtin_amdgcn_sched_barrier(0);
             settle(s0, pf, ts);
+            if (a.causal && j * kBKV >= kfull) pv_residual(s0, pf);
 
             // phase B: PV of tile j (8 MFMA) || mask + scale of tile j+1, exp2 +
             // fp16 pack of its first half
@@ -822,6 +869,7 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
         read_v((ntiles - 1) & 1);
         exp_half(s0, pf, 1);
         settle(s0, pf, tile_sum(pf));
+        if (a.causal && (ntiles - 1) * kBKV >= kfull) pv_residual(s0, pf);
         pv(pf);
     }
 
