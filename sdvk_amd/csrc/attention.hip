@@ -532,7 +532,10 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
 // j+1), so one barrier per tile keeps both double buffers race-free. The
 // workgroup has NW waves of 32 queries; blocks are mapped so that the
 // workgroups of one (batch, head) share an XCD (and its L2).
-template <typename TO, int NW>
+// CAUSAL: the launch's causal flag at compile time, so that only causal
+// launches carry the diagonal tiles' residual product (a runtime test of the
+// flag in the loop cost non-causal launches 2.4%).
+template <typename TO, int NW, bool CAUSAL>
 __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t qtiles) {
     constexpr int BQ = 32 * NW;
     constexpr int DMA_IT = 8 / NW;  // 1 KB (8-row) DMA pieces per wave per tile, for K and for V
@@ -836,7 +839,9 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
             }
             __builtin_amdgcn_sched_barrier(0);
             settle(s0, pf, ts);
-            if (a.causal && j * kBKV >= kfull) pv_residual(s0, pf);
+            if constexpr (CAUSAL) {
+                if (j * kBKV >= kfull) pv_residual(s0, pf);
+            }
 
             // phase B: PV of tile j (8 MFMA) || mask + scale of tile j+1, exp2 +
             // fp16 pack of its first half
@@ -869,7 +874,9 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
         read_v((ntiles - 1) & 1);
         exp_half(s0, pf, 1);
         settle(s0, pf, tile_sum(pf));
-        if (a.causal && (ntiles - 1) * kBKV >= kfull) pv_residual(s0, pf);
+        if constexpr (CAUSAL) {
+            if ((ntiles - 1) * kBKV >= kfull) pv_residual(s0, pf);
+        }
         pv(pf);
     }
 
@@ -1059,12 +1066,19 @@ void launch_f16(const AttnArgs& a, uint32_t batch, hipStream_t s) {
     const uint64_t groups = static_cast<uint64_t>(a.heads) * batch;
     if (a.pieces > 1) {  // a key-split plan (4-wave workgroups)
         const uint32_t rest = static_cast<uint32_t>(q4 * groups - a.nfull);
-        attn_f16_kernel<TO, 4><<<a.nfull + rest * a.pieces, 256, 0, s>>>(a, q4);
+        attn_f16_kernel<TO, 4, false><<<a.nfull + rest * a.pieces, 256, 0, s>>>(a, q4);
         attn_merge_kernel<TO><<<rest * 4, 256, 0, s>>>(a, q4);
         return;
     }
-    if (f16_waves(a, batch) == 4) attn_f16_kernel<TO, 4><<<static_cast<unsigned>(q4 * groups), 256, 0, s>>>(a, q4);
-    else attn_f16_kernel<TO, 2><<<static_cast<unsigned>(q2 * groups), 128, 0, s>>>(a, q2);
+    const bool nw4 = f16_waves(a, batch) == 4;
+    const unsigned g4 = static_cast<unsigned>(q4 * groups), g2 = static_cast<unsigned>(q2 * groups);
+    if (a.causal) {
+        if (nw4) attn_f16_kernel<TO, 4, true><<<g4, 256, 0, s>>>(a, q4);
+        else attn_f16_kernel<TO, 2, true><<<g2, 128, 0, s>>>(a, q2);
+    } else {
+        if (nw4) attn_f16_kernel<TO, 4, false><<<g4, 256, 0, s>>>(a, q4);
+        else attn_f16_kernel<TO, 2, false><<<g2, 128, 0, s>>>(a, q2);
+    }
 }
 
 template <typename TI, typename TO>
