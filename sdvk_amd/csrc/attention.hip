@@ -61,6 +61,7 @@ struct AttnArgs {
     const int32_t* kv_len;
     float c;  // scale * log2(e)
     int ostage;  // output rows and head columns 16-byte aligned: store O through LDS (store_o_rows)
+    int precise;  // MI_ATTN_PRECISE: P's fp16 residual as a second PV product on every tile
     // Key-split plan of the fp16 kernel (mi_fused_attention_ws): the first nfull query blocks run
     // whole; each later one runs as `pieces` workgroups over consecutive key-tile ranges that write
     // unnormalised partials to `part` (kPartFloats floats per piece), merged by attn_merge_kernel.
@@ -440,9 +441,10 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
                 }
             }
         }
-        if (a.causal && kv0 >= kfull) {
-            // causal diagonal tile: P's fp16 residual as a second product (the
-            // first queries average a handful of keys; see attn_f16_kernel)
+        if (a.precise || (a.causal && kv0 >= kfull)) {
+            // causal diagonal tile (or every tile under MI_ATTN_PRECISE): P's
+            // fp16 residual as a second product (the first queries of a causal
+            // launch average a handful of keys; see attn_f16_kernel)
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
 #pragma unroll
@@ -532,10 +534,12 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
 // j+1), so one barrier per tile keeps both double buffers race-free. The
 // workgroup has NW waves of 32 queries; blocks are mapped so that the
 // workgroups of one (batch, head) share an XCD (and its L2).
-// CAUSAL: the launch's causal flag at compile time, so that only causal
-// launches carry the diagonal tiles' residual product (a runtime test of the
-// flag in the loop cost non-causal launches 2.4%).
-template <typename TO, int NW, bool CAUSAL>
+// RESID: which tiles add P's fp16 residual as a second PV product, at compile
+// time (a runtime test of the flag inside the loop cost non-causal launches
+// 2.4%): kResidNone; kResidDiagonal, a causal launch's diagonal tiles;
+// kResidAll, every tile (MI_ATTN_PRECISE).
+constexpr int kResidNone = 0, kResidDiagonal = 1, kResidAll = 2;
+template <typename TO, int NW, int RESID>
 __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t qtiles) {
     constexpr int BQ = 32 * NW;
     constexpr int DMA_IT = 8 / NW;  // 1 KB (8-row) DMA pieces per wave per tile, for K and for V
@@ -839,7 +843,9 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
             }
             __builtin_amdgcn_sched_barrier(0);
             settle(s0, pf, ts);
-            if constexpr (CAUSAL) {
+            if constexpr (RESID == kResidAll) {
+                pv_residual(s0, pf);
+            } else if constexpr (RESID == kResidDiagonal) {
                 if (j * kBKV >= kfull) pv_residual(s0, pf);
             }
 
@@ -874,7 +880,9 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
         read_v((ntiles - 1) & 1);
         exp_half(s0, pf, 1);
         settle(s0, pf, tile_sum(pf));
-        if constexpr (CAUSAL) {
+        if constexpr (RESID == kResidAll) {
+            pv_residual(s0, pf);
+        } else if constexpr (RESID == kResidDiagonal) {
             if ((ntiles - 1) * kBKV >= kfull) pv_residual(s0, pf);
         }
         pv(pf);
@@ -1066,18 +1074,22 @@ void launch_f16(const AttnArgs& a, uint32_t batch, hipStream_t s) {
     const uint64_t groups = static_cast<uint64_t>(a.heads) * batch;
     if (a.pieces > 1) {  // a key-split plan (4-wave workgroups)
         const uint32_t rest = static_cast<uint32_t>(q4 * groups - a.nfull);
-        attn_f16_kernel<TO, 4, false><<<a.nfull + rest * a.pieces, 256, 0, s>>>(a, q4);
+        if (a.precise) attn_f16_kernel<TO, 4, kResidAll><<<a.nfull + rest * a.pieces, 256, 0, s>>>(a, q4);
+        else attn_f16_kernel<TO, 4, kResidNone><<<a.nfull + rest * a.pieces, 256, 0, s>>>(a, q4);
         attn_merge_kernel<TO><<<rest * 4, 256, 0, s>>>(a, q4);
         return;
     }
     const bool nw4 = f16_waves(a, batch) == 4;
     const unsigned g4 = static_cast<unsigned>(q4 * groups), g2 = static_cast<unsigned>(q2 * groups);
-    if (a.causal) {
-        if (nw4) attn_f16_kernel<TO, 4, true><<<g4, 256, 0, s>>>(a, q4);
-        else attn_f16_kernel<TO, 2, true><<<g2, 128, 0, s>>>(a, q2);
+    if (a.precise) {
+        if (nw4) attn_f16_kernel<TO, 4, kResidAll><<<g4, 256, 0, s>>>(a, q4);
+        else attn_f16_kernel<TO, 2, kResidAll><<<g2, 128, 0, s>>>(a, q2);
+    } else if (a.causal) {
+        if (nw4) attn_f16_kernel<TO, 4, kResidDiagonal><<<g4, 256, 0, s>>>(a, q4);
+        else attn_f16_kernel<TO, 2, kResidDiagonal><<<g2, 128, 0, s>>>(a, q2);
     } else {
-        if (nw4) attn_f16_kernel<TO, 4, false><<<g4, 256, 0, s>>>(a, q4);
-        else attn_f16_kernel<TO, 2, false><<<g2, 128, 0, s>>>(a, q2);
+        if (nw4) attn_f16_kernel<TO, 4, kResidNone><<<g4, 256, 0, s>>>(a, q4);
+        else attn_f16_kernel<TO, 2, kResidNone><<<g2, 128, 0, s>>>(a, q2);
     }
 }
 
@@ -1130,6 +1142,10 @@ int run(const mi_attn_args& x, hipStream_t s, const char* fn, void* ws = nullptr
     a.c = scale * 1.4426950408889634f;
     a.ostage = aligned(x.out, 16) && (ldo * eo) % 16 == 0 && (so * eo) % 16 == 0 && (a.hd * eo) % 16 == 0 &&
                !std::getenv("MI_ATTN_DIRECT_STORE");
+    {
+        const char* p = std::getenv("MI_ATTN_PRECISE");
+        a.precise = p && *p && std::strcmp(p, "0") != 0 ? 1 : 0;
+    }
 
     // 16-byte vector path: every 8-element chunk of every row is 16-byte aligned.
     const uintptr_t vin = 8 * ei, vout = 4 * eo;

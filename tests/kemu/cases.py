@@ -200,7 +200,8 @@ def gemm_nn(E, *, M, N, K, mode=0, batch=1, lda=0, ldb=0, ldc=0, sA=0, sB=0, sC=
 
 
 def attention(E, *, batch=1, Tq, Tk, C, heads, causal=False, f16_in=False, f16_out=False, kv_len=None, seed=1,
-              front=False, order=0, tol=2e-3, nw=None, outliers=None, direct_store=False, split=None):
+              front=False, order=0, tol=2e-3, nw=None, outliers=None, direct_store=False, split=None,
+              precise=False):
     """mi_fused_attention_ex (contiguous [batch, T, C]) against the oracle;
     split "<rest>:<pieces>": through mi_fused_attention_ws with that key-split
     plan forced (MI_ATTN_SPLIT) and the workspace the library asks for;
@@ -208,7 +209,8 @@ def attention(E, *, batch=1, Tq, Tk, C, heads, causal=False, f16_in=False, f16_o
     indices whose scores stand far above the rest (q ~ 1, k ~ 0.1 N(0, 1),
     those keys 3.0), so that a running max that misses them overflows;
     direct_store: output stores straight from the MFMA layout
-    (MI_ATTN_DIRECT_STORE) instead of whole rows through LDS."""
+    (MI_ATTN_DIRECT_STORE) instead of whole rows through LDS; precise: P's
+    fp16 residual as a second PV product on every tile (MI_ATTN_PRECISE)."""
     E.order(order)
     if nw:
         os.environ["MI_ATTN_NW"] = str(nw)
@@ -222,6 +224,10 @@ def attention(E, *, batch=1, Tq, Tk, C, heads, causal=False, f16_in=False, f16_o
         os.environ["MI_ATTN_SPLIT"] = split
     else:
         os.environ.pop("MI_ATTN_SPLIT", None)
+    if precise:
+        os.environ["MI_ATTN_PRECISE"] = "1"
+    else:
+        os.environ.pop("MI_ATTN_PRECISE", None)
     idt = np.float16 if f16_in else np.float32
     q = ob.normal(seed, batch * Tq * C).astype(idt)
     k = ob.normal(seed + 1, batch * Tk * C).astype(idt)

@@ -186,6 +186,41 @@ def test_two_and_four_wave_workgroups(gpu, oracle, monkeypatch, nw, B, Tq, Tk, C
             assert np.all(np.abs(g - w) <= bound), f"nw={nw}: fp16 output beyond parity + storage rounding"
 
 
+@pytest.mark.parametrize("B,H,T,Tk,causal,ws", [(1, 20, 1024, 1024, False, False), (2, 10, 4096, 4096, False, True),
+                                                 (1, 8, 1024, 1024, True, False), (2, 4, 300, 77, False, False)])
+def test_precise_mode(gpu, oracle, monkeypatch, B, H, T, Tk, causal, ws):
+    """MI_ATTN_PRECISE: P's fp16 residual as a second PV product on every tile,
+    held to a tenth of the bar (sampled rows against the oracle), through the
+    plain entry, the key-split workspace entry and the fp32 reference-layout
+    entry (batch 1)."""
+    print(f"[case] precise B={B} H={H} T={T} Tk={Tk} causal={causal} ws={ws}", flush=True)
+    monkeypatch.setenv("MI_ATTN_PRECISE", "1")
+    C = H * 64
+    q = oracle.normal(21, B * T * C).astype(np.float16)
+    k = oracle.normal(22, B * Tk * C).astype(np.float16)
+    v = oracle.normal(23, B * Tk * C).astype(np.float16)
+    rows = _sample_rows(T, 40, 7) if T > 512 else np.arange(T, dtype=np.uint32)
+    want = oracle.fused_attention_ex(q, k, v, batch=B, Tq=T, Tk=Tk, C=C, heads=H, causal=causal, in_dtype=1,
+                                     rows=rows, threads=oracle.max_threads()).astype(np.float64)
+    kw = dict(batch=B, Tq=T, Tk=Tk, C=C, heads=H, causal=causal, in_dtype=MI_F16, out_dtype=MI_F32)
+    dq, dk, dv = (DeviceBuffer.from_array(x) for x in (q, k, v))
+    do = DeviceBuffer(B * T * C * 4)
+    if ws:
+        n = ops.fused_attention_ws_bytes(**kw)
+        assert n > 0, "the shape has no key-split plan"
+        ops.fused_attention_ws(dq, dk, dv, do, DeviceBuffer(n), **kw)
+    else:
+        ops.fused_attention_ex(dq, dk, dv, do, **kw)
+    synchronize()
+    got = do.download(np.float32, B * T * C).reshape(B, T, C)[:, rows].astype(np.float64)
+    e = assert_parity(got, want, tol=REL_RMS_TOL / 10, what="precise")
+    print(f"  err/rms = {e:.3e}", flush=True)
+    if B == 1:
+        got32 = run_ref_api(q, k, v, T, Tk, C, H, causal)[rows].astype(np.float64)
+        e32 = assert_parity(got32, want.reshape(got32.shape), tol=REL_RMS_TOL / 10, what="precise, reference layout")
+        print(f"  reference layout err/rms = {e32:.3e}", flush=True)
+
+
 def test_strided_layouts_and_scale(gpu, oracle):
     """Token strides > C (e.g. fused QKV buffers), batch strides with gaps, custom scale."""
     B, Tq, Tk, C, heads = 2, 150, 200, 128, 2

@@ -133,6 +133,12 @@ FAMILIES = {
         dict(batch=2, Tq=300, Tk=1000, C=128, heads=2, f16_in=True, f16_out=False, split="3:3", nw=4),
         dict(Tq=200, Tk=130, C=80, heads=2, f16_in=True, f16_out=False, split="1:2", nw=4),
         dict(Tq=128, Tk=256, C=64, heads=1, f16_in=True, split="1:4", nw=4, outliers=[5, 70, 200]),
+        # MI_ATTN_PRECISE (P's fp16 residual on every tile), held to a tenth of the bar: both kernels,
+        # key padding, causal, a forced key split
+        dict(batch=2, Tq=130, Tk=150, C=128, heads=2, f16_in=True, kv_len=[150, 37], nw=4, precise=True, tol=2e-4),
+        dict(Tq=100, Tk=300, C=128, heads=2, f16_in=True, causal=True, nw=2, precise=True, tol=2e-4),
+        dict(Tq=70, Tk=130, C=128, heads=2, causal=True, precise=True, tol=2e-4),
+        dict(Tq=200, Tk=130, C=80, heads=2, f16_in=True, split="1:2", nw=4, precise=True, tol=2e-4),
     ],
     "block": [
         dict(B=1, T=33, C=64, H=1, Tc=5, Cc=96, F=160),
