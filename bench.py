@@ -307,7 +307,7 @@ def time_case(c, stream, hip, reps):
                  "gbs": round(c.bytes / sec / 1e9, 1)}
 
 
-# Every tile build (MI_GEMM_CFG "<cfg>[:<K splits>]"), timed on every GEMM shape
+# Every tile build (mi_tuning_set("gemm_cfg", "<cfg>[:<K splits>]")), timed on every GEMM shape
 # of the step and on config 0, so the tile rules can be re-derived from one run:
 # the LDS kernel's 256x128 / 128x128 / 128x64 / 64x64 / 256x256 tiles (0-4) with
 # and without K splits, the row-stationary builds (5, 6; row-coalesced A 7-10)
@@ -366,7 +366,7 @@ def extras(rng, hip, ops, stream, reps, emit=None):
 
     def candidates():
         """{"shapes": [tag], "us": {cfg: [us per shape]}, "default_us": [...], "best": [[cfg, us] per shape]}:
-        the default plan ("default", no MI_GEMM_CFG) and every build, timed in two passes (forward, then
+        the default plan ("default", no gemm_cfg override) and every build, timed in two passes (forward, then
         reverse order) and kept at the per-shape minimum, so no build gains from its place in the order
         (the default next to build 1 in both)."""
         cases = [GemmCase(t, M, N, K, rng, hip, ops) for t, M, N, K in GEMM_SHAPES + [CONFIG0]]
@@ -390,7 +390,7 @@ def extras(rng, hip, ops, stream, reps, emit=None):
         order = GEMM_CANDIDATES[:i1] + ["default"] + GEMM_CANDIDATES[i1:]
         for cfg in order + order[::-1]:
             if cfg != "default":
-                os.environ["MI_GEMM_CFG"] = cfg
+                ops.tuning_set("gemm_cfg", cfg)
             try:
                 us = [time_case(c, stream, hip, reps)[1]["us"] for c in cases]
                 prev = res["us"].get(cfg)
@@ -399,7 +399,7 @@ def extras(rng, hip, ops, stream, reps, emit=None):
             except Exception as e:  # noqa: BLE001 -- one build's failure keeps the others
                 res["us"][cfg] = f"{type(e).__name__}: {e}"
             finally:
-                os.environ.pop("MI_GEMM_CFG", None)
+                ops.tuning_set("gemm_cfg", None)
             best()
             if isinstance(res["us"].get("default"), list):
                 res["default_us"] = res["us"]["default"]
@@ -410,20 +410,16 @@ def extras(rng, hip, ops, stream, reps, emit=None):
 
     def attn_candidates():
         """{"shapes": [tag], "us": {"default" | "nw2" | "nw4" | "nosplit": [us per shape]}}: the fp16
-        attention kernel's 2- and 4-wave workgroups (MI_ATTN_NW) and the default plan without its key
-        split (MI_ATTN_SPLIT=0) on every attention shape of the step, timed in two passes (forward, then
+        attention kernel's 2- and 4-wave workgroups (attn_nw override) and the default plan without its key
+        split (attn_split "0") on every attention shape of the step, timed in two passes (forward, then
         reverse order) and kept at the per-shape minimum."""
         cases = [AttnCase(t, B, H, Tq, Tk, m, rng, hip, ops) for t, B, H, Tq, Tk, m in ATTN_SHAPES]
         res = {"shapes": [c.tag for c in cases], "us": {}}
-        variants = [("default", {}), ("nw2", {"MI_ATTN_NW": "2"}), ("nw4", {"MI_ATTN_NW": "4"}),
-                    ("nosplit", {"MI_ATTN_SPLIT": "0"})]
-        for key, env in variants + variants[::-1]:
-            os.environ.update(env)
-            try:
+        variants = [("default", {}), ("nw2", {"attn_nw": "2"}), ("nw4", {"attn_nw": "4"}),
+                    ("nosplit", {"attn_split": "0"})]
+        for key, over in variants + variants[::-1]:
+            with ops.tuning(**over):
                 us = [time_case(c, stream, hip, reps)[1]["us"] for c in cases]
-            finally:
-                for k in env:
-                    os.environ.pop(k, None)
             prev = res["us"].get(key)
             res["us"][key] = [min(a, b) for a, b in zip(prev, us)] if prev else us
         return res
@@ -597,6 +593,11 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip the measurements outside the step metric")
     ap.add_argument("--extras-child", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--gemm-cfg", default=None,
+                    help='pin the NT GEMM tile build, "<cfg>[:<K splits>]" (mi_tuning_set("gemm_cfg"); profiling)')
+    ap.add_argument("--preroll-s", type=float, default=0.3,
+                    help="seconds of untimed steps before the --warmup steps, whatever --warmup is: the GPU's "
+                         "clocks ramp over the first tens of milliseconds of load")
     ap.add_argument("--only", choices=["step", "gemm", "attention", "block", "cfg0"], default=None,
                     help="run one part only (profiling): the step's kernels (GEMM and attention shapes, no block "
                          "stack, CPU baseline or extras), a kernel family, the config-4 block stack, or the "
@@ -614,6 +615,8 @@ def main() -> int:
     _lib.load()
     if hip.device_count() < 1:
         raise SystemExit("no HIP device")
+    if args.gemm_cfg:
+        ops.tuning_set("gemm_cfg", args.gemm_cfg)
     rng = np.random.default_rng(1)
     stream = hip.Stream()
     if args.only == "block":
@@ -632,6 +635,13 @@ def main() -> int:
     hip.synchronize()
     print(f"[bench] {hip.device_name(0)}: {len(cases)} shapes resident", file=sys.stderr, flush=True)
 
+    # clock pre-roll (time-based, so a short --warmup does not leave the timed
+    # steps on ramping clocks), then the --warmup steps
+    t_end = time.perf_counter() + max(args.preroll_s, 0.0)
+    while time.perf_counter() < t_end:
+        for c in cases:
+            c.run(stream)
+        stream.synchronize()
     for _ in range(args.warmup):
         for c in cases:
             c.run(stream)

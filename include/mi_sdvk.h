@@ -64,6 +64,26 @@ const char* mi_last_error(void);
 /* Library version: major * 10000 + minor * 100 + patch. */
 int mi_version(void);
 
+/* Plan overrides (extension, no reference counterpart): for tuning sweeps and
+ * tests that pin one kernel plan. Process-wide; the library never reads the
+ * environment. An override picks tiles, K splits or workgroup sizes only, so
+ * results stay within the operators' documented error (a different plan can
+ * change the summation order, never the arithmetic). value NULL or "" clears.
+ *   "gemm_cfg"          "<build 0..15>[:<K splits>]" (Q8 NT GEMM tile build;
+ *                       the splits apply to the workspace entries)
+ *   "nn_kernel"         "general": the NN GEMM's untiled kernel for every shape
+ *   "nn_splits"         "<1..64>": NN GEMM K splits (workspace entry)
+ *   "attn_nw"           "2" | "4": fp16 attention waves per workgroup
+ *   "attn_split"        "<rest>[:<pieces>]": key-split plan of
+ *                       mi_fused_attention_ws ("0": never split)
+ *   "attn_direct_store" "1": attention outputs stored from the MFMA layout
+ *                       instead of whole rows through LDS
+ * MI_ERR_INVALID_ARG for an unknown name or a malformed value. Not
+ * synchronised with calls in flight on other threads.                      */
+int mi_tuning_set(const char* name, const char* value);
+/* Clears every override.                                                   */
+void mi_tuning_reset(void);
+
 /* ------------------------------------------------------------ Q8_0 format --
  * GGUF Q8_0 block: 34 bytes {fp16 d (little-endian), int8 q[32]}; element i of
  * a tensor lives in block i/32 (flat GGUF order, Gguf.cpp:83, :514-523).
@@ -155,12 +175,19 @@ int mi_gemm_nt_q8_0_ws(const float* A, const void* W, const float* bias, float* 
  * 128 x 128 tiles, into at most 512 / tiles parts, or fewer than 512 64 x 64
  * tiles into about 256 workgroups, at most 32 MiB of partials). Calls on one GPU share
  * the scratch: calls that overlap on one GPU (unordered streams) race, so
- * order them (one stream). Calls no hipMalloc / hipFree; the scratch's device
- * address is looked up once per GPU, on the first call made there.          */
+ * order them (one stream). Calls no hipMalloc / hipFree. The scratch's device
+ * address is looked up once per GPU (hipGetSymbolAddress, which may load the
+ * code object there): by mi_gemm_noalloc_init, or else by the first call on
+ * that GPU. A caller that captures the entry into a HIP graph calls
+ * mi_gemm_noalloc_init on the GPU before capturing; a first call made inside
+ * a capture without it returns MI_ERR_UNSUPPORTED and records nothing.      */
 #define MI_GEMM_NOALLOC_SCRATCH_BYTES (32ull << 20)
 int mi_gemm_nt_q8_0_noalloc(const float* A, const void* W, const float* bias, float* C, uint32_t M,
                             uint32_t N, uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldc,
                             uint32_t batch, uint64_t sA, uint64_t sC, void* stream);
+/* Looks up the current GPU's scratch address for mi_gemm_nt_q8_0_noalloc
+ * (no counterpart in the reference; for the same callers). Idempotent.      */
+int mi_gemm_noalloc_init(void);
 
 /* Reference device layout: payload (int8 x4 per uint32, flat [N,K] order) +
  * fp32 scale per 32 flat elements (any fp32 value: LoRA requantisation writes
@@ -235,7 +262,9 @@ int mi_fused_attn_supported(uint32_t C, uint32_t heads);
 
 /* fusedAttention(Engine&, const FusedAttnArgs&) (fused_attn.cpp:40-61):
  * fp32 q/k/v/out [T, C] contiguous, scale 1/sqrt(C/heads).
- * q, k, v, out 16-byte aligned; out must not overlap q, k or v.            */
+ * q, k, v, out 16-byte aligned; out must not overlap q, k or v.
+ * fp32 output, so MI_ATTN_PREC_AUTO computes P in two fp16 parts (below):
+ * max |err| ~1e-5 x RMS, inside the reference test's rel 2e-5.             */
 int mi_fused_attention(const float* q, const float* k, const float* v, float* out, uint32_t Tq,
                        uint32_t Tk, uint32_t C, uint32_t heads, int causal, void* stream);
 
@@ -256,7 +285,25 @@ typedef struct mi_attn_args {
     uint64_t sq, sk, sv, so;       /* batch stride, 0 -> T * ld */
     const int32_t* kv_len;         /* device int32[batch] or NULL (all Tk keys) */
     float scale;                   /* 0 -> 1/sqrt(C/heads) (fused_attn.cpp:55) */
+    int32_t precision;             /* mi_attn_precision (extension; 0 = MI_ATTN_PREC_AUTO) */
 } mi_attn_args;
+
+/* How the softmax weights P enter the PV product (extension; the reference
+ * computes in fp32 throughout, fused_attn_tiled.comp:130-182). The MFMA takes
+ * fp16 operands, so P = exp2(s - m) is rounded to fp16 (2^-11 relative):
+ *   MI_ATTN_PREC_FP16:  one product with fp16 P (plus P's residual on the
+ *                       diagonal tiles of a causal launch). Max |err| vs fp32
+ *                       math up to ~2e-3 x RMS(out) on rows whose weight sits
+ *                       on a few keys; typically 0.5-1.2e-3.
+ *   MI_ATTN_PREC_SPLIT: P as fp16 hi + lo (lo = fp16(P - hi)) in two
+ *                       products, P exact to ~2^-22: max |err| 1-5e-6 x RMS,
+ *                       about +45% time on long key ranges, +6% on short ones.
+ *   MI_ATTN_PREC_AUTO:  SPLIT for fp32 outputs (fp32-grade accuracy, as the
+ *                       reference's own test asks of its fp32 kernel,
+ *                       tests/fused_attn_test.cpp:118-126), FP16 for fp16
+ *                       outputs (whose own storage rounding, 2^-12 |out|, is of
+ *                       the same order as P's).                             */
+enum mi_attn_precision { MI_ATTN_PREC_AUTO = 0, MI_ATTN_PREC_FP16 = 1, MI_ATTN_PREC_SPLIT = 2 };
 
 int mi_fused_attention_ex(const mi_attn_args* args, void* stream);
 

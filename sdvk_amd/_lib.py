@@ -15,6 +15,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libmi_sdvk.so"
 (MI_OK, MI_ERR_INVALID_ARG, MI_ERR_UNSUPPORTED, MI_ERR_ALIGNMENT, MI_ERR_ALIASING, MI_ERR_HIP, MI_ERR_IO,
  MI_ERR_NOT_FOUND) = range(8)
 MI_F32, MI_F16 = 0, 1
+MI_ATTN_PREC_AUTO, MI_ATTN_PREC_FP16, MI_ATTN_PREC_SPLIT = 0, 1, 2
 
 # Every function declared in include/mi_sdvk.h, with its ctypes signature.
 _u32, _u64, _i32, _vp = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int32, ctypes.c_void_p
@@ -30,6 +31,7 @@ class MiAttnArgs(ctypes.Structure):
         ("sq", _u64), ("sk", _u64), ("sv", _u64), ("so", _u64),
         ("kv_len", _vp),
         ("scale", ctypes.c_float),
+        ("precision", _i32),
     ]
 
 
@@ -67,6 +69,8 @@ SIGNATURES = {
     "mi_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "mi_last_error": (ctypes.c_char_p, []),
     "mi_version": (ctypes.c_int, []),
+    "mi_tuning_set": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p]),
+    "mi_tuning_reset": (None, []),
     "mi_q8_0_dequant": (ctypes.c_int, [_vp, _vp, ctypes.c_int, _u64, _vp]),
     "mi_q8_split_dequant": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_int, _u64, _vp]),
     "mi_q8_0_to_split": (ctypes.c_int, [_vp, _vp, _vp, _u64, _vp]),
@@ -80,6 +84,7 @@ SIGNATURES = {
                                           _u64, _u64, _vp, _u64, _vp]),
     "mi_gemm_nt_q8_0_noalloc": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32,
                                                _u64, _u64, _vp]),
+    "mi_gemm_noalloc_init": (ctypes.c_int, []),
     "mi_gemm_nt_q8_split_ws": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32,
                                               _u32, _u64, _u64, _vp, _u64, _vp]),
     "mi_gemm_nt_q8_0_geglu": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp]),

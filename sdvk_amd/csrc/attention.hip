@@ -61,7 +61,7 @@ struct AttnArgs {
     const int32_t* kv_len;
     float c;  // scale * log2(e)
     int ostage;  // output rows and head columns 16-byte aligned: store O through LDS (store_o_rows)
-    int precise;  // MI_ATTN_PRECISE: P's fp16 residual as a second PV product on every tile
+    int precise;  // P's fp16 residual as a second PV product on every tile (mi_attn_precision)
     // Key-split plan of the fp16 kernel (mi_fused_attention_ws): the first nfull query blocks run
     // whole; each later one runs as `pieces` workgroups over consecutive key-tile ranges that write
     // unnormalised partials to `part` (kPartFloats floats per piece), merged by attn_merge_kernel.
@@ -537,7 +537,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
 // RESID: which tiles add P's fp16 residual as a second PV product, at compile
 // time (a runtime test of the flag inside the loop cost non-causal launches
 // 2.4%): kResidNone; kResidDiagonal, a causal launch's diagonal tiles;
-// kResidAll, every tile (MI_ATTN_PRECISE).
+// kResidAll, every tile (MI_ATTN_PREC_SPLIT).
 constexpr int kResidNone = 0, kResidDiagonal = 1, kResidAll = 2;
 template <typename TO, int NW, int RESID>
 __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t qtiles) {
@@ -1002,10 +1002,10 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, uint32_t qt
 // 64-query block holds every query. Measured on MI355X, 4-wave workgroups are
 // as fast or faster on every grid size, small ones included (160-256 blocks of
 // 128 queries: 23% faster than twice as many 2-wave workgroups).
-// MI_ATTN_NW = 2 or 4 pins one (tuning sweeps).
+// mi_tuning_set("attn_nw", "2" | "4") pins one (tuning sweeps).
 int f16_waves(const AttnArgs& a, uint32_t /*batch*/) {
-    const char* env = std::getenv("MI_ATTN_NW");
-    return env && std::strcmp(env, "2") == 0 ? 2 : env && std::strcmp(env, "4") == 0 ? 4 : a.Tq <= 64 ? 2 : 4;
+    const int forced = tuning().attn_nw.load(std::memory_order_relaxed);
+    return forced == 2 || forced == 4 ? forced : a.Tq <= 64 ? 2 : 4;
 }
 
 // Compute units of the current device (queried once per device).
@@ -1032,8 +1032,8 @@ uint32_t cu_count() {
 // 8 pieces 110.3; 2 x 9 heads (64 rest) unsplit 116.4, 2 / 4 / 8 pieces 119.5 /
 // 110.0 / 113.4; 2 x 12 heads (256 rest: no plan, CUs / rest = 1) 131 unsplit
 // against 141 in 2 pieces.
-// Only unmasked, non-causal fp16 launches split. MI_ATTN_SPLIT="<rest>:<pieces>"
-// forces a plan (tests; "0" turns the split off).
+// Only unmasked, non-causal fp16 launches split. mi_tuning_set("attn_split",
+// "<rest>:<pieces>") forces a plan (tests; "0" turns the split off).
 struct SplitPlan {
     uint32_t nfull = 0, pieces = 1, rest = 0;
 };
@@ -1044,11 +1044,10 @@ SplitPlan plan_split(const AttnArgs& a, uint32_t batch) {
     const uint64_t W = static_cast<uint64_t>(ceil_div(a.Tq, kBQ)) * a.heads * batch;
     const uint32_t nt = ceil_div(a.Tk, kBKV);
     uint64_t rest = 0, pieces = 1;
-    const char* env = std::getenv("MI_ATTN_SPLIT");
-    if (env && *env) {
-        rest = std::strtoull(env, nullptr, 10);
-        const char* c = std::strchr(env, ':');
-        pieces = c ? std::strtoull(c + 1, nullptr, 10) : 2;
+    const int forced_rest = tuning().attn_split_rest.load(std::memory_order_relaxed);
+    if (forced_rest >= 0) {
+        rest = static_cast<uint64_t>(forced_rest);
+        pieces = static_cast<uint64_t>(tuning().attn_split_pieces.load(std::memory_order_relaxed));
         rest = rest < W ? rest : W;
         if (pieces > nt) pieces = nt;
     } else {
@@ -1108,6 +1107,8 @@ int run(const mi_attn_args& x, hipStream_t s, const char* fn, void* ws = nullptr
     if (x.in_dtype != MI_F32 && x.in_dtype != MI_F16) return fail(MI_ERR_INVALID_ARG, "%s: in_dtype %d", fn, x.in_dtype);
     if (x.out_dtype != MI_F32 && x.out_dtype != MI_F16) return fail(MI_ERR_INVALID_ARG, "%s: out_dtype %d", fn, x.out_dtype);
     if (x.batch == 0) return fail(MI_ERR_INVALID_ARG, "%s: batch 0", fn);
+    if (x.precision != MI_ATTN_PREC_AUTO && x.precision != MI_ATTN_PREC_FP16 && x.precision != MI_ATTN_PREC_SPLIT)
+        return fail(MI_ERR_INVALID_ARG, "%s: precision %d", fn, x.precision);
     if (!mi_fused_attn_supported(x.C, x.heads))
         return fail(MI_ERR_UNSUPPORTED, "%s: unsupported C=%u heads=%u (need heads | C and C/heads <= 64)", fn, x.C, x.heads);
     if (x.batch > 65535 || x.heads > 65535) return fail(MI_ERR_UNSUPPORTED, "%s: batch/heads > 65535", fn);
@@ -1141,11 +1142,8 @@ int run(const mi_attn_args& x, hipStream_t s, const char* fn, void* ws = nullptr
     const float scale = x.scale != 0.0f ? x.scale : 1.0f / sqrtf(static_cast<float>(a.hd));
     a.c = scale * 1.4426950408889634f;
     a.ostage = aligned(x.out, 16) && (ldo * eo) % 16 == 0 && (so * eo) % 16 == 0 && (a.hd * eo) % 16 == 0 &&
-               !std::getenv("MI_ATTN_DIRECT_STORE");
-    {
-        const char* p = std::getenv("MI_ATTN_PRECISE");
-        a.precise = p && *p && std::strcmp(p, "0") != 0 ? 1 : 0;
-    }
+               tuning().attn_direct_store.load(std::memory_order_relaxed) == 0;
+    a.precise = x.precision == MI_ATTN_PREC_SPLIT || (x.precision == MI_ATTN_PREC_AUTO && x.out_dtype == MI_F32);
 
     // 16-byte vector path: every 8-element chunk of every row is 16-byte aligned.
     const uintptr_t vin = 8 * ei, vout = 4 * eo;

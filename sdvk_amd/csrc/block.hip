@@ -105,6 +105,9 @@ int attention(const mi_block_dims& d, const float* q, const float* k, const floa
     x.in_dtype = MI_F32;
     x.out_dtype = MI_F32;
     x.kv_len = kv_len;
+    // the output only feeds the out-projection GEMM, which rounds its A
+    // operand to fp16: one fp16 P product (2^-11 per weight) is below that
+    x.precision = MI_ATTN_PREC_FP16;
     return mi_fused_attention_ex(&x, s);
 }
 

@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
@@ -24,6 +25,24 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 // Maps the launch's hipGetLastError() to MI_ERR_HIP (with its text) or MI_OK.
 int check_launch(const char* what);
+
+// Plan overrides set through mi_tuning_set (status.hip): process-wide, read
+// with one atomic load per call, never from the environment. Defaults mean
+// "the built-in rules decide". They pick tiles, split counts and workgroup
+// sizes only: no override changes an operator's arithmetic beyond the
+// summation order of a different plan.
+constexpr int kGemmBuilds = 16;  // tile builds of gemm_q8.hip (kNumCfg)
+struct Tuning {
+    std::atomic<int> gemm_cfg{-1};          // tile build, or -1
+    std::atomic<int> gemm_splits{1};        // K splits with gemm_cfg (workspace entries)
+    std::atomic<int> nn_general{0};         // 1: the NN GEMM's untiled kernel for every shape
+    std::atomic<int> nn_splits{0};          // NN GEMM K splits, or 0
+    std::atomic<int> attn_nw{0};            // fp16 attention waves per workgroup (2, 4), or 0
+    std::atomic<int> attn_split_rest{-1};   // key split: rest blocks (0 = never split), or -1
+    std::atomic<int> attn_split_pieces{2};  // key split: pieces per rest block
+    std::atomic<int> attn_direct_store{0};  // 1: attention outputs stored from the MFMA layout
+};
+Tuning& tuning();
 
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 

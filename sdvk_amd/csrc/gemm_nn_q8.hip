@@ -312,9 +312,9 @@ namespace mi {
 namespace {
 
 bool nn_tiled(const uint32_t* payload, uint32_t K, uint32_t lda, uint64_t sA) {
-    const char* env = std::getenv("MI_NN_KERNEL");  // "general": the untiled kernel for every shape (tests)
+    // mi_tuning_set("nn_kernel", "general"): the untiled kernel for every shape (tests)
     return K > 0 && K % kBK2 == 0 && aligned(payload, 16) && lda % 16 == 0 && sA % 16 == 0 &&
-           !(env && std::strcmp(env, "general") == 0);
+           tuning().nn_general.load(std::memory_order_relaxed) == 0;
 }
 
 // K splits of the tiled kernel: one 8-wave workgroup per CU; the most splits
@@ -328,9 +328,9 @@ uint32_t nn_splits(uint32_t M, uint32_t N, uint32_t K, uint32_t batch) {
     const uint64_t tiles = static_cast<uint64_t>(ceil_div(N, kBN2)) * ceil_div(M, kBM2) * batch;
     const uint32_t ksteps = K / kBK2;
     uint32_t splits = 1;
-    const char* env = std::getenv("MI_NN_SPLITS");  // a fixed split count (tuning sweeps)
-    if (env && *env) {
-        splits = static_cast<uint32_t>(std::max(1, std::atoi(env)));
+    const int forced = tuning().nn_splits.load(std::memory_order_relaxed);  // mi_tuning_set("nn_splits")
+    if (forced > 0) {
+        splits = static_cast<uint32_t>(forced);
         splits = std::min<uint32_t>({splits, std::max(1u, ksteps), 65535u / std::max(1u, batch)});
     } else if (tiles < kCUs) {
         splits = static_cast<uint32_t>(std::min<uint64_t>({kCUs / tiles, ksteps / 4, 65535u / std::max(1u, batch)}));

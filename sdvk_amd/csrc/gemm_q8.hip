@@ -1315,6 +1315,7 @@ enum CfgId {
     kP192x256,                                                // producer / consumer kernel
     kNumCfg
 };
+static_assert(kNumCfg == kGemmBuilds, "mi_tuning_set bounds gemm_cfg by kGemmBuilds");
 
 // Group height for the tile order: the XCD chunks (blocks b with b % 8 == x,
 // contiguous in the grouped order) each read the A panels of the rows and the
@@ -1537,13 +1538,12 @@ struct Plan {
 // 69.4 us for 4), and small 64x64 grids split K until ~256 workgroups run.
 Plan choose(uint32_t M, uint32_t N, uint32_t K, uint32_t batch, bool allow_split) {
     Plan p{kC64x64, 1};
-    const char* env = std::getenv("MI_GEMM_CFG");  // "<cfg>[:<splits>]" overrides (tuning sweeps)
-    if (env && *env) {
-        p.cfg = std::atoi(env);
-        const char* c = std::strchr(env, ':');
-        p.splits = c ? static_cast<uint32_t>(std::atoi(c + 1)) : 1u;
-        if (p.cfg < 0 || p.cfg >= kNumCfg) p.cfg = kC64x64;
-        if (p.splits < 1 || !allow_split) p.splits = 1;
+    // mi_tuning_set("gemm_cfg", "<cfg>[:<splits>]") pins a build (tuning sweeps, tests)
+    const int forced = tuning().gemm_cfg.load(std::memory_order_relaxed);
+    if (forced >= 0) {
+        p.cfg = forced < kNumCfg ? forced : kC64x64;
+        p.splits = allow_split ? static_cast<uint32_t>(std::max(1, tuning().gemm_splits.load(std::memory_order_relaxed)))
+                               : 1u;
         return p;
     }
     auto tiles = [&](uint32_t bm, uint32_t bn) {
@@ -1781,13 +1781,24 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
 
-// Device address of the current GPU's scratch (looked up on its first use).
-int scratch_on_current_device(const char* fn, void** out) {
+// Device address of the current GPU's scratch, looked up on its first use.
+// The lookup can load the code object on that GPU, which has no place inside
+// a stream capture: with `capturing` set and no address yet, the call fails
+// instead (mi_gemm_noalloc_init does the lookup beforehand).
+int scratch_on_current_device(const char* fn, void** out, hipStream_t stream = nullptr, bool check_capture = false) {
     int dev = -1;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return fail(MI_ERR_HIP, "%s: hipGetDevice: %s", fn, hipGetErrorString(e));
     if (dev < 0 || dev >= kMaxDevices) return fail(MI_ERR_UNSUPPORTED, "%s: device index %d >= %d", fn, dev, kMaxDevices);
     std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev] && check_capture) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        e = hipStreamIsCapturing(stream, &cs);
+        if (e != hipSuccess) return fail(MI_ERR_HIP, "%s: hipStreamIsCapturing: %s", fn, hipGetErrorString(e));
+        if (cs != hipStreamCaptureStatusNone)
+            return fail(MI_ERR_UNSUPPORTED, "%s: first call on device %d inside a stream capture: call "
+                        "mi_gemm_noalloc_init() on the device before capturing", fn, dev);
+    }
     if (!g_scratch_ptr[dev]) {
         void* p = nullptr;
         e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
@@ -1810,10 +1821,15 @@ extern "C" int mi_gemm_nt_q8_0_noalloc(const float* A, const void* W, const floa
     const char* fn = "mi_gemm_nt_q8_0_noalloc";
     if (M == 0 || N == 0) return MI_OK;
     void* ws = nullptr;
-    const int st = scratch_on_current_device(fn, &ws);
+    const int st = scratch_on_current_device(fn, &ws, static_cast<hipStream_t>(stream), true);
     if (st) return st;
     return gemm_blocks(fn, A, W, bias, C, M, N, K, mode, lda, ldc, batch, sA, sC, ws, kScratchBytes,
                        static_cast<hipStream_t>(stream), true);
+}
+
+extern "C" int mi_gemm_noalloc_init(void) {
+    void* ws = nullptr;
+    return scratch_on_current_device("mi_gemm_noalloc_init", &ws);
 }
 
 extern "C" int mi_gemm_nt_q8_0(const float* A, const void* W, const float* bias, float* C, uint32_t M, uint32_t N,

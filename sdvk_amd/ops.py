@@ -28,11 +28,12 @@ from dataclasses import dataclass
 from typing import Optional, Sequence
 
 from . import _lib
-from ._lib import (MI_BLOCK_FUSED_EPILOGUES, MI_BLOCK_JOINT_QKV, MI_F16, MI_F32, MiAttnArgs, MiBlockDims,
-                   MiBlockWeights, MiError, call, ptr)
+from ._lib import (MI_ATTN_PREC_AUTO, MI_ATTN_PREC_FP16, MI_ATTN_PREC_SPLIT, MI_BLOCK_FUSED_EPILOGUES,
+                   MI_BLOCK_JOINT_QKV, MI_F16, MI_F32, MiAttnArgs, MiBlockDims, MiBlockWeights, MiError, call, ptr)
 
 __all__ = [
-    "MiError", "MI_F32", "MI_F16", "MI_BLOCK_FUSED_EPILOGUES", "MI_BLOCK_JOINT_QKV", "FusedAttnArgs", "fused_attn_supported", "fused_attention",
+    "MiError", "MI_F32", "MI_F16", "MI_ATTN_PREC_AUTO", "MI_ATTN_PREC_FP16", "MI_ATTN_PREC_SPLIT",
+    "tuning", "tuning_set", "tuning_reset", "MI_BLOCK_FUSED_EPILOGUES", "MI_BLOCK_JOINT_QKV", "FusedAttnArgs", "fused_attn_supported", "fused_attention",
     "fused_attention_ex", "gemm_nt_q8", "gemm_nt_q8_bias", "gemm_nt_q8_0", "gemm_nt_q8_0_geglu", "gemm_nn_q8",
     "gemm_workspace_bytes", "gemm_nn_workspace_bytes",
     "q8_0_dequant",
@@ -46,6 +47,36 @@ def _s(stream) -> Optional[int]:
     if stream is None:
         return None
     return stream.handle.value if hasattr(stream, "handle") else int(stream)
+
+
+# ---------------------------------------------------------------- plan overrides --
+
+def tuning_set(name: str, value: Optional[str]) -> None:
+    """mi_tuning_set: pins one plan choice process-wide (None clears it)."""
+    call("mi_tuning_set", name.encode(), None if value is None else str(value).encode())
+
+
+def tuning_reset() -> None:
+    """mi_tuning_reset: every plan choice back to the built-in rules."""
+    _lib.load().mi_tuning_reset()
+
+
+class tuning:
+    """Context manager: `with ops.tuning(gemm_cfg="1:2"):` sets the overrides
+    for the block and clears them on exit."""
+
+    def __init__(self, **overrides):
+        self.overrides = {k: v for k, v in overrides.items()}
+
+    def __enter__(self):
+        for k, v in self.overrides.items():
+            tuning_set(k, v)
+        return self
+
+    def __exit__(self, *exc):
+        for k in self.overrides:
+            tuning_set(k, None)
+        return False
 
 
 # ------------------------------------------------------------------ attention --
@@ -80,39 +111,38 @@ def fused_attention_ex(q, k, v, out, *, batch: int, Tq: int, Tk: int, C: int, he
                        causal: bool = False, in_dtype: int = MI_F32, out_dtype: int = MI_F32,
                        ldq: int = 0, ldk: int = 0, ldv: int = 0, ldo: int = 0, sq: int = 0,
                        sk: int = 0, sv: int = 0, so: int = 0, kv_len=None, scale: float = 0.0,
-                       stream=None) -> None:
+                       precision: int = MI_ATTN_PREC_AUTO, stream=None) -> None:
     """Batched / strided / fp16 / key-padded form (mi_fused_attention_ex)."""
-    x = MiAttnArgs(q=ptr(q), k=ptr(k), v=ptr(v), out=ptr(out), batch=batch, Tq=Tq, Tk=Tk, C=C,
-                   heads=heads, causal=1 if causal else 0, in_dtype=in_dtype, out_dtype=out_dtype,
-                   ldq=ldq, ldk=ldk, ldv=ldv, ldo=ldo, sq=sq, sk=sk, sv=sv, so=so,
-                   kv_len=ptr(kv_len), scale=scale)
+    x = _attn_args(q, k, v, out, batch, Tq, Tk, C, heads, causal, in_dtype, out_dtype, ldq, ldk, ldv, ldo, sq, sk,
+                   sv, so, kv_len, scale, precision)
     call("mi_fused_attention_ex", ctypes.byref(x), _s(stream))
 
 
 def _attn_args(q, k, v, out, batch, Tq, Tk, C, heads, causal, in_dtype, out_dtype, ldq, ldk, ldv, ldo, sq, sk, sv, so,
-               kv_len, scale) -> MiAttnArgs:
+               kv_len, scale, precision=MI_ATTN_PREC_AUTO) -> MiAttnArgs:
     return MiAttnArgs(q=ptr(q), k=ptr(k), v=ptr(v), out=ptr(out), batch=batch, Tq=Tq, Tk=Tk, C=C,
                       heads=heads, causal=1 if causal else 0, in_dtype=in_dtype, out_dtype=out_dtype,
                       ldq=ldq, ldk=ldk, ldv=ldv, ldo=ldo, sq=sq, sk=sk, sv=sv, so=so,
-                      kv_len=ptr(kv_len), scale=scale)
+                      kv_len=ptr(kv_len), scale=scale, precision=precision)
 
 
 def fused_attention_ws_bytes(*, batch: int, Tq: int, Tk: int, C: int, heads: int, causal: bool = False,
-                             in_dtype: int = MI_F32, out_dtype: int = MI_F32, kv_len=None) -> int:
+                             in_dtype: int = MI_F32, out_dtype: int = MI_F32, kv_len=None,
+                             precision: int = MI_ATTN_PREC_AUTO) -> int:
     """Workspace mi_fused_attention_ws uses for this call's key-split plan (0: no split); contiguous tensors
     with 16-byte aligned rows assumed (the plan does not depend on the addresses otherwise)."""
     x = _attn_args(0x1000, 0x2000_0000_000, 0x4000_0000_000, 0x6000_0000_000, batch, Tq, Tk, C, heads, causal,
-                   in_dtype, out_dtype, 0, 0, 0, 0, 0, 0, 0, 0, kv_len, 0.0)
+                   in_dtype, out_dtype, 0, 0, 0, 0, 0, 0, 0, 0, kv_len, 0.0, precision)
     return int(_lib.load().mi_fused_attention_ws_bytes(ctypes.byref(x)))
 
 
 def fused_attention_ws(q, k, v, out, workspace, *, batch: int, Tq: int, Tk: int, C: int, heads: int,
                        causal: bool = False, in_dtype: int = MI_F32, out_dtype: int = MI_F32, ldq: int = 0,
                        ldk: int = 0, ldv: int = 0, ldo: int = 0, sq: int = 0, sk: int = 0, sv: int = 0, so: int = 0,
-                       kv_len=None, scale: float = 0.0, stream=None) -> None:
+                       kv_len=None, scale: float = 0.0, precision: int = MI_ATTN_PREC_AUTO, stream=None) -> None:
     """mi_fused_attention_ws: fused_attention_ex with a workspace for the key-split plan."""
     x = _attn_args(q, k, v, out, batch, Tq, Tk, C, heads, causal, in_dtype, out_dtype, ldq, ldk, ldv, ldo, sq, sk,
-                   sv, so, kv_len, scale)
+                   sv, so, kv_len, scale, precision)
     wp, wn = _ws(workspace)
     call("mi_fused_attention_ws", ctypes.byref(x), wp, wn, _s(stream))
 

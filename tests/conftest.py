@@ -47,3 +47,14 @@ def pytest_terminal_summary(terminalreporter):
     for key, (e, tol, test) in sorted(WORST.items()):
         case = test.split("::")[-1]
         tr.write_line(f"{key:<64} {e:.3e}  bar {tol:.1e}  ({100 * e / tol:5.1f}% of the bar)  {case}")
+
+
+@pytest.fixture
+def tune(gpu):
+    """tune(name, value): a plan override through mi_tuning_set for this test
+    (value None clears it); every override is cleared when the test ends."""
+    from sdvk_amd import ops
+
+    ops.tuning_reset()
+    yield ops.tuning_set
+    ops.tuning_reset()

@@ -12,7 +12,6 @@ columns, batch gaps). Test infrastructure only.
 from __future__ import annotations
 
 import json
-import os
 import sys
 from pathlib import Path
 
@@ -27,8 +26,8 @@ import ctypes  # noqa: E402
 import emu as kemu  # noqa: E402
 from helpers import assert_parity, fp16_half_ulp, q8_weights, rms  # noqa: E402
 from oracle import binding as ob  # noqa: E402
-from sdvk_amd._lib import (MI_BLOCK_FUSED_EPILOGUES, MI_BLOCK_JOINT_QKV, MI_F16, MI_F32, MiAttnArgs,  # noqa: E402
-                           MiBlockDims, MiBlockWeights)
+from sdvk_amd._lib import (MI_ATTN_PREC_FP16, MI_ATTN_PREC_SPLIT, MI_BLOCK_FUSED_EPILOGUES,  # noqa: E402
+                           MI_BLOCK_JOINT_QKV, MI_F16, MI_F32, MiAttnArgs, MiBlockDims, MiBlockWeights)
 from test_gpu_block import BLOCK_TOL, make_weights  # noqa: E402
 import gguf_writer as gw  # noqa: E402
 from sdvk_amd._lib import MiGgufTensorInfo  # noqa: E402
@@ -36,11 +35,17 @@ from sdvk_amd._lib import MiGgufTensorInfo  # noqa: E402
 SENTINEL = np.float32(12345.0)
 
 
+_EMU = None
+
+
+def _tune(name, value):
+    """mi_tuning_set on the emulation build (value None clears the override)."""
+    st = _EMU.lib.mi_tuning_set(name.encode(), None if value is None else str(value).encode())
+    assert st == 0, f"mi_tuning_set({name}, {value}): status {st}"
+
+
 def _set_cfg(cfg):
-    if cfg is None:
-        os.environ.pop("MI_GEMM_CFG", None)
-    else:
-        os.environ["MI_GEMM_CFG"] = str(cfg)
+    _tune("gemm_cfg", cfg)
 
 
 def _logical_mask(M, N, ldc, batch, sC, size):
@@ -135,9 +140,7 @@ def gemm_geglu(E, *, M, F, K, cfg=None, bias=True, lda=0, ldg=0, seed=1, front=F
     assert np.array_equal(got[~mask], np.full((~mask).sum(), SENTINEL, np.float32)), "padding of G changed"
     got = got[mask].reshape(M, F)
     # separate path on the same build: same MFMA sums (no K split), fp32 epilogue arithmetic
-    os.environ["MI_GEMM_CFG"] = (cfg.split(":")[0] if cfg else os.environ.get("MI_GEMM_CFG", "")) or "0"
-    if cfg is None:
-        os.environ.pop("MI_GEMM_CFG", None)
+    _tune("gemm_cfg", cfg.split(":")[0] if cfg else None)
     dH, dY = E.buf(nbytes=M * 2 * F * 4), E.buf(nbytes=M * F * 4)
     E.call("mi_gemm_nt_q8_0", dA.ptr, dW.ptr, dB.ptr if dB else None, dH.ptr, M, 2 * F, K, 0, lda, 0, 1, 0, 0, None)
     E.call("mi_geglu", dH.ptr, dY.ptr, M, F, None)
@@ -165,12 +168,9 @@ def gemm_geglu(E, *, M, F, K, cfg=None, bias=True, lda=0, ldg=0, seed=1, front=F
 def gemm_nn(E, *, M, N, K, mode=0, batch=1, lda=0, ldb=0, ldc=0, sA=0, sB=0, sC=0, seed=1, front=False,
             order=0, tol=2e-3, kernel=None, ws=True):
     """mi_gemm_nn_q8_split against the oracle (flat-index scales). kernel="general"
-    forces the untiled kernel (MI_NN_KERNEL) on shapes the tiled one would take."""
+    forces the untiled kernel (the nn_kernel override) on shapes the tiled one would take."""
     E.order(order)
-    if kernel:
-        os.environ["MI_NN_KERNEL"] = kernel
-    else:
-        os.environ.pop("MI_NN_KERNEL", None)
+    _tune("nn_kernel", kernel or None)
     lda_e, ldb_e, ldc_e = lda or K, ldb or N, ldc or N
     a_el = (batch - 1) * sA + (M - 1) * lda_e + K
     b_el = (batch - 1) * sB + (K - 1) * ldb_e + N if K else N
@@ -201,33 +201,24 @@ def gemm_nn(E, *, M, N, K, mode=0, batch=1, lda=0, ldb=0, ldc=0, sA=0, sB=0, sC=
 
 def attention(E, *, batch=1, Tq, Tk, C, heads, causal=False, f16_in=False, f16_out=False, kv_len=None, seed=1,
               front=False, order=0, tol=2e-3, nw=None, outliers=None, direct_store=False, split=None,
-              precise=False):
+              precise=False, precision=None):
     """mi_fused_attention_ex (contiguous [batch, T, C]) against the oracle;
     split "<rest>:<pieces>": through mi_fused_attention_ws with that key-split
-    plan forced (MI_ATTN_SPLIT) and the workspace the library asks for;
-    nw pins the fp16 kernel's workgroup size (MI_ATTN_NW); outliers: key
+    plan forced (the attn_split override) and the workspace the library asks
+    for; nw pins the fp16 kernel's workgroup size (attn_nw); outliers: key
     indices whose scores stand far above the rest (q ~ 1, k ~ 0.1 N(0, 1),
     those keys 3.0), so that a running max that misses them overflows;
     direct_store: output stores straight from the MFMA layout
-    (MI_ATTN_DIRECT_STORE) instead of whole rows through LDS; precise: P's
-    fp16 residual as a second PV product on every tile (MI_ATTN_PRECISE)."""
+    (attn_direct_store) instead of whole rows through LDS; precision: the
+    mi_attn_args field, by default MI_ATTN_PREC_FP16 (one fp16 P product);
+    precise: MI_ATTN_PREC_SPLIT (P's fp16 residual as a second PV product on
+    every tile)."""
     E.order(order)
-    if nw:
-        os.environ["MI_ATTN_NW"] = str(nw)
-    else:
-        os.environ.pop("MI_ATTN_NW", None)
-    if direct_store:
-        os.environ["MI_ATTN_DIRECT_STORE"] = "1"
-    else:
-        os.environ.pop("MI_ATTN_DIRECT_STORE", None)
-    if split:
-        os.environ["MI_ATTN_SPLIT"] = split
-    else:
-        os.environ.pop("MI_ATTN_SPLIT", None)
-    if precise:
-        os.environ["MI_ATTN_PRECISE"] = "1"
-    else:
-        os.environ.pop("MI_ATTN_PRECISE", None)
+    _tune("attn_nw", nw)
+    _tune("attn_direct_store", "1" if direct_store else None)
+    _tune("attn_split", split)
+    if precision is None:
+        precision = MI_ATTN_PREC_SPLIT if precise else MI_ATTN_PREC_FP16
     idt = np.float16 if f16_in else np.float32
     q = ob.normal(seed, batch * Tq * C).astype(idt)
     k = ob.normal(seed + 1, batch * Tk * C).astype(idt)
@@ -244,13 +235,13 @@ def attention(E, *, batch=1, Tq, Tk, C, heads, causal=False, f16_in=False, f16_o
     dl = E.buf(np.asarray(kv_len, dtype=np.int32), front=front) if kv_len is not None else None
     x = MiAttnArgs(q=dq.ptr, k=dk.ptr, v=dv.ptr, out=do.ptr, batch=batch, Tq=Tq, Tk=Tk, C=C, heads=heads,
                    causal=1 if causal else 0, in_dtype=MI_F16 if f16_in else MI_F32,
-                   out_dtype=MI_F16 if f16_out else MI_F32, kv_len=dl.ptr if dl else None)
+                   out_dtype=MI_F16 if f16_out else MI_F32, kv_len=dl.ptr if dl else None, precision=precision)
     if split:
         nws = E.lib.mi_fused_attention_ws_bytes(ctypes.byref(x))
         assert nws > 0, f"attention: split {split} planned no workspace"
         dws = E.buf(nbytes=nws, front=front).fill(0xFF)  # NaN bytes: every partial read must have been written
         E.call("mi_fused_attention_ws", ctypes.byref(x), dws.ptr, nws, None)
-        os.environ.pop("MI_ATTN_SPLIT", None)
+        _tune("attn_split", None)
     else:
         E.call("mi_fused_attention_ex", ctypes.byref(x), None)
     got = do.get(odt, n_out).astype(np.float64)
@@ -357,7 +348,7 @@ def gemm_nn_full(E, *, M, N, K, seed=1, order=0, tol=2e-3):
     """mi_gemm_nn_q8_split at a full SDXL conv shape, sampled workgroups (the
     first and last column tiles of the last row tile, every K split)."""
     E.order(order)
-    os.environ.pop("MI_NN_KERNEL", None)
+    _tune("nn_kernel", None)
     w = ob.normal(seed, M * K, 0.0, 0.02)
     payload, scales = ob.q8_0_to_split(ob.q8_0_quantize(w), M * K)
     B = ob.normal(seed + 1, K * N)
@@ -386,11 +377,8 @@ def attention_full(E, *, batch, Tq, Tk, C, heads, masked=False, nw=None, seed=1,
     """fp16 mi_fused_attention_ex at a full benchmark shape, sampled workgroups
     (the first and the last in the kernel's order)."""
     E.order(order)
-    if nw:
-        os.environ["MI_ATTN_NW"] = str(nw)
-    else:
-        os.environ.pop("MI_ATTN_NW", None)
-    os.environ.pop("MI_ATTN_DIRECT_STORE", None)
+    _tune("attn_nw", nw)
+    _tune("attn_direct_store", None)
     q = ob.normal(seed, batch * Tq * C).astype(np.float16)
     k = ob.normal(seed + 1, batch * Tk * C).astype(np.float16)
     v = ob.normal(seed + 2, batch * Tk * C).astype(np.float16)
@@ -498,8 +486,7 @@ def routing(E, *, table, order=0):
     entry [op, dims, grid, threads] is launched with no workgroup emulated and
     its main launch must have that grid and block size."""
     E.order(order)
-    for var in ("MI_GEMM_CFG", "MI_NN_KERNEL", "MI_ATTN_NW"):
-        os.environ.pop(var, None)
+    E.lib.mi_tuning_reset()
     E.sample("*|-|-|-")
     bad = []
     for op, dims, grid, threads in table:
@@ -706,7 +693,8 @@ def main(argv):
     spec = json.loads(argv[1])
     name = spec.pop("case")
     schedules = spec.pop("schedules", [spec.pop("order", 0)])
-    E = kemu.Emu()
+    global _EMU
+    E = _EMU = kemu.Emu()
     ob.build()
     for order in schedules:
         e = CASES[name](E, order=order, **spec)

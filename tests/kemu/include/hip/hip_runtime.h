@@ -69,6 +69,12 @@ inline hipError_t hipGetSymbolAddress(void** p, const void* sym) {
     *p = const_cast<void*>(sym);
     return hipSuccess;
 }
+// The emulator records no graphs: no stream is ever capturing.
+enum hipStreamCaptureStatus { hipStreamCaptureStatusNone = 0, hipStreamCaptureStatusActive = 1 };
+inline hipError_t hipStreamIsCapturing(hipStream_t, hipStreamCaptureStatus* st) {
+    *st = hipStreamCaptureStatusNone;
+    return hipSuccess;
+}
 
 inline const char* hipGetErrorString(hipError_t e) { return e == hipSuccess ? "no error" : "emulated HIP error"; }
 // Asynchronous copies are deferred: they run at the event synchronisation that

@@ -111,6 +111,22 @@ def _fake_ops(calls):
     ns = {n: wrap(n) for n in names}
     ns.update(BlockDims=real.BlockDims, BlockWeights=real.BlockWeights,
               MI_BLOCK_FUSED_EPILOGUES=real.MI_BLOCK_FUSED_EPILOGUES, MI_BLOCK_JOINT_QKV=real.MI_BLOCK_JOINT_QKV)
+
+    class _Tuning:  # the context-manager form of tuning_set
+        def __init__(self, **over):
+            self.over = over
+
+        def __enter__(self):
+            for k, v in self.over.items():
+                ns["tuning_set"](k, v)
+            return self
+
+        def __exit__(self, *exc):
+            for k in self.over:
+                ns["tuning_set"](k, None)
+            return False
+
+    ns["tuning"] = _Tuning
     return types.SimpleNamespace(**ns)
 
 

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 from helpers import REL_RMS_TOL, assert_parity, fp16_half_ulp, rms
-from sdvk_amd import MI_F16, MI_F32, ops
+from sdvk_amd import MI_ATTN_PREC_AUTO, MI_ATTN_PREC_FP16, MI_ATTN_PREC_SPLIT, MI_F16, MI_F32, ops
 from sdvk_amd.hip import DeviceBuffer, synchronize
 
 pytestmark = pytest.mark.gpu
@@ -161,12 +161,12 @@ def test_config3_cross_attention(gpu, oracle, heads, T):
     (2, 130, 77, 640, 10, False, [77, 13]),
     (1, 1024, 1024, 1280, 20, False, None),
 ])
-def test_two_and_four_wave_workgroups(gpu, oracle, monkeypatch, nw, B, Tq, Tk, C, heads, causal, kv_len):
+def test_two_and_four_wave_workgroups(gpu, oracle, tune, nw, B, Tq, Tk, C, heads, causal, kv_len):
     """The fp16 kernel's 64-query (2-wave) and 128-query (4-wave) workgroups,
-    pinned with MI_ATTN_NW, each against the oracle (the default rule takes
+    pinned with the attn_nw override, each against the oracle (the default rule takes
     4 waves unless Tq <= 64)."""
     print(f"[case] nw={nw} B={B} Tq={Tq} Tk={Tk} C={C} H={heads} causal={causal} kv_len={kv_len}", flush=True)
-    monkeypatch.setenv("MI_ATTN_NW", nw)
+    tune("attn_nw", nw)
     q = oracle.normal(21, B * Tq * C).astype(np.float16)
     k = oracle.normal(22, B * Tk * C).astype(np.float16)
     v = oracle.normal(23, B * Tk * C).astype(np.float16)
@@ -174,27 +174,32 @@ def test_two_and_four_wave_workgroups(gpu, oracle, monkeypatch, nw, B, Tq, Tk, C
     rows = _sample_rows(Tq, 40, 5) if Tq > 512 else None
     want = oracle.fused_attention_ex(q, k, v, batch=B, Tq=Tq, Tk=Tk, C=C, heads=heads, in_dtype=1, causal=causal,
                                      kv_len=kl, rows=rows, threads=oracle.max_threads())
-    for out_dtype in (MI_F32, MI_F16):
+    for out_dtype, prec in ((MI_F32, MI_ATTN_PREC_AUTO), (MI_F32, MI_ATTN_PREC_FP16), (MI_F16, MI_ATTN_PREC_AUTO)):
         got = run_ex(q, k, v, batch=B, Tq=Tq, Tk=Tk, C=C, heads=heads, in_dtype=MI_F16, out_dtype=out_dtype,
-                     kv_len=kl, causal=causal)
+                     kv_len=kl, causal=causal, precision=prec)
         g = (got[:, rows] if rows is not None else got).astype(np.float64)
         w = want.reshape(g.shape)
         if out_dtype == MI_F32:
-            assert_parity(g, w, what=f"nw={nw}")
+            # fp32 out: the default computes P in two parts (a tenth of the bar); one fp16 P product to the bar
+            tol = REL_RMS_TOL / 10 if prec == MI_ATTN_PREC_AUTO else REL_RMS_TOL
+            assert_parity(g, w, tol=tol, what=f"nw={nw} precision={prec}")
         else:
             bound = REL_RMS_TOL * rms(w) + fp16_half_ulp(w)
             assert np.all(np.abs(g - w) <= bound), f"nw={nw}: fp16 output beyond parity + storage rounding"
 
 
-@pytest.mark.parametrize("B,H,T,Tk,causal,ws", [(1, 20, 1024, 1024, False, False), (2, 10, 4096, 4096, False, True),
-                                                 (1, 8, 1024, 1024, True, False), (2, 4, 300, 77, False, False)])
-def test_precise_mode(gpu, oracle, monkeypatch, B, H, T, Tk, causal, ws):
-    """MI_ATTN_PRECISE: P's fp16 residual as a second PV product on every tile,
-    held to a tenth of the bar (sampled rows against the oracle), through the
-    plain entry, the key-split workspace entry and the fp32 reference-layout
-    entry (batch 1)."""
-    print(f"[case] precise B={B} H={H} T={T} Tk={Tk} causal={causal} ws={ws}", flush=True)
-    monkeypatch.setenv("MI_ATTN_PRECISE", "1")
+@pytest.mark.parametrize("B,H,T,Tk,causal,ws,prec", [(1, 20, 1024, 1024, False, False, MI_ATTN_PREC_AUTO),
+                                                      (1, 20, 1024, 1024, False, False, MI_ATTN_PREC_SPLIT),
+                                                      (2, 10, 4096, 4096, False, True, MI_ATTN_PREC_SPLIT),
+                                                      (1, 8, 1024, 1024, True, False, MI_ATTN_PREC_AUTO),
+                                                      (2, 4, 300, 77, False, False, MI_ATTN_PREC_SPLIT)])
+def test_precise_mode(gpu, oracle, B, H, T, Tk, causal, ws, prec):
+    """MI_ATTN_PREC_SPLIT (and MI_ATTN_PREC_AUTO with fp32 output, which
+    picks it): P's fp16 residual as a second PV product on every tile, held to
+    a tenth of the bar (sampled rows against the oracle), through the plain
+    entry, the key-split workspace entry and the fp32 reference-layout entry
+    (batch 1, whose fp32 output takes the same mode by default)."""
+    print(f"[case] precise B={B} H={H} T={T} Tk={Tk} causal={causal} ws={ws} precision={prec}", flush=True)
     C = H * 64
     q = oracle.normal(21, B * T * C).astype(np.float16)
     k = oracle.normal(22, B * Tk * C).astype(np.float16)
@@ -202,7 +207,7 @@ def test_precise_mode(gpu, oracle, monkeypatch, B, H, T, Tk, causal, ws):
     rows = _sample_rows(T, 40, 7) if T > 512 else np.arange(T, dtype=np.uint32)
     want = oracle.fused_attention_ex(q, k, v, batch=B, Tq=T, Tk=Tk, C=C, heads=H, causal=causal, in_dtype=1,
                                      rows=rows, threads=oracle.max_threads()).astype(np.float64)
-    kw = dict(batch=B, Tq=T, Tk=Tk, C=C, heads=H, causal=causal, in_dtype=MI_F16, out_dtype=MI_F32)
+    kw = dict(batch=B, Tq=T, Tk=Tk, C=C, heads=H, causal=causal, in_dtype=MI_F16, out_dtype=MI_F32, precision=prec)
     dq, dk, dv = (DeviceBuffer.from_array(x) for x in (q, k, v))
     do = DeviceBuffer(B * T * C * 4)
     if ws:
@@ -251,10 +256,10 @@ def test_strided_layouts_and_scale(gpu, oracle):
 
 
 @pytest.mark.parametrize("C,heads", [(128, 2), (80, 2)])
-def test_staged_and_direct_output_stores_agree(gpu, oracle, monkeypatch, C, heads):
+def test_staged_and_direct_output_stores_agree(gpu, oracle, tune, C, heads):
     """Output rows go through LDS (16-byte stores of whole rows) when the rows and head columns are 16-byte
     aligned, else straight from the MFMA layout: both give the same bits, in both kernels (fp16 and fp32
-    inputs), for both output types, with a partial last row block and key padding. MI_ATTN_DIRECT_STORE
+    inputs), for both output types, with a partial last row block and key padding. The attn_direct_store override
     forces the direct stores; an output 8 bytes off 16-byte alignment takes them by itself (fp16)."""
     B, Tq, Tk = 2, 130, 150
     kv_len = np.array([150, 61], dtype=np.int32)
@@ -273,14 +278,14 @@ def test_staged_and_direct_output_stores_agree(gpu, oracle, monkeypatch, C, head
                     continue
                 print(f"[case] C={C} in={in_dtype} out={out_dtype} direct={direct} offset={off}", flush=True)
                 if direct:
-                    monkeypatch.setenv("MI_ATTN_DIRECT_STORE", "1")
+                    tune("attn_direct_store", "1")
                 else:
-                    monkeypatch.delenv("MI_ATTN_DIRECT_STORE", raising=False)
+                    tune("attn_direct_store", None)
                 ops.fused_attention_ex(dq, dk, dv, do.value + off, batch=B, Tq=Tq, Tk=Tk, C=C, heads=heads,
                                        in_dtype=in_dtype, out_dtype=out_dtype, kv_len=dl)
                 synchronize()
                 outs.append(do.download(odt, n, offset=off))
-            monkeypatch.delenv("MI_ATTN_DIRECT_STORE", raising=False)
+            tune("attn_direct_store", None)
             for o in outs[1:]:
                 assert np.array_equal(o.view(np.uint8), outs[0].view(np.uint8)), "staged and direct stores differ"
             want = oracle.fused_attention_ex(q, k, v, batch=B, Tq=Tq, Tk=Tk, C=C, heads=heads,
@@ -293,13 +298,13 @@ def test_staged_and_direct_output_stores_agree(gpu, oracle, monkeypatch, C, head
                 assert_parity(got, want, what="staged store")
 
 
-def test_key_split_workspace_entry(gpu, oracle, monkeypatch):
+def test_key_split_workspace_entry(gpu, oracle, tune):
     """mi_fused_attention_ws: the key-split plan of the last partial round of query blocks (2 x 10 heads x
     4096, 640 blocks against 512 resident: 128 blocks in 2 key ranges, one per CU) against the oracle on
     sampled rows, its repeat bit for bit, and agreement with mi_fused_attention_ex; a workspace below the
     plan's size (and none) runs mi_fused_attention_ex's plan exactly; the 4-range plan of 2 x 9 heads;
     forced plans on small shapes (uneven pieces, partial query block, hd = 40) against the oracle."""
-    monkeypatch.delenv("MI_ATTN_SPLIT", raising=False)
+    tune("attn_split", None)
     B, H, T = 2, 10, 4096
     C = H * 64
     kw = dict(batch=B, Tq=T, Tk=T, C=C, heads=H, in_dtype=MI_F16, out_dtype=MI_F16)
@@ -347,8 +352,8 @@ def test_key_split_workspace_entry(gpu, oracle, monkeypatch):
     for (B, Tq, Tk, C, heads, split, odt) in [(2, 300, 1000, 128, 2, "3:3", MI_F32), (1, 200, 130, 80, 2, "1:2", MI_F32),
                                              (1, 256, 512, 128, 2, "2:4", MI_F16)]:
         print(f"[case] forced split {split} B={B} Tq={Tq} Tk={Tk} C={C} heads={heads}", flush=True)
-        monkeypatch.setenv("MI_ATTN_SPLIT", split)
-        monkeypatch.setenv("MI_ATTN_NW", "4")
+        tune("attn_split", split)
+        tune("attn_nw", "4")
         kw = dict(batch=B, Tq=Tq, Tk=Tk, C=C, heads=heads, in_dtype=MI_F16, out_dtype=odt)
         nws = ops.fused_attention_ws_bytes(**kw)
         assert nws > 0
@@ -365,5 +370,5 @@ def test_key_split_workspace_entry(gpu, oracle, monkeypatch):
             assert_parity(got, want, what=f"forced split {split}")
         else:
             assert np.all(np.abs(got - want) <= REL_RMS_TOL * rms(want) + fp16_half_ulp(want))
-    monkeypatch.delenv("MI_ATTN_SPLIT", raising=False)
-    monkeypatch.delenv("MI_ATTN_NW", raising=False)
+    tune("attn_split", None)
+    tune("attn_nw", None)

@@ -49,7 +49,7 @@ def test_gemm_repeats_bit_for_bit(gpu, oracle, M, N, K):
           flush=True)
 
 
-def test_unsplit_sums_do_not_depend_on_the_tile_build(gpu, oracle, monkeypatch):
+def test_unsplit_sums_do_not_depend_on_the_tile_build(gpu, oracle, tune):
     M, N, K = 700, 520, 640
     A = oracle.normal(5, M * K)
     blocks = q8_weights(oracle, 6, N, K)
@@ -58,7 +58,7 @@ def test_unsplit_sums_do_not_depend_on_the_tile_build(gpu, oracle, monkeypatch):
     dP, dS = DeviceBuffer.from_array(payload), DeviceBuffer.from_array(scales)
     ref = None
     for cfg in ("0", "1", "2", "3", "4", "11", "12", "13", "14", "15"):
-        monkeypatch.setenv("MI_GEMM_CFG", cfg)
+        tune("gemm_cfg", cfg)
         for layout in ("blocks", "split"):
             dC = DeviceBuffer(M * N * 4)
             if layout == "blocks":

@@ -148,11 +148,11 @@ def test_split_unaligned_a_and_odd_lda(gpu, oracle):
 
 @pytest.mark.parametrize("ldc_pad,sc_pad,K,cfg", [(8, 8, 96, ""), (3, 5, 96, ""), (8, 8, 128, ""), (1, 0, 256, ""),
                                                   (8, 8, 128, "5"), (3, 5, 256, "6:2")])
-def test_batch_and_strides(gpu, oracle, monkeypatch, ldc_pad, sc_pad, K, cfg):
+def test_batch_and_strides(gpu, oracle, tune, ldc_pad, sc_pad, K, cfg):
     """Grid z offsets A and C, never W (gemm_nt_q8_v.comp:51-52,87); lda/ldc padding untouched.
     Odd ldc / sC take the scalar epilogue, multiples of 4 the 16-byte one."""
     if cfg:
-        monkeypatch.setenv("MI_GEMM_CFG", cfg)
+        tune("gemm_cfg", cfg)
     M, N, batch = 300, 200, 3
     lda, ldc = K + 4, N + ldc_pad
     sA, sC = M * lda + 16, M * ldc + sc_pad
@@ -215,11 +215,11 @@ def test_rule_k_splits_sampled_rows(gpu, oracle, M, N, K, splits):
 @pytest.mark.parametrize("cfg", ["0", "1", "2", "3", "4", "5", "6", "12", "13", "14", "15", "0:3", "1:2", "2:5",
                                  "3:16", "4:2", "5:2", "6:3", "14:2", "15:3"])
 @pytest.mark.parametrize("M,N,K", [(300, 200, 640), (1030, 130, 256)])
-def test_every_tile_config_and_split_k(gpu, oracle, monkeypatch, cfg, M, N, K):
-    """Forces each tile configuration / K split (MI_GEMM_CFG="<cfg>[:<splits>]";
+def test_every_tile_config_and_split_k(gpu, oracle, tune, cfg, M, N, K):
+    """Forces each tile configuration / K split (gemm_cfg "<cfg>[:<splits>]";
     the splits run through the workspace entries)."""
     print(f"[case] cfg={cfg} M={M} N={N} K={K}", flush=True)
-    monkeypatch.setenv("MI_GEMM_CFG", cfg)
+    tune("gemm_cfg", cfg)
     A = oracle.normal(11, M * K)
     blocks = q8_weights(oracle, 12, N, K)
     bias = oracle.normal(13, N, 0.0, 0.02)

@@ -73,16 +73,16 @@ def test_nn_batch_strides_and_flat_scales(gpu, oracle):
 
 @pytest.mark.parametrize("kernel", ["tiled", "general"])
 @pytest.mark.parametrize("mode", [0, 1])
-def test_nn_tiled_strides_and_k_splits(gpu, oracle, monkeypatch, kernel, mode):
+def test_nn_tiled_strides_and_k_splits(gpu, oracle, tune, kernel, mode):
     """The tiled kernel (K % 64 == 0, lda and sA multiples of 16) with batch /
     leading dimensions, and with K split across workgroups through the
     workspace (64 x 64 x 1024: one tile, four splits summed in order by the
-    reduce pass); MI_NN_KERNEL=general runs the same cases on the untiled
+    reduce pass); the nn_kernel=general override runs the same cases on the untiled
     kernel."""
     if kernel == "general":
-        monkeypatch.setenv("MI_NN_KERNEL", "general")
+        tune("nn_kernel", "general")
     else:
-        monkeypatch.delenv("MI_NN_KERNEL", raising=False)
+        tune("nn_kernel", None)
     M, N, K, batch = 70, 36, 256, 3
     lda, ldb, ldc = 272, 40, 44
     sA, sB, sC = 19056, 10248, 3100

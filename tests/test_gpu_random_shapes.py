@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 from helpers import REL_RMS_TOL, assert_parity, err_vs_rms, fp16_half_ulp, q8_weights, rms
-from sdvk_amd import MI_F16, MI_F32, ops
+from sdvk_amd import MI_ATTN_PREC_AUTO, MI_ATTN_PREC_FP16, MI_F16, MI_F32, ops
 from sdvk_amd.hip import DeviceBuffer, synchronize
 
 pytestmark = pytest.mark.gpu
@@ -103,7 +103,7 @@ def _attn_shapes(n, seed):
 
 
 @pytest.mark.parametrize("B,H,Tq,Tk,hd,causal,masked,split", _attn_shapes(14, 4242))
-def test_random_attention(gpu, oracle, monkeypatch, B, H, Tq, Tk, hd, causal, masked, split):
+def test_random_attention(gpu, oracle, tune, B, H, Tq, Tk, hd, causal, masked, split):
     """fp16 in / fp16 and fp32 out through the workspace entry (a forced key
     split where `split` is set: it applies to unmasked, non-causal, 4-wave
     launches), and the fp32 reference-layout entry for batch 1."""
@@ -111,7 +111,7 @@ def test_random_attention(gpu, oracle, monkeypatch, B, H, Tq, Tk, hd, causal, ma
           f"split={split or '-'}", flush=True)
     C = H * hd
     if split:
-        monkeypatch.setenv("MI_ATTN_SPLIT", split)
+        tune("attn_split", split)
     q = oracle.normal(Tq + 1, B * Tq * C).astype(np.float16)
     k = oracle.normal(Tk + 2, B * Tk * C).astype(np.float16)
     v = oracle.normal(Tk + 3, B * Tk * C).astype(np.float16)
@@ -124,14 +124,18 @@ def test_random_attention(gpu, oracle, monkeypatch, B, H, Tq, Tk, hd, causal, ma
     dq, dk, dv = (DeviceBuffer.from_array(x) for x in (q, k, v))
     dl = DeviceBuffer.from_array(kv_len) if kv_len is not None else None
     kw = dict(batch=B, Tq=Tq, Tk=Tk, C=C, heads=H, causal=causal, in_dtype=MI_F16, kv_len=dl)
-    for odt in (MI_F32, MI_F16):
-        nws = ops.fused_attention_ws_bytes(out_dtype=odt, **kw)
+    # fp32 out: the default (two-part P) to a tenth of the bar, and one fp16 P
+    # product (MI_ATTN_PREC_FP16) to the bar; fp16 out: its default (one product)
+    for odt, prec in ((MI_F32, MI_ATTN_PREC_AUTO), (MI_F32, MI_ATTN_PREC_FP16), (MI_F16, MI_ATTN_PREC_AUTO)):
+        nws = ops.fused_attention_ws_bytes(out_dtype=odt, precision=prec, **kw)
         do = DeviceBuffer(B * Tq * C * (4 if odt == MI_F32 else 2))
-        ops.fused_attention_ws(dq, dk, dv, do, DeviceBuffer(nws) if nws else None, out_dtype=odt, **kw)
+        ops.fused_attention_ws(dq, dk, dv, do, DeviceBuffer(nws) if nws else None, out_dtype=odt, precision=prec,
+                               **kw)
         synchronize()
         if odt == MI_F32:
             got = do.download(np.float32, B * Tq * C).reshape(want.shape).astype(np.float64)
-            assert_parity(got, want, what="random attention fp32 out")
+            tol = REL_RMS_TOL / 10 if prec == MI_ATTN_PREC_AUTO else REL_RMS_TOL
+            assert_parity(got, want, tol=tol, what=f"random attention fp32 out, precision {prec}")
         else:
             got = do.download(np.float16, B * Tq * C).reshape(want.shape).astype(np.float64)
             bound = REL_RMS_TOL * rms(want) + fp16_half_ulp(want)
@@ -144,4 +148,4 @@ def test_random_attention(gpu, oracle, monkeypatch, B, H, Tq, Tk, hd, causal, ma
         synchronize()
         got = do32.download(np.float32, Tq * C).reshape(want.shape).astype(np.float64)
         if not masked:
-            assert_parity(got, want, what="random attention, reference layout")
+            assert_parity(got, want, tol=REL_RMS_TOL / 10, what="random attention, reference layout")

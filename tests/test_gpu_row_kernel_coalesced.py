@@ -1,9 +1,9 @@
 """GPU parity of the candidate Q8_0 GEMM builds that the tile rules do not
 choose until measured faster, against the CPU oracle (the same bar and cases as
 the other tile configurations, tests/test_gpu_gemm.py): the row-stationary
-kernel with row-coalesced A loads and the quad transpose (MI_GEMM_CFG=7..10:
+kernel with row-coalesced A loads and the quad transpose (gemm_cfg 7..10:
 256 x 256 / 192 / 160 / 128 tiles) and the 4-wave 256 x 256 LDS kernel
-(MI_GEMM_CFG=11, one wave per SIMD, no K split), and the 4-wave 256 x 128 and
+(gemm_cfg 11, one wave per SIMD, no K split), and the 4-wave 256 x 128 and
 128 x 256 LDS builds (12, 13: 128 x 64 / 64 x 128 per wave), and the 8-wave
 192 x 256 LDS build (14: 96 x 64 per wave)."""
 import numpy as np
@@ -19,9 +19,9 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("cfg", ["7", "7:2", "8", "9:3", "10", "11", "12", "12:2", "13", "13:3", "14", "14:2"])
 @pytest.mark.parametrize("M,N,K", [(300, 200, 640), (1030, 130, 256), (257, 512, 128)])
-def test_coalesced_rows_config(gpu, oracle, monkeypatch, cfg, M, N, K):
+def test_coalesced_rows_config(gpu, oracle, tune, cfg, M, N, K):
     print(f"[case] cfg={cfg} M={M} N={N} K={K}", flush=True)
-    monkeypatch.setenv("MI_GEMM_CFG", cfg)
+    tune("gemm_cfg", cfg)
     A = oracle.normal(11, M * K)
     blocks = q8_weights(oracle, 12, N, K)
     bias = oracle.normal(13, N, 0.0, 0.02)
@@ -41,10 +41,10 @@ def test_coalesced_rows_config(gpu, oracle, monkeypatch, cfg, M, N, K):
 
 
 @pytest.mark.parametrize("cfg", ["7", "11", "12", "13", "14", "15"])
-def test_candidate_config_baseline_shape(gpu, oracle, monkeypatch, cfg):
+def test_candidate_config_baseline_shape(gpu, oracle, tune, cfg):
     M, N, K = 9216, 1280, 1280
     print(f"[case] cfg={cfg} baseline M={M} N={N} K={K}", flush=True)
-    monkeypatch.setenv("MI_GEMM_CFG", cfg)
+    tune("gemm_cfg", cfg)
     A = oracle.normal(1, M * K)
     blocks = q8_weights(oracle, 2, N, K)
     got = run_q8_0(A, blocks, M, N, K).reshape(M, N)

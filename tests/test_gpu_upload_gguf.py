@@ -87,10 +87,10 @@ def test_large_tensor_streams_through_staging(gpu, oracle, tmp_path):
         assert np.array_equal(bits(ds.download(np.float32, N * K // 32)), bits(scales))
 
 
-def test_file_weight_through_both_gemm_layouts(gpu, oracle, tmp_path, monkeypatch):
+def test_file_weight_through_both_gemm_layouts(gpu, oracle, tmp_path, tune):
     """A Q8_0 linear weight [N, K] read from a GGUF file feeds mi_gemm_nt_q8_0
     as 34-byte blocks and mi_gemm_nt_q8_split as payload + scales."""
-    monkeypatch.setenv("MI_GEMM_CFG", "1")  # one tile config, no K split: both entries sum in the same order
+    tune("gemm_cfg", "1")  # one tile config, no K split: both entries sum in the same order
     M, N, K = 300, 640, 1280
     print(f"[case] gguf weight -> gemm M={M} N={N} K={K}", flush=True)
     blocks = oracle.q8_0_quantize(oracle.normal(6, N * K, 0.0, 0.02))

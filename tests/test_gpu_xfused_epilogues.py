@@ -28,10 +28,10 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("M,N,K,cfg", [(77, 96, 64, None), (130, 257, 320, None), (2048, 1280, 1280, None),
                                        (300, 200, 256, "7:2"), (154, 1280, 5120, None)])
-def test_residual_mode(gpu, oracle, monkeypatch, M, N, K, cfg):
+def test_residual_mode(gpu, oracle, tune, M, N, K, cfg):
     print(f"[case] gemm mode 2 M={M} N={N} K={K} cfg={cfg}", flush=True)
     if cfg:
-        monkeypatch.setenv("MI_GEMM_CFG", cfg)
+        tune("gemm_cfg", cfg)
     A = oracle.normal(1, M * K)
     blocks = q8_weights(oracle, 2, N, K)
     bias = oracle.normal(3, N, 0.0, 0.02)
@@ -49,10 +49,10 @@ def test_residual_mode(gpu, oracle, monkeypatch, M, N, K, cfg):
 
 @pytest.mark.parametrize("M,F,K,cfg", [(77, 48, 64, None), (300, 200, 256, "4"), (130, 100, 96, None),
                                        (2048, 5120, 1280, None), (300, 130, 256, "7"), (300, 130, 256, "15")])
-def test_geglu_gemm(gpu, oracle, monkeypatch, M, F, K, cfg):
+def test_geglu_gemm(gpu, oracle, tune, M, F, K, cfg):
     print(f"[case] gemm geglu M={M} F={F} K={K} cfg={cfg}", flush=True)
     if cfg:
-        monkeypatch.setenv("MI_GEMM_CFG", cfg)
+        tune("gemm_cfg", cfg)
     A = oracle.normal(1, M * K)
     blocks = q8_weights(oracle, 2, 2 * F, K)
     bias = oracle.normal(3, 2 * F, 0.0, 0.5)
@@ -67,7 +67,7 @@ def test_geglu_gemm(gpu, oracle, monkeypatch, M, F, K, cfg):
     d_sep = float(np.max(np.abs(got - sep)) / rms(sep))
     print(f"  fused vs separate = {d_sep:.3e} x RMS", flush=True)
     if cfg:
-        monkeypatch.delenv("MI_GEMM_CFG")
+        tune("gemm_cfg", None)
     h = oracle.gemm_nt_q8_0(A, blocks, M, 2 * F, K, bias=bias, threads=oracle.max_threads()).reshape(M, 2 * F)
     want = oracle.geglu(h, M, F).reshape(M, F)
     v, g = h[:, :F].astype(np.float64), h[:, F:].astype(np.float64)

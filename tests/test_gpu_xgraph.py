@@ -4,7 +4,7 @@ C-ABI launches) and replayed give the eager results.
 The sequence holds a GEMM without K splits, a K-split GEMM (partials in a
 workspace, then the reduce pass), a K-split tiled NN GEMM (the same), a
 key-padded fp16 attention and a key-split fp16 attention (pieces in a
-workspace, then the merge pass; the split forced with MI_ATTN_SPLIT). The graph is replayed three times with eager work
+workspace, then the merge pass; the split forced with the attn_split override). The graph is replayed three times with eager work
 and a synchronisation between the replays; every replay must equal the eager
 results bit for bit (every sum has a fixed order).
 """
@@ -18,7 +18,7 @@ from sdvk_amd.hip import DeviceBuffer
 pytestmark = pytest.mark.gpu
 
 
-def test_graph_replays_match_eager(gpu, oracle, monkeypatch):
+def test_graph_replays_match_eager(gpu, oracle, tune):
     print("[case] graph capture / replay of GEMM, split-K GEMM, NN GEMM, attention", flush=True)
     st = hip.Stream()
     M1, N1, K1 = 2048, 1280, 1280            # no K split
@@ -42,8 +42,8 @@ def test_graph_replays_match_eager(gpu, oracle, monkeypatch):
     ks = DeviceBuffer.from_array(oracle.normal(11, Tks * Hs * 64).astype(np.float16))
     vs = DeviceBuffer.from_array(oracle.normal(12, Tks * Hs * 64).astype(np.float16))
     skw = dict(batch=1, Tq=Ts, Tk=Tks, C=Hs * 64, heads=Hs, in_dtype=MI_F16, out_dtype=MI_F16)
-    monkeypatch.setenv("MI_ATTN_NW", "4")
-    monkeypatch.setenv("MI_ATTN_SPLIT", "2:4")
+    tune("attn_nw", "4")
+    tune("attn_split", "2:4")
     ws4 = DeviceBuffer(ops.fused_attention_ws_bytes(**skw))
     assert ws4.nbytes > 0, "the forced key split has no workspace"
     outs = [DeviceBuffer(M1 * N1 * 4), DeviceBuffer(M2 * N2 * 4), DeviceBuffer(M3 * N3 * 4),

@@ -133,8 +133,10 @@ FAMILIES = {
         dict(batch=2, Tq=300, Tk=1000, C=128, heads=2, f16_in=True, f16_out=False, split="3:3", nw=4),
         dict(Tq=200, Tk=130, C=80, heads=2, f16_in=True, f16_out=False, split="1:2", nw=4),
         dict(Tq=128, Tk=256, C=64, heads=1, f16_in=True, split="1:4", nw=4, outliers=[5, 70, 200]),
-        # MI_ATTN_PRECISE (P's fp16 residual on every tile), held to a tenth of the bar: both kernels,
-        # key padding, causal, a forced key split
+        # MI_ATTN_PREC_SPLIT (P's fp16 residual on every tile), held to a tenth of the bar: both kernels,
+        # key padding, causal, a forced key split; MI_ATTN_PREC_AUTO picks it for fp32 outputs
+        dict(Tq=130, Tk=300, C=128, heads=2, f16_in=True, precision=0, tol=2e-4),
+        dict(Tq=100, Tk=150, C=128, heads=2, causal=True, precision=0, tol=2e-4),
         dict(batch=2, Tq=130, Tk=150, C=128, heads=2, f16_in=True, kv_len=[150, 37], nw=4, precise=True, tol=2e-4),
         dict(Tq=100, Tk=300, C=128, heads=2, f16_in=True, causal=True, nw=2, precise=True, tol=2e-4),
         dict(Tq=70, Tk=130, C=128, heads=2, causal=True, precise=True, tol=2e-4),
