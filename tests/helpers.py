@@ -21,27 +21,29 @@ def rms(x: np.ndarray) -> float:
 WORST: dict[str, tuple[float, float, str]] = {}
 
 
-def record(e: float, tol: float = REL_RMS_TOL) -> float:
-    """Notes an error (relative to its bar `tol`) for the end-of-session summary."""
+def record(e: float, tol: float = REL_RMS_TOL, label: str = "") -> float:
+    """Notes an error (relative to its bar `tol`) for the end-of-session summary;
+    `label` keeps a mode apart from the test function's default path."""
     test = os.environ.get("PYTEST_CURRENT_TEST", "").split(" ")[0]
-    mod = test.rsplit("/", 1)[-1].replace(".py", "").split("[")[0] if test else "?"
+    mod = (test.rsplit("/", 1)[-1].replace(".py", "").split("[")[0] if test else "?") + label
     prev = WORST.get(mod)
     if prev is None or e / tol > prev[0] / prev[1]:
         WORST[mod] = (float(e), float(tol), test)
     return e
 
 
-def err_vs_rms(got: np.ndarray, ref: np.ndarray) -> float:
+def err_vs_rms(got: np.ndarray, ref: np.ndarray, note: bool = True) -> float:
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
     r = rms(ref)
     e = float(np.max(np.abs(got - ref)) / r) if r > 0 else float(np.max(np.abs(got - ref)))
-    return record(e) if np.isfinite(e) else e
+    return record(e) if note and np.isfinite(e) else e
 
 
-def assert_parity(got, ref, tol=REL_RMS_TOL, what=""):
-    e = err_vs_rms(got, ref)
-    record(e, tol)
+def assert_parity(got, ref, tol=REL_RMS_TOL, what="", label=""):
+    e = err_vs_rms(got, ref, note=False)
+    if np.isfinite(e):
+        record(e, tol, label)
     assert np.all(np.isfinite(np.asarray(got, dtype=np.float64))), f"{what}: non-finite output"
     assert e <= tol, f"{what}: max|err| = {e:.3e} x RMS > {tol:.1e}"
     return e

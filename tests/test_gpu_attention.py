@@ -182,7 +182,8 @@ def test_two_and_four_wave_workgroups(gpu, oracle, tune, nw, B, Tq, Tk, C, heads
         if out_dtype == MI_F32:
             # fp32 out: the default computes P in two parts (a tenth of the bar); one fp16 P product to the bar
             tol = REL_RMS_TOL / 10 if prec == MI_ATTN_PREC_AUTO else REL_RMS_TOL
-            assert_parity(g, w, tol=tol, what=f"nw={nw} precision={prec}")
+            assert_parity(g, w, tol=tol, what=f"nw={nw} precision={prec}",
+                          label="" if prec == MI_ATTN_PREC_AUTO else "[precision=fp16]")
         else:
             bound = REL_RMS_TOL * rms(w) + fp16_half_ulp(w)
             assert np.all(np.abs(g - w) <= bound), f"nw={nw}: fp16 output beyond parity + storage rounding"

@@ -135,7 +135,8 @@ def test_random_attention(gpu, oracle, tune, B, H, Tq, Tk, hd, causal, masked, s
         if odt == MI_F32:
             got = do.download(np.float32, B * Tq * C).reshape(want.shape).astype(np.float64)
             tol = REL_RMS_TOL / 10 if prec == MI_ATTN_PREC_AUTO else REL_RMS_TOL
-            assert_parity(got, want, tol=tol, what=f"random attention fp32 out, precision {prec}")
+            assert_parity(got, want, tol=tol, what=f"random attention fp32 out, precision {prec}",
+                          label="" if prec == MI_ATTN_PREC_AUTO else "[precision=fp16]")
         else:
             got = do.download(np.float16, B * Tq * C).reshape(want.shape).astype(np.float64)
             bound = REL_RMS_TOL * rms(want) + fp16_half_ulp(want)
