@@ -309,12 +309,10 @@ def time_case(c, stream, hip, reps):
 
 # Every tile build (mi_tuning_set("gemm_cfg", "<cfg>[:<K splits>]")), timed on every GEMM shape
 # of the step and on config 0, so the tile rules can be re-derived from one run:
-# the LDS kernel's 256x128 / 128x128 / 128x64 / 64x64 / 256x256 tiles (0-4) with
-# and without K splits, the row-stationary builds (5, 6; row-coalesced A 7-10)
-# the 4-wave LDS builds: 256x256 (11), 256x128 (12) and 128x256 (13), the
-# 8-wave 192x256 LDS build (14) and the 192x256 producer / consumer build (15).
-GEMM_CANDIDATES = ["0", "0:2", "0:4", "1", "1:2", "2", "2:2", "3", "3:2", "3:4", "3:8", "4", "4:2", "5", "6",
-                   "7", "8", "9", "10", "11", "12", "12:2", "13", "13:2", "14", "14:2", "15", "15:2"]
+# the LDS kernel's 256x128 / 128x128 / 128x64 / 64x64 / 256x256 / 192x256 tiles
+# (0-5) with and without K splits.
+GEMM_CANDIDATES = ["0", "0:2", "0:4", "1", "1:2", "1:3", "2", "2:2", "3", "3:2", "3:4", "3:8", "4", "4:2", "5",
+                   "5:2"]
 
 
 def _part(out, name, fn):

@@ -23,6 +23,8 @@
 //     applies bias / accumulate. Every plan sums in a fixed order, so a call
 //     repeats bit for bit; entries without a workspace never split K.
 #include <algorithm>
+#include <atomic>
+#include <chrono>
 #include <type_traits>
 #include <cstdlib>
 #include <cstring>
@@ -51,6 +53,16 @@ struct GemmArgs {
     uint32_t bvec;          // bias 16-byte aligned
     uint32_t F;             // GEGLU epilogue: output columns (W has 2F rows: value rows, then gate rows)
     uint64_t split_stride;  // K-split partials: elements between the planes of consecutive splits
+    // K-split launches: C / ldc / sC above address the partial planes; the
+    // workgroup that finishes a tile last adds its planes, in split order,
+    // into the real output (out, ldo, so) with the reduce op of the call.
+    float* out;
+    uint32_t ldo;
+    uint32_t nsplit;
+    uint64_t so;
+    int op;                        // 0: out = sum + bias; 1: out += sum; 2: out += sum + bias
+    unsigned long long* counters;  // arrival counters, one per (batch item, tile)
+    unsigned long long epoch;      // this launch's arrival tag (48 bits, never 0)
 };
 
 // Epilogues. kEpiPlain: the reference's modes (0 stores acc + bias, 1 adds acc
@@ -274,6 +286,69 @@ __device__ __forceinline__ void store_tiles(const GemmArgs& a, float* C, float* 
         }
         // every read of this tile precedes the next tile's writes
         __builtin_amdgcn_wave_barrier();
+    }
+}
+
+// K-split arrival: counter word = (epoch << 16) | workgroups arrived. A word
+// holding another launch's epoch (or anything else) counts as zero arrivals,
+// so the workspace needs no clearing; the last of the nsplit workgroups of a
+// tile returns true and resets the word to 0, which no launch's epoch equals
+// (graph replays that reuse a launch's epoch start from 0 again). The CAS
+// loop ends: every failed attempt means another workgroup's succeeded, and at
+// most nsplit succeed.
+__device__ __forceinline__ bool arrive_last(unsigned long long* c, unsigned long long epoch, uint32_t n) {
+    unsigned long long cur = atomicCAS(c, 0ull, 0ull);  // an atomic read (swaps 0 for 0)
+    for (;;) {
+        const unsigned long long next = (cur >> 16) == epoch ? cur + 1ull : (epoch << 16) | 1ull;
+        const unsigned long long seen = atomicCAS(c, cur, next);
+        if (seen == cur) return (next & 0xffffull) == n;
+        cur = seen;
+    }
+}
+
+// The last workgroup of a K-split tile: adds the tile's partial planes in split
+// order -- ((P0 + P1) + P2) + ..., whichever workgroup arrives last -- and
+// applies the call's op, the arithmetic of splitk_reduce_kernel, so a call
+// repeats bit for bit. Lane positions are those of the partial stores (column
+// l32 of each 32-wide tile, rows 8 (r / 4) + 4 g + r % 4): 32 consecutive
+// floats per load / store instruction.
+template <int FM, int FN>
+__device__ __forceinline__ void split_fixup(const GemmArgs& a, uint32_t mw, uint32_t nw, int lane, int tid,
+                                            int* s_last) {
+    __threadfence();  // this thread's partial stores are visible device-wide ...
+    __syncthreads();  // ... for every thread of the workgroup, before the arrival
+    if (tid == 0) {
+        unsigned long long* c = a.counters + static_cast<uint64_t>(blockIdx.z) * gridDim.x + blockIdx.x;
+        const bool last = arrive_last(c, a.epoch, a.nsplit);
+        if (last) atomicExch(c, 0ull);
+        *s_last = last ? 1 : 0;
+    }
+    __syncthreads();
+    if (!*s_last) return;
+    __threadfence();  // the other splits' partials, after their arrivals
+    const int l32 = lane & 31, g = lane >> 5;
+    const float* P = a.C + static_cast<uint64_t>(blockIdx.z) * a.sC;
+    float* O = a.out + static_cast<uint64_t>(blockIdx.z) * a.so;
+    const bool use_bias = a.op != 1 && a.bias != nullptr;
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) {
+        const uint32_t n = nw + 32 * fn + l32;
+        if (n >= a.N) continue;
+        const float b = use_bias ? a.bias[n] : 0.0f;
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t m = mw + 32 * fm + 8 * (r >> 2) + 4 * g + (r & 3);
+                if (m >= a.M) continue;
+                const float* q = P + static_cast<uint64_t>(m) * a.N + n;
+                float v = q[0];
+                for (uint32_t sp = 1; sp < a.nsplit; ++sp) v += q[sp * a.split_stride];
+                float* o = O + static_cast<uint64_t>(m) * a.ldo + n;
+                if (a.op == 0) *o = use_bias ? v + b : v;
+                else if (a.op == 1) *o = *o + v;
+                else *o = *o + (use_bias ? v + b : v);
+            }
     }
 }
 
@@ -639,576 +714,10 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     store_tiles<FM, FN, SPLITK, EPI>(a, C, reinterpret_cast<float*>(smem) + wave_s * kStageFloats, m0 + wm_s * TM,
                                      EPI == kEpiGeglu ? n0 + wn_s * TN / 2 : n0 + wn_s * TN, acc,
                                      kFreshLane ? lane_id() : lane);
-}
-
-// ---- row-stationary kernel --------------------------------------------------------
-//
-// One workgroup = 4 waves, one per SIMD, stacked in M: wave w owns rows
-// [64w, 64w + 64) of a 256 x BN tile (BN = 32 * FN) and keeps its 2 x FN
-// 32x32 fp32 accumulators (256 registers at FN = 8) for the whole K sweep.
-//
-//   * A never touches LDS. A lane loads the fp32 values of its own MFMA
-//     operand straight into registers and rounds them to fp16 there. K is
-//     permuted inside each 32-wide step (operand slot (slice s, half g) holds
-//     k = 16 g + 8 s .. + 8, applied to both operands), so a lane's 16 values
-//     of a step are contiguous: four 16-byte loads per 32 rows, and the two
-//     halves of a wave cover one 128-byte line per row.
-//   * W is read once per workgroup: thread t dequantises column n0 + t's
-//     Q8_0 block of the step (a 36-byte window, three loads) into LDS row t,
-//     where the four waves read their operand fragments (rows >= BN are
-//     staged but never read, so the loop has no thread-dependent branch).
-//   * Steps alternate between two register sets and two LDS stages by the
-//     parity of the step, so the raw loads of step j + 2 are in flight while
-//     step j's MFMAs run and step j + 1 is dequantised / converted; one
-//     barrier per step.
-// 4 x 4 transpose of dwords across the four lanes of each quad: lane j's
-// register k becomes lane k's register j (two DPP quad-permute rounds: swap
-// across lane bit 1 / register bit 1, then across lane bit 0 / register bit 0).
-__device__ __forceinline__ void quad_transpose4(uint32_t (&e)[4], int lane) {
-    const bool b1 = (lane & 2) != 0, b0 = (lane & 1) != 0;
-    uint32_t r[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        // quad_perm [2,3,0,1]: lane j reads lane j ^ 2's register k ^ 2
-        const uint32_t x = static_cast<uint32_t>(
-            __builtin_amdgcn_mov_dpp(static_cast<int>(e[k ^ 2]), 0x4E, 0xF, 0xF, false));
-        r[k] = (b1 == ((k & 2) != 0)) ? e[k] : x;
+    if constexpr (SPLITK) {
+        __shared__ int s_last;
+        split_fixup<FM, FN>(a, m0 + wm_s * TM, n0 + wn_s * TN, kFreshLane ? lane_id() : lane, tid, &s_last);
     }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        // quad_perm [1,0,3,2]: lane j reads lane j ^ 1's register k ^ 1
-        const uint32_t x = static_cast<uint32_t>(
-            __builtin_amdgcn_mov_dpp(static_cast<int>(r[k ^ 1]), 0xB1, 0xF, 0xF, false));
-        e[k] = (b0 == ((k & 1) != 0)) ? r[k] : x;
-    }
-}
-
-// AQ = false: a lane loads its own MFMA operand row (16-byte loads touching 64
-//   rows per instruction).
-// AQ = true: row-coalesced A. Load k (0..3) of a 32-row half gives lane 4Q + j
-//   row 4 (Q % 8) + k, 16-byte chunk 4 (Q / 8) + j of the step, so each
-//   instruction reads 8 whole 128-byte rows; a 4 x 4 quad transpose (after the
-//   fp16 conversion) then leaves lane l holding chunks 4 g .. 4 g + 3 of row
-//   l % 32 -- the same operand layout as AQ = false, so W, the MFMAs and the
-//   epilogue are shared.
-template <int FN, int WK, bool SPLITK, bool AQ = false, int EPI = kEpiPlain>
-__global__ __launch_bounds__(256) void gemm_q8_rows_kernel(GemmArgs a) {
-    constexpr int BM = 256, BN = 32 * FN, FM = 2, LDW = 40;  // LDW: 32 halves + 16-byte pad per column
-    // every thread stages one W column (threads t >= BN a clamped column into
-    // LDS rows no wave reads), so the K loop has no thread-dependent branch
-    constexpr int kOperandHalves = 2 * 256 * LDW;
-    constexpr int kStageHalves = 2 * 4 * kStageFloats;
-    __shared__ __attribute__((aligned(16))) _Float16 smem[kOperandHalves > kStageHalves ? kOperandHalves : kStageHalves];
-    auto Ws = reinterpret_cast<_Float16 (*)[256 * LDW]>(smem);
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int l32 = lane & 31, g = lane >> 5;
-
-    const unsigned lin = xcd_swizzle(blockIdx.x, gridDim.x);
-    const uint32_t gsz = a.group_m * a.tiles_n;
-    const uint32_t grp = lin / gsz, rem = lin % gsz;
-    const uint32_t rows_in = min(a.group_m, a.tiles_m - grp * a.group_m);
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane((grp * a.group_m + rem % rows_in) * BM);
-    // GEGLU: n0 is the tile's first output column (BN / 2 outputs per tile)
-    const uint32_t n0 = __builtin_amdgcn_readfirstlane((rem / rows_in) * (EPI == kEpiGeglu ? BN / 2 : BN));
-    // split K: steps_per_split is even, so a split starts on an even step and
-    // step parity = register set = LDS stage
-    const uint32_t s_begin = SPLITK ? blockIdx.y * a.steps_per_split : 0;
-    const uint32_t s_end = SPLITK ? min(a.ksteps, s_begin + a.steps_per_split) : a.ksteps;
-
-    const float* Apanel = a.A + static_cast<uint64_t>(blockIdx.z) * a.sA + static_cast<uint64_t>(m0) * a.lda;
-    // the range covers exactly the panel's rows: a read past them returns zeros, never faults
-    const uint32_t a_bytes = ((min(a.M - m0, static_cast<uint32_t>(BM)) - 1) * a.lda + a.K) * 4;
-    const __amdgpu_buffer_rsrc_t rA =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Apanel), 0, static_cast<int>(a_bytes), 0x00020000);
-    const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t*>(a.W), 0, WK == kBlocks34 ? static_cast<int>((a.N * a.rowbytes + 15u) & ~15u) : -1,
-        0x00020000);
-    const __amdgpu_buffer_rsrc_t rS =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(WK == kSplit ? a.scales : a.A), 0, -1, 0x00020000);
-
-    // A: rows past M read row M - 1 (their outputs are never stored)
-    uint32_t a_off[FM][AQ ? 4 : 1];
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm) {
-        if constexpr (AQ) {
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const uint32_t row = min(m0 + 64 * wave + 32 * fm + 4 * ((lane >> 2) & 7) + k, a.M - 1) - m0;
-                a_off[fm][k] = (row * a.lda + 16 * g + 4 * (lane & 3)) * 4;
-            }
-        } else {
-            const uint32_t row = min(m0 + 64 * wave + 32 * fm + l32, a.M - 1) - m0;
-            a_off[fm][0] = (row * a.lda + 16 * g) * 4;
-        }
-    }
-    // W: column n0 + tid (clamped to N - 1). 34-byte layout: the block of step ks
-    // starts at byte wb + 34 ks; even steps read the window at
-    // (wb & ~3) + 68 (ks / 2), odd steps at ((wb + 34) & ~3) + 68 (ks / 2), and
-    // the block sits 0 or 2 bytes into its window (v_perm selectors per parity).
-    const uint32_t wn = EPI == kEpiGeglu ? geglu_wrow(n0, min(static_cast<uint32_t>(tid), BN - 1u), a.F)
-                                         : min(n0 + static_cast<uint32_t>(tid), a.N - 1);
-    uint32_t w_vo[2], w_qsel[2], w_dsel[2];
-    if constexpr (WK == kBlocks34) {
-        const uint32_t wb = wn * a.rowbytes;
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            const uint32_t byte = wb + 34u * p;
-            w_vo[p] = byte & ~3u;
-            w_qsel[p] = (byte & 2u) ? 0x07060504u : 0x05040302u;
-            w_dsel[p] = (byte & 2u) ? 0x0c0c0302u : 0x0c0c0100u;
-        }
-    } else {
-        // split layout: payload byte wn*K + 32 ks, scale float (wn*K)/32 + ks
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            w_vo[p] = wn * a.K + 32u * p;
-            w_qsel[p] = (wn * a.K / 32u + p) * 4u;
-            w_dsel[p] = 0;
-        }
-    }
-
-    floatx4 ar[2][FM][4];   // raw A of a step, per parity
-    uint32_t wx[2][9];      // raw W of a step, per parity
-
-    auto load = [&](uint32_t ks_in, auto P) {
-        constexpr int p = decltype(P)::value;
-        const uint32_t ks = __builtin_amdgcn_readfirstlane(ks_in);
-#pragma unroll
-        for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-                ar[p][fm][q] = __builtin_bit_cast(
-                    floatx4, __builtin_amdgcn_raw_buffer_load_b128(rA, AQ ? a_off[fm][q] : a_off[fm][0] + 16 * q,
-                                                                    ks * 128, 0));
-        {
-            if constexpr (WK == kBlocks34) {
-                const uint32_t so = 68u * (ks >> 1);
-                const auto x0 = __builtin_amdgcn_raw_buffer_load_b128(rW, w_vo[p], so, 0);
-                const auto x1 = __builtin_amdgcn_raw_buffer_load_b128(rW, w_vo[p] + 16, so, 0);
-                wx[p][8] = __builtin_amdgcn_raw_buffer_load_b32(rW, w_vo[p] + 32, so, 0);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    wx[p][e] = x0[e];
-                    wx[p][4 + e] = x1[e];
-                }
-            } else {
-                const uint32_t so = 64u * (ks >> 1);
-                const auto x0 = __builtin_amdgcn_raw_buffer_load_b128(rW, w_vo[p], so, 0);
-                const auto x1 = __builtin_amdgcn_raw_buffer_load_b128(rW, w_vo[p] + 16, so, 0);
-                wx[p][8] = __builtin_amdgcn_raw_buffer_load_b32(rS, w_qsel[p], 8u * (ks >> 1), 0);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    wx[p][e] = x0[e];
-                    wx[p][4 + e] = x1[e];
-                }
-            }
-        }
-    };
-    // dequantise the W block of set p into LDS stage p
-    auto store_w = [&](auto P) {
-        constexpr int p = decltype(P)::value;
-        _Float16* dst = &Ws[p][tid * LDW];
-        if constexpr (WK == kBlocks34) {
-            const uint32_t* x = wx[p];
-            const _Float16 d = __builtin_bit_cast(
-                _Float16, static_cast<uint16_t>(__builtin_amdgcn_perm(x[0], x[0], w_dsel[p])));
-            uint32_t q[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) q[j] = __builtin_amdgcn_perm(x[j + 1], x[j], w_qsel[p]);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) *reinterpret_cast<half8*>(dst + 8 * j) = dequant8_f16(q[2 * j], q[2 * j + 1], d);
-        } else {
-            const float s = __builtin_bit_cast(float, wx[p][8]);
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                *reinterpret_cast<half8*>(dst + 8 * j) = dequant8_f32(wx[p][2 * j], wx[p][2 * j + 1], s, s);
-        }
-    };
-    half8 af[2][FM][2];     // fp16 A operands of a step, per parity: [fm][slice]
-    auto cvt_a = [&](auto P) {
-        constexpr int p = decltype(P)::value;
-#pragma unroll
-        for (int fm = 0; fm < FM; ++fm) {
-            if constexpr (AQ) {
-                // fp16 pairs of the four loads, then the quad transpose of each dword
-                uint32_t d0[4], d1[4];
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const floatx4 v = ar[p][fm][k];
-                    d0[k] = __builtin_bit_cast(uint32_t, half2{static_cast<_Float16>(v[0]), static_cast<_Float16>(v[1])});
-                    d1[k] = __builtin_bit_cast(uint32_t, half2{static_cast<_Float16>(v[2]), static_cast<_Float16>(v[3])});
-                }
-                quad_transpose4(d0, lane);
-                quad_transpose4(d1, lane);
-#pragma unroll
-                for (int s = 0; s < 2; ++s) {
-                    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-                    af[p][fm][s] = __builtin_bit_cast(half8, u32x4{d0[2 * s], d1[2 * s], d0[2 * s + 1], d1[2 * s + 1]});
-                    asm volatile("" : "+v"(af[p][fm][s]));
-                }
-                continue;
-            }
-#pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                const floatx4 lo = ar[p][fm][2 * s], hi = ar[p][fm][2 * s + 1];
-                af[p][fm][s] = half8{static_cast<_Float16>(lo[0]), static_cast<_Float16>(lo[1]),
-                                     static_cast<_Float16>(lo[2]), static_cast<_Float16>(lo[3]),
-                                     static_cast<_Float16>(hi[0]), static_cast<_Float16>(hi[1]),
-                                     static_cast<_Float16>(hi[2]), static_cast<_Float16>(hi[3])};
-                // materialise the operand here: the raw registers must be free
-                // before the loads that refill them are issued
-                asm volatile("" : "+v"(af[p][fm][s]));
-            }
-        }
-    };
-
-    floatx16 acc[FM][FN];
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-    using P0 = std::integral_constant<int, 0>;
-    using P1 = std::integral_constant<int, 1>;
-
-    auto mfma1 = [&](auto P, int s, int fn, const half8& w) {
-        constexpr int p = decltype(P)::value;
-#pragma unroll
-        for (int fm = 0; fm < FM; ++fm)
-            if constexpr (SPLITK)
-                acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[p][fm][s], w, acc[fm][fn], 0, 0, 0);
-            else
-                acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w, af[p][fm][s], acc[fm][fn], 0, 0, 0);
-    };
-    auto read1 = [&](auto P, int s, int fn) {
-        constexpr int p = decltype(P)::value;
-        return *reinterpret_cast<const half8*>(&Ws[p][(32 * fn + l32) * LDW + 16 * g + 8 * s]);
-    };
-
-    // W fragments in flight: one slice (FN x 16 bytes per lane). A step with
-    // operand set P (LDS stage P, A operands af[P]) enters with slice 0 of
-    // stage P in wf and runs three scheduling regions:
-    //   A: slice 0's MFMAs; each column fragment is re-read for slice 1 once
-    //      its MFMAs are issued; meanwhile the other set Q (step + 1) is
-    //      dequantised into stage Q and its A values converted;
-    //   B: set Q's loads for step + 3 (behind a fence: never hoisted above the
-    //      last use of the registers they refill) and slice 1's MFMAs but the
-    //      last two columns;
-    //   barrier (stage Q complete, stage P no longer read), then C: the last
-    //      two columns' MFMAs overlap the reads of slice 0 of stage Q.
-    constexpr int kTail = FN >= 4 ? 2 : 1;
-    constexpr int kValu = 8 * FM + (WK == kBlocks34 ? 60 : 40);
-    constexpr int kVmem = 4 * FM + 3;
-    half8 wf[FN];
-    auto step = [&](auto P, auto Q, uint32_t ks_next3) {
-#pragma unroll
-        for (int fn = 0; fn < FN; ++fn) {
-            mfma1(P, 0, fn, wf[fn]);
-            wf[fn] = read1(P, 1, fn);
-        }
-        store_w(Q);
-        cvt_a(Q);
-#pragma unroll
-        for (int i = 0; i < FN; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, FM, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, (kValu + FN - 1) / FN, 0);
-            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        load(ks_next3, Q);
-#pragma unroll
-        for (int fn = 0; fn < FN - kTail; ++fn) mfma1(P, 1, fn, wf[fn]);
-#pragma unroll
-        for (int i = 0; i < FN - kTail; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, FM, 0);
-            __builtin_amdgcn_sched_group_barrier(0x020, (kVmem + FN - kTail - 1) / (FN - kTail), 0);
-        }
-        __syncthreads();
-#pragma unroll
-        for (int fn = 0; fn < FN - kTail; ++fn) wf[fn] = read1(Q, 0, fn);
-#pragma unroll
-        for (int fn = FN - kTail; fn < FN; ++fn) {
-            mfma1(P, 1, fn, wf[fn]);
-            wf[fn] = read1(Q, 0, fn);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-    };
-
-    const uint32_t n_steps = s_end - s_begin;
-    const uint32_t last = s_end - 1;
-    if (n_steps > 0) {
-        load(s_begin, P0{});
-        load(min(s_begin + 1, last), P1{});
-        store_w(P0{});
-        cvt_a(P0{});
-        load(min(s_begin + 2, last), P0{});
-    }
-    __syncthreads();
-#pragma unroll
-    for (int fn = 0; fn < FN; ++fn) wf[fn] = read1(P0{}, 0, fn);
-    uint32_t j = 0;
-    for (; j + 2 <= n_steps; j += 2) {
-        const uint32_t ks = s_begin + j;
-        step(P0{}, P1{}, min(ks + 3, last));
-        step(P1{}, P0{}, min(ks + 4, last));
-    }
-    if (j < n_steps) {
-#pragma unroll
-        for (int fn = 0; fn < FN; ++fn) {
-            mfma1(P0{}, 0, fn, wf[fn]);
-            wf[fn] = read1(P0{}, 1, fn);
-        }
-#pragma unroll
-        for (int fn = 0; fn < FN; ++fn) mfma1(P0{}, 1, fn, wf[fn]);
-    }
-
-    float* C = a.C + static_cast<uint64_t>(blockIdx.z) * a.sC + (SPLITK ? blockIdx.y * a.split_stride : 0);
-    __syncthreads();  // every wave is done with the W tiles before LDS is reused
-    store_tiles<FM, FN, SPLITK, EPI>(a, C, reinterpret_cast<float*>(smem) + wave * kStageFloats, m0 + 64 * wave, n0,
-                                     acc, lane);
-}
-
-// ---- producer / consumer kernel -------------------------------------------------------
-//
-// One workgroup = 8 waves, two per SIMD, for a 192 x 256 tile (BM x BN), one
-// Q8_0 block (32 k) per step:
-//   * waves 4-7 (producers) only move data: each of their 256 threads keeps
-//     three register sets of raw loads in flight (A: six 16-byte pieces, W:
-//     one whole block, 36-byte window) and, one step at a time, rounds A to
-//     fp16 and dequantises its W block into an LDS stage;
-//   * waves 0-3 (consumers, 2 x 2, 96 x 128 each) only read fragments and
-//     issue v_mfma_f32_32x32x16_f16 (3 x 4 accumulator tiles per wave).
-// Two waves share each SIMD, so the producers' VALU work and memory waits
-// overlap the consumers' MFMAs in hardware instead of in one instruction
-// stream. Three LDS stages: step t lives in stage t % 3, written by the
-// producers two steps ahead of its use, so the consumers read the first
-// fragments of step t + 1 before the barrier that ends step t (stage
-// (t + 1) % 3 was complete one barrier earlier). One barrier per step; both
-// roles pass the same number of barriers. The sums run over k16 slices in
-// the same order as every other build, so an unsplit call gives the same bits.
-template <int WK, bool SPLITK, int EPI = kEpiPlain>
-__global__ __launch_bounds__(512) void gemm_q8_pc_kernel(GemmArgs a) {
-    constexpr int BM = 192, BN = 256, BK = 32, LDK = 40;  // LDS row stride in halves (32 k + 16-byte pad)
-    constexpr int WMC = 96, WNC = 128, FM = 3, FN = 4;   // consumer wave tile, 32x32 MFMA tiles per wave
-    constexpr int NP = 256;                              // producer threads
-    constexpr int A_IT = BM * BK / 4 / NP;               // 16-byte A pieces per producer thread and step (6)
-    constexpr int kStage = (BM + BN) * LDK;              // halves per LDS stage
-    constexpr int kOperandHalves = 3 * kStage;
-    constexpr int kStageHalves = 2 * 4 * kStageFloats;   // epilogue staging of the 4 consumer waves
-    static_assert(BN == NP, "one W block per producer thread and step");
-    __shared__ __attribute__((aligned(16))) _Float16 smem[kOperandHalves > kStageHalves ? kOperandHalves : kStageHalves];
-
-    const int tid = threadIdx.x;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int lane = tid & 63;
-
-    const unsigned lin = xcd_swizzle(blockIdx.x, gridDim.x);
-    const uint32_t gsz = a.group_m * a.tiles_n;
-    const uint32_t grp = lin / gsz, rem = lin % gsz;
-    const uint32_t rows_in = min(a.group_m, a.tiles_m - grp * a.group_m);
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane((grp * a.group_m + rem % rows_in) * BM);
-    const uint32_t n0 = __builtin_amdgcn_readfirstlane((rem / rows_in) * (EPI == kEpiGeglu ? BN / 2 : BN));
-    const uint32_t s_begin = SPLITK ? blockIdx.y * a.steps_per_split : 0;
-    const uint32_t s_end = SPLITK ? min(a.ksteps, s_begin + a.steps_per_split) : a.ksteps;
-    const uint32_t n_steps = s_end - s_begin;  // >= 1
-
-    if (wave >= 4) {
-        // ---------------- producers ----------------
-        const int pt = tid - 256;  // 0..255
-        const float* Apanel = a.A + static_cast<uint64_t>(blockIdx.z) * a.sA + static_cast<uint64_t>(m0) * a.lda;
-        const uint32_t a_bytes = ((min(a.M - m0, static_cast<uint32_t>(BM)) - 1) * a.lda + a.K) * 4;
-        const __amdgpu_buffer_rsrc_t rA =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Apanel), 0, static_cast<int>(a_bytes), 0x00020000);
-        const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint8_t*>(a.W), 0, WK == kBlocks34 ? static_cast<int>((a.N * a.rowbytes + 15u) & ~15u) : -1,
-            0x00020000);
-        const __amdgpu_buffer_rsrc_t rS =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(WK == kSplit ? a.scales : a.A), 0, -1, 0x00020000);
-        // A piece i of a step: row (pt + 256 i) / 8, 16-byte chunk (pt + 256 i) % 8
-        uint32_t a_off[A_IT];
-#pragma unroll
-        for (int i = 0; i < A_IT; ++i) {
-            const int u = pt + NP * i;
-            const uint32_t row = min(m0 + u / 8, a.M - 1) - m0;
-            a_off[i] = (row * a.lda + (u % 8) * 4) * 4;
-        }
-        // W: column n0 + pt (GEGLU: value / gate rows interleaved per 32 columns)
-        const uint32_t wn = EPI == kEpiGeglu ? geglu_wrow(n0, pt, a.F) : min(n0 + static_cast<uint32_t>(pt), a.N - 1);
-        // 34-byte layout: block of step ks at byte wn * rowbytes + 34 ks; the 36-byte window starts at its
-        // 4-byte-aligned floor and the block sits 0 or 2 bytes into it (v_perm selectors per step)
-        const uint32_t wrow = WK == kBlocks34 ? wn * a.rowbytes : wn * a.K;
-
-        floatx4 ar[3][A_IT];
-        uint32_t wx[3][9];
-        auto load = [&](uint32_t ks_in, auto R) {
-            constexpr int r = decltype(R)::value;
-            const uint32_t ks = __builtin_amdgcn_readfirstlane(ks_in);
-#pragma unroll
-            for (int i = 0; i < A_IT; ++i)
-                ar[r][i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rA, a_off[i], ks * BK * 4, 0));
-            if constexpr (WK == kBlocks34) {
-                const uint32_t w0 = (wrow + 34u * ks) & ~3u;
-                const auto x0 = __builtin_amdgcn_raw_buffer_load_b128(rW, w0, 0, 0);
-                const auto x1 = __builtin_amdgcn_raw_buffer_load_b128(rW, w0 + 16, 0, 0);
-                wx[r][8] = __builtin_amdgcn_raw_buffer_load_b32(rW, w0 + 32, 0, 0);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    wx[r][e] = x0[e];
-                    wx[r][4 + e] = x1[e];
-                }
-            } else {
-                const uint32_t w0 = wrow + 32u * ks;
-                const auto x0 = __builtin_amdgcn_raw_buffer_load_b128(rW, w0, 0, 0);
-                const auto x1 = __builtin_amdgcn_raw_buffer_load_b128(rW, w0 + 16, 0, 0);
-                wx[r][8] = __builtin_amdgcn_raw_buffer_load_b32(rS, (w0 >> 5) * 4, 0, 0);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    wx[r][e] = x0[e];
-                    wx[r][4 + e] = x1[e];
-                }
-            }
-        };
-        auto store = [&](uint32_t ks, auto R) {
-            constexpr int r = decltype(R)::value;  // register set = LDS stage
-            _Float16* As = smem + r * kStage;
-            _Float16* Ws = As + BM * LDK;
-#pragma unroll
-            for (int i = 0; i < A_IT; ++i) {
-                const int u = pt + NP * i;
-                half4 h;
-                h[0] = static_cast<_Float16>(ar[r][i][0]);
-                h[1] = static_cast<_Float16>(ar[r][i][1]);
-                h[2] = static_cast<_Float16>(ar[r][i][2]);
-                h[3] = static_cast<_Float16>(ar[r][i][3]);
-                *reinterpret_cast<half4*>(&As[(u / 8) * LDK + (u % 8) * 4]) = h;
-            }
-            const uint32_t* x = wx[r];
-            _Float16* dst = &Ws[pt * LDK];
-            if constexpr (WK == kBlocks34) {
-                const bool sh = ((wrow + 34u * ks) & 2u) != 0;
-                const uint32_t qsel = sh ? 0x07060504u : 0x05040302u;  // bytes 4..7 or 2..5 of (x[j+1]:x[j])
-                const uint32_t dsel = sh ? 0x0c0c0302u : 0x0c0c0100u;  // bytes 2,3 or 0,1 of x[0]; 0x0c = zero
-                const _Float16 d = __builtin_bit_cast(_Float16, static_cast<uint16_t>(__builtin_amdgcn_perm(x[0], x[0], dsel)));
-                uint32_t q[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) q[j] = __builtin_amdgcn_perm(x[j + 1], x[j], qsel);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) *reinterpret_cast<half8*>(dst + 8 * j) = dequant8_f16(q[2 * j], q[2 * j + 1], d);
-            } else {
-                const float sc = __builtin_bit_cast(float, x[8]);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) *reinterpret_cast<half8*>(dst + 8 * j) = dequant8_f32(x[2 * j], x[2 * j + 1], sc, sc);
-            }
-        };
-        using R0 = std::integral_constant<int, 0>;
-        using R1 = std::integral_constant<int, 1>;
-        using R2 = std::integral_constant<int, 2>;
-        const uint32_t last = s_end - 1;
-        auto ph = [&](uint32_t t) { return min(s_begin + t, last); };  // clamped step (loads past the end re-read it)
-        // A step's work stays between its barriers (sched_barrier): left free, the compiler moves the
-        // conversions of later register sets up across the barriers, and the waits for their loads
-        // then take the prefetch lead away.
-        auto barrier = [] {
-            __builtin_amdgcn_sched_barrier(0);
-            __syncthreads();
-            __builtin_amdgcn_sched_barrier(0);
-        };
-        // Each step first consumes its register set completely (the oldest loads in flight, so the
-        // in-order vmcnt wait retires only them), then refills it: a refill hoisted above the
-        // consumption makes the wait retire the newer sets' loads as well.
-        auto step = [&](uint32_t t_store, uint32_t t_load, auto R) {
-            store(t_store, R);
-            __builtin_amdgcn_sched_barrier(0);
-            load(t_load, R);
-        };
-        load(ph(0), R0{});
-        load(ph(1), R1{});
-        load(ph(2), R2{});
-        step(ph(0), ph(3), R0{});
-        __builtin_amdgcn_sched_barrier(0);
-        step(ph(1), ph(4), R1{});
-        barrier();
-        // iteration j converts step j + 2 into stage (j + 2) % 3 (harmless past the end: that stage is
-        // never read again) and refills its register set with step j + 5
-        uint32_t j = 0;
-        for (; j + 3 <= n_steps; j += 3) {
-            step(ph(j + 2), ph(j + 5), R2{});
-            barrier();
-            step(ph(j + 3), ph(j + 6), R0{});
-            barrier();
-            step(ph(j + 4), ph(j + 7), R1{});
-            barrier();
-        }
-        // the last one or two steps were stored by earlier iterations: only the barriers remain
-        for (; j < n_steps; ++j) __syncthreads();
-        return;
-    }
-
-    // ---------------- consumers ----------------
-    const int wm = wave & 1, wn = wave >> 1;
-    const int l32 = lane & 31, g = lane >> 5;
-    floatx16 acc[FM][FN];
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int jn = 0; jn < FN; ++jn)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][jn][r] = 0.0f;
-
-    half8 fa[2][FM], fb[2][FN];  // fragments of a k16 slice: [slice parity]
-    auto read = [&](int stage, int s, int p) {
-        const _Float16* As = smem + stage * kStage;
-        const _Float16* Ws = As + BM * LDK;
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-            fa[p][i] = *reinterpret_cast<const half8*>(&As[(wm * WMC + 32 * i + l32) * LDK + 16 * s + 8 * g]);
-#pragma unroll
-        for (int jn = 0; jn < FN; ++jn)
-            fb[p][jn] = *reinterpret_cast<const half8*>(&Ws[(wn * WNC + 32 * jn + l32) * LDK + 16 * s + 8 * g]);
-    };
-    auto mfma = [&](int p) {
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int jn = 0; jn < FN; ++jn)
-                if constexpr (SPLITK)
-                    acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[p][i], fb[p][jn], acc[i][jn], 0, 0, 0);
-                else
-                    acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[p][jn], fa[p][i], acc[i][jn], 0, 0, 0);
-    };
-    __syncthreads();
-    read(0, 0, 0);
-    int st = 0;
-    for (uint32_t j = 0; j < n_steps; ++j) {
-        const int nx = st == 2 ? 0 : st + 1;
-        read(st, 1, 1);
-        mfma(0);
-        // step j + 1 was stored one barrier ago: its first slice is read before this step's barrier
-        // (after the last step this reads a stage no producer writes any more; the values go unused)
-        read(nx, 0, 0);
-        mfma(1);
-        // slice 0's MFMAs carry slice 1's fragment reads, slice 1's MFMAs the next step's slice 0
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int i = 0; i < FM * FN; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                if (i < FM + FN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            }
-        __builtin_amdgcn_sched_barrier(0);  // every MFMA of the step is issued before the barrier
-        __syncthreads();
-        st = nx;
-    }
-
-    float* C = a.C + static_cast<uint64_t>(blockIdx.z) * a.sC + (SPLITK ? blockIdx.y * a.split_stride : 0);
-    // the producers' last LDS writes precede the loop's last barrier: the staging area is free
-    store_tiles<FM, FN, SPLITK, EPI>(a, C, reinterpret_cast<float*>(smem) + wave * kStageFloats, m0 + wm * WMC,
-                                     EPI == kEpiGeglu ? n0 + wn * WNC / 2 : n0 + wn * WNC, acc, lane);
 }
 
 // K == 0: C[m, n] = bias[n] (or 0) in mode 0, C[m, n] += bias[n] in mode 2.
@@ -1303,16 +812,12 @@ namespace {
 
 // ---- configurations -------------------------------------------------------------
 
-// Tile shapes (BM x BN, waves WM x WN, two 32-wide K blocks per step). The
-// 256x256 tile keeps one register set in flight (PF = 1) to stay within 256 VGPRs.
+// Tile shapes (BM x BN, waves WM x WN, two 32-wide K blocks per step) of the
+// LDS kernel (gemm_q8_kernel). The 256x256 tile keeps one register set in
+// flight (PF = 1) to stay within 256 VGPRs.
 enum CfgId {
-    kC256x128 = 0, kC128x128, kC128x64, kC64x64, kC256x256,  // LDS kernel (gemm_q8_kernel)
-    kR256x256, kR256x128,                                     // row kernel, per-lane-row A loads
-    kR256x256Q, kR256x192Q, kR256x160Q, kR256x128Q,           // row kernel, row-coalesced A
-    kC256x256W4,                                              // LDS kernel, 4 waves of 128x128, one set in flight
-    kC256x128W4, kC128x256W4,                                 // LDS kernel, 4 waves of 128x64 / 64x128
-    kC192x256,                                                // LDS kernel, 8 waves of 96x64
-    kP192x256,                                                // producer / consumer kernel
+    kC256x128 = 0, kC128x128, kC128x64, kC64x64, kC256x256,  // 8 / 4 / 4 / 4 / 8 waves
+    kC192x256,                                                // 8 waves of 96x64
     kNumCfg
 };
 static_assert(kNumCfg == kGemmBuilds, "mi_tuning_set bounds gemm_cfg by kGemmBuilds");
@@ -1367,22 +872,47 @@ uint32_t pick_group(uint32_t tm, uint32_t tn, uint32_t BM, uint32_t BN, uint32_t
     return best;
 }
 
-// The partial planes of a K split: the kernel's C becomes the workspace
-// (row stride N, split planes M * N apart, batch items splits planes apart).
-GemmArgs partial_args(const GemmArgs& a, uint32_t splits, float* ws) {
+// Workspace of a K split: the partial planes (batch * splits * M * N floats,
+// rounded up to 256 bytes), then one 8-byte arrival counter per (batch item,
+// tile) for the smallest tile (64 x 64), which bounds every build's count.
+uint64_t split_plane_bytes(uint32_t M, uint32_t N, uint32_t batch, uint32_t splits) {
+    return (static_cast<uint64_t>(batch) * splits * M * N * 4 + 255) & ~255ull;
+}
+uint64_t split_ws_bytes(uint32_t M, uint32_t N, uint32_t batch, uint32_t splits) {
+    if (splits <= 1) return 0;
+    return split_plane_bytes(M, N, batch, splits) + static_cast<uint64_t>(batch) * ceil_div(M, 64) * ceil_div(N, 64) * 8;
+}
+
+// A fresh arrival tag per K-split launch (48 bits, never 0), so counters left
+// by other launches never match. Process-wide and monotonic.
+unsigned long long next_epoch() {
+    static std::atomic<unsigned long long> g_epoch{
+        (static_cast<unsigned long long>(std::chrono::steady_clock::now().time_since_epoch().count()) * 0x9E3779B97F4A7C15ull) >> 20};
+    unsigned long long e;
+    do e = g_epoch.fetch_add(1, std::memory_order_relaxed) & ((1ull << 48) - 1);
+    while (e == 0);
+    return e;
+}
+
+// The arguments of a K-split launch: the kernel's C becomes the workspace's
+// planes (row stride N, split planes M * N apart, batch items splits planes
+// apart); the call's C, its op and the counters go to the fixup fields.
+template <int EPI>
+GemmArgs split_args(const GemmArgs& a, uint32_t splits, uint32_t batch, float* ws) {
     GemmArgs p = a;
     p.C = ws;
     p.ldc = a.N;
     p.split_stride = static_cast<uint64_t>(a.M) * a.N;
     p.sC = p.split_stride * splits;
+    p.out = a.C;
+    p.ldo = a.ldc;
+    p.so = a.sC;
+    p.nsplit = splits;
+    p.op = EPI == kEpiResidual ? 2 : a.mode == 0 ? 0 : 1;
+    p.counters = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) +
+                                                       split_plane_bytes(a.M, a.N, batch, splits));
+    p.epoch = next_epoch();
     return p;
-}
-
-// Adds the partial planes into C in split order (reduce op from the epilogue / mode).
-template <int EPI>
-void finish_split(const GemmArgs& a, uint32_t splits, const float* ws, uint32_t batch, hipStream_t s) {
-    const int op = EPI == kEpiResidual ? 2 : a.mode == 0 ? 0 : 1;
-    launch_splitk_reduce(ws, splits, a.C, a.bias, a.M, a.N, a.ldc, a.sC, batch, op, s);
 }
 
 // SPLIT = false: a build without a K-split variant (requested splits are ignored).
@@ -1404,9 +934,8 @@ void launch_cfg(const GemmArgs& a0, uint32_t batch, uint32_t splits, float* ws, 
     }
     if (splits > 1) {
         if constexpr (EPI != kEpiGeglu && SPLIT) {
-            const GemmArgs p = partial_args(a, splits, ws);
+            const GemmArgs p = split_args<EPI>(a, splits, batch, ws);
             gemm_q8_kernel<BM, BN, WM, WN, KB, WK, true, KTAIL, PF><<<dim3(tiles, splits, batch), WM * WN * 64, 0, s>>>(p);
-            finish_split<EPI>(a, splits, ws, batch, s);
         }
     } else {
         a.steps_per_split = a.ksteps;
@@ -1414,71 +943,9 @@ void launch_cfg(const GemmArgs& a0, uint32_t batch, uint32_t splits, float* ws, 
     }
 }
 
-// Row-stationary kernel: 256 x (32 FN) tiles, K % 32 == 0. A K split covers an
-// even number of 32-wide steps.
-template <int FN, int WK, bool AQ = false, int EPI = kEpiPlain>
-void launch_rows(const GemmArgs& a0, uint32_t batch, uint32_t splits, float* ws, hipStream_t s) {
-    GemmArgs a = a0;
-    constexpr uint32_t BM = 256, BN = 32 * FN;
-    a.tiles_n = EPI == kEpiGeglu ? ceil_div(a.F, BN / 2) : ceil_div(a.N, BN);
-    if (EPI == kEpiGeglu || !ws) splits = 1;
-    a.tiles_m = ceil_div(a.M, BM);
-    a.group_m = pick_group(a.tiles_m, a.tiles_n, BM, BN, a.K);
-    a.ksteps = a.K / 32;
-    const unsigned tiles = a.tiles_m * a.tiles_n;
-    if (splits > 1) {
-        a.steps_per_split = (ceil_div(a.ksteps, splits) + 1u) & ~1u;
-        splits = ceil_div(a.ksteps, a.steps_per_split);
-    }
-    if (splits > 1) {
-        if constexpr (EPI != kEpiGeglu) {
-            const GemmArgs p = partial_args(a, splits, ws);
-            gemm_q8_rows_kernel<FN, WK, true, AQ><<<dim3(tiles, splits, batch), 256, 0, s>>>(p);
-            finish_split<EPI>(a, splits, ws, batch, s);
-        }
-    } else {
-        a.steps_per_split = a.ksteps;
-        gemm_q8_rows_kernel<FN, WK, false, AQ, EPI><<<dim3(tiles, 1, batch), 256, 0, s>>>(a);
-    }
-}
-
-// Producer / consumer kernel: 192 x 256 tiles, one Q8_0 block per step (K % 32 == 0).
-template <int WK, int EPI = kEpiPlain>
-void launch_pc(const GemmArgs& a0, uint32_t batch, uint32_t splits, float* ws, hipStream_t s) {
-    GemmArgs a = a0;
-    constexpr uint32_t BM = 192, BN = 256;
-    a.tiles_n = EPI == kEpiGeglu ? ceil_div(a.F, BN / 2) : ceil_div(a.N, BN);
-    if (EPI == kEpiGeglu || !ws) splits = 1;
-    a.tiles_m = ceil_div(a.M, BM);
-    a.group_m = pick_group(a.tiles_m, a.tiles_n, BM, BN, a.K);
-    a.ksteps = a.K / 32;
-    const unsigned tiles = a.tiles_m * a.tiles_n;
-    if (splits > 1) {
-        a.steps_per_split = ceil_div(a.ksteps, splits);
-        splits = ceil_div(a.ksteps, a.steps_per_split);
-    }
-    if (splits > 1) {
-        if constexpr (EPI != kEpiGeglu) {
-            const GemmArgs p = partial_args(a, splits, ws);
-            gemm_q8_pc_kernel<WK, true><<<dim3(tiles, splits, batch), 512, 0, s>>>(p);
-            finish_split<EPI>(a, splits, ws, batch, s);
-        }
-    } else {
-        a.steps_per_split = a.ksteps;
-        gemm_q8_pc_kernel<WK, false, EPI><<<dim3(tiles, 1, batch), 512, 0, s>>>(a);
-    }
-}
-
 template <int WK, int EPI = kEpiPlain>
 void launch(int cfg, const GemmArgs& a, uint32_t batch, uint32_t splits, float* ws, hipStream_t s) {
     switch (cfg) {
-        case kP192x256: launch_pc<WK, EPI>(a, batch, splits, ws, s); break;
-        case kR256x256: launch_rows<8, WK, false, EPI>(a, batch, splits, ws, s); break;
-        case kR256x256Q: launch_rows<8, WK, true, EPI>(a, batch, splits, ws, s); break;
-        case kR256x192Q: launch_rows<6, WK, true, EPI>(a, batch, splits, ws, s); break;
-        case kR256x160Q: launch_rows<5, WK, true, EPI>(a, batch, splits, ws, s); break;
-        case kR256x128Q: launch_rows<4, WK, true, EPI>(a, batch, splits, ws, s); break;
-        case kR256x128: launch_rows<4, WK, false, EPI>(a, batch, splits, ws, s); break;
         case kC256x128: launch_cfg<256, 128, 4, 2, 2, WK, false, 2, EPI>(a, batch, splits, ws, s); break;
         case kC128x128:
             // one register set: the loop then issues most of a step's MFMAs before
@@ -1486,14 +953,7 @@ void launch(int cfg, const GemmArgs& a, uint32_t batch, uint32_t splits, float* 
             // sets, 2048x1280x5120 71 vs 76, 8192x640x640 20 vs 22, the rest equal)
             launch_cfg<128, 128, 2, 2, 2, WK, false, 1, EPI>(a, batch, splits, ws, s);
             break;
-        case kC256x128W4: launch_cfg<256, 128, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, ws, s); break;
         case kC192x256: launch_cfg<192, 256, 2, 4, 2, WK, false, 2, EPI>(a, batch, splits, ws, s); break;
-        case kC128x256W4: launch_cfg<128, 256, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, ws, s); break;
-        case kC256x256W4:
-            // one wave per SIMD with 128 x 128 per wave (256 accumulator AGPRs)
-            // and one register set; its K-split build would spill in the loop
-            launch_cfg<256, 256, 2, 2, 2, WK, false, 1, EPI, false>(a, batch, splits, ws, s);
-            break;
         case kC128x64: launch_cfg<128, 64, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, ws, s); break;
         case kC256x256:
             // The split layout's and the GEGLU epilogue's 256x256 builds need
@@ -1568,17 +1028,11 @@ Plan choose(uint32_t M, uint32_t N, uint32_t K, uint32_t batch, bool allow_split
     return p;
 }
 
-// Floats of workspace a K-split plan uses: one [M, N] partial plane per split
-// and batch item.
-uint64_t split_floats(uint32_t M, uint32_t N, uint32_t batch, uint32_t splits) {
-    return splits > 1 ? static_cast<uint64_t>(batch) * splits * M * N : 0;
-}
-
 // The plan for a call: a split plan only when the caller's workspace holds
 // its partials, else the best plan without a split.
 Plan plan_for(uint32_t M, uint32_t N, uint32_t K, uint32_t batch, const void* ws, uint64_t ws_bytes) {
     Plan p = choose(M, N, K, batch, ws != nullptr);
-    if (p.splits > 1 && split_floats(M, N, batch, p.splits) * 4 > ws_bytes) p = choose(M, N, K, batch, false);
+    if (p.splits > 1 && split_ws_bytes(M, N, batch, p.splits) > ws_bytes) p = choose(M, N, K, batch, false);
     return p;
 }
 
@@ -1710,7 +1164,7 @@ int gemm_blocks(const char* fn, const float* A, const void* W, const float* bias
     }
     if (fixed_ws) {
         const Plan want = choose(M, N, K, batch, true);
-        const uint64_t need = split_floats(M, N, batch, want.splits) * 4;
+        const uint64_t need = split_ws_bytes(M, N, batch, want.splits);
         if (need > ws_bytes)
             return fail(MI_ERR_UNSUPPORTED,
                         "%s: M=%u N=%u K=%u batch=%u plans %u K splits whose partials need %llu bytes of scratch; "
@@ -1864,7 +1318,7 @@ extern "C" int mi_gemm_nt_q8_split_ws(const float* A, const uint32_t* payload, c
 extern "C" uint64_t mi_gemm_nt_q8_workspace_bytes(uint32_t M, uint32_t N, uint32_t K, uint32_t batch) {
     if (M == 0 || N == 0 || K == 0 || batch == 0) return 0;
     const Plan p = choose(M, N, K, batch, true);
-    return split_floats(M, N, batch, p.splits) * 4;
+    return split_ws_bytes(M, N, batch, p.splits);
 }
 
 extern "C" int mi_gemm_nt_q8_0_geglu(const float* A, const void* W, const float* bias, float* G, uint32_t M, uint32_t F,

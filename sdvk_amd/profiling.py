@@ -38,7 +38,7 @@ from pathlib import Path
 # family -> (main kernels: one launch per API call, helper kernels of the same calls)
 # (the K-split reduce pass is shared by both GEMMs; it is counted with gemm_q8)
 FAMILIES = {
-    "gemm_q8": (("gemm_q8_kernel", "gemm_q8_rows_kernel", "gemm_q8_any_kernel"),
+    "gemm_q8": (("gemm_q8_kernel", "gemm_q8_any_kernel"),
                 ("gemm_fill_kernel", "splitk_reduce_kernel")),
     "attention": (("attn_kernel", "attn_f16_kernel"), ("attn_merge_kernel",)),
     "gemm_nn_q8": (("gemm_nn_q8_kernel", "gemm_nn_q8_tiled_kernel"), ()),

@@ -9,7 +9,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from helpers import REL_RMS_TOL, assert_parity, err_vs_rms, q8_weights
+from helpers import REL_RMS_TOL, assert_parity, err_vs_rms, q8_weights, split_ws_bytes
 from sdvk_amd import ops
 from sdvk_amd.hip import DeviceBuffer, synchronize
 
@@ -147,7 +147,7 @@ def test_split_unaligned_a_and_odd_lda(gpu, oracle):
 
 
 @pytest.mark.parametrize("ldc_pad,sc_pad,K,cfg", [(8, 8, 96, ""), (3, 5, 96, ""), (8, 8, 128, ""), (1, 0, 256, ""),
-                                                  (8, 8, 128, "5"), (3, 5, 256, "6:2")])
+                                                  (8, 8, 128, "5"), (3, 5, 256, "5:2")])
 def test_batch_and_strides(gpu, oracle, tune, ldc_pad, sc_pad, K, cfg):
     """Grid z offsets A and C, never W (gemm_nt_q8_v.comp:51-52,87); lda/ldc padding untouched.
     Odd ldc / sC take the scalar epilogue, multiples of 4 the 16-byte one."""
@@ -199,7 +199,7 @@ def test_rule_k_splits_sampled_rows(gpu, oracle, M, N, K, splits):
     once; 64 x 64 grids split toward ~256 workgroups): the workspace the
     library asks for pins the split count, sampled rows match the oracle."""
     print(f"[case] rule split M={M} N={N} K={K} splits={splits}", flush=True)
-    assert ops.gemm_workspace_bytes(M, N, K) == splits * M * N * 4
+    assert ops.gemm_workspace_bytes(M, N, K) == split_ws_bytes(M, N, 1, splits)
     A = oracle.normal(11, M * K)
     blocks = q8_weights(oracle, 12, N, K)
     bias = oracle.normal(13, N, 0.0, 0.02)
@@ -212,8 +212,7 @@ def test_rule_k_splits_sampled_rows(gpu, oracle, M, N, K, splits):
     assert e <= REL_RMS_TOL
 
 
-@pytest.mark.parametrize("cfg", ["0", "1", "2", "3", "4", "5", "6", "12", "13", "14", "15", "0:3", "1:2", "2:5",
-                                 "3:16", "4:2", "5:2", "6:3", "14:2", "15:3"])
+@pytest.mark.parametrize("cfg", ["0", "1", "2", "3", "4", "5", "0:3", "1:2", "2:5", "3:16", "4:2", "5:2", "5:3"])
 @pytest.mark.parametrize("M,N,K", [(300, 200, 640), (1030, 130, 256)])
 def test_every_tile_config_and_split_k(gpu, oracle, tune, cfg, M, N, K):
     """Forces each tile configuration / K split (gemm_cfg "<cfg>[:<splits>]";

@@ -24,7 +24,7 @@ import pytest
 import isa_sched
 
 CASES = {
-    "gemm_q8.hip": ("gemm_q8_kernel", "gemm_q8_rows_kernel"),
+    "gemm_q8.hip": ("gemm_q8_kernel",),
     "attention.hip": ("attn_f16_kernel", "attn_kernel"),
     "gemm_nn_q8.hip": ("gemm_nn_q8_tiled_kernel",),
 }
@@ -65,8 +65,8 @@ def test_k_loops_keep_loads_ahead_of_their_waits(asm, src):
 
 # Kernels that may keep values in scratch around (never inside) their K loop,
 # and how many bytes per lane: the 8-wave 256x256 LDS build at its 256-register
-# limit (epilogue indices across the loop).
-SCRATCH_ALLOWED = {"gemm_q8_kernelILi256ELi256ELi4ELi2E": 16}
+# limit (epilogue indices and, in its K-split build, the fixup's operands across the loop).
+SCRATCH_ALLOWED = {"gemm_q8_kernelILi256ELi256ELi4ELi2E": 24}
 
 
 @pytest.mark.parametrize("src", list(CASES))

@@ -11,7 +11,6 @@ from sdvk_amd import profiling as p
 
 ATTN_F16 = "_ZN2mi12_GLOBAL__N_115attn_f16_kernelIDF16_Li4EEEvNS0_8AttnArgsEj"
 GEMM = "_ZN2mi12_GLOBAL__N_114gemm_q8_kernelILi256ELi128ELi4ELi2ELi2ELi0ELb0ELb0ELi2ELi0EEEvNS0_8GemmArgsE"
-ROWS = "_ZN2mi12_GLOBAL__N_119gemm_q8_rows_kernelILi8ELi0ELb0ELb1ELi0EEEvNS0_8GemmArgsE"
 INIT = "_ZN2mi12_GLOBAL__N_116gemm_fill_kernelEPfPKfjjjmj"
 REDUCE = "_ZN2mi12_GLOBAL__N_120splitk_reduce_kernelILi0ELb1EEEvPKfmjPfS3_jjjmj"
 ANY = "_ZN2mi12_GLOBAL__N_118gemm_q8_any_kernelENS0_8GemmArgsE"
@@ -21,7 +20,7 @@ COPY = "__amd_rocclr_copyBuffer"
 
 
 @pytest.mark.parametrize("name,family,main", [
-    (ATTN_F16, "attention", True), (MERGE, "attention", False), (GEMM, "gemm_q8", True), (ROWS, "gemm_q8", True), (INIT, "gemm_q8", False),
+    (ATTN_F16, "attention", True), (MERGE, "attention", False), (GEMM, "gemm_q8", True), (INIT, "gemm_q8", False),
     (REDUCE, "gemm_q8", False), (ANY, "gemm_q8", True), (NN, "gemm_nn_q8", True),
     (COPY, None, None),
     ("void mi::(anonymous namespace)::gemm_q8_kernel<64, 64, 2, 2, 2, 0, true, false, 2, 0>(mi::GemmArgs)",
@@ -50,7 +49,7 @@ def test_stats_report_aggregates_per_call(tmp_path):
     hdr = ["Name", "Calls", "TotalDurationNs", "AverageNs", "Percentage", "MinNs", "MaxNs"]
     _write(f, hdr, [[GEMM, 4, 400000, 100000, 40, 90000, 110000],
                     [INIT, 2, 20000, 10000, 2, 9000, 11000],
-                    [ROWS, 2, 100000, 50000, 10, 50000, 50000],
+                    [ANY, 2, 100000, 50000, 10, 50000, 50000],
                     [ATTN_F16, 3, 300000, 100000, 30, 100000, 100000],
                     [NN, 1, 50000, 50000, 5, 50000, 50000],
                     [COPY, 1, 1000, 1000, 0.1, 1000, 1000]])
