@@ -23,8 +23,6 @@
 //     applies bias / accumulate. Every plan sums in a fixed order, so a call
 //     repeats bit for bit; entries without a workspace never split K.
 #include <algorithm>
-#include <atomic>
-#include <chrono>
 #include <type_traits>
 #include <cstdlib>
 #include <cstring>
@@ -53,16 +51,6 @@ struct GemmArgs {
     uint32_t bvec;          // bias 16-byte aligned
     uint32_t F;             // GEGLU epilogue: output columns (W has 2F rows: value rows, then gate rows)
     uint64_t split_stride;  // K-split partials: elements between the planes of consecutive splits
-    // K-split launches: C / ldc / sC above address the partial planes; the
-    // workgroup that finishes a tile last adds its planes, in split order,
-    // into the real output (out, ldo, so) with the reduce op of the call.
-    float* out;
-    uint32_t ldo;
-    uint32_t nsplit;
-    uint64_t so;
-    int op;                        // 0: out = sum + bias; 1: out += sum; 2: out += sum + bias
-    unsigned long long* counters;  // arrival counters, one per (batch item, tile)
-    unsigned long long epoch;      // this launch's arrival tag (48 bits, never 0)
 };
 
 // Epilogues. kEpiPlain: the reference's modes (0 stores acc + bias, 1 adds acc
@@ -286,69 +274,6 @@ __device__ __forceinline__ void store_tiles(const GemmArgs& a, float* C, float* 
         }
         // every read of this tile precedes the next tile's writes
         __builtin_amdgcn_wave_barrier();
-    }
-}
-
-// K-split arrival: counter word = (epoch << 16) | workgroups arrived. A word
-// holding another launch's epoch (or anything else) counts as zero arrivals,
-// so the workspace needs no clearing; the last of the nsplit workgroups of a
-// tile returns true and resets the word to 0, which no launch's epoch equals
-// (graph replays that reuse a launch's epoch start from 0 again). The CAS
-// loop ends: every failed attempt means another workgroup's succeeded, and at
-// most nsplit succeed.
-__device__ __forceinline__ bool arrive_last(unsigned long long* c, unsigned long long epoch, uint32_t n) {
-    unsigned long long cur = atomicCAS(c, 0ull, 0ull);  // an atomic read (swaps 0 for 0)
-    for (;;) {
-        const unsigned long long next = (cur >> 16) == epoch ? cur + 1ull : (epoch << 16) | 1ull;
-        const unsigned long long seen = atomicCAS(c, cur, next);
-        if (seen == cur) return (next & 0xffffull) == n;
-        cur = seen;
-    }
-}
-
-// The last workgroup of a K-split tile: adds the tile's partial planes in split
-// order -- ((P0 + P1) + P2) + ..., whichever workgroup arrives last -- and
-// applies the call's op, the arithmetic of splitk_reduce_kernel, so a call
-// repeats bit for bit. Lane positions are those of the partial stores (column
-// l32 of each 32-wide tile, rows 8 (r / 4) + 4 g + r % 4): 32 consecutive
-// floats per load / store instruction.
-template <int FM, int FN>
-__device__ __forceinline__ void split_fixup(const GemmArgs& a, uint32_t mw, uint32_t nw, int lane, int tid,
-                                            int* s_last) {
-    __threadfence();  // this thread's partial stores are visible device-wide ...
-    __syncthreads();  // ... for every thread of the workgroup, before the arrival
-    if (tid == 0) {
-        unsigned long long* c = a.counters + static_cast<uint64_t>(blockIdx.z) * gridDim.x + blockIdx.x;
-        const bool last = arrive_last(c, a.epoch, a.nsplit);
-        if (last) atomicExch(c, 0ull);
-        *s_last = last ? 1 : 0;
-    }
-    __syncthreads();
-    if (!*s_last) return;
-    __threadfence();  // the other splits' partials, after their arrivals
-    const int l32 = lane & 31, g = lane >> 5;
-    const float* P = a.C + static_cast<uint64_t>(blockIdx.z) * a.sC;
-    float* O = a.out + static_cast<uint64_t>(blockIdx.z) * a.so;
-    const bool use_bias = a.op != 1 && a.bias != nullptr;
-#pragma unroll
-    for (int fn = 0; fn < FN; ++fn) {
-        const uint32_t n = nw + 32 * fn + l32;
-        if (n >= a.N) continue;
-        const float b = use_bias ? a.bias[n] : 0.0f;
-#pragma unroll
-        for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const uint32_t m = mw + 32 * fm + 8 * (r >> 2) + 4 * g + (r & 3);
-                if (m >= a.M) continue;
-                const float* q = P + static_cast<uint64_t>(m) * a.N + n;
-                float v = q[0];
-                for (uint32_t sp = 1; sp < a.nsplit; ++sp) v += q[sp * a.split_stride];
-                float* o = O + static_cast<uint64_t>(m) * a.ldo + n;
-                if (a.op == 0) *o = use_bias ? v + b : v;
-                else if (a.op == 1) *o = *o + v;
-                else *o = *o + (use_bias ? v + b : v);
-            }
     }
 }
 
@@ -714,10 +639,6 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     store_tiles<FM, FN, SPLITK, EPI>(a, C, reinterpret_cast<float*>(smem) + wave_s * kStageFloats, m0 + wm_s * TM,
                                      EPI == kEpiGeglu ? n0 + wn_s * TN / 2 : n0 + wn_s * TN, acc,
                                      kFreshLane ? lane_id() : lane);
-    if constexpr (SPLITK) {
-        __shared__ int s_last;
-        split_fixup<FM, FN>(a, m0 + wm_s * TM, n0 + wn_s * TN, kFreshLane ? lane_id() : lane, tid, &s_last);
-    }
 }
 
 // K == 0: C[m, n] = bias[n] (or 0) in mode 0, C[m, n] += bias[n] in mode 2.
@@ -872,47 +793,22 @@ uint32_t pick_group(uint32_t tm, uint32_t tn, uint32_t BM, uint32_t BN, uint32_t
     return best;
 }
 
-// Workspace of a K split: the partial planes (batch * splits * M * N floats,
-// rounded up to 256 bytes), then one 8-byte arrival counter per (batch item,
-// tile) for the smallest tile (64 x 64), which bounds every build's count.
-uint64_t split_plane_bytes(uint32_t M, uint32_t N, uint32_t batch, uint32_t splits) {
-    return (static_cast<uint64_t>(batch) * splits * M * N * 4 + 255) & ~255ull;
-}
-uint64_t split_ws_bytes(uint32_t M, uint32_t N, uint32_t batch, uint32_t splits) {
-    if (splits <= 1) return 0;
-    return split_plane_bytes(M, N, batch, splits) + static_cast<uint64_t>(batch) * ceil_div(M, 64) * ceil_div(N, 64) * 8;
-}
-
-// A fresh arrival tag per K-split launch (48 bits, never 0), so counters left
-// by other launches never match. Process-wide and monotonic.
-unsigned long long next_epoch() {
-    static std::atomic<unsigned long long> g_epoch{
-        (static_cast<unsigned long long>(std::chrono::steady_clock::now().time_since_epoch().count()) * 0x9E3779B97F4A7C15ull) >> 20};
-    unsigned long long e;
-    do e = g_epoch.fetch_add(1, std::memory_order_relaxed) & ((1ull << 48) - 1);
-    while (e == 0);
-    return e;
-}
-
-// The arguments of a K-split launch: the kernel's C becomes the workspace's
-// planes (row stride N, split planes M * N apart, batch items splits planes
-// apart); the call's C, its op and the counters go to the fixup fields.
-template <int EPI>
-GemmArgs split_args(const GemmArgs& a, uint32_t splits, uint32_t batch, float* ws) {
+// The partial planes of a K split: the kernel's C becomes the workspace
+// (row stride N, split planes M * N apart, batch items splits planes apart).
+GemmArgs partial_args(const GemmArgs& a, uint32_t splits, float* ws) {
     GemmArgs p = a;
     p.C = ws;
     p.ldc = a.N;
     p.split_stride = static_cast<uint64_t>(a.M) * a.N;
     p.sC = p.split_stride * splits;
-    p.out = a.C;
-    p.ldo = a.ldc;
-    p.so = a.sC;
-    p.nsplit = splits;
-    p.op = EPI == kEpiResidual ? 2 : a.mode == 0 ? 0 : 1;
-    p.counters = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) +
-                                                       split_plane_bytes(a.M, a.N, batch, splits));
-    p.epoch = next_epoch();
     return p;
+}
+
+// Adds the partial planes into C in split order (reduce op from the epilogue / mode).
+template <int EPI>
+void finish_split(const GemmArgs& a, uint32_t splits, const float* ws, uint32_t batch, hipStream_t s) {
+    const int op = EPI == kEpiResidual ? 2 : a.mode == 0 ? 0 : 1;
+    launch_splitk_reduce(ws, splits, a.C, a.bias, a.M, a.N, a.ldc, a.sC, batch, op, s);
 }
 
 // SPLIT = false: a build without a K-split variant (requested splits are ignored).
@@ -934,8 +830,9 @@ void launch_cfg(const GemmArgs& a0, uint32_t batch, uint32_t splits, float* ws, 
     }
     if (splits > 1) {
         if constexpr (EPI != kEpiGeglu && SPLIT) {
-            const GemmArgs p = split_args<EPI>(a, splits, batch, ws);
+            const GemmArgs p = partial_args(a, splits, ws);
             gemm_q8_kernel<BM, BN, WM, WN, KB, WK, true, KTAIL, PF><<<dim3(tiles, splits, batch), WM * WN * 64, 0, s>>>(p);
+            finish_split<EPI>(a, splits, ws, batch, s);
         }
     } else {
         a.steps_per_split = a.ksteps;
@@ -1028,11 +925,17 @@ Plan choose(uint32_t M, uint32_t N, uint32_t K, uint32_t batch, bool allow_split
     return p;
 }
 
+// Floats of workspace a K-split plan uses: one [M, N] partial plane per split
+// and batch item.
+uint64_t split_floats(uint32_t M, uint32_t N, uint32_t batch, uint32_t splits) {
+    return splits > 1 ? static_cast<uint64_t>(batch) * splits * M * N : 0;
+}
+
 // The plan for a call: a split plan only when the caller's workspace holds
 // its partials, else the best plan without a split.
 Plan plan_for(uint32_t M, uint32_t N, uint32_t K, uint32_t batch, const void* ws, uint64_t ws_bytes) {
     Plan p = choose(M, N, K, batch, ws != nullptr);
-    if (p.splits > 1 && split_ws_bytes(M, N, batch, p.splits) > ws_bytes) p = choose(M, N, K, batch, false);
+    if (p.splits > 1 && split_floats(M, N, batch, p.splits) * 4 > ws_bytes) p = choose(M, N, K, batch, false);
     return p;
 }
 
@@ -1164,7 +1067,7 @@ int gemm_blocks(const char* fn, const float* A, const void* W, const float* bias
     }
     if (fixed_ws) {
         const Plan want = choose(M, N, K, batch, true);
-        const uint64_t need = split_ws_bytes(M, N, batch, want.splits);
+        const uint64_t need = split_floats(M, N, batch, want.splits) * 4;
         if (need > ws_bytes)
             return fail(MI_ERR_UNSUPPORTED,
                         "%s: M=%u N=%u K=%u batch=%u plans %u K splits whose partials need %llu bytes of scratch; "
@@ -1318,7 +1221,7 @@ extern "C" int mi_gemm_nt_q8_split_ws(const float* A, const uint32_t* payload, c
 extern "C" uint64_t mi_gemm_nt_q8_workspace_bytes(uint32_t M, uint32_t N, uint32_t K, uint32_t batch) {
     if (M == 0 || N == 0 || K == 0 || batch == 0) return 0;
     const Plan p = choose(M, N, K, batch, true);
-    return split_ws_bytes(M, N, batch, p.splits);
+    return split_floats(M, N, batch, p.splits) * 4;
 }
 
 extern "C" int mi_gemm_nt_q8_0_geglu(const float* A, const void* W, const float* bias, float* G, uint32_t M, uint32_t F,

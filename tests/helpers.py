@@ -65,12 +65,3 @@ def q8_weights(oracle, seed: int, N: int, K: int, std: float = 0.02) -> np.ndarr
 def split_from_blocks(oracle, blocks: np.ndarray, n: int):
     payload, scales = oracle.q8_0_to_split(blocks, n)
     return payload, scales
-
-
-def split_ws_bytes(M: int, N: int, batch: int, splits: int) -> int:
-    """Workspace bytes of a K-split GEMM plan: the partial planes (batch x
-    splits x M x N floats, rounded up to 256 bytes) and one 8-byte arrival
-    counter per 64 x 64 tile and batch item."""
-    if splits <= 1:
-        return 0
-    return -(-(batch * splits * M * N * 4) // 256) * 256 + batch * -(-M // 64) * -(-N // 64) * 8

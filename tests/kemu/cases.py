@@ -297,8 +297,8 @@ def _whole_tiles(mask: np.ndarray, what: str) -> None:
 
 def gemm_full(E, *, M, N, K, cfg=None, layout="q8_0", seed=1, order=0, tol=2e-3, ws=True):
     """mi_gemm_nt_q8_0[_ws] / _split[_ws] at a full benchmark shape, sampled
-    workgroups (with ws: the K-split plan the benchmark runs, every split of a
-    sampled tile, so its last workgroup writes the tile; unsampled tiles stay 0)."""
+    workgroups (with ws: the K-split plan the benchmark runs; the reduce pass
+    runs whole over a zeroed workspace, so unsampled tiles read back as 0)."""
     _set_cfg(cfg)
     E.order(order)
     A = ob.normal(seed, M * K)
@@ -316,7 +316,8 @@ def gemm_full(E, *, M, N, K, cfg=None, layout="q8_0", seed=1, order=0, tol=2e-3,
         dP, dS = E.buf(payload), E.buf(scales)
         call = lambda: E.call("mi_gemm_nt_q8_split" + sfx, dA.ptr, dP.ptr, dS.ptr, None, dC.ptr, M, N, K, 0, 0, 0, 1,
                               0, 0, *extra, None)
-    kern, grid = _probe_grid(E, "gemm_q8_kernel|-|-|-;gemm_fill|-|-|-", call)
+    helpers = "gemm_fill|-|-|-;splitk_reduce|-|-|-"  # the K == 0 fill and the split reduce pass
+    kern, grid = _probe_grid(E, f"gemm_q8_kernel|-|-|-;{helpers}", call)
     assert not np.any(dC.get(np.float32, M * N)), "a launch with no workgroup wrote C"
     xs = sorted({0, _block_of_tile(grid[0] - 1, grid[0])})
     x = ",".join(map(str, xs))
@@ -325,7 +326,10 @@ def gemm_full(E, *, M, N, K, cfg=None, layout="q8_0", seed=1, order=0, tol=2e-3,
     before = E.lib.kemu_blocks_run()
     call()
     ran = E.lib.kemu_blocks_run() - before
-    assert ran == len(xs) * grid[1] * grid[2], f"{ran} workgroups ran, expected {len(xs)} x {grid[1]} x {grid[2]}"
+    # a split plan's reduce pass runs whole: a capped grid over the [M, N / 4] units
+    reduce = min(max(-(-(M * N // 4) // 256), 1), 1024) if grid[1] > 1 else 0
+    assert ran == len(xs) * grid[1] * grid[2] + reduce, \
+        f"{ran} workgroups ran, expected {len(xs)} x {grid[1]} x {grid[2]} + {reduce} (reduce)"
     got = dC.get(np.float32, M * N).reshape(M, N)
     mask = got != 0
     assert mask.any(), "the sampled workgroups wrote nothing"

@@ -135,20 +135,6 @@ inline float unsafeAtomicAdd(float* p, float v) {
     return o;
 }
 inline float atomicAdd(float* p, float v) { return unsafeAtomicAdd(p, v); }
-// 64-bit compare-and-swap / exchange and the device fence: a work-item runs
-// alone until its next synchronisation point, so plain accesses are atomic
-// and already ordered.
-inline unsigned long long atomicCAS(unsigned long long* p, unsigned long long cmp, unsigned long long v) {
-    const unsigned long long o = *p;
-    if (o == cmp) *p = v;
-    return o;
-}
-inline unsigned long long atomicExch(unsigned long long* p, unsigned long long v) {
-    const unsigned long long o = *p;
-    *p = v;
-    return o;
-}
-inline void __threadfence() {}
 
 namespace kemu {
 

@@ -7,7 +7,6 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from helpers import split_ws_bytes
 from sdvk_amd import _lib, ops
 
 HEADER = Path(__file__).resolve().parents[1] / "include" / "mi_sdvk.h"
@@ -94,11 +93,10 @@ def test_errors_are_returned_not_raised_through_the_abi():
     assert st == _lib.MI_ERR_ALIASING
     st = lib.mi_gemm_nt_q8_0_ws(fake, fake * 2, None, fake * 3, 8, 8, 32, 0, 0, 0, 1, 0, 0, fake * 5 + 4, 4096, None)
     assert st == _lib.MI_ERR_ALIGNMENT
-    # the workspace a plan needs: none for a grid that fills the GPU, split planes (256-byte rounded)
-    # plus one 8-byte arrival counter per 64 x 64 tile and batch item for a small one
+    # the workspace a plan needs: none for a grid that fills the GPU, split planes for a small one
     assert lib.mi_gemm_nt_q8_workspace_bytes(8192, 5120, 640, 1) == 0
-    assert lib.mi_gemm_nt_q8_workspace_bytes(154, 640, 2048, 1) == split_ws_bytes(154, 640, 1, 8)
-    assert lib.mi_gemm_nt_q8_workspace_bytes(154, 640, 2048, 2) == split_ws_bytes(154, 640, 2, 4)
+    assert lib.mi_gemm_nt_q8_workspace_bytes(154, 640, 2048, 1) == 8 * 154 * 640 * 4
+    assert lib.mi_gemm_nt_q8_workspace_bytes(154, 640, 2048, 2) == 2 * 4 * 154 * 640 * 4
     assert lib.mi_gemm_nn_q8_workspace_bytes(1280, 1024, 640, 1) == 2 * 1280 * 1024 * 4
     assert lib.mi_gemm_nn_q8_workspace_bytes(1280, 1024, 100, 1) == 0  # K % 64 != 0: the untiled kernel
     # unsupported attention head dim: the reference exit(1)s; here an error code

@@ -11,9 +11,8 @@ kernel, workgroup and work-item), and runs under two schedules: one
 wave operation per wave per pass, and wave-major with lanes and waves
 reversed, so a missing barrier changes the result under one of them.
 
-This is where paths are checked before they reach a GPU (the K-split fixup by
-the last workgroup of a tile, the NN GEMM, the cached-K/V block, the GGUF
-uploads, the fused GEGLU / residual epilogues). The "fullsize" family runs every
+This is where paths are checked before they reach a GPU (the NN GEMM, the
+cached-K/V block, the GGUF uploads, the fused GEGLU / residual epilogues). The "fullsize" family runs every
 kernel build the benchmark launches at the benchmark's own shapes, with a
 few workgroups emulated per launch (the first and the bottom-right tile,
 every K split of them): grids, split choices and offsets are those of the
@@ -63,8 +62,7 @@ FAMILIES = {
         dict(M=70, N=36, K=128, batch=2, lda=132, ldc=40, sA=9300, sC=3000, cfg="4:2", mode=1),
         # 192x256 (8 waves of 96x64)
         dict(M=400, N=300, K=256, cfg="5"), dict(M=200, N=260, K=320, cfg="5:2", layout="split", mode=1),
-        # K splits summed by the last workgroup to finish each tile: many splits of one tile, batch items
-        # with strides, mode 2 (the residual op), every 64 x 64 workgroup of a tile arriving in turn
+        # more K splits: many splits of one tile, batch items with strides, mode 2 (the residual op)
         dict(M=64, N=64, K=2048, cfg="3:16"), dict(M=70, N=36, K=512, batch=3, lda=520, ldc=40, sA=37000,
                                                    sC=3000, cfg="3:4", mode=1),
         dict(M=130, N=200, K=512, cfg="1:3", mode=2), dict(M=200, N=300, K=640, cfg="5:3", front=True),
@@ -243,13 +241,6 @@ def test_routing_at_sdxl_shapes(emulator):
 
 # One planted mistake per copy of the sources: (file, text, replacement, case).
 PLANTED = {
-    # K split: arrival counters taken at face value, without the launch's epoch: the workspace starts
-    # as 0xFF bytes, so no workgroup finds itself last and no tile is written
-    "split_epoch": ("gemm_q8.hip", "(cur >> 16) == epoch ? cur + 1ull : (epoch << 16) | 1ull", "cur + 1ull",
-                    dict(case="gemm_nt", M=154, N=96, K=2048)),
-    # K split: the last workgroup leaves the last split's plane out of the sum
-    "split_sum": ("gemm_q8.hip", "for (uint32_t sp = 1; sp < a.nsplit; ++sp)", "for (uint32_t sp = 1; sp + 1 < a.nsplit; ++sp)",
-                  dict(case="gemm_nt", M=154, N=96, K=2048)),
     # the LDS kernel's barrier between a step's MFMAs / store phase and the next step removed
     "missing_barrier": ("gemm_q8.hip",
                         "            __syncthreads();\n            load_step(phys(min(j + 3, last)), S1{});",
