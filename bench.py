@@ -174,7 +174,7 @@ class NnCase:
 # (MI_BLOCK_FUSED_EPILOGUES). Every flag combination computes the same bits as
 # the plain block (tests/test_gpu_xfused_epilogues.py, test_gpu_xattn_kv_cache.py);
 # the extras time the plain block and each flag alone.
-BLOCK_VARIANT = {"cached_kv": True, "fused_epilogues": True, "joint_qkv": True}
+BLOCK_VARIANT = {"cached_kv": True, "fused_epilogues": True, "joint_qkv": True, "fp16_activations": True}
 
 
 class BlockStack:
@@ -187,14 +187,17 @@ class BlockStack:
 
     DIMS = (2, 1024, 1280, 20, 77, 2048, 5120)  # batch, tokens, channels, heads, ctx_tokens, ctx_channels, ff_inner
 
-    def __init__(self, rng, hip, ops, nblocks=10, joint_qkv=False, fused=False):
+    def __init__(self, rng, hip, ops, nblocks=10, joint_qkv=False, fused=False, half=False):
         """joint_qkv: each block's to_q / to_k / to_v weights in one allocation,
         back to back, and MI_BLOCK_JOINT_QKV: one Q/K/V projection GEMM (N = 3C);
         fused: MI_BLOCK_FUSED_EPILOGUES (residual adds and GEGLU in the GEMM
-        epilogues)."""
+        epilogues); half: MI_BLOCK_FP16_ACTIVATIONS (LayerNorm, attention and
+        GEGLU outputs stored as fp16 for the GEMMs that read them)."""
         B, T, C, H, Tc, Cc, F = self.DIMS
         self.ops, self.hip, self.nblocks = ops, hip, nblocks
-        flags = (ops.MI_BLOCK_JOINT_QKV if joint_qkv else 0) | (ops.MI_BLOCK_FUSED_EPILOGUES if fused else 0)
+        self.joint_qkv, self.fused, self.half = joint_qkv, fused, half
+        flags = ((ops.MI_BLOCK_JOINT_QKV if joint_qkv else 0) | (ops.MI_BLOCK_FUSED_EPILOGUES if fused else 0) |
+                 (ops.MI_BLOCK_FP16_ACTIVATIONS if half else 0))
         self.dims = ops.BlockDims(*self.DIMS, flags)
         shapes = {"attn1_q": (C, C), "attn1_k": (C, C), "attn1_v": (C, C), "attn1_out": (C, C),
                   "attn2_q": (C, C), "attn2_k": (C, Cc), "attn2_v": (C, Cc), "attn2_out": (C, C),
@@ -267,10 +270,96 @@ class BlockStack:
             B, T, C, H, Tc, Cc, F = self.DIMS
             flops -= 2.0 * B * Tc * C * Cc * 2 * self.nblocks  # the K / V projections are not in the timed pass
         return {"config": "BASELINE config 4: %d SDXL BasicTransformerBlocks, level 2 (C=1280, 2x1024 tokens, "
-                          "20 heads, ctx 2x77x2048, FF 1280->10240->5120->1280), Q8_0 weights, fp32 activations"
+                          "20 heads, ctx 2x77x2048, FF 1280->10240->5120->1280), Q8_0 weights, fp32 residual stream"
                           % self.nblocks,
                 "blocks": self.nblocks, "latency_ms": round(ms, 4), "ms_per_block": round(ms / self.nblocks, 4),
                 "gflop": round(flops / 1e9, 1), "tflops": round(flops / (ms / 1e3) / 1e12, 2), "reps": reps}
+
+    def kernel_share(self, stream, ms_per_block):
+        """The block's operators one by one, in the block's order and with its
+        flags, on buffers of the block's shapes (the first block's weights and
+        cached context K / V), each timed alone from a HIP graph (minimum of
+        three replays of 10 launches): time per kernel family, and the share of
+        the measured block latency each takes. The two hot kernels of the path
+        are the Q8 GEMM (gemm_q8: every projection, the K-split reduce passes
+        included) and the fused attention; glue = the LayerNorms. A measurement
+        only: the block itself is one mi_sdxl_block_forward_kv call."""
+        ops, hip = self.ops, self.hip
+        B, T, C, H, Tc, Cc, F = self.DIMS
+        rows = B * T
+        w = self.keep[1]
+        kv = self.kv[0]
+        half = self.half
+        esz = 2 if half else 4
+        n, o = hip.DeviceBuffer(rows * C * esz), hip.DeviceBuffer(rows * C * esz)
+        h = hip.DeviceBuffer(rows * 3 * C * 4)
+        q = hip.DeviceBuffer(rows * C * 4)
+        g = hip.DeviceBuffer(rows * F * esz)
+        x = hip.DeviceBuffer(rows * C * 4)
+        x.copy_from(self.x, rows * C * 4, stream)
+        wsb = max(ops.gemm_workspace_bytes(rows, C, C), ops.gemm_workspace_bytes(rows, C, F))
+        ws = hip.DeviceBuffer(wsb) if wsb else None
+        kb = ops.block_ctx_kv_bytes(self.dims) // 2
+        ln = ops.layernorm_f16 if half else ops.layernorm
+        gemm = ops.gemm_nt_q8_0_f16a if half else ops.gemm_nt_q8_0
+        odt = ops.MI_F16 if half else ops.MI_F32
+
+        def resid(A, W, b, K):
+            return lambda st: gemm(A, W, x, rows, C, K, bias=b, mode=2, workspace=ws, stream=st)
+
+        def ln_op(i):
+            return lambda st: ln(x, w[f"norm{i}_w"], w[f"norm{i}_b"], n, rows, C, stream=st)
+
+        def attn(qb, kb_, vb, ld, tk):
+            return lambda st: ops.fused_attention_ex(qb, kb_, vb, o, batch=B, Tq=T, Tk=tk, C=C, heads=H, ldq=ld,
+                                                     ldk=ld, ldv=ld, in_dtype=ops.MI_F32, out_dtype=odt,
+                                                     precision=ops.MI_ATTN_PREC_FP16, stream=st)
+        qkv = w["_qkv"] if "_qkv" in w else None
+        steps = [("glue", ln_op(1))]
+        if qkv is not None:
+            steps += [("gemm_q8", lambda st: gemm(n, qkv, h, rows, 3 * C, C, stream=st)),
+                      ("attention", attn(h.value, h.value + 4 * C, h.value + 8 * C, 3 * C, T))]
+        else:
+            steps += [("gemm_q8", lambda st: gemm(n, w["attn1_q"], h, rows, C, C, stream=st)),
+                      ("gemm_q8", lambda st: gemm(n, w["attn1_k"], h.value + rows * C * 4, rows, C, C, stream=st)),
+                      ("gemm_q8", lambda st: gemm(n, w["attn1_v"], h.value + 2 * rows * C * 4, rows, C, C, stream=st)),
+                      ("attention", attn(h.value, h.value + rows * C * 4, h.value + 2 * rows * C * 4, C, T))]
+        steps += [("gemm_q8", resid(o, w["attn1_out"], w["attn1_out_b"], C)), ("glue", ln_op(2)),
+                  ("gemm_q8", lambda st: gemm(n, w["attn2_q"], q, rows, C, C, stream=st)),
+                  ("attention", attn(q.value, kv.value, kv.value + kb, C, Tc)),
+                  ("gemm_q8", resid(o, w["attn2_out"], w["attn2_out_b"], C)), ("glue", ln_op(3)),
+                  ("gemm_q8", lambda st: (ops.gemm_nt_q8_0_geglu_f16 if half else ops.gemm_nt_q8_0_geglu)(
+                      n, w["ff_up"], g, rows, F, C, bias=w["ff_up_b"], stream=st)),
+                  ("gemm_q8", resid(g, w["ff_down"], w["ff_down_b"], F))]
+        fam = {}
+        for family, run in steps:
+            run(stream)  # warm: buffers hold the block's intermediates, workspaces sized
+        stream.synchronize()
+        for family, run in steps:
+            gr = hip.Graph(stream)
+            gr.begin()
+            for _ in range(10):
+                run(stream)
+            gr.end()
+            gr.launch()
+            best = None
+            for _ in range(3):
+                a, b = hip.Event(TIMING_EVENT), hip.Event(TIMING_EVENT)
+                a.record(stream)
+                gr.launch()
+                b.record(stream)
+                b.synchronize()
+                t = a.elapsed_ms(b) / 10
+                best = t if best is None else min(best, t)
+            fam[family] = fam.get(family, 0.0) + best
+            del gr
+        total = sum(fam.values())
+        return {"method": "each operator of one block timed alone (HIP graph, min of 3 replays x 10), the "
+                          "block's flags and shapes; share = family time / measured ms_per_block",
+                "us_per_block": {k: round(v * 1e3, 2) for k, v in fam.items()},
+                "share": {k: round(v / ms_per_block, 4) for k, v in fam.items()},
+                "hot_kernels_share": round((fam.get("gemm_q8", 0.0) + fam.get("attention", 0.0)) / ms_per_block, 4),
+                "operators_sum_over_latency": round(total / ms_per_block, 4)}
 
 
 def time_case(c, stream, hip, reps):
@@ -353,11 +442,12 @@ def extras(rng, hip, ops, stream, reps, emit=None):
             res.append(time_case(NnCase(t, M, N, K, rng, hip, ops), stream, hip, reps)[1])
         return res
 
-    def stack(cached_kv=False, fused=False, joint_qkv=False):
+    def stack(cached_kv=False, fused=False, joint_qkv=False, half=False):
         def run():
-            st = BlockStack(rng, hip, ops, joint_qkv=joint_qkv, fused=fused)
+            st = BlockStack(rng, hip, ops, joint_qkv=joint_qkv, fused=fused, half=half)
             res = st.measure(stream, 5, cached_kv=cached_kv)
-            res["variant"] = {"cached_kv": cached_kv, "fused_epilogues": fused, "joint_qkv": joint_qkv}
+            res["variant"] = {"cached_kv": cached_kv, "fused_epilogues": fused, "joint_qkv": joint_qkv,
+                              "fp16_activations": half}
             del st
             return res
         return run
@@ -466,6 +556,8 @@ def extras(rng, hip, ops, stream, reps, emit=None):
     part("block_stack_cached_kv", stack(cached_kv=True))
     part("block_stack_fused_epilogues", stack(fused=True))
     part("block_stack_joint_qkv", stack(joint_qkv=True))
+    part("block_stack_fp16_activations", stack(half=True))
+    part("block_stack_all_but_fp16_activations", stack(cached_kv=True, fused=True, joint_qkv=True))
     part("step_graph", step_graph)
     return out
 
@@ -618,7 +710,7 @@ def main() -> int:
     rng = np.random.default_rng(1)
     stream = hip.Stream()
     if args.only == "block":
-        stack = BlockStack(rng, hip, ops, joint_qkv=True, fused=True)
+        stack = BlockStack(rng, hip, ops, joint_qkv=True, fused=True, half=True)
         res = stack.measure(stream, max(args.steps // 4, 1), cached_kv=True)
         res["variant"] = BLOCK_VARIANT
         print(json.dumps({"block_stack": res}), flush=True)
@@ -750,11 +842,16 @@ def main() -> int:
     block, stack = None, None
     if args.only is None:
         print("[bench] config-4 block stack", file=sys.stderr, flush=True)
-        stack = BlockStack(rng, hip, ops, joint_qkv=True, fused=True)
+        stack = BlockStack(rng, hip, ops, joint_qkv=True, fused=True, half=True)
         block = stack.measure(stream, 5, cached_kv=True)
         block["variant"] = BLOCK_VARIANT
         print(f"[bench] block stack: {block['latency_ms']:.3f} ms for {block['blocks']} blocks "
               f"({block['tflops']:.1f} TFLOP/s)", file=sys.stderr, flush=True)
+        try:
+            block["kernel_share"] = stack.kernel_share(stream, block["ms_per_block"])
+        except Exception as e:  # noqa: BLE001 -- reported, not fatal
+            block["kernel_share"] = {"error": f"{type(e).__name__}: {e}"}
+        print(f"[bench] block kernel share: {block['kernel_share']}", file=sys.stderr, flush=True)
 
     del stack
 

@@ -221,6 +221,23 @@ int mi_gemm_nt_q8_split_ws(const float* A, const uint32_t* payload, const float*
 int mi_gemm_nt_q8_0_geglu(const float* A, const void* W, const float* bias, float* G, uint32_t M,
                           uint32_t F, uint32_t K, uint32_t lda, uint32_t ldg, void* stream);
 
+/* fp16 activations (extension, no reference counterpart: the reference keeps
+ * fp32 activations, sdvkgen.cpp:917-936). A holds IEEE binary16 values
+ * (uint16_t bits), 16-byte aligned, lda and sA multiples of 8. The GEMM
+ * rounds an fp32 A to fp16 when staging it, so a producer that stores fp16
+ * (the same RNE rounding of the same fp32 value) gives the fp32 entries'
+ * results bit for bit while moving half the bytes -- the config-4 block's
+ * LayerNorm, attention and GEGLU outputs, which only feed GEMMs.
+ * mi_gemm_nt_q8_0_f16a: mi_gemm_nt_q8_0_ws with fp16 A (workspace NULL: no
+ * K split). mi_gemm_nt_q8_0_geglu_f16: mi_gemm_nt_q8_0_geglu with fp16 A and
+ * G stored as fp16 (the fp32 result rounded once, RNE; G 8-byte aligned).  */
+int mi_gemm_nt_q8_0_f16a(const void* A, const void* W, const float* bias, float* C, uint32_t M,
+                         uint32_t N, uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldc,
+                         uint32_t batch, uint64_t sA, uint64_t sC, void* workspace,
+                         uint64_t workspace_bytes, void* stream);
+int mi_gemm_nt_q8_0_geglu_f16(const void* A, const void* W, const float* bias, void* G, uint32_t M,
+                              uint32_t F, uint32_t K, uint32_t lda, uint32_t ldg, void* stream);
+
 /* Q8 NN GEMM (the conv / 1x1 paths' weights-left product):
  *   C[M,N] (=|+=) deq(A[M,K]) . B[K,N]
  * A in the split layout, read at FLAT index fl = z*sA + m*lda + k: value
@@ -330,10 +347,18 @@ int mi_fused_attention_ws(const mi_attn_args* args, void* workspace, uint64_t wo
  * passes. gamma and beta both NULL (no affine) or both set. y may equal x. */
 int mi_layernorm(const float* x, const float* gamma, const float* beta, float* y, uint32_t rows,
                  uint32_t d, float eps, void* stream);
+/* mi_layernorm with y stored as fp16 (extension): each fp32 result rounded
+ * once (RNE), the value a following GEMM would stage from an fp32 y.
+ * d % 4 == 0, x and y 16-byte / 8-byte aligned; y must not overlap x.      */
+int mi_layernorm_f16(const float* x, const float* gamma, const float* beta, void* y, uint32_t rows,
+                     uint32_t d, float eps, void* stream);
 
 /* geglu (sdvkgen.cpp:1709-1720, unary_fwd.comp:28-36): h = [rows, 2F],
  * y[r, j] = h[r, j] * gelu_erf(h[r, F + j]), erf by Abramowitz-Stegun 7.1.26. */
 int mi_geglu(const float* h, float* y, uint32_t rows, uint32_t F, void* stream);
+/* mi_geglu with y stored as fp16 (extension; the fp32 result rounded once, RNE).
+ * F % 4 == 0, h 16-byte and y 8-byte aligned.                               */
+int mi_geglu_f16(const float* h, void* y, uint32_t rows, uint32_t F, void* stream);
 
 /* add2 in place (sdvkgen.cpp:1746,1751,1762): x[i] += a[i], i < n.         */
 int mi_add_inplace(float* x, const float* a, uint64_t n, void* stream);
@@ -356,7 +381,12 @@ int mi_add_inplace(float* x, const float* a, uint64_t n, void* stream);
  *   MI_BLOCK_JOINT_QKV: attn1_q / attn1_k / attn1_v are the three C x C parts
  *     of one [3C, C] Q8_0 matrix (attn1_k = attn1_q + C*(C/32)*34 bytes,
  *     attn1_v = attn1_k + as much; else MI_ERR_INVALID_ARG), projected by one
- *     GEMM.
+ *     GEMM;
+ *   MI_BLOCK_FP16_ACTIVATIONS: the tensors whose only consumer is a GEMM --
+ *     the LayerNorm outputs, the attention outputs and the GEGLU output --
+ *     are stored as fp16 (each fp32 value rounded once, RNE, which is what the
+ *     GEMM's A staging does to an fp32 tensor) and read by the fp16-A GEMM:
+ *     half the bytes, no conversion in the GEMM.
  * Every flag combination computes the same bits (the block sums in a fixed
  * order, and the GEMMs that differ between the variants never split K).   */
 typedef struct mi_block_weights {
@@ -373,7 +403,7 @@ typedef struct mi_block_weights {
     const float* ff_down_b;                                  /* [channels] or NULL */
 } mi_block_weights;
 
-enum { MI_BLOCK_FUSED_EPILOGUES = 1, MI_BLOCK_JOINT_QKV = 2 };
+enum { MI_BLOCK_FUSED_EPILOGUES = 1, MI_BLOCK_JOINT_QKV = 2, MI_BLOCK_FP16_ACTIVATIONS = 4 };
 
 typedef struct mi_block_dims {
     uint32_t batch, tokens, channels, heads, ctx_tokens, ctx_channels, ff_inner;

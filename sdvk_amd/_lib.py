@@ -50,7 +50,7 @@ class MiBlockDims(ctypes.Structure):
                                     "ff_inner", "flags")]
 
 
-MI_BLOCK_FUSED_EPILOGUES, MI_BLOCK_JOINT_QKV = 1, 2
+MI_BLOCK_FUSED_EPILOGUES, MI_BLOCK_JOINT_QKV, MI_BLOCK_FP16_ACTIVATIONS = 1, 2, 4
 
 
 class MiGgufTensorInfo(ctypes.Structure):
@@ -88,6 +88,9 @@ SIGNATURES = {
     "mi_gemm_nt_q8_split_ws": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32,
                                               _u32, _u64, _u64, _vp, _u64, _vp]),
     "mi_gemm_nt_q8_0_geglu": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp]),
+    "mi_gemm_nt_q8_0_geglu_f16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp]),
+    "mi_gemm_nt_q8_0_f16a": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u64, _u64,
+                                            _vp, _u64, _vp]),
     "mi_gemm_nn_q8_split": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32,
                                            _u64, _u64, _u64, _vp]),
     "mi_gemm_nn_q8_workspace_bytes": (_u64, [_u32, _u32, _u32, _u32]),
@@ -99,7 +102,9 @@ SIGNATURES = {
     "mi_fused_attention_ws_bytes": (ctypes.c_uint64, [ctypes.POINTER(MiAttnArgs)]),
     "mi_fused_attention_ws": (ctypes.c_int, [ctypes.POINTER(MiAttnArgs), _vp, ctypes.c_uint64, _vp]),
     "mi_layernorm": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, ctypes.c_float, _vp]),
+    "mi_layernorm_f16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, ctypes.c_float, _vp]),
     "mi_geglu": (ctypes.c_int, [_vp, _vp, _u32, _u32, _vp]),
+    "mi_geglu_f16": (ctypes.c_int, [_vp, _vp, _u32, _u32, _vp]),
     "mi_add_inplace": (ctypes.c_int, [_vp, _vp, _u64, _vp]),
     "mi_block_workspace_bytes": (_u64, [ctypes.POINTER(MiBlockDims)]),
     "mi_sdxl_block_forward": (ctypes.c_int, [ctypes.POINTER(MiBlockWeights), ctypes.POINTER(MiBlockDims), _vp, _vp,

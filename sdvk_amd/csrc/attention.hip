@@ -143,6 +143,18 @@ __device__ __forceinline__ uint32_t tile_bytes(uint32_t kv0, uint32_t L, uint64_
     return static_cast<uint32_t>(((rows - 1) * ld + hd) * esz);
 }
 
+// Four outputs o * inv as fp16: the fp32 products rounded once each (RNE),
+// the values an fp32 output would round to in a consumer that stages it as
+// fp16 (the block's out-projection GEMM). The empty register constraint keeps the rounding
+// from fusing into the multiply (a mixed-precision multiply rounds the exact
+// product once, which can differ).
+__device__ __forceinline__ half4 half4_of(float a, float b, float c, float d) {
+    floatx4 v = {a, b, c, d};
+    asm volatile("" : "+v"(v));
+    return half4{static_cast<_Float16>(v[0]), static_cast<_Float16>(v[1]), static_cast<_Float16>(v[2]),
+                 static_cast<_Float16>(v[3])};
+}
+
 // 16 bytes per lane from a buffer into LDS (lane l's bytes land at lds + 16 l).
 __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voffset) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, 0, 0, 0);
@@ -180,9 +192,8 @@ __device__ __forceinline__ void store_o_rows(const floatx16* o, float inv, char*
                 *reinterpret_cast<floatx4*>(p) =
                     floatx4{o[u][4 * run] * inv, o[u][4 * run + 1] * inv, o[u][4 * run + 2] * inv, o[u][4 * run + 3] * inv};
             } else {
-                *reinterpret_cast<half4*>(p) =
-                    half4{static_cast<_Float16>(o[u][4 * run] * inv), static_cast<_Float16>(o[u][4 * run + 1] * inv),
-                          static_cast<_Float16>(o[u][4 * run + 2] * inv), static_cast<_Float16>(o[u][4 * run + 3] * inv)};
+                *reinterpret_cast<half4*>(p) = half4_of(o[u][4 * run] * inv, o[u][4 * run + 1] * inv,
+                                                        o[u][4 * run + 2] * inv, o[u][4 * run + 3] * inv);
             }
         }
     __builtin_amdgcn_wave_barrier();
@@ -498,9 +509,8 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
                     *reinterpret_cast<floatx4*>(Op + d0) =
                         floatx4{o[u][4 * run] * inv, o[u][4 * run + 1] * inv, o[u][4 * run + 2] * inv, o[u][4 * run + 3] * inv};
                 } else {
-                    *reinterpret_cast<half4*>(Op + d0) =
-                        half4{static_cast<_Float16>(o[u][4 * run] * inv), static_cast<_Float16>(o[u][4 * run + 1] * inv),
-                              static_cast<_Float16>(o[u][4 * run + 2] * inv), static_cast<_Float16>(o[u][4 * run + 3] * inv)};
+                    *reinterpret_cast<half4*>(Op + d0) = half4_of(o[u][4 * run] * inv, o[u][4 * run + 1] * inv,
+                                                                  o[u][4 * run + 2] * inv, o[u][4 * run + 3] * inv);
                 }
             } else {
 #pragma unroll
@@ -933,9 +943,8 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
                 *reinterpret_cast<floatx4*>(Op + d0) =
                     floatx4{o[u][4 * run] * inv, o[u][4 * run + 1] * inv, o[u][4 * run + 2] * inv, o[u][4 * run + 3] * inv};
             } else {
-                *reinterpret_cast<half4*>(Op + d0) =
-                    half4{static_cast<_Float16>(o[u][4 * run] * inv), static_cast<_Float16>(o[u][4 * run + 1] * inv),
-                          static_cast<_Float16>(o[u][4 * run + 2] * inv), static_cast<_Float16>(o[u][4 * run + 3] * inv)};
+                *reinterpret_cast<half4*>(Op + d0) = half4_of(o[u][4 * run] * inv, o[u][4 * run + 1] * inv,
+                                                              o[u][4 * run + 2] * inv, o[u][4 * run + 3] * inv);
             }
         }
 }
@@ -975,9 +984,8 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, uint32_t qt
     acc1 *= inv;
     TO* Op = static_cast<TO*>(a.o) + b * a.so + static_cast<uint64_t>(qi) * a.ldo + static_cast<uint64_t>(h) * a.hd + c;
     if constexpr (sizeof(TO) == 2) {
-        const half8 v = {static_cast<_Float16>(acc0[0]), static_cast<_Float16>(acc0[1]), static_cast<_Float16>(acc0[2]),
-                         static_cast<_Float16>(acc0[3]), static_cast<_Float16>(acc1[0]), static_cast<_Float16>(acc1[1]),
-                         static_cast<_Float16>(acc1[2]), static_cast<_Float16>(acc1[3])};
+        const half4 v0 = half4_of(acc0[0], acc0[1], acc0[2], acc0[3]), v1 = half4_of(acc1[0], acc1[1], acc1[2], acc1[3]);
+        const half8 v = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
         if (a.ostage) {
             *reinterpret_cast<half8*>(Op) = v;
         } else {

@@ -75,7 +75,7 @@ int check_dims(const mi_block_dims& d, const char* fn) {
                     d.heads);
     if (d.channels % 32 || d.ctx_channels % 32 || d.ff_inner % 32)
         return fail(MI_ERR_UNSUPPORTED, "%s: channels, ctx_channels and ff_inner must be multiples of 32 (Q8_0 K)", fn);
-    if (d.flags & ~static_cast<uint32_t>(MI_BLOCK_FUSED_EPILOGUES | MI_BLOCK_JOINT_QKV))
+    if (d.flags & ~static_cast<uint32_t>(MI_BLOCK_FUSED_EPILOGUES | MI_BLOCK_JOINT_QKV | MI_BLOCK_FP16_ACTIVATIONS))
         return fail(MI_ERR_INVALID_ARG, "%s: unknown flags 0x%x", fn, d.flags);
     return MI_OK;
 }
@@ -86,9 +86,10 @@ int check_dims(const mi_block_dims& d, const char* fn) {
         if (st_ != MI_OK) return st_; \
     } while (0)
 
-// ld: token stride of q, k and v (C, or 3C for the joint Q/K/V projection)
-int attention(const mi_block_dims& d, const float* q, const float* k, const float* v, uint64_t ld, float* o,
-              uint32_t tk, const int32_t* kv_len, hipStream_t s) {
+// ld: token stride of q, k and v (C, or 3C for the joint Q/K/V projection);
+// o_half: the output stored as fp16
+int attention(const mi_block_dims& d, const float* q, const float* k, const float* v, uint64_t ld, void* o,
+              uint32_t tk, const int32_t* kv_len, bool o_half, hipStream_t s) {
     mi_attn_args x{};
     x.q = q;
     x.k = k;
@@ -103,7 +104,7 @@ int attention(const mi_block_dims& d, const float* q, const float* k, const floa
     x.C = d.channels;
     x.heads = d.heads;
     x.in_dtype = MI_F32;
-    x.out_dtype = MI_F32;
+    x.out_dtype = o_half ? MI_F16 : MI_F32;
     x.kv_len = kv_len;
     // the output only feeds the out-projection GEMM, which rounds its A
     // operand to fp16: one fp16 P product (2^-11 per weight) is below that
@@ -158,33 +159,46 @@ int forward(const mi_block_weights& w, const mi_block_dims& d, float* x, const f
 
     const uint32_t rows = d.batch * d.tokens, C = d.channels;
     const uint64_t nx = static_cast<uint64_t>(rows) * C;
-    auto gemm = [&](const float* A, const void* W, const float* bias, float* out, uint32_t M, uint32_t N, uint32_t K) {
-        return mi_gemm_nt_q8_0(A, W, bias, out, M, N, K, 0, 0, 0, 1, 0, 0, s);
-    };
     const bool fused = (d.flags & MI_BLOCK_FUSED_EPILOGUES) != 0;
+    // fp16 activations: n (LayerNorm out), o (attention out) and g (GEGLU out)
+    // hold fp16 and feed the fp16-A GEMM (same bits as fp32 + staging)
+    const bool half = (d.flags & MI_BLOCK_FP16_ACTIVATIONS) != 0;
+    auto gemm = [&](const void* A, const void* W, const float* bias, float* out, uint32_t M, uint32_t N, uint32_t K) {
+        if (half) return mi_gemm_nt_q8_0_f16a(A, W, bias, out, M, N, K, 0, 0, 0, 1, 0, 0, nullptr, 0, s);
+        return mi_gemm_nt_q8_0(static_cast<const float*>(A), W, bias, out, M, N, K, 0, 0, 0, 1, 0, 0, s);
+    };
+    auto gemm_ws = [&](const void* A, const void* W, const float* bias, float* out, uint32_t K, uint32_t mode) {
+        if (half) return mi_gemm_nt_q8_0_f16a(A, W, bias, out, rows, C, K, mode, 0, 0, 1, 0, 0, ws.split,
+                                              ws.split_bytes, s);
+        return mi_gemm_nt_q8_0_ws(static_cast<const float*>(A), W, bias, out, rows, C, K, mode, 0, 0, 1, 0, 0,
+                                  ws.split, ws.split_bytes, s);
+    };
+    auto layernorm = [&](const float* g, const float* b) {
+        return half ? mi_layernorm_f16(x, g, b, ws.n, rows, C, 1e-5f, s) : mi_layernorm(x, g, b, ws.n, rows, C, 1e-5f, s);
+    };
     // x += A . W^T + bias: one GEMM with the residual epilogue, or GEMM + add;
     // both split K the same way (the workspace's partials region)
-    auto residual = [&](const float* A, const void* W, const float* bias, uint32_t K) {
-        if (fused) return mi_gemm_nt_q8_0_ws(A, W, bias, x, rows, C, K, 2, 0, 0, 1, 0, 0, ws.split, ws.split_bytes, s);
-        const int st = mi_gemm_nt_q8_0_ws(A, W, bias, ws.a, rows, C, K, 0, 0, 0, 1, 0, 0, ws.split, ws.split_bytes, s);
+    auto residual = [&](const void* A, const void* W, const float* bias, uint32_t K) {
+        if (fused) return gemm_ws(A, W, bias, x, K, 2);
+        const int st = gemm_ws(A, W, bias, ws.a, K, 0);
         return st != MI_OK ? st : mi_add_inplace(x, ws.a, nx, s);
     };
 
     // self-attention
-    MI_TRY(mi_layernorm(x, w.norm1_w, w.norm1_b, ws.n, rows, C, 1e-5f, s));
+    MI_TRY(layernorm(w.norm1_w, w.norm1_b));
     // the joint result [rows, 3C] goes to the FF-up region, free until the FF stage
     if (d.flags & MI_BLOCK_JOINT_QKV) {
         MI_TRY(gemm(ws.n, w.attn1_q, nullptr, ws.h, rows, 3 * C, C));
-        MI_TRY(attention(d, ws.h, ws.h + C, ws.h + 2 * C, 3ull * C, ws.o, d.tokens, nullptr, s));
+        MI_TRY(attention(d, ws.h, ws.h + C, ws.h + 2 * C, 3ull * C, ws.o, d.tokens, nullptr, half, s));
     } else {
         MI_TRY(gemm(ws.n, w.attn1_q, nullptr, ws.q, rows, C, C));
         MI_TRY(gemm(ws.n, w.attn1_k, nullptr, ws.k, rows, C, C));
         MI_TRY(gemm(ws.n, w.attn1_v, nullptr, ws.v, rows, C, C));
-        MI_TRY(attention(d, ws.q, ws.k, ws.v, C, ws.o, d.tokens, nullptr, s));
+        MI_TRY(attention(d, ws.q, ws.k, ws.v, C, ws.o, d.tokens, nullptr, half, s));
     }
     MI_TRY(residual(ws.o, w.attn1_out, w.attn1_out_b, C));
     // cross-attention over the context
-    MI_TRY(mi_layernorm(x, w.norm2_w, w.norm2_b, ws.n, rows, C, 1e-5f, s));
+    MI_TRY(layernorm(w.norm2_w, w.norm2_b));
     MI_TRY(gemm(ws.n, w.attn2_q, nullptr, ws.q, rows, C, C));
     const float *ck = ws.k, *cv = ws.v;
     if (kv) {
@@ -193,15 +207,17 @@ int forward(const mi_block_weights& w, const mi_block_dims& d, float* x, const f
     } else {
         MI_TRY(ctx_kv(w, d, ctx, ws.k, ws.v, s));
     }
-    MI_TRY(attention(d, ws.q, ck, cv, C, ws.o, d.ctx_tokens, ctx_len, s));
+    MI_TRY(attention(d, ws.q, ck, cv, C, ws.o, d.ctx_tokens, ctx_len, half, s));
     MI_TRY(residual(ws.o, w.attn2_out, w.attn2_out_b, C));
     // GEGLU feed-forward
-    MI_TRY(mi_layernorm(x, w.norm3_w, w.norm3_b, ws.n, rows, C, 1e-5f, s));
+    MI_TRY(layernorm(w.norm3_w, w.norm3_b));
     if (fused) {
-        MI_TRY(mi_gemm_nt_q8_0_geglu(ws.n, w.ff_up, w.ff_up_b, ws.g, rows, d.ff_inner, C, 0, 0, s));
+        if (half) MI_TRY(mi_gemm_nt_q8_0_geglu_f16(ws.n, w.ff_up, w.ff_up_b, ws.g, rows, d.ff_inner, C, 0, 0, s));
+        else MI_TRY(mi_gemm_nt_q8_0_geglu(ws.n, w.ff_up, w.ff_up_b, ws.g, rows, d.ff_inner, C, 0, 0, s));
     } else {
         MI_TRY(gemm(ws.n, w.ff_up, w.ff_up_b, ws.h, rows, 2 * d.ff_inner, C));
-        MI_TRY(mi_geglu(ws.h, ws.g, rows, d.ff_inner, s));
+        if (half) MI_TRY(mi_geglu_f16(ws.h, ws.g, rows, d.ff_inner, s));
+        else MI_TRY(mi_geglu(ws.h, ws.g, rows, d.ff_inner, s));
     }
     MI_TRY(residual(ws.g, w.ff_down, w.ff_down_b, d.ff_inner));
     return MI_OK;

@@ -50,6 +50,7 @@ struct GemmArgs {
     uint32_t cvec;          // C rows 16-byte aligned (C % 16 == 0, ldc % 4 == 0, sC % 4 == 0)
     uint32_t bvec;          // bias 16-byte aligned
     uint32_t F;             // GEGLU epilogue: output columns (W has 2F rows: value rows, then gate rows)
+    uint32_t out_half;      // GEGLU epilogue: G stored as fp16 (ldc in halves), the fp32 result rounded once
     uint64_t split_stride;  // K-split partials: elements between the planes of consecutive splits
 };
 
@@ -227,7 +228,22 @@ __device__ __forceinline__ void store_tiles(const GemmArgs& a, float* C, float* 
                     const float bv = a.bias ? a.bias[j] : 0.0f, bg = a.bias ? a.bias[a.F + j] : 0.0f;
                     o[e] = (v[e] + bv) * gelu_erf(gt[e] + bg);
                 }
-                if (vec && n + 3 < a.F) {
+                if (a.out_half) {
+                    // the fp32 value, then one RNE rounding to fp16 (the value an
+                    // fp32 G would give the next GEMM's A staging); the empty register
+                    // constraint keeps the rounding from fusing into the multiply
+                    asm volatile("" : "+v"(o));
+                    _Float16* ch = reinterpret_cast<_Float16*>(C) + static_cast<uint64_t>(m) * a.ldc + n;
+                    const half4 h = {static_cast<_Float16>(o[0]), static_cast<_Float16>(o[1]),
+                                     static_cast<_Float16>(o[2]), static_cast<_Float16>(o[3])};
+                    if (vec && n + 3 < a.F) {
+                        *reinterpret_cast<half4*>(ch) = h;
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (n + e < a.F) ch[e] = h[e];
+                    }
+                } else if (vec && n + 3 < a.F) {
                     __builtin_nontemporal_store(o, reinterpret_cast<floatx4*>(c));
                 } else {
 #pragma unroll
@@ -277,14 +293,22 @@ __device__ __forceinline__ void store_tiles(const GemmArgs& a, float* C, float* 
     }
 }
 
-template <int BM, int BN, int WM, int WN, int KB, int WK, bool SPLITK, bool KTAIL, int PF, int EPI = kEpiPlain>
+// AH: A holds fp16 values (fp16 activations from a producer that rounded them
+// already); the staging then copies 16-byte units of 8 halves into LDS with no
+// conversion. Otherwise A is fp32 and each 16-byte unit of 4 floats is rounded
+// to fp16 (RNE) on its way to LDS: for A values that are fp16 numbers both
+// paths stage the same bits.
+template <int BM, int BN, int WM, int WN, int KB, int WK, bool SPLITK, bool KTAIL, int PF, int EPI = kEpiPlain,
+          bool AH = false>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     constexpr int NT = WM * WN * 64;
     constexpr int BK = 32 * KB;
     constexpr int LDK = BK + 8;                   // LDS row stride in halves (16-B pad)
     constexpr int TM = BM / WM, TN = BN / WN;     // wave tile
     constexpr int FM = TM / 32, FN = TN / 32;     // 32x32 MFMA tiles per wave
-    constexpr int A_UNITS = BM * BK / 4;          // float4 per step
+    constexpr int AE = AH ? 2 : 4;                // bytes per A element
+    constexpr int AV = 16 / AE;                   // A elements per 16-byte unit
+    constexpr int A_UNITS = BM * BK / AV;         // 16-byte A units per step
     constexpr int A_IT = A_UNITS / NT;
     constexpr int W_UNITS = BN * BK / 8;          // (row, 8-k group) per step
     constexpr int W_IT = W_UNITS / NT;
@@ -340,11 +364,12 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
 
     // Per-thread byte offsets, fixed for the whole K loop. Rows past M / N read
     // the last valid row: they only feed outputs that are never stored.
-    const float* Apanel = a.A + static_cast<uint64_t>(blockIdx.z) * a.sA + static_cast<uint64_t>(m0) * a.lda;
+    const char* Apanel = reinterpret_cast<const char*>(a.A) +
+                         (static_cast<uint64_t>(blockIdx.z) * a.sA + static_cast<uint64_t>(m0) * a.lda) * AE;
     // the range covers exactly the panel's rows: a read past them returns zeros, never faults
-    const uint32_t a_bytes = ((min(a.M - m0, static_cast<uint32_t>(BM)) - 1) * a.lda + a.K) * 4;
+    const uint32_t a_bytes = ((min(a.M - m0, static_cast<uint32_t>(BM)) - 1) * a.lda + a.K) * AE;
     const __amdgpu_buffer_rsrc_t rA =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Apanel), 0, static_cast<int>(a_bytes), 0x00020000);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(Apanel), 0, static_cast<int>(a_bytes), 0x00020000);
     // 34-byte layout: records up to W's 16-byte-aligned end (the documented
     // read extent); the range check zeroes whole dwords only past that.
     const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc(
@@ -356,8 +381,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < A_IT; ++i) {
         const int f = tid + i * NT;
-        const uint32_t row = min(m0 + f / (BK / 4), a.M - 1) - m0;
-        a_off[i] = (row * a.lda + (f % (BK / 4)) * 4) * 4;
+        const uint32_t row = min(m0 + f / (BK / AV), a.M - 1) - m0;
+        a_off[i] = (row * a.lda + (f % (BK / AV)) * AV) * AE;
     }
     uint32_t w_off[W_IT];   // blocks: byte of the unit's first q; split: flat element
     uint32_t w_aux[W_IT];   // blocks: byte of the block's scale; split: byte of the scale
@@ -421,11 +446,11 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < A_IT; ++i) {
             if constexpr (KTAIL) {
-                const uint32_t k = ks * BK + ((tid + i * NT) % (BK / 4)) * 4;
+                const uint32_t k = ks * BK + ((tid + i * NT) % (BK / AV)) * AV;
                 areg_[rs][i] = floatx4{0.f, 0.f, 0.f, 0.f};
-                if (k < a.K) areg_[rs][i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rA, a_off[i], ks * BK * 4, 0));
+                if (k < a.K) areg_[rs][i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rA, a_off[i], ks * BK * AE, 0));
             } else {
-                areg_[rs][i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rA, a_off[i], ks * BK * 4, 0));
+                areg_[rs][i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rA, a_off[i], ks * BK * AE, 0));
             }
         }
         if constexpr (WBLK) {
@@ -487,12 +512,17 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < A_IT; ++i) {
             const int f = tid + i * NT;
-            half4 h;
-            h[0] = static_cast<_Float16>(areg_[rs][i][0]);
-            h[1] = static_cast<_Float16>(areg_[rs][i][1]);
-            h[2] = static_cast<_Float16>(areg_[rs][i][2]);
-            h[3] = static_cast<_Float16>(areg_[rs][i][3]);
-            *reinterpret_cast<half4*>(&As[st][(f / (BK / 4)) * LDK + (f % (BK / 4)) * 4]) = h;
+            if constexpr (AH) {
+                *reinterpret_cast<half8*>(&As[st][(f / (BK / 8)) * LDK + (f % (BK / 8)) * 8]) =
+                    __builtin_bit_cast(half8, areg_[rs][i]);
+            } else {
+                half4 h;
+                h[0] = static_cast<_Float16>(areg_[rs][i][0]);
+                h[1] = static_cast<_Float16>(areg_[rs][i][1]);
+                h[2] = static_cast<_Float16>(areg_[rs][i][2]);
+                h[3] = static_cast<_Float16>(areg_[rs][i][3]);
+                *reinterpret_cast<half4*>(&As[st][(f / (BK / 4)) * LDK + (f % (BK / 4)) * 4]) = h;
+            }
         }
         if constexpr (WHALF) {
             const uint32_t* x = wbx_[rs][0];
@@ -589,7 +619,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     constexpr int kRead0 = FM + FN;                  // fragment reads of the first k16 slice
     constexpr int kReads = (FM + FN) * (BK / 16);    // all fragment reads of a step
     constexpr int kWrites = A_IT + (WHALF ? 2 : WBLK ? 4 * WB_IT : W_IT);              // LDS writes of the store phase
-    constexpr int kValu = A_IT * 2 + (WHALF ? 36 : WBLK ? 60 * WB_IT : W_IT * 16);   // conversions + dequant (approx.)
+    constexpr int kValu = (AH ? 0 : A_IT * 2) + (WHALF ? 36 : WBLK ? 60 * WB_IT : W_IT * 16);  // conversions + dequant (approx.)
     // Every workgroup sweeps K in the same order, so the workgroups that share
     // a panel read the same K slice at about the same time (L2 reuse).
     const uint32_t n_steps = s_end - s_begin;
@@ -814,7 +844,7 @@ void finish_split(const GemmArgs& a, uint32_t splits, const float* ws, uint32_t 
 // SPLIT = false: a build without a K-split variant (requested splits are ignored).
 // splits > 1 needs ws: batch * splits * M * N floats (split_workspace_floats).
 template <int BM, int BN, int WM, int WN, int KB, int WK, bool KTAIL, int PF = 2, int EPI = kEpiPlain,
-          bool SPLIT = true>
+          bool SPLIT = true, bool AH = false>
 void launch_cfg(const GemmArgs& a0, uint32_t batch, uint32_t splits, float* ws, hipStream_t s) {
     GemmArgs a = a0;
     // GEGLU: BN / 2 outputs per tile, and the epilogue needs the whole K sum
@@ -831,27 +861,29 @@ void launch_cfg(const GemmArgs& a0, uint32_t batch, uint32_t splits, float* ws, 
     if (splits > 1) {
         if constexpr (EPI != kEpiGeglu && SPLIT) {
             const GemmArgs p = partial_args(a, splits, ws);
-            gemm_q8_kernel<BM, BN, WM, WN, KB, WK, true, KTAIL, PF><<<dim3(tiles, splits, batch), WM * WN * 64, 0, s>>>(p);
+            gemm_q8_kernel<BM, BN, WM, WN, KB, WK, true, KTAIL, PF, kEpiPlain, AH>
+                <<<dim3(tiles, splits, batch), WM * WN * 64, 0, s>>>(p);
             finish_split<EPI>(a, splits, ws, batch, s);
         }
     } else {
         a.steps_per_split = a.ksteps;
-        gemm_q8_kernel<BM, BN, WM, WN, KB, WK, false, KTAIL, PF, EPI><<<dim3(tiles, 1, batch), WM * WN * 64, 0, s>>>(a);
+        gemm_q8_kernel<BM, BN, WM, WN, KB, WK, false, KTAIL, PF, EPI, AH>
+            <<<dim3(tiles, 1, batch), WM * WN * 64, 0, s>>>(a);
     }
 }
 
-template <int WK, int EPI = kEpiPlain>
+template <int WK, int EPI = kEpiPlain, bool AH = false>
 void launch(int cfg, const GemmArgs& a, uint32_t batch, uint32_t splits, float* ws, hipStream_t s) {
     switch (cfg) {
-        case kC256x128: launch_cfg<256, 128, 4, 2, 2, WK, false, 2, EPI>(a, batch, splits, ws, s); break;
+        case kC256x128: launch_cfg<256, 128, 4, 2, 2, WK, false, 2, EPI, true, AH>(a, batch, splits, ws, s); break;
         case kC128x128:
             // one register set: the loop then issues most of a step's MFMAs before
             // converting the next step's loads (8192x640x2560 58 vs 68 us with two
             // sets, 2048x1280x5120 71 vs 76, 8192x640x640 20 vs 22, the rest equal)
-            launch_cfg<128, 128, 2, 2, 2, WK, false, 1, EPI>(a, batch, splits, ws, s);
+            launch_cfg<128, 128, 2, 2, 2, WK, false, 1, EPI, true, AH>(a, batch, splits, ws, s);
             break;
-        case kC192x256: launch_cfg<192, 256, 2, 4, 2, WK, false, 2, EPI>(a, batch, splits, ws, s); break;
-        case kC128x64: launch_cfg<128, 64, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, ws, s); break;
+        case kC192x256: launch_cfg<192, 256, 2, 4, 2, WK, false, 2, EPI, true, AH>(a, batch, splits, ws, s); break;
+        case kC128x64: launch_cfg<128, 64, 2, 2, 2, WK, false, 2, EPI, true, AH>(a, batch, splits, ws, s); break;
         case kC256x256:
             // The split layout's and the GEGLU epilogue's 256x256 builds need
             // more than the 256 VGPRs of a wave at two waves per SIMD: the
@@ -859,20 +891,20 @@ void launch(int cfg, const GemmArgs& a, uint32_t batch, uint32_t splits, float* 
             // scratch reload waits for all global loads in flight. They run
             // 256x128 tiles instead.
             if constexpr (WK == kSplit || EPI == kEpiGeglu)
-                launch_cfg<256, 128, 4, 2, 2, WK, false, 2, EPI>(a, batch, splits, ws, s);
+                launch_cfg<256, 128, 4, 2, 2, WK, false, 2, EPI, true, AH>(a, batch, splits, ws, s);
             else
-                launch_cfg<256, 256, 4, 2, 2, WK, false, 1, EPI>(a, batch, splits, ws, s);
+                launch_cfg<256, 256, 4, 2, 2, WK, false, 1, EPI, true, AH>(a, batch, splits, ws, s);
             break;
-        default: launch_cfg<64, 64, 2, 2, 2, WK, false, 2, EPI>(a, batch, splits, ws, s); break;
+        default: launch_cfg<64, 64, 2, 2, 2, WK, false, 2, EPI, true, AH>(a, batch, splits, ws, s); break;
     }
 }
 
 // General K (K % 64 != 0): one block column per step, 64x64 tiles; the split
 // layout with K % 32 != 0 also zero-fills the partial last step.
-template <int WK, int EPI = kEpiPlain>
+template <int WK, int EPI = kEpiPlain, bool AH = false>
 void launch_general(const GemmArgs& a, uint32_t batch, uint32_t splits, float* ws, hipStream_t s) {
-    if (a.K % 32 == 0) launch_cfg<64, 64, 2, 2, 1, WK, false, 2, EPI>(a, batch, splits, ws, s);
-    else launch_cfg<64, 64, 2, 2, 1, WK, true, 2, EPI>(a, batch, splits, ws, s);
+    if (a.K % 32 == 0) launch_cfg<64, 64, 2, 2, 1, WK, false, 2, EPI, true, AH>(a, batch, splits, ws, s);
+    else launch_cfg<64, 64, 2, 2, 1, WK, true, 2, EPI, true, AH>(a, batch, splits, ws, s);
 }
 
 constexpr int kCUs = 256;
@@ -939,10 +971,10 @@ Plan plan_for(uint32_t M, uint32_t N, uint32_t K, uint32_t batch, const void* ws
     return p;
 }
 
-template <int WK, int EPI = kEpiPlain>
+template <int WK, int EPI = kEpiPlain, bool AH = false>
 void dispatch(const GemmArgs& a, uint32_t batch, const Plan& p, float* ws, hipStream_t s) {
-    if (a.K % 64 != 0) launch_general<WK, EPI>(a, batch, p.splits, ws, s);
-    else launch<WK, EPI>(p.cfg, a, batch, p.splits, ws, s);
+    if (a.K % 64 != 0) launch_general<WK, EPI, AH>(a, batch, p.splits, ws, s);
+    else launch<WK, EPI, AH>(p.cfg, a, batch, p.splits, ws, s);
 }
 
 // ---- any-K kernel (split layout) ---------------------------------------------------
@@ -1011,8 +1043,10 @@ __global__ __launch_bounds__(256) void gemm_q8_any_kernel(GemmArgs a) {
 // vec_a: the tiled kernels' A path (16-byte loads) -- A 16-byte aligned, lda
 // and sA multiples of 4; otherwise A only needs 4-byte alignment (the any-K
 // kernel of the split layout).
-int validate(const char* fn, const float* A, const void* W, const float* C, uint32_t M, uint32_t N, uint32_t K,
-             uint32_t mode, uint32_t& lda, uint32_t& ldc, uint32_t batch, uint64_t sA, uint64_t sC, bool vec_a) {
+// a_half: A is fp16 (the 16-byte path then needs lda and sA multiples of 8).
+int validate(const char* fn, const void* A, const void* W, const void* C, uint32_t M, uint32_t N, uint32_t K,
+             uint32_t mode, uint32_t& lda, uint32_t& ldc, uint32_t batch, uint64_t sA, uint64_t sC, bool vec_a,
+             bool a_half = false) {
     if (!A || !W || !C) return fail(MI_ERR_INVALID_ARG, "%s: null pointer", fn);
     if (mode > 2)
         return fail(MI_ERR_INVALID_ARG, "%s: mode %u (0 = store, 1 = accumulate, 2 = accumulate + bias)", fn, mode);
@@ -1021,8 +1055,9 @@ int validate(const char* fn, const float* A, const void* W, const float* C, uint
     if (lda == 0) lda = K;
     if (ldc == 0) ldc = N;
     if (lda < K || ldc < N) return fail(MI_ERR_INVALID_ARG, "%s: lda %u < K %u or ldc %u < N %u", fn, lda, K, ldc, N);
-    if (vec_a && (!aligned(A, 16) || lda % 4 || sA % 4))
-        return fail(MI_ERR_ALIGNMENT, "%s: A must be 16-byte aligned, lda and sA multiples of 4", fn);
+    const uint32_t av = a_half ? 8 : 4;  // elements per 16-byte unit
+    if (vec_a && (!aligned(A, 16) || lda % av || sA % av))
+        return fail(MI_ERR_ALIGNMENT, "%s: A must be 16-byte aligned, lda and sA multiples of %u", fn, av);
     if (!aligned(A, 4)) return fail(MI_ERR_ALIGNMENT, "%s: A must be 4-byte aligned", fn);
     if (!aligned(C, 4)) return fail(MI_ERR_ALIGNMENT, "%s: C must be 4-byte aligned", fn);
     // per-workgroup A offsets are 32-bit: a 256-row panel must stay below 4 GiB
@@ -1045,18 +1080,20 @@ int check_ws(const char* fn, const void* ws, uint64_t ws_bytes, const void* A, u
 // fixed_ws: `ws` is the library's fixed-size scratch (the no-allocation
 // entry): a plan whose K-split partials exceed it is an error, not a reason to
 // run unsplit, so that the entry's results always equal the workspace entry's.
-int gemm_blocks(const char* fn, const float* A, const void* W, const float* bias, float* C, uint32_t M, uint32_t N,
+// a_half: A holds fp16 values (mi_gemm_nt_q8_0_f16a), else fp32.
+int gemm_blocks(const char* fn, const void* A, const void* W, const float* bias, float* C, uint32_t M, uint32_t N,
                 uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldc, uint32_t batch, uint64_t sA, uint64_t sC,
-                void* ws, uint64_t ws_bytes, hipStream_t stream, bool fixed_ws = false) {
+                void* ws, uint64_t ws_bytes, hipStream_t stream, bool fixed_ws = false, bool a_half = false) {
     if (M == 0 || N == 0) return MI_OK;
     if (K % 32) return fail(MI_ERR_UNSUPPORTED, "%s: K=%u is not a multiple of 32 (Q8_0 block)", fn, K);
-    int st = validate(fn, A, W, C, M, N, K, mode, lda, ldc, batch, sA, sC, true);
+    int st = validate(fn, A, W, C, M, N, K, mode, lda, ldc, batch, sA, sC, true, a_half);
     if (st) return st;
     if (!aligned(W, 16)) return fail(MI_ERR_ALIGNMENT, "%s: W must be 16-byte aligned", fn);
     const uint64_t wbytes = static_cast<uint64_t>(N) * (K / 32) * 34;
     if (wbytes + 16 >= (uint64_t(1) << 32)) return fail(MI_ERR_UNSUPPORTED, "%s: weight >= 4 GiB", fn);
     const uint64_t cbytes = (static_cast<uint64_t>(batch - 1) * sC + static_cast<uint64_t>(M - 1) * ldc + N) * 4;
-    const uint64_t abytes = (static_cast<uint64_t>(batch - 1) * sA + static_cast<uint64_t>(M - 1) * lda + K) * 4;
+    const uint64_t abytes =
+        (static_cast<uint64_t>(batch - 1) * sA + static_cast<uint64_t>(M - 1) * lda + K) * (a_half ? 2 : 4);
     if (overlaps(C, cbytes, A, abytes) || overlaps(C, cbytes, W, wbytes) || overlaps(C, cbytes, bias, uint64_t(N) * 4))
         return fail(MI_ERR_ALIASING, "%s: C overlaps an input", fn);
     st = check_ws(fn, ws, ws_bytes, A, abytes, W, wbytes, C, cbytes, bias, N);
@@ -1075,11 +1112,17 @@ int gemm_blocks(const char* fn, const float* A, const void* W, const float* bias
                         fn, M, N, K, batch, want.splits, static_cast<unsigned long long>(need),
                         static_cast<unsigned long long>(ws_bytes));
     }
-    GemmArgs a = make_args(A, static_cast<const uint8_t*>(W), nullptr, bias, C, M, N, K, mode, lda, ldc, sA, sC,
-                           (K / 32) * 34);
+    GemmArgs a = make_args(static_cast<const float*>(A), static_cast<const uint8_t*>(W), nullptr, bias, C, M, N, K,
+                           mode, lda, ldc, sA, sC, (K / 32) * 34);
     const Plan p = plan_for(M, N, K, batch, ws, ws_bytes);
-    if (mode == 2) dispatch<kBlocks34, kEpiResidual>(a, batch, p, static_cast<float*>(ws), stream);
-    else dispatch<kBlocks34>(a, batch, p, static_cast<float*>(ws), stream);
+    float* wsf = static_cast<float*>(ws);
+    if (a_half) {
+        if (mode == 2) dispatch<kBlocks34, kEpiResidual, true>(a, batch, p, wsf, stream);
+        else dispatch<kBlocks34, kEpiPlain, true>(a, batch, p, wsf, stream);
+    } else {
+        if (mode == 2) dispatch<kBlocks34, kEpiResidual>(a, batch, p, wsf, stream);
+        else dispatch<kBlocks34>(a, batch, p, wsf, stream);
+    }
     return check_launch(fn);
 }
 
@@ -1224,27 +1267,55 @@ extern "C" uint64_t mi_gemm_nt_q8_workspace_bytes(uint32_t M, uint32_t N, uint32
     return split_floats(M, N, batch, p.splits) * 4;
 }
 
-extern "C" int mi_gemm_nt_q8_0_geglu(const float* A, const void* W, const float* bias, float* G, uint32_t M, uint32_t F,
-                                     uint32_t K, uint32_t lda, uint32_t ldg, void* stream) {
-    const char* fn = "mi_gemm_nt_q8_0_geglu";
+namespace mi {
+namespace {
+int gemm_geglu(const char* fn, const void* A, const void* W, const float* bias, void* G, uint32_t M, uint32_t F,
+               uint32_t K, uint32_t lda, uint32_t ldg, hipStream_t stream, bool a_half, bool g_half) {
     if (M == 0 || F == 0) return MI_OK;
     if (K == 0 || K % 32) return fail(MI_ERR_UNSUPPORTED, "%s: K=%u must be a positive multiple of 32", fn, K);
     if (F > (1u << 30)) return fail(MI_ERR_UNSUPPORTED, "%s: F=%u too large", fn, F);
     const uint32_t N = 2 * F;
     uint32_t ldc = ldg, mode = 0;
-    int st = validate(fn, A, W, G, M, F, K, mode, lda, ldc, 1, 0, 0, true);
+    int st = validate(fn, A, W, G, M, F, K, mode, lda, ldc, 1, 0, 0, true, a_half);
     if (st) return st;
     if (!aligned(W, 16)) return fail(MI_ERR_ALIGNMENT, "%s: W must be 16-byte aligned", fn);
+    if (g_half && !aligned(G, 8)) return fail(MI_ERR_ALIGNMENT, "%s: G must be 8-byte aligned", fn);
     const uint64_t wbytes = static_cast<uint64_t>(N) * (K / 32) * 34;
     if (wbytes + 16 >= (uint64_t(1) << 32)) return fail(MI_ERR_UNSUPPORTED, "%s: weight >= 4 GiB", fn);
-    const uint64_t gbytes = (static_cast<uint64_t>(M - 1) * ldc + F) * 4;
-    const uint64_t abytes = (static_cast<uint64_t>(M - 1) * lda + K) * 4;
+    const uint64_t gbytes = (static_cast<uint64_t>(M - 1) * ldc + F) * (g_half ? 2 : 4);
+    const uint64_t abytes = (static_cast<uint64_t>(M - 1) * lda + K) * (a_half ? 2 : 4);
     if (overlaps(G, gbytes, A, abytes) || overlaps(G, gbytes, W, wbytes) || overlaps(G, gbytes, bias, uint64_t(N) * 4))
         return fail(MI_ERR_ALIASING, "%s: G overlaps an input", fn);
-    GemmArgs a = make_args(A, static_cast<const uint8_t*>(W), nullptr, bias, G, M, N, K, 0, lda, ldc, 0, 0,
-                           (K / 32) * 34);
+    GemmArgs a = make_args(static_cast<const float*>(A), static_cast<const uint8_t*>(W), nullptr, bias,
+                           static_cast<float*>(G), M, N, K, 0, lda, ldc, 0, 0, (K / 32) * 34);
     a.F = F;
+    a.out_half = g_half ? 1u : 0u;
+    if (g_half)  // 8-byte stores of four fp16 outputs
+        a.cvec = aligned(G, 8) && ldc % 4 == 0 ? 1u : 0u;
     // the GEGLU epilogue needs the whole K sum: never split
-    dispatch<kBlocks34, kEpiGeglu>(a, 1, plan_for(M, N, K, 1, nullptr, 0), nullptr, static_cast<hipStream_t>(stream));
+    const Plan p = plan_for(M, N, K, 1, nullptr, 0);
+    if (a_half) dispatch<kBlocks34, kEpiGeglu, true>(a, 1, p, nullptr, stream);
+    else dispatch<kBlocks34, kEpiGeglu>(a, 1, p, nullptr, stream);
     return check_launch(fn);
+}
+}  // namespace
+}  // namespace mi
+
+extern "C" int mi_gemm_nt_q8_0_geglu(const float* A, const void* W, const float* bias, float* G, uint32_t M, uint32_t F,
+                                     uint32_t K, uint32_t lda, uint32_t ldg, void* stream) {
+    return gemm_geglu("mi_gemm_nt_q8_0_geglu", A, W, bias, G, M, F, K, lda, ldg, static_cast<hipStream_t>(stream),
+                      false, false);
+}
+
+extern "C" int mi_gemm_nt_q8_0_geglu_f16(const void* A, const void* W, const float* bias, void* G, uint32_t M,
+                                         uint32_t F, uint32_t K, uint32_t lda, uint32_t ldg, void* stream) {
+    return gemm_geglu("mi_gemm_nt_q8_0_geglu_f16", A, W, bias, G, M, F, K, lda, ldg,
+                      static_cast<hipStream_t>(stream), true, true);
+}
+
+extern "C" int mi_gemm_nt_q8_0_f16a(const void* A, const void* W, const float* bias, float* C, uint32_t M, uint32_t N,
+                                    uint32_t K, uint32_t mode, uint32_t lda, uint32_t ldc, uint32_t batch, uint64_t sA,
+                                    uint64_t sC, void* workspace, uint64_t workspace_bytes, void* stream) {
+    return gemm_blocks("mi_gemm_nt_q8_0_f16a", A, W, bias, C, M, N, K, mode, lda, ldc, batch, sA, sC, workspace,
+                       workspace_bytes, static_cast<hipStream_t>(stream), false, true);
 }

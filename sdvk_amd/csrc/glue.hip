@@ -30,16 +30,34 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-// One wave per row; 4 rows per 256-thread workgroup. d % 4 == 0, 16-byte aligned rows.
+// Stores four fp32 results as TO: fp32 as they are, fp16 rounded once (RNE)
+// each -- the value a GEMM staging an fp32 tensor would round them to. The
+// empty register constraint makes the fp32 values opaque, so the rounding to fp16 cannot fuse
+// into the instruction that produced them (a mixed-precision fma rounds the
+// exact result once, which can differ from rounding the fp32 result).
+template <typename TO>
+__device__ __forceinline__ void store4(TO* p, floatx4 v) {
+    if constexpr (sizeof(TO) == 4) {
+        *reinterpret_cast<floatx4*>(p) = v;
+    } else {
+        asm volatile("" : "+v"(v));
+        *reinterpret_cast<half4*>(p) = half4{static_cast<_Float16>(v[0]), static_cast<_Float16>(v[1]),
+                                             static_cast<_Float16>(v[2]), static_cast<_Float16>(v[3])};
+    }
+}
+
+// One wave per row; 4 rows per 256-thread workgroup. d % 4 == 0, 16-byte aligned rows
+// (8-byte for fp16 output).
+template <typename TO>
 __global__ __launch_bounds__(256) void layernorm_vec_kernel(const float* __restrict__ x, const float* __restrict__ gamma,
-                                                            const float* __restrict__ beta, float* __restrict__ y,
+                                                            const float* __restrict__ beta, TO* __restrict__ y,
                                                             uint32_t rows, uint32_t d, float eps) {
     const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= rows) return;
     const uint32_t n4 = d / 4;
     const floatx4* xr = reinterpret_cast<const floatx4*>(x + static_cast<uint64_t>(row) * d);
-    floatx4* yr = reinterpret_cast<floatx4*>(y + static_cast<uint64_t>(row) * d);
+    TO* yr = y + static_cast<uint64_t>(row) * d;
     floatx4 c[kLnCache];
     float s = 0.0f;
 #pragma unroll
@@ -76,7 +94,7 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(const float* __restr
 #pragma unroll
                 for (int e = 0; e < 4; ++e) v[e] = v[e] * g[e] + b[e];
             }
-            yr[j] = v;
+            store4(yr + 4 * j, v);
         }
     }
 }
@@ -106,10 +124,12 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict_
     }
 }
 
-// y[r, j] = h[r, j] * gelu(h[r, F + j]); F % 4 == 0 and 16-byte aligned rows.
-// Thread (x, y) of the grid takes float4 column blockIdx.x * 256 + tid of rows
-// blockIdx.y, blockIdx.y + gridDim.y, ... (no index division per element).
-__global__ __launch_bounds__(256) void geglu_vec_kernel(const float* __restrict__ h, float* __restrict__ y, uint32_t rows,
+// y[r, j] = h[r, j] * gelu(h[r, F + j]); F % 4 == 0 and 16-byte aligned rows
+// (8-byte for fp16 y). Thread (x, y) of the grid takes float4 column
+// blockIdx.x * 256 + tid of rows blockIdx.y, blockIdx.y + gridDim.y, ... (no
+// index division per element).
+template <typename TO>
+__global__ __launch_bounds__(256) void geglu_vec_kernel(const float* __restrict__ h, TO* __restrict__ y, uint32_t rows,
                                                         uint32_t F) {
     const uint32_t f4 = F / 4;
     const uint32_t j = blockIdx.x * 256 + threadIdx.x;
@@ -120,7 +140,7 @@ __global__ __launch_bounds__(256) void geglu_vec_kernel(const float* __restrict_
         floatx4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[e] = a[e] * gelu_erf(b[e]);
-        reinterpret_cast<floatx4*>(y + static_cast<uint64_t>(r) * F)[j] = o;
+        store4(y + static_cast<uint64_t>(r) * F + 4 * j, o);
     }
 }
 
@@ -172,7 +192,7 @@ extern "C" int mi_layernorm(const float* x, const float* gamma, const float* bet
     const bool vec = d % 4 == 0 && d <= 64u * 4 * kLnCache && aligned(x, 16) && aligned(y, 16) &&
                      (!gamma || (aligned(gamma, 16) && aligned(beta, 16)));
     const unsigned grid = ceil_div(rows, 4);
-    if (vec) layernorm_vec_kernel<<<grid, 256, 0, s>>>(x, gamma, beta, y, rows, d, eps);
+    if (vec) layernorm_vec_kernel<float><<<grid, 256, 0, s>>>(x, gamma, beta, y, rows, d, eps);
     else layernorm_kernel<<<grid, 256, 0, s>>>(x, gamma, beta, y, rows, d, eps);
     return check_launch(fn);
 }
@@ -188,10 +208,42 @@ extern "C" int mi_geglu(const float* h, float* y, uint32_t rows, uint32_t F, voi
         // ~2048 workgroups in all: the rows are strided over grid.y
         const unsigned gx = ceil_div(F / 4, 256);
         const unsigned gy = static_cast<unsigned>(std::min<uint64_t>(rows, std::max<uint64_t>(1, 2048 / gx)));
-        geglu_vec_kernel<<<dim3(gx, gy), 256, 0, s>>>(h, y, rows, F);
+        geglu_vec_kernel<float><<<dim3(gx, gy), 256, 0, s>>>(h, y, rows, F);
     }
     else
         geglu_kernel<<<stride_grid(static_cast<uint64_t>(rows) * F), 256, 0, s>>>(h, y, rows, F);
+    return check_launch(fn);
+}
+
+extern "C" int mi_layernorm_f16(const float* x, const float* gamma, const float* beta, void* y, uint32_t rows,
+                                uint32_t d, float eps, void* stream) {
+    const char* fn = "mi_layernorm_f16";
+    if (!x || !y) return fail(MI_ERR_INVALID_ARG, "%s: null pointer", fn);
+    if ((gamma == nullptr) != (beta == nullptr)) return fail(MI_ERR_INVALID_ARG, "%s: gamma and beta go together", fn);
+    if (rows == 0) return MI_OK;
+    if (d == 0 || d % 4 || d > 64u * 4 * kLnCache)
+        return fail(MI_ERR_UNSUPPORTED, "%s: d=%u (a multiple of 4, at most %u)", fn, d, 64u * 4 * kLnCache);
+    if (!aligned(x, 16) || !aligned(y, 8) || (gamma && (!aligned(gamma, 16) || !aligned(beta, 16))))
+        return fail(MI_ERR_ALIGNMENT, "%s: x, gamma, beta 16-byte and y 8-byte aligned", fn);
+    if (overlaps(x, static_cast<uint64_t>(rows) * d * 4, y, static_cast<uint64_t>(rows) * d * 2))
+        return fail(MI_ERR_ALIASING, "%s: y overlaps x", fn);
+    layernorm_vec_kernel<_Float16><<<ceil_div(rows, 4), 256, 0, static_cast<hipStream_t>(stream)>>>(
+        x, gamma, beta, static_cast<_Float16*>(y), rows, d, eps);
+    return check_launch(fn);
+}
+
+extern "C" int mi_geglu_f16(const float* h, void* y, uint32_t rows, uint32_t F, void* stream) {
+    const char* fn = "mi_geglu_f16";
+    if (!h || !y) return fail(MI_ERR_INVALID_ARG, "%s: null pointer", fn);
+    if (rows == 0 || F == 0) return MI_OK;
+    if (F % 4) return fail(MI_ERR_UNSUPPORTED, "%s: F=%u is not a multiple of 4", fn, F);
+    if (!aligned(h, 16) || !aligned(y, 8)) return fail(MI_ERR_ALIGNMENT, "%s: h 16-byte and y 8-byte aligned", fn);
+    if (overlaps(h, static_cast<uint64_t>(rows) * 2 * F * 4, y, static_cast<uint64_t>(rows) * F * 2))
+        return fail(MI_ERR_ALIASING, "%s: y overlaps h", fn);
+    const unsigned gx = ceil_div(F / 4, 256);
+    const unsigned gy = static_cast<unsigned>(std::min<uint64_t>(rows, std::max<uint64_t>(1, 2048 / gx)));
+    geglu_vec_kernel<_Float16><<<dim3(gx, gy), 256, 0, static_cast<hipStream_t>(stream)>>>(
+        h, static_cast<_Float16*>(y), rows, F);
     return check_launch(fn);
 }
 

@@ -28,13 +28,15 @@ from dataclasses import dataclass
 from typing import Optional, Sequence
 
 from . import _lib
-from ._lib import (MI_ATTN_PREC_AUTO, MI_ATTN_PREC_FP16, MI_ATTN_PREC_SPLIT, MI_BLOCK_FUSED_EPILOGUES,
-                   MI_BLOCK_JOINT_QKV, MI_F16, MI_F32, MiAttnArgs, MiBlockDims, MiBlockWeights, MiError, call, ptr)
+from ._lib import (MI_ATTN_PREC_AUTO, MI_ATTN_PREC_FP16, MI_ATTN_PREC_SPLIT, MI_BLOCK_FP16_ACTIVATIONS,
+                   MI_BLOCK_FUSED_EPILOGUES, MI_BLOCK_JOINT_QKV, MI_F16, MI_F32, MiAttnArgs, MiBlockDims, MiBlockWeights,
+                   MiError, call, ptr)
 
 __all__ = [
     "MiError", "MI_F32", "MI_F16", "MI_ATTN_PREC_AUTO", "MI_ATTN_PREC_FP16", "MI_ATTN_PREC_SPLIT",
-    "tuning", "tuning_set", "tuning_reset", "MI_BLOCK_FUSED_EPILOGUES", "MI_BLOCK_JOINT_QKV", "FusedAttnArgs", "fused_attn_supported", "fused_attention",
+    "tuning", "tuning_set", "tuning_reset", "MI_BLOCK_FUSED_EPILOGUES", "MI_BLOCK_FP16_ACTIVATIONS", "MI_BLOCK_JOINT_QKV", "FusedAttnArgs", "fused_attn_supported", "fused_attention",
     "fused_attention_ex", "gemm_nt_q8", "gemm_nt_q8_bias", "gemm_nt_q8_0", "gemm_nt_q8_0_geglu", "gemm_nn_q8",
+    "gemm_nt_q8_0_f16a", "gemm_nt_q8_0_geglu_f16", "layernorm_f16", "geglu_f16",
     "gemm_workspace_bytes", "gemm_nn_workspace_bytes",
     "q8_0_dequant",
     "q8_split_dequant", "q8_0_to_split", "q8_0_quantize", "Pg", "dispatch", "KERNELS", "layernorm", "geglu", "add2",
@@ -216,6 +218,20 @@ def gemm_nt_q8_0(A, W, C, M: int, N: int, K: int, *, bias=None, mode: int = 0, l
          sC, _s(stream))
 
 
+def gemm_nt_q8_0_f16a(A, W, C, M: int, N: int, K: int, *, bias=None, mode: int = 0, lda: int = 0, ldc: int = 0,
+                      batch: int = 1, sA: int = 0, sC: int = 0, workspace=None, stream=None) -> None:
+    """gemm_nt_q8_0 with fp16 activations A (mi_gemm_nt_q8_0_f16a; extension): the same bits as the fp32
+    entry given A's fp16 values as fp32."""
+    call("mi_gemm_nt_q8_0_f16a", ptr(A), ptr(W), ptr(bias), ptr(C), M, N, K, mode, lda, ldc, batch, sA, sC,
+         *_ws(workspace), _s(stream))
+
+
+def gemm_nt_q8_0_geglu_f16(A, W, G, M: int, F: int, K: int, *, bias=None, lda: int = 0, ldg: int = 0,
+                           stream=None) -> None:
+    """gemm_nt_q8_0_geglu with fp16 A and fp16 G (mi_gemm_nt_q8_0_geglu_f16; extension)."""
+    call("mi_gemm_nt_q8_0_geglu_f16", ptr(A), ptr(W), ptr(bias), ptr(G), M, F, K, lda, ldg, _s(stream))
+
+
 # ------------------------------------------------------------------ Q8_0 utils --
 
 def q8_0_dequant(blocks, out, n: int, out_dtype: int = MI_F32, stream=None) -> None:
@@ -242,6 +258,16 @@ def q8_0_to_split(blocks, payload, scales, n: int, stream=None) -> None:
 def layernorm(x, gamma, beta, y, rows: int, d: int, eps: float = 1e-5, stream=None) -> None:
     """layernorm_fwd (two-pass mean / variance, affine when gamma/beta are given)."""
     call("mi_layernorm", ptr(x), ptr(gamma), ptr(beta), ptr(y), rows, d, eps, _s(stream))
+
+
+def layernorm_f16(x, gamma, beta, y, rows: int, d: int, eps: float = 1e-5, stream=None) -> None:
+    """layernorm with y stored as fp16 (mi_layernorm_f16; extension)."""
+    call("mi_layernorm_f16", ptr(x), ptr(gamma), ptr(beta), ptr(y), rows, d, eps, _s(stream))
+
+
+def geglu_f16(h, y, rows: int, F: int, stream=None) -> None:
+    """geglu with y stored as fp16 (mi_geglu_f16; extension)."""
+    call("mi_geglu_f16", ptr(h), ptr(y), rows, F, _s(stream))
 
 
 def geglu(h, y, rows: int, F: int, stream=None) -> None:

@@ -26,8 +26,9 @@ import ctypes  # noqa: E402
 import emu as kemu  # noqa: E402
 from helpers import assert_parity, fp16_half_ulp, q8_weights, rms  # noqa: E402
 from oracle import binding as ob  # noqa: E402
-from sdvk_amd._lib import (MI_ATTN_PREC_FP16, MI_ATTN_PREC_SPLIT, MI_BLOCK_FUSED_EPILOGUES,  # noqa: E402
-                           MI_BLOCK_JOINT_QKV, MI_F16, MI_F32, MiAttnArgs, MiBlockDims, MiBlockWeights)
+from sdvk_amd._lib import (MI_ATTN_PREC_FP16, MI_ATTN_PREC_SPLIT, MI_BLOCK_FP16_ACTIVATIONS,  # noqa: E402
+                           MI_BLOCK_FUSED_EPILOGUES, MI_BLOCK_JOINT_QKV, MI_F16, MI_F32, MiAttnArgs, MiBlockDims,
+                           MiBlockWeights)
 from test_gpu_block import BLOCK_TOL, make_weights  # noqa: E402
 import gguf_writer as gw  # noqa: E402
 from sdvk_amd._lib import MiGgufTensorInfo  # noqa: E402
@@ -419,15 +420,18 @@ def attention_full(E, *, batch, Tq, Tk, C, heads, masked=False, nw=None, seed=1,
     return float(np.max(np.abs(g - w)) / rms(w))
 
 
-def block(E, *, B, T, C, H, Tc, Cc, F, masked=False, blocks=2, order=0, front=False, fused=False, qkv_joint=False):
+def block(E, *, B, T, C, H, Tc, Cc, F, masked=False, blocks=2, order=0, front=False, fused=False, qkv_joint=False,
+          half=False):
     """Two applications of one SDXL transformer block: uncached
     (mi_sdxl_block_forward) vs context K / V projected once (mi_block_ctx_kv,
     mi_sdxl_block_forward_kv), against the oracle's block; cached and fresh
     runs must be bit-identical (same GEMM plans, fixed summation order). With
-    fused / qkv_joint: one block with those flags against the plain block,
-    bit for bit (every flag combination computes the same sums)."""
+    fused / qkv_joint / half (fp16 activations): one block with those flags
+    against the plain block, bit for bit (every flag combination computes the
+    same sums)."""
     E.order(order)
-    flags = (MI_BLOCK_FUSED_EPILOGUES if fused else 0) | (MI_BLOCK_JOINT_QKV if qkv_joint else 0)
+    flags = ((MI_BLOCK_FUSED_EPILOGUES if fused else 0) | (MI_BLOCK_JOINT_QKV if qkv_joint else 0) |
+             (MI_BLOCK_FP16_ACTIVATIONS if half else 0))
     w = make_weights(ob, C, Cc, F, seed=500)
     dw = {k: E.buf(v, front=front) for k, v in w.items()}
     ptrs = {k: b.ptr for k, b in dw.items()}
@@ -478,6 +482,29 @@ def block(E, *, B, T, C, H, Tc, Cc, F, masked=False, blocks=2, order=0, front=Fa
         assert np.array_equal(outs[0], outs[1]), \
             f"flags {flags:#x} vs plain block differ by {float(np.max(np.abs(outs[0] - outs[1]))):.3e}"
     return e
+
+
+def gemm_f16a(E, *, M, N, K, mode=0, cfg=None, seed=1, order=0, front=False):
+    """mi_gemm_nt_q8_0_f16a (fp16 A) against mi_gemm_nt_q8_0_ws on the same
+    values as fp32, bit for bit, with the workspace the library asks for."""
+    _set_cfg(cfg)
+    E.order(order)
+    a16 = ob.normal(seed, M * K).astype(np.float16)
+    blocks = q8_weights(ob, seed + 1, N, K)
+    bias = ob.normal(seed + 2, N, 0.0, 0.02)
+    C0 = ob.normal(seed + 3, M * N)
+    dW, dB = E.buf(blocks, front=front), E.buf(bias, front=front)
+    nws = E.lib.mi_gemm_nt_q8_workspace_bytes(M, N, K, 1)
+    wsp, wsn, _keep = _workspace(E, nws, front)
+    outs = []
+    for entry, A in (("mi_gemm_nt_q8_0_f16a", a16), ("mi_gemm_nt_q8_0_ws", a16.astype(np.float32))):
+        dA, dC = E.buf(A, front=front), E.buf(C0, front=front)
+        E.call(entry, dA.ptr, dW.ptr, dB.ptr, dC.ptr, M, N, K, mode, 0, 0, 1, 0, 0, wsp, wsn, None)
+        outs.append(dC.get(np.float32))
+    assert np.array_equal(outs[0], outs[1]), "fp16-A GEMM differs from the fp32 GEMM on the same values"
+    want = ob.gemm_nt_q8_0(a16.astype(np.float32), blocks, M, N, K, bias=None if mode == 1 else bias,
+                           threads=ob.max_threads())
+    return assert_parity(outs[0] - (C0 if mode else 0), want, what="gemm f16a")
 
 
 def routing(E, *, table, order=0):
@@ -683,7 +710,8 @@ def gguf_upload(E, *, big_rows=10240, big_cols=1280, order=0, front=False):
     return 0.0
 
 
-CASES = {"gemm_nt": gemm_nt, "gemm_geglu": gemm_geglu, "gemm_nn": gemm_nn, "attention": attention, "block": block,
+CASES = {"gemm_nt": gemm_nt, "gemm_geglu": gemm_geglu, "gemm_f16a": gemm_f16a, "gemm_nn": gemm_nn,
+         "attention": attention, "block": block,
          "gguf_upload": gguf_upload, "q8": q8, "glue": glue, "gemm_full": gemm_full, "gemm_nn_full": gemm_nn_full,
          "attention_full": attention_full, "block_full": block_full, "routing": routing}
 

@@ -85,11 +85,15 @@ def test_geglu_gemm(gpu, oracle, tune, M, F, K, cfg):
                                                     (2, 100, 320, 5, 77, 2048, 1280, True),
                                                     (2, 1024, 1280, 20, 77, 2048, 5120, False)])
 @pytest.mark.parametrize("flags", [ops.MI_BLOCK_FUSED_EPILOGUES, ops.MI_BLOCK_JOINT_QKV,
-                                   ops.MI_BLOCK_FUSED_EPILOGUES | ops.MI_BLOCK_JOINT_QKV])
+                                   ops.MI_BLOCK_FUSED_EPILOGUES | ops.MI_BLOCK_JOINT_QKV,
+                                   ops.MI_BLOCK_FP16_ACTIVATIONS,
+                                   ops.MI_BLOCK_FP16_ACTIVATIONS | ops.MI_BLOCK_FUSED_EPILOGUES,
+                                   ops.MI_BLOCK_FP16_ACTIVATIONS | ops.MI_BLOCK_FUSED_EPILOGUES |
+                                   ops.MI_BLOCK_JOINT_QKV])
 def test_block_flags(gpu, oracle, B, T, C, H, Tc, Cc, F, masked, flags):
-    """The block with fused epilogues and / or the joint Q/K/V projection: within
-    the block bar of the oracle and bit-identical to the plain block (weights
-    stored apart, separate epilogues)."""
+    """The block with fused epilogues, the joint Q/K/V projection and / or fp16
+    activations: within the block bar of the oracle and bit-identical to the
+    plain block (weights stored apart, separate epilogues, fp32 activations)."""
     print(f"[case] block flags={flags} B={B} T={T} C={C} F={F}", flush=True)
     w = make_weights(oracle, C, Cc, F, seed=500)
     x = oracle.normal(3, B * T * C)

@@ -79,6 +79,10 @@ FAMILIES = {
         dict(case="gemm_geglu", M=70, F=40, K=128, cfg="1", bias=False),
         dict(case="gemm_nt", M=200, N=300, K=256, cfg="1:2", mode=2), dict(case="gemm_geglu", M=200, F=260, K=128, cfg="3"),
         dict(case="gemm_geglu", M=200, F=130, K=128, cfg="5"), dict(case="gemm_nt", M=200, N=300, K=256, cfg="5:2", mode=2),
+        # fp16 activations: the fp16-A GEMM equals the fp32 GEMM on the same values (tiles, K splits, modes)
+        dict(case="gemm_f16a", M=77, N=96, K=64), dict(case="gemm_f16a", M=154, N=96, K=2048, mode=2),
+        dict(case="gemm_f16a", M=300, N=200, K=256, cfg="0", mode=1), dict(case="gemm_f16a", M=400, N=300, K=256, cfg="5"),
+        dict(case="gemm_f16a", M=130, N=100, K=96, front=True),
     ],
     "gemm_nn": [
         dict(M=64, N=64, K=32), dict(M=100, N=72, K=96), dict(M=130, N=260, K=100, mode=1),
@@ -130,6 +134,8 @@ FAMILIES = {
         dict(B=2, T=64, C=128, H=2, Tc=77, Cc=256, F=256, masked=True, qkv_joint=True),
         dict(B=1, T=33, C=64, H=1, Tc=5, Cc=96, F=160, qkv_joint=True, fused=True),
         dict(B=1, T=33, C=64, H=1, Tc=5, Cc=96, F=64, qkv_joint=True),
+        dict(B=2, T=64, C=128, H=2, Tc=77, Cc=256, F=256, masked=True, half=True),
+        dict(B=1, T=33, C=64, H=1, Tc=5, Cc=96, F=160, qkv_joint=True, fused=True, half=True),
     ],
     "gguf_upload": [dict()],
     "q8": [dict(n=32), dict(n=4096), dict(n=224, front=True)],
