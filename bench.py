@@ -174,7 +174,8 @@ class NnCase:
 # (MI_BLOCK_FUSED_EPILOGUES). Every flag combination computes the same bits as
 # the plain block (tests/test_gpu_xfused_epilogues.py, test_gpu_xattn_kv_cache.py);
 # the extras time the plain block and each flag alone.
-BLOCK_VARIANT = {"cached_kv": True, "fused_epilogues": True, "joint_qkv": True, "fp16_activations": True}
+BLOCK_VARIANT = {"cached_kv": True, "fused_epilogues": True, "joint_qkv": True, "fp16_activations": True,
+                 "fp16_attention": True}
 
 
 class BlockStack:
@@ -187,17 +188,19 @@ class BlockStack:
 
     DIMS = (2, 1024, 1280, 20, 77, 2048, 5120)  # batch, tokens, channels, heads, ctx_tokens, ctx_channels, ff_inner
 
-    def __init__(self, rng, hip, ops, nblocks=10, joint_qkv=False, fused=False, half=False):
+    def __init__(self, rng, hip, ops, nblocks=10, joint_qkv=False, fused=False, half=False, hattn=False):
         """joint_qkv: each block's to_q / to_k / to_v weights in one allocation,
         back to back, and MI_BLOCK_JOINT_QKV: one Q/K/V projection GEMM (N = 3C);
         fused: MI_BLOCK_FUSED_EPILOGUES (residual adds and GEGLU in the GEMM
         epilogues); half: MI_BLOCK_FP16_ACTIVATIONS (LayerNorm, attention and
-        GEGLU outputs stored as fp16 for the GEMMs that read them)."""
+        GEGLU outputs stored as fp16 for the GEMMs that read them); hattn:
+        MI_BLOCK_FP16_ATTENTION (Q / K / V and the cached context K / V stored as
+        fp16, attention on fp16 inputs)."""
         B, T, C, H, Tc, Cc, F = self.DIMS
         self.ops, self.hip, self.nblocks = ops, hip, nblocks
-        self.joint_qkv, self.fused, self.half = joint_qkv, fused, half
+        self.joint_qkv, self.fused, self.half, self.hattn = joint_qkv, fused, half, hattn
         flags = ((ops.MI_BLOCK_JOINT_QKV if joint_qkv else 0) | (ops.MI_BLOCK_FUSED_EPILOGUES if fused else 0) |
-                 (ops.MI_BLOCK_FP16_ACTIVATIONS if half else 0))
+                 (ops.MI_BLOCK_FP16_ACTIVATIONS if half else 0) | (ops.MI_BLOCK_FP16_ATTENTION if hattn else 0))
         self.dims = ops.BlockDims(*self.DIMS, flags)
         shapes = {"attn1_q": (C, C), "attn1_k": (C, C), "attn1_v": (C, C), "attn1_out": (C, C),
                   "attn2_q": (C, C), "attn2_k": (C, Cc), "attn2_v": (C, Cc), "attn2_out": (C, C),
@@ -244,10 +247,12 @@ class BlockStack:
         for w, kv in zip(self.weights, self.kv):
             self.ops.sdxl_block_forward_kv(w, self.dims, self.x, kv, self.ws, stream=stream)
 
-    def measure(self, stream, reps, cached_kv=False):
+    def measure(self, stream, reps, cached_kv=False, preroll_s=0.3):
         """Latency of one pass over the stack; cached_kv: the context's K / V
         projected once per block before timing (a sampling job does this once,
-        mi_block_ctx_kv) and every timed pass runs mi_sdxl_block_forward_kv."""
+        mi_block_ctx_kv) and every timed pass runs mi_sdxl_block_forward_kv.
+        Passes over the stack run for preroll_s seconds before the timed ones,
+        so that those do not run on ramping clocks."""
         run = self.run
         if cached_kv:
             self.kv = []
@@ -258,6 +263,10 @@ class BlockStack:
             run = self.run_cached
         run(stream)
         stream.synchronize()
+        t_end = time.perf_counter() + max(preroll_s, 0.0)
+        while time.perf_counter() < t_end:
+            run(stream)
+            stream.synchronize()
         a, b = self.hip.Event(TIMING_EVENT), self.hip.Event(TIMING_EVENT)
         a.record(stream)
         for _ in range(reps):
@@ -289,8 +298,9 @@ class BlockStack:
         rows = B * T
         w = self.keep[1]
         kv = self.kv[0]
-        half = self.half
+        half, hattn = self.half, self.hattn
         esz = 2 if half else 4
+        qsz = 2 if hattn else 4  # Q / K / V element size
         n, o = hip.DeviceBuffer(rows * C * esz), hip.DeviceBuffer(rows * C * esz)
         h = hip.DeviceBuffer(rows * 3 * C * 4)
         q = hip.DeviceBuffer(rows * C * 4)
@@ -312,20 +322,26 @@ class BlockStack:
 
         def attn(qb, kb_, vb, ld, tk):
             return lambda st: ops.fused_attention_ex(qb, kb_, vb, o, batch=B, Tq=T, Tk=tk, C=C, heads=H, ldq=ld,
-                                                     ldk=ld, ldv=ld, in_dtype=ops.MI_F32, out_dtype=odt,
-                                                     precision=ops.MI_ATTN_PREC_FP16, stream=st)
+                                                     ldk=ld, ldv=ld, in_dtype=ops.MI_F16 if hattn else ops.MI_F32,
+                                                     out_dtype=odt, precision=ops.MI_ATTN_PREC_FP16, stream=st)
+
+        def proj(Wt, out, N):  # Q / K / V projection: fp16 output with MI_BLOCK_FP16_ATTENTION
+            if hattn:
+                return lambda st: ops.gemm_nt_q8_0_f16o(n, Wt, out, rows, N, C, a_dtype=ops.MI_F16 if half else
+                                                        ops.MI_F32, stream=st)
+            return lambda st: gemm(n, Wt, out, rows, N, C, stream=st)
         qkv = w["_qkv"] if "_qkv" in w else None
         steps = [("glue", ln_op(1))]
         if qkv is not None:
-            steps += [("gemm_q8", lambda st: gemm(n, qkv, h, rows, 3 * C, C, stream=st)),
-                      ("attention", attn(h.value, h.value + 4 * C, h.value + 8 * C, 3 * C, T))]
+            steps += [("gemm_q8", proj(qkv, h, 3 * C)),
+                      ("attention", attn(h.value, h.value + qsz * C, h.value + 2 * qsz * C, 3 * C, T))]
         else:
-            steps += [("gemm_q8", lambda st: gemm(n, w["attn1_q"], h, rows, C, C, stream=st)),
-                      ("gemm_q8", lambda st: gemm(n, w["attn1_k"], h.value + rows * C * 4, rows, C, C, stream=st)),
-                      ("gemm_q8", lambda st: gemm(n, w["attn1_v"], h.value + 2 * rows * C * 4, rows, C, C, stream=st)),
-                      ("attention", attn(h.value, h.value + rows * C * 4, h.value + 2 * rows * C * 4, C, T))]
+            steps += [("gemm_q8", proj(w["attn1_q"], h, C)),
+                      ("gemm_q8", proj(w["attn1_k"], h.value + rows * C * qsz, C)),
+                      ("gemm_q8", proj(w["attn1_v"], h.value + 2 * rows * C * qsz, C)),
+                      ("attention", attn(h.value, h.value + rows * C * qsz, h.value + 2 * rows * C * qsz, C, T))]
         steps += [("gemm_q8", resid(o, w["attn1_out"], w["attn1_out_b"], C)), ("glue", ln_op(2)),
-                  ("gemm_q8", lambda st: gemm(n, w["attn2_q"], q, rows, C, C, stream=st)),
+                  ("gemm_q8", proj(w["attn2_q"], q, C)),
                   ("attention", attn(q.value, kv.value, kv.value + kb, C, Tc)),
                   ("gemm_q8", resid(o, w["attn2_out"], w["attn2_out_b"], C)), ("glue", ln_op(3)),
                   ("gemm_q8", lambda st: (ops.gemm_nt_q8_0_geglu_f16 if half else ops.gemm_nt_q8_0_geglu)(
@@ -442,12 +458,12 @@ def extras(rng, hip, ops, stream, reps, emit=None):
             res.append(time_case(NnCase(t, M, N, K, rng, hip, ops), stream, hip, reps)[1])
         return res
 
-    def stack(cached_kv=False, fused=False, joint_qkv=False, half=False):
+    def stack(cached_kv=False, fused=False, joint_qkv=False, half=False, hattn=False):
         def run():
-            st = BlockStack(rng, hip, ops, joint_qkv=joint_qkv, fused=fused, half=half)
+            st = BlockStack(rng, hip, ops, joint_qkv=joint_qkv, fused=fused, half=half, hattn=hattn)
             res = st.measure(stream, 5, cached_kv=cached_kv)
             res["variant"] = {"cached_kv": cached_kv, "fused_epilogues": fused, "joint_qkv": joint_qkv,
-                              "fp16_activations": half}
+                              "fp16_activations": half, "fp16_attention": hattn}
             del st
             return res
         return run
@@ -557,7 +573,9 @@ def extras(rng, hip, ops, stream, reps, emit=None):
     part("block_stack_fused_epilogues", stack(fused=True))
     part("block_stack_joint_qkv", stack(joint_qkv=True))
     part("block_stack_fp16_activations", stack(half=True))
-    part("block_stack_all_but_fp16_activations", stack(cached_kv=True, fused=True, joint_qkv=True))
+    part("block_stack_all_but_fp16_activations", stack(cached_kv=True, fused=True, joint_qkv=True, hattn=True))
+    part("block_stack_fp16_attention", stack(hattn=True))
+    part("block_stack_all_but_fp16_attention", stack(cached_kv=True, fused=True, joint_qkv=True, half=True))
     part("step_graph", step_graph)
     return out
 
@@ -710,7 +728,7 @@ def main() -> int:
     rng = np.random.default_rng(1)
     stream = hip.Stream()
     if args.only == "block":
-        stack = BlockStack(rng, hip, ops, joint_qkv=True, fused=True, half=True)
+        stack = BlockStack(rng, hip, ops, joint_qkv=True, fused=True, half=True, hattn=True)
         res = stack.measure(stream, max(args.steps // 4, 1), cached_kv=True)
         res["variant"] = BLOCK_VARIANT
         print(json.dumps({"block_stack": res}), flush=True)
@@ -842,7 +860,7 @@ def main() -> int:
     block, stack = None, None
     if args.only is None:
         print("[bench] config-4 block stack", file=sys.stderr, flush=True)
-        stack = BlockStack(rng, hip, ops, joint_qkv=True, fused=True, half=True)
+        stack = BlockStack(rng, hip, ops, joint_qkv=True, fused=True, half=True, hattn=True)
         block = stack.measure(stream, 5, cached_kv=True)
         block["variant"] = BLOCK_VARIANT
         print(f"[bench] block stack: {block['latency_ms']:.3f} ms for {block['blocks']} blocks "

@@ -238,6 +238,16 @@ int mi_gemm_nt_q8_0_f16a(const void* A, const void* W, const float* bias, float*
 int mi_gemm_nt_q8_0_geglu_f16(const void* A, const void* W, const float* bias, void* G, uint32_t M,
                               uint32_t F, uint32_t K, uint32_t lda, uint32_t ldg, void* stream);
 
+/* fp16 output (extension, no counterpart in the reference; for the block's
+ * MI_BLOCK_FP16_ATTENTION): C[M,N] = fp16(A . deq(W)^T + bias), the fp32
+ * result of the unsplit GEMM rounded once (RNE). A is fp32 or fp16
+ * (a_dtype MI_F32 / MI_F16, layout as in mi_gemm_nt_q8_0 / _f16a); C is
+ * fp16 with row stride ldc (0 -> N) in elements; mode 0, batch 1, no K
+ * split. K a positive multiple of 32, W 16-byte aligned, C 2-byte aligned
+ * (8-byte aligned with ldc % 4 == 0 for the vector stores).                  */
+int mi_gemm_nt_q8_0_f16o(const void* A, uint32_t a_dtype, const void* W, const float* bias, void* C,
+                         uint32_t M, uint32_t N, uint32_t K, uint32_t lda, uint32_t ldc, void* stream);
+
 /* Q8 NN GEMM (the conv / 1x1 paths' weights-left product):
  *   C[M,N] (=|+=) deq(A[M,K]) . B[K,N]
  * A in the split layout, read at FLAT index fl = z*sA + m*lda + k: value
@@ -386,9 +396,16 @@ int mi_add_inplace(float* x, const float* a, uint64_t n, void* stream);
  *     the LayerNorm outputs, the attention outputs and the GEGLU output --
  *     are stored as fp16 (each fp32 value rounded once, RNE, which is what the
  *     GEMM's A staging does to an fp32 tensor) and read by the fp16-A GEMM:
- *     half the bytes, no conversion in the GEMM.
- * Every flag combination computes the same bits (the block sums in a fixed
- * order, and the GEMMs that differ between the variants never split K).   */
+ *     half the bytes, no conversion in the GEMM;
+ *   MI_BLOCK_FP16_ATTENTION: the Q / K / V projections and the cached
+ *     context K / V are stored as fp16 (mi_gemm_nt_q8_0_f16o: the fp32 result
+ *     rounded once) and both attentions take fp16 inputs, i.e. attention at the
+ *     precision of the fp16 attention entries (configs 2 and 3) instead of the
+ *     fp32 inputs' hi + lo split. A precision choice, not a layout one: the
+ *     block's result differs from the flag-off block's by that rounding.
+ * Within one setting of MI_BLOCK_FP16_ATTENTION every combination of the other
+ * flags computes the same bits (the block sums in a fixed order, and the
+ * GEMMs that differ between the variants never split K).                   */
 typedef struct mi_block_weights {
     const float *norm1_w, *norm1_b, *norm2_w, *norm2_b, *norm3_w, *norm3_b; /* [channels] */
     const void *attn1_q, *attn1_k, *attn1_v, *attn1_out;    /* [channels, channels] */
@@ -403,7 +420,7 @@ typedef struct mi_block_weights {
     const float* ff_down_b;                                  /* [channels] or NULL */
 } mi_block_weights;
 
-enum { MI_BLOCK_FUSED_EPILOGUES = 1, MI_BLOCK_JOINT_QKV = 2, MI_BLOCK_FP16_ACTIVATIONS = 4 };
+enum { MI_BLOCK_FUSED_EPILOGUES = 1, MI_BLOCK_JOINT_QKV = 2, MI_BLOCK_FP16_ACTIVATIONS = 4, MI_BLOCK_FP16_ATTENTION = 8 };
 
 typedef struct mi_block_dims {
     uint32_t batch, tokens, channels, heads, ctx_tokens, ctx_channels, ff_inner;
@@ -420,7 +437,9 @@ int mi_sdxl_block_forward(const mi_block_weights* w, const mi_block_dims* dims, 
  * and step (sdvkgen.cpp:1283-1290; ctx uploaded once at :3659-3667).
  * mi_block_ctx_kv computes K = ctx . attn2_k^T and V = ctx . attn2_v^T once
  * into `kv` (K, then V at byte offset mi_block_ctx_kv_bytes / 2; each
- * [batch * ctx_tokens, channels] fp32; 256-byte aligned, caller-owned);
+ * [batch * ctx_tokens, channels] fp32, or fp16 when dims->flags has
+ * MI_BLOCK_FP16_ATTENTION; 256-byte aligned, caller-owned; the cache must be
+ * built and read with the same flag);
  * mi_sdxl_block_forward_kv then runs the block exactly like
  * mi_sdxl_block_forward but reads K / V from `kv` instead of projecting ctx;
  * both project with the same unsplit GEMMs, so cached and fresh results are

@@ -50,7 +50,7 @@ class MiBlockDims(ctypes.Structure):
                                     "ff_inner", "flags")]
 
 
-MI_BLOCK_FUSED_EPILOGUES, MI_BLOCK_JOINT_QKV, MI_BLOCK_FP16_ACTIVATIONS = 1, 2, 4
+MI_BLOCK_FUSED_EPILOGUES, MI_BLOCK_JOINT_QKV, MI_BLOCK_FP16_ACTIVATIONS, MI_BLOCK_FP16_ATTENTION = 1, 2, 4, 8
 
 
 class MiGgufTensorInfo(ctypes.Structure):
@@ -91,6 +91,7 @@ SIGNATURES = {
     "mi_gemm_nt_q8_0_geglu_f16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp]),
     "mi_gemm_nt_q8_0_f16a": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u64, _u64,
                                             _vp, _u64, _vp]),
+    "mi_gemm_nt_q8_0_f16o": (ctypes.c_int, [_vp, _u32, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp]),
     "mi_gemm_nn_q8_split": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32,
                                            _u64, _u64, _u64, _vp]),
     "mi_gemm_nn_q8_workspace_bytes": (_u64, [_u32, _u32, _u32, _u32]),

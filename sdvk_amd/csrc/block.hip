@@ -17,8 +17,17 @@
 //     epilogue (mi_gemm_nt_q8_0_geglu), which removes the three residual-add
 //     passes and the [rows, 2 ff_inner] intermediate;
 //   MI_BLOCK_JOINT_QKV: attn1 to_q / to_k / to_v are one [3C, C] Q8_0 matrix
-//     (the three pointers must be C x C matrices apart), projected by one GEMM.
-// Every variant computes the same bits: the GEMMs whose results must agree
+//     (the three pointers must be C x C matrices apart), projected by one GEMM;
+//   MI_BLOCK_FP16_ACTIVATIONS: LayerNorm, attention and GEGLU outputs stored as
+//     fp16 for the GEMMs that read them (the GEMM rounds its A operand to fp16
+//     anyway: the same bits);
+//   MI_BLOCK_FP16_ATTENTION: the Q / K / V projections (and the cached context
+//     K / V) are stored as fp16, the RNE rounding of their fp32 results, and
+//     both attentions run on fp16 inputs (the fp16 kernel's pipeline) instead
+//     of splitting fp32 inputs into fp16 hi + lo parts. Attention then works at
+//     the precision of the library's fp16 attention entries; the block's bits
+//     differ from the flag-off block by that rounding.
+// Within one setting of MI_BLOCK_FP16_ATTENTION every variant computes the same bits: the GEMMs whose results must agree
 // across variants (Q / K / V, context K / V, FF-up) never split K, the
 // residual GEMMs split K the same way in both epilogue forms (partials in the
 // workspace, summed in a fixed order), and an unsplit GEMM's sums do not
@@ -75,7 +84,8 @@ int check_dims(const mi_block_dims& d, const char* fn) {
                     d.heads);
     if (d.channels % 32 || d.ctx_channels % 32 || d.ff_inner % 32)
         return fail(MI_ERR_UNSUPPORTED, "%s: channels, ctx_channels and ff_inner must be multiples of 32 (Q8_0 K)", fn);
-    if (d.flags & ~static_cast<uint32_t>(MI_BLOCK_FUSED_EPILOGUES | MI_BLOCK_JOINT_QKV | MI_BLOCK_FP16_ACTIVATIONS))
+    if (d.flags & ~static_cast<uint32_t>(MI_BLOCK_FUSED_EPILOGUES | MI_BLOCK_JOINT_QKV | MI_BLOCK_FP16_ACTIVATIONS |
+                                         MI_BLOCK_FP16_ATTENTION))
         return fail(MI_ERR_INVALID_ARG, "%s: unknown flags 0x%x", fn, d.flags);
     return MI_OK;
 }
@@ -87,9 +97,9 @@ int check_dims(const mi_block_dims& d, const char* fn) {
     } while (0)
 
 // ld: token stride of q, k and v (C, or 3C for the joint Q/K/V projection);
-// o_half: the output stored as fp16
-int attention(const mi_block_dims& d, const float* q, const float* k, const float* v, uint64_t ld, void* o,
-              uint32_t tk, const int32_t* kv_len, bool o_half, hipStream_t s) {
+// in_half: q, k, v hold fp16; o_half: the output stored as fp16
+int attention(const mi_block_dims& d, const void* q, const void* k, const void* v, uint64_t ld, void* o,
+              uint32_t tk, const int32_t* kv_len, bool in_half, bool o_half, hipStream_t s) {
     mi_attn_args x{};
     x.q = q;
     x.k = k;
@@ -103,7 +113,7 @@ int attention(const mi_block_dims& d, const float* q, const float* k, const floa
     x.Tk = tk;
     x.C = d.channels;
     x.heads = d.heads;
-    x.in_dtype = MI_F32;
+    x.in_dtype = in_half ? MI_F16 : MI_F32;
     x.out_dtype = o_half ? MI_F16 : MI_F32;
     x.kv_len = kv_len;
     // the output only feeds the out-projection GEMM, which rounds its A
@@ -133,20 +143,30 @@ int check_weights(const mi_block_weights& w, const mi_block_dims& d, const char*
     return MI_OK;
 }
 
-// Bytes of the cached cross-attention K and V: two [batch * ctx_tokens, channels] fp32 tensors.
+bool fp16_attention(const mi_block_dims& d) { return (d.flags & MI_BLOCK_FP16_ATTENTION) != 0; }
+
+// Bytes of the cached cross-attention K and V: two [batch * ctx_tokens, channels]
+// tensors, fp32 (fp16 with MI_BLOCK_FP16_ATTENTION).
 uint64_t ctx_kv_bytes(const mi_block_dims& d) {
-    return 2 * round256(static_cast<uint64_t>(d.batch) * d.ctx_tokens * d.channels * 4);
+    return 2 * round256(static_cast<uint64_t>(d.batch) * d.ctx_tokens * d.channels * (fp16_attention(d) ? 2 : 4));
 }
 
-int ctx_kv(const mi_block_weights& w, const mi_block_dims& d, const float* ctx, float* k, float* v, hipStream_t s) {
+// K and V of the context, into k / v (fp32, or fp16 with MI_BLOCK_FP16_ATTENTION).
+int ctx_kv(const mi_block_weights& w, const mi_block_dims& d, const float* ctx, void* k, void* v, hipStream_t s) {
     const uint32_t crow = d.batch * d.ctx_tokens;
-    MI_TRY(mi_gemm_nt_q8_0(ctx, w.attn2_k, nullptr, k, crow, d.channels, d.ctx_channels, 0, 0, 0, 1, 0, 0, s));
-    return mi_gemm_nt_q8_0(ctx, w.attn2_v, nullptr, v, crow, d.channels, d.ctx_channels, 0, 0, 0, 1, 0, 0, s);
+    if (fp16_attention(d)) {
+        MI_TRY(mi_gemm_nt_q8_0_f16o(ctx, MI_F32, w.attn2_k, nullptr, k, crow, d.channels, d.ctx_channels, 0, 0, s));
+        return mi_gemm_nt_q8_0_f16o(ctx, MI_F32, w.attn2_v, nullptr, v, crow, d.channels, d.ctx_channels, 0, 0, s);
+    }
+    MI_TRY(mi_gemm_nt_q8_0(ctx, w.attn2_k, nullptr, static_cast<float*>(k), crow, d.channels, d.ctx_channels, 0, 0, 0,
+                           1, 0, 0, s));
+    return mi_gemm_nt_q8_0(ctx, w.attn2_v, nullptr, static_cast<float*>(v), crow, d.channels, d.ctx_channels, 0, 0, 0,
+                           1, 0, 0, s);
 }
 
 // One block. Cross-attention K / V come from `kv` (K then V, ctx_kv_bytes
 // layout) when given, else are projected from `ctx` into the workspace.
-int forward(const mi_block_weights& w, const mi_block_dims& d, float* x, const float* ctx, const float* kv,
+int forward(const mi_block_weights& w, const mi_block_dims& d, float* x, const float* ctx, const void* kv,
             const int32_t* ctx_len, void* workspace, uint64_t workspace_bytes, hipStream_t s, const char* fn) {
     MI_TRY(check_dims(d, fn));
     MI_TRY(check_weights(w, d, fn));
@@ -173,6 +193,15 @@ int forward(const mi_block_weights& w, const mi_block_dims& d, float* x, const f
         return mi_gemm_nt_q8_0_ws(static_cast<const float*>(A), W, bias, out, rows, C, K, mode, 0, 0, 1, 0, 0,
                                   ws.split, ws.split_bytes, s);
     };
+    // MI_BLOCK_FP16_ATTENTION: the Q / K / V projections store fp16 (element
+    // offsets below count halves then)
+    const bool hattn = fp16_attention(d);
+    const uint64_t esz = hattn ? 2 : 4;
+    auto proj = [&](const void* A, const void* W, void* out, uint32_t N) {
+        if (hattn) return mi_gemm_nt_q8_0_f16o(A, half ? MI_F16 : MI_F32, W, nullptr, out, rows, N, C, 0, 0, s);
+        return gemm(A, W, nullptr, static_cast<float*>(out), rows, N, C);
+    };
+    auto at = [&](const void* base, uint64_t elems) { return static_cast<const char*>(base) + elems * esz; };
     auto layernorm = [&](const float* g, const float* b) {
         return half ? mi_layernorm_f16(x, g, b, ws.n, rows, C, 1e-5f, s) : mi_layernorm(x, g, b, ws.n, rows, C, 1e-5f, s);
     };
@@ -188,26 +217,26 @@ int forward(const mi_block_weights& w, const mi_block_dims& d, float* x, const f
     MI_TRY(layernorm(w.norm1_w, w.norm1_b));
     // the joint result [rows, 3C] goes to the FF-up region, free until the FF stage
     if (d.flags & MI_BLOCK_JOINT_QKV) {
-        MI_TRY(gemm(ws.n, w.attn1_q, nullptr, ws.h, rows, 3 * C, C));
-        MI_TRY(attention(d, ws.h, ws.h + C, ws.h + 2 * C, 3ull * C, ws.o, d.tokens, nullptr, half, s));
+        MI_TRY(proj(ws.n, w.attn1_q, ws.h, 3 * C));
+        MI_TRY(attention(d, ws.h, at(ws.h, C), at(ws.h, 2ull * C), 3ull * C, ws.o, d.tokens, nullptr, hattn, half, s));
     } else {
-        MI_TRY(gemm(ws.n, w.attn1_q, nullptr, ws.q, rows, C, C));
-        MI_TRY(gemm(ws.n, w.attn1_k, nullptr, ws.k, rows, C, C));
-        MI_TRY(gemm(ws.n, w.attn1_v, nullptr, ws.v, rows, C, C));
-        MI_TRY(attention(d, ws.q, ws.k, ws.v, C, ws.o, d.tokens, nullptr, half, s));
+        MI_TRY(proj(ws.n, w.attn1_q, ws.q, C));
+        MI_TRY(proj(ws.n, w.attn1_k, ws.k, C));
+        MI_TRY(proj(ws.n, w.attn1_v, ws.v, C));
+        MI_TRY(attention(d, ws.q, ws.k, ws.v, C, ws.o, d.tokens, nullptr, hattn, half, s));
     }
     MI_TRY(residual(ws.o, w.attn1_out, w.attn1_out_b, C));
     // cross-attention over the context
     MI_TRY(layernorm(w.norm2_w, w.norm2_b));
-    MI_TRY(gemm(ws.n, w.attn2_q, nullptr, ws.q, rows, C, C));
-    const float *ck = ws.k, *cv = ws.v;
+    MI_TRY(proj(ws.n, w.attn2_q, ws.q, C));
+    const void *ck = ws.k, *cv = ws.v;
     if (kv) {
         ck = kv;
-        cv = kv + ctx_kv_bytes(d) / 2 / 4;
+        cv = static_cast<const char*>(kv) + ctx_kv_bytes(d) / 2;
     } else {
         MI_TRY(ctx_kv(w, d, ctx, ws.k, ws.v, s));
     }
-    MI_TRY(attention(d, ws.q, ck, cv, C, ws.o, d.ctx_tokens, ctx_len, half, s));
+    MI_TRY(attention(d, ws.q, ck, cv, C, ws.o, d.ctx_tokens, ctx_len, hattn, half, s));
     MI_TRY(residual(ws.o, w.attn2_out, w.attn2_out_b, C));
     // GEGLU feed-forward
     MI_TRY(layernorm(w.norm3_w, w.norm3_b));
@@ -254,7 +283,8 @@ extern "C" int mi_block_ctx_kv(const mi_block_weights* wt, const mi_block_dims* 
         return fail(MI_ERR_INVALID_ARG, "%s: kv buffer %llu bytes < %llu needed", fn,
                     static_cast<unsigned long long>(kv_bytes), static_cast<unsigned long long>(ctx_kv_bytes(*dims)));
     if (!aligned(kv, 256)) return fail(MI_ERR_ALIGNMENT, "%s: kv buffer must be 256-byte aligned", fn);
-    return ctx_kv(*wt, *dims, ctx, kv, kv + ctx_kv_bytes(*dims) / 2 / 4, static_cast<hipStream_t>(stream));
+    return ctx_kv(*wt, *dims, ctx, kv, reinterpret_cast<char*>(kv) + ctx_kv_bytes(*dims) / 2,
+                  static_cast<hipStream_t>(stream));
 }
 
 extern "C" int mi_sdxl_block_forward_kv(const mi_block_weights* wt, const mi_block_dims* dims, float* x,

@@ -50,7 +50,7 @@ struct GemmArgs {
     uint32_t cvec;          // C rows 16-byte aligned (C % 16 == 0, ldc % 4 == 0, sC % 4 == 0)
     uint32_t bvec;          // bias 16-byte aligned
     uint32_t F;             // GEGLU epilogue: output columns (W has 2F rows: value rows, then gate rows)
-    uint32_t out_half;      // GEGLU epilogue: G stored as fp16 (ldc in halves), the fp32 result rounded once
+    uint32_t out_half;      // GEGLU / plain mode-0 epilogue: output stored as fp16 (ldc in halves), the fp32 result rounded once
     uint64_t split_stride;  // K-split partials: elements between the planes of consecutive splits
 };
 
@@ -262,6 +262,27 @@ __device__ __forceinline__ void store_tiles(const GemmArgs& a, float* C, float* 
             const floatx4 v = *reinterpret_cast<const floatx4*>(&stage[row * kStageLd + col]);
             const uint32_t m = mb + row, n = nb + col;
             if (m >= a.M) continue;
+            if (EPI == kEpiPlain && a.out_half) {
+                // mode 0 with an fp16 output: acc + bias in fp32, then one RNE
+                // rounding (the empty register constraint keeps the rounding from
+                // fusing into the add)
+                floatx4 o = v;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (use_bias) o[e] += a.bias[min(n + e, a.N - 1)];
+                asm volatile("" : "+v"(o));
+                const half4 h = {static_cast<_Float16>(o[0]), static_cast<_Float16>(o[1]),
+                                 static_cast<_Float16>(o[2]), static_cast<_Float16>(o[3])};
+                _Float16* ch = reinterpret_cast<_Float16*>(C) + static_cast<uint64_t>(m) * a.ldc + n;
+                if (vec && n + 3 < a.N) {
+                    *reinterpret_cast<half4*>(ch) = h;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (n + e < a.N) ch[e] = h[e];
+                }
+                continue;
+            }
             float* c = C + static_cast<uint64_t>(m) * a.ldc + n;
             if (vec && vec_bias && n + 3 < a.N) {
                 if (EPI == kEpiResidual) {
@@ -1311,6 +1332,46 @@ extern "C" int mi_gemm_nt_q8_0_geglu_f16(const void* A, const void* W, const flo
                                          uint32_t F, uint32_t K, uint32_t lda, uint32_t ldg, void* stream) {
     return gemm_geglu("mi_gemm_nt_q8_0_geglu_f16", A, W, bias, G, M, F, K, lda, ldg,
                       static_cast<hipStream_t>(stream), true, true);
+}
+
+namespace mi {
+namespace {
+// C (fp16) = A . W^T (+ bias), one RNE rounding of the fp32 result; A fp32 or
+// fp16 (a_half). Mode 0 only and never split (no workspace), so the result is
+// the rounding of the unsplit fp32 GEMM's bits.
+int gemm_f16out(const char* fn, const void* A, bool a_half, const void* W, const float* bias, void* C, uint32_t M,
+                uint32_t N, uint32_t K, uint32_t lda, uint32_t ldc, hipStream_t stream) {
+    if (M == 0 || N == 0) return MI_OK;
+    if (K == 0 || K % 32) return fail(MI_ERR_UNSUPPORTED, "%s: K=%u must be a positive multiple of 32", fn, K);
+    uint32_t mode = 0;
+    int st = validate(fn, A, W, C, M, N, K, mode, lda, ldc, 1, 0, 0, true, a_half);
+    if (st) return st;
+    if (!aligned(W, 16)) return fail(MI_ERR_ALIGNMENT, "%s: W must be 16-byte aligned", fn);
+    const uint64_t wbytes = static_cast<uint64_t>(N) * (K / 32) * 34;
+    if (wbytes + 16 >= (uint64_t(1) << 32)) return fail(MI_ERR_UNSUPPORTED, "%s: weight >= 4 GiB", fn);
+    const uint64_t cbytes = (static_cast<uint64_t>(M - 1) * ldc + N) * 2;
+    const uint64_t abytes = (static_cast<uint64_t>(M - 1) * lda + K) * (a_half ? 2 : 4);
+    if (overlaps(C, cbytes, A, abytes) || overlaps(C, cbytes, W, wbytes) || overlaps(C, cbytes, bias, uint64_t(N) * 4))
+        return fail(MI_ERR_ALIASING, "%s: C overlaps an input", fn);
+    GemmArgs a = make_args(static_cast<const float*>(A), static_cast<const uint8_t*>(W), nullptr, bias,
+                           static_cast<float*>(C), M, N, K, 0, lda, ldc, 0, 0, (K / 32) * 34);
+    a.out_half = 1u;
+    a.cvec = aligned(C, 8) && ldc % 4 == 0 ? 1u : 0u;  // 8-byte stores of four fp16 outputs
+    a.bvec = 0u;
+    const Plan p = plan_for(M, N, K, 1, nullptr, 0);
+    if (a_half) dispatch<kBlocks34, kEpiPlain, true>(a, 1, p, nullptr, stream);
+    else dispatch<kBlocks34, kEpiPlain>(a, 1, p, nullptr, stream);
+    return check_launch(fn);
+}
+}  // namespace
+}  // namespace mi
+
+extern "C" int mi_gemm_nt_q8_0_f16o(const void* A, uint32_t a_dtype, const void* W, const float* bias, void* C,
+                                    uint32_t M, uint32_t N, uint32_t K, uint32_t lda, uint32_t ldc, void* stream) {
+    if (a_dtype != MI_F32 && a_dtype != MI_F16)
+        return fail(MI_ERR_INVALID_ARG, "mi_gemm_nt_q8_0_f16o: a_dtype %u (MI_F32 or MI_F16)", a_dtype);
+    return gemm_f16out("mi_gemm_nt_q8_0_f16o", A, a_dtype == MI_F16, W, bias, C, M, N, K, lda, ldc,
+                       static_cast<hipStream_t>(stream));
 }
 
 extern "C" int mi_gemm_nt_q8_0_f16a(const void* A, const void* W, const float* bias, float* C, uint32_t M, uint32_t N,

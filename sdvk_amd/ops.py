@@ -29,14 +29,14 @@ from typing import Optional, Sequence
 
 from . import _lib
 from ._lib import (MI_ATTN_PREC_AUTO, MI_ATTN_PREC_FP16, MI_ATTN_PREC_SPLIT, MI_BLOCK_FP16_ACTIVATIONS,
-                   MI_BLOCK_FUSED_EPILOGUES, MI_BLOCK_JOINT_QKV, MI_F16, MI_F32, MiAttnArgs, MiBlockDims, MiBlockWeights,
+                   MI_BLOCK_FP16_ATTENTION, MI_BLOCK_FUSED_EPILOGUES, MI_BLOCK_JOINT_QKV, MI_F16, MI_F32, MiAttnArgs, MiBlockDims, MiBlockWeights,
                    MiError, call, ptr)
 
 __all__ = [
     "MiError", "MI_F32", "MI_F16", "MI_ATTN_PREC_AUTO", "MI_ATTN_PREC_FP16", "MI_ATTN_PREC_SPLIT",
-    "tuning", "tuning_set", "tuning_reset", "MI_BLOCK_FUSED_EPILOGUES", "MI_BLOCK_FP16_ACTIVATIONS", "MI_BLOCK_JOINT_QKV", "FusedAttnArgs", "fused_attn_supported", "fused_attention",
+    "tuning", "tuning_set", "tuning_reset", "MI_BLOCK_FUSED_EPILOGUES", "MI_BLOCK_FP16_ACTIVATIONS", "MI_BLOCK_FP16_ATTENTION", "MI_BLOCK_JOINT_QKV", "FusedAttnArgs", "fused_attn_supported", "fused_attention",
     "fused_attention_ex", "gemm_nt_q8", "gemm_nt_q8_bias", "gemm_nt_q8_0", "gemm_nt_q8_0_geglu", "gemm_nn_q8",
-    "gemm_nt_q8_0_f16a", "gemm_nt_q8_0_geglu_f16", "layernorm_f16", "geglu_f16",
+    "gemm_nt_q8_0_f16a", "gemm_nt_q8_0_f16o", "gemm_nt_q8_0_geglu_f16", "layernorm_f16", "geglu_f16",
     "gemm_workspace_bytes", "gemm_nn_workspace_bytes",
     "q8_0_dequant",
     "q8_split_dequant", "q8_0_to_split", "q8_0_quantize", "Pg", "dispatch", "KERNELS", "layernorm", "geglu", "add2",
@@ -224,6 +224,13 @@ def gemm_nt_q8_0_f16a(A, W, C, M: int, N: int, K: int, *, bias=None, mode: int =
     entry given A's fp16 values as fp32."""
     call("mi_gemm_nt_q8_0_f16a", ptr(A), ptr(W), ptr(bias), ptr(C), M, N, K, mode, lda, ldc, batch, sA, sC,
          *_ws(workspace), _s(stream))
+
+
+def gemm_nt_q8_0_f16o(A, W, C, M: int, N: int, K: int, *, a_dtype: int = MI_F32, bias=None, lda: int = 0,
+                      ldc: int = 0, stream=None) -> None:
+    """C (fp16) = fp16(A . W^T + bias), the unsplit fp32 result rounded once (mi_gemm_nt_q8_0_f16o; extension);
+    A fp32 or fp16 (a_dtype)."""
+    call("mi_gemm_nt_q8_0_f16o", ptr(A), a_dtype, ptr(W), ptr(bias), ptr(C), M, N, K, lda, ldc, _s(stream))
 
 
 def gemm_nt_q8_0_geglu_f16(A, W, G, M: int, F: int, K: int, *, bias=None, lda: int = 0, ldg: int = 0,

@@ -27,6 +27,7 @@ import emu as kemu  # noqa: E402
 from helpers import assert_parity, fp16_half_ulp, q8_weights, rms  # noqa: E402
 from oracle import binding as ob  # noqa: E402
 from sdvk_amd._lib import (MI_ATTN_PREC_FP16, MI_ATTN_PREC_SPLIT, MI_BLOCK_FP16_ACTIVATIONS,  # noqa: E402
+                           MI_BLOCK_FP16_ATTENTION,
                            MI_BLOCK_FUSED_EPILOGUES, MI_BLOCK_JOINT_QKV, MI_F16, MI_F32, MiAttnArgs, MiBlockDims,
                            MiBlockWeights)
 from test_gpu_block import BLOCK_TOL, make_weights  # noqa: E402
@@ -421,17 +422,20 @@ def attention_full(E, *, batch, Tq, Tk, C, heads, masked=False, nw=None, seed=1,
 
 
 def block(E, *, B, T, C, H, Tc, Cc, F, masked=False, blocks=2, order=0, front=False, fused=False, qkv_joint=False,
-          half=False):
+          half=False, hattn=False):
     """Two applications of one SDXL transformer block: uncached
     (mi_sdxl_block_forward) vs context K / V projected once (mi_block_ctx_kv,
     mi_sdxl_block_forward_kv), against the oracle's block; cached and fresh
     runs must be bit-identical (same GEMM plans, fixed summation order). With
     fused / qkv_joint / half (fp16 activations): one block with those flags
     against the plain block, bit for bit (every flag combination computes the
-    same sums)."""
+    same sums). hattn (MI_BLOCK_FP16_ATTENTION, fp16 Q / K / V and attention
+    inputs): against the oracle to the block bar, and the other flags against
+    the block with that flag alone."""
     E.order(order)
+    base = MI_BLOCK_FP16_ATTENTION if hattn else 0
     flags = ((MI_BLOCK_FUSED_EPILOGUES if fused else 0) | (MI_BLOCK_JOINT_QKV if qkv_joint else 0) |
-             (MI_BLOCK_FP16_ACTIVATIONS if half else 0))
+             (MI_BLOCK_FP16_ACTIVATIONS if half else 0) | base)
     w = make_weights(ob, C, Cc, F, seed=500)
     dw = {k: E.buf(v, front=front) for k, v in w.items()}
     ptrs = {k: b.ptr for k, b in dw.items()}
@@ -444,7 +448,7 @@ def block(E, *, B, T, C, H, Tc, Cc, F, masked=False, blocks=2, order=0, front=Fa
     # the same weights stored apart (three projection GEMMs)
     bw_apart = MiBlockWeights(*[dw[f[0]].ptr for f in MiBlockWeights._fields_])
     dims = MiBlockDims(B, T, C, H, Tc, Cc, F, flags)
-    plain = MiBlockDims(B, T, C, H, Tc, Cc, F, 0)
+    plain = MiBlockDims(B, T, C, H, Tc, Cc, F, base)
     x = ob.normal(3, B * T * C)
     ctx = ob.normal(4, B * Tc * Cc).astype(np.float16).astype(np.float32)
     kl = ob.uniform_int(8, 1, Tc, B) if masked else None
@@ -471,7 +475,7 @@ def block(E, *, B, T, C, H, Tc, Cc, F, masked=False, blocks=2, order=0, front=Fa
     assert e <= blocks * BLOCK_TOL, f"block vs oracle: {e:.3e} x RMS(update)"
     assert np.array_equal(cached, fresh), \
         f"cached vs fresh K / V differ by {float(np.max(np.abs(cached - fresh))):.3e}"
-    if flags:
+    if flags != base:
         # one block with the flags vs the plain block (weights apart, separate epilogues)
         outs = []
         for wts, dd in ((bw, dims), (bw_apart, plain)):
@@ -482,6 +486,34 @@ def block(E, *, B, T, C, H, Tc, Cc, F, masked=False, blocks=2, order=0, front=Fa
         assert np.array_equal(outs[0], outs[1]), \
             f"flags {flags:#x} vs plain block differ by {float(np.max(np.abs(outs[0] - outs[1]))):.3e}"
     return e
+
+
+def gemm_f16o(E, *, M, N, K, cfg=None, seed=1, order=0, front=False, ldc=0):
+    """mi_gemm_nt_q8_0_f16o (fp16 output, A fp32 and fp16) against the RNE
+    rounding of mi_gemm_nt_q8_0's fp32 output, bit for bit."""
+    _set_cfg(cfg)
+    E.order(order)
+    a16 = ob.normal(seed, M * K).astype(np.float16)
+    blocks = q8_weights(ob, seed + 1, N, K)
+    bias = ob.normal(seed + 2, N, 0.0, 0.02)
+    dW, dB = E.buf(blocks, front=front), E.buf(bias, front=front)
+    dA32, dA16 = E.buf(a16.astype(np.float32), front=front), E.buf(a16, front=front)
+    dC = E.buf(np.zeros(M * N, np.float32), front=front)
+    E.call("mi_gemm_nt_q8_0", dA32.ptr, dW.ptr, dB.ptr, dC.ptr, M, N, K, 0, 0, 0, 1, 0, 0, None)
+    want16 = dC.get(np.float32).astype(np.float16)
+    ld = ldc or N
+    for a_dtype, dA in ((0, dA32), (1, dA16)):
+        dH = E.buf(np.full((M - 1) * ld + N, np.float16(7.0), np.float16), front=front)
+        E.call("mi_gemm_nt_q8_0_f16o", dA.ptr, a_dtype, dW.ptr, dB.ptr, dH.ptr, M, N, K, 0, ldc, None)
+        got = dH.get(np.float16).reshape(-1)
+        rows = np.stack([got[m * ld:m * ld + N] for m in range(M)]).reshape(-1)
+        assert np.array_equal(rows.view(np.uint16), want16.view(np.uint16)), \
+            f"f16o (a_dtype {a_dtype}) differs from the rounded fp32 GEMM"
+        if ld > N:  # the padding columns stay untouched
+            pad = np.concatenate([got[m * ld + N:(m + 1) * ld] for m in range(M - 1)])
+            assert np.all(pad == np.float16(7.0)), "f16o wrote past N"
+    want = ob.gemm_nt_q8_0(a16.astype(np.float32), blocks, M, N, K, bias=bias, threads=ob.max_threads())
+    return assert_parity(want16.astype(np.float32), want, what="gemm f16o")
 
 
 def gemm_f16a(E, *, M, N, K, mode=0, cfg=None, seed=1, order=0, front=False):
@@ -553,7 +585,7 @@ def routing(E, *, table, order=0):
     return 0.0
 
 
-def block_full(E, *, fused=False, qkv_joint=False, cached=False, order=0):
+def block_full(E, *, fused=False, qkv_joint=False, cached=False, order=0, half=False, hattn=False):
     """The config-4 block (level 2: 2 x 1024 tokens, C 1280, 20 heads, context
     2 x 77 x 2048, FF 1280 -> 2 x 5120 -> 1280) at full size with the first and
     last workgroup of every grid dimension of every launch emulated: a bounds
@@ -572,7 +604,8 @@ def block_full(E, *, fused=False, qkv_joint=False, cached=False, order=0):
         nb = w["attn1_q"].nbytes
         ptrs.update(attn1_q=joint.ptr, attn1_k=joint.ptr + nb, attn1_v=joint.ptr + 2 * nb)
     bw = MiBlockWeights(*[ptrs[f[0]] for f in MiBlockWeights._fields_])
-    flags = (MI_BLOCK_FUSED_EPILOGUES if fused else 0) | (MI_BLOCK_JOINT_QKV if qkv_joint else 0)
+    flags = ((MI_BLOCK_FUSED_EPILOGUES if fused else 0) | (MI_BLOCK_JOINT_QKV if qkv_joint else 0) |
+             (MI_BLOCK_FP16_ACTIVATIONS if half else 0) | (MI_BLOCK_FP16_ATTENTION if hattn else 0))
     dims = MiBlockDims(B, T, C, H, Tc, Cc, F, flags)
     dx = E.buf(ob.normal(3, B * T * C))
     dc = E.buf(ob.normal(4, B * Tc * Cc).astype(np.float16).astype(np.float32))
@@ -710,7 +743,7 @@ def gguf_upload(E, *, big_rows=10240, big_cols=1280, order=0, front=False):
     return 0.0
 
 
-CASES = {"gemm_nt": gemm_nt, "gemm_geglu": gemm_geglu, "gemm_f16a": gemm_f16a, "gemm_nn": gemm_nn,
+CASES = {"gemm_nt": gemm_nt, "gemm_geglu": gemm_geglu, "gemm_f16a": gemm_f16a, "gemm_f16o": gemm_f16o, "gemm_nn": gemm_nn,
          "attention": attention, "block": block,
          "gguf_upload": gguf_upload, "q8": q8, "glue": glue, "gemm_full": gemm_full, "gemm_nn_full": gemm_nn_full,
          "attention_full": attention_full, "block_full": block_full, "routing": routing}

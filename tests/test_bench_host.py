@@ -173,7 +173,7 @@ def test_bench_line_on_stand_in_device(fake_device, monkeypatch, capsys, launch)
     assert len(out["breakdown"]) == len(bench.GEMM_SHAPES) + len(bench.ATTN_SHAPES)
     assert out["block_stack"]["blocks"] == 10
     assert out["block_stack"]["variant"] == {"cached_kv": True, "fused_epilogues": True, "joint_qkv": True,
-                                             "fp16_activations": True}
+                                             "fp16_activations": True, "fp16_attention": True}
     ks = out["block_stack"]["kernel_share"]
     assert "error" not in ks, ks
     assert set(ks["us_per_block"]) == {"gemm_q8", "attention", "glue"}
@@ -181,16 +181,17 @@ def test_bench_line_on_stand_in_device(fake_device, monkeypatch, capsys, launch)
     ex = out["extras"]
     for part in ("config0_gemm", "nn_gemm", "block_stack_plain", "block_stack_cached_kv",
                  "block_stack_fused_epilogues", "block_stack_joint_qkv", "block_stack_fp16_activations",
-                 "block_stack_all_but_fp16_activations", "gemm_candidates", "attention_candidates", "step_graph"):
+                 "block_stack_all_but_fp16_activations", "block_stack_fp16_attention",
+                 "block_stack_all_but_fp16_attention", "gemm_candidates", "attention_candidates", "step_graph"):
         assert part in ex and "error" not in ex[part], (part, ex.get(part))
     assert set(ex["gemm_candidates"]["us"]) == set(bench.GEMM_CANDIDATES) | {"default"}
     assert len(ex["gemm_candidates"]["default_us"]) == len(bench.GEMM_SHAPES) + 1
     assert set(ex["attention_candidates"]["us"]) == {"default", "nw2", "nw4", "nosplit"}
     assert len(ex["gemm_candidates"]["best"]) == len(bench.GEMM_SHAPES) + 1
     assert ex["block_stack_plain"]["variant"] == {"cached_kv": False, "fused_epilogues": False, "joint_qkv": False,
-                                                  "fp16_activations": False}
+                                                  "fp16_activations": False, "fp16_attention": False}
     for name in ("gemm_nt_q8_0", "fused_attention_ws", "gemm_nn_q8", "sdxl_block_forward", "block_ctx_kv",
-                 "sdxl_block_forward_kv", "q8_0_quantize"):
+                 "sdxl_block_forward_kv", "q8_0_quantize", "gemm_nt_q8_0_f16o"):
         assert name in fake_device, name
 
 

@@ -138,3 +138,30 @@ def test_attention_f16_out_equals_rounded_fp32(gpu, oracle, B, H, Tq, Tk, ws, kv
             outs.append(do.download(np.float16 if odt == MI_F16 else np.float32, B * Tq * C))
         assert np.array_equal(outs[0].view(np.uint16), outs[1].astype(np.float16).view(np.uint16)), \
             f"in {in_dt}: fp16 output is not the rounded fp32 output"
+
+
+@pytest.mark.parametrize("M,N,K,ldc", [(77, 96, 64, 0), (2048, 3840, 1280, 0), (154, 1280, 2048, 0),
+                                       (300, 260, 256, 264), (2048, 1280, 1280, 0)])
+def test_f16o_gemm_is_the_rounded_fp32_gemm(gpu, oracle, M, N, K, ldc):
+    """mi_gemm_nt_q8_0_f16o (the block's fp16 Q / K / V projections) stores the
+    RNE rounding of mi_gemm_nt_q8_0's fp32 result, for fp32 and fp16 A; padding
+    columns of a strided C stay untouched."""
+    print(f"[case] f16o gemm M={M} N={N} K={K} ldc={ldc}", flush=True)
+    a16, a32 = _half_a(oracle, 31, M * K)
+    blocks = q8_weights(oracle, 32, N, K)
+    bias = oracle.normal(33, N, 0.0, 0.02)
+    dW, dB = DeviceBuffer.from_array(blocks), DeviceBuffer.from_array(bias)
+    d32 = DeviceBuffer(M * N * 4)
+    ops.gemm_nt_q8_0(DeviceBuffer.from_array(a32), dW, d32, M, N, K, bias=dB)
+    synchronize()
+    want = d32.download(np.float32, M * N).astype(np.float16)
+    ld = ldc or N
+    for a_dtype, A in ((MI_F32, a32), (MI_F16, a16)):
+        dH = DeviceBuffer.from_array(np.full((M - 1) * ld + N, np.float16(7.0), np.float16))
+        ops.gemm_nt_q8_0_f16o(DeviceBuffer.from_array(A), dW, dH, M, N, K, a_dtype=a_dtype, bias=dB, ldc=ldc)
+        synchronize()
+        got = dH.download(np.float16, (M - 1) * ld + N)
+        rows = np.concatenate([got[m * ld:m * ld + N] for m in range(M)])
+        assert np.array_equal(rows.view(np.uint16), want.view(np.uint16)), f"a_dtype {a_dtype}"
+        if ld > N:
+            assert all(np.all(got[m * ld + N:(m + 1) * ld] == np.float16(7.0)) for m in range(M - 1))

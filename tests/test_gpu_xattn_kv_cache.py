@@ -16,17 +16,19 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("B,T,C,H,Tc,Cc,F,masked", [(2, 100, 320, 5, 77, 2048, 1280, True),
                                                     (1, 33, 64, 1, 5, 96, 160, False)])
-def test_block_cached_ctx_kv(gpu, oracle, B, T, C, H, Tc, Cc, F, masked):
+@pytest.mark.parametrize("flags", [0, ops.MI_BLOCK_FP16_ATTENTION | ops.MI_BLOCK_FP16_ACTIVATIONS |
+                                   ops.MI_BLOCK_FUSED_EPILOGUES])
+def test_block_cached_ctx_kv(gpu, oracle, B, T, C, H, Tc, Cc, F, masked, flags):
     """K / V of the context projected once (mi_block_ctx_kv) and reused by two
     block applications (mi_sdxl_block_forward_kv): within the block bar of the
     oracle's two blocks, and bit-identical to two uncached calls (both project
     with the same unsplit GEMMs and every sum has a fixed order)."""
-    print(f"[case] block cached kv B={B} T={T} C={C} Tc={Tc} Cc={Cc}", flush=True)
+    print(f"[case] block cached kv B={B} T={T} C={C} Tc={Tc} Cc={Cc} flags={flags}", flush=True)
     w = make_weights(oracle, C, Cc, F, seed=500)
     x = oracle.normal(3, B * T * C)
     ctx = oracle.normal(4, B * Tc * Cc).astype(np.float16).astype(np.float32)
     kl = oracle.uniform_int(8, 1, Tc, B) if masked else None
-    dims = ops.BlockDims(B, T, C, H, Tc, Cc, F)
+    dims = ops.BlockDims(B, T, C, H, Tc, Cc, F, flags)
     dev, bw = to_device(w)
     dx, dc = DeviceBuffer.from_array(x), DeviceBuffer.from_array(ctx)
     dl = DeviceBuffer.from_array(np.asarray(kl, np.int32)) if kl is not None else None

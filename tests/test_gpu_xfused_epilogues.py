@@ -89,12 +89,18 @@ def test_geglu_gemm(gpu, oracle, tune, M, F, K, cfg):
                                    ops.MI_BLOCK_FP16_ACTIVATIONS,
                                    ops.MI_BLOCK_FP16_ACTIVATIONS | ops.MI_BLOCK_FUSED_EPILOGUES,
                                    ops.MI_BLOCK_FP16_ACTIVATIONS | ops.MI_BLOCK_FUSED_EPILOGUES |
-                                   ops.MI_BLOCK_JOINT_QKV])
+                                   ops.MI_BLOCK_JOINT_QKV,
+                                   ops.MI_BLOCK_FP16_ATTENTION | ops.MI_BLOCK_FP16_ACTIVATIONS |
+                                   ops.MI_BLOCK_FUSED_EPILOGUES | ops.MI_BLOCK_JOINT_QKV,
+                                   ops.MI_BLOCK_FP16_ATTENTION | ops.MI_BLOCK_JOINT_QKV])
 def test_block_flags(gpu, oracle, B, T, C, H, Tc, Cc, F, masked, flags):
     """The block with fused epilogues, the joint Q/K/V projection and / or fp16
     activations: within the block bar of the oracle and bit-identical to the
-    plain block (weights stored apart, separate epilogues, fp32 activations)."""
+    plain block (weights stored apart, separate epilogues, fp32 activations).
+    With MI_BLOCK_FP16_ATTENTION (fp16 Q / K / V, a precision choice) the plain
+    block of the comparison carries that flag alone."""
     print(f"[case] block flags={flags} B={B} T={T} C={C} F={F}", flush=True)
+    base = flags & ops.MI_BLOCK_FP16_ATTENTION
     w = make_weights(oracle, C, Cc, F, seed=500)
     x = oracle.normal(3, B * T * C)
     ctx = oracle.normal(4, B * Tc * Cc).astype(np.float16).astype(np.float32)
@@ -110,7 +116,8 @@ def test_block_flags(gpu, oracle, B, T, C, H, Tc, Cc, F, masked, flags):
     dc = DeviceBuffer.from_array(ctx)
     dl = DeviceBuffer.from_array(np.asarray(kl, np.int32)) if kl is not None else None
     outs = []
-    for weights, dims in ((bw_f, ops.BlockDims(B, T, C, H, Tc, Cc, F, flags)), (bw, ops.BlockDims(B, T, C, H, Tc, Cc, F))):
+    for weights, dims in ((bw_f, ops.BlockDims(B, T, C, H, Tc, Cc, F, flags)),
+                          (bw, ops.BlockDims(B, T, C, H, Tc, Cc, F, base))):
         ws = DeviceBuffer(ops.block_workspace_bytes(dims))
         dx = DeviceBuffer.from_array(x)
         ops.sdxl_block_forward(weights, dims, dx, dc, ws, ctx_len=dl)

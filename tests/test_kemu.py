@@ -83,6 +83,9 @@ FAMILIES = {
         dict(case="gemm_f16a", M=77, N=96, K=64), dict(case="gemm_f16a", M=154, N=96, K=2048, mode=2),
         dict(case="gemm_f16a", M=300, N=200, K=256, cfg="0", mode=1), dict(case="gemm_f16a", M=400, N=300, K=256, cfg="5"),
         dict(case="gemm_f16a", M=130, N=100, K=96, front=True),
+        # fp16 output (the block's fp16 Q / K / V): the rounding of the fp32 GEMM's result, padded rows
+        dict(case="gemm_f16o", M=77, N=96, K=64), dict(case="gemm_f16o", M=300, N=260, K=256, cfg="5", ldc=264),
+        dict(case="gemm_f16o", M=130, N=98, K=320, front=True),
     ],
     "gemm_nn": [
         dict(M=64, N=64, K=32), dict(M=100, N=72, K=96), dict(M=130, N=260, K=100, mode=1),
@@ -136,6 +139,9 @@ FAMILIES = {
         dict(B=1, T=33, C=64, H=1, Tc=5, Cc=96, F=64, qkv_joint=True),
         dict(B=2, T=64, C=128, H=2, Tc=77, Cc=256, F=256, masked=True, half=True),
         dict(B=1, T=33, C=64, H=1, Tc=5, Cc=96, F=160, qkv_joint=True, fused=True, half=True),
+        # fp16 attention inputs: against the oracle, and the other flags bit for bit against the flag alone
+        dict(B=2, T=64, C=128, H=2, Tc=77, Cc=256, F=256, masked=True, hattn=True),
+        dict(B=1, T=33, C=64, H=1, Tc=5, Cc=96, F=160, qkv_joint=True, fused=True, half=True, hattn=True),
     ],
     "gguf_upload": [dict()],
     "q8": [dict(n=32), dict(n=4096), dict(n=224, front=True)],
@@ -169,7 +175,8 @@ def _fullsize() -> list[dict]:
             specs.append(dict(case="attention_full", batch=b, Tq=tq, Tk=tk, C=64 * h, heads=h, masked=masked, nw=nw))
     # the config-4 block: bounds only (first / last workgroups of every launch)
     specs += [dict(case="block_full"), dict(case="block_full", cached=True),
-              dict(case="block_full", fused=True, qkv_joint=True)]
+              dict(case="block_full", fused=True, qkv_joint=True),
+              dict(case="block_full", fused=True, qkv_joint=True, half=True, hattn=True, cached=True)]
     unique = {json.dumps(s, sort_keys=True): s for s in specs}
     return list(unique.values())
 
