@@ -117,10 +117,14 @@ def stats_report(csv_path: str, command: str, flops: dict | None = None) -> str:
 
 
 def _per_dispatch(csv_path: str, counter: str):
+    """[(kernel, grid, counter value, duration ns or None)] in dispatch order."""
     out = []
     for r in csv.DictReader(open(csv_path)):
         if r["Counter_Name"] == counter:
-            out.append((r["Kernel_Name"], int(r["Grid_Size"]), float(r["Counter_Value"])))
+            dur = None
+            if r.get("Start_Timestamp") and r.get("End_Timestamp"):
+                dur = float(r["End_Timestamp"]) - float(r["Start_Timestamp"])
+            out.append((r["Kernel_Name"], int(r["Grid_Size"]), float(r["Counter_Value"]), dur))
     return out
 
 
@@ -141,30 +145,43 @@ def sources_digest(root: Path | None = None) -> str:
 def traffic_report(fetch_csv: str, write_csv: str, copy_mib: int, family: str, command: str) -> dict:
     nbytes = copy_mib << 20
     result = {"family": family, "copy_probe_bytes": nbytes, "command": command, "sources_sha256": sources_digest()}
-    per_shape = collections.OrderedDict()
+    per_shape = collections.OrderedDict()  # (kernel, grid) -> {"fetch": [(bytes, ns)], "write": [...]}
     for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
         rows = _per_dispatch(path, counter)
-        copies = [v for n, _, v in rows if COPY_KERNEL.search(n)]
+        copies = [v for n, _, v, _ in rows if COPY_KERNEL.search(n)]
         if not copies:
             raise SystemExit(f"{path}: no copy-probe dispatch found")
         factor = nbytes / (max(copies) * 1024.0)
         result[f"{counter.lower()}_factor"] = round(factor, 5)
         result[f"{counter.lower()}_copy_kib"] = max(copies)
-        for n, grid, v in rows:
+        for n, grid, v, dur in rows:
             if is_main(n, family):
                 d = per_shape.setdefault((short_name(n), grid), {"fetch": [], "write": []})
-                d["fetch" if counter == "FETCH_SIZE" else "write"].append(v * 1024.0 * factor)
+                d["fetch" if counter == "FETCH_SIZE" else "write"].append((v * 1024.0 * factor, dur))
     shapes = []
     tot, cnt = 0.0, 0
     for (name, grid), d in per_shape.items():
-        f = sum(d["fetch"]) / max(len(d["fetch"]), 1)
-        w = sum(d["write"]) / max(len(d["write"]), 1)
-        shapes.append({"kernel": name, "grid": grid, "fetch_bytes": round(f), "write_bytes": round(w),
-                       "dispatches": len(d["fetch"])})
-        tot += (f + w) * len(d["fetch"])
-        cnt += len(d["fetch"])
+        # the two runs launch the same sequence: pair the i-th dispatch of each, then split
+        # the pairs into duration classes (one grid can serve shapes of very different cost)
+        pairs = [(fd[1] if fd[1] is not None else 0.0, (fd[0], wd[0], fd[1], wd[1]))
+                 for fd, wd in zip(d["fetch"], d["write"])]
+        for cls in _duration_classes(pairs):
+            k = len(cls)
+            f = sum(x[0] for _, x in cls) / k
+            w = sum(x[1] for _, x in cls) / k
+            durs = [x[2] for _, x in cls if x[2] is not None] + [x[3] for _, x in cls if x[3] is not None]
+            entry = {"kernel": name, "grid": grid, "fetch_bytes": round(f), "write_bytes": round(w), "dispatches": k}
+            if durs:
+                us = sum(durs) / len(durs) / 1e3
+                entry["profiled_us"] = round(us, 2)
+                entry["gbs"] = round((f + w) / (us * 1e3), 1)  # bytes / ns = GB/s
+            shapes.append(entry)
+            tot += (f + w) * k
+            cnt += k
     result["per_kernel_grid"] = shapes
     result["bytes_per_launch"] = round(tot / cnt) if cnt else None
+    result["note"] = ("fetch_bytes / write_bytes: HBM-side bytes per dispatch (FETCH_SIZE / WRITE_SIZE scaled by the "
+                      "copy probe); profiled_us: the profiled (serialised) dispatch's duration; gbs: their sum over it")
     return result
 
 

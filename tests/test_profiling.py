@@ -77,3 +77,20 @@ def test_traffic_report_scales_by_the_copy_probe(tmp_path):
     assert k["fetch_bytes"] == round(2000 * 1024 * 2.0) and k["write_bytes"] == round(100 * 1024)
     assert r["bytes_per_launch"] == round(2000 * 1024 * 2.0 + 100 * 1024)
     assert r["sources_sha256"] == p.sources_digest()  # the build the counters were read on
+
+
+def test_traffic_report_splits_duration_classes_and_rates(tmp_path):
+    """One grid serving shapes of very different cost (self- and cross-attention)
+    is reported per duration class, each with its GB/s over the profiled duration."""
+    hdr = ["Kernel_Name", "Grid_Size", "Counter_Name", "Counter_Value", "Start_Timestamp", "End_Timestamp"]
+    fetch, write = tmp_path / "f.csv", tmp_path / "w.csv"
+    _write(fetch, hdr, [[COPY, 1024, "FETCH_SIZE", 512, 0, 10], [ATTN_F16, 512, "FETCH_SIZE", 1000, 0, 100000],
+                        [ATTN_F16, 512, "FETCH_SIZE", 10, 0, 5000], [ATTN_F16, 512, "FETCH_SIZE", 1000, 0, 100000]])
+    _write(write, hdr, [[COPY, 1024, "WRITE_SIZE", 1024, 0, 10], [ATTN_F16, 512, "WRITE_SIZE", 500, 0, 100000],
+                        [ATTN_F16, 512, "WRITE_SIZE", 10, 0, 5000], [ATTN_F16, 512, "WRITE_SIZE", 500, 0, 100000]])
+    r = p.traffic_report(str(fetch), str(write), 1, "attention", "cmd")
+    short, long_ = r["per_kernel_grid"]
+    assert short["dispatches"] == 1 and long_["dispatches"] == 2
+    assert short["profiled_us"] == 5.0 and long_["profiled_us"] == 100.0
+    assert long_["fetch_bytes"] == round(1000 * 1024 * 2.0) and long_["write_bytes"] == 500 * 1024
+    assert long_["gbs"] == pytest.approx((1000 * 1024 * 2.0 + 500 * 1024) / 100e3, rel=1e-3)
