@@ -279,8 +279,8 @@ class BlockStack:
             B, T, C, H, Tc, Cc, F = self.DIMS
             flops -= 2.0 * B * Tc * C * Cc * 2 * self.nblocks  # the K / V projections are not in the timed pass
         return {"config": "BASELINE config 4: %d SDXL BasicTransformerBlocks, level 2 (C=1280, 2x1024 tokens, "
-                          "20 heads, ctx 2x77x2048, FF 1280->10240->5120->1280), Q8_0 weights, fp32 residual stream"
-                          % self.nblocks,
+                          "20 heads, ctx 2x77x2048, FF 1280->10240->5120->1280), Q8_0 weights, fp32 residual stream%s"
+                          % (self.nblocks, ", attention on fp16 Q/K/V (MI_BLOCK_FP16_ATTENTION)" if self.hattn else ""),
                 "blocks": self.nblocks, "latency_ms": round(ms, 4), "ms_per_block": round(ms / self.nblocks, 4),
                 "gflop": round(flops / 1e9, 1), "tflops": round(flops / (ms / 1e3) / 1e12, 2), "reps": reps}
 

@@ -29,12 +29,13 @@ from typing import Optional, Sequence
 
 from . import _lib
 from ._lib import (MI_ATTN_PREC_AUTO, MI_ATTN_PREC_FP16, MI_ATTN_PREC_SPLIT, MI_BLOCK_FP16_ACTIVATIONS,
-                   MI_BLOCK_FP16_ATTENTION, MI_BLOCK_FUSED_EPILOGUES, MI_BLOCK_JOINT_QKV, MI_F16, MI_F32, MiAttnArgs, MiBlockDims, MiBlockWeights,
-                   MiError, call, ptr)
+                   MI_BLOCK_FP16_ATTENTION, MI_BLOCK_FUSED_EPILOGUES, MI_BLOCK_JOINT_QKV, MI_F16, MI_F32, MiAttnArgs,
+                   MiBlockDims, MiBlockWeights, MiError, call, ptr)
 
 __all__ = [
     "MiError", "MI_F32", "MI_F16", "MI_ATTN_PREC_AUTO", "MI_ATTN_PREC_FP16", "MI_ATTN_PREC_SPLIT",
-    "tuning", "tuning_set", "tuning_reset", "MI_BLOCK_FUSED_EPILOGUES", "MI_BLOCK_FP16_ACTIVATIONS", "MI_BLOCK_FP16_ATTENTION", "MI_BLOCK_JOINT_QKV", "FusedAttnArgs", "fused_attn_supported", "fused_attention",
+    "tuning", "tuning_set", "tuning_reset", "MI_BLOCK_FUSED_EPILOGUES", "MI_BLOCK_FP16_ACTIVATIONS",
+    "MI_BLOCK_FP16_ATTENTION", "MI_BLOCK_JOINT_QKV", "FusedAttnArgs", "fused_attn_supported", "fused_attention",
     "fused_attention_ex", "gemm_nt_q8", "gemm_nt_q8_bias", "gemm_nt_q8_0", "gemm_nt_q8_0_geglu", "gemm_nn_q8",
     "gemm_nt_q8_0_f16a", "gemm_nt_q8_0_f16o", "gemm_nt_q8_0_geglu_f16", "layernorm_f16", "geglu_f16",
     "gemm_workspace_bytes", "gemm_nn_workspace_bytes",
