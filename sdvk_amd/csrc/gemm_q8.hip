@@ -334,8 +334,14 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     constexpr int W_UNITS = BN * BK / 8;          // (row, 8-k group) per step
     constexpr int W_IT = W_UNITS / NT;
     // 34-byte blocks with two blocks per step: one whole block per lane (three
-    // loads for 32 weights). Block wb of a step is weight row wb % BN, block
-    // column wb / BN, so a wave's blocks share one byte alignment.
+    // loads for 32 weights). Block wb of a step is weight row wb / KB, block
+    // column wb % KB: the KB blocks of a row (its 68 contiguous bytes of the
+    // step) sit on adjacent lanes, so one load instruction of a wave touches
+    // 32 weight rows instead of 64. A load instruction's cost grows with the
+    // rows it touches: one 192x256 step's W loads take 890 cycles of a CU's
+    // load path this way against 1209 with a wave's lanes on 64 rows (a
+    // load-only probe of the step on MI355X; 16 rows, the four blocks of two
+    // steps, take 607 but gained nothing in the kernel).
     constexpr bool WBLK = WK == kBlocks34 && KB == 2 && !KTAIL;
     constexpr int W_BLOCKS = BN * KB;
     constexpr int WB_IT = (W_BLOCKS + NT - 1) / NT;
@@ -452,8 +458,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < WB_IT; ++i) {
         const int wb = (tid + i * NT) % W_BLOCKS;
-        const uint32_t n = EPI == kEpiGeglu ? geglu_wrow(n0, wb % BN, a.F) : min(n0 + wb % BN, a.N - 1);
-        const uint32_t byte = n * a.rowbytes + (wb / BN) * 34;
+        const uint32_t n = EPI == kEpiGeglu ? geglu_wrow(n0, wb / KB, a.F) : min(n0 + wb / KB, a.N - 1);
+        const uint32_t byte = n * a.rowbytes + (wb % KB) * 34;
         wb_off[i] = byte & ~3u;
         wb_qsel[i] = (byte & 2u) ? 0x07060504u : 0x05040302u;  // bytes 4..7 or 2..5 of (x[j+1]:x[j])
         wb_dsel[i] = (byte & 2u) ? 0x0c0c0302u : 0x0c0c0100u;  // bytes 2,3 or 0,1 of x[0]; 0x0c = zero
@@ -557,7 +563,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) q[j] = __builtin_amdgcn_perm(xs[j + 1], xs[j], wb_qsel[0]);
             const int wb = hi ? tid - W_BLOCKS : tid;
-            _Float16* dst = &Ws[st][(wb % BN) * LDK + (wb / BN) * 32 + (hi ? 16 : 0)];
+            _Float16* dst = &Ws[st][(wb / KB) * LDK + (wb % KB) * 32 + (hi ? 16 : 0)];
 #pragma unroll
             for (int j = 0; j < 2; ++j)
                 *reinterpret_cast<half8*>(dst + 8 * j) = dequant8_f16(q[2 * j], q[2 * j + 1], d);
@@ -572,7 +578,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
                     uint32_t q[8];
 #pragma unroll
                     for (int j = 0; j < 8; ++j) q[j] = __builtin_amdgcn_perm(x[j + 1], x[j], wb_qsel[i]);
-                    _Float16* dst = &Ws[st][(wb % BN) * LDK + (wb / BN) * 32];
+                    _Float16* dst = &Ws[st][(wb / KB) * LDK + (wb % KB) * 32];
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
                         *reinterpret_cast<half8*>(dst + 8 * j) = dequant8_f16(q[2 * j], q[2 * j + 1], d);
