@@ -417,7 +417,7 @@ def time_case(c, stream, hip, reps):
 # the LDS kernel's 256x128 / 128x128 / 128x64 / 64x64 / 256x256 / 192x256 tiles
 # (0-5) with and without K splits.
 GEMM_CANDIDATES = ["0", "0:2", "0:4", "1", "1:2", "1:3", "2", "2:2", "3", "3:2", "3:4", "3:8", "4", "4:2", "5",
-                   "5:2"]
+                   "5:2", "6"]
 
 
 def _part(out, name, fn):

@@ -69,7 +69,7 @@ int mi_version(void);
  * environment. An override picks tiles, K splits or workgroup sizes only, so
  * results stay within the operators' documented error (a different plan can
  * change the summation order, never the arithmetic). value NULL or "" clears.
- *   "gemm_cfg"          "<build 0..15>[:<K splits>]" (Q8 NT GEMM tile build;
+ *   "gemm_cfg"          "<build 0..6>[:<K splits>]" (Q8 NT GEMM tile build;
  *                       the splits apply to the workspace entries)
  *   "nn_kernel"         "general": the NN GEMM's untiled kernel for every shape
  *   "nn_splits"         "<1..64>": NN GEMM K splits (workspace entry)

@@ -31,7 +31,7 @@ int check_launch(const char* what);
 // "the built-in rules decide". They pick tiles, split counts and workgroup
 // sizes only: no override changes an operator's arithmetic beyond the
 // summation order of a different plan.
-constexpr int kGemmBuilds = 6;  // tile builds of gemm_q8.hip (kNumCfg)
+constexpr int kGemmBuilds = 7;  // tile builds of gemm_q8.hip (kNumCfg)
 struct Tuning {
     std::atomic<int> gemm_cfg{-1};          // tile build, or -1
     std::atomic<int> gemm_splits{1};        // K splits with gemm_cfg (workspace entries)

@@ -796,6 +796,7 @@ namespace {
 enum CfgId {
     kC256x128 = 0, kC128x128, kC128x64, kC64x64, kC256x256,  // 8 / 4 / 4 / 4 / 8 waves
     kC192x256,                                                // 8 waves of 96x64
+    kC128x128W8,                                              // 8 waves of 32x64
     kNumCfg
 };
 static_assert(kNumCfg == kGemmBuilds, "mi_tuning_set bounds gemm_cfg by kGemmBuilds");
@@ -910,6 +911,10 @@ void launch(int cfg, const GemmArgs& a, uint32_t batch, uint32_t splits, float* 
             launch_cfg<128, 128, 2, 2, 2, WK, false, 1, EPI, true, AH>(a, batch, splits, ws, s);
             break;
         case kC192x256: launch_cfg<192, 256, 2, 4, 2, WK, false, 2, EPI, true, AH>(a, batch, splits, ws, s); break;
+        case kC128x128W8:
+            // grids of one workgroup per CU: two waves per SIMD instead of one
+            launch_cfg<128, 128, 4, 2, 2, WK, false, 2, EPI, true, AH>(a, batch, splits, ws, s);
+            break;
         case kC128x64: launch_cfg<128, 64, 2, 2, 2, WK, false, 2, EPI, true, AH>(a, batch, splits, ws, s); break;
         case kC256x256:
             // The split layout's and the GEGLU epilogue's 256x256 builds need
@@ -946,7 +951,10 @@ struct Plan {
 // tile (8 waves, one workgroup per CU) where it yields a wave or more of
 // long-K tiles over more than 640 columns (at N = 640 the 128x128 tile is
 // faster: 8192x640x2560 61.6 vs 66.0 us); 128x128 (4 waves, two workgroups per
-// CU) for mid-size grids; 64x64 for the rest.
+// CU) for mid-size grids, as 8 waves of 32x64 when the grid has fewer tiles
+// than CUs and no K split (one workgroup per CU: two waves per SIMD instead
+// of one; 2048x1280x1280 20.7 vs 22.9 us, 2048x1280x5120 unsplit 75 vs 91);
+// 64x64 for the rest.
 // With a workspace (allow_split), long-K 128x128 grids of fewer tiles than
 // CUs split K into the most parts (>= 1024 k each; 2 or 3, as these grids
 // have >= 160 tiles) whose workgroups all fit two per CU (2048x1280x5120:
@@ -972,6 +980,8 @@ Plan choose(uint32_t M, uint32_t N, uint32_t K, uint32_t batch, bool allow_split
         p.cfg = kC128x128;
         if (allow_split && t128 < kCUs && K >= 4096)
             p.splits = static_cast<uint32_t>(std::max<uint64_t>(2, std::min<uint64_t>({2 * kCUs / t128, K / 1024, 4})));
+        else if (t128 < kCUs)
+            p.cfg = kC128x128W8;
     } else {
         p.cfg = kC64x64;
         if (allow_split && t64 < 2 * kCUs) {

@@ -57,7 +57,7 @@ def test_unsplit_sums_do_not_depend_on_the_tile_build(gpu, oracle, tune):
     dA, dW = DeviceBuffer.from_array(A), DeviceBuffer.from_array(blocks)
     dP, dS = DeviceBuffer.from_array(payload), DeviceBuffer.from_array(scales)
     ref = None
-    for cfg in ("0", "1", "2", "3", "4", "5"):
+    for cfg in ("0", "1", "2", "3", "4", "5", "6"):
         tune("gemm_cfg", cfg)
         for layout in ("blocks", "split"):
             dC = DeviceBuffer(M * N * 4)

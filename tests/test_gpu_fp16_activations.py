@@ -33,7 +33,7 @@ def _half_a(oracle, seed, n):
                                             (2048, 1280, 5120, 2, None), (300, 200, 256, 0, "0"),
                                             (300, 200, 256, 0, "2"), (300, 300, 256, 1, "4"),
                                             (400, 300, 256, 0, "5"), (200, 300, 512, 2, "5:2"),
-                                            (130, 100, 96, 0, None)])
+                                            (130, 100, 96, 0, None), (300, 200, 256, 1, "6")])
 def test_f16a_gemm_equals_fp32_gemm(gpu, oracle, tune, M, N, K, mode, cfg):
     print(f"[case] f16a gemm M={M} N={N} K={K} mode={mode} cfg={cfg}", flush=True)
     if cfg:

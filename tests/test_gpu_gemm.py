@@ -214,7 +214,8 @@ def test_rule_k_splits_sampled_rows(gpu, oracle, M, N, K, splits):
     assert e <= REL_RMS_TOL
 
 
-@pytest.mark.parametrize("cfg", ["0", "1", "2", "3", "4", "5", "0:3", "1:2", "2:5", "3:16", "4:2", "5:2", "5:3"])
+@pytest.mark.parametrize("cfg", ["0", "1", "2", "3", "4", "5", "6", "0:3", "1:2", "2:5", "3:16", "4:2", "5:2", "5:3",
+                                 "6:2"])
 @pytest.mark.parametrize("M,N,K", [(300, 200, 640), (1030, 130, 256)])
 def test_every_tile_config_and_split_k(gpu, oracle, tune, cfg, M, N, K):
     """Forces each tile configuration / K split (gemm_cfg "<cfg>[:<splits>]";

@@ -48,7 +48,8 @@ def test_residual_mode(gpu, oracle, tune, M, N, K, cfg):
 
 
 @pytest.mark.parametrize("M,F,K,cfg", [(77, 48, 64, None), (300, 200, 256, "4"), (130, 100, 96, None),
-                                       (2048, 5120, 1280, None), (300, 130, 256, "0"), (300, 130, 256, "5")])
+                                       (2048, 5120, 1280, None), (300, 130, 256, "0"), (300, 130, 256, "5"),
+                                       (300, 130, 256, "6")])
 def test_geglu_gemm(gpu, oracle, tune, M, F, K, cfg):
     print(f"[case] gemm geglu M={M} F={F} K={K} cfg={cfg}", flush=True)
     if cfg:

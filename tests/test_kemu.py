@@ -66,6 +66,9 @@ FAMILIES = {
         dict(M=64, N=64, K=2048, cfg="3:16"), dict(M=70, N=36, K=512, batch=3, lda=520, ldc=40, sA=37000,
                                                    sC=3000, cfg="3:4", mode=1),
         dict(M=130, N=200, K=512, cfg="1:3", mode=2), dict(M=200, N=300, K=640, cfg="5:3", front=True),
+        # 128x128 as 8 waves of 32x64: partial tiles, a K split, the split layout
+        dict(M=300, N=300, K=640, cfg="6"), dict(M=130, N=200, K=512, cfg="6:2", mode=1),
+        dict(M=200, N=260, K=320, cfg="6", layout="split", mode=2, front=True),
     ],
     # fused epilogues: residual mode 2 (C += A W^T + bias) and the GEGLU GEMM
     "gemm_fused": [
@@ -86,6 +89,8 @@ FAMILIES = {
         # fp16 output (the block's fp16 Q / K / V): the rounding of the fp32 GEMM's result, padded rows
         dict(case="gemm_f16o", M=77, N=96, K=64), dict(case="gemm_f16o", M=300, N=260, K=256, cfg="5", ldc=264),
         dict(case="gemm_f16o", M=130, N=98, K=320, front=True),
+        dict(case="gemm_geglu", M=200, F=130, K=128, cfg="6"), dict(case="gemm_f16a", M=300, N=200, K=256, cfg="6"),
+        dict(case="gemm_f16o", M=300, N=260, K=256, cfg="6", ldc=264), dict(case="gemm_nt", M=260, N=300, K=256, cfg="6", mode=2),
     ],
     "gemm_nn": [
         dict(M=64, N=64, K=32), dict(M=100, N=72, K=96), dict(M=130, N=260, K=100, mode=1),
@@ -222,8 +227,9 @@ def test_kernels_on_emulator(emulator, family):
 
 # The tile rules at the SDXL shapes of the benchmark: (op, dims, grid, work-items
 # per workgroup). GEMM (choose in gemm_q8.hip): 192x256 (8 waves) when that gives
-# >= 120 tiles and K >= 1280; 128x128 (4 waves) when that gives >= 160 tiles;
-# else 64x64 (4 waves). Grid = (tiles, splits, batch). With a workspace
+# >= 120 tiles and K >= 1280; 128x128 (4 waves) when that gives >= 160 tiles,
+# as 8 waves of 32x64 when those are fewer than 256 and K is not split; else
+# 64x64 (4 waves). Grid = (tiles, splits, batch). With a workspace
 # ("gemm_ws"): 128x128 grids under 256 tiles with K >= 4096 split K into the most
 # parts (2 or 3, >= 1024 k each) with tiles x parts <= 512, 64x64
 # grids under 512 tiles split K (powers of two) to about 256 workgroups with
@@ -233,8 +239,8 @@ def test_kernels_on_emulator(emulator, family):
 # 128 queries, 2-wave ones of 64 when Tq <= 64.
 ROUTING = [
     ["gemm", [8192, 640, 640], [320, 1, 1], 256], ["gemm", [8192, 5120, 640], [2560, 1, 1], 256],
-    ["gemm", [8192, 640, 2560], [320, 1, 1], 256], ["gemm", [2048, 1280, 1280], [160, 1, 1], 256],
-    ["gemm", [2048, 10240, 1280], [440, 1, 1], 512], ["gemm", [2048, 1280, 5120], [160, 1, 1], 256],
+    ["gemm", [8192, 640, 2560], [320, 1, 1], 256], ["gemm", [2048, 1280, 1280], [160, 1, 1], 512],
+    ["gemm", [2048, 10240, 1280], [440, 1, 1], 512], ["gemm", [2048, 1280, 5120], [160, 1, 1], 512],
     ["gemm_ws", [2048, 1280, 5120], [160, 3, 1], 256],
     ["gemm", [154, 640, 2048], [30, 1, 1], 256], ["gemm_ws", [154, 640, 2048], [30, 8, 1], 256],
     ["gemm", [154, 1280, 2048], [60, 1, 1], 256], ["gemm_ws", [154, 1280, 2048], [60, 4, 1], 256],
