@@ -345,12 +345,17 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     constexpr bool WBLK = WK == kBlocks34 && KB == 2 && !KTAIL;
     constexpr int W_BLOCKS = BN * KB;
     constexpr int WB_IT = (W_BLOCKS + NT - 1) / NT;
-    // Twice as many threads as blocks (the 4-wave 64x64 and 128x64 tiles, the
-    // 8-wave 256x128 tile): thread t dequantises half h = t / W_BLOCKS of block
+    // Twice as many threads as blocks in a 4-wave workgroup (the 64x64 and
+    // 128x64 tiles): thread t dequantises half h = t / W_BLOCKS of block
     // t % W_BLOCKS (every thread loads its block's window), so the
-    // dequantisation is spread over all waves instead of half of them, which
-    // on a 4-wave workgroup would be half of the SIMDs.
-    constexpr bool WHALF = WBLK && 2 * W_BLOCKS == NT;
+    // dequantisation is spread over all four waves instead of two, which would
+    // be half of the SIMDs. An 8-wave workgroup with as many threads (the
+    // 256x128 tile, the 8-wave 128x128 tile) keeps whole blocks on its first
+    // four waves, one per SIMD, and the other four issue their block loads out
+    // of range (no memory access): 482 load-path cycles per step for the
+    // 128x128 tile's weights in the probe, against 674 with every block loaded
+    // twice.
+    constexpr bool WHALF = WBLK && 2 * W_BLOCKS == NT && NT == 256;
     // Buffer-load fast path: two blocks per step keep each lane's byte
     // alignment fixed (68 = 0 mod 4), so the step advance is a scalar offset.
     constexpr bool FAST = KB == 2 && !KTAIL;
@@ -449,10 +454,10 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
     // start; the row stride is 0 mod 4 (K % 64 == 0) and a step advances 68
     // bytes, so a block's position inside its window (0 or 2 bytes) is fixed
     // for the lane. v_perm selectors pick d and the eight q dwords for either.
-    // Threads past the step's W_BLOCKS blocks load a duplicate (block
-    // wb mod W_BLOCKS) and store nothing: a load under a branch makes the
-    // compiler's wait counts assume it was skipped, so every later wait would
-    // also retire the loads of the step just issued.
+    // Threads past the step's W_BLOCKS blocks still issue the loads (out of
+    // range: zeros, no memory access) and store nothing: a load under a branch
+    // makes the compiler's wait counts assume it was skipped, so every later
+    // wait would also retire the loads of the step just issued.
     uint32_t wb_off[WB_IT], wb_qsel[WB_IT], wb_dsel[WB_IT];
     uint32_t wbx_[PF][WB_IT][9];
 #pragma unroll
@@ -460,7 +465,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q8_kernel(GemmArgs a) {
         const int wb = (tid + i * NT) % W_BLOCKS;
         const uint32_t n = EPI == kEpiGeglu ? geglu_wrow(n0, wb / KB, a.F) : min(n0 + wb / KB, a.N - 1);
         const uint32_t byte = n * a.rowbytes + (wb % KB) * 34;
-        wb_off[i] = byte & ~3u;
+        // past the step's blocks: out of range, so the load returns zeros and touches no memory
+        wb_off[i] = (!WHALF && W_BLOCKS % NT != 0 && tid + i * NT >= W_BLOCKS) ? 0x80000000u : byte & ~3u;
         wb_qsel[i] = (byte & 2u) ? 0x07060504u : 0x05040302u;  // bytes 4..7 or 2..5 of (x[j+1]:x[j])
         wb_dsel[i] = (byte & 2u) ? 0x0c0c0302u : 0x0c0c0100u;  // bytes 2,3 or 0,1 of x[0]; 0x0c = zero
     }
