@@ -955,7 +955,8 @@ struct Plan {
 // Picks the tile and K split for a shape (rules from per-shape sweeps of every
 // tile build on MI355X over the SDXL shapes, timed interleaved): the 192x256
 // tile (8 waves, one workgroup per CU) where it yields a wave or more of
-// long-K tiles over more than 640 columns (at N = 640 the 128x128 tile is
+// long-K tiles over more than 640 columns (256x128 where that fills more of a
+// single round) (at N = 640 the 128x128 tile is
 // faster: 8192x640x2560 61.6 vs 66.0 us); 128x128 (4 waves, two workgroups per
 // CU) for mid-size grids, as 8 waves of 32x64 when the grid has fewer tiles
 // than CUs and no K split (one workgroup per CU: two waves per SIMD instead
@@ -979,9 +980,12 @@ Plan choose(uint32_t M, uint32_t N, uint32_t K, uint32_t batch, bool allow_split
     auto tiles = [&](uint32_t bm, uint32_t bn) {
         return static_cast<uint64_t>(ceil_div(M, bm)) * ceil_div(N, bn) * batch;
     };
-    const uint64_t t192 = tiles(192, 256), t128 = tiles(128, 128), t64 = tiles(64, 64);
+    const uint64_t t192 = tiles(192, 256), t128 = tiles(128, 128), t64 = tiles(64, 64), t256 = tiles(256, 128);
     if (t192 >= 120 && K >= 1280 && N > 640) {
-        p.cfg = kC192x256;
+        // under one round, 256x128 tiles fill more CUs where they still fit one
+        // (the block's joint Q/K/V 2048x3840x1280: 240 against 165 tiles, 30.9
+        // against 32.7 us with fp16 A)
+        p.cfg = t192 < kCUs && t256 > t192 && t256 <= kCUs ? kC256x128 : kC192x256;
     } else if (t128 >= 160) {
         p.cfg = kC128x128;
         if (allow_split && t128 < kCUs && K >= 4096)

@@ -227,7 +227,8 @@ def test_kernels_on_emulator(emulator, family):
 
 # The tile rules at the SDXL shapes of the benchmark: (op, dims, grid, work-items
 # per workgroup). GEMM (choose in gemm_q8.hip): 192x256 (8 waves) when that gives
-# >= 120 tiles and K >= 1280; 128x128 (4 waves) when that gives >= 160 tiles,
+# >= 120 tiles and K >= 1280 (256x128, 8 waves, when both give under one round
+# and 256x128 more tiles); 128x128 (4 waves) when that gives >= 160 tiles,
 # as 8 waves of 32x64 when those are fewer than 256 and K is not split; else
 # 64x64 (4 waves). Grid = (tiles, splits, batch). With a workspace
 # ("gemm_ws"): 128x128 grids under 256 tiles with K >= 4096 split K into the most
@@ -245,6 +246,7 @@ ROUTING = [
     ["gemm", [154, 640, 2048], [30, 1, 1], 256], ["gemm_ws", [154, 640, 2048], [30, 8, 1], 256],
     ["gemm", [154, 1280, 2048], [60, 1, 1], 256], ["gemm_ws", [154, 1280, 2048], [60, 4, 1], 256],
     ["gemm", [9216, 1280, 1280], [240, 1, 1], 512], ["gemm_ws", [9216, 1280, 1280], [240, 1, 1], 512],
+    ["gemm", [2048, 3840, 1280], [240, 1, 1], 512],  # the block's joint Q/K/V: 256x128 tiles
     ["nn_ws", [320, 4096, 2880], [16, 3, 5], 512], ["nn_ws", [640, 4096, 5760], [16, 5, 3], 512],
     ["nn_ws", [1280, 1024, 11520], [4, 10, 6], 512], ["nn_ws", [1280, 1024, 640], [4, 10, 2], 512],
     ["nn", [1280, 1024, 11520], [4, 10, 1], 512],
