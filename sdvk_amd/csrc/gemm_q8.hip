@@ -962,11 +962,13 @@ struct Plan {
 // than CUs and no K split (one workgroup per CU: two waves per SIMD instead
 // of one; 2048x1280x1280 20.7 vs 22.9 us, 2048x1280x5120 unsplit 75 vs 91);
 // 64x64 for the rest.
-// With a workspace (allow_split), long-K 128x128 grids of fewer tiles than
-// CUs split K into the most parts (>= 1024 k each; 2 or 3, as these grids
-// have >= 160 tiles) whose workgroups all fit two per CU (2048x1280x5120:
-// 160 tiles x 3 = 480 workgroups, 55.2 us against 67.7 us for 2 parts and
-// 69.4 us for 4), and small 64x64 grids split K until ~256 workgroups run.
+// With a workspace (allow_split), long-K (>= 4096) 128x128 grids of fewer
+// tiles than CUs run as 256x128 tiles (8 waves) with K split into the most
+// parts (>= 1024 k each) that keep one round (2048x1280x5120: 80 tiles x 3 =
+// 240 workgroups, 52.3 us against 54.1 us for 128x128 tiles in 3 parts with
+// fp32 A and 45.6 against 48.6 with fp16 A; 128x128 in 3 parts had beaten 2
+// and 4 parts, 55.2 against 67.7 and 69.4 us), and small 64x64 grids split K
+// until ~256 workgroups run.
 Plan choose(uint32_t M, uint32_t N, uint32_t K, uint32_t batch, bool allow_split) {
     Plan p{kC64x64, 1};
     // mi_tuning_set("gemm_cfg", "<cfg>[:<splits>]") pins a build (tuning sweeps, tests)
@@ -988,10 +990,12 @@ Plan choose(uint32_t M, uint32_t N, uint32_t K, uint32_t batch, bool allow_split
         p.cfg = t192 < kCUs && t256 > t192 && t256 <= kCUs ? kC256x128 : kC192x256;
     } else if (t128 >= 160) {
         p.cfg = kC128x128;
-        if (allow_split && t128 < kCUs && K >= 4096)
-            p.splits = static_cast<uint32_t>(std::max<uint64_t>(2, std::min<uint64_t>({2 * kCUs / t128, K / 1024, 4})));
-        else if (t128 < kCUs)
+        if (allow_split && t128 < kCUs && K >= 4096) {
+            p.cfg = kC256x128;
+            p.splits = static_cast<uint32_t>(std::max<uint64_t>(2, std::min<uint64_t>(kCUs / t256, K / 1024)));
+        } else if (t128 < kCUs) {
             p.cfg = kC128x128W8;
+        }
     } else {
         p.cfg = kC64x64;
         if (allow_split && t64 < 2 * kCUs) {

@@ -194,10 +194,10 @@ def test_baseline_shapes_sampled_rows(gpu, oracle, M, N, K):
 @pytest.mark.parametrize("M,N,K,splits", [(2048, 1280, 5120, 3), (2048, 1280, 8192, 3), (2304, 1280, 4096, 2),
                                           (154, 1280, 2048, 4), (154, 640, 2048, 8)])
 def test_rule_k_splits_sampled_rows(gpu, oracle, M, N, K, splits):
-    """The planner's own K splits through the workspace entry (128 x 128 grids
-    below one wave of tiles split 2 or 3 ways so that every workgroup runs at
-    once; 64 x 64 grids split toward ~256 workgroups): the workspace the
-    library asks for pins the split count, sampled rows match the oracle (every
+    """The planner's own K splits through the workspace entry (long-K grids
+    below one round of 128 x 128 tiles run 256 x 128 tiles split 2 or 3 ways,
+    every workgroup at once; 64 x 64 grids split toward ~256 workgroups): the
+    workspace the library asks for pins the split count, sampled rows match the oracle (every
     row at M = 154: the cross-attention K / V projections of the bench, whose
     640-column plan is the 8-way split)."""
     print(f"[case] rule split M={M} N={N} K={K} splits={splits}", flush=True)

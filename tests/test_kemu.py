@@ -231,8 +231,8 @@ def test_kernels_on_emulator(emulator, family):
 # and 256x128 more tiles); 128x128 (4 waves) when that gives >= 160 tiles,
 # as 8 waves of 32x64 when those are fewer than 256 and K is not split; else
 # 64x64 (4 waves). Grid = (tiles, splits, batch). With a workspace
-# ("gemm_ws"): 128x128 grids under 256 tiles with K >= 4096 split K into the most
-# parts (2 or 3, >= 1024 k each) with tiles x parts <= 512, 64x64
+# ("gemm_ws"): 128x128 grids under 256 tiles with K >= 4096 run 256x128 tiles (8
+# waves) with K split into the most parts (>= 1024 k each) with tiles x parts <= 256, 64x64
 # grids under 512 tiles split K (powers of two) to about 256 workgroups with
 # >= 128 k per split. NN GEMM: 128x256 tiles (8 waves), grid (N tiles, M tiles,
 # splits); with a workspace ("nn_ws") the most K splits with tiles x splits <= 256
@@ -242,7 +242,7 @@ ROUTING = [
     ["gemm", [8192, 640, 640], [320, 1, 1], 256], ["gemm", [8192, 5120, 640], [2560, 1, 1], 256],
     ["gemm", [8192, 640, 2560], [320, 1, 1], 256], ["gemm", [2048, 1280, 1280], [160, 1, 1], 512],
     ["gemm", [2048, 10240, 1280], [440, 1, 1], 512], ["gemm", [2048, 1280, 5120], [160, 1, 1], 512],
-    ["gemm_ws", [2048, 1280, 5120], [160, 3, 1], 256],
+    ["gemm_ws", [2048, 1280, 5120], [80, 3, 1], 512],
     ["gemm", [154, 640, 2048], [30, 1, 1], 256], ["gemm_ws", [154, 640, 2048], [30, 8, 1], 256],
     ["gemm", [154, 1280, 2048], [60, 1, 1], 256], ["gemm_ws", [154, 1280, 2048], [60, 4, 1], 256],
     ["gemm", [9216, 1280, 1280], [240, 1, 1], 512], ["gemm_ws", [9216, 1280, 1280], [240, 1, 1], 512],

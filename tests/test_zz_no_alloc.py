@@ -58,7 +58,7 @@ def _run(lib, oracle, M, N, K, mode, seed):
 
 @pytest.mark.parametrize("first,second", [
     ((154, 1280, 2048, 0), (100, 640, 1024, 0)),    # 64x64 tiles, 4 then 8 K splits
-    ((2048, 1280, 5120, 2), (1000, 700, 4096, 1)),  # 128x128 tiles with 3 K splits, then 64x64 splits
+    ((2048, 1280, 5120, 2), (1000, 700, 4096, 1)),  # 256x128 tiles with 3 K splits, then 64x64 splits
     ((520, 384, 640, 0), (33, 96, 64, 2)),           # splits, then a single-step K
 ])
 def test_noalloc_matches_workspace_entry(gpu, oracle, first, second):
@@ -67,7 +67,7 @@ def test_noalloc_matches_workspace_entry(gpu, oracle, first, second):
     for i, (M, N, K, mode) in enumerate((first, second)):
         got, want, ref, nws = _run(lib, oracle, M, N, K, mode, 10 * i + 1)
         sizes.append(nws)
-        if (M, N, K) == (2048, 1280, 5120):  # the planner's 3-way split of 160 tiles of 128 x 128
+        if (M, N, K) == (2048, 1280, 5120):  # the planner's 3-way split of 80 tiles of 256 x 128
             assert nws == 3 * M * N * 4, f"2048x1280x5120 plans {nws} bytes of partials, not 3 planes"
         assert np.array_equal(got, want), f"call {i + 1}: noalloc differs from the workspace entry"
         assert_parity(got, ref, what=f"noalloc call {i + 1} vs oracle")
