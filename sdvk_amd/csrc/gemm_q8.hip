@@ -955,12 +955,12 @@ struct Plan {
 // Picks the tile and K split for a shape (rules from per-shape sweeps of every
 // tile build on MI355X over the SDXL shapes, timed interleaved): the 192x256
 // tile (8 waves, one workgroup per CU) where it yields a wave or more of
-// long-K tiles over more than 640 columns (256x128 where that fills more of a
-// single round) (at N = 640 the 128x128 tile is
-// faster: 8192x640x2560 61.6 vs 66.0 us); 128x128 (4 waves, two workgroups per
-// CU) for mid-size grids, as 8 waves of 32x64 when the grid has fewer tiles
-// than CUs and no K split (one workgroup per CU: two waves per SIMD instead
-// of one; 2048x1280x1280 20.7 vs 22.9 us, 2048x1280x5120 unsplit 75 vs 91);
+// long-K tiles over more than 640 columns (at N = 640 the 128x128 tile is
+// faster: 8192x640x2560 61.6 vs 66.0 us), or 256x128 where that fills more of
+// a single round; 128x128 (4 waves, two workgroups per CU) for mid-size
+// grids, as 8 waves of 32x64 when the grid has fewer tiles than CUs and no K
+// split (one workgroup per CU: two waves per SIMD instead of one;
+// 2048x1280x1280 17.6 vs 21.8 us, 2048x1280x5120 unsplit 60.5 vs 89.5);
 // 64x64 for the rest.
 // With a workspace (allow_split), long-K (>= 4096) 128x128 grids of fewer
 // tiles than CUs run as 256x128 tiles (8 waves) with K split into the most
