@@ -30,6 +30,24 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// The wave's sum in every lane, mostly by DPP: quad swaps, then the half-row
+// and row mirrors (lane i of 8 / 16 reads lane 7 - i / 15 - i) leave each row
+// of 16 with its sum; two cross-row exchanges finish. Four of the six steps
+// stay in the VALU instead of six LDS permutes of the xor butterfly.
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v = dpp_add<0xb1>(v);   // quad_perm [1, 0, 3, 2]
+    v = dpp_add<0x4e>(v);   // quad_perm [2, 3, 0, 1]
+    v = dpp_add<0x141>(v);  // row_half_mirror
+    v = dpp_add<0x140>(v);  // row_mirror
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    return v;
+}
+
 // Stores four fp32 results as TO: fp32 as they are, fp16 rounded once (RNE)
 // each -- the value a GEMM staging an fp32 tensor would round them to. The
 // empty register constraint makes the fp32 values opaque, so the rounding to fp16 cannot fuse
@@ -47,8 +65,9 @@ __device__ __forceinline__ void store4(TO* p, floatx4 v) {
 }
 
 // One wave per row; 4 rows per 256-thread workgroup. d % 4 == 0, 16-byte aligned rows
-// (8-byte for fp16 output).
-template <typename TO>
+// (8-byte for fp16 output). NC float4 per lane (d <= 256 NC): the loops are
+// as long as the row, so the loads issue together without a branch per chunk.
+template <typename TO, int NC>
 __global__ __launch_bounds__(256) void layernorm_vec_kernel(const float* __restrict__ x, const float* __restrict__ gamma,
                                                             const float* __restrict__ beta, TO* __restrict__ y,
                                                             uint32_t rows, uint32_t d, float eps) {
@@ -58,18 +77,18 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(const float* __restr
     const uint32_t n4 = d / 4;
     const floatx4* xr = reinterpret_cast<const floatx4*>(x + static_cast<uint64_t>(row) * d);
     TO* yr = y + static_cast<uint64_t>(row) * d;
-    floatx4 c[kLnCache];
+    floatx4 c[NC];
     float s = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kLnCache; ++i) {
+    for (int i = 0; i < NC; ++i) {
         const uint32_t j = lane + 64 * i;
         c[i] = j < n4 ? xr[j] : floatx4{0, 0, 0, 0};
         s += (c[i][0] + c[i][1]) + (c[i][2] + c[i][3]);
     }
-    const float mean = wave_sum(s) / static_cast<float>(d);
+    const float mean = wave_sum_dpp(s) / static_cast<float>(d);
     float ss = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kLnCache; ++i) {
+    for (int i = 0; i < NC; ++i) {
         const uint32_t j = lane + 64 * i;
         if (j < n4) {
 #pragma unroll
@@ -79,10 +98,10 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(const float* __restr
             }
         }
     }
-    const float var = wave_sum(ss) / static_cast<float>(d);
+    const float var = wave_sum_dpp(ss) / static_cast<float>(d);
     const float inv = 1.0f / sqrtf(var + eps);
 #pragma unroll
-    for (int i = 0; i < kLnCache; ++i) {
+    for (int i = 0; i < NC; ++i) {
         const uint32_t j = lane + 64 * i;
         if (j < n4) {
             floatx4 v;
@@ -174,6 +193,19 @@ unsigned stride_grid(uint64_t items) {
     return static_cast<unsigned>(g < 2048 ? (g ? g : 1) : 2048);
 }
 
+// The vector LayerNorm with the fewest float4 per lane that hold a row of d.
+template <typename TO>
+void launch_layernorm_vec(const float* x, const float* gamma, const float* beta, TO* y, uint32_t rows, uint32_t d,
+                          float eps, hipStream_t s) {
+    const unsigned grid = ceil_div(rows, 4);
+    const uint32_t nc = ceil_div(d / 4, 64u);
+    if (nc <= 2) layernorm_vec_kernel<TO, 2><<<grid, 256, 0, s>>>(x, gamma, beta, y, rows, d, eps);
+    else if (nc <= 3) layernorm_vec_kernel<TO, 3><<<grid, 256, 0, s>>>(x, gamma, beta, y, rows, d, eps);
+    else if (nc <= 5) layernorm_vec_kernel<TO, 5><<<grid, 256, 0, s>>>(x, gamma, beta, y, rows, d, eps);
+    else if (nc <= 8) layernorm_vec_kernel<TO, 8><<<grid, 256, 0, s>>>(x, gamma, beta, y, rows, d, eps);
+    else layernorm_vec_kernel<TO, kLnCache><<<grid, 256, 0, s>>>(x, gamma, beta, y, rows, d, eps);
+}
+
 }  // namespace
 }  // namespace mi
 
@@ -191,9 +223,8 @@ extern "C" int mi_layernorm(const float* x, const float* gamma, const float* bet
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool vec = d % 4 == 0 && d <= 64u * 4 * kLnCache && aligned(x, 16) && aligned(y, 16) &&
                      (!gamma || (aligned(gamma, 16) && aligned(beta, 16)));
-    const unsigned grid = ceil_div(rows, 4);
-    if (vec) layernorm_vec_kernel<float><<<grid, 256, 0, s>>>(x, gamma, beta, y, rows, d, eps);
-    else layernorm_kernel<<<grid, 256, 0, s>>>(x, gamma, beta, y, rows, d, eps);
+    if (vec) launch_layernorm_vec<float>(x, gamma, beta, y, rows, d, eps, s);
+    else layernorm_kernel<<<ceil_div(rows, 4), 256, 0, s>>>(x, gamma, beta, y, rows, d, eps);
     return check_launch(fn);
 }
 
@@ -227,8 +258,8 @@ extern "C" int mi_layernorm_f16(const float* x, const float* gamma, const float*
         return fail(MI_ERR_ALIGNMENT, "%s: x, gamma, beta 16-byte and y 8-byte aligned", fn);
     if (overlaps(x, static_cast<uint64_t>(rows) * d * 4, y, static_cast<uint64_t>(rows) * d * 2))
         return fail(MI_ERR_ALIASING, "%s: y overlaps x", fn);
-    layernorm_vec_kernel<_Float16><<<ceil_div(rows, 4), 256, 0, static_cast<hipStream_t>(stream)>>>(
-        x, gamma, beta, static_cast<_Float16*>(y), rows, d, eps);
+    launch_layernorm_vec<_Float16>(x, gamma, beta, static_cast<_Float16*>(y), rows, d, eps,
+                                   static_cast<hipStream_t>(stream));
     return check_launch(fn);
 }
 

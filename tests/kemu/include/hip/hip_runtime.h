@@ -271,15 +271,24 @@ struct DppCtl {
     int ctrl;
 };
 // DPP quad_perm (ctrl 0x00..0xFF): lane l reads lane 4 (l / 4) + sel(l % 4),
-// sel(j) = bits [2j, 2j + 2) of ctrl. Other DPP controls are not emulated.
+// sel(j) = bits [2j, 2j + 2) of ctrl; row_mirror (0x140): lane l reads lane
+// 15 - l within its row of 16; row_half_mirror (0x141): lane 7 - l within its
+// half-row of 8. Other DPP controls are not emulated.
 template <class T>
 inline void dpp_fn(const unsigned char (*ins)[256], unsigned char (*outs)[256], const void* ctx) {
     const int ctrl = static_cast<const DppCtl*>(ctx)->ctrl;
-    for (int l = 0; l < 64; ++l) std::memcpy(outs[l], ins[(l & ~3) + ((ctrl >> (2 * (l & 3))) & 3)], sizeof(T));
+    for (int l = 0; l < 64; ++l) {
+        int src;
+        if (ctrl == 0x140) src = (l & ~15) + (15 - (l & 15));
+        else if (ctrl == 0x141) src = (l & ~7) + (7 - (l & 7));
+        else src = (l & ~3) + ((ctrl >> (2 * (l & 3))) & 3);
+        std::memcpy(outs[l], ins[src], sizeof(T));
+    }
 }
 template <class T>
 inline T mov_dpp(T x, int ctrl, int row_mask, int bank_mask, bool) {
-    if (ctrl < 0 || ctrl > 0xff || row_mask != 0xf || bank_mask != 0xf) die("mov_dpp: only full-mask quad_perm is emulated");
+    if (ctrl < 0 || (ctrl > 0xff && ctrl != 0x140 && ctrl != 0x141) || row_mask != 0xf || bank_mask != 0xf)
+        die("mov_dpp: only full-mask quad_perm, row_mirror and row_half_mirror are emulated");
     const DppCtl c{ctrl};
     T y;
     wave_op("mov_dpp", &x, sizeof x, &y, sizeof y, dpp_fn<T>, &c);
