@@ -55,24 +55,78 @@ def _is_load(ins: str) -> bool:
     return ins.startswith(("buffer_load", "global_load", "scratch_load", "flat_load"))
 
 
+@dataclass
+class _Block:
+    label: str
+    header: bool
+    ins: list
+    succ: list
+
+
+def _blocks(body: list) -> list:
+    """Basic blocks of one function's assembly: a block starts at a label or
+    after a branch; its successors are the branch target and, unless it ends
+    in an unconditional branch or s_endpgm, the next block."""
+    out = [_Block("", False, [], [])]
+    for line in body:
+        x = line.strip()
+        lab = re.match(r"^(\.LBB\w+):", x)
+        if lab:
+            out.append(_Block(lab.group(1), "Loop Header" in line, [], []))
+            continue
+        if not x or x.startswith((";", ".")):
+            continue
+        out[-1].ins.append(x)
+        if re.match(r"s_c?branch", x) or x.startswith("s_endpgm"):
+            out.append(_Block("", False, [], []))
+    index = {b.label: i for i, b in enumerate(out) if b.label}
+    for i, b in enumerate(out):
+        last = b.ins[-1] if b.ins else ""
+        br = re.match(r"s_(c?)branch\w*\s+(\.LBB\w+)", last)
+        if br and br.group(2) in index:
+            b.succ.append(index[br.group(2)])
+        if not (last.startswith("s_endpgm") or (br and not br.group(1))) and i + 1 < len(out):
+            b.succ.append(i + 1)
+    return out
+
+
+def _natural_loop(blocks: list, h: int) -> set:
+    reach, todo = set(), [h]
+    while todo:  # blocks reachable from the header
+        b = todo.pop()
+        for t in blocks[b].succ:
+            if t not in reach:
+                reach.add(t)
+                todo.append(t)
+    loop = {h}
+    todo = [b for b in reach if h in blocks[b].succ]
+    while todo:  # back from the latches to the header
+        b = todo.pop()
+        if b in loop:
+            continue
+        loop.add(b)
+        todo += [p for p in range(len(blocks)) if b in blocks[p].succ and p in reach and p not in loop]
+    return loop
+
+
 def loops(asm_path: Path) -> list[Loop]:
-    """Every loop (LLVM's 'Loop Header' blocks, up to the branch back) that issues MFMAs."""
+    """Every loop (LLVM's 'Loop Header' blocks and the blocks of their natural
+    loop) that issues MFMAs."""
     text = asm_path.read_text()
     found = []
     for part in re.split(r"\n(?=_Z\S+:\s*; @)", text):
         m = re.match(r"(_Z\S+):", part)
         if not m:
             continue
-        body = part.split(".Lfunc_end")[0].split("\n")
-        for i, line in enumerate(body):
-            if "Loop Header" not in line:
+        blocks = _blocks(part.split(".Lfunc_end")[0].split("\n"))
+        for h, blk in enumerate(blocks):
+            if not blk.header:
                 continue
-            label = line.split(":")[0]
-            j = i + 1
-            while j < len(body) and not (re.match(r"\s*s_c?branch", body[j]) and body[j].strip().endswith(label)):
-                j += 1
-            ins = [x.strip() for x in body[i + 1:j]]
-            ins = [x for x in ins if x and not x.startswith((";", "."))]
+            label = blk.label
+            # the natural loop: the header and every block that reaches one of
+            # its back edges without passing the header (the compiler may place
+            # the latch blocks above the header), in layout order
+            ins = [x for b in sorted(_natural_loop(blocks, h)) for x in blocks[b].ins]
             nm = sum("v_mfma" in x for x in ins)
             if nm == 0:
                 continue
