@@ -981,7 +981,11 @@ void launch_cfg(const GemmArgs& a0, uint32_t batch, uint32_t splits, float* ws, 
 template <int WK, int EPI = kEpiPlain, bool AH = false>
 void launch(int cfg, const GemmArgs& a, uint32_t batch, uint32_t splits, float* ws, hipStream_t s) {
     switch (cfg) {
-        case kC256x128: launch_cfg<256, 128, 4, 2, 2, WK, false, 2, EPI, true, AH>(a, batch, splits, ws, s); break;
+        case kC256x128:
+            // ping-pong K loop (PP): 2048x3840x1280 34.3 vs 36.0 us, 2048x1280x5120 in
+            // three K splits 50.7 vs 53.6 (one-barrier loop; fp16 A 3-4% faster)
+            launch_cfg<256, 128, 4, 2, 2, WK, false, 2, EPI, true, AH, true>(a, batch, splits, ws, s);
+            break;
         case kC128x128:
             // one register set: the loop then issues most of a step's MFMAs before
             // converting the next step's loads (8192x640x2560 58 vs 68 us with two

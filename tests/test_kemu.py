@@ -266,7 +266,15 @@ PLANTED = {
     "missing_barrier": ("gemm_q8.hip",
                         "            __syncthreads();\n            load_step(phys(min(j + 3, last)), S1{});",
                         "            load_step(phys(min(j + 3, last)), S1{});",
-                        dict(case="gemm_nt", M=300, N=200, K=256, cfg="0")),
+                        dict(case="gemm_nt", M=300, N=200, K=256, cfg="6")),
+    # ping-pong loop (builds 0 and 5): a wave group reads the stage it has just written before the
+    # barrier that orders every wave's writes (the barrier count kept)
+    "missing_barrier_pingpong": ("gemm_q8.hip",
+                                 "                mem(min(j + 2, last), S0{}, S1{});\n                __syncthreads();\n"
+                                 "                comp(S1{});\n                __syncthreads();\n",
+                                 "                mem(min(j + 2, last), S0{}, S1{});\n"
+                                 "                comp(S1{});\n                __syncthreads();\n                __syncthreads();\n",
+                                 dict(case="gemm_nt", M=300, N=300, K=640, cfg="5")),
     # staged epilogue without the wave barrier between its LDS writes and reads
     "missing_wave_barrier": ("gemm_q8.hip", "__builtin_amdgcn_wave_barrier();", "",
                              dict(case="gemm_nt", M=77, N=96, K=64)),
