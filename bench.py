@@ -513,13 +513,15 @@ def extras(rng, hip, ops, stream, reps, emit=None):
         return res
 
     def attn_candidates():
-        """{"shapes": [tag], "us": {"default" | "nw2" | "nw4" | "nosplit": [us per shape]}}: the fp16
-        attention kernel's 2- and 4-wave workgroups (attn_nw override) and the default plan without its key
-        split (attn_split "0") on every attention shape of the step, timed in two passes (forward, then
-        reverse order) and kept at the per-shape minimum."""
+        """{"shapes": [tag], "us": {"default" | "nw2" | "nw4" | "simd2" | "simd3" | "nosplit": [us per
+        shape]}}: the fp16 attention kernel's 2- and 4-wave workgroups (attn_nw override), its interleaved
+        and burst builds (2 or 3 waves per SIMD, attn_simd_waves) and the default plan without its key split
+        (attn_split "0") on every attention shape of the step, timed in two passes (forward, then reverse
+        order) and kept at the per-shape minimum."""
         cases = [AttnCase(t, B, H, Tq, Tk, m, rng, hip, ops) for t, B, H, Tq, Tk, m in ATTN_SHAPES]
         res = {"shapes": [c.tag for c in cases], "us": {}}
         variants = [("default", {}), ("nw2", {"attn_nw": "2"}), ("nw4", {"attn_nw": "4"}),
+                    ("simd2", {"attn_simd_waves": "2"}), ("simd3", {"attn_simd_waves": "3"}),
                     ("nosplit", {"attn_split": "0"})]
         for key, over in variants + variants[::-1]:
             with ops.tuning(**over):

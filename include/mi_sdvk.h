@@ -78,6 +78,8 @@ int mi_version(void);
  *                       mi_fused_attention_ws ("0": never split)
  *   "attn_direct_store" "1": attention outputs stored from the MFMA layout
  *                       instead of whole rows through LDS
+ *   "attn_simd_waves"   "2" | "3": fp16 attention build of 2 or 3 waves per
+ *                       SIMD (fp16-precision, non-causal launches)
  * MI_ERR_INVALID_ARG for an unknown name or a malformed value. Not
  * synchronised with calls in flight on other threads.                      */
 int mi_tuning_set(const char* name, const char* value);

@@ -549,8 +549,11 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnArgs a) {
 // 2.4%): kResidNone; kResidDiagonal, a causal launch's diagonal tiles;
 // kResidAll, every tile (MI_ATTN_PREC_SPLIT).
 constexpr int kResidNone = 0, kResidDiagonal = 1, kResidAll = 2;
-template <typename TO, int NW, int RESID>
-__global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t qtiles) {
+// BURST: the burst-ordered loop (below) built for three waves per SIMD
+// (168 registers): a third workgroup per CU for grids of more than two per CU.
+template <typename TO, int NW, int RESID, int BURST = 0>
+__global__ __launch_bounds__(64 * NW, BURST ? 3 : 1) void attn_f16_kernel(AttnArgs a, uint32_t qtiles) {
+    static_assert(!BURST || (RESID == kResidNone && NW == 4), "burst build: 4 waves, one PV product per tile");
     constexpr int BQ = 32 * NW;
     constexpr int DMA_IT = 8 / NW;  // 1 KB (8-row) DMA pieces per wave per tile, for K and for V
     __shared__ __attribute__((aligned(16))) _Float16 Ks[2][kBKV * 64];
@@ -823,6 +826,10 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
         // splits the exp2 work between the two MFMA phases
         half8 pf[2][2];
         exp_half(s0, pf, 0);
+        if constexpr (BURST != 0) {  // the burst loop takes tile t0's whole P
+            exp_half(s0, pf, 1);
+            settle(s0, pf, tile_sum(pf));
+        }
         __syncthreads();  // every wave has read K tile t0 before it is overwritten
 
         // One pipelined iteration; boundary tiles (key padding, Tk end, causal
@@ -882,14 +889,58 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(AttnArgs a, uint32_t 
             dma_wait();
             __syncthreads();
         };
+        // BURST: iteration j issues its 16 MFMAs back to back (S of tile j+1,
+        // then PV of tile j, whose P the previous iteration completed), then
+        // the whole softmax of tile j+1 on the VALU, so one wave's MFMAs can
+        // run under another wave's vector work; the loop keeps fewer values
+        // live (168 registers: three waves per SIMD). Same operations in the
+        // same order per tile as the interleaved loop: the same bits.
+        auto step_burst = [&](uint32_t j, auto masked) {
+            constexpr bool kMasked = decltype(masked)::value;
+            const uint32_t kv1 = (j + 1) * kBKV;
+            const bool more = j + 2 < ntiles;
+            read_k((j + 1) & 1);
+            read_v(j & 1);
+            __builtin_amdgcn_sched_barrier(0);
+            if (more) dma_k(kv1 + kBKV, j & 1);
+            dma_v(kv1, (j + 1) & 1);
+            __builtin_amdgcn_sched_barrier(0);
+            floatx16 s1[2];
+            qk(s1);
+            if constexpr (RESID == kResidAll) {
+                pv_residual(s0, pf);
+            } else if constexpr (RESID == kResidDiagonal) {
+                if (j * kBKV >= kfull) pv_residual(s0, pf);
+            }
+            pv(pf);
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (kMasked) mask(s1, kv1);
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) s1[t][r] = __builtin_fmaf(s1[t][r], a.c, -m);
+            exp_pack(s1, pf);
+            settle(s1, pf, tile_sum(pf));
+#pragma unroll
+            for (int t = 0; t < 2; ++t) s0[t] = s1[t];
+            dma_wait();
+            __syncthreads();
+        };
         for (uint32_t j = t0; j + 1 < ntiles; ++j) {
-            if ((j + 1) * kBKV >= kfull) step(j, std::true_type{});
-            else step(j, std::false_type{});
+            if constexpr (BURST != 0) {
+                if ((j + 1) * kBKV >= kfull) step_burst(j, std::true_type{});
+                else step_burst(j, std::false_type{});
+            } else {
+                if ((j + 1) * kBKV >= kfull) step(j, std::true_type{});
+                else step(j, std::false_type{});
+            }
         }
         // last tile
         read_v((ntiles - 1) & 1);
-        exp_half(s0, pf, 1);
-        settle(s0, pf, tile_sum(pf));
+        if constexpr (BURST == 0) {
+            exp_half(s0, pf, 1);
+            settle(s0, pf, tile_sum(pf));
+        }
         if constexpr (RESID == kResidAll) {
             pv_residual(s0, pf);
         } else if constexpr (RESID == kResidDiagonal) {
@@ -1075,14 +1126,31 @@ SplitPlan plan_split(const AttnArgs& a, uint32_t batch) {
 
 uint64_t split_bytes(const SplitPlan& p) { return static_cast<uint64_t>(p.rest) * p.pieces * kPartFloats * 4; }
 
+// The burst build (three 4-wave workgroups per CU) for fp16-precision,
+// non-causal launches whose grid holds more than two workgroups per CU; the
+// interleaved build (two per CU) otherwise. Measured on MI355X (graph-timed,
+// interleaved runs, us, interleaved / burst): 2 x 10 x 4096^2 with its key
+// split 102.5 / 100.4, cross 2 x 10 x 4096 x 77 9.59 / 7.62; with at most two
+// workgroups per CU the burst loop has no second wave to overlap with
+// (2 x 20 x 1024^2 21.1 / 22.4). mi_tuning_set("attn_simd_waves", "2" | "3")
+// pins one (fp16-precision non-causal launches only).
+bool use_burst(const AttnArgs& a, uint64_t grid) {
+    if (a.precise || a.causal) return false;
+    const int forced = tuning().attn_simd_waves.load(std::memory_order_relaxed);
+    if (forced == 2 || forced == 3) return forced == 3;
+    return grid > 2ull * cu_count();
+}
+
 template <typename TO>
 void launch_f16(const AttnArgs& a, uint32_t batch, hipStream_t s) {
     const uint32_t q4 = ceil_div(a.Tq, 128u), q2 = ceil_div(a.Tq, 64u);
     const uint64_t groups = static_cast<uint64_t>(a.heads) * batch;
     if (a.pieces > 1) {  // a key-split plan (4-wave workgroups)
         const uint32_t rest = static_cast<uint32_t>(q4 * groups - a.nfull);
-        if (a.precise) attn_f16_kernel<TO, 4, kResidAll><<<a.nfull + rest * a.pieces, 256, 0, s>>>(a, q4);
-        else attn_f16_kernel<TO, 4, kResidNone><<<a.nfull + rest * a.pieces, 256, 0, s>>>(a, q4);
+        const unsigned grid = a.nfull + rest * a.pieces;
+        if (a.precise) attn_f16_kernel<TO, 4, kResidAll><<<grid, 256, 0, s>>>(a, q4);
+        else if (use_burst(a, grid)) attn_f16_kernel<TO, 4, kResidNone, 1><<<grid, 256, 0, s>>>(a, q4);
+        else attn_f16_kernel<TO, 4, kResidNone><<<grid, 256, 0, s>>>(a, q4);
         attn_merge_kernel<TO><<<rest * 4, 256, 0, s>>>(a, q4);
         return;
     }
@@ -1095,7 +1163,8 @@ void launch_f16(const AttnArgs& a, uint32_t batch, hipStream_t s) {
         if (nw4) attn_f16_kernel<TO, 4, kResidDiagonal><<<g4, 256, 0, s>>>(a, q4);
         else attn_f16_kernel<TO, 2, kResidDiagonal><<<g2, 128, 0, s>>>(a, q2);
     } else {
-        if (nw4) attn_f16_kernel<TO, 4, kResidNone><<<g4, 256, 0, s>>>(a, q4);
+        if (nw4 && use_burst(a, g4)) attn_f16_kernel<TO, 4, kResidNone, 1><<<g4, 256, 0, s>>>(a, q4);
+        else if (nw4) attn_f16_kernel<TO, 4, kResidNone><<<g4, 256, 0, s>>>(a, q4);
         else attn_f16_kernel<TO, 2, kResidNone><<<g2, 128, 0, s>>>(a, q2);
     }
 }

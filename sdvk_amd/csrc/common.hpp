@@ -41,6 +41,7 @@ struct Tuning {
     std::atomic<int> attn_split_rest{-1};   // key split: rest blocks (0 = never split), or -1
     std::atomic<int> attn_split_pieces{2};  // key split: pieces per rest block
     std::atomic<int> attn_direct_store{0};  // 1: attention outputs stored from the MFMA layout
+    std::atomic<int> attn_simd_waves{0};    // fp16 attention build: 2 or 3 waves per SIMD, or 0
 };
 Tuning& tuning();
 

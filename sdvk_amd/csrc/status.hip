@@ -122,6 +122,12 @@ extern "C" int mi_tuning_set(const char* name, const char* value) {
         t.attn_direct_store.store(!clear && value[0] == '1' ? 1 : 0);
         return MI_OK;
     }
+    if (std::strcmp(name, "attn_simd_waves") == 0) {
+        if (!clear && std::strcmp(value, "2") != 0 && std::strcmp(value, "3") != 0)
+            return fail(MI_ERR_INVALID_ARG, "mi_tuning_set: attn_simd_waves \"%s\" (want 2 or 3)", value);
+        t.attn_simd_waves.store(clear ? 0 : std::atoi(value));
+        return MI_OK;
+    }
     return fail(MI_ERR_INVALID_ARG, "mi_tuning_set: unknown name \"%s\"", name);
 }
 
@@ -135,6 +141,7 @@ extern "C" void mi_tuning_reset(void) {
     t.attn_split_rest.store(-1);
     t.attn_split_pieces.store(2);
     t.attn_direct_store.store(0);
+    t.attn_simd_waves.store(0);
 }
 
 extern "C" const char* mi_status_string(int status) {

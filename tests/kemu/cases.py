@@ -203,7 +203,7 @@ def gemm_nn(E, *, M, N, K, mode=0, batch=1, lda=0, ldb=0, ldc=0, sA=0, sB=0, sC=
 
 def attention(E, *, batch=1, Tq, Tk, C, heads, causal=False, f16_in=False, f16_out=False, kv_len=None, seed=1,
               front=False, order=0, tol=2e-3, nw=None, outliers=None, direct_store=False, split=None,
-              precise=False, precision=None):
+              precise=False, precision=None, simd_waves=None):
     """mi_fused_attention_ex (contiguous [batch, T, C]) against the oracle;
     split "<rest>:<pieces>": through mi_fused_attention_ws with that key-split
     plan forced (the attn_split override) and the workspace the library asks
@@ -214,9 +214,11 @@ def attention(E, *, batch=1, Tq, Tk, C, heads, causal=False, f16_in=False, f16_o
     (attn_direct_store) instead of whole rows through LDS; precision: the
     mi_attn_args field, by default MI_ATTN_PREC_FP16 (one fp16 P product);
     precise: MI_ATTN_PREC_SPLIT (P's fp16 residual as a second PV product on
-    every tile)."""
+    every tile); simd_waves "2" | "3": the interleaved or the burst build of
+    the fp16 kernel (attn_simd_waves)."""
     E.order(order)
     _tune("attn_nw", nw)
+    _tune("attn_simd_waves", simd_waves)
     _tune("attn_direct_store", "1" if direct_store else None)
     _tune("attn_split", split)
     if precision is None:
@@ -374,11 +376,13 @@ def gemm_nn_full(E, *, M, N, K, seed=1, order=0, tol=2e-3):
     return assert_parity(got[rows][sub], want[sub], tol=tol, what=f"gemm_nn full {kern} grid {grid}")
 
 
-def attention_full(E, *, batch, Tq, Tk, C, heads, masked=False, nw=None, seed=1, order=0, tol=2e-3):
+def attention_full(E, *, batch, Tq, Tk, C, heads, masked=False, nw=None, seed=1, order=0, tol=2e-3,
+                   simd_waves=None):
     """fp16 mi_fused_attention_ex at a full benchmark shape, sampled workgroups
     (the first and the last in the kernel's order)."""
     E.order(order)
     _tune("attn_nw", nw)
+    _tune("attn_simd_waves", simd_waves)
     _tune("attn_direct_store", None)
     q = ob.normal(seed, batch * Tq * C).astype(np.float16)
     k = ob.normal(seed + 1, batch * Tk * C).astype(np.float16)

@@ -203,14 +203,16 @@ def test_c_and_cpp_callers_link_and_run(tmp_path):
 def test_tuning_overrides_are_bounded():
     """mi_tuning_set accepts the documented ranges only: GEMM builds 0..6 with
     1..64 K splits, attention key-split plans of 1..64 pieces, 2 or 4 attention
-    waves, and rejects the rest."""
+    waves per workgroup, 2 or 3 per SIMD, and rejects the rest."""
     lib = _lib.load()
     try:
         for name, value in [(b"gemm_cfg", b"6"), (b"gemm_cfg", b"0:64"), (b"attn_split", b"2:8"),
-                            (b"attn_split", b"0"), (b"attn_nw", b"2")]:
+                            (b"attn_split", b"0"), (b"attn_nw", b"2"), (b"attn_simd_waves", b"3"),
+                            (b"attn_simd_waves", b"2")]:
             assert lib.mi_tuning_set(name, value) == 0, (name, value)
         for name, value in [(b"gemm_cfg", b"7"), (b"gemm_cfg", b"1:65"), (b"attn_split", b"2:65"),
-                            (b"attn_split", b"2:0"), (b"attn_nw", b"3"), (b"no_such_knob", b"1")]:
+                            (b"attn_split", b"2:0"), (b"attn_nw", b"3"), (b"attn_simd_waves", b"4"),
+                            (b"no_such_knob", b"1")]:
             assert lib.mi_tuning_set(name, value) != 0, (name, value)
     finally:
         lib.mi_tuning_reset()

@@ -186,7 +186,7 @@ def test_bench_line_on_stand_in_device(fake_device, monkeypatch, capsys, launch)
         assert part in ex and "error" not in ex[part], (part, ex.get(part))
     assert set(ex["gemm_candidates"]["us"]) == set(bench.GEMM_CANDIDATES) | {"default"}
     assert len(ex["gemm_candidates"]["default_us"]) == len(bench.GEMM_SHAPES) + 1
-    assert set(ex["attention_candidates"]["us"]) == {"default", "nw2", "nw4", "nosplit"}
+    assert set(ex["attention_candidates"]["us"]) == {"default", "nw2", "nw4", "simd2", "simd3", "nosplit"}
     assert len(ex["gemm_candidates"]["best"]) == len(bench.GEMM_SHAPES) + 1
     assert ex["block_stack_plain"]["variant"] == {"cached_kv": False, "fused_epilogues": False, "joint_qkv": False,
                                                   "fp16_activations": False, "fp16_attention": False}

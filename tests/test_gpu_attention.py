@@ -189,6 +189,48 @@ def test_two_and_four_wave_workgroups(gpu, oracle, tune, nw, B, Tq, Tk, C, heads
             assert np.all(np.abs(g - w) <= bound), f"nw={nw}: fp16 output beyond parity + storage rounding"
 
 
+@pytest.mark.parametrize("B,Tq,Tk,C,heads,kv_len,ws,odt", [
+    (2, 4096, 77, 640, 10, [77, 40], False, MI_F16),
+    (2, 4096, 4096, 640, 10, None, True, MI_F16),
+    (2, 300, 1000, 128, 2, None, False, MI_F32),
+    (1, 200, 130, 80, 2, [1], False, MI_F16),
+    (2, 1024, 1024, 1280, 20, None, False, MI_F16),
+])
+def test_burst_build_equals_interleaved_build(gpu, oracle, tune, B, Tq, Tk, C, heads, kv_len, ws, odt):
+    """The fp16 kernel's burst build (three waves per SIMD, the rule's choice
+    for grids of more than two workgroups per CU) computes the interleaved
+    build's bits: the same operations in the same order per tile. Pinned with
+    attn_simd_waves on key padding, partial tiles, hd = 40, the key-split
+    workspace entry and both output types; the interleaved result is checked
+    against the oracle on sampled rows."""
+    print(f"[case] burst vs interleaved B={B} Tq={Tq} Tk={Tk} C={C} H={heads} kv_len={kv_len} ws={ws}", flush=True)
+    q = oracle.normal(31, B * Tq * C).astype(np.float16)
+    k = oracle.normal(32, B * Tk * C).astype(np.float16)
+    v = oracle.normal(33, B * Tk * C).astype(np.float16)
+    kl = np.asarray(kv_len, dtype=np.int32) if kv_len is not None else None
+    dq, dk, dv = (DeviceBuffer.from_array(x) for x in (q, k, v))
+    dl = DeviceBuffer.from_array(kl) if kl is not None else None
+    kw = dict(batch=B, Tq=Tq, Tk=Tk, C=C, heads=heads, in_dtype=MI_F16, out_dtype=odt, kv_len=dl,
+              precision=MI_ATTN_PREC_FP16)
+    outs = []
+    for waves in ("2", "3"):
+        tune("attn_simd_waves", waves)
+        do = DeviceBuffer(B * Tq * C * (2 if odt == MI_F16 else 4))
+        n = ops.fused_attention_ws_bytes(**kw) if ws else 0
+        ops.fused_attention_ws(dq, dk, dv, do, DeviceBuffer(n) if n else None, **kw)
+        synchronize()
+        outs.append(do.download(np.float16 if odt == MI_F16 else np.float32, B * Tq * C))
+    assert np.array_equal(outs[0].view(np.uint8), outs[1].view(np.uint8)), "burst build differs from interleaved"
+    rows = _sample_rows(Tq, 24, 7) if Tq > 512 else None
+    want = oracle.fused_attention_ex(q, k, v, batch=B, Tq=Tq, Tk=Tk, C=C, heads=heads, in_dtype=1, kv_len=kl,
+                                     rows=rows, threads=oracle.max_threads())
+    g = outs[0].reshape(B, Tq, C).astype(np.float64)
+    g = g[:, rows] if rows is not None else g
+    w = want.reshape(g.shape)
+    bound = REL_RMS_TOL * rms(w) + (fp16_half_ulp(w) if odt == MI_F16 else 0.0)
+    assert np.all(np.abs(g - w) <= bound), "interleaved build beyond parity"
+
+
 @pytest.mark.parametrize("B,H,T,Tk,causal,ws,prec", [(1, 20, 1024, 1024, False, False, MI_ATTN_PREC_AUTO),
                                                       (1, 20, 1024, 1024, False, False, MI_ATTN_PREC_SPLIT),
                                                       (2, 10, 4096, 4096, False, True, MI_ATTN_PREC_SPLIT),

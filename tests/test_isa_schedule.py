@@ -65,14 +65,19 @@ def test_k_loops_keep_loads_ahead_of_their_waits(asm, src):
 
 # Kernels that may keep values in scratch around (never inside) their K loop,
 # and how many bytes per lane: the 8-wave 256x256 LDS build at its 256-register
-# limit (epilogue indices across the loop).
-SCRATCH_ALLOWED = {"gemm_q8_kernelILi256ELi256ELi4ELi2E": 16}
+# limit (epilogue indices across the loop); the burst attention build at its
+# 168-register limit (three waves per SIMD; prologue values across the loop).
+SCRATCH_ALLOWED = {"gemm_q8_kernelILi256ELi256ELi4ELi2E": 16, "attn_f16_kernelIDF16_Li4ELi0ELi1E": 24,
+                   "attn_f16_kernelIfLi4ELi0ELi1E": 24}
+# Builds that must hold three waves per SIMD (their purpose).
+THREE_WAVES = ("attn_f16_kernelIDF16_Li4ELi0ELi1E", "attn_f16_kernelIfLi4ELi0ELi1E")
 
 
 @pytest.mark.parametrize("src", list(CASES))
 def test_register_budgets(asm, src):
-    """Every 8-wave (512-thread) build fits two waves per SIMD, every kernel's
-    LDS fits the CU, and scratch appears only where listed, within its budget."""
+    """Every 8-wave (512-thread) build fits two waves per SIMD, the burst
+    attention build three, every kernel's LDS fits the CU, and scratch appears
+    only where listed, within its budget."""
     res = asm[("resources", src)]
     assert res, f"no kernels in {src}"
     bad = []
@@ -84,5 +89,7 @@ def test_register_budgets(asm, src):
             bad.append(f"{r.kernel}: {r.lds} B of LDS")
         if r.max_threads == 512 and r.waves_per_simd < 2:
             bad.append(f"{r.kernel}: {r.vgpr} registers, under two waves per SIMD")
+        if any(k in r.kernel for k in THREE_WAVES) and r.waves_per_simd < 3:
+            bad.append(f"{r.kernel}: {r.vgpr} registers, under three waves per SIMD")
     print(f"{src}: {len(res)} kernels checked")
     assert not bad, "\n".join(bad)

@@ -133,6 +133,13 @@ FAMILIES = {
         dict(Tq=100, Tk=300, C=128, heads=2, f16_in=True, causal=True, nw=2, precise=True, tol=2e-4),
         dict(Tq=70, Tk=130, C=128, heads=2, causal=True, precise=True, tol=2e-4),
         dict(Tq=200, Tk=130, C=80, heads=2, f16_in=True, split="1:2", nw=4, precise=True, tol=2e-4),
+        # the burst build (three waves per SIMD, picked for grids of more than two workgroups per CU):
+        # key padding, partial query and key tiles, hd = 40, a key split, outlying keys, fp32 output
+        dict(batch=2, Tq=130, Tk=77, C=640, heads=10, f16_in=True, f16_out=True, kv_len=[77, 13], simd_waves="3"),
+        dict(batch=2, Tq=300, Tk=1000, C=128, heads=2, f16_in=True, f16_out=False, split="3:3", simd_waves="3"),
+        dict(Tq=200, Tk=130, C=80, heads=2, f16_in=True, f16_out=True, simd_waves="3"),
+        dict(Tq=64, Tk=192, C=128, heads=2, f16_in=True, nw=4, outliers=[5, 66, 134], simd_waves="3"),
+        dict(Tq=128, Tk=64, C=64, heads=1, f16_in=True, f16_out=True, simd_waves="3"),
     ],
     "block": [
         dict(B=1, T=33, C=64, H=1, Tc=5, Cc=96, F=160),
