@@ -1038,11 +1038,12 @@ struct Plan {
 // tile (8 waves, one workgroup per CU) where it yields a wave or more of
 // long-K tiles over more than 640 columns (at N = 640 the 128x128 tile is
 // faster: 8192x640x2560 61.6 vs 66.0 us), or 256x128 where that fills more of
-// a single round; 128x128 (4 waves, two workgroups per CU) for mid-size
-// grids, as 8 waves of 32x64 when the grid has fewer tiles than CUs and no K
-// split (one workgroup per CU: two waves per SIMD instead of one;
-// 2048x1280x1280 17.6 vs 21.8 us, 2048x1280x5120 unsplit 60.5 vs 89.5);
-// 64x64 for the rest.
+// a single round; among the grids of at least 160 128x128 tiles, 256x128 (8
+// waves, ping-pong) where it makes 160 tiles or more, else 128x128 (4 waves,
+// two workgroups per CU), as 8 waves of 32x64 when the grid has fewer tiles
+// than CUs and no K split (one workgroup per CU: two waves per SIMD instead
+// of one; 2048x1280x1280 17.6 vs 21.8 us, 2048x1280x5120 unsplit 60.5 vs
+// 89.5); 64x64 for the rest.
 // With a workspace (allow_split), long-K (>= 4096) 128x128 grids of fewer
 // tiles than CUs run as 256x128 tiles (8 waves) with K split into the most
 // parts (>= 1024 k each) that keep one round (2048x1280x5120: 80 tiles x 3 =
@@ -1071,7 +1072,12 @@ Plan choose(uint32_t M, uint32_t N, uint32_t K, uint32_t batch, bool allow_split
         p.cfg = t192 < kCUs && t256 > t192 && t256 <= kCUs ? kC256x128 : kC192x256;
     } else if (t128 >= 160) {
         p.cfg = kC128x128;
-        if (allow_split && t128 < kCUs && K >= 4096) {
+        if (t256 >= 160) {
+            // grids of at least 160 256x128 tiles: the 8-wave ping-pong build
+            // (8192x640x2560 48.4 vs 50.9 us, 8192x640x640 17.1 vs 17.8,
+            // 8192x5120x640 90.5 vs 91.7; with fp16 A 5-9% faster)
+            p.cfg = kC256x128;
+        } else if (allow_split && t128 < kCUs && K >= 4096) {
             p.cfg = kC256x128;
             p.splits = static_cast<uint32_t>(std::max<uint64_t>(2, std::min<uint64_t>(kCUs / t256, K / 1024)));
         } else if (t128 < kCUs) {

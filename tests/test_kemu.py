@@ -246,8 +246,8 @@ def test_kernels_on_emulator(emulator, family):
 # and each split keeps >= 4 steps of 64. fp16 attention: 4-wave workgroups of
 # 128 queries, 2-wave ones of 64 when Tq <= 64.
 ROUTING = [
-    ["gemm", [8192, 640, 640], [320, 1, 1], 256], ["gemm", [8192, 5120, 640], [2560, 1, 1], 256],
-    ["gemm", [8192, 640, 2560], [320, 1, 1], 256], ["gemm", [2048, 1280, 1280], [160, 1, 1], 512],
+    ["gemm", [8192, 640, 640], [160, 1, 1], 512], ["gemm", [8192, 5120, 640], [1280, 1, 1], 512],
+    ["gemm", [8192, 640, 2560], [160, 1, 1], 512], ["gemm", [2048, 1280, 1280], [160, 1, 1], 512],
     ["gemm", [2048, 10240, 1280], [440, 1, 1], 512], ["gemm", [2048, 1280, 5120], [160, 1, 1], 512],
     ["gemm_ws", [2048, 1280, 5120], [80, 3, 1], 512],
     ["gemm", [154, 640, 2048], [30, 1, 1], 256], ["gemm_ws", [154, 640, 2048], [30, 8, 1], 256],
