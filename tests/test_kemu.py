@@ -300,6 +300,12 @@ PLANTED = {
     "attn_dma_wait": ("attention.hip", "            dma_wait();\n            __syncthreads();\n        };",
                       "            __syncthreads();\n        };",
                       dict(case="attention", batch=2, Tq=130, Tk=200, C=128, heads=2, f16_in=True, f16_out=True)),
+    # the burst attention loop without its wait for the iteration's K / V DMA before the barrier
+    "attn_burst_dma_wait": ("attention.hip",
+                            "            for (int t = 0; t < 2; ++t) s0[t] = s1[t];\n            dma_wait();\n",
+                            "            for (int t = 0; t < 2; ++t) s0[t] = s1[t];\n",
+                            dict(case="attention", batch=2, Tq=130, Tk=200, C=128, heads=2, f16_in=True,
+                                 f16_out=True, simd_waves="3")),
     # attention: output rows read back from LDS without the wave barrier after the wave's writes
     "attn_store_wave_barrier": ("attention.hip", "    __builtin_amdgcn_wave_barrier();\n    constexpr int RPI",
                                 "    constexpr int RPI",
