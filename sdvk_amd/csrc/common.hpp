@@ -85,14 +85,18 @@ __device__ __forceinline__ float fp16_bits_to_f32(uint32_t h) {
 // t = 1 / (1 + p z), z >= 0, odd extension.
 // Contraction is off: every multiply and add rounds on its own, so the GELU
 // computes the same bits in every kernel it is inlined into (the GEGLU GEMM
-// epilogue and the separate GEGLU kernel agree exactly).
+// epilogue and the separate GEGLU kernel agree exactly). The reciprocal and
+// the exponential are the hardware's (v_rcp_f32, 1 ulp; v_exp_f32 on
+// -z^2 log2(e)): the shader's division and exp carry GLSL's relaxed precision
+// too (unary_fwd.comp:32-34), and the error they add here (~1e-7 of the
+// output, where exp(-z^2) matters) is far inside the approximation's own.
 __device__ __forceinline__ float gelu_erf(float v) {
 #pragma clang fp contract(off)
     const float xs = v * 0.70710678118654752440f;
     const float ax = fabsf(xs);
-    const float t = 1.0f / (1.0f + 0.3275911f * ax);
+    const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * ax);
     const float poly = ((((1.061405429f * t - 1.453152027f) * t + 1.421413741f) * t - 0.284496736f) * t + 0.254829592f) * t;
-    const float e = 1.0f - poly * expf(-ax * ax);
+    const float e = 1.0f - poly * __builtin_amdgcn_exp2f(-ax * ax * 1.44269504088896341f);
     const float erf = xs >= 0.0f ? e : -e;
     return 0.5f * v * (1.0f + erf);
 }

@@ -465,6 +465,7 @@ inline T __shfl_xor(T v, int mask, int width = 64) {
 #define __builtin_amdgcn_perm ::kemu::perm
 #define __builtin_amdgcn_alignbit ::kemu::alignbit
 #define __builtin_amdgcn_exp2f exp2f
+#define __builtin_amdgcn_rcpf(x) (1.0f / (x))
 #define __builtin_amdgcn_ds_read_tr16_b64_v4f16 ::kemu::ds_read_tr16_b64
 #define __builtin_amdgcn_permlane32_swap ::kemu::permlane32_swap
 #define __builtin_amdgcn_fdot2 ::kemu::fdot2
