@@ -65,8 +65,11 @@ __device__ __forceinline__ void store4(TO* p, floatx4 v) {
 }
 
 // One wave per row; 4 rows per 256-thread workgroup. d % 4 == 0, 16-byte aligned rows
-// (8-byte for fp16 output). NC float4 per lane (d <= 256 NC): the loops are
-// as long as the row, so the loads issue together without a branch per chunk.
+// (8-byte for fp16 output). NC float4 per lane (d <= 256 NC). Every load of the
+// row -- x, and gamma / beta -- issues at the start as buffer loads whose range
+// is the row (chunks past d read as zeros: no branch, no access), so a wave
+// waits out one memory round trip; gamma / beta loaded after the reductions,
+// chunk by chunk, had cost a round trip per chunk.
 template <typename TO, int NC>
 __global__ __launch_bounds__(256) void layernorm_vec_kernel(const float* __restrict__ x, const float* __restrict__ gamma,
                                                             const float* __restrict__ beta, TO* __restrict__ y,
@@ -75,16 +78,28 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(const float* __restr
     const int lane = threadIdx.x & 63;
     if (row >= rows) return;
     const uint32_t n4 = d / 4;
-    const floatx4* xr = reinterpret_cast<const floatx4*>(x + static_cast<uint64_t>(row) * d);
+    const int nbytes = static_cast<int>(d * 4);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(x + static_cast<uint64_t>(row) * d), 0, nbytes, 0x00020000);
     TO* yr = y + static_cast<uint64_t>(row) * d;
-    floatx4 c[NC];
+    floatx4 c[NC], g[NC], b[NC];
+#pragma unroll
+    for (int i = 0; i < NC; ++i)
+        c[i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rx, (lane + 64 * i) * 16, 0, 0));
+    if (gamma) {
+        const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(gamma), 0, nbytes,
+                                                                            0x00020000);
+        const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(beta), 0, nbytes,
+                                                                            0x00020000);
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            g[i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rg, (lane + 64 * i) * 16, 0, 0));
+            b[i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rb, (lane + 64 * i) * 16, 0, 0));
+        }
+    }
     float s = 0.0f;
 #pragma unroll
-    for (int i = 0; i < NC; ++i) {
-        const uint32_t j = lane + 64 * i;
-        c[i] = j < n4 ? xr[j] : floatx4{0, 0, 0, 0};
-        s += (c[i][0] + c[i][1]) + (c[i][2] + c[i][3]);
-    }
+    for (int i = 0; i < NC; ++i) s += (c[i][0] + c[i][1]) + (c[i][2] + c[i][3]);
     const float mean = wave_sum_dpp(s) / static_cast<float>(d);
     float ss = 0.0f;
 #pragma unroll
@@ -108,10 +123,8 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(const float* __restr
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] = (c[i][e] - mean) * inv;
             if (gamma) {
-                const floatx4 g = reinterpret_cast<const floatx4*>(gamma)[j];
-                const floatx4 b = reinterpret_cast<const floatx4*>(beta)[j];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = v[e] * g[e] + b[e];
+                for (int e = 0; e < 4; ++e) v[e] = v[e] * g[i][e] + b[i][e];
             }
             store4(yr + 4 * j, v);
         }
