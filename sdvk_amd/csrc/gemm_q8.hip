@@ -802,8 +802,10 @@ void launch_fill(float* C, const float* bias, uint32_t M, uint32_t N, uint32_t l
 //   OP 1: C = C + sum         (mode 1)
 //   OP 2: C = C + (sum + bias[n])   (mode 2, the residual epilogue)
 // VEC: 16-byte accesses over the flattened [M, N / 4] index (N % 4 == 0, C rows
-// 16-byte aligned); a capped grid strides over the tile.
-template <int OP, bool VEC>
+// 16-byte aligned); a capped grid strides over the tile. SP > 0: exactly SP
+// splits, every partial of a unit loaded before the first add (one memory
+// round trip instead of one per split; the same adds in the same order).
+template <int OP, bool VEC, int SP = 0>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* P, uint64_t plane, uint32_t splits, float* C,
                                                             const float* bias, uint32_t M, uint32_t N, uint32_t ldc,
                                                             uint64_t sC, uint32_t bvec) {
@@ -816,8 +818,18 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* P, uint
         for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x; i < total; i += stride) {
             const uint32_t m = static_cast<uint32_t>(i / N4), n = static_cast<uint32_t>(i % N4) * 4;
             const float* q = p + static_cast<uint64_t>(m) * N + n;
-            floatx4 v = *reinterpret_cast<const floatx4*>(q);
-            for (uint32_t sp = 1; sp < splits; ++sp) v += *reinterpret_cast<const floatx4*>(q + sp * plane);
+            floatx4 v;
+            if constexpr (SP > 0) {
+                floatx4 part[SP];
+#pragma unroll
+                for (int sp = 0; sp < SP; ++sp) part[sp] = *reinterpret_cast<const floatx4*>(q + sp * plane);
+                v = part[0];
+#pragma unroll
+                for (int sp = 1; sp < SP; ++sp) v += part[sp];
+            } else {
+                v = *reinterpret_cast<const floatx4*>(q);
+                for (uint32_t sp = 1; sp < splits; ++sp) v += *reinterpret_cast<const floatx4*>(q + sp * plane);
+            }
             floatx4 b = {0.0f, 0.0f, 0.0f, 0.0f};
             if (OP != 1 && bias)
                 b = bvec ? *reinterpret_cast<const floatx4*>(bias + n)
@@ -850,8 +862,18 @@ void launch_reduce_op(const float* P, uint64_t plane, uint32_t splits, float* C,
     const uint64_t units = static_cast<uint64_t>(M) * (vec ? N / 4 : N);
     const unsigned gx = static_cast<unsigned>(std::min<uint64_t>(std::max<uint64_t>(ceil_div(units, 256ull), 1), 1024));
     const uint32_t bvec = reinterpret_cast<uintptr_t>(bias) % 16 == 0 ? 1u : 0u;
-    if (vec) splitk_reduce_kernel<OP, true><<<dim3(gx, batch), 256, 0, s>>>(P, plane, splits, C, bias, M, N, ldc, sC, bvec);
-    else splitk_reduce_kernel<OP, false><<<dim3(gx, batch), 256, 0, s>>>(P, plane, splits, C, bias, M, N, ldc, sC, bvec);
+    const dim3 grid(gx, batch);
+    if (!vec) {
+        splitk_reduce_kernel<OP, false><<<grid, 256, 0, s>>>(P, plane, splits, C, bias, M, N, ldc, sC, bvec);
+        return;
+    }
+    switch (splits) {
+        case 2: splitk_reduce_kernel<OP, true, 2><<<grid, 256, 0, s>>>(P, plane, splits, C, bias, M, N, ldc, sC, bvec); break;
+        case 3: splitk_reduce_kernel<OP, true, 3><<<grid, 256, 0, s>>>(P, plane, splits, C, bias, M, N, ldc, sC, bvec); break;
+        case 4: splitk_reduce_kernel<OP, true, 4><<<grid, 256, 0, s>>>(P, plane, splits, C, bias, M, N, ldc, sC, bvec); break;
+        case 8: splitk_reduce_kernel<OP, true, 8><<<grid, 256, 0, s>>>(P, plane, splits, C, bias, M, N, ldc, sC, bvec); break;
+        default: splitk_reduce_kernel<OP, true><<<grid, 256, 0, s>>>(P, plane, splits, C, bias, M, N, ldc, sC, bvec); break;
+    }
 }
 
 }  // namespace
