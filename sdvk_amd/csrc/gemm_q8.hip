@@ -205,6 +205,30 @@ __device__ __forceinline__ void store_tiles(const GemmArgs& a, float* C, float* 
         }
         return;
     }
+    // The bias values of the lane's columns, loaded once before the tile loop
+    // (they depend on the tile's column block only): a load inside the loop
+    // waits out a memory round trip -- and every store issued before it -- per
+    // tile. GEGLU: value and gate biases of output columns nw + 16 fn + 4 (lane
+    // % 4) + e; 16-byte path: columns nw + 32 fn + 4 (lane % 8) + e.
+    float gbv[EPI == kEpiGeglu ? FN : 1][4], gbg[EPI == kEpiGeglu ? FN : 1][4];
+    floatx4 bias4[EPI == kEpiGeglu ? 1 : FN];
+    if constexpr (EPI == kEpiGeglu) {
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t j = min(nw + 16 * fn + (lane & 3) * 4 + e, a.F - 1);  // columns past F are never stored
+                gbv[fn][e] = a.bias ? a.bias[j] : 0.0f;
+                gbg[fn][e] = a.bias ? a.bias[a.F + j] : 0.0f;
+            }
+    } else {
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+            const uint32_t n = nw + 32 * fn + (lane & 7) * 4;
+            bias4[fn] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (use_bias && vec && vec_bias && n + 3 < a.N) bias4[fn] = *reinterpret_cast<const floatx4*>(a.bias + n);
+        }
+    }
     for (int b = 0; b < FM * FN; ++b) {
 #pragma unroll
         for (int fm = 0; fm < FM; ++fm)
@@ -233,12 +257,18 @@ __device__ __forceinline__ void store_tiles(const GemmArgs& a, float* C, float* 
                 if (m >= a.M) continue;
                 float* c = C + static_cast<uint64_t>(m) * a.ldc + n;
                 floatx4 o;
+                float bv[4], bg[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const uint32_t j = min(n + e, a.F - 1);  // columns past F are computed, never stored
-                    const float bv = a.bias ? a.bias[j] : 0.0f, bg = a.bias ? a.bias[a.F + j] : 0.0f;
-                    o[e] = (v[e] + bv) * gelu_erf(gt[e] + bg);
-                }
+                for (int fn = 0; fn < FN; ++fn)
+                    if (b % FN == fn) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            bv[e] = gbv[fn][e];
+                            bg[e] = gbg[fn][e];
+                        }
+                    }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] = (v[e] + bv[e]) * gelu_erf(gt[e] + bg[e]);
                 if (a.out_half) {
                     // the fp32 value, then one RNE rounding to fp16 (the value an
                     // fp32 G would give the next GEMM's A staging); the empty register
@@ -296,14 +326,18 @@ __device__ __forceinline__ void store_tiles(const GemmArgs& a, float* C, float* 
             }
             float* c = C + static_cast<uint64_t>(m) * a.ldc + n;
             if (vec && vec_bias && n + 3 < a.N) {
+                floatx4 bb = bias4[0];
+#pragma unroll
+                for (int fn = 1; fn < FN; ++fn)
+                    if (b % FN == fn) bb = bias4[fn];
                 if (EPI == kEpiResidual) {
                     // x + (acc + bias): the rounding of the separate GEMM + add
                     floatx4 o = v;
-                    if (use_bias) o += *reinterpret_cast<const floatx4*>(a.bias + n);
+                    if (use_bias) o += bb;
                     *reinterpret_cast<floatx4*>(c) = *reinterpret_cast<const floatx4*>(c) + o;
                 } else if (a.mode == 0) {
                     floatx4 o = v;
-                    if (use_bias) o += *reinterpret_cast<const floatx4*>(a.bias + n);
+                    if (use_bias) o += bb;
                     // C is written once and not re-read here: streaming stores keep
                     // it from displacing the operand working set in L2
                     __builtin_nontemporal_store(o, reinterpret_cast<floatx4*>(c));
