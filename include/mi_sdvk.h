@@ -79,7 +79,7 @@ int mi_version(void);
  *   "attn_direct_store" "1": attention outputs stored from the MFMA layout
  *                       instead of whole rows through LDS
  *   "attn_simd_waves"   "2" | "3": fp16 attention build of 2 or 3 waves per
- *                       SIMD (fp16-precision, non-causal launches)
+ *                       SIMD (fp16-precision, non-causal, 4-wave launches)
  * MI_ERR_INVALID_ARG for an unknown name or a malformed value. Not
  * synchronised with calls in flight on other threads.                      */
 int mi_tuning_set(const char* name, const char* value);

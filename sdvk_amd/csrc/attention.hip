@@ -907,12 +907,7 @@ __global__ __launch_bounds__(64 * NW, BURST ? 3 : 1) void attn_f16_kernel(AttnAr
             __builtin_amdgcn_sched_barrier(0);
             floatx16 s1[2];
             qk(s1);
-            if constexpr (RESID == kResidAll) {
-                pv_residual(s0, pf);
-            } else if constexpr (RESID == kResidDiagonal) {
-                if (j * kBKV >= kfull) pv_residual(s0, pf);
-            }
-            pv(pf);
+            pv(pf);  // (the burst build has one PV product per tile: RESID == kResidNone)
             __builtin_amdgcn_sched_barrier(0);
             if constexpr (kMasked) mask(s1, kv1);
 #pragma unroll
