@@ -102,6 +102,44 @@ def _attn_shapes(n, seed):
     return out
 
 
+@pytest.mark.parametrize("B,H,Tq,Tk,hd,causal,masked,split",
+                         [x for x in _attn_shapes(24, 977) if not x[5]][:10])
+def test_random_burst_attention(gpu, oracle, tune, B, H, Tq, Tk, hd, causal, masked, split):
+    """The burst build (attn_simd_waves "3", 4-wave workgroups, one fp16 P
+    product) on random non-causal shapes: within the bar of the oracle and bit
+    for bit the interleaved build's output (attn_simd_waves "2")."""
+    print(f"[case] random burst attention B={B} H={H} Tq={Tq} Tk={Tk} hd={hd} masked={masked} "
+          f"split={split or '-'}", flush=True)
+    C = H * hd
+    tune("attn_nw", "4")
+    if split:
+        tune("attn_split", split)
+    q = oracle.normal(Tq + 11, B * Tq * C).astype(np.float16)
+    k = oracle.normal(Tk + 12, B * Tk * C).astype(np.float16)
+    v = oracle.normal(Tk + 13, B * Tk * C).astype(np.float16)
+    kv_len = None
+    if masked:
+        kv_len = np.random.default_rng(Tk + 1).integers(0, Tk + 1, B).astype(np.int32)
+        kv_len[0] = max(int(kv_len[0]), 1)
+    want = oracle.fused_attention_ex(q, k, v, batch=B, Tq=Tq, Tk=Tk, C=C, heads=H, in_dtype=1, kv_len=kv_len,
+                                     threads=oracle.max_threads()).astype(np.float64)
+    dq, dk, dv = (DeviceBuffer.from_array(x) for x in (q, k, v))
+    dl = DeviceBuffer.from_array(kv_len) if kv_len is not None else None
+    kw = dict(batch=B, Tq=Tq, Tk=Tk, C=C, heads=H, in_dtype=MI_F16, out_dtype=MI_F32, kv_len=dl,
+              precision=MI_ATTN_PREC_FP16)
+    outs = []
+    for waves in ("2", "3"):
+        tune("attn_simd_waves", waves)
+        nws = ops.fused_attention_ws_bytes(**kw)
+        do = DeviceBuffer(B * Tq * C * 4)
+        ops.fused_attention_ws(dq, dk, dv, do, DeviceBuffer(nws) if nws else None, **kw)
+        synchronize()
+        outs.append(do.download(np.float32, B * Tq * C))
+    assert np.array_equal(outs[0], outs[1]), "burst build differs from the interleaved build"
+    assert_parity(outs[1].reshape(want.shape).astype(np.float64), want, what="random burst attention",
+                  label="[precision=fp16]")
+
+
 @pytest.mark.parametrize("B,H,Tq,Tk,hd,causal,masked,split", _attn_shapes(14, 4242))
 def test_random_attention(gpu, oracle, tune, B, H, Tq, Tk, hd, causal, masked, split):
     """fp16 in / fp16 and fp32 out through the workspace entry (a forced key
