@@ -1001,7 +1001,8 @@ __global__ __launch_bounds__(64 * NW, BURST ? 3 : 1) void attn_f16_kernel(AttnAr
 // workgroups per split query block; thread t of a workgroup takes query t / 8 of its 32 and the 8
 // columns 8 (t % 8) of the head, so a warp-wide access covers whole 256-byte partial rows and whole
 // output rows (one 16-byte store per thread for fp16 output when rows are 16-byte aligned).
-template <typename TO>
+// NP > 0: exactly NP pieces (the 2- and 4-piece plans), unrolled so that all loads issue together.
+template <typename TO, int NP = 0>
 __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, uint32_t qtiles) {
     const uint32_t rb = blockIdx.x / 4, blk = a.nfull + rb;
     const uint32_t qt = blk % qtiles, bh = blk / qtiles;
@@ -1013,17 +1014,41 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, uint32_t qt
     if (qi >= a.Tq || c >= hd) return;
     const float* P = a.part + static_cast<uint64_t>(rb) * a.pieces * kPartFloats;
     float M = -INFINITY;
-    for (uint32_t i = 0; i < a.pieces; ++i) M = fmaxf(M, P[i * kPartFloats + kBQ * 64 + q]);
     float l = 0.0f;
     floatx4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (uint32_t i = 0; i < a.pieces; ++i) {
-        const float* Pi = P + i * kPartFloats;
-        const float mi = Pi[kBQ * 64 + q];
-        const float sc = mi == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mi - M);
-        l += sc * Pi[kBQ * 64 + kBQ + q];
-        const floatx4* row = reinterpret_cast<const floatx4*>(Pi + q * 64 + c);
-        acc0 += sc * row[0];
-        acc1 += sc * row[1];
+    if constexpr (NP > 0) {
+        // NP pieces exactly: every load first (one memory round trip), then
+        // the same operations in the same order as the loops of any count
+        float mi[NP], li[NP];
+        floatx4 r0[NP], r1[NP];
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            const float* Pi = P + i * kPartFloats;
+            mi[i] = Pi[kBQ * 64 + q];
+            li[i] = Pi[kBQ * 64 + kBQ + q];
+            r0[i] = reinterpret_cast<const floatx4*>(Pi + q * 64 + c)[0];
+            r1[i] = reinterpret_cast<const floatx4*>(Pi + q * 64 + c)[1];
+        }
+#pragma unroll
+        for (int i = 0; i < NP; ++i) M = fmaxf(M, mi[i]);
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            const float sc = mi[i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mi[i] - M);
+            l += sc * li[i];
+            acc0 += sc * r0[i];
+            acc1 += sc * r1[i];
+        }
+    } else {
+        for (uint32_t i = 0; i < a.pieces; ++i) M = fmaxf(M, P[i * kPartFloats + kBQ * 64 + q]);
+        for (uint32_t i = 0; i < a.pieces; ++i) {
+            const float* Pi = P + i * kPartFloats;
+            const float mi = Pi[kBQ * 64 + q];
+            const float sc = mi == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mi - M);
+            l += sc * Pi[kBQ * 64 + kBQ + q];
+            const floatx4* row = reinterpret_cast<const floatx4*>(Pi + q * 64 + c);
+            acc0 += sc * row[0];
+            acc1 += sc * row[1];
+        }
     }
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     acc0 *= inv;
@@ -1146,7 +1171,9 @@ void launch_f16(const AttnArgs& a, uint32_t batch, hipStream_t s) {
         if (a.precise) attn_f16_kernel<TO, 4, kResidAll><<<grid, 256, 0, s>>>(a, q4);
         else if (use_burst(a, grid)) attn_f16_kernel<TO, 4, kResidNone, 1><<<grid, 256, 0, s>>>(a, q4);
         else attn_f16_kernel<TO, 4, kResidNone><<<grid, 256, 0, s>>>(a, q4);
-        attn_merge_kernel<TO><<<rest * 4, 256, 0, s>>>(a, q4);
+        if (a.pieces == 2) attn_merge_kernel<TO, 2><<<rest * 4, 256, 0, s>>>(a, q4);
+        else if (a.pieces == 4) attn_merge_kernel<TO, 4><<<rest * 4, 256, 0, s>>>(a, q4);
+        else attn_merge_kernel<TO><<<rest * 4, 256, 0, s>>>(a, q4);
         return;
     }
     const bool nw4 = f16_waves(a, batch) == 4;
